@@ -1,0 +1,93 @@
+// ien_internal.h -- shared internals of libien_hip.so (not part of the ABI).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+#include <string>
+#include <vector>
+
+#include "../../include/ien_hip.h"
+
+namespace ien {
+
+// Thread-local message behind ien_last_error (crates/native-engine/src/lib.rs:73-83).
+void set_error(const char *fmt, ...) __attribute__((format(printf, 1, 2)));
+
+// Return `status` after recording a formatted message.
+ien_status fail(ien_status status, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+
+#define IEN_HIP(call)                                                                     \
+  do {                                                                                    \
+    hipError_t e_ = (call);                                                               \
+    if (e_ != hipSuccess)                                                                 \
+      return ::ien::fail(IEN_ERR_GPU, "%s: %s (%s:%d)", #call, hipGetErrorString(e_),     \
+                         __FILE__, __LINE__);                                             \
+  } while (0)
+
+#define IEN_CHECK(cond, status, ...)                       \
+  do {                                                     \
+    if (!(cond)) return ::ien::fail(status, __VA_ARGS__);  \
+  } while (0)
+
+}  // namespace ien
+
+struct ien_ctx {
+  int device = 0;
+  hipStream_t own = nullptr;     // the context's stream
+  hipStream_t stream = nullptr;  // where work goes (own, or the caller's)
+  std::string name;
+  int cus = 0;
+};
+
+// Packed weights (gemm.rs Matrix): k x n padded to whole 16 x 32 MFMA
+// fragments.  Fragment (kb, nb) holds 512 halves: lane l's 8 consecutive
+// values are W[16 kb + 8 (l / 32) + i][32 nb + l % 32], the B-operand
+// register layout of v_mfma_f32_32x32x16_f16, so a wave loads one fragment
+// with one 16-byte load per lane.
+struct ien_matrix {
+  ien_ctx *ctx = nullptr;
+  size_t k = 0, n = 0;
+  int kb = 0, nb = 0;          // fragments along k (16) and n (32)
+  uint16_t *d_packed = nullptr;  // nb x kb fragments of 512 halves, n-block major
+  float *d_bias = nullptr;       // 32 nb floats, zero padded
+};
+
+namespace ien {
+
+// Pack row-major k x n weights (as floats) into the fragment layout above.
+std::vector<uint16_t> pack_fragments(const float *w, size_t k, size_t n, int *kb, int *nb);
+
+// Host-side round to nearest even (the same map as half.rs:7-40).
+uint16_t f32_to_half(float v);
+
+// Launch helpers of conv.hip, shared by the ops and the model drivers.
+struct ConvCall {
+  // input
+  const uint16_t *x = nullptr;
+  int H = 0, W = 0, C = 0;
+  long xs = 0;  // NHWC: halves between pixels; NCHW: halves between planes
+  int in_nchw = 0;
+  int rows_mode = 0;  // Input::Rows: M rows of k values, no image grid
+  int ks = 1, stride = 1, pad_reflect = 0;
+  int noff = 0;  // Taps::Offsets count (0: Conv taps)
+  int offy[4] = {0, 0, 0, 0}, offx[4] = {0, 0, 0, 0};
+  // output grid and range
+  int OH = 0, OW = 0;
+  long row0 = 0, rows = 0;
+  // weights
+  const ien_matrix *w = nullptr;
+  // output
+  void *y = nullptr;
+  long ys = 0;
+  int out_nchw = 0, out_f32 = 0;
+  int act = IEN_ACT_NONE;
+  const float *slope = nullptr;
+  int accumulate = 0;
+};
+
+ien_status launch_conv(ien_ctx *ctx, const ConvCall &c);
+
+}  // namespace ien

@@ -1,0 +1,219 @@
+// runtime.hip -- contexts, memory, errors and weight packing of libien_hip.so.
+//
+// The role of crates/native-vulkan (device choice, buffers, one-off weight
+// upload, ordered submissions) on HIP: one stream per context, device
+// buffers from hipMalloc, weights packed once into MFMA fragment order.
+
+#include <cstring>
+#include <mutex>
+
+#include "ien_internal.h"
+
+namespace ien {
+
+static thread_local std::string g_error;
+
+void set_error(const char *fmt, ...) {
+  char buf[1024];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_error = buf;
+}
+
+ien_status fail(ien_status status, const char *fmt, ...) {
+  char buf[1024];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  // crates/native-engine/src/lib.rs:73-83: "weights: ...", "input: ...".
+  const char *kind = status == IEN_ERR_IO ? "io" :
+                     status == IEN_ERR_WEIGHTS ? "weights" :
+                     status == IEN_ERR_INPUT ? "input" :
+                     status == IEN_ERR_CANCELLED ? "cancelled" : "GPU";
+  g_error = std::string(kind) + ": " + buf;
+  return status;
+}
+
+// half.rs:7-40, on the host: round to nearest, ties to even.
+uint16_t f32_to_half(float v) {
+  uint32_t x;
+  std::memcpy(&x, &v, 4);
+  uint16_t sign = (uint16_t)((x >> 16) & 0x8000u);
+  uint32_t mant = x & 0x7fffffu;
+  if (((x >> 23) & 0xffu) == 0xffu) return sign | 0x7c00u | (mant ? 0x200u : 0);
+  int e = (int)((x >> 23) & 0xffu) - 112;
+  auto round = [](uint32_t kept, uint32_t low, uint32_t shift) {
+    uint32_t half = 1u << (shift - 1);
+    return kept + ((low > half || (low == half && (kept & 1u))) ? 1u : 0u);
+  };
+  if (e >= 31) return sign | 0x7c00u;
+  if (e <= 0) {
+    if (e < -10) return sign;
+    uint32_t sig = mant | 0x800000u, shift = (uint32_t)(14 - e);
+    return sign | (uint16_t)round(sig >> shift, sig & ((1u << shift) - 1u), shift);
+  }
+  return sign | (uint16_t)round(((uint32_t)e << 10) | (mant >> 13), mant & 0x1fffu, 13);
+}
+
+std::vector<uint16_t> pack_fragments(const float *w, size_t k, size_t n, int *kb_out,
+                                     int *nb_out) {
+  // n padded to whole 128-column tiles, so that any tile width reads zeros.
+  int kb = (int)((k + 15) / 16), nb = (int)((n + 127) / 128) * 4;
+  std::vector<uint16_t> out((size_t)kb * nb * 512, 0);
+  for (int b = 0; b < nb; b++)
+    for (int a = 0; a < kb; a++) {
+      uint16_t *frag = out.data() + ((size_t)b * kb + a) * 512;
+      for (int l = 0; l < 64; l++)
+        for (int i = 0; i < 8; i++) {
+          size_t kk = (size_t)a * 16 + 8 * (l / 32) + i, nn = (size_t)b * 32 + l % 32;
+          if (kk < k && nn < n) frag[l * 8 + i] = f32_to_half(w[kk * n + nn]);
+        }
+    }
+  *kb_out = kb;
+  *nb_out = nb;
+  return out;
+}
+
+}  // namespace ien
+
+using namespace ien;
+
+extern "C" {
+
+const char *ien_last_error(void) { return g_error.c_str(); }
+
+ien_status ien_open(int device, ien_ctx **out) {
+  IEN_CHECK(out, IEN_ERR_INPUT, "no output pointer");
+  int count = 0;
+  if (hipGetDeviceCount(&count) != hipSuccess || count == 0)
+    return fail(IEN_ERR_GPU, "no HIP device");
+  IEN_CHECK(device >= 0 && device < count, IEN_ERR_GPU, "device %d of %d", device, count);
+  hipDeviceProp_t prop;
+  IEN_HIP(hipGetDeviceProperties(&prop, device));
+  if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+    return fail(IEN_ERR_GPU, "device %d is %s, this library is built for gfx950", device,
+                prop.gcnArchName);
+  IEN_HIP(hipSetDevice(device));
+  ien_ctx *ctx = new ien_ctx;
+  ctx->device = device;
+  ctx->cus = prop.multiProcessorCount;
+  ctx->name = prop.name[0] ? prop.name : prop.gcnArchName;
+  hipError_t e = hipStreamCreateWithFlags(&ctx->own, hipStreamNonBlocking);
+  if (e != hipSuccess) {
+    delete ctx;
+    return fail(IEN_ERR_GPU, "stream: %s", hipGetErrorString(e));
+  }
+  ctx->stream = ctx->own;
+  *out = ctx;
+  return IEN_OK;
+}
+
+void ien_close(ien_ctx *ctx) {
+  if (!ctx) return;
+  (void)hipSetDevice(ctx->device);
+  (void)hipStreamSynchronize(ctx->stream);
+  (void)hipStreamDestroy(ctx->own);
+  delete ctx;
+}
+
+const char *ien_device_name(const ien_ctx *ctx) { return ctx ? ctx->name.c_str() : ""; }
+
+void *ien_stream(ien_ctx *ctx) { return ctx ? (void *)ctx->stream : nullptr; }
+
+ien_status ien_set_stream(ien_ctx *ctx, void *stream) {
+  IEN_CHECK(ctx, IEN_ERR_INPUT, "no context");
+  ctx->stream = stream ? (hipStream_t)stream : ctx->own;
+  return IEN_OK;
+}
+
+ien_status ien_alloc(ien_ctx *ctx, size_t bytes, void **d_out) {
+  IEN_CHECK(ctx && d_out, IEN_ERR_INPUT, "no context or output pointer");
+  IEN_HIP(hipSetDevice(ctx->device));
+  IEN_HIP(hipMalloc(d_out, bytes ? bytes : 1));
+  return IEN_OK;
+}
+
+ien_status ien_free(ien_ctx *ctx, void *d_ptr) {
+  IEN_CHECK(ctx, IEN_ERR_INPUT, "no context");
+  if (!d_ptr) return IEN_OK;
+  IEN_HIP(hipSetDevice(ctx->device));
+  IEN_HIP(hipFree(d_ptr));
+  return IEN_OK;
+}
+
+ien_status ien_upload(ien_ctx *ctx, void *d_dst, const void *src, size_t bytes) {
+  IEN_CHECK(ctx && (bytes == 0 || (d_dst && src)), IEN_ERR_INPUT, "null buffer");
+  IEN_HIP(hipMemcpyAsync(d_dst, src, bytes, hipMemcpyHostToDevice, ctx->stream));
+  IEN_HIP(hipStreamSynchronize(ctx->stream));
+  return IEN_OK;
+}
+
+ien_status ien_download(ien_ctx *ctx, void *dst, const void *d_src, size_t bytes) {
+  IEN_CHECK(ctx && (bytes == 0 || (dst && d_src)), IEN_ERR_INPUT, "null buffer");
+  IEN_HIP(hipMemcpyAsync(dst, d_src, bytes, hipMemcpyDeviceToHost, ctx->stream));
+  IEN_HIP(hipStreamSynchronize(ctx->stream));
+  return IEN_OK;
+}
+
+ien_status ien_sync(ien_ctx *ctx) {
+  IEN_CHECK(ctx, IEN_ERR_INPUT, "no context");
+  IEN_HIP(hipStreamSynchronize(ctx->stream));
+  return IEN_OK;
+}
+
+ien_status ien_matrix_new(ien_ctx *ctx, const void *w, ien_wtype wtype, size_t k, size_t n,
+                          const float *bias, ien_matrix **out) {
+  IEN_CHECK(ctx && w && out, IEN_ERR_INPUT, "null argument");
+  IEN_CHECK(k > 0 && n > 0 && k < (1u << 24) && n < (1u << 20), IEN_ERR_INPUT,
+            "matrix of %zu x %zu", k, n);
+  std::vector<float> wf;
+  const float *src = (const float *)w;
+  if (wtype == IEN_W_F16) {
+    // half.rs:125-140, widened exactly; packing rounds back to the same half.
+    wf.resize(k * n);
+    const uint16_t *h = (const uint16_t *)w;
+    for (size_t i = 0; i < k * n; i++) {
+      _Float16 v;
+      std::memcpy(&v, &h[i], 2);
+      wf[i] = (float)v;
+    }
+    src = wf.data();
+  } else {
+    IEN_CHECK(wtype == IEN_W_F32, IEN_ERR_INPUT, "weight type %d", (int)wtype);
+  }
+  ien_matrix *m = new ien_matrix;
+  m->ctx = ctx;
+  m->k = k;
+  m->n = n;
+  std::vector<uint16_t> packed = pack_fragments(src, k, n, &m->kb, &m->nb);
+  std::vector<float> b((size_t)m->nb * 32, 0.0f);
+  if (bias) std::memcpy(b.data(), bias, n * sizeof(float));
+  hipError_t e = hipSetDevice(ctx->device);
+  if (e == hipSuccess) e = hipMalloc(&m->d_packed, packed.size() * 2);
+  if (e == hipSuccess) e = hipMalloc(&m->d_bias, b.size() * 4);
+  if (e == hipSuccess)
+    e = hipMemcpyAsync(m->d_packed, packed.data(), packed.size() * 2, hipMemcpyHostToDevice,
+                       ctx->stream);
+  if (e == hipSuccess)
+    e = hipMemcpyAsync(m->d_bias, b.data(), b.size() * 4, hipMemcpyHostToDevice, ctx->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  if (e != hipSuccess) {
+    ien_matrix_free(m);
+    return fail(IEN_ERR_GPU, "matrix upload: %s", hipGetErrorString(e));
+  }
+  *out = m;
+  return IEN_OK;
+}
+
+void ien_matrix_free(ien_matrix *m) {
+  if (!m) return;
+  if (m->ctx) (void)hipSetDevice(m->ctx->device);
+  if (m->d_packed) (void)hipFree(m->d_packed);
+  if (m->d_bias) (void)hipFree(m->d_bias);
+  delete m;
+}
+
+}  // extern "C"

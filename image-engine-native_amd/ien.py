@@ -1,0 +1,326 @@
+"""ctypes binding of libien_hip.so, the MI355X backend's C ABI
+(include/ien_hip.h), for the tests and the benchmark.
+
+Device buffers are torch tensors on the GPU (plumbing only: the kernels are
+the library's); the library runs on torch's current stream, so torch events
+and synchronisation order with it.  Nothing here falls back to the CPU: a
+missing or unloadable library raises.
+"""
+
+import ctypes
+import pathlib
+
+HERE = pathlib.Path(__file__).resolve().parent
+LIB_PATH = HERE / "libien_hip.so"
+
+OK, ERR_IO, ERR_WEIGHTS, ERR_INPUT, ERR_CANCELLED, ERR_GPU = range(6)
+W_F32, W_F16 = 0, 1
+PAD_ZERO, PAD_REFLECT = 0, 1
+TAPS_CONV, TAPS_OFFSETS = 0, 1
+INPUT_ROWS, INPUT_IMAGE = 0, 1
+NHWC, NCHW = 0, 1
+ACT_NONE, ACT_RELU, ACT_GELU, ACT_PRELU, ACT_SIGMOID = range(5)
+OUT_F16, OUT_F32 = 0, 1
+MODEL_REALESRGAN = 0
+
+# Every symbol include/ien_hip.h declares.
+EXPORTS = (
+    "ien_last_error", "ien_open", "ien_close", "ien_device_name", "ien_stream", "ien_set_stream",
+    "ien_alloc", "ien_free", "ien_upload", "ien_download", "ien_sync",
+    "ien_floats_to_halves", "ien_halves_to_floats",
+    "ien_matrix_new", "ien_matrix_free", "ien_multiply", "ien_multiply_ex", "ien_conv3",
+    "ien_layer_norm", "ien_gelu", "ien_sigmoid", "ien_pixel_shuffle_add", "ien_depthwise",
+    "ien_model_load", "ien_model_from_tensors", "ien_model_free", "ien_model_run",
+    "ien_model_run_device", "ien_model_set_graph",
+)
+
+
+class IenError(RuntimeError):
+    def __init__(self, status, message):
+        super().__init__(message)
+        self.status = status
+
+
+class Input(ctypes.Structure):
+    _fields_ = [
+        ("kind", ctypes.c_int),
+        ("data", ctypes.c_void_p),
+        ("height", ctypes.c_size_t),
+        ("width", ctypes.c_size_t),
+        ("channels", ctypes.c_size_t),
+        ("stride", ctypes.c_size_t),
+        ("layout", ctypes.c_int),
+        ("taps", ctypes.c_int),
+        ("size", ctypes.c_size_t),
+        ("step", ctypes.c_size_t),
+        ("pad", ctypes.c_int),
+        ("offsets", (ctypes.c_size_t * 2) * 4),
+        ("count", ctypes.c_size_t),
+    ]
+
+
+class Output(ctypes.Structure):
+    _fields_ = [
+        ("data", ctypes.c_void_p),
+        ("stride", ctypes.c_size_t),
+        ("layout", ctypes.c_int),
+        ("type", ctypes.c_int),
+    ]
+
+
+class Tensor(ctypes.Structure):
+    _fields_ = [
+        ("name", ctypes.c_char_p),
+        ("rank", ctypes.c_size_t),
+        ("dims", ctypes.c_size_t * 4),
+        ("values", ctypes.c_void_p),
+    ]
+
+
+PROGRESS = ctypes.CFUNCTYPE(ctypes.c_int, ctypes.c_float, ctypes.c_void_p)
+
+_lib = None
+
+
+def load():
+    """The library, loaded once; raises if it is not built."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise OSError(f"{LIB_PATH} is not built: run __graft_entry__.build()")
+        L = ctypes.CDLL(str(LIB_PATH))
+        vp, sz, st, i = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_int
+        L.ien_last_error.restype = ctypes.c_char_p
+        L.ien_open.argtypes = [i, ctypes.POINTER(vp)]
+        L.ien_close.argtypes = [vp]
+        L.ien_close.restype = None
+        L.ien_device_name.argtypes = [vp]
+        L.ien_device_name.restype = ctypes.c_char_p
+        L.ien_stream.argtypes = [vp]
+        L.ien_stream.restype = vp
+        L.ien_set_stream.argtypes = [vp, vp]
+        L.ien_alloc.argtypes = [vp, sz, ctypes.POINTER(vp)]
+        L.ien_free.argtypes = [vp, vp]
+        L.ien_upload.argtypes = [vp, vp, vp, sz]
+        L.ien_download.argtypes = [vp, vp, vp, sz]
+        L.ien_sync.argtypes = [vp]
+        L.ien_floats_to_halves.argtypes = [vp, vp, vp, sz]
+        L.ien_halves_to_floats.argtypes = [vp, vp, vp, sz]
+        L.ien_matrix_new.argtypes = [vp, vp, i, sz, sz, vp, ctypes.POINTER(vp)]
+        L.ien_matrix_free.argtypes = [vp]
+        L.ien_matrix_free.restype = None
+        L.ien_multiply.argtypes = [vp, ctypes.POINTER(Input), sz, sz, vp, vp, sz, i, i]
+        L.ien_multiply_ex.argtypes = [vp, ctypes.POINTER(Input), sz, sz, vp, ctypes.POINTER(Output), i, vp, i]
+        L.ien_conv3.argtypes = [vp, ctypes.POINTER(Input), vp, vp, sz, i, i, vp]
+        L.ien_layer_norm.argtypes = [vp, vp, sz, sz, sz, vp, vp]
+        L.ien_gelu.argtypes = [vp, vp, sz]
+        L.ien_sigmoid.argtypes = [vp, vp, sz]
+        L.ien_pixel_shuffle_add.argtypes = [vp, vp, sz, vp, sz, sz, vp]
+        L.ien_depthwise.argtypes = [vp, vp, sz, sz, sz, i, vp, sz, vp, vp]
+        L.ien_model_load.argtypes = [vp, i, ctypes.c_char_p, ctypes.POINTER(vp)]
+        L.ien_model_from_tensors.argtypes = [vp, i, ctypes.POINTER(Tensor), sz, ctypes.POINTER(vp)]
+        L.ien_model_free.argtypes = [vp]
+        L.ien_model_free.restype = None
+        L.ien_model_run.argtypes = [vp, vp, vp, sz, sz, vp, vp, vp]
+        L.ien_model_run_device.argtypes = [vp, vp, vp, sz, sz, vp]
+        L.ien_model_set_graph.argtypes = [vp, i]
+        for name in EXPORTS:
+            getattr(L, name)
+        _lib = L
+    return _lib
+
+
+def check(status):
+    if status != OK:
+        raise IenError(status, load().ien_last_error().decode(errors="replace"))
+
+
+def _ptr(t):
+    """Device pointer of a torch tensor, or None."""
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+class Context:
+    """ien_ctx on one device, running on torch's current stream."""
+
+    def __init__(self, device=0):
+        import torch
+
+        L = load()
+        h = ctypes.c_void_p()
+        check(L.ien_open(device, ctypes.byref(h)))
+        self.h = h
+        self.device = device
+        check(L.ien_set_stream(h, ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)))
+
+    @property
+    def name(self):
+        return load().ien_device_name(self.h).decode()
+
+    def close(self):
+        if self.h:
+            load().ien_close(self.h)
+            self.h = None
+
+    def sync(self):
+        check(load().ien_sync(self.h))
+
+
+class Matrix:
+    """gemm.rs Matrix::new: host weights k x n (numpy f32 or f16) + bias."""
+
+    def __init__(self, ctx, w, bias=None):
+        import numpy as np
+
+        w = np.ascontiguousarray(w)
+        wtype = W_F16 if w.dtype == np.float16 else W_F32
+        if wtype == W_F32:
+            w = np.ascontiguousarray(w, dtype=np.float32)
+        k, n = w.shape
+        b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+        h = ctypes.c_void_p()
+        check(load().ien_matrix_new(ctx.h, w.ctypes.data_as(ctypes.c_void_p), wtype, k, n,
+                                    None if b is None else b.ctypes.data_as(ctypes.c_void_p),
+                                    ctypes.byref(h)))
+        self.h, self.k, self.n, self.ctx = h, k, n, ctx
+
+    def free(self):
+        if self.h:
+            load().ien_matrix_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+def image_input(x, height, width, channels, stride=None, layout=NHWC, size=3, step=1, pad=PAD_ZERO,
+                offsets=None):
+    s = Input()
+    s.kind = INPUT_IMAGE
+    s.data = x.data_ptr()
+    s.height, s.width, s.channels = height, width, channels
+    s.stride = stride if stride is not None else (channels if layout == NHWC else height * width)
+    s.layout = layout
+    if offsets is None:
+        s.taps, s.size, s.step, s.pad = TAPS_CONV, size, step, pad
+    else:
+        s.taps, s.count = TAPS_OFFSETS, len(offsets)
+        for j, (dy, dx) in enumerate(offsets):
+            s.offsets[j][0], s.offsets[j][1] = dy, dx
+    return s
+
+
+def rows_input(x, stride):
+    s = Input()
+    s.kind = INPUT_ROWS
+    s.data = x.data_ptr()
+    s.stride = stride
+    return s
+
+
+def multiply_ex(ctx, inp, row0, rows, matrix, out, out_stride, layout=NHWC, out_f32=False, act=ACT_NONE,
+                slope=None, accumulate=False):
+    o = Output()
+    o.data = out.data_ptr()
+    o.stride = out_stride
+    o.layout = layout
+    o.type = OUT_F32 if out_f32 else OUT_F16
+    check(load().ien_multiply_ex(ctx.h, ctypes.byref(inp), row0, rows, matrix.h, ctypes.byref(o), act,
+                                 _ptr(slope), int(accumulate)))
+
+
+def multiply(ctx, inp, row0, rows, matrix, out, stride, act=ACT_NONE, accumulate=False):
+    check(load().ien_multiply(ctx.h, ctypes.byref(inp), row0, rows, matrix.h, _ptr(out), stride, act,
+                              int(accumulate)))
+
+
+def conv3(ctx, inp, matrix, out, stride, accumulate=False, finish=ACT_NONE, slope=None):
+    check(load().ien_conv3(ctx.h, ctypes.byref(inp), matrix.h, _ptr(out), stride, int(accumulate), finish,
+                           _ptr(slope)))
+
+
+def floats_to_halves(ctx, src, dst):
+    check(load().ien_floats_to_halves(ctx.h, _ptr(src), _ptr(dst), src.numel()))
+
+
+def halves_to_floats(ctx, src, dst):
+    check(load().ien_halves_to_floats(ctx.h, _ptr(src), _ptr(dst), src.numel()))
+
+
+def layer_norm(ctx, x, rows, c, stride, gamma, beta):
+    check(load().ien_layer_norm(ctx.h, _ptr(x), rows, c, stride, _ptr(gamma), _ptr(beta)))
+
+
+def gelu(ctx, x):
+    check(load().ien_gelu(ctx.h, _ptr(x), x.numel()))
+
+
+def sigmoid(ctx, x):
+    check(load().ien_sigmoid(ctx.h, _ptr(x), x.numel()))
+
+
+def pixel_shuffle_add(ctx, last, last_stride, image, width, height, out):
+    check(load().ien_pixel_shuffle_add(ctx.h, _ptr(last), last_stride, _ptr(image), width, height, _ptr(out)))
+
+
+def depthwise(ctx, x, height, width, channels, layout, w, size, bias, y):
+    check(load().ien_depthwise(ctx.h, _ptr(x), height, width, channels, layout, _ptr(w), size, _ptr(bias),
+                               _ptr(y)))
+
+
+class Model:
+    """ien_model: the reference's Model with the HIP engine."""
+
+    def __init__(self, ctx, kind, tensors=None, path=None):
+        import numpy as np
+
+        L = load()
+        h = ctypes.c_void_p()
+        if path is not None:
+            check(L.ien_model_load(ctx.h, kind, str(path).encode(), ctypes.byref(h)))
+        else:
+            arr = (Tensor * len(tensors))()
+            keep = []
+            for j, (name, value) in enumerate(tensors.items()):
+                v = np.ascontiguousarray(value, dtype=np.float32)
+                keep.append(v)
+                arr[j].name = name.encode()
+                arr[j].rank = v.ndim
+                for d, s in enumerate(v.shape):
+                    arr[j].dims[d] = s
+                arr[j].values = v.ctypes.data
+            check(L.ien_model_from_tensors(ctx.h, kind, arr, len(tensors), ctypes.byref(h)))
+        self.h, self.ctx = h, ctx
+
+    def free(self):
+        if self.h:
+            load().ien_model_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+    def set_graph(self, enabled):
+        check(load().ien_model_set_graph(self.h, int(enabled)))
+
+    def run(self, image, progress=None):
+        """Host f32 H x W x 3 in, host f32 4H x 4W x 3 out (Model::run_float)."""
+        import numpy as np
+
+        image = np.ascontiguousarray(image, dtype=np.float32)
+        h, w, _ = image.shape
+        out = np.empty((4 * h, 4 * w, 3), np.float32)
+        cb = PROGRESS(progress) if progress else None
+        check(load().ien_model_run(self.h, image.ctypes.data_as(ctypes.c_void_p), None, w, h,
+                                   out.ctypes.data_as(ctypes.c_void_p),
+                                   ctypes.cast(cb, ctypes.c_void_p) if cb else None, None))
+        return out
+
+    def run_device(self, d_image, width, height, d_out):
+        check(load().ien_model_run_device(self.h, _ptr(d_image), None, width, height, _ptr(d_out)))

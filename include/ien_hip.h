@@ -1,0 +1,224 @@
+/*
+ * ien_hip.h -- C ABI of the MI355X (gfx950) backend for image-engine-native.
+ *
+ * The library (libien_hip.so) sits beside the reference's Vulkan backend
+ * (crates/native-vulkan) behind the same model interface: each model crate's
+ * `Engine` enum (crates/realesrgan-native/src/lib.rs:48-79) would gain a
+ * `Hip` variant whose `load`/`run` call the ien_model_* entry points below,
+ * and the native-engine op interface (crates/native-engine/src/lib.rs:51-57:
+ * gemm::{Matrix, multiply, Input, Taps, Pad, Act}, winograd::conv3,
+ * attention::attention, math::*, half::*) maps onto the ien_* op entry points.
+ *
+ * Conventions
+ *  - Every entry point returns an ien_status; on failure ien_last_error()
+ *    (thread-local) holds the message, as the reference's Error's Display
+ *    (crates/native-engine/src/lib.rs:61-85).  IEN_ERR_GPU means "this GPU
+ *    cannot run it; fall back to the CPU" (realesrgan-native lib.rs:134).
+ *  - A context owns one HIP stream on one device.  It is Send but not Sync,
+ *    like native-vulkan's Gpu (native-vulkan/src/lib.rs:140-143): calls on
+ *    one context must not overlap.  Ops are asynchronous on the context's
+ *    stream; ien_sync waits.
+ *  - Device activations are IEEE half floats (f16), NHWC with a pixel
+ *    stride in halves (the reference's layout, gemm.rs:3-7), or NCHW with a
+ *    channel-plane stride; products accumulate in f32 on f16 MFMA.
+ *  - Pointers named `d_*` or documented as device pointers are device
+ *    memory from ien_alloc (or any hipMalloc'd memory of the same device).
+ */
+#ifndef IEN_HIP_H
+#define IEN_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* crates/native-engine/src/lib.rs:61-71 Error {Io, Weights, Input,
+ * Cancelled, Gpu} */
+typedef enum {
+  IEN_OK = 0,
+  IEN_ERR_IO = 1,
+  IEN_ERR_WEIGHTS = 2,
+  IEN_ERR_INPUT = 3,
+  IEN_ERR_CANCELLED = 4,
+  IEN_ERR_GPU = 5
+} ien_status;
+
+typedef struct ien_ctx ien_ctx;
+typedef struct ien_matrix ien_matrix;
+typedef struct ien_model ien_model;
+
+/* Message of the last failure on this thread (lib.rs:73-83 Display). */
+const char *ien_last_error(void);
+
+/* ---- device context: native-vulkan/src/lib.rs:168 Gpu::open, name ----- */
+ien_status ien_open(int device, ien_ctx **out);
+void ien_close(ien_ctx *ctx);
+/* The GPU's name (native-vulkan lib.rs Gpu::name). */
+const char *ien_device_name(const ien_ctx *ctx);
+/* The context's hipStream_t, for callers that order their own work on it. */
+void *ien_stream(ien_ctx *ctx);
+/* Run this context's work on the caller's hipStream_t instead (NULL: the
+ * context's own stream).  The caller keeps the stream alive. */
+ien_status ien_set_stream(ien_ctx *ctx, void *stream);
+
+/* ---- memory: native-vulkan lib.rs buffer/upload/Buffer::bytes ---------- */
+ien_status ien_alloc(ien_ctx *ctx, size_t bytes, void **d_out);
+ien_status ien_free(ien_ctx *ctx, void *d_ptr);
+ien_status ien_upload(ien_ctx *ctx, void *d_dst, const void *src, size_t bytes);
+ien_status ien_download(ien_ctx *ctx, void *dst, const void *d_src, size_t bytes);
+ien_status ien_sync(ien_ctx *ctx);
+
+/* ---- half floats: crates/native-engine/src/half.rs:50-79 --------------- */
+/* floats_to_halves / halves_to_f32 on the device, round to nearest even. */
+ien_status ien_floats_to_halves(ien_ctx *ctx, const float *d_src, uint16_t *d_dst, size_t n);
+ien_status ien_halves_to_floats(ien_ctx *ctx, const uint16_t *d_src, float *d_dst, size_t n);
+
+/* ---- products: crates/native-engine/src/gemm.rs ------------------------ */
+typedef enum { IEN_W_F32 = 0, IEN_W_F16 = 1 } ien_wtype;
+
+/* gemm.rs:109-147 Matrix::new: row-major k x n host weights (f32, or f16
+ * bits), k = taps * channels with channels fastest, plus an optional
+ * length-n host bias.  Packed once onto the device in MFMA fragment order. */
+ien_status ien_matrix_new(ien_ctx *ctx, const void *w, ien_wtype wtype, size_t k, size_t n,
+                          const float *bias, ien_matrix **out);
+void ien_matrix_free(ien_matrix *m);
+
+/* gemm.rs:264-270 Pad */
+typedef enum { IEN_PAD_ZERO = 0, IEN_PAD_REFLECT = 1 } ien_pad;
+/* gemm.rs:273-286 Taps */
+typedef enum { IEN_TAPS_CONV = 0, IEN_TAPS_OFFSETS = 1 } ien_taps;
+/* gemm.rs:289-304 Input */
+typedef enum { IEN_INPUT_ROWS = 0, IEN_INPUT_IMAGE = 1 } ien_input_kind;
+typedef enum { IEN_LAYOUT_NHWC = 0, IEN_LAYOUT_NCHW = 1 } ien_layout;
+/* gemm.rs:486-491 Act, plus the per-pixel `finish` closures the callers
+ * pass to winograd::conv3 (PReLU: realesrgan network.rs:31-41) and the
+ * logistic output of LaMa/BiRefNet (math.rs:145-152). */
+typedef enum {
+  IEN_ACT_NONE = 0,
+  IEN_ACT_RELU = 1,
+  IEN_ACT_GELU = 2,
+  IEN_ACT_PRELU = 3,
+  IEN_ACT_SIGMOID = 4
+} ien_act;
+
+/* The left operand of a product (gemm.rs:289-304).  `data` is device f16.
+ * ROWS: row r is data[r * stride ..][..k].
+ * IMAGE: a height x width image of `channels` channels; NHWC pixels are
+ * `stride` halves apart, NCHW channel planes are `stride` halves apart.
+ * Taps CONV: centred size x size every `step` pixels with `pad`;
+ * OFFSETS: output pixel (y, x) reads (y + dy, x + dx) for `count` offsets,
+ * zeros past the edge. */
+typedef struct {
+  ien_input_kind kind;
+  const void *data;
+  size_t height, width, channels, stride;
+  ien_layout layout;
+  ien_taps taps;
+  size_t size, step;
+  ien_pad pad;
+  size_t offsets[4][2];
+  size_t count;
+} ien_input;
+
+/* Where a product's results go: device memory, f16 or f32, NHWC rows
+ * `stride` elements apart (row = output pixel) or NCHW planes `stride`
+ * apart. */
+typedef enum { IEN_OUT_F16 = 0, IEN_OUT_F32 = 1 } ien_out_type;
+typedef struct {
+  void *data;
+  size_t stride;
+  ien_layout layout;
+  ien_out_type type;
+} ien_output;
+
+/* gemm.rs:514-667 multiply: out[r] = act((accumulate ? out[r] : 0) +
+ * input[r] . w + bias) for rows row0 .. row0 + rows of the input's output
+ * grid (row-major pixels), into f16 NHWC rows `stride` halves apart
+ * starting at d_out (row row0 at d_out). */
+ien_status ien_multiply(ien_ctx *ctx, const ien_input *input, size_t row0, size_t rows,
+                        const ien_matrix *w, void *d_out, size_t stride, ien_act act,
+                        int accumulate);
+
+/* The general form of ien_multiply: any output layout/type, PReLU slopes
+ * (device f32, length n) for IEN_ACT_PRELU. */
+ien_status ien_multiply_ex(ien_ctx *ctx, const ien_input *input, size_t row0, size_t rows,
+                           const ien_matrix *w, const ien_output *out, ien_act act,
+                           const float *d_slope, int accumulate);
+
+/* winograd.rs:612-672 conv3: the 3x3 stride-1 convolution of an IMAGE
+ * input with w (9 cin x n), bias, stored to or (accumulate) added to the
+ * f16 NHWC pixels of d_out `stride` halves apart, then `finish` (NONE,
+ * RELU or PRELU with d_slope) on each pixel.  Computed as an implicit GEMM
+ * on MFMA, not by Winograd's transforms (which lose accuracy in f16). */
+ien_status ien_conv3(ien_ctx *ctx, const ien_input *input, const ien_matrix *w, void *d_out,
+                     size_t stride, int accumulate, ien_act finish, const float *d_slope);
+
+/* ---- elementwise: crates/native-engine/src/math.rs --------------------- */
+/* math.rs:154-170 layer_norm over rows of c values (f16 in place, f32
+ * statistics, epsilon 1e-5); gamma/beta device f32. */
+ien_status ien_layer_norm(ien_ctx *ctx, uint16_t *d_x, size_t rows, size_t c, size_t stride,
+                          const float *d_gamma, const float *d_beta);
+/* math.rs:136-152 gelu / sigmoid in place on n f16 values. */
+ien_status ien_gelu(ien_ctx *ctx, uint16_t *d_x, size_t n);
+ien_status ien_sigmoid(ien_ctx *ctx, uint16_t *d_x, size_t n);
+
+/* realesrgan-native network.rs:115-141 shuffled: out (f32, (4h) x (4w) x 3
+ * NHWC) = pixel shuffle x4 of `last` (f16 NHWC, 48 channels used of
+ * `last_stride`) plus the f32 RGB image repeated 4 x 4. */
+ien_status ien_pixel_shuffle_add(ien_ctx *ctx, const uint16_t *d_last, size_t last_stride,
+                                 const float *d_image, size_t width, size_t height,
+                                 float *d_out);
+
+/* Depthwise size x size convolution, zero padding, stride 1 (no reference
+ * implementation; the reference op interface expresses it as `channels`
+ * one-channel products, gemm.rs:288-304).  f16 in and out, NHWC or NCHW,
+ * weights (size*size) x channels and bias as device f32. */
+ien_status ien_depthwise(ien_ctx *ctx, const uint16_t *d_x, size_t height, size_t width,
+                         size_t channels, ien_layout layout, const float *d_w, size_t size,
+                         const float *d_bias, uint16_t *d_y);
+
+/* ---- models: crates/<model>-native/src/lib.rs Model ------------------- */
+typedef enum { IEN_MODEL_REALESRGAN = 0 } ien_model_kind;
+
+/* Model::load (realesrgan-native lib.rs:120-137 with the GPU engine): read
+ * the weights file (weight_file.rs format, magic b"REALESRG"), check every
+ * tensor, upload once. */
+ien_status ien_model_load(ien_ctx *ctx, ien_model_kind kind, const char *weights_path,
+                          ien_model **out);
+/* The same from weights already in memory: `tensors` name/shape/value
+ * triples as a weights file holds them (for synthetic random-init weights). */
+typedef struct {
+  const char *name;
+  size_t rank;
+  size_t dims[4];
+  const float *values; /* host f32 */
+} ien_tensor;
+ien_status ien_model_from_tensors(ien_ctx *ctx, ien_model_kind kind, const ien_tensor *tensors,
+                                  size_t count, ien_model **out);
+void ien_model_free(ien_model *model);
+
+/* Progress callback: share done in 0..1, after each layer; nonzero return
+ * cancels the run with IEN_ERR_CANCELLED (lib.rs:168-188). */
+typedef int (*ien_progress)(float done, void *user);
+
+/* Model::run_float (realesrgan-native lib.rs:194-214): host f32 NHWC image
+ * of width x height x 3 in [0, 1], host f32 output (4h x 4w x 3).  `mask` is
+ * for LaMa and NULL otherwise. */
+ien_status ien_model_run(ien_model *model, const float *image, const float *mask, size_t width,
+                         size_t height, float *out, ien_progress progress, void *user);
+
+/* The same on device buffers (f32 NHWC in and out), no host copies and no
+ * synchronisation: the hot path a serving loop or a benchmark times. */
+ien_status ien_model_run_device(ien_model *model, const float *d_image, const float *d_mask,
+                                size_t width, size_t height, float *d_out);
+
+/* Launch-free replay: capture ien_model_run_device at this size into a HIP
+ * graph once, then replay it (0 = eager launches). */
+ien_status ien_model_set_graph(ien_model *model, int enabled);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

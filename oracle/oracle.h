@@ -1,0 +1,115 @@
+/*
+ * oracle.h -- CPU restatement of image-engine-native's f32 CPU path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This library is the parity checker for the HIP
+ * backend and the timed CPU baseline: only tests/, __graft_entry__.smoke()
+ * and bench.py's cpu_baseline leg load it.  The product (libien_hip.so)
+ * never links, loads or calls it.
+ *
+ * Each function restates the reference's algorithm, including its order of
+ * sums, from the Rust sources it cites (paths relative to the reference
+ * root).  The multiply-adds are unfused (the reference's SSE/AVX tiers 0-1;
+ * tier 2 fuses them, which moves results by rounding only).
+ *
+ * Pins (tests/test_oracle_*.py): f64 definitions, brute force on small
+ * shapes, the reference's own known answers (half.rs tests) and torch
+ * functional fixtures under tests/golden/.  Every function below has at least
+ * one pin; none is "parity unpinned".
+ */
+#ifndef IEN_ORACLE_H
+#define IEN_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- half.rs ---------------------------------------------------------- */
+uint16_t or_f32_to_half(float v);              /* half.rs:7-40 */
+float or_half_to_f32(uint16_t h);              /* half.rs:125-140 */
+void or_floats_to_halves(const float *src, uint16_t *dst, size_t n);
+void or_halves_to_f32(const uint16_t *src, float *dst, size_t n);
+
+/* ---- math.rs ---------------------------------------------------------- */
+float or_exp_neg(float z);                     /* math.rs:21-31 */
+void or_sigmoid(float *x, size_t n);           /* math.rs:33-39,145-152 */
+void or_gelu(float *x, size_t n);              /* math.rs:41-75,136-143 */
+void or_layer_norm(float *x, size_t len, const float *gamma,
+                   const float *beta, size_t c); /* math.rs:95-116,154-170 */
+void or_softmax(float *x, size_t n);           /* math.rs:118-134 */
+
+/* ---- gemm.rs ---------------------------------------------------------- */
+enum { OR_INPUT_ROWS = 0, OR_INPUT_IMAGE = 1 };
+enum { OR_TAPS_CONV = 0, OR_TAPS_OFFSETS = 1 };
+enum { OR_PAD_ZERO = 0, OR_PAD_REFLECT = 1 };
+enum { OR_ACT_NONE = 0, OR_ACT_RELU = 1, OR_ACT_GELU = 2 };
+
+/* gemm.rs:272-304: Input::{Rows, Image} with Taps::{Conv, Offsets}. */
+typedef struct {
+  int kind;             /* OR_INPUT_* */
+  const float *data;
+  size_t height, width, channels, stride;
+  int taps;             /* OR_TAPS_* */
+  size_t size, step;    /* Conv */
+  int pad;              /* OR_PAD_* */
+  size_t offsets[4][2]; /* Offsets: (dy, dx) */
+  size_t count;
+} or_input;
+
+/* gemm.rs:514-667 multiply: out[r] = act((acc ? out[r] : 0) + bias +
+ * sum_k in(r,k) w[k][n]), rows row0..row0+rows, weights row-major k x n
+ * (the reference packs them into panels, which changes no sum). */
+void or_multiply(const or_input *in, size_t row0, size_t rows, const float *w,
+                 size_t k, size_t n, const float *bias, float *out,
+                 size_t stride, int act, int accumulate);
+/* The same, split over `threads` threads by rows (pool.rs: a task never
+ * splits one output's reduction, so results do not depend on threads). */
+void or_multiply_mt(int threads, const or_input *in, size_t rows,
+                    const float *w, size_t k, size_t n, const float *bias,
+                    float *out, size_t stride, int act, int accumulate);
+
+/* ---- winograd.rs ------------------------------------------------------ */
+enum { OR_FINISH_NONE = 0, OR_FINISH_PRELU = 1, OR_FINISH_RELU = 2 };
+/* winograd.rs:612-773 conv3: 3x3 stride-1 conv, F(4x4,3x3) when
+ * cin + cout <= 576, F(2x2,3x3) above, direct product when cin < 16; then
+ * `finish` on each output pixel (PReLU slopes or ReLU). */
+void or_conv3(int threads, const or_input *in, const float *w, size_t n,
+              const float *bias, float *out, size_t stride, int accumulate,
+              int finish, const float *slope);
+/* Force a form (2 or 4), for tests of both transforms. */
+void or_conv3_form(int threads, int form, const or_input *in, const float *w,
+                   size_t n, const float *bias, float *out, size_t stride,
+                   int accumulate, int finish, const float *slope);
+
+/* ---- attention.rs ----------------------------------------------------- */
+/* attention.rs:25-111: one head of one window of `tokens` tokens; qkv rows of
+ * 3c (q | k | v), head dim 32, bias tokens x tokens (mask included). */
+void or_attention(const float *qkv, size_t tokens, size_t c, size_t head,
+                  const float *bias, float *out);
+
+/* ---- realesrgan-native network.rs ------------------------------------- */
+/* network.rs:80-141: 34 conv3 layers (PReLU on all but the last), then the
+ * x4 pixel shuffle plus the input repeated.  w[i] is 9cin x cout row-major
+ * ((ky,kx,cin) rows), b[i] cout, slope[i] 64 (ignored for the last). */
+int or_realesrgan_run(int threads, const float *const *w,
+                      const float *const *b, const float *const *slope,
+                      const float *image, size_t width, size_t height,
+                      float *out);
+/* network.rs:115-141 alone: last is pixels x 48, image pixels x 3. */
+void or_pixel_shuffle_add(const float *last, const float *image, size_t width,
+                          size_t height, float *out);
+
+/* ---- depthwise (no reference implementation) -------------------------- */
+/* y[p][c] = bias[c] + sum_{ky,kx} w[(ky*size+kx)][c] * x[p + tap][c], NHWC,
+ * zero padding, stride 1: the 192 single-channel products of the reference
+ * op interface (gemm.rs:288-304 with channels 1, stride C), in tap order. */
+void or_depthwise(int threads, const float *x, size_t height, size_t width,
+                  size_t channels, const float *w, size_t size,
+                  const float *bias, float *y);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

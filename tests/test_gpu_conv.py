@@ -1,0 +1,218 @@
+"""GPU parity of the implicit-GEMM MFMA product (ien_multiply_ex,
+ien_multiply, ien_conv3) against the oracle's gemm::multiply / conv3 on the
+same seeded, f16-representable inputs.
+
+The oracle sums in f32 in the reference's order; the GPU sums f16 products
+in f32 on MFMA in another order and stores f16.  Bound: |gpu - oracle| <=
+2e-3 |oracle| + 2e-3 for f16 outputs (half an f16 ulp is 2^-11 relative,
+plus reordering), 1e-4 (1 + |oracle|) for f32 outputs.
+"""
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+def f16(a):
+    return np.asarray(a, np.float32).astype(np.float16).astype(np.float32)
+
+
+def case(seed, h, w, c, n, taps):
+    rng = np.random.default_rng(seed)
+    x = f16(rng.standard_normal((h, w, c)))
+    wt = f16(rng.standard_normal((taps * c, n)) / np.sqrt(taps * c))
+    b = rng.standard_normal(n).astype(np.float32) * 0.1
+    return x, wt, b
+
+
+def run_gpu(ctx, x, wt, b, size=3, step=1, pad=0, offsets=None, act=0, slope=None, nchw_in=False,
+            nchw_out=False, out_f32=False, init=None, row0=0, rows=None, stride_pad=0):
+    import torch
+    import ien
+
+    h, wd, c = x.shape
+    n = wt.shape[1]
+    if offsets is None:
+        oh, ow = (h - 1) // step + 1, (wd - 1) // step + 1
+    else:
+        oh, ow = h, wd
+    total = oh * ow
+    rows = total - row0 if rows is None else rows
+    if nchw_in:
+        xt = torch.from_numpy(np.ascontiguousarray(x.transpose(2, 0, 1))).half().cuda()
+        inp = ien.image_input(xt, h, wd, c, layout=ien.NCHW, size=size, step=step, pad=pad, offsets=offsets)
+    else:
+        xs = c + stride_pad
+        xp = np.zeros((h, wd, xs), np.float32)
+        xp[..., :c] = x
+        xt = torch.from_numpy(xp).half().cuda()
+        inp = ien.image_input(xt, h, wd, c, stride=xs, size=size, step=step, pad=pad, offsets=offsets)
+    m = ien.Matrix(ctx, wt, b)
+    dt = torch.float32 if out_f32 else torch.float16
+    if nchw_out:
+        out = torch.zeros((n, rows), dtype=dt, device="cuda")
+        if init is not None:
+            out.copy_(torch.from_numpy(init[row0:row0 + rows].T.copy()))
+        ostride = rows
+    else:
+        ostride = n + stride_pad
+        out = torch.zeros((rows, ostride), dtype=dt, device="cuda")
+        if init is not None:
+            out[:, :n].copy_(torch.from_numpy(init[row0:row0 + rows]))
+    sl = None if slope is None else torch.from_numpy(slope).cuda()
+    ien.multiply_ex(ctx, inp, row0, rows, m, out, ostride, layout=ien.NCHW if nchw_out else ien.NHWC,
+                    out_f32=out_f32, act=act, slope=sl, accumulate=init is not None)
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy()
+    got = got.T if nchw_out else got[:, :n]
+    m.free()
+    return got
+
+
+def want_cpu(oracle, x, wt, b, size=3, step=1, pad=0, offsets=None, act=0, slope=None, init=None):
+    import ien
+
+    oact = {ien.ACT_NONE: oracle.ACT_NONE, ien.ACT_RELU: oracle.ACT_RELU, ien.ACT_GELU: oracle.ACT_GELU}
+    y = oracle.multiply_conv(x, wt, b, size=size, step=step, pad=pad, offsets=offsets,
+                             act=oact.get(act, oracle.ACT_NONE),
+                             out=None if init is None else init, accumulate=init is not None)
+    y = y.reshape(-1, wt.shape[1])
+    if act == ien.ACT_PRELU:
+        y = np.where(y < 0, y * slope[None, :], y)
+    if act == ien.ACT_SIGMOID:
+        y = oracle.sigmoid(y)
+    return y
+
+
+def close(got, want, f32=False):
+    err = np.abs(got - want)
+    bound = (1e-4 * (1 + np.abs(want))) if f32 else (2e-3 * np.abs(want) + 2e-3)
+    bad = err > bound
+    assert not bad.any(), f"{bad.sum()} of {bad.size} off; max err {err.max():.3g}"
+
+
+@pytest.mark.parametrize("h,w,c,n", [(8, 96, 64, 64), (12, 192, 64, 48), (7, 45, 64, 64), (9, 33, 32, 80),
+                                     (5, 40, 128, 128), (4, 17, 48, 16)])
+def test_conv3x3_nhwc(ctx, oracle, h, w, c, n):
+    x, wt, b = case(1, h, w, c, n, 9)
+    close(run_gpu(ctx, x, wt, b), want_cpu(oracle, x, wt, b))
+
+
+@pytest.mark.parametrize("c", [3, 4, 8, 16])
+def test_conv3x3_few_channels(ctx, oracle, c):
+    x, wt, b = case(2, 11, 37, c, 64, 9)
+    close(run_gpu(ctx, x, wt, b), want_cpu(oracle, x, wt, b))
+
+
+@pytest.mark.parametrize("act", [1, 2, 3, 4])
+def test_activations_and_accumulate(ctx, oracle, act):
+    import ien
+
+    x, wt, b = case(3, 6, 40, 64, 64, 9)
+    slope = np.linspace(0.05, 0.5, 64).astype(np.float32)
+    init = f16(np.random.default_rng(9).standard_normal((6 * 40, 64)))
+    got = run_gpu(ctx, x, wt, b, act=act, slope=slope, init=init)
+    want = want_cpu(oracle, x, wt, b, act=act, slope=slope, init=init)
+    close(got, want)
+
+
+def test_nchw_in_and_out(ctx, oracle):
+    import ien
+
+    x, wt, b = case(4, 16, 96, 64, 64, 9)
+    want = want_cpu(oracle, x, wt, b)
+    close(run_gpu(ctx, x, wt, b, nchw_in=True, nchw_out=True), want)
+    close(run_gpu(ctx, x, wt, b, nchw_in=True, nchw_out=True, out_f32=True), want, f32=False)
+
+
+def test_f32_output_and_strides(ctx, oracle):
+    x, wt, b = case(5, 9, 50, 32, 40, 9)
+    want = want_cpu(oracle, x, wt, b)
+    close(run_gpu(ctx, x, wt, b, out_f32=True, stride_pad=8), want, f32=True)
+
+
+def test_row_range(ctx, oracle):
+    x, wt, b = case(6, 10, 30, 64, 64, 9)
+    want = want_cpu(oracle, x, wt, b)
+    got = run_gpu(ctx, x, wt, b, row0=47, rows=133)
+    close(got, want[47:180])
+
+
+@pytest.mark.parametrize("pad", [0, 1])
+def test_stride2(ctx, oracle, pad):
+    x, wt, b = case(7, 13, 34, 64, 32, 9)
+    close(run_gpu(ctx, x, wt, b, step=2, pad=pad), want_cpu(oracle, x, wt, b, step=2, pad=pad))
+
+
+def test_reflect_3x3(ctx, oracle):
+    x, wt, b = case(8, 9, 70, 64, 64, 9)
+    close(run_gpu(ctx, x, wt, b, pad=1), want_cpu(oracle, x, wt, b, pad=1))
+
+
+@pytest.mark.parametrize("c,pad", [(4, 1), (64, 1), (64, 0)])
+def test_conv7x7(ctx, oracle, c, pad):
+    x, wt, b = case(9, 12, 40, c, 64, 49)
+    close(run_gpu(ctx, x, wt, b, size=7, pad=pad), want_cpu(oracle, x, wt, b, size=7, pad=pad))
+
+
+def test_1x1(ctx, oracle):
+    x, wt, b = case(10, 16, 64, 256, 512, 1)
+    close(run_gpu(ctx, x, wt, b, size=1), want_cpu(oracle, x, wt, b, size=1))
+
+
+@pytest.mark.parametrize("offsets", [[(0, 0)], [(0, 0), (0, 1)], [(0, 0), (1, 0), (0, 1), (1, 1)]])
+def test_offset_taps(ctx, oracle, offsets):
+    x, wt, b = case(11, 9, 40, 64, 64, len(offsets))
+    close(run_gpu(ctx, x, wt, b, offsets=offsets), want_cpu(oracle, x, wt, b, offsets=offsets))
+
+
+@pytest.mark.parametrize("m,k,n", [(1, 16, 1), (100, 64, 96), (333, 256, 128), (64, 48, 96), (70, 40, 20)])
+def test_rows(ctx, oracle, m, k, n):
+    import torch
+    import ien
+
+    rng = np.random.default_rng(12)
+    a = f16(rng.standard_normal((m, k)))
+    wt = f16(rng.standard_normal((k, n)) / np.sqrt(k))
+    b = rng.standard_normal(n).astype(np.float32)
+    want = oracle.multiply_rows(a, wt, b, act=oracle.ACT_GELU)
+    stride = k + (8 if k % 8 == 0 else 0)
+    ap = np.zeros((m, stride), np.float32)
+    ap[:, :k] = a
+    at = torch.from_numpy(ap).half().cuda()
+    mat = ien.Matrix(ctx, wt, b)
+    out = torch.zeros((m, n), dtype=torch.float16, device="cuda")
+    ien.multiply(ctx, ien.rows_input(at, stride), 0, m, mat, out, n, act=ien.ACT_GELU)
+    torch.cuda.synchronize()
+    close(out.float().cpu().numpy(), want)
+
+
+def test_conv3_finish_prelu(ctx, oracle):
+    import torch
+    import ien
+
+    x, wt, b = case(13, 8, 96, 64, 64, 9)
+    slope = np.full(64, 0.25, np.float32)
+    want = oracle.conv3(x, wt, b, finish=oracle.FINISH_PRELU, slope=slope).reshape(-1, 64)
+    xt = torch.from_numpy(x).half().cuda()
+    m = ien.Matrix(ctx, wt, b)
+    out = torch.zeros((8 * 96, 64), dtype=torch.float16, device="cuda")
+    ien.conv3(ctx, ien.image_input(xt, 8, 96, 64), m, out, 64, finish=ien.ACT_PRELU,
+              slope=torch.from_numpy(slope).cuda())
+    torch.cuda.synchronize()
+    close(out.float().cpu().numpy(), want)
+
+
+def test_errors(ctx):
+    import torch
+    import ien
+
+    x = torch.zeros((4, 4, 64), dtype=torch.float16, device="cuda")
+    m = ien.Matrix(ctx, np.zeros((9 * 32, 16), np.float32))
+    out = torch.zeros((16, 16), dtype=torch.float16, device="cuda")
+    with pytest.raises(ien.IenError) as e:
+        ien.multiply(ctx, ien.image_input(x, 4, 4, 64), 0, 16, m, out, 16)
+    assert e.value.status == ien.ERR_INPUT and "does not match" in str(e.value)
+    with pytest.raises(ien.IenError):
+        ien.multiply(ctx, ien.image_input(x, 4, 4, 32), 10, 16, m, out, 16)
