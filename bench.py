@@ -1,0 +1,248 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X backend: Real-ESRGAN general x4v3
+(SRVGGNetCompact) on a 1x3x256x384 image, per-image latency on one GPU,
+plus the conv sweep's MFMA utilisation and the CPU baseline.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-sweep]
+
+A step is one forward pass of the whole network over one synthetic image
+(seeded uniform [0, 1) input, Kaiming-normal random-init weights) with the
+input already resident in HBM: the 36 launches of a step are replayed from
+one HIP graph.  Prints one JSON line.
+
+roofline: the dominant kernel is the 3x3 64->64 convolution (32 of the 34
+layers, sweep shape 1).  Its algorithmic work per launch is
+2 * 98304 px * 64 * 576 = 7.248 GFLOP; its average duration is measured
+with HIP events on the library's stream over back-to-back launches of that
+layer.  `traffic` (HBM bytes per launch from rocprofv3 FETCH_SIZE /
+WRITE_SIZE, scaled by a copy kernel of known size) is read from
+profiles/conv3x3_64_256x384_hbm_traffic.txt when that summary exists.
+
+cpu_baseline: the oracle -- the C restatement of the reference's CPU f32
+path (crates/realesrgan-native/src/network.rs over native-engine's
+Winograd F(4x4, 3x3) and indirect GEMM) -- timed on this host's cores on
+the same image, median of 3 runs after a warm-up.
+"""
+
+import argparse
+import json
+import os
+import pathlib
+import re
+import sys
+import time
+
+ROOT = pathlib.Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "image-engine-native_amd"))
+
+MFMA_F16_PEAK_TFLOPS = 2516.6  # MI355X dense f16 MFMA
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+METRIC = "ms/image at 1 MI355X per model; conv/attn GEMM MFMA util % of f16 peak"
+
+
+def conv_flops(h, w, cin, cout, size):
+    return 2.0 * h * w * cout * cin * size * size
+
+
+def event_time(fn, reps, stream):
+    """Average milliseconds of one `fn` (which launches on `stream`): `reps`
+    back-to-back calls captured into one HIP graph (so host launch overhead
+    does not starve the GPU), replayed between two HIP events recorded on
+    that stream."""
+    import torch
+
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        for _ in range(reps):
+            fn()
+    graph.replay()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    graph.replay()
+    end.record(stream)
+    end.synchronize()
+    return start.elapsed_time(end) / reps
+
+
+def sweep(ctx, stream, reps):
+    """Each conv-sweep shape (NCHW, f16, N(0,1)) through the library."""
+    import numpy as np
+    import torch
+
+    import ien
+    import synthetic
+
+    results = []
+    for entry in synthetic.SWEEP:
+        (name, kind, cin, cout, size, h, w), x, wt, bias = synthetic.sweep_case(entry[0])
+        xt = torch.from_numpy(x).half().cuda()
+        if kind == "conv":
+            m = ien.Matrix(ctx, wt, bias)
+            inp = ien.image_input(xt, h, w, cin, layout=ien.NCHW, size=size)
+            out = torch.empty((cout, h * w), dtype=torch.float16, device="cuda")
+
+            def launch():
+                ien.multiply_ex(ctx, inp, 0, h * w, m, out, h * w, layout=ien.NCHW)
+
+            flops = conv_flops(h, w, cin, cout, size)
+            nbytes = 2.0 * (cin + cout) * h * w + 2.0 * wt.size
+        else:
+            wd = torch.from_numpy(wt).cuda()
+            bd = torch.from_numpy(bias).cuda()
+            out = torch.empty_like(xt)
+
+            def launch():
+                ien.depthwise(ctx, xt, h, w, cin, ien.NCHW, wd, size, bd, out)
+
+            flops = 2.0 * h * w * cin * size * size
+            nbytes = 2.0 * 2 * cin * h * w + 4.0 * wt.size
+        for _ in range(5):
+            launch()
+        ms = event_time(launch, reps, stream)
+        tflops = flops / (ms * 1e-3) / 1e12
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        row = {"shape": name, "us": round(ms * 1e3, 2), "tflops": round(tflops, 1),
+               "mfma_util_pct": round(100 * tflops / MFMA_F16_PEAK_TFLOPS, 1),
+               "hbm_gbs": round(gbs, 0), "hbm_pct": round(100 * gbs / HBM_PEAK_GBS, 1)}
+        results.append(row)
+        if kind == "conv":
+            m.free()
+    return results
+
+
+def traffic_from_profiles():
+    path = ROOT / "profiles" / "conv3x3_64_256x384_hbm_traffic.txt"
+    if not path.exists():
+        return None
+    m = re.search(r"^traffic_bytes_per_launch:\s*([0-9.eE+]+)", path.read_text(), re.M)
+    return float(m.group(1)) if m else None
+
+
+def cpu_baseline(tensors, image):
+    sys.path.insert(0, str(ROOT))
+    from oracle import oracle as O
+
+    import synthetic
+
+    layers = synthetic.esrgan_layers(tensors)
+    threads = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    O.realesrgan_run(layers, image, threads=threads)  # warm-up
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        O.realesrgan_run(layers, image, threads=threads)
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    cpu = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"value": round(times[1] * 1e3, 1), "unit": "ms/image", "cores": threads, "kind": "port",
+            "sample": f"one full 1x3x256x384 image, median of 3 runs after a warm-up, {threads} threads "
+                      f"on {cpu}; the oracle (C restatement of the reference CPU f32 path)"}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-sweep", action="store_true", help="skip the conv sweep")
+    ap.add_argument("--kernel-reps", type=int, default=100)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py runs on one GPU only: this backend has no multi-GPU path "
+              "(one image per GPU; see the sharding notes of the design)", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    import ien
+    import synthetic
+
+    if not torch.cuda.is_available():
+        sys.exit("bench.py needs a GPU")
+    torch.cuda.set_device(0)
+    ctx = ien.Context(0)
+    stream = ctx.stream
+    H, W = 256, 384
+    tensors = synthetic.esrgan_tensors()
+    image = synthetic.esrgan_image(H, W)
+    model = ien.Model(ctx, ien.MODEL_REALESRGAN, tensors=tensors)
+    d_in = torch.from_numpy(image).cuda()
+    d_out = torch.empty((4 * H, 4 * W, 3), dtype=torch.float32, device="cuda")
+    model.set_graph(True)
+
+    for _ in range(args.warmup):
+        model.run_device(d_in, W, H, d_out)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        model.run_device(d_in, W, H, d_out)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms_per_step = elapsed * 1e3 / args.steps
+    if not bool(torch.isfinite(d_out).all()):
+        sys.exit("non-finite output")
+
+    # Dominant kernel: one body layer (3x3 64->64 + PReLU) at 256x384.
+    w_body, b_body, s_body = synthetic.esrgan_layers(tensors)[1]
+    m = ien.Matrix(ctx, w_body, b_body)
+    slope = torch.from_numpy(s_body).cuda()
+    src = torch.from_numpy(np.random.default_rng(3).standard_normal((H * W, 64))).half().cuda()
+    dst = torch.empty((H * W, 64), dtype=torch.float16, device="cuda")
+    inp = ien.image_input(src, H, W, 64)
+
+    def body():
+        ien.multiply_ex(ctx, inp, 0, H * W, m, dst, 64, act=ien.ACT_PRELU, slope=slope)
+
+    for _ in range(5):
+        body()
+    kms = event_time(body, args.kernel_reps, stream)
+    flops = conv_flops(H, W, 64, 64, 3)
+    achieved = flops / (kms * 1e-3) / 1e12
+    roofline = {"bound": "mfma", "achieved": round(achieved, 1), "peak": MFMA_F16_PEAK_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(achieved / MFMA_F16_PEAK_TFLOPS, 4),
+                "traffic": traffic_from_profiles(),
+                "kernel": "conv_mfma<3,1,4,96,4,2,64,true,false> (3x3 64->64 + PReLU, 256x384)",
+                "kernel_us": round(kms * 1e3, 2), "flop_per_launch": flops}
+    m.free()
+
+    gemm_sweep = None if args.no_sweep else sweep(ctx, stream, args.kernel_reps)
+    cpu = None if args.no_cpu else cpu_baseline(tensors, image)
+
+    line = {
+        "metric": METRIC,
+        "value": round(ms_per_step, 4),
+        "unit": "ms/image",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic (seeded uniform [0,1) image, Kaiming-normal random-init weights)",
+        "config": {"workload": "Real-ESRGAN general x4v3 (SRVGGNetCompact), 1x3x256x384 -> 1x3x1024x1536",
+                   "global_batch": 1, "height": H, "width": W, "layers": 34, "parallelism": "none",
+                   "execution": "one HIP graph per image"},
+        "images_per_s": round(1e3 / ms_per_step, 1),
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "gemm_sweep": gemm_sweep,
+        "device": ctx.name,
+    }
+    model.free()
+    ctx.close()
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

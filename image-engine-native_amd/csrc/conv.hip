@@ -13,15 +13,21 @@
 //
 // One workgroup = 4 wave64s computes a TR x TC tile of output pixels for
 // BN = 32 * NBW * NSPLIT output channels.  Per chunk of CK input channels it
-// stages the tile's input halo ((TR-1) S + KS) x ((TC-1) S + KS) pixels in
-// LDS, NHWC with a padded pixel stride (CK + 8 halves) so the A-fragment
-// reads (16 bytes per lane, 32 consecutive pixels) hit distinct banks, then
-// walks taps x 16-channel steps: A fragments from LDS (one ds_read_b128 per
-// lane), B fragments straight from the packed weights in global memory
-// (L2-resident, one 16-byte load per lane, prefetched a step ahead), one
-// MFMA per (M-block, N-block).  The epilogue stages f32 results per wave in
-// LDS and writes 16-byte vectors: bias, the old output when accumulating,
-// then the activation, as gemm.rs:583-666 orders them.
+// stages in LDS
+//   - the tile's input halo, ((TR-1) S + KS) x ((TC-1) S + KS) pixels,
+//     NHWC with a padded pixel stride (CK + 8 halves, so the 32 lanes of an
+//     A-fragment read -- 16 bytes each, 32 consecutive pixels -- hit
+//     distinct banks), and
+//   - the chunk's weights, already packed as MFMA B fragments,
+// with every thread keeping 8 independent 16-byte loads in flight (a
+// workgroup fills its CU's LDS, so one wave per SIMD has to hide its own
+// latency).  Then it walks taps x 16-channel steps fully unrolled: the LDS
+// offset of every fragment is a compile-time constant from one base
+// address, fragments are double-buffered in registers, and each step issues
+// MBW x NBW MFMAs.  The epilogue adds the bias and applies the activation in
+// the accumulators (bias, old output when accumulating, activation: the
+// order of gemm.rs:583-666), stages f32 results per wave in LDS and writes
+// 16-byte vectors.
 //
 // Block ids are remapped so that each XCD (blocks are dealt round-robin to
 // the 8 XCDs) gets a contiguous band of tiles: neighbouring tiles share halo
@@ -41,14 +47,14 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 struct ConvArgs {
   const uint16_t *x;
   int H, W, C;
-  long xs;
+  int xs;  // NHWC: halves between pixels; NCHW: halves between planes
   int rows_mode;
-  long M;  // rows_mode: number of input rows (= output pixels)
+  int M;  // rows_mode: number of input rows (= output pixels)
   int pad_reflect;
   int noff;
   int offy[4], offx[4];
   int OH, OW;
-  long p_begin, p_end;  // output pixel range [row0, row0 + rows)
+  int p_begin, p_end;  // output pixel range [row0, row0 + rows)
   int ty_begin, tiles_x, tiles_y, tiles_n;
   const uint16_t *wp;
   int KB;  // k fragments (16) of the packed weights
@@ -57,7 +63,7 @@ struct ConvArgs {
   const float *bias;
   const float *slope;
   void *y;
-  long ys;
+  int ys;
   int out_nchw, out_f32, act, accumulate;
 };
 
@@ -95,10 +101,11 @@ __device__ __forceinline__ float sigmoid_f(float x) {
   return x > 0.0f ? 1.0f - s : s;
 }
 
-__device__ __forceinline__ float activate(float v, int act, const float *slope, int n) {
+// `slope` is the PReLU slope of this value's channel.
+__device__ __forceinline__ float activate(float v, int act, float slope) {
   switch (act) {
     case IEN_ACT_RELU: return v > 0.0f ? v : 0.0f;
-    case IEN_ACT_PRELU: return v < 0.0f ? v * slope[n] : v;
+    case IEN_ACT_PRELU: return v < 0.0f ? v * slope : v;
     case IEN_ACT_GELU: return gelu_f(v);
     case IEN_ACT_SIGMOID: return sigmoid_f(v);
     default: return v;
@@ -124,35 +131,65 @@ __device__ __forceinline__ int xcd_remap(int b, int nblocks) {
   return (b & 7) * (nblocks >> 3) + (b >> 3);
 }
 
+// Global -> LDS staging, BATCH independent loads in flight per thread
+// before any of them is written: with one wave per SIMD nothing else hides
+// a load's latency, so a load-wait-store loop would pay it every time.
+// `load(e)` must load unconditionally from a valid address (padding is
+// decided in `store(e, v)`), so that no branch separates the loads.
+template <int BATCH, typename Load, typename Store>
+__device__ __forceinline__ void staged_copy(int total, int tid, Load load, Store store) {
+  for (int base = tid; base < total; base += 256 * BATCH) {
+    u32x4 v[BATCH];
+#pragma unroll
+    for (int b = 0; b < BATCH; b++) v[b] = load(min(base + b * 256, total - 1));
+#pragma unroll
+    for (int b = 0; b < BATCH; b++) {
+      const int e = base + b * 256;
+      if (e < total) store(e, v[b]);
+    }
+  }
+}
+
 template <int KS, int S, int TR, int TC, int MSPLIT, int NBW, int CK, bool VEC, bool IN_NCHW>
 struct ConvCfg {
   static constexpr int NSPLIT = 4 / MSPLIT;
   static constexpr int BN = 32 * NBW * NSPLIT;
+  static constexpr int NBT = BN / 32;           // 32-channel blocks per tile
   static constexpr int MB = TR * TC / 32;       // M-blocks per tile
   static constexpr int MBW = MB / MSPLIT;       // M-blocks per wave
   static constexpr int EXT = KS == 0 ? 2 : KS;  // offset taps read one pixel on
+  static constexpr int TMAX = KS == 0 ? 4 : KS * KS;
   static constexpr int HR = (TR - 1) * S + EXT;
   static constexpr int HC = (TC - 1) * S + EXT;
   static constexpr int CKP = VEC ? CK + 8 : CK;  // LDS halves per halo pixel
   static constexpr int HALO_HALVES = HR * HC * CKP;
-  static constexpr int STAGE_FLOATS = 4 * MBW * 32 * 36;  // 4 waves x (MBW*32 px) x (32+4)
-  static constexpr int LDS_BYTES =
-      HALO_HALVES * 2 > STAGE_FLOATS * 4 ? HALO_HALVES * 2 : STAGE_FLOATS * 4;
+  // 16-deep k steps of one chunk: VEC walks taps x CK/16; otherwise K is
+  // flattened over (tap, channel) and rounded up to 16.
+  static constexpr int KSTEPS = VEC ? TMAX * (CK / 16) : (TMAX * CK + 15) / 16;
+  static constexpr int B_HALVES = NBT * KSTEPS * 512;  // B fragments of the chunk
+  // Epilogue staging per wave: NHWC [px][NBW*32 + 8] or NCHW [NBW*32][px + 4] floats.
+  static constexpr int STAGE_NHWC = MBW * 32 * (NBW * 32 + 8);
+  static constexpr int STAGE_NCHW = NBW * 32 * (MBW * 32 + 4);
+  static constexpr int STAGE = STAGE_NHWC > STAGE_NCHW ? STAGE_NHWC : STAGE_NCHW;
+  static constexpr int MAIN_BYTES = (HALO_HALVES + B_HALVES) * 2;
+  static constexpr int LDS_BYTES = MAIN_BYTES > 4 * STAGE * 4 ? MAIN_BYTES : 4 * STAGE * 4;
   static_assert(MB % MSPLIT == 0, "M-blocks must split evenly over waves");
   static_assert(TC % 32 == 0, "tile columns are whole M-blocks");
+  static_assert(!VEC || CK % 16 == 0, "16-channel steps");
   static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
 };
 
 template <int KS, int S, int TR, int TC, int MSPLIT, int NBW, int CK, bool VEC, bool IN_NCHW>
 __global__ __launch_bounds__(256) void conv_mfma(ConvArgs a) {
   using Cfg = ConvCfg<KS, S, TR, TC, MSPLIT, NBW, CK, VEC, IN_NCHW>;
-  constexpr int HR = Cfg::HR, HC = Cfg::HC, CKP = Cfg::CKP, MBW = Cfg::MBW;
+  constexpr int HR = Cfg::HR, HC = Cfg::HC, CKP = Cfg::CKP, MBW = Cfg::MBW, NBT = Cfg::NBT;
+  constexpr int KSTEPS = Cfg::KSTEPS;
   constexpr int P = KS == 0 ? 0 : KS / 2;
   __shared__ __attribute__((aligned(16))) unsigned char lds_raw[Cfg::LDS_BYTES];
   uint16_t *halo = (uint16_t *)lds_raw;
+  uint16_t *bl = halo + Cfg::HALO_HALVES;
 
-  const int nblocks = gridDim.x;
-  const int bid = xcd_remap(blockIdx.x, nblocks);
+  const int bid = xcd_remap(blockIdx.x, gridDim.x);
   const int tn = bid % a.tiles_n;
   const int t = bid / a.tiles_n;
   const int tx = t % a.tiles_x;
@@ -160,8 +197,19 @@ __global__ __launch_bounds__(256) void conv_mfma(ConvArgs a) {
   const int oy0 = ty * TR, ox0 = tx * TC;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int mg = wave % MSPLIT, ng = wave / MSPLIT;
-  const int nblk0 = tn * (Cfg::BN / 32) + ng * NBW;  // first 32-channel block of this wave
+  const int nblk_tile = tn * NBT;          // first 32-channel block of the tile
+  const int nblk0 = nblk_tile + ng * NBW;  // first 32-channel block of this wave
   const int T = KS == 0 ? a.noff : KS * KS;
+
+  // Bias and PReLU slope of this lane's accumulator column, per N-block:
+  // loaded now, used after the products.
+  float bias_r[NBW], slope_r[NBW];
+#pragma unroll
+  for (int j = 0; j < NBW; j++) {
+    const int n = (nblk0 + j) * 32 + (lane & 31);  // < NB * 32: the bias is padded
+    bias_r[j] = a.bias[n];
+    slope_r[j] = a.act == IEN_ACT_PRELU ? a.slope[min(n, a.N - 1)] : 0.0f;
+  }
 
   floatx16 acc[MBW][NBW];
 #pragma unroll
@@ -175,9 +223,9 @@ __global__ __launch_bounds__(256) void conv_mfma(ConvArgs a) {
   const int iy0 = oy0 * S - P, ix0 = ox0 * S - P;
 
   // Offset of input pixel (iy, ix), or -1 for a zero (padding, outside).
-  auto resolve = [&](int iy, int ix) -> long {
+  auto resolve = [&](int iy, int ix) -> int {
     if (a.rows_mode) {
-      long r = (long)iy * a.W + ix;
+      const int r = iy * a.W + ix;
       if (iy < 0 || ix < 0 || ix >= a.W || r >= a.M) return -1;
       return r * a.xs;
     }
@@ -188,230 +236,368 @@ __global__ __launch_bounds__(256) void conv_mfma(ConvArgs a) {
       iy = min(max(reflect_idx(iy, a.H), 0), a.H - 1);
       ix = min(max(reflect_idx(ix, a.W), 0), a.W - 1);
     }
-    long p = (long)iy * a.W + ix;
+    const int p = iy * a.W + ix;
     return IN_NCHW ? p : p * a.xs;
   };
 
+  // This wave's A-fragment base per M-block: halo pixel of tap (0, 0) for
+  // the lane's pixel, plus the lane's 8-channel half of a 16-channel step.
+  int abase[MBW];
+#pragma unroll
+  for (int i = 0; i < MBW; i++) {
+    const int mb = mg * MBW + i;
+    const int r = mb / (TC / 32), cx = (mb % (TC / 32)) * 32 + (lane & 31);
+    abase[i] = ((r * S) * HC + cx * S) * CKP + (VEC ? 8 * (lane >> 5) : 0);
+  }
+
   for (int c0 = 0; c0 < a.C; c0 += CK) {
-    const int cc = min(CK, a.C - c0);
+    const int cc = min(CK, a.C - c0);  // == CK when VEC
     __syncthreads();
     // ---- global -> LDS: the halo of this channel chunk ----
-    if (VEC && !IN_NCHW) {
-      const int vpp = cc >> 3;  // 16-byte vectors per pixel
-      const int total = HR * HC * vpp;
-      for (int e = tid; e < total; e += 256) {
-        int hp = e / vpp, v = e - hp * vpp;
-        int hy = hp / HC, hx = hp - hy * HC;
-        long off = resolve(iy0 + hy, ix0 + hx);
-        u32x4 val = {0u, 0u, 0u, 0u};
-        if (off >= 0) val = *(const u32x4 *)(a.x + off + c0 + 8 * v);
-        *(u32x4 *)(halo + hp * CKP + 8 * v) = val;
-      }
-    } else if (!IN_NCHW) {
-      const int total = HR * HC * cc;
-      for (int e = tid; e < total; e += 256) {
-        int hp = e / cc, c = e - hp * cc;
-        int hy = hp / HC, hx = hp - hy * HC;
-        long off = resolve(iy0 + hy, ix0 + hx);
-        halo[hp * CKP + c] = off >= 0 ? a.x[off + c0 + c] : (uint16_t)0;
-      }
+    if constexpr (VEC && !IN_NCHW) {
+      auto pixel = [&](int hp) {
+        const int hy = hp / HC, hx = hp - hy * HC;
+        return resolve(iy0 + hy, ix0 + hx);
+      };
+      staged_copy<8>(
+          HR * HC * (CK / 8), tid,
+          [&](int e) -> u32x4 {
+            const int hp = e / (CK / 8), v = e % (CK / 8);
+            const int off = pixel(hp);
+            return *(const u32x4 *)(a.x + (off >= 0 ? off : 0) + c0 + 8 * v);
+          },
+          [&](int e, u32x4 val) {
+            const int hp = e / (CK / 8), v = e % (CK / 8);
+            if (pixel(hp) < 0) val = u32x4{0u, 0u, 0u, 0u};
+            *(u32x4 *)(halo + hp * CKP + 8 * v) = val;
+          });
+    } else if constexpr (!IN_NCHW) {
+      // Few channels: one half per element.
+      auto where = [&](int e, int &hp, int &c) {
+        hp = e / cc;
+        c = e - hp * cc;
+        const int hy = hp / HC, hx = hp - hy * HC;
+        return resolve(iy0 + hy, ix0 + hx);
+      };
+      staged_copy<8>(
+          HR * HC * cc, tid,
+          [&](int e) -> u32x4 {
+            int hp, c;
+            const int off = where(e, hp, c);
+            return u32x4{(uint32_t)a.x[(off >= 0 ? off : 0) + c0 + c], 0u, 0u, 0u};
+          },
+          [&](int e, u32x4 val) {
+            int hp, c;
+            const int off = where(e, hp, c);
+            halo[hp * CKP + c] = off >= 0 ? (uint16_t)val[0] : (uint16_t)0;
+          });
     } else {
-      // NCHW: pixels fastest, so neighbouring lanes read neighbouring halves.
-      const int total = HR * HC * cc;
-      for (int e = tid; e < total; e += 256) {
-        int c = e / (HR * HC), hp = e - c * (HR * HC);
-        int hy = hp / HC, hx = hp - hy * HC;
-        long off = resolve(iy0 + hy, ix0 + hx);
-        halo[hp * CKP + c] = off >= 0 ? a.x[(long)(c0 + c) * a.xs + off] : (uint16_t)0;
+      // NCHW.  Fast path (rows of whole 16-byte groups, zero padding): 8
+      // neighbouring pixels of one channel row per load; a group lies wholly
+      // inside or wholly outside the image.  Otherwise one half per element.
+      const bool fast = !a.rows_mode && !a.pad_reflect && (a.W & 7) == 0 && (a.xs & 7) == 0 &&
+                        (((uintptr_t)a.x) & 15) == 0;
+      if (fast) {
+        auto floor8 = [](int v) { return v >= 0 ? v / 8 : -((7 - v) / 8); };
+        const int g0 = floor8(ix0);
+        const int groups = floor8(ix0 + HC - 1) + 1 - g0;
+        auto where = [&](int e, int &hy, int &c, int &gx) {
+          const int g = e % groups, rest = e / groups;
+          hy = rest % HR;
+          c = rest / HR;
+          gx = (g0 + g) * 8;
+          const int iy = iy0 + hy;
+          return iy >= 0 && iy < a.H && gx >= 0 && gx < a.W;
+        };
+        staged_copy<8>(
+            cc * HR * groups, tid,
+            [&](int e) -> u32x4 {
+              int hy, c, gx;
+              const bool ok = where(e, hy, c, gx);
+              const int off = ok ? (c0 + c) * a.xs + (iy0 + hy) * a.W + gx : 0;
+              return *(const u32x4 *)(a.x + off);
+            },
+            [&](int e, u32x4 val) {
+              int hy, c, gx;
+              if (!where(e, hy, c, gx)) val = u32x4{0u, 0u, 0u, 0u};
+              uint16_t v8[8];
+              __builtin_memcpy(v8, &val, 16);
+#pragma unroll
+              for (int q = 0; q < 8; q++) {
+                const int hx = gx + q - ix0;
+                if (hx >= 0 && hx < HC) halo[(hy * HC + hx) * CKP + c] = v8[q];
+              }
+            });
+      } else {
+        auto where = [&](int e, int &hp, int &c) {
+          c = e / (HR * HC);
+          hp = e - c * (HR * HC);
+          const int hy = hp / HC, hx = hp - hy * HC;
+          return resolve(iy0 + hy, ix0 + hx);
+        };
+        staged_copy<8>(
+            cc * HR * HC, tid,
+            [&](int e) -> u32x4 {
+              int hp, c;
+              const int off = where(e, hp, c);
+              return u32x4{(uint32_t)a.x[(c0 + c) * a.xs + (off >= 0 ? off : 0)], 0u, 0u, 0u};
+            },
+            [&](int e, u32x4 val) {
+              int hp, c;
+              const int off = where(e, hp, c);
+              halo[hp * CKP + c] = off >= 0 ? (uint16_t)val[0] : (uint16_t)0;
+            });
       }
+    }
+
+    // ---- global -> LDS: this chunk's weight fragments, [block][step] ----
+    {
+      const int steps = VEC ? T * (CK / 16) : (T * cc + 15) / 16;
+      staged_copy<8>(
+          NBT * steps * 64, tid,
+          [&](int e) -> u32x4 {
+            const int f = e >> 6, l = e & 63;
+            const int jn = f / steps, s = f - jn * steps;
+            int kb = s;  // one chunk holds all channels: fragments in order
+            if (VEC) {
+              const int tap = s / (CK / 16), kc = s % (CK / 16);
+              kb = tap * (a.C / 16) + c0 / 16 + kc;
+            }
+            return *(const u32x4 *)(a.wp + ((nblk_tile + jn) * a.KB + kb) * 512 + l * 8);
+          },
+          [&](int e, u32x4 v) {
+            const int f = e >> 6, l = e & 63;
+            const int jn = f / steps, s = f - jn * steps;
+            *(u32x4 *)(bl + (jn * KSTEPS + s) * 512 + l * 8) = v;
+          });
     }
     __syncthreads();
 
-    // ---- MFMA over taps x 16-channel steps of this chunk ----
-    if (VEC) {
-      const int kcs = cc >> 4;
-      const int steps = T * kcs;
-      const uint16_t *wbase = a.wp + (long)lane * 8;
-      auto kb_of = [&](int s) {
-        int tap = s / kcs, kc = s - tap * kcs;
-        return (tap * a.C + c0) / 16 + kc;
+    const uint16_t *bw = bl + ng * NBW * KSTEPS * 512 + lane * 8;
+    auto mma = [&](const half8 *av, const half8 *bv) {
+#pragma unroll
+      for (int i = 0; i < MBW; i++)
+#pragma unroll
+        for (int j = 0; j < NBW; j++)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[i], bv[j], acc[i][j], 0, 0, 0);
+    };
+    if constexpr (VEC && KS > 0) {
+      // ---- taps x 16-channel steps, unrolled: constant LDS offsets ----
+      auto frag = [&](int s, half8 *av, half8 *bv) {
+        const int tap = s / (CK / 16), kc = s % (CK / 16);
+        const int dy = tap / KS, dx = tap % KS;
+        const int off = (dy * HC + dx) * CKP + kc * 16;
+#pragma unroll
+        for (int i = 0; i < MBW; i++) av[i] = *(const half8 *)(halo + abase[i] + off);
+#pragma unroll
+        for (int j = 0; j < NBW; j++) bv[j] = *(const half8 *)(bw + (j * KSTEPS + s) * 512);
       };
-      half8 bcur[NBW], bnext[NBW];
+      half8 av[2][MBW], bv[2][NBW];
+      frag(0, av[0], bv[0]);
 #pragma unroll
-      for (int j = 0; j < NBW; j++)
-        bcur[j] = *(const half8 *)(wbase + ((long)(nblk0 + j) * a.KB + kb_of(0)) * 512);
+      for (int s = 0; s < KSTEPS; s++) {
+        if (s + 1 < KSTEPS) frag(s + 1, av[(s + 1) & 1], bv[(s + 1) & 1]);
+        mma(av[s & 1], bv[s & 1]);
+      }
+    } else if constexpr (VEC) {
+      // Offset taps (transposed-conv phases): at most 4, known at run time.
+      const int steps = T * (CK / 16);
       for (int s = 0; s < steps; s++) {
-        if (s + 1 < steps) {
-          int kbn = kb_of(s + 1);
+        const int tap = s / (CK / 16), kc = s % (CK / 16);
+        const int off = (a.offy[tap] * HC + a.offx[tap]) * CKP + kc * 16;
+        half8 av[MBW], bv[NBW];
 #pragma unroll
-          for (int j = 0; j < NBW; j++)
-            bnext[j] = *(const half8 *)(wbase + ((long)(nblk0 + j) * a.KB + kbn) * 512);
-        }
-        const int tap = s / kcs, kc = s - tap * kcs;
-        int dy, dx;
-        if constexpr (KS == 0) {
-          dy = a.offy[tap];
-          dx = a.offx[tap];
-        } else {
-          dy = tap / KS;
-          dx = tap - dy * KS;
-        }
-        half8 av[MBW];
+        for (int i = 0; i < MBW; i++) av[i] = *(const half8 *)(halo + abase[i] + off);
 #pragma unroll
-        for (int i = 0; i < MBW; i++) {
-          const int mb = mg * MBW + i;
-          const int r = mb / (TC / 32), cx = (mb % (TC / 32)) * 32 + (lane & 31);
-          const int hp = (r * S + dy) * HC + cx * S + dx;
-          av[i] = *(const half8 *)(halo + hp * CKP + kc * 16 + 8 * (lane >> 5));
-        }
-#pragma unroll
-        for (int i = 0; i < MBW; i++)
-#pragma unroll
-          for (int j = 0; j < NBW; j++)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[i], bcur[j], acc[i][j], 0, 0, 0);
-        if (s + 1 < steps) {
-#pragma unroll
-          for (int j = 0; j < NBW; j++) bcur[j] = bnext[j];
-        }
+        for (int j = 0; j < NBW; j++) bv[j] = *(const half8 *)(bw + (j * KSTEPS + s) * 512);
+        mma(av, bv);
       }
     } else {
-      // Small channel counts (one chunk holds them all): K flattened over
+      // Few channels (one chunk holds them all): K flattened over
       // (tap, channel) as the reference orders it, 16 at a time.
       const int K = T * cc;
       const int kbs = (K + 15) / 16;
       for (int kb = 0; kb < kbs; kb++) {
-        half8 bv[NBW];
+        half8 av[MBW], bv[NBW];
 #pragma unroll
-        for (int j = 0; j < NBW; j++)
-          bv[j] = *(const half8 *)(a.wp + ((long)(nblk0 + j) * a.KB + kb) * 512 + lane * 8);
-        half8 av[MBW];
+        for (int j = 0; j < NBW; j++) bv[j] = *(const half8 *)(bw + (j * KSTEPS + kb) * 512);
 #pragma unroll
-        for (int i = 0; i < MBW; i++) {
-          const int mb = mg * MBW + i;
-          const int r = mb / (TC / 32), cx = (mb % (TC / 32)) * 32 + (lane & 31);
+        for (int q = 0; q < 8; q++) {
+          const int k = kb * 16 + 8 * (lane >> 5) + q;
+          const int kk = k < K ? k : 0;
+          const int tap = kk / cc, c = kk - tap * cc;
+          int dy, dx;
+          if constexpr (KS == 0) {
+            dy = a.offy[tap];
+            dx = a.offx[tap];
+          } else {
+            dy = tap / KS;
+            dx = tap - dy * KS;
+          }
+          const int off = (dy * HC + dx) * CKP + c;
 #pragma unroll
-          for (int q = 0; q < 8; q++) {
-            int k = kb * 16 + 8 * (lane >> 5) + q;
-            uint16_t hv = 0;
-            if (k < K) {
-              int tap = k / cc, c = k - tap * cc;
-              int dy, dx;
-              if constexpr (KS == 0) {
-                dy = a.offy[tap];
-                dx = a.offx[tap];
-              } else {
-                dy = tap / KS;
-                dx = tap - dy * KS;
-              }
-              hv = halo[((r * S + dy) * HC + cx * S + dx) * CKP + c];
-            }
+          for (int i = 0; i < MBW; i++) {
+            uint16_t hv = k < K ? halo[abase[i] + off] : (uint16_t)0;
             _Float16 f;
             __builtin_memcpy(&f, &hv, 2);
             av[i][q] = f;
           }
         }
-#pragma unroll
-        for (int i = 0; i < MBW; i++)
-#pragma unroll
-          for (int j = 0; j < NBW; j++)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[i], bv[j], acc[i][j], 0, 0, 0);
+        mma(av, bv);
       }
     }
   }
 
-  // ---- epilogue: stage per wave in LDS, then 8 outputs per lane ----
-  __syncthreads();
-  float *stage = (float *)lds_raw + wave * (MBW * 32 * 36);
-#pragma unroll
-  for (int j = 0; j < NBW; j++) {
-    const int nbase = (nblk0 + j) * 32;
-    if (nbase >= a.N) break;  // wave-uniform
-    // C fragment: lane holds column n = lane % 32 and rows
-    // 8 (r / 4) + 4 (lane / 32) + r % 4 of each 32x32 block.
+  // ---- epilogue -----------------------------------------------------------
+  // Bias (and, when not accumulating, the activation) in the accumulators;
+  // then a per-wave f32 staging in LDS and 8 outputs per lane per store.
+  __syncthreads();  // every wave is done with the halo and the weights
+  float *stage = (float *)lds_raw + wave * Cfg::STAGE;
+  auto finish = [&](auto f) {
 #pragma unroll
     for (int i = 0; i < MBW; i++)
 #pragma unroll
-      for (int r = 0; r < 16; r++) {
-        int m = 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        stage[(i * 32 + m) * 36 + (lane & 31)] = acc[i][j][r];
-      }
-    __builtin_amdgcn_s_waitcnt(0);
+      for (int j = 0; j < NBW; j++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) acc[i][j][r] = f(acc[i][j][r] + bias_r[j], slope_r[j]);
+  };
+  // One loop per activation (uniform per launch), not a switch per value.
+  const int act_now = a.accumulate ? IEN_ACT_NONE : a.act;
+  if (act_now == IEN_ACT_RELU)
+    finish([](float v, float) { return v > 0.0f ? v : 0.0f; });
+  else if (act_now == IEN_ACT_PRELU)
+    finish([](float v, float sl) { return v < 0.0f ? v * sl : v; });
+  else if (act_now == IEN_ACT_GELU)
+    finish([](float v, float) { return gelu_f(v); });
+  else if (act_now == IEN_ACT_SIGMOID)
+    finish([](float v, float) { return sigmoid_f(v); });
+  else
+    finish([](float v, float) { return v; });
+  // C fragment: lane holds column n = lane % 32 and rows
+  // 8 (r / 4) + 4 (lane / 32) + r % 4 of each 32 x 32 block.
+  if (!a.out_nchw) {
+    constexpr int SP = NBW * 32 + 8;  // floats per staged pixel
+#pragma unroll
+    for (int i = 0; i < MBW; i++)
+#pragma unroll
+      for (int j = 0; j < NBW; j++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+          const int m = 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+          stage[(i * 32 + m) * SP + j * 32 + (lane & 31)] = acc[i][j][r];
+        }
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes done
     __builtin_amdgcn_wave_barrier();
-    const int g = lane & 3;  // 8-channel group
-    const int n = nbase + 8 * g;
-    for (int q = lane >> 2; q < MBW * 32; q += 16) {
+    constexpr int GROUPS = NBW * 4;  // 8-channel groups per staged pixel
+    for (int item = lane; item < MBW * 32 * GROUPS; item += 64) {
+      const int q = item / GROUPS, g = item % GROUPS;
       const int mb = mg * MBW + q / 32;
       const int r = mb / (TC / 32), cx = (mb % (TC / 32)) * 32 + (q & 31);
       const int oy = oy0 + r, ox = ox0 + cx;
-      long p = (long)oy * a.OW + ox;
-      bool valid = oy < a.OH && ox < a.OW && p >= a.p_begin && p < a.p_end;
-      if (!valid || n >= a.N) continue;
-      const long rel = p - a.p_begin;
-      float v[8];
-      const float4v s0 = *(const float4v *)(stage + q * 36 + 8 * g);
-      const float4v s1 = *(const float4v *)(stage + q * 36 + 8 * g + 4);
-#pragma unroll
-      for (int e = 0; e < 4; e++) {
-        v[e] = s0[e];
-        v[4 + e] = s1[e];
-      }
+      const int p = oy * a.OW + ox;
+      const int n = nblk0 * 32 + 8 * g;
+      if (oy >= a.OH || ox >= a.OW || p < a.p_begin || p >= a.p_end || n >= a.N) continue;
+      const float4v s0 = *(const float4v *)(stage + q * SP + 8 * g);
+      const float4v s1 = *(const float4v *)(stage + q * SP + 8 * g + 4);
+      float v[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
       const int nv = min(8, a.N - n);
-      if (!a.out_nchw) {
-        const long base = rel * a.ys + n;
-        if (a.out_f32) {
-          float *yo = (float *)a.y + base;
-#pragma unroll
-          for (int e = 0; e < 8; e++)
-            if (e < nv) {
-              float o = v[e] + a.bias[n + e];
-              if (a.accumulate) o += yo[e];
-              yo[e] = activate(o, a.act, a.slope, n + e);
-            }
-        } else {
-          uint16_t *yo = (uint16_t *)a.y + base;
-          const bool vec = nv == 8 && (((uintptr_t)yo & 15) == 0);
-          uint16_t old[8];
-          if (a.accumulate) {
-            if (vec) {
-              u32x4 ov = *(const u32x4 *)yo;
-              __builtin_memcpy(old, &ov, 16);
-            } else {
-              for (int e = 0; e < nv; e++) old[e] = yo[e];
-            }
-          }
-          uint16_t outv[8];
-#pragma unroll
-          for (int e = 0; e < 8; e++) {
-            float o = v[e] + a.bias[min(n + e, a.N - 1)];
-            if (a.accumulate && e < nv) o += h2f(old[e]);
-            outv[e] = f2h(activate(o, a.act, a.slope, min(n + e, a.N - 1)));
-          }
-          if (vec) {
-            u32x4 ov;
-            __builtin_memcpy(&ov, outv, 16);
-            *(u32x4 *)yo = ov;
-          } else {
-            for (int e = 0; e < nv; e++) yo[e] = outv[e];
-          }
+      const long base = (long)(p - a.p_begin) * a.ys + n;
+      if (a.out_f32) {
+        float *yo = (float *)a.y + base;
+        for (int e = 0; e < nv; e++) {
+          float o = v[e];
+          if (a.accumulate)
+            o = activate(o + yo[e], a.act, a.act == IEN_ACT_PRELU ? a.slope[n + e] : 0.0f);
+          yo[e] = o;
         }
       } else {
-        // NCHW: channel planes `ys` apart.
-        for (int e = 0; e < nv; e++) {
-          const long at = (long)(n + e) * a.ys + rel;
-          float o = v[e] + a.bias[n + e];
-          if (a.out_f32) {
-            float *yo = (float *)a.y + at;
-            if (a.accumulate) o += *yo;
-            *yo = activate(o, a.act, a.slope, n + e);
+        uint16_t *yo = (uint16_t *)a.y + base;
+        const bool vec = nv == 8 && (((uintptr_t)yo & 15) == 0);
+        if (a.accumulate) {
+          uint16_t old[8];
+          if (vec) {
+            u32x4 ov = *(const u32x4 *)yo;
+            __builtin_memcpy(old, &ov, 16);
           } else {
-            uint16_t *yo = (uint16_t *)a.y + at;
-            if (a.accumulate) o += h2f(*yo);
-            *yo = f2h(activate(o, a.act, a.slope, n + e));
+            for (int e = 0; e < nv; e++) old[e] = yo[e];
           }
+#pragma unroll
+          for (int e = 0; e < 8; e++) {
+            const int ne = min(n + e, a.N - 1);
+            v[e] = activate(v[e] + (e < nv ? h2f(old[e]) : 0.0f), a.act,
+                            a.act == IEN_ACT_PRELU ? a.slope[ne] : 0.0f);
+          }
+        }
+        uint16_t outv[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) outv[e] = f2h(v[e]);
+        if (vec) {
+          u32x4 ov;
+          __builtin_memcpy(&ov, outv, 16);
+          *(u32x4 *)yo = ov;
+        } else {
+          for (int e = 0; e < nv; e++) yo[e] = outv[e];
         }
       }
     }
+  } else {
+    constexpr int PXS = MBW * 32 + 4;  // floats per staged channel row
+#pragma unroll
+    for (int i = 0; i < MBW; i++)
+#pragma unroll
+      for (int j = 0; j < NBW; j++)
+#pragma unroll
+        for (int r4 = 0; r4 < 4; r4++) {
+          const int m = 8 * r4 + 4 * (lane >> 5);
+          float4v v4 = {acc[i][j][4 * r4], acc[i][j][4 * r4 + 1], acc[i][j][4 * r4 + 2],
+                        acc[i][j][4 * r4 + 3]};
+          *(float4v *)(stage + (j * 32 + (lane & 31)) * PXS + i * 32 + m) = v4;
+        }
+    __builtin_amdgcn_s_waitcnt(0xc07f);
     __builtin_amdgcn_wave_barrier();
+    // 8 consecutive pixels of one channel per item: a 16-byte store where
+    // they share an output row.
+    constexpr int PG = MBW * 4;  // 8-pixel groups per staged channel row
+    for (int item = lane; item < NBW * 32 * PG; item += 64) {
+      const int ch = item / PG, pg = item % PG;
+      const int n = nblk0 * 32 + ch;
+      if (n >= a.N) continue;
+      const int q0 = pg * 8;
+      const int mb = mg * MBW + q0 / 32;
+      const int r = mb / (TC / 32), cx = (mb % (TC / 32)) * 32 + (q0 & 31);
+      const int oy = oy0 + r, ox = ox0 + cx;
+      const int p = oy * a.OW + ox;
+      const float4v s0 = *(const float4v *)(stage + ch * PXS + q0);
+      const float4v s1 = *(const float4v *)(stage + ch * PXS + q0 + 4);
+      float v[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
+      const float sl = a.act == IEN_ACT_PRELU ? a.slope[n] : 0.0f;
+      const bool whole = oy < a.OH && ox + 8 <= a.OW && p >= a.p_begin && p + 8 <= a.p_end;
+      const long at = (long)n * a.ys + (p - a.p_begin);
+      if (!a.out_f32 && !a.accumulate && whole && ((((uintptr_t)((uint16_t *)a.y + at)) & 15) == 0)) {
+        uint16_t outv[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) outv[e] = f2h(v[e]);
+        u32x4 ov;
+        __builtin_memcpy(&ov, outv, 16);
+        *(u32x4 *)((uint16_t *)a.y + at) = ov;
+        continue;
+      }
+      for (int e = 0; e < 8; e++) {
+        const int pe = p + e;
+        if (oy >= a.OH || ox + e >= a.OW || pe < a.p_begin || pe >= a.p_end) continue;
+        const long ae = (long)n * a.ys + (pe - a.p_begin);
+        float o = v[e];
+        if (a.out_f32) {
+          float *yo = (float *)a.y + ae;
+          if (a.accumulate) o = activate(o + *yo, a.act, sl);
+          *yo = o;
+        } else {
+          uint16_t *yo = (uint16_t *)a.y + ae;
+          if (a.accumulate) o = activate(o + h2f(*yo), a.act, sl);
+          *yo = f2h(o);
+        }
+      }
+    }
   }
 }
 
@@ -422,21 +608,24 @@ template <int KS, int S, int TR, int TC, int MSPLIT, int NBW, int CK, bool VEC, 
 static ien_status run_cfg(ien_ctx *ctx, ConvArgs a) {
   using Cfg = ConvCfg<KS, S, TR, TC, MSPLIT, NBW, CK, VEC, IN_NCHW>;
   // Tile grid over the requested pixel range.
-  const long first_row = a.p_begin / a.OW, last_row = (a.p_end - 1) / a.OW;
-  a.ty_begin = (int)(first_row / TR);
-  const int ty_end = (int)(last_row / TR) + 1;
-  a.tiles_y = ty_end - a.ty_begin;
+  const int first_row = a.p_begin / a.OW, last_row = (a.p_end - 1) / a.OW;
+  a.ty_begin = first_row / TR;
+  a.tiles_y = last_row / TR + 1 - a.ty_begin;
   a.tiles_x = (a.OW + TC - 1) / TC;
   a.tiles_n = (a.N + Cfg::BN - 1) / Cfg::BN;
-  long blocks = (long)a.tiles_y * a.tiles_x * a.tiles_n;
+  const long blocks = (long)a.tiles_y * a.tiles_x * a.tiles_n;
   IEN_CHECK(blocks > 0 && blocks < (1L << 31), IEN_ERR_INPUT, "grid of %ld tiles", blocks);
   // The packed weights must cover every fragment the tiles touch.
-  IEN_CHECK(a.tiles_n * (Cfg::BN / 32) <= a.NB, IEN_ERR_INPUT, "weights narrower than the tile");
-  hipLaunchKernelGGL((conv_mfma<KS, S, TR, TC, MSPLIT, NBW, CK, VEC, IN_NCHW>), dim3((unsigned)blocks),
-                     dim3(256), 0, ctx->stream, a);
+  IEN_CHECK(a.tiles_n * Cfg::NBT <= a.NB, IEN_ERR_INPUT, "weights narrower than the tile");
+  hipLaunchKernelGGL((conv_mfma<KS, S, TR, TC, MSPLIT, NBW, CK, VEC, IN_NCHW>),
+                     dim3((unsigned)blocks), dim3(256), 0, ctx->stream, a);
   IEN_HIP(hipGetLastError());
   return IEN_OK;
 }
+
+// Channel chunk of the 16-channel-step kernels: the largest of 64, 32, 16
+// that divides the channel count.
+static int pick_ck(int c) { return c % 64 == 0 ? 64 : c % 32 == 0 ? 32 : 16; }
 
 ien_status launch_conv(ien_ctx *ctx, const ConvCall &c) {
   const ien_matrix *w = c.w;
@@ -445,13 +634,22 @@ ien_status launch_conv(ien_ctx *ctx, const ConvCall &c) {
   IEN_CHECK((size_t)T * c.C == w->k, IEN_ERR_INPUT,
             "input does not match the weights: %d taps x %d channels, k = %zu", T, c.C, w->k);
   IEN_CHECK(c.rows > 0, IEN_ERR_INPUT, "no rows");
+  IEN_CHECK(c.act != IEN_ACT_PRELU || c.slope, IEN_ERR_INPUT, "PReLU without slopes");
+  const bool nchw = c.in_nchw != 0;
+  // The kernels index with 32-bit offsets.
+  const long in_extent = c.rows_mode ? (c.row0 + c.rows) * c.xs
+                         : nchw     ? (long)c.C * c.xs
+                                    : (long)c.H * c.W * c.xs;
+  const long out_extent = c.out_nchw ? (long)w->n * c.ys : c.rows * c.ys;
+  IEN_CHECK(in_extent < (1L << 31) && out_extent < (1L << 31) && c.row0 + c.rows < (1L << 31),
+            IEN_ERR_INPUT, "tensors over 2^31 elements");
   ConvArgs a;
   std::memset(&a, 0, sizeof a);
   a.x = c.x;
   a.H = c.H;
   a.W = c.W;
   a.C = c.C;
-  a.xs = c.xs;
+  a.xs = (int)c.xs;
   a.rows_mode = c.rows_mode;
   a.pad_reflect = c.pad_reflect;
   a.noff = c.noff;
@@ -461,8 +659,8 @@ ien_status launch_conv(ien_ctx *ctx, const ConvCall &c) {
   }
   a.OH = c.OH;
   a.OW = c.OW;
-  a.p_begin = c.row0;
-  a.p_end = c.row0 + c.rows;
+  a.p_begin = (int)c.row0;
+  a.p_end = (int)(c.row0 + c.rows);
   a.wp = w->d_packed;
   a.KB = w->kb;
   a.NB = w->nb;
@@ -470,61 +668,67 @@ ien_status launch_conv(ien_ctx *ctx, const ConvCall &c) {
   a.bias = w->d_bias;
   a.slope = c.slope;
   a.y = c.y;
-  a.ys = c.ys;
+  a.ys = (int)c.ys;
   a.out_nchw = c.out_nchw;
   a.out_f32 = c.out_f32;
   a.act = c.act;
   a.accumulate = c.accumulate;
-  IEN_CHECK(c.act != IEN_ACT_PRELU || c.slope, IEN_ERR_INPUT, "PReLU without slopes");
 
-  const bool nchw = c.in_nchw != 0;
   // 16-channel MFMA steps; NHWC halo loads of 16 bytes need aligned pixels.
-  const bool vec = c.C % 16 == 0 &&
-                   (nchw || (c.xs % 8 == 0 && ((uintptr_t)c.x & 15) == 0));
+  const bool vec = c.C % 16 == 0 && (nchw || (c.xs % 8 == 0 && ((uintptr_t)c.x & 15) == 0));
+  const int ck = pick_ck(c.C);
+#define IEN_CK(KS, S, TR, TC, L)                                                   \
+  return ck == 64 ? run_cfg<KS, S, TR, TC, 4, 2, 64, true, L>(ctx, a)              \
+         : ck == 32 ? run_cfg<KS, S, TR, TC, 4, 2, 32, true, L>(ctx, a)            \
+                    : run_cfg<KS, S, TR, TC, 4, 2, 16, true, L>(ctx, a)
   if (c.rows_mode) {
-    // Input::Rows: a virtual image TC wide, rows in order.
+    // Input::Rows: a virtual image 32 pixels wide, rows in order.
     IEN_CHECK(!nchw && c.ks == 1 && c.noff == 0, IEN_ERR_INPUT, "rows are NHWC, one tap");
-    constexpr int TC = 32;
-    a.W = TC;
-    a.OW = TC;
-    a.M = c.row0 + c.rows;
-    a.H = a.OH = (int)((a.M + TC - 1) / TC);
-    if (vec) return run_cfg<1, 1, 4, 32, 4, 2, 64, true, false>(ctx, a);
+    a.W = a.OW = 32;
+    a.M = a.p_end;
+    a.H = a.OH = (a.M + 31) / 32;
+    if (vec) IEN_CK(1, 1, 4, 32, false);
     IEN_CHECK(c.C <= 64, IEN_ERR_INPUT, "rows of %d values (not a multiple of 16, over 64)", c.C);
     return run_cfg<1, 1, 4, 32, 4, 2, 64, false, false>(ctx, a);
   }
-  IEN_CHECK(vec || c.C <= 16, IEN_ERR_INPUT,
-            "%d channels: a multiple of 16, or at most 16", c.C);
+  IEN_CHECK(vec || c.C <= 16, IEN_ERR_INPUT, "%d channels: a multiple of 16, or at most 16", c.C);
   if (c.noff) {
     IEN_CHECK(!nchw, IEN_ERR_INPUT, "offset taps read NHWC");
     for (int i = 0; i < c.noff; i++)
       IEN_CHECK(c.offy[i] >= 0 && c.offy[i] <= 1 && c.offx[i] >= 0 && c.offx[i] <= 1,
                 IEN_ERR_INPUT, "offsets past one pixel");
-    if (vec) return run_cfg<0, 1, 4, 32, 4, 2, 64, true, false>(ctx, a);
+    if (vec) IEN_CK(0, 1, 4, 32, false);
     return run_cfg<0, 1, 4, 32, 4, 2, 16, false, false>(ctx, a);
   }
-#define IEN_CONV_LAYOUTS(KS, S, TR, TC, MS, NBW, CK, V)                            \
-  return nchw ? run_cfg<KS, S, TR, TC, MS, NBW, CK, V, true>(ctx, a)               \
-              : run_cfg<KS, S, TR, TC, MS, NBW, CK, V, false>(ctx, a)
   if (c.ks == 3 && c.stride == 1) {
-    if (!vec) IEN_CONV_LAYOUTS(3, 1, 4, 32, 4, 2, 16, false);
-    if (c.OW % 96 == 0 && c.C <= 64) IEN_CONV_LAYOUTS(3, 1, 4, 96, 4, 2, 64, true);
-    IEN_CONV_LAYOUTS(3, 1, 4, 32, 4, 2, 64, true);
+    if (!vec) {
+      if (nchw) return run_cfg<3, 1, 4, 32, 4, 2, 16, false, true>(ctx, a);
+      return run_cfg<3, 1, 4, 32, 4, 2, 16, false, false>(ctx, a);
+    }
+    if (c.OW % 96 == 0 && ck == 64) {
+      if (nchw) return run_cfg<3, 1, 4, 96, 4, 2, 64, true, true>(ctx, a);
+      return run_cfg<3, 1, 4, 96, 4, 2, 64, true, false>(ctx, a);
+    }
+    if (nchw) IEN_CK(3, 1, 4, 32, true);
+    IEN_CK(3, 1, 4, 32, false);
   }
   if (c.ks == 3 && c.stride == 2) {
+    IEN_CHECK(!nchw, IEN_ERR_INPUT, "strided convolutions read NHWC");
     if (!vec) return run_cfg<3, 2, 4, 32, 4, 2, 16, false, false>(ctx, a);
-    return run_cfg<3, 2, 4, 32, 4, 2, 32, true, false>(ctx, a);
+    if (ck >= 32) return run_cfg<3, 2, 4, 32, 4, 2, 32, true, false>(ctx, a);
+    return run_cfg<3, 2, 4, 32, 4, 2, 16, true, false>(ctx, a);
   }
   if (c.ks == 1 && c.stride == 1) {
     IEN_CHECK(vec, IEN_ERR_INPUT, "1x1 products over %d channels", c.C);
-    IEN_CONV_LAYOUTS(1, 1, 4, 32, 4, 2, 64, true);
+    if (nchw) IEN_CK(1, 1, 4, 32, true);
+    IEN_CK(1, 1, 4, 32, false);
   }
   if (c.ks == 7 && c.stride == 1) {
     IEN_CHECK(!nchw, IEN_ERR_INPUT, "7x7 convolutions read NHWC");
     if (!vec) return run_cfg<7, 1, 4, 32, 4, 2, 16, false, false>(ctx, a);
-    return run_cfg<7, 1, 4, 32, 4, 2, 32, true, false>(ctx, a);
+    return run_cfg<7, 1, 4, 32, 4, 2, 16, true, false>(ctx, a);
   }
-#undef IEN_CONV_LAYOUTS
+#undef IEN_CK
   return fail(IEN_ERR_INPUT, "no kernel for %dx%d stride %d convolutions", c.ks, c.ks, c.stride);
 }
 

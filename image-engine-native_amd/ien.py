@@ -141,7 +141,9 @@ def _ptr(t):
 
 
 class Context:
-    """ien_ctx on one device, running on torch's current stream."""
+    """ien_ctx on one device.  The context's own (non-blocking) HIP stream
+    becomes torch's current stream, so torch's copies, fills and events are
+    ordered with the library's launches."""
 
     def __init__(self, device=0):
         import torch
@@ -151,7 +153,8 @@ class Context:
         check(L.ien_open(device, ctypes.byref(h)))
         self.h = h
         self.device = device
-        check(L.ien_set_stream(h, ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)))
+        self.stream = torch.cuda.ExternalStream(L.ien_stream(h), device=torch.device("cuda", device))
+        torch.cuda.set_stream(self.stream)
 
     @property
     def name(self):
@@ -159,6 +162,10 @@ class Context:
 
     def close(self):
         if self.h:
+            import torch
+
+            torch.cuda.synchronize(self.device)
+            torch.cuda.set_stream(torch.cuda.default_stream(self.device))
             load().ien_close(self.h)
             self.h = None
 

@@ -1,0 +1,155 @@
+#!/usr/bin/env python3
+"""Write golden.npz: small input/output vectors computed with torch's
+functional operators in float64, in this container, for pinning the oracle.
+
+    python tests/golden/make_golden.py
+
+The reference (a Rust workspace) cannot be built or run here and commits no
+golden files of its own; its tests check each op against textbook
+definitions.  These vectors pin the same ops by an independent route:
+torch.nn.functional.conv2d / conv_transpose2d / layer_norm / gelu /
+scaled_dot_product_attention / pixel_shuffle / interpolate, all in float64.
+Conventions follow the reference's layouts: images NHWC, convolution
+weights as (kh, kw, cin) rows by cout columns (tools/realesrgan/
+export_weights.py:48-56).  Inputs are seeded (numpy PCG64) and stored with
+the outputs.  The Real-ESRGAN vector runs SRVGGNetCompact (conv3x3 + PReLU
+x33, conv3x3 to 48, pixel shuffle x4, plus the nearest-upsampled input) on
+the random-init weights of image-engine-native_amd/synthetic.py.
+"""
+
+import pathlib
+import sys
+
+import numpy as np
+import torch
+import torch.nn.functional as F
+
+HERE = pathlib.Path(__file__).resolve().parent
+sys.path.insert(0, str(HERE.parent.parent / "image-engine-native_amd"))
+import synthetic  # noqa: E402
+
+torch.set_default_dtype(torch.float64)
+
+
+def to_oihw(w, size, cin, cout):
+    """(kh, kw, cin) x cout rows -> torch's [cout, cin, kh, kw]."""
+    return torch.from_numpy(w.reshape(size, size, cin, cout).transpose(3, 2, 0, 1).copy())
+
+
+def conv_nhwc(x, w, b, size, step=1, pad="zero"):
+    h, wd, cin = x.shape
+    cout = w.shape[1]
+    t = torch.from_numpy(x.transpose(2, 0, 1)[None].copy())
+    p = size // 2
+    if pad == "reflect":
+        t = F.pad(t, (p, p, p, p), mode="reflect")
+        p = 0
+    y = F.conv2d(t, to_oihw(w, size, cin, cout), torch.from_numpy(b), stride=step, padding=p)
+    return y[0].numpy().transpose(1, 2, 0)
+
+
+def main():
+    rng = np.random.default_rng(20261201)
+    out = {}
+
+    def f32(a):
+        return np.asarray(a, np.float32)
+
+    # gemm.rs Input::Image taps: zero padding, several sizes and strides.
+    for name, (h, w, c, n, size, step, pad) in {
+        "conv_3x3_zero": (5, 7, 3, 20, 3, 1, "zero"),
+        "conv_7x7_zero": (6, 9, 8, 16, 7, 1, "zero"),
+        "conv_1x1": (4, 6, 24, 10, 1, 1, "zero"),
+        "conv_3x3_reflect": (6, 5, 16, 12, 3, 1, "reflect"),
+        "conv_3x3_s2_reflect": (9, 8, 16, 24, 3, 2, "reflect"),
+        "conv_7x7_reflect": (8, 10, 4, 8, 7, 1, "reflect"),
+    }.items():
+        x = f32(rng.standard_normal((h, w, c)))
+        wt = f32(rng.standard_normal((size * size * c, n)) / np.sqrt(size * size * c))
+        b = f32(rng.standard_normal(n))
+        out[name + "_x"], out[name + "_w"], out[name + "_b"] = x, wt, b
+        out[name + "_y"] = conv_nhwc(x.astype(np.float64), wt.astype(np.float64), b.astype(np.float64),
+                                     size, step, pad)
+
+    # A stride-2, padding-1, output-padding-1 3x3 transposed convolution
+    # (LaMa's upsampling), for the offset-tap phases.
+    x = f32(rng.standard_normal((5, 6, 8)))
+    wt = f32(rng.standard_normal((8, 6, 3, 3)) / 6)  # torch layout [cin, cout, kh, kw]
+    b = f32(rng.standard_normal(6))
+    y = F.conv_transpose2d(torch.from_numpy(x.astype(np.float64).transpose(2, 0, 1)[None].copy()),
+                           torch.from_numpy(wt.astype(np.float64)), torch.from_numpy(b.astype(np.float64)),
+                           stride=2, padding=1, output_padding=1)
+    out["convT_x"], out["convT_w"], out["convT_b"] = x, wt, b
+    out["convT_y"] = y[0].numpy().transpose(1, 2, 0)
+
+    # Depthwise 7x7 (groups = channels), NHWC, weights (tap, channel).
+    x = f32(rng.standard_normal((11, 13, 6)))
+    wt = f32(rng.standard_normal((49, 6)) / 7)
+    b = f32(rng.standard_normal(6))
+    k = torch.from_numpy(wt.astype(np.float64).T.reshape(6, 1, 7, 7).copy())
+    y = F.conv2d(torch.from_numpy(x.astype(np.float64).transpose(2, 0, 1)[None].copy()), k,
+                 torch.from_numpy(b.astype(np.float64)), padding=3, groups=6)
+    out["dw_x"], out["dw_w"], out["dw_b"], out["dw_y"] = x, wt, b, y[0].numpy().transpose(1, 2, 0)
+
+    # math.rs: LayerNorm (eps 1e-5), exact GELU, logistic.
+    x = f32(rng.standard_normal((7, 96)) * 3 + 0.5)
+    g = f32(1 + 0.2 * rng.standard_normal(96))
+    bb = f32(0.2 * rng.standard_normal(96))
+    out["ln_x"], out["ln_g"], out["ln_b"] = x, g, bb
+    out["ln_y"] = F.layer_norm(torch.from_numpy(x.astype(np.float64)), (96,), torch.from_numpy(g.astype(np.float64)),
+                               torch.from_numpy(bb.astype(np.float64)), eps=1e-5).numpy()
+    x = f32(np.linspace(-9, 9, 3001))
+    out["act_x"] = x
+    out["gelu_y"] = F.gelu(torch.from_numpy(x.astype(np.float64)), approximate="none").numpy()
+    out["sigmoid_y"] = torch.sigmoid(torch.from_numpy(x.astype(np.float64))).numpy()
+
+    # attention.rs: one head of a window, softmax(q k^T / sqrt(32) + bias) v,
+    # with masked (-100 and -inf) biases; N = 49, 64 and 144.
+    for tokens in (49, 64, 144):
+        c = 64
+        qkv = f32(rng.standard_normal((tokens, 3 * c)))
+        bias = f32(rng.standard_normal((tokens, tokens)))
+        bias[rng.random((tokens, tokens)) < 0.2] = -100.0
+        if tokens == 64:
+            bias[:, 60:] = -np.inf  # whole masked key columns, as SCUNet's shift mask
+        head = 1
+        q = torch.from_numpy(qkv[:, head * 32:head * 32 + 32].astype(np.float64))[None, None]
+        kk = torch.from_numpy(qkv[:, c + head * 32:c + head * 32 + 32].astype(np.float64))[None, None]
+        v = torch.from_numpy(qkv[:, 2 * c + head * 32:2 * c + head * 32 + 32].astype(np.float64))[None, None]
+        y = F.scaled_dot_product_attention(q, kk, v, attn_mask=torch.from_numpy(bias.astype(np.float64))[None, None])
+        out[f"attn{tokens}_qkv"], out[f"attn{tokens}_bias"], out[f"attn{tokens}_y"] = qkv, bias, y[0, 0].numpy()
+
+    # realesrgan network.rs:115-141: pixel shuffle x4 of 48 channels plus
+    # the input repeated, against pixel_shuffle + nearest interpolate.
+    last = f32(rng.standard_normal((3, 5, 48)))
+    img = f32(rng.random((3, 5, 3)))
+    ps = F.pixel_shuffle(torch.from_numpy(last.astype(np.float64).transpose(2, 0, 1)[None].copy()), 4)
+    up = F.interpolate(torch.from_numpy(img.astype(np.float64).transpose(2, 0, 1)[None].copy()),
+                       scale_factor=4, mode="nearest")
+    out["shuffle_last"], out["shuffle_img"] = last, img
+    out["shuffle_y"] = (ps + up)[0].numpy().transpose(1, 2, 0)
+
+    # Real-ESRGAN SRVGGNetCompact on the synthetic random-init weights.
+    tensors = synthetic.esrgan_tensors()
+    img = synthetic.esrgan_image(12, 16, seed=7)
+    t = torch.from_numpy(img.astype(np.float64).transpose(2, 0, 1)[None].copy())
+    x = t
+    for i in range(synthetic.ESRGAN_STEPS):
+        cin = 3 if i == 0 else 64
+        w = tensors[f"body.{2 * i}.weight"].astype(np.float64)
+        cout = w.shape[1]
+        x = F.conv2d(x, to_oihw(w, 3, cin, cout), torch.from_numpy(tensors[f"body.{2 * i}.bias"].astype(np.float64)),
+                     padding=1)
+        if i != synthetic.ESRGAN_STEPS - 1:
+            x = F.prelu(x, torch.from_numpy(tensors[f"body.{2 * i + 1}.weight"].astype(np.float64)))
+    x = F.pixel_shuffle(x, 4) + F.interpolate(t, scale_factor=4, mode="nearest")
+    out["esrgan_img"] = img
+    out["esrgan_y"] = x[0].numpy().transpose(1, 2, 0)
+
+    packed = {k: (v.astype(np.float32) if v.dtype == np.float64 else v) for k, v in out.items()}
+    np.savez_compressed(HERE / "golden.npz", **packed)
+    print(f"wrote {len(packed)} arrays, {sum(v.nbytes for v in packed.values())} bytes")
+
+
+if __name__ == "__main__":
+    main()
