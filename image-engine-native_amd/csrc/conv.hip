@@ -33,122 +33,9 @@
 // the 8 XCDs) gets a contiguous band of tiles: neighbouring tiles share halo
 // rows, which then stay in that XCD's L2.
 
-#include <cstring>
-
-#include "ien_internal.h"
+#include "conv_common.h"
 
 namespace ien {
-
-typedef _Float16 half8 __attribute__((ext_vector_type(8)));
-typedef float floatx16 __attribute__((ext_vector_type(16)));
-typedef float float4v __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-
-struct ConvArgs {
-  const uint16_t *x;
-  int H, W, C;
-  int xs;  // NHWC: halves between pixels; NCHW: halves between planes
-  int rows_mode;
-  int M;  // rows_mode: number of input rows (= output pixels)
-  int pad_reflect;
-  int noff;
-  int offy[4], offx[4];
-  int OH, OW;
-  int p_begin, p_end;  // output pixel range [row0, row0 + rows)
-  int ty_begin, tiles_x, tiles_y, tiles_n;
-  const uint16_t *wp;
-  int KB;  // k fragments (16) of the packed weights
-  int NB;  // n fragments (32), a multiple of 4
-  int N;
-  const float *bias;
-  const float *slope;
-  void *y;
-  int ys;
-  int out_nchw, out_f32, act, accumulate;
-};
-
-__device__ __forceinline__ int reflect_idx(int i, int n) {
-  int last = n - 1;
-  int a = i < 0 ? -i : i;
-  int b = 2 * last - i;
-  return a < b ? a : b;
-}
-
-// math.rs:41-75: exact GELU through erf(x) = x P(x^2) / Q(x^2) on [-4, 4]
-// with Eigen's generic_fast_erf_float coefficients.
-__device__ __forceinline__ float gelu_f(float x) {
-  float z = fminf(fmaxf(x * 0.70710678118654752f, -4.0f), 4.0f);
-  float z2 = z * z;
-  float p = -2.7261423e-10f;
-  p = p * z2 + 2.7706814e-08f;
-  p = p * z2 + -2.101024e-06f;
-  p = p * z2 + -5.6925064e-05f;
-  p = p * z2 + -7.3499063e-04f;
-  p = p * z2 + -2.9546e-03f;
-  p = p * z2 + -1.6096033e-02f;
-  float q = -1.4566072e-05f;
-  q = q * z2 + -2.1337406e-04f;
-  q = q * z2 + -1.682827e-03f;
-  q = q * z2 + -7.373329e-03f;
-  q = q * z2 + -1.426474e-02f;
-  return 0.5f * x * (1.0f + z * p / q);
-}
-
-__device__ __forceinline__ float sigmoid_f(float x) {
-  // math.rs:33-39: from exp(-|x|) so neither tail cancels.
-  float e = __expf(-fabsf(x));
-  float s = e / (e + 1.0f);
-  return x > 0.0f ? 1.0f - s : s;
-}
-
-// `slope` is the PReLU slope of this value's channel.
-__device__ __forceinline__ float activate(float v, int act, float slope) {
-  switch (act) {
-    case IEN_ACT_RELU: return v > 0.0f ? v : 0.0f;
-    case IEN_ACT_PRELU: return v < 0.0f ? v * slope : v;
-    case IEN_ACT_GELU: return gelu_f(v);
-    case IEN_ACT_SIGMOID: return sigmoid_f(v);
-    default: return v;
-  }
-}
-
-__device__ __forceinline__ float h2f(uint16_t h) {
-  _Float16 v;
-  __builtin_memcpy(&v, &h, 2);
-  return (float)v;
-}
-__device__ __forceinline__ uint16_t f2h(float f) {
-  _Float16 v = (_Float16)f;  // round to nearest even
-  uint16_t h;
-  __builtin_memcpy(&h, &v, 2);
-  return h;
-}
-
-// XCD-aware order: block b runs on XCD b % 8; give each XCD a contiguous
-// band of the logical tile order when the grid divides evenly.
-__device__ __forceinline__ int xcd_remap(int b, int nblocks) {
-  if ((nblocks & 7) != 0) return b;
-  return (b & 7) * (nblocks >> 3) + (b >> 3);
-}
-
-// Global -> LDS staging, BATCH independent loads in flight per thread
-// before any of them is written: with one wave per SIMD nothing else hides
-// a load's latency, so a load-wait-store loop would pay it every time.
-// `load(e)` must load unconditionally from a valid address (padding is
-// decided in `store(e, v)`), so that no branch separates the loads.
-template <int BATCH, typename Load, typename Store>
-__device__ __forceinline__ void staged_copy(int total, int tid, Load load, Store store) {
-  for (int base = tid; base < total; base += 256 * BATCH) {
-    u32x4 v[BATCH];
-#pragma unroll
-    for (int b = 0; b < BATCH; b++) v[b] = load(min(base + b * 256, total - 1));
-#pragma unroll
-    for (int b = 0; b < BATCH; b++) {
-      const int e = base + b * 256;
-      if (e < total) store(e, v[b]);
-    }
-  }
-}
 
 template <int KS, int S, int TR, int TC, int MSPLIT, int NBW, int CK, bool VEC, bool IN_NCHW>
 struct ConvCfg {
@@ -161,23 +48,39 @@ struct ConvCfg {
   static constexpr int TMAX = KS == 0 ? 4 : KS * KS;
   static constexpr int HR = (TR - 1) * S + EXT;
   static constexpr int HC = (TC - 1) * S + EXT;
-  static constexpr int CKP = VEC ? CK + 8 : CK;  // LDS halves per halo pixel
-  static constexpr int HALO_HALVES = HR * HC * CKP;
+  // NHWC 16-channel inputs are staged by direct-to-LDS loads into an
+  // unpadded halo whose 16-byte chunks are XOR-swizzled per pixel (SWZ);
+  // the other layouts are written through registers into a halo whose
+  // pixel stride is padded by 8 halves.  Either way the 32 lanes of an
+  // A-fragment read hit distinct banks.
+  static constexpr bool DMA = VEC && !IN_NCHW;
+  static constexpr int CKP = DMA ? CK : (VEC ? CK + 8 : CK);  // halves per halo pixel
+  static constexpr int PB = CK * 2;                           // bytes per DMA halo pixel
+  static constexpr int NCH = PB / 16;                         // 16-byte chunks per pixel
+  static constexpr int RPB = PB >= 256 ? 1 : 256 / PB;        // pixels per 256-byte bank row
+  static constexpr int HALO_BYTES = DMA ? (HR * HC * PB + 1023) / 1024 * 1024 : HR * HC * CKP * 2;
   // 16-deep k steps of one chunk: VEC walks taps x CK/16; otherwise K is
   // flattened over (tap, channel) and rounded up to 16.
   static constexpr int KSTEPS = VEC ? TMAX * (CK / 16) : (TMAX * CK + 15) / 16;
-  static constexpr int B_HALVES = NBT * KSTEPS * 512;  // B fragments of the chunk
+  static constexpr int B_BYTES = NBT * KSTEPS * 1024;  // B fragments of the chunk
   // Epilogue staging per wave: NHWC [px][NBW*32 + 8] or NCHW [NBW*32][px + 4] floats.
   static constexpr int STAGE_NHWC = MBW * 32 * (NBW * 32 + 8);
   static constexpr int STAGE_NCHW = NBW * 32 * (MBW * 32 + 4);
   static constexpr int STAGE = STAGE_NHWC > STAGE_NCHW ? STAGE_NHWC : STAGE_NCHW;
-  static constexpr int MAIN_BYTES = (HALO_HALVES + B_HALVES) * 2;
+  static constexpr int MAIN_BYTES = HALO_BYTES + B_BYTES;
   static constexpr int LDS_BYTES = MAIN_BYTES > 4 * STAGE * 4 ? MAIN_BYTES : 4 * STAGE * 4;
   static_assert(MB % MSPLIT == 0, "M-blocks must split evenly over waves");
   static_assert(TC % 32 == 0, "tile columns are whole M-blocks");
   static_assert(!VEC || CK % 16 == 0, "16-channel steps");
+  static_assert(HALO_BYTES % 16 == 0, "B fragments start 16-byte aligned");
   static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
 };
+
+// Swizzled chunk slot of 16-byte chunk c of DMA halo pixel p.
+template <class Cfg>
+__device__ __forceinline__ int swz_slot(int p, int c) {
+  return c ^ ((p / Cfg::RPB) & (Cfg::NCH - 1));
+}
 
 template <int KS, int S, int TR, int TC, int MSPLIT, int NBW, int CK, bool VEC, bool IN_NCHW>
 __global__ __launch_bounds__(256) void conv_mfma(ConvArgs a) {
@@ -187,7 +90,7 @@ __global__ __launch_bounds__(256) void conv_mfma(ConvArgs a) {
   constexpr int P = KS == 0 ? 0 : KS / 2;
   __shared__ __attribute__((aligned(16))) unsigned char lds_raw[Cfg::LDS_BYTES];
   uint16_t *halo = (uint16_t *)lds_raw;
-  uint16_t *bl = halo + Cfg::HALO_HALVES;
+  uint16_t *bl = (uint16_t *)(lds_raw + Cfg::HALO_BYTES);
 
   const int bid = xcd_remap(blockIdx.x, gridDim.x);
   const int tn = bid % a.tiles_n;
@@ -242,35 +145,35 @@ __global__ __launch_bounds__(256) void conv_mfma(ConvArgs a) {
 
   // This wave's A-fragment base per M-block: halo pixel of tap (0, 0) for
   // the lane's pixel, plus the lane's 8-channel half of a 16-channel step.
-  int abase[MBW];
+  int abase[MBW], apix[MBW];
 #pragma unroll
   for (int i = 0; i < MBW; i++) {
     const int mb = mg * MBW + i;
     const int r = mb / (TC / 32), cx = (mb % (TC / 32)) * 32 + (lane & 31);
-    abase[i] = ((r * S) * HC + cx * S) * CKP + (VEC ? 8 * (lane >> 5) : 0);
+    apix[i] = (r * S) * HC + cx * S;
+    abase[i] = apix[i] * CKP + (VEC ? 8 * (lane >> 5) : 0);
   }
 
   for (int c0 = 0; c0 < a.C; c0 += CK) {
     const int cc = min(CK, a.C - c0);  // == CK when VEC
     __syncthreads();
     // ---- global -> LDS: the halo of this channel chunk ----
-    if constexpr (VEC && !IN_NCHW) {
-      auto pixel = [&](int hp) {
-        const int hy = hp / HC, hx = hp - hy * HC;
-        return resolve(iy0 + hy, ix0 + hx);
-      };
-      staged_copy<8>(
-          HR * HC * (CK / 8), tid,
-          [&](int e) -> u32x4 {
-            const int hp = e / (CK / 8), v = e % (CK / 8);
-            const int off = pixel(hp);
-            return *(const u32x4 *)(a.x + (off >= 0 ? off : 0) + c0 + 8 * v);
-          },
-          [&](int e, u32x4 val) {
-            const int hp = e / (CK / 8), v = e % (CK / 8);
-            if (pixel(hp) < 0) val = u32x4{0u, 0u, 0u, 0u};
-            *(u32x4 *)(halo + hp * CKP + 8 * v) = val;
-          });
+    if constexpr (Cfg::DMA) {
+      // One KiB per wave instruction: lane l fills byte 16 l of it, which
+      // is chunk slot s of halo pixel p, holding input chunk
+      // s ^ swizzle(p); padding pixels read the zero page.
+      constexpr int G = Cfg::HALO_BYTES / 1024;
+      for (int g = wave; g < G; g += 4) {
+        const int byte = g * 1024 + lane * 16;
+        const int hp = byte / Cfg::PB, slot = (byte % Cfg::PB) / 16;
+        const uint16_t *src = a.zeros;
+        if (hp < HR * HC) {
+          const int hy = hp / HC, hx = hp - hy * HC;
+          const int off = resolve(iy0 + hy, ix0 + hx);
+          if (off >= 0) src = a.x + off + c0 + 8 * swz_slot<Cfg>(hp, slot);
+        }
+        dma16(src, lds_raw + g * 1024);
+      }
     } else if constexpr (!IN_NCHW) {
       // Few channels: one half per element.
       auto where = [&](int e, int &hp, int &c) {
@@ -350,27 +253,22 @@ __global__ __launch_bounds__(256) void conv_mfma(ConvArgs a) {
       }
     }
 
-    // ---- global -> LDS: this chunk's weight fragments, [block][step] ----
+    // ---- global -> LDS: this chunk's weight fragments, [block][step], ----
+    // one KiB fragment per wave instruction.
     {
       const int steps = VEC ? T * (CK / 16) : (T * cc + 15) / 16;
-      staged_copy<8>(
-          NBT * steps * 64, tid,
-          [&](int e) -> u32x4 {
-            const int f = e >> 6, l = e & 63;
-            const int jn = f / steps, s = f - jn * steps;
-            int kb = s;  // one chunk holds all channels: fragments in order
-            if (VEC) {
-              const int tap = s / (CK / 16), kc = s % (CK / 16);
-              kb = tap * (a.C / 16) + c0 / 16 + kc;
-            }
-            return *(const u32x4 *)(a.wp + ((nblk_tile + jn) * a.KB + kb) * 512 + l * 8);
-          },
-          [&](int e, u32x4 v) {
-            const int f = e >> 6, l = e & 63;
-            const int jn = f / steps, s = f - jn * steps;
-            *(u32x4 *)(bl + (jn * KSTEPS + s) * 512 + l * 8) = v;
-          });
+      for (int f = wave; f < NBT * steps; f += 4) {
+        const int jn = f / steps, s = f - jn * steps;
+        int kb = s;  // one chunk holds all channels: fragments in order
+        if (VEC) {
+          const int tap = s / (CK / 16), kc = s % (CK / 16);
+          kb = tap * (a.C / 16) + c0 / 16 + kc;
+        }
+        dma16(a.wp + ((nblk_tile + jn) * a.KB + kb) * 512 + lane * 8,
+              bl + (jn * KSTEPS + s) * 512);
+      }
     }
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): the direct-to-LDS loads have landed
     __syncthreads();
 
     const uint16_t *bw = bl + ng * NBW * KSTEPS * 512 + lane * 8;
@@ -386,28 +284,45 @@ __global__ __launch_bounds__(256) void conv_mfma(ConvArgs a) {
       auto frag = [&](int s, half8 *av, half8 *bv) {
         const int tap = s / (CK / 16), kc = s % (CK / 16);
         const int dy = tap / KS, dx = tap % KS;
-        const int off = (dy * HC + dx) * CKP + kc * 16;
+        if constexpr (Cfg::DMA) {
+          const int c = 2 * kc + (lane >> 5);
 #pragma unroll
-        for (int i = 0; i < MBW; i++) av[i] = *(const half8 *)(halo + abase[i] + off);
+          for (int i = 0; i < MBW; i++) {
+            const int p = apix[i] + dy * HC + dx;
+            av[i] = *(const half8 *)(lds_raw + p * Cfg::PB + 16 * swz_slot<Cfg>(p, c));
+          }
+        } else {
+          const int off = (dy * HC + dx) * CKP + kc * 16;
+#pragma unroll
+          for (int i = 0; i < MBW; i++) av[i] = *(const half8 *)(halo + abase[i] + off);
+        }
 #pragma unroll
         for (int j = 0; j < NBW; j++) bv[j] = *(const half8 *)(bw + (j * KSTEPS + s) * 512);
       };
+      // The scheduler barriers keep step s+1's fragment reads ahead of
+      // step s's MFMAs; left alone, the compiler sinks each read next to
+      // its use and every MFMA pair then waits out an LDS round trip.
       half8 av[2][MBW], bv[2][NBW];
       frag(0, av[0], bv[0]);
 #pragma unroll
       for (int s = 0; s < KSTEPS; s++) {
         if (s + 1 < KSTEPS) frag(s + 1, av[(s + 1) & 1], bv[(s + 1) & 1]);
+        __builtin_amdgcn_sched_barrier(0);
         mma(av[s & 1], bv[s & 1]);
+        __builtin_amdgcn_sched_barrier(0);
       }
     } else if constexpr (VEC) {
       // Offset taps (transposed-conv phases): at most 4, known at run time.
       const int steps = T * (CK / 16);
       for (int s = 0; s < steps; s++) {
         const int tap = s / (CK / 16), kc = s % (CK / 16);
-        const int off = (a.offy[tap] * HC + a.offx[tap]) * CKP + kc * 16;
         half8 av[MBW], bv[NBW];
+        const int c = 2 * kc + (lane >> 5);
 #pragma unroll
-        for (int i = 0; i < MBW; i++) av[i] = *(const half8 *)(halo + abase[i] + off);
+        for (int i = 0; i < MBW; i++) {
+          const int p = apix[i] + a.offy[tap] * HC + a.offx[tap];
+          av[i] = *(const half8 *)(lds_raw + p * Cfg::PB + 16 * swz_slot<Cfg>(p, c));
+        }
 #pragma unroll
         for (int j = 0; j < NBW; j++) bv[j] = *(const half8 *)(bw + (j * KSTEPS + s) * 512);
         mma(av, bv);
@@ -662,6 +577,7 @@ ien_status launch_conv(ien_ctx *ctx, const ConvCall &c) {
   a.p_begin = (int)c.row0;
   a.p_end = (int)(c.row0 + c.rows);
   a.wp = w->d_packed;
+  a.zeros = ctx->zeros;
   a.KB = w->kb;
   a.NB = w->nb;
   a.N = (int)w->n;
@@ -700,6 +616,10 @@ ien_status launch_conv(ien_ctx *ctx, const ConvCall &c) {
     if (vec) IEN_CK(0, 1, 4, 32, false);
     return run_cfg<0, 1, 4, 32, 4, 2, 16, false, false>(ctx, a);
   }
+  // Resident weights: NHWC, zero padding, 16, 32 or 64 channels, K <= 640.
+  // Its results are staged as f16: f32 outputs take the general kernel.
+  if (vec && !c.out_f32 && resident_supported(c.ks, c.stride, c.C, nchw, c.pad_reflect, c.noff, c.rows_mode))
+    return launch_resident(ctx, a, c.ks);
   if (c.ks == 3 && c.stride == 1) {
     if (!vec) {
       if (nchw) return run_cfg<3, 1, 4, 32, 4, 2, 16, false, true>(ctx, a);

@@ -1,0 +1,147 @@
+// conv_common.h -- definitions shared by the convolution kernels
+// (conv.hip: general implicit GEMM; conv_res.hip: resident weights).
+#pragma once
+
+#include <algorithm>
+#include <cstring>
+
+#include "ien_internal.h"
+
+namespace ien {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef float float4v __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+struct ConvArgs {
+  const uint16_t *x;
+  int H, W, C;
+  int xs;  // NHWC: halves between pixels; NCHW: halves between planes
+  int rows_mode;
+  int M;  // rows_mode: number of input rows (= output pixels)
+  int pad_reflect;
+  int noff;
+  int offy[4], offx[4];
+  int OH, OW;
+  int p_begin, p_end;  // output pixel range [row0, row0 + rows)
+  int ty_begin, tiles_x, tiles_y, tiles_n;
+  const uint16_t *wp;
+  const uint16_t *zeros;  // 4 KiB of zeros: the source of padding pixels
+  int KB;  // k fragments (16) of the packed weights
+  int NB;  // n fragments (32), a multiple of 4
+  int N;
+  const float *bias;
+  const float *slope;
+  void *y;
+  int ys;
+  int out_nchw, out_f32, act, accumulate;
+};
+
+__device__ __forceinline__ int reflect_idx(int i, int n) {
+  int last = n - 1;
+  int a = i < 0 ? -i : i;
+  int b = 2 * last - i;
+  return a < b ? a : b;
+}
+
+// math.rs:41-75: exact GELU through erf(x) = x P(x^2) / Q(x^2) on [-4, 4]
+// with Eigen's generic_fast_erf_float coefficients.
+__device__ __forceinline__ float gelu_f(float x) {
+  float z = fminf(fmaxf(x * 0.70710678118654752f, -4.0f), 4.0f);
+  float z2 = z * z;
+  float p = -2.7261423e-10f;
+  p = p * z2 + 2.7706814e-08f;
+  p = p * z2 + -2.101024e-06f;
+  p = p * z2 + -5.6925064e-05f;
+  p = p * z2 + -7.3499063e-04f;
+  p = p * z2 + -2.9546e-03f;
+  p = p * z2 + -1.6096033e-02f;
+  float q = -1.4566072e-05f;
+  q = q * z2 + -2.1337406e-04f;
+  q = q * z2 + -1.682827e-03f;
+  q = q * z2 + -7.373329e-03f;
+  q = q * z2 + -1.426474e-02f;
+  return 0.5f * x * (1.0f + z * p / q);
+}
+
+__device__ __forceinline__ float sigmoid_f(float x) {
+  // math.rs:33-39: from exp(-|x|) so neither tail cancels.
+  float e = __expf(-fabsf(x));
+  float s = e / (e + 1.0f);
+  return x > 0.0f ? 1.0f - s : s;
+}
+
+// `slope` is the PReLU slope of this value's channel.
+__device__ __forceinline__ float activate(float v, int act, float slope) {
+  switch (act) {
+    case IEN_ACT_RELU: return v > 0.0f ? v : 0.0f;
+    case IEN_ACT_PRELU: return v < 0.0f ? v * slope : v;
+    case IEN_ACT_GELU: return gelu_f(v);
+    case IEN_ACT_SIGMOID: return sigmoid_f(v);
+    default: return v;
+  }
+}
+
+// The activation as a compile-time choice (one epilogue per kernel).
+template <int ACT>
+__device__ __forceinline__ float act_c(float v, float slope) {
+  if constexpr (ACT == IEN_ACT_RELU) return v > 0.0f ? v : 0.0f;
+  else if constexpr (ACT == IEN_ACT_PRELU) return v < 0.0f ? v * slope : v;
+  else if constexpr (ACT == IEN_ACT_GELU) return gelu_f(v);
+  else if constexpr (ACT == IEN_ACT_SIGMOID) return sigmoid_f(v);
+  else return v;
+}
+
+__device__ __forceinline__ float h2f(uint16_t h) {
+  _Float16 v;
+  __builtin_memcpy(&v, &h, 2);
+  return (float)v;
+}
+__device__ __forceinline__ uint16_t f2h(float f) {
+  _Float16 v = (_Float16)f;  // round to nearest even
+  uint16_t h;
+  __builtin_memcpy(&h, &v, 2);
+  return h;
+}
+
+// XCD-aware order: block b runs on XCD b % 8; give each XCD a contiguous
+// band of the logical tile order when the grid divides evenly.
+__device__ __forceinline__ int xcd_remap(int b, int nblocks) {
+  if ((nblocks & 7) != 0) return b;
+  return (b & 7) * (nblocks >> 3) + (b >> 3);
+}
+
+// Global -> LDS staging, BATCH independent loads in flight per thread
+// before any of them is written: with one wave per SIMD nothing else hides
+// a load's latency, so a load-wait-store loop would pay it every time.
+// `load(e)` must load unconditionally from a valid address (padding is
+// decided in `store(e, v)`), so that no branch separates the loads.
+template <int BATCH, typename Load, typename Store>
+__device__ __forceinline__ void staged_copy(int total, int tid, Load load, Store store) {
+  for (int base = tid; base < total; base += 256 * BATCH) {
+    u32x4 v[BATCH];
+#pragma unroll
+    for (int b = 0; b < BATCH; b++) v[b] = load(min(base + b * 256, total - 1));
+#pragma unroll
+    for (int b = 0; b < BATCH; b++) {
+      const int e = base + b * 256;
+      if (e < total) store(e, v[b]);
+    }
+  }
+}
+
+// 16 bytes per lane from global memory straight into LDS
+// (global_load_lds_dwordx4): lane l's bytes land at lds + 16 l, so a wave
+// fills one contiguous KiB; no register holds the data and nothing waits
+// until s_waitcnt vmcnt.  `lds` must be the same for the whole wave.
+__device__ __forceinline__ void dma16(const void *src, void *lds) {
+  __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)lds, 16, 0, 0);
+}
+
+// conv_res.hip: the resident-weight kernel for NHWC inputs of 16, 32 or 64
+// channels with k x k (k = 1, 3) zero-padded taps and K = k k C <= 640.
+bool resident_supported(int ks, int stride, int c, int nchw, int reflect, int noff, int rows_mode);
+ien_status launch_resident(ien_ctx *ctx, ConvArgs a, int ks);
+
+}  // namespace ien

@@ -40,6 +40,9 @@ struct ien_ctx {
   hipStream_t stream = nullptr;  // where work goes (own, or the caller's)
   std::string name;
   int cus = 0;
+  // 4 KiB of zeros in device memory: the source of padding pixels for
+  // loads that write LDS directly (they cannot write a constant).
+  uint16_t *zeros = nullptr;
 };
 
 // Packed weights (gemm.rs Matrix): k x n padded to whole 16 x 32 MFMA

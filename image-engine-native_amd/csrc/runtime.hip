@@ -107,6 +107,13 @@ ien_status ien_open(int device, ien_ctx **out) {
     return fail(IEN_ERR_GPU, "stream: %s", hipGetErrorString(e));
   }
   ctx->stream = ctx->own;
+  e = hipMalloc(&ctx->zeros, 4096);
+  if (e == hipSuccess) e = hipMemset(ctx->zeros, 0, 4096);
+  if (e != hipSuccess) {
+    (void)hipStreamDestroy(ctx->own);
+    delete ctx;
+    return fail(IEN_ERR_GPU, "zero page: %s", hipGetErrorString(e));
+  }
   *out = ctx;
   return IEN_OK;
 }
@@ -116,6 +123,7 @@ void ien_close(ien_ctx *ctx) {
   (void)hipSetDevice(ctx->device);
   (void)hipStreamSynchronize(ctx->stream);
   (void)hipStreamDestroy(ctx->own);
+  (void)hipFree(ctx->zeros);
   delete ctx;
 }
 
