@@ -146,6 +146,49 @@ def cpu_baseline(tensors, image):
                       f"on {cpu}; the oracle (C restatement of the reference CPU f32 path)"}
 
 
+def body_layer(ctx, tensors, H, W):
+    """The dominant launch: one body layer (3x3 64->64 + PReLU) at H x W on a
+    seeded N(0, 1) f16 NHWC map; returns (launch, free)."""
+    import numpy as np
+    import torch
+
+    import ien
+    import synthetic
+
+    w_body, b_body, s_body = synthetic.esrgan_layers(tensors)[1]
+    m = ien.Matrix(ctx, w_body, b_body)
+    slope = torch.from_numpy(s_body).cuda()
+    src = torch.from_numpy(np.random.default_rng(3).standard_normal((H * W, 64))).half().cuda()
+    dst = torch.empty((H * W, 64), dtype=torch.float16, device="cuda")
+    inp = ien.image_input(src, H, W, 64)
+
+    def launch():
+        # inp holds src (the descriptor keeps its tensor); dst and slope are
+        # held by this closure, so no buffer a captured launch reads is freed.
+        ien.multiply_ex(ctx, inp, 0, H * W, m, dst, 64, act=ien.ACT_PRELU, slope=slope)
+
+    assert inp._tensor is src
+    return launch, m.free
+
+
+def traffic_probe(ctx, tensors, H, W):
+    """Counter-pass workload: the body layer x10, then a copy of 128 MiB
+    (a kernel of known traffic, for scaling FETCH_SIZE and WRITE_SIZE)."""
+    import torch
+
+    launch, free = body_layer(ctx, tensors, H, W)
+    for _ in range(10):
+        launch()
+    torch.cuda.synchronize()
+    a = torch.empty(64 << 20, dtype=torch.float16, device="cuda").fill_(1)
+    c = torch.empty_like(a)
+    torch.cuda.synchronize()
+    c.copy_(a)
+    torch.cuda.synchronize()
+    free()
+    print("traffic probe: body layer x10, then a 134217728-byte copy", flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -154,6 +197,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-sweep", action="store_true", help="skip the conv sweep")
     ap.add_argument("--kernel-reps", type=int, default=100)
+    ap.add_argument("--traffic-probe", action="store_true",
+                    help="only run the dominant layer 10 times and a 128 MiB device copy "
+                         "(the workload of the FETCH_SIZE / WRITE_SIZE counter passes)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py runs on one GPU only: this backend has no multi-GPU path "
@@ -173,6 +219,9 @@ def main():
     stream = ctx.stream
     H, W = 256, 384
     tensors = synthetic.esrgan_tensors()
+    if args.traffic_probe:
+        traffic_probe(ctx, tensors, H, W)
+        return
     image = synthetic.esrgan_image(H, W)
     model = ien.Model(ctx, ien.MODEL_REALESRGAN, tensors=tensors)
     d_in = torch.from_numpy(image).cuda()
@@ -192,16 +241,7 @@ def main():
         sys.exit("non-finite output")
 
     # Dominant kernel: one body layer (3x3 64->64 + PReLU) at 256x384.
-    w_body, b_body, s_body = synthetic.esrgan_layers(tensors)[1]
-    m = ien.Matrix(ctx, w_body, b_body)
-    slope = torch.from_numpy(s_body).cuda()
-    src = torch.from_numpy(np.random.default_rng(3).standard_normal((H * W, 64))).half().cuda()
-    dst = torch.empty((H * W, 64), dtype=torch.float16, device="cuda")
-    inp = ien.image_input(src, H, W, 64)
-
-    def body():
-        ien.multiply_ex(ctx, inp, 0, H * W, m, dst, 64, act=ien.ACT_PRELU, slope=slope)
-
+    body, body_free = body_layer(ctx, tensors, H, W)
     for _ in range(5):
         body()
     kms = event_time(body, args.kernel_reps, stream)
@@ -210,9 +250,9 @@ def main():
     roofline = {"bound": "mfma", "achieved": round(achieved, 1), "peak": MFMA_F16_PEAK_TFLOPS,
                 "unit": "TFLOP/s", "frac": round(achieved / MFMA_F16_PEAK_TFLOPS, 4),
                 "traffic": traffic_from_profiles(),
-                "kernel": "conv_mfma<3,1,4,96,4,2,64,true,false> (3x3 64->64 + PReLU, 256x384)",
+                "kernel": "conv_res8<3,64,PReLU> (resident-weight 3x3 64->64 + PReLU, 256x384)",
                 "kernel_us": round(kms * 1e3, 2), "flop_per_launch": flops}
-    m.free()
+    body_free()
 
     gemm_sweep = None if args.no_sweep else sweep(ctx, stream, args.kernel_reps)
     cpu = None if args.no_cpu else cpu_baseline(tensors, image)

@@ -618,7 +618,9 @@ ien_status launch_conv(ien_ctx *ctx, const ConvCall &c) {
   }
   // Resident weights: NHWC, zero padding, 16, 32 or 64 channels, K <= 640.
   // Its results are staged as f16: f32 outputs take the general kernel.
-  if (vec && !c.out_f32 && resident_supported(c.ks, c.stride, c.C, nchw, c.pad_reflect, c.noff, c.rows_mode))
+  if (vec && !c.out_f32 &&
+      resident_supported(c.ks, c.stride, c.C, nchw, c.pad_reflect, c.noff, c.rows_mode,
+                         (long)c.H * c.W * c.xs * 2))
     return launch_resident(ctx, a, c.ks);
   if (c.ks == 3 && c.stride == 1) {
     if (!vec) {

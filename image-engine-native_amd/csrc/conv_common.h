@@ -87,7 +87,13 @@ __device__ __forceinline__ float activate(float v, int act, float slope) {
 template <int ACT>
 __device__ __forceinline__ float act_c(float v, float slope) {
   if constexpr (ACT == IEN_ACT_RELU) return v > 0.0f ? v : 0.0f;
-  else if constexpr (ACT == IEN_ACT_PRELU) return v < 0.0f ? v * slope : v;
+  else if constexpr (ACT == IEN_ACT_PRELU) {
+    // v < 0 ? v slope : v as a bit select on v's sign (no compare, so no
+    // mask register per value); only -0 with a negative slope differs (+0).
+    const int m = __builtin_bit_cast(int, v) >> 31;
+    return __builtin_bit_cast(float, (__builtin_bit_cast(int, v * slope) & m) |
+                                         (__builtin_bit_cast(int, v) & ~m));
+  }
   else if constexpr (ACT == IEN_ACT_GELU) return gelu_f(v);
   else if constexpr (ACT == IEN_ACT_SIGMOID) return sigmoid_f(v);
   else return v;
@@ -141,7 +147,8 @@ __device__ __forceinline__ void dma16(const void *src, void *lds) {
 
 // conv_res.hip: the resident-weight kernel for NHWC inputs of 16, 32 or 64
 // channels with k x k (k = 1, 3) zero-padded taps and K = k k C <= 640.
-bool resident_supported(int ks, int stride, int c, int nchw, int reflect, int noff, int rows_mode);
+bool resident_supported(int ks, int stride, int c, int nchw, int reflect, int noff, int rows_mode,
+                        long in_bytes);
 ien_status launch_resident(ien_ctx *ctx, ConvArgs a, int ks);
 
 }  // namespace ien

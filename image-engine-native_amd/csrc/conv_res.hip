@@ -5,109 +5,219 @@
 // native/src/network.rs:96-109, gemm.rs multiply semantics) and the 1x1
 // products of that width.
 //
-// One workgroup per CU, 8 waves (2 per SIMD: the second wave hides the
-// other's MFMA and LDS latency and doubles the LDS read rate), persistent
-// over 2 x 64-pixel output tiles, all 64 output channels of a tile.
-//  - Prologue: the 64 channels' weight fragments go global -> LDS by
-//    direct-to-LDS loads (one contiguous KiB per wave instruction, read once
-//    per CU from L2), then each wave copies its 32-channel slice into VGPRs
-//    (A operand of v_mfma_f32_32x32x16_f16: the packing is the A layout, so
-//    the product is C^T = W^T X^T) and the LDS is reused for activations.
-//  - Per tile: wait for the tile's halo (double-buffered, loaded by
-//    direct-to-LDS loads issued one tile ahead, 16-byte chunks XOR-swizzled
-//    per pixel so the B-operand reads are conflict-free); write the previous
-//    tile's results from the LDS staging buffer to HBM as full 128-byte
-//    lines; run the tile's MFMAs (each wave: one 32-pixel x 32-channel block,
-//    two accumulator chains); stage bias + activation results as f16.
+// One workgroup per CU, 8 waves (2 per SIMD), persistent over 2 x 64-pixel
+// output tiles, all 64 output channels of a tile; wave w computes 32 pixels
+// (block w % 4) by 32 channels (half w / 4) with v_mfma_f32_32x32x16_f16.
+// The packed weights are the A operand, so the product is C^T = W^T X^T,
+// and each wave keeps its 32 channels' weights in VGPRs for all its tiles.
+//  - Every global read is a buffer load straight into LDS, issued from
+//    inline assembly: the compiler neither sees nor waits for them (its
+//    waits after such loads flush whole counters), so the kernel counts
+//    them itself.  Loads complete in order, so waiting until at most n
+//    vector-memory operations are outstanding means all loads but the last
+//    n issued have landed, stores in between or not.  The range check of
+//    the buffer loads supplies the zero padding.
+//  - Halo pixels are stored with a 16-byte pad chunk, so the 32 pixels of a
+//    B fragment fall on distinct LDS banks and every fragment of a tap is a
+//    fixed offset from the lane's base (ds_read_b128 with an immediate).
+//  - Three halo buffers: tile t+2's halo is loaded while tile t computes,
+//    which covers the memory latency of a whole tile.
+//  - Per tile t, one barrier, then one unrolled, branch-free MFMA sequence
+//    (one accumulator chain seeded with the bias) into which are
+//    interleaved: tile t+2's halo loads; tile t-1's epilogue (activation,
+//    f16, into a staging buffer) from the accumulators kept since; tile
+//    t-2's stores from the other staging buffer (16-byte buffer stores of
+//    whole 128-byte pixel rows; the range check drops items outside the
+//    output).
 // Bias then activation, or bias, old output, activation when accumulating:
 // the order of gemm.rs:583-666.
 
 #include "conv_common.h"
 
+#pragma clang diagnostic ignored "-Winline-asm"  // m0 is written by the loads below
+
 namespace ien {
+
+namespace {
+
+typedef int int4v __attribute__((ext_vector_type(4)));
+
+// A raw buffer resource over `bytes` bytes at `p` (offsets past it read 0).
+__device__ __forceinline__ int4v buffer_rsrc(const void *p, int bytes) {
+  const unsigned long long a = (unsigned long long)p;
+  int4v r;
+  r.x = (int)(unsigned)a;
+  r.y = (int)((a >> 32) & 0xffff);
+  r.z = bytes;
+  r.w = 0x00020000;
+  return r;
+}
+
+// LDS byte address of a pointer into __shared__ memory.
+__device__ __forceinline__ unsigned lds_addr(const void *p) {
+  return (unsigned)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+}
+
+// 16 bytes per lane from buffer offset `off` to LDS `wave_base` + 16 lane.
+// `wave_base` must be uniform.  Counted by vmcnt; invisible to the compiler.
+__device__ __forceinline__ void dma_lds(int4v rsrc, unsigned wave_base, int off) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               :: "s"(wave_base), "v"(off), "s"(rsrc) : "memory", "m0");
+}
+
+// s_waitcnt vmcnt(n) alone.
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt(0x0f70 | (N & 15) | ((N >> 4) << 14));
+}
+
+}  // namespace
 
 template <int KS, int C>
 struct Res8 {
   static constexpr int TR = 2, TC = 64;  // output tile: 2 rows of 64 pixels
   static constexpr int STEPS = KS * KS * C / 16;
-  static constexpr int HR = TR + KS - 1, HC = TC + KS - 1;
-  static constexpr int PB = C * 2, NCH = PB / 16, RPB = 256 / PB;
-  static constexpr int HALO = (HR * HC * PB + 1023) / 1024 * 1024;
-  static constexpr int SPX = 64 + 8;                  // staged halves per pixel (padded)
-  static constexpr int STAGE = TR * TC * SPX * 2;     // bytes
-  static constexpr int WBYTES = 2 * STEPS * 1024;     // B fragments of 64 channels
-  static constexpr int MAIN = 2 * HALO + STAGE;
-  static constexpr int PARAM = MAIN > WBYTES ? MAIN : WBYTES;  // bias, slopes after this
-  static constexpr int LDS = PARAM + 2 * 64 * 4;
-  static_assert(C == 16 || C == 32 || C == 64, "power-of-two chunk swizzle");
+  static constexpr int HR = TR + KS - 1, HC = TC + KS - 1, HPIX = HR * HC;
+  // Halo pixel stride: the channels plus one 16-byte pad chunk.
+  static constexpr int PB = C * 2 + 16;
+  // Whole 8 KiB, so that each of the 8 waves issues the same number of
+  // 1 KiB loads per halo.
+  static constexpr int HALO = (HPIX * PB + 8191) / 8192 * 8192;
+  static constexpr int HIT = HALO / 8192;     // halo loads per wave
+  static constexpr int SPX = 64 + 8;          // staged halves per pixel (padded)
+  static constexpr int STAGE = TR * TC * SPX * 2;
+  static constexpr int WBYTES = 2 * STEPS * 1024;  // B fragments of 64 channels
+  // LDS: 3 halo buffers | 2 staging buffers | bias (1 KiB) | slopes (1 KiB).
+  // In the prologue the weights sit over halo 2 and the staging buffers.
+  static constexpr int STG = 3 * HALO;
+  static constexpr int PARAM = STG + 2 * STAGE;
+  static constexpr int WOFF = 2 * HALO;
+  static constexpr int LDS = PARAM + 2048;
+  static constexpr int SITEMS = TR * TC * 8 / 512;  // 16-byte stores per thread and tile
+  static constexpr int DEPTH = 3;                   // fragment prefetch
+  static_assert(C == 16 || C == 32 || C == 64, "channels");
   static_assert(STEPS <= 36, "weights must fit in registers");
+  static_assert(WOFF + WBYTES <= PARAM, "prologue weights overlap the parameters");
   static_assert(LDS <= 160 * 1024, "LDS budget");
+  static_assert(SITEMS * 512 == TR * TC * 8, "store split");
+  static_assert(2 * HIT < 64, "vmcnt range");
 };
 
 template <int KS, int C, int ACT>
 __global__ __launch_bounds__(512) void conv_res8(ConvArgs a) {
   using R = Res8<KS, C>;
-  constexpr int STEPS = R::STEPS, HC = R::HC, PB = R::PB, P = KS / 2;
+  constexpr int STEPS = R::STEPS, HC = R::HC, PB = R::PB, P = KS / 2, DEPTH = R::DEPTH;
+  constexpr int HIT = R::HIT;
   __shared__ __attribute__((aligned(1024))) unsigned char lds[R::LDS];
-  unsigned char *stage = lds + 2 * R::HALO;
-  float *bias_l = (float *)(lds + R::PARAM), *slope_l = bias_l + 64;
+  const float *bias_l = (const float *)(lds + R::PARAM), *slope_l = bias_l + 256;
 
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int mg = wave & 3, ng = wave >> 2;  // 32-pixel block, 32-channel half
   const int lb = xcd_remap(blockIdx.x, gridDim.x);
   const int tn = lb % a.tiles_n;            // this block's 64-channel tile
   const int per_n = gridDim.x / a.tiles_n;  // blocks sharing it
   const int tiles_m = a.tiles_x * a.tiles_y;
-
-  // ---- prologue: weights through LDS into VGPRs; bias and slopes to LDS ----
-  for (int f = wave; f < 2 * STEPS; f += 8) {
-    const int jn = f / STEPS, s = f - jn * STEPS;
-    dma16(a.wp + ((tn * 2 + jn) * a.KB + s) * 512 + lane * 8, lds + f * 1024);
-  }
-  if (tid < 64) {
-    const int n = tn * 64 + tid;  // < NB * 32: the bias is padded
-    bias_l[tid] = a.bias[n];
-    slope_l[tid] = ACT == IEN_ACT_PRELU ? a.slope[min(n, a.N - 1)] : 0.0f;
-  }
-  __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
-  __syncthreads();
-  half8 wr[STEPS];
-#pragma unroll
-  for (int s = 0; s < STEPS; s++)
-    wr[s] = *(const half8 *)(lds + (ng * STEPS + s) * 1024 + lane * 16);
-  __syncthreads();  // every wave holds its weights: the LDS is free
-
-  // Halo pixel of tap (0, 0) for the lane's pixel; tile pixel of the lane.
-  const int tpix = (mg >> 1) * 64 + (mg & 1) * 32 + (lane & 31);
-  const int apix = (mg >> 1) * HC + (mg & 1) * 32 + (lane & 31);
+  const unsigned lds0 = lds_addr(lds);
 
   auto origin = [&](int mt, int &oy0, int &ox0) {
     oy0 = (mt / a.tiles_x + a.ty_begin) * R::TR;
     ox0 = (mt % a.tiles_x) * R::TC;
   };
 
-  auto load_halo = [&](int mt, unsigned char *buf) {
+  // Part i of a tile's halo: wave w fills KiB w + 8 i of the buffer; lane l
+  // its 16 bytes at 16 l, which belong to halo pixel hp, chunk ch (offsets
+  // past the input read the zeros of the pad chunk and padding pixels).
+  constexpr int OOB = 0x7ffffff0;
+  const int4v xr = buffer_rsrc(a.x, (int)((long)a.H * a.W * a.xs * 2));
+  auto load_halo = [&](int i, int oy0, int ox0, int buf) {
+    const int g = wave + 8 * i;
+    const int byte = g * 1024 + lane * 16;
+    const int hp = byte / PB, ch = (byte - hp * PB) >> 4;
+    const int hy = hp / HC, hx = hp - hy * HC;
+    const int iy = oy0 + hy - P, ix = ox0 + hx - P;
+    const bool ok = hp < R::HPIX && ch < C / 8 && (unsigned)iy < (unsigned)a.H &&
+                    (unsigned)ix < (unsigned)a.W;
+    const int off = ok ? ((iy * a.W + ix) * a.xs + 8 * ch) * 2 : OOB;
+    dma_lds(xr, __builtin_amdgcn_readfirstlane(lds0 + buf * R::HALO + g * 1024), off);
+  };
+  auto load_tile = [&](int mtl, int buf) {
     int oy0, ox0;
-    origin(mt, oy0, ox0);
-    for (int g = wave; g < R::HALO / 1024; g += 8) {
-      const int byte = g * 1024 + lane * 16;
-      const int hp = byte / PB, slot = (byte % PB) / 16;
-      const uint16_t *src = a.zeros;
-      if (hp < R::HR * HC) {
-        const int hy = hp / HC, hx = hp - hy * HC;
-        const int iy = oy0 + hy - P, ix = ox0 + hx - P;
-        if (iy >= 0 && iy < a.H && ix >= 0 && ix < a.W)
-          src = a.x + (iy * a.W + ix) * a.xs + 8 * (slot ^ ((hp / R::RPB) & (R::NCH - 1)));
-      }
-      dma16(src, buf + g * 1024);
-    }
+    origin(mtl, oy0, ox0);
+#pragma unroll
+    for (int i = 0; i < HIT; i++) load_halo(i, oy0, ox0, buf);
   };
 
-  // The staged tile to HBM: 16 bytes (8 channels of one pixel) per item,
-  // 8 items per pixel, so a wave writes 8 whole pixels (full lines).
-  auto store_tile = [&](int mt) {
+  // ---- prologue: bias, slopes, weights, then the halos of the first two
+  // tiles (the second is the first again when there is none) ----
+  if (wave == 0) {  // lanes 0-15: the 64 biases of the tile (padded to NB * 32)
+    dma_lds(buffer_rsrc(a.bias, a.NB * 32 * 4), __builtin_amdgcn_readfirstlane(lds0 + R::PARAM),
+            lane < 16 ? (tn * 64 + 4 * lane) * 4 : OOB);
+  } else if (wave == 1) {  // lanes 0-15: the slopes (zeros unless PReLU)
+    dma_lds(buffer_rsrc(a.slope, a.act == IEN_ACT_PRELU ? a.N * 4 : 0),
+            __builtin_amdgcn_readfirstlane(lds0 + R::PARAM + 1024),
+            lane < 16 ? (tn * 64 + 4 * lane) * 4 : OOB);
+  }
+  {
+    const int4v wrs = buffer_rsrc(a.wp, a.NB * a.KB * 1024);
+    for (int f = wave; f < 2 * STEPS; f += 8) {
+      const int jn = f / STEPS, s = f - jn * STEPS;
+      dma_lds(wrs, __builtin_amdgcn_readfirstlane(lds0 + R::WOFF + f * 1024),
+              ((tn * 2 + jn) * a.KB + s) * 1024 + lane * 16);
+    }
+  }
+  int mt = lb / a.tiles_n;
+  const bool any = mt < tiles_m;
+  if (any) {
+    load_tile(mt, 0);
+    load_tile(mt + per_n < tiles_m ? mt + per_n : mt, 1);
+  }
+  wait_vm<2 * HIT>();  // bias, slopes, weights (the halos may be in flight)
+  __syncthreads();
+  half8 wr[STEPS];
+#pragma unroll
+  for (int s = 0; s < STEPS; s++)
+    wr[s] = *(const half8 *)(lds + R::WOFF + (ng * STEPS + s) * 1024 + lane * 16);
+  if (any)
+    wait_vm<HIT>();  // the first tile's halo
+  else
+    wait_vm<0>();  // no tile: nothing may still be writing LDS at the end
+  __syncthreads();  // ... of every wave; the weights are in registers
+
+  const int tpix = (mg >> 1) * 64 + (mg & 1) * 32 + (lane & 31);
+  const int abase = ((mg >> 1) * HC + (mg & 1) * 32 + (lane & 31)) * PB + 16 * (lane >> 5);
+
+  // Plain f16 NHWC outputs of whole 16-byte chunks below 2 GiB go out as
+  // buffer stores; anything else element by element (store_slow).
+  const long out_bytes = (long)(a.p_end - a.p_begin) * a.ys * 2;
+  const bool fast = !a.accumulate && !a.out_f32 && !a.out_nchw && a.N % 8 == 0 &&
+                    a.ys % 8 == 0 && (((uintptr_t)a.y) & 15) == 0 && out_bytes <= 0x7fff0000L;
+  const __amdgpu_buffer_rsrc_t yr =
+      __builtin_amdgcn_make_buffer_rsrc(a.y, 0, fast ? (int)out_bytes : 0, 0x00020000);
+
+  // Byte offset of output item j of this thread (16 bytes: 8 channels of
+  // one pixel; 8 consecutive threads write one pixel's 128 bytes), or OOB.
+  auto item_off = [&](int j, int mts, bool valid) -> int {
     int oy0, ox0;
-    origin(mt, oy0, ox0);
+    origin(mts, oy0, ox0);
+    const int v = tid + 512 * j, tp = v >> 3, chunk = v & 7;
+    const int oy = oy0 + tp / R::TC, ox = ox0 + tp % R::TC;
+    const int p = oy * a.OW + ox;
+    const int n0 = tn * 64 + chunk * 8;
+    const bool ok = valid && oy < a.OH && ox < a.OW && p >= a.p_begin && p < a.p_end && n0 < a.N;
+    return ok ? ((p - a.p_begin) * a.ys + n0) * 2 : OOB;
+  };
+  auto item_src = [&](int j, const unsigned char *stage) {
+    const int v = tid + 512 * j;
+    return *(const u32x4 *)(stage + ((v >> 3) * R::SPX + (v & 7) * 8) * 2);
+  };
+
+  // Accumulating, NCHW or ragged outputs: the staged sums (bias included,
+  // no activation when accumulating) element by element.
+  auto store_slow = [&](int mts, const unsigned char *stage) {
+    int oy0, ox0;
+    origin(mts, oy0, ox0);
     for (int v = tid; v < R::TR * R::TC * 8; v += 512) {
       const int tp = v >> 3, chunk = v & 7;
       const int oy = oy0 + tp / R::TC, ox = ox0 + tp % R::TC;
@@ -116,110 +226,179 @@ __global__ __launch_bounds__(512) void conv_res8(ConvArgs a) {
       if (oy >= a.OH || ox >= a.OW || p < a.p_begin || p >= a.p_end || n0 >= a.N) continue;
       const int rel = p - a.p_begin;
       u32x4 hv = *(const u32x4 *)(stage + (tp * R::SPX + chunk * 8) * 2);
-      uint16_t *yo = (uint16_t *)a.y + (long)rel * a.ys + n0;
-      if (!a.accumulate && !a.out_f32 && !a.out_nchw && n0 + 8 <= a.N &&
-          (((uintptr_t)yo) & 15) == 0) {
-        *(u32x4 *)yo = hv;
-        continue;
-      }
       uint16_t h[8];
       __builtin_memcpy(h, &hv, 16);
       for (int e = 0; e < 8 && n0 + e < a.N; e++) {
         const long at = a.out_nchw ? (long)(n0 + e) * a.ys + rel : (long)rel * a.ys + n0 + e;
         float o = h2f(h[e]);
-        const float sl = slope_l[chunk * 8 + e];
-        if (a.out_f32) {
-          float *yf = (float *)a.y + at;
-          if (a.accumulate) o = act_c<ACT>(o + *yf, sl);
-          *yf = o;
-        } else {
-          uint16_t *yh = (uint16_t *)a.y + at;
-          if (a.accumulate) o = act_c<ACT>(o + h2f(*yh), sl);
-          *yh = f2h(o);
-        }
+        uint16_t *yh = (uint16_t *)a.y + at;
+        if (a.accumulate) o = activate(o + h2f(*yh), a.act, slope_l[chunk * 8 + e]);
+        *yh = f2h(o);
       }
     }
   };
 
-  auto mma = [&](const unsigned char *buf, floatx16 &acc_a, floatx16 &acc_b) {
+  // One of the 4 epilogue groups of a finished tile.  C^T fragment: the
+  // lane holds pixel lane % 32 of its block; register 4 g + e is channel
+  // 32 ng + 8 g + 4 (lane / 32) + e.  (When accumulating, the dispatch
+  // picks ACT = none: the sum is staged and activated after the old output.)
+  auto epilogue = [&](const floatx16 &acc, int g, unsigned char *stage) {
+    const int ch = ng * 32 + 8 * g + 4 * (lane >> 5);
+    const float4v s4 = *(const float4v *)(slope_l + ch);
+    uint16_t h[4];
 #pragma unroll
-    for (int r = 0; r < 16; r++) {
-      acc_a[r] = 0.0f;
-      acc_b[r] = 0.0f;
-    }
-    auto frag = [&](int s) {
-      const int tap = s / (C / 16), kc = s % (C / 16);
-      const int p = apix + (tap / KS) * HC + tap % KS;
-      const int c = 2 * kc + (lane >> 5);
-      return *(const half8 *)(buf + p * PB + 16 * (c ^ ((p / R::RPB) & (R::NCH - 1))));
-    };
-    half8 xv[2];
-    xv[0] = frag(0);
-#pragma unroll
-    for (int s = 0; s < STEPS; s++) {
-      if (s + 1 < STEPS) xv[(s + 1) & 1] = frag(s + 1);
-      __builtin_amdgcn_sched_barrier(0);
-      if (s & 1)
-        acc_b = __builtin_amdgcn_mfma_f32_32x32x16_f16(wr[s], xv[s & 1], acc_b, 0, 0, 0);
-      else
-        acc_a = __builtin_amdgcn_mfma_f32_32x32x16_f16(wr[s], xv[s & 1], acc_a, 0, 0, 0);
-      __builtin_amdgcn_sched_barrier(0);
-    }
+    for (int e = 0; e < 4; e++) h[e] = f2h(act_c<ACT>(acc[4 * g + e], s4[e]));
+    uint2 o;
+    __builtin_memcpy(&o, h, 8);
+    *(uint2 *)(stage + (tpix * R::SPX + ch) * 2) = o;
   };
 
-  // C^T fragment: the lane holds pixel lane % 32 of its block and channels
-  // 32 ng + 8 g + 4 (lane / 32) + e of the tile.
-  auto stage_tile = [&](const floatx16 &acc_a, const floatx16 &acc_b) {
+  auto bias_acc = [&]() {
+    floatx16 acc;
 #pragma unroll
     for (int g = 0; g < 4; g++) {
-      const int ch = ng * 32 + 8 * g + 4 * (lane >> 5);
-      const float4v b4 = *(const float4v *)(bias_l + ch);
-      const float4v s4 = *(const float4v *)(slope_l + ch);
-      uint16_t h[4];
+      const float4v b4 = *(const float4v *)(bias_l + ng * 32 + 8 * g + 4 * (lane >> 5));
 #pragma unroll
-      for (int e = 0; e < 4; e++) {
-        float v = acc_a[4 * g + e] + acc_b[4 * g + e] + b4[e];
-        if (!a.accumulate) v = act_c<ACT>(v, s4[e]);
-        h[e] = f2h(v);
-      }
-      uint2 o;
-      __builtin_memcpy(&o, h, 8);
-      *(uint2 *)(stage + (tpix * R::SPX + ch) * 2) = o;
+      for (int e = 0; e < 4; e++) acc[4 * g + e] = b4[e];
     }
+    return acc;
   };
 
-  int mt = lb / a.tiles_n;
-  if (mt < tiles_m) load_halo(mt, lds);
-  int prev = -1;
-  bool odd = false;
+  // The MFMA sequence of tile t on halo buffer `cur`, with tile t+2's halo
+  // loads into buffer `nxt` and (unless FIRST: no earlier tile) tile t-1's
+  // epilogue and tile t-2's stores spread over the steps.
+  auto mma = [&](auto first, int cur, int nxt, int nmt, bool dma, const floatx16 &acc1,
+                 unsigned char *stage1, const int *soff, const unsigned char *stage2) {
+    constexpr bool FIRST = decltype(first)::value;
+    int noy0, nox0;
+    origin(nmt, noy0, nox0);
+    const unsigned char *bp = lds + cur * R::HALO + abase;
+    auto frag = [&](int s) {
+      const int tap = s / (C / 16), kc = s % (C / 16);
+      return *(const half8 *)(bp + ((tap / KS) * HC + tap % KS) * PB + 32 * kc);
+    };
+    u32x4 sv[R::SITEMS];
+    // Event e at step e * STEPS / NEV, in this order: staged reads of tile
+    // t-2, the first halo load, the stores of tile t-2, the other halo
+    // loads, the epilogue groups of tile t-1.
+    constexpr int NS = R::SITEMS, NEV = FIRST ? HIT : 2 * NS + HIT + 4;
+    auto event = [&](int e) {
+      if constexpr (FIRST) {
+        if (dma) load_halo(e, noy0, nox0, nxt);
+      } else {
+        if (e < NS) {
+          sv[e] = item_src(e, stage2);
+        } else if (e == NS) {
+          if (dma) load_halo(0, noy0, nox0, nxt);
+        } else if (e < 2 * NS + 1) {
+          const int j = e - NS - 1;
+          __builtin_amdgcn_raw_buffer_store_b128(sv[j], yr, soff[j], 0, 0);
+        } else if (e < 2 * NS + HIT) {
+          if (dma) load_halo(e - 2 * NS, noy0, nox0, nxt);
+        } else {
+          epilogue(acc1, e - 2 * NS - HIT, stage1);
+        }
+      }
+    };
+    floatx16 acc = bias_acc();
+    half8 xv[DEPTH + 1];
+#pragma unroll
+    for (int s = 0; s < DEPTH && s < STEPS; s++) xv[s] = frag(s);
+#pragma unroll
+    for (int s = 0; s < STEPS; s++) {
+      if (s + DEPTH < STEPS) xv[(s + DEPTH) % (DEPTH + 1)] = frag(s + DEPTH);
+#pragma unroll
+      for (int e = 0; e < NEV; e++)
+        if (e * STEPS / NEV == s) event(e);
+      __builtin_amdgcn_sched_barrier(0);
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(wr[s], xv[s % (DEPTH + 1)], acc, 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    return acc;
+  };
+
+  // Iteration t: halo buffer t % 3 holds tile t (t+1's is in flight, t+2's
+  // is loaded here into buffer (t + 2) % 3, which held tile t-1); staging
+  // buffer t % 2 receives tile t-1 and buffer (t + 1) % 2 holds tile t-2.
+  auto stage_buf = [&](int k) { return lds + R::STG + k * R::STAGE; };
+  floatx16 acc1 = {};
+  int mt1 = -1, mt2 = -1;  // the tiles one and two iterations back
+  int t = 0, h = 0;        // h = t % 3
   while (mt < tiles_m) {
-    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this tile's halo has landed
-    __syncthreads();  // ... for every wave; the staging holds the previous tile
-    const int next = mt + per_n;
-    if (next < tiles_m) load_halo(next, odd ? lds : lds + R::HALO);
-    if (prev >= 0) store_tile(prev);
-    floatx16 acc_a, acc_b;
-    mma(odd ? lds + R::HALO : lds, acc_a, acc_b);
-    __syncthreads();  // every wave has read the staging
-    stage_tile(acc_a, acc_b);
-    prev = mt;
-    mt = next;
-    odd = !odd;
+    const int far = mt + 2 * per_n;
+    const bool dma = far < tiles_m;  // a uniform branch: no load without a tile
+    const int h2 = h == 0 ? 2 : h - 1;  // (t + 2) % 3
+    floatx16 acc;
+    if (t == 0) {
+      acc = mma(std::true_type{}, h, h2, far, dma, acc1, nullptr, nullptr, nullptr);
+    } else {
+      const int par = t & 1;
+      unsigned char *st1 = stage_buf(par);
+      const unsigned char *st2 = stage_buf(par ^ 1);
+      if (mt2 >= 0 && !fast) store_slow(mt2, st2);
+      int soff[R::SITEMS];
+#pragma unroll
+      for (int j = 0; j < R::SITEMS; j++)
+        soff[j] = item_off(j, mt2 < 0 ? mt : mt2, mt2 >= 0 && fast);
+      acc = mma(std::false_type{}, h, h2, far, dma, acc1, st1, soff, st2);
+    }
+    acc1 = acc;
+    mt2 = mt1;
+    mt1 = mt;
+    mt += per_n;
+    t++;
+    h = h == 2 ? 0 : h + 1;
+    // Tile t+1's halo (loaded before this iteration's HIT loads, which may
+    // be in flight; without them the stores in between could be counted
+    // in their place, so then wait for everything).
+    if (dma)
+      wait_vm<HIT>();
+    else
+      wait_vm<0>();
+    __syncthreads();  // ... of every wave; staging written, buffers read
+  }
+  // Drain: tile t-2's stores and tile t-1's epilogue, then tile t-1's stores.
+  const int par = t & 1;
+  if (mt2 >= 0) {
+    if (fast) {
+#pragma unroll
+      for (int j = 0; j < R::SITEMS; j++)
+        __builtin_amdgcn_raw_buffer_store_b128(item_src(j, stage_buf(par ^ 1)), yr,
+                                               item_off(j, mt2, true), 0, 0);
+    } else {
+      store_slow(mt2, stage_buf(par ^ 1));
+    }
+  }
+  if (mt1 >= 0) {
+#pragma unroll
+    for (int g = 0; g < 4; g++) epilogue(acc1, g, stage_buf(par));
   }
   __syncthreads();
-  if (prev >= 0) store_tile(prev);
+  if (mt1 >= 0) {
+    if (fast) {
+#pragma unroll
+      for (int j = 0; j < R::SITEMS; j++)
+        __builtin_amdgcn_raw_buffer_store_b128(item_src(j, stage_buf(par)), yr,
+                                               item_off(j, mt1, true), 0, 0);
+    } else {
+      store_slow(mt1, stage_buf(par));
+    }
+  }
 }
 
-bool resident_supported(int ks, int stride, int c, int nchw, int reflect, int noff, int rows_mode) {
+bool resident_supported(int ks, int stride, int c, int nchw, int reflect, int noff, int rows_mode,
+                        long in_bytes) {
+  // Buffer-load offsets are 32-bit: inputs below 2 GiB.
   return (ks == 1 || ks == 3) && stride == 1 && (c == 16 || c == 32 || c == 64) && !nchw &&
-         !reflect && noff == 0 && !rows_mode && ks * ks * c / 16 <= 36;
+         !reflect && noff == 0 && !rows_mode && ks * ks * c / 16 <= 36 && in_bytes <= 0x7fff0000L;
 }
 
 template <int KS, int C>
 static ien_status run_res8(ien_ctx *ctx, ConvArgs a) {
   using R = Res8<KS, C>;
   void (*kernel)(ConvArgs) = nullptr;
-  switch (a.act) {
+  // Accumulating: the sums are staged and activated after the old output.
+  switch (a.accumulate ? IEN_ACT_NONE : a.act) {
     case IEN_ACT_RELU: kernel = conv_res8<KS, C, IEN_ACT_RELU>; break;
     case IEN_ACT_PRELU: kernel = conv_res8<KS, C, IEN_ACT_PRELU>; break;
     case IEN_ACT_GELU: kernel = conv_res8<KS, C, IEN_ACT_GELU>; break;

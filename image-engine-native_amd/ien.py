@@ -208,6 +208,7 @@ def image_input(x, height, width, channels, stride=None, layout=NHWC, size=3, st
     s = Input()
     s.kind = INPUT_IMAGE
     s.data = x.data_ptr()
+    s._tensor = x  # the descriptor holds a raw pointer: keep its storage alive
     s.height, s.width, s.channels = height, width, channels
     s.stride = stride if stride is not None else (channels if layout == NHWC else height * width)
     s.layout = layout
@@ -224,6 +225,7 @@ def rows_input(x, stride):
     s = Input()
     s.kind = INPUT_ROWS
     s.data = x.data_ptr()
+    s._tensor = x  # the descriptor holds a raw pointer: keep its storage alive
     s.stride = stride
     return s
 

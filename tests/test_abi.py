@@ -47,3 +47,26 @@ def test_null_arguments_are_input_errors():
     assert L.ien_sync(None) == ien.ERR_INPUT
     assert L.ien_last_error().startswith(b"input: ")
     assert L.ien_model_set_graph(None, 1) == ien.ERR_INPUT
+
+
+def test_descriptors_keep_their_tensor_alive():
+    """An ien_input holds a raw pointer; the Python descriptor must keep the
+    tensor behind it alive (a capture's empty_cache would otherwise return
+    the freed block to the driver while a replay still reads it)."""
+    import gc
+    import weakref
+
+    import torch
+
+    import ien
+
+    x = torch.zeros(64, 16, dtype=torch.float16)
+    ref = weakref.ref(x)
+    inp = ien.image_input(x, 4, 16, 16)
+    rows = ien.rows_input(x, 16)
+    del x
+    gc.collect()
+    assert ref() is not None and inp._tensor is ref() and rows._tensor is ref()
+    del inp, rows
+    gc.collect()
+    assert ref() is None
