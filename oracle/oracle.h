@@ -89,6 +89,33 @@ void or_conv3_form(int threads, int form, const or_input *in, const float *w,
 void or_attention(const float *qkv, size_t tokens, size_t c, size_t head,
                   const float *bias, float *out);
 
+/* ---- Swin window attention (scunet swin.rs, birefnet swin.rs) -------- */
+enum { OR_POS_SCUNET = 0, OR_POS_SWIN = 1 };
+/* The relative-position bias [heads][N][N] of a W x W window from its table:
+ * OR_POS_SCUNET [heads][2W-1][2W-1] (tools/scunet/export_weights.py:61-67),
+ * OR_POS_SWIN [(2W-1)^2][heads] indexed (dy+W-1)(2W-1)+(dx+W-1). */
+void or_position_bias(const float *table, size_t heads, size_t window, int layout,
+                      float *out);
+/* swin.rs bias_tables (scunet :26-50, birefnet :31-51): returns the number of
+ * classes written to out ([classes][heads][N][N]): 1 unshifted, 4 shifted. */
+size_t or_bias_tables(const float *position, size_t heads, size_t window, size_t shift,
+                      float masked, float *out);
+/* Source token of window token i of window w (-1: padding past the edge). */
+long or_window_source(size_t w, size_t i, size_t window, size_t shift, size_t height,
+                      size_t width);
+/* Class of window w in a block rolled by `shift` (0 when unshifted). */
+size_t or_window_class(size_t w, size_t window, size_t shift, size_t height, size_t width);
+/* The attention half of a Swin block, in place (scunet swin.rs:131-232,
+ * birefnet swin.rs:219-306); weights row-major k x n. */
+void or_swin_attend(int threads, float *map, size_t stride, size_t height, size_t width,
+                    size_t c, size_t window, size_t shift, const float *gamma,
+                    const float *beta, const float *wqkv, const float *bqkv,
+                    const float *tables, const float *wproj, const float *bproj);
+/* The MLP half (scunet swin.rs:236-275, birefnet swin.rs:308-347), in place. */
+void or_swin_mlp(int threads, float *map, size_t stride, size_t rows, size_t c,
+                 const float *gamma, const float *beta, const float *w1, const float *b1,
+                 const float *w2, const float *b2);
+
 /* ---- realesrgan-native network.rs ------------------------------------- */
 /* network.rs:80-141: 34 conv3 layers (PReLU on all but the last), then the
  * x4 pixel shuffle plus the input repeated.  w[i] is 9cin x cout row-major

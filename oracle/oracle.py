@@ -74,6 +74,15 @@ def lib():
         L.or_conv3.argtypes = [ctypes.c_int, vp, vp, sz, vp, vp, sz, ctypes.c_int, ctypes.c_int, vp]
         L.or_conv3_form.argtypes = [ctypes.c_int, ctypes.c_int, vp, vp, sz, vp, vp, sz, ctypes.c_int, ctypes.c_int, vp]
         L.or_attention.argtypes = [vp, sz, sz, sz, vp, vp]
+        L.or_position_bias.argtypes = [vp, sz, sz, ctypes.c_int, vp]
+        L.or_bias_tables.restype = sz
+        L.or_bias_tables.argtypes = [vp, sz, sz, sz, f, vp]
+        L.or_window_source.restype = ctypes.c_long
+        L.or_window_source.argtypes = [sz, sz, sz, sz, sz, sz]
+        L.or_window_class.restype = sz
+        L.or_window_class.argtypes = [sz, sz, sz, sz, sz]
+        L.or_swin_attend.argtypes = [ctypes.c_int, vp, sz, sz, sz, sz, sz, sz, vp, vp, vp, vp, vp, vp, vp]
+        L.or_swin_mlp.argtypes = [ctypes.c_int, vp, sz, sz, sz, vp, vp, vp, vp, vp, vp]
         L.or_realesrgan_run.restype = ctypes.c_int
         L.or_realesrgan_run.argtypes = [ctypes.c_int, vp, vp, vp, vp, sz, sz, vp]
         L.or_pixel_shuffle_add.argtypes = [vp, vp, sz, sz, vp]
@@ -220,6 +229,55 @@ def attention(qkv, c, head, bias):
     out = np.zeros((tokens, c), np.float32)
     lib().or_attention(_p(qkv), tokens, c, head, _p(bias), _p(out))
     return out
+
+
+# ---- Swin window attention -------------------------------------------------
+POS_SCUNET, POS_SWIN = 0, 1
+
+
+def position_bias(table, heads, window, layout):
+    """[heads, N, N] relative-position bias of a window from its table."""
+    n = window * window
+    out = np.zeros((heads, n, n), np.float32)
+    lib().or_position_bias(_p(_f32(table)), heads, window, layout, _p(out))
+    return out
+
+
+def bias_tables(position, window, shift, masked):
+    """[classes, heads, N, N]: 1 class unshifted, 4 shifted."""
+    position = _f32(position)
+    heads, n = position.shape[0], window * window
+    out = np.zeros((4, heads, n, n), np.float32)
+    k = lib().or_bias_tables(_p(position), heads, window, shift, masked, _p(out))
+    return out[:k]
+
+
+def window_source(w, i, window, shift, height, width):
+    return lib().or_window_source(w, i, window, shift, height, width)
+
+
+def window_class(w, window, shift, height, width):
+    return lib().or_window_class(w, window, shift, height, width)
+
+
+def swin_attend(x, window, shift, gamma, beta, wqkv, bqkv, tables, wproj, bproj, threads=None):
+    """The attention half of a Swin block on an H x W x c map (returns a copy)."""
+    x = _f32(x).copy()
+    h, wd, c = x.shape
+    lib().or_swin_attend(threads or threads_default(), _p(x), c, h, wd, c, window, shift, _p(_f32(gamma)),
+                         _p(_f32(beta)), _p(_f32(wqkv)), _p(_f32(bqkv)), _p(_f32(tables)), _p(_f32(wproj)),
+                         _p(_f32(bproj)))
+    return x
+
+
+def swin_mlp(x, gamma, beta, w1, b1, w2, b2, threads=None):
+    """The MLP half on rows of c values (returns a copy)."""
+    x = _f32(x).copy()
+    c = x.shape[-1]
+    rows = x.size // c
+    lib().or_swin_mlp(threads or threads_default(), _p(x), c, rows, c, _p(_f32(gamma)), _p(_f32(beta)),
+                      _p(_f32(w1)), _p(_f32(b1)), _p(_f32(w2)), _p(_f32(b2)))
+    return x
 
 
 # ---- realesrgan-native -----------------------------------------------------

@@ -48,6 +48,56 @@ def conv_nhwc(x, w, b, size, step=1, pad="zero"):
     return y[0].numpy().transpose(1, 2, 0)
 
 
+def swin_attend_torch(x, window, shift, masked, gamma, beta, wqkv, bqkv, pos, wproj, bproj):
+    """The attention half of a Swin block in the standard formulation:
+    LayerNorm, zero-pad to whole windows, roll by -shift, window partition,
+    multi-head attention with the position bias and the region mask of the
+    shifted map (img_mask slices, as in timm / SCUNet), reverse partition,
+    roll back, crop, residual.  x: [H, W, c] float64."""
+    h, wd, c = x.shape
+    heads, n = c // 32, window * window
+    xn = F.layer_norm(x, (c,), gamma, beta, eps=1e-5)
+    ph, pw = -(-h // window) * window, -(-wd // window) * window
+    xp = F.pad(xn, (0, 0, 0, pw - wd, 0, ph - h))
+    if shift:
+        xp = torch.roll(xp, shifts=(-shift, -shift), dims=(0, 1))
+
+    def part(t):
+        return t.reshape(ph // window, window, pw // window, window, -1).permute(0, 2, 1, 3, 4).reshape(-1, n, t.shape[-1])
+
+    win = part(xp)
+    nw = win.shape[0]
+    qkv = win @ wqkv + bqkv
+    q, k, v = qkv.split(c, dim=-1)
+    q = q.reshape(nw, n, heads, 32).transpose(1, 2)
+    k = k.reshape(nw, n, heads, 32).transpose(1, 2)
+    v = v.reshape(nw, n, heads, 32).transpose(1, 2)
+    attn = (q * 32 ** -0.5) @ k.transpose(-2, -1) + pos[None]
+    if shift:
+        img = torch.zeros(ph, pw, 1, dtype=torch.float64)
+        cnt = 0
+        for hs in (slice(0, -window), slice(-window, -shift), slice(-shift, None)):
+            for ws in (slice(0, -window), slice(-window, -shift), slice(-shift, None)):
+                img[hs, ws] = cnt
+                cnt += 1
+        mw = part(img)[..., 0]
+        am = mw[:, None, :] - mw[:, :, None]
+        am = torch.where(am != 0, torch.tensor(masked, dtype=torch.float64), torch.tensor(0.0, dtype=torch.float64))
+        attn = attn + am[:, None]
+    attn = torch.softmax(attn, dim=-1)
+    o = (attn @ v).transpose(1, 2).reshape(nw, n, c) @ wproj + bproj
+    y = o.reshape(ph // window, pw // window, window, window, c).permute(0, 2, 1, 3, 4).reshape(ph, pw, c)
+    if shift:
+        y = torch.roll(y, shifts=(shift, shift), dims=(0, 1))
+    return x + y[:h, :wd]
+
+
+def swin_mlp_torch(x, gamma, beta, w1, b1, w2, b2):
+    c = x.shape[-1]
+    hdn = F.gelu(F.layer_norm(x, (c,), gamma, beta, eps=1e-5) @ w1 + b1, approximate="none")
+    return x + hdn @ w2 + b2
+
+
 def main():
     rng = np.random.default_rng(20261201)
     out = {}
@@ -118,6 +168,41 @@ def main():
         v = torch.from_numpy(qkv[:, 2 * c + head * 32:2 * c + head * 32 + 32].astype(np.float64))[None, None]
         y = F.scaled_dot_product_attention(q, kk, v, attn_mask=torch.from_numpy(bias.astype(np.float64))[None, None])
         out[f"attn{tokens}_qkv"], out[f"attn{tokens}_bias"], out[f"attn{tokens}_y"] = qkv, bias, y[0, 0].numpy()
+
+    # Swin window attention blocks (scunet swin.rs, birefnet swin.rs) on small
+    # maps: SCUNet's window 8 / shift 4 with a -inf mask, the configuration's
+    # BiRefNet window 12 / shift 6 with -100 on a map that needs padding, and
+    # unshifted blocks.  For these (window = 2 shift) the standard three-slice
+    # region mask is the reference's two-region one.
+    for name, (h, wd, c, window, shift, masked) in {
+        "swin_w8s4": (16, 24, 64, 8, 4, float("-inf")),
+        "swin_w8s0": (16, 16, 64, 8, 0, float("-inf")),
+        "swin_w12s6": (15, 13, 32, 12, 6, -100.0),
+    }.items():
+        heads, n = c // 32, window * window
+        x = f32(rng.standard_normal((h, wd, c)))
+        g = f32(1 + 0.1 * rng.standard_normal(c))
+        bt = f32(0.1 * rng.standard_normal(c))
+        wqkv = f32(rng.standard_normal((c, 3 * c)) / np.sqrt(c))
+        bqkv = f32(0.1 * rng.standard_normal(3 * c))
+        pos = f32(rng.standard_normal((heads, n, n)))
+        wproj = f32(rng.standard_normal((c, c)) / np.sqrt(c))
+        bproj = f32(0.1 * rng.standard_normal(c))
+        t = lambda a: torch.from_numpy(a.astype(np.float64))
+        y = swin_attend_torch(t(x), window, shift, masked, t(g), t(bt), t(wqkv), t(bqkv), t(pos), t(wproj), t(bproj))
+        for k, v in dict(x=x, g=g, b=bt, wqkv=wqkv, bqkv=bqkv, pos=pos, wproj=wproj, bproj=bproj).items():
+            out[f"{name}_{k}"] = v
+        out[f"{name}_y"] = y.numpy()
+    x = f32(rng.standard_normal((37, 64)))
+    g = f32(1 + 0.1 * rng.standard_normal(64))
+    bt = f32(0.1 * rng.standard_normal(64))
+    w1 = f32(rng.standard_normal((64, 256)) / 8)
+    b1 = f32(0.1 * rng.standard_normal(256))
+    w2 = f32(rng.standard_normal((256, 64)) / 16)
+    b2 = f32(0.1 * rng.standard_normal(64))
+    t = lambda a: torch.from_numpy(a.astype(np.float64))
+    out.update(mlp_x=x, mlp_g=g, mlp_b=bt, mlp_w1=w1, mlp_b1=b1, mlp_w2=w2, mlp_b2=b2)
+    out["mlp_y"] = swin_mlp_torch(t(x), t(g), t(bt), t(w1), t(b1), t(w2), t(b2)).numpy()
 
     # realesrgan network.rs:115-141: pixel shuffle x4 of 48 channels plus
     # the input repeated, against pixel_shuffle + nearest interpolate.
