@@ -1,0 +1,399 @@
+// window.hip -- Swin window attention on gfx950: the rolled window gather
+// with its LayerNorm, attention over every window and head on MFMA, the
+// residual scatter, and the host-side position-bias and mask tables
+// (crates/scunet-native/src/swin.rs, crates/birefnet-native/src/swin.rs,
+// crates/native-engine/src/attention.rs).
+
+#include "conv_common.h"
+
+namespace ien {
+namespace {
+
+// A block's window geometry (ien_windows plus what follows from it).
+struct WinGeo {
+  int window, shift, height, width;
+  int ph, pw;  // the map padded to whole windows
+  int wx;      // windows per row of windows
+  int n;       // tokens per window
+  long windows;
+};
+
+// Source token of window token i of window w, or -1 past the map's edge:
+// ((wy W + i / W + shift) mod ph, (wx W + i % W + shift) mod pw).
+__device__ __forceinline__ long win_source(const WinGeo &g, long w, int i) {
+  const int wy = (int)(w / g.wx), wxi = (int)(w - (long)wy * g.wx);
+  int y = wy * g.window + i / g.window + g.shift;
+  int x = wxi * g.window + i % g.window + g.shift;
+  if (y >= g.ph) y -= g.ph;  // shift < window <= ph: one wrap at most
+  if (x >= g.pw) x -= g.pw;
+  if (y >= g.height || x >= g.width) return -1;
+  return (long)y * g.width + x;
+}
+
+// swin.rs:171-176: 1 for a window last in its row, 2 last in its column.
+__device__ __forceinline__ int win_class(const WinGeo &g, long w) {
+  if (g.shift == 0) return 0;
+  const long rows = g.windows / g.wx;
+  return (int)(w % g.wx == g.wx - 1) + 2 * (int)(w / g.wx == rows - 1);
+}
+
+__device__ __forceinline__ void unpack8(const u32x4 &raw, float *v) {
+  uint16_t h[8];
+  __builtin_memcpy(h, &raw, 16);
+#pragma unroll
+  for (int e = 0; e < 8; e++) v[e] = h2f(h[e]);
+}
+
+__device__ __forceinline__ u32x4 pack8(const float *v) {
+  uint16_t h[8];
+#pragma unroll
+  for (int e = 0; e < 8; e++) h[e] = f2h(v[e]);
+  u32x4 raw;
+  __builtin_memcpy(&raw, h, 16);
+  return raw;
+}
+
+// One wave per window row: gather, LayerNorm (mean, then the mean square
+// deviation, eps 1e-5: math.rs:95-116), or a zero row past the edge.  Each
+// lane holds up to two 8-channel chunks (c <= 1024).
+__global__ __launch_bounds__(256) void k_window_gather(WinGeo g, const uint16_t *__restrict__ map,
+                                                       long stride, int c,
+                                                       const float *__restrict__ gamma,
+                                                       const float *__restrict__ beta,
+                                                       uint16_t *__restrict__ tokens) {
+  const int lane = threadIdx.x & 63;
+  const long row = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= g.windows * g.n) return;
+  const long src = win_source(g, row / g.n, (int)(row % g.n));
+  uint16_t *dst = tokens + row * c;
+  const int chunks = c >> 3;
+  if (src < 0) {
+    const u32x4 zero = {0u, 0u, 0u, 0u};
+    for (int k = lane; k < chunks; k += 64) *(u32x4 *)(dst + 8 * k) = zero;
+    return;
+  }
+  const uint16_t *s = map + src * stride;
+  float v[16];
+  float sum = 0.0f;
+#pragma unroll
+  for (int q = 0; q < 2; q++) {
+    const int k = lane + 64 * q;
+    if (k < chunks) {
+      unpack8(*(const u32x4 *)(s + 8 * k), v + 8 * q);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; e++) v[8 * q + e] = 0.0f;
+    }
+#pragma unroll
+    for (int e = 0; e < 8; e++) sum += v[8 * q + e];
+  }
+  for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
+  const float mean = sum / (float)c;
+  float sq = 0.0f;
+#pragma unroll
+  for (int q = 0; q < 2; q++) {
+    if (lane + 64 * q < chunks) {
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        const float d = v[8 * q + e] - mean;
+        sq += d * d;
+      }
+    }
+  }
+  for (int off = 32; off > 0; off >>= 1) sq += __shfl_xor(sq, off);
+  const float inv = 1.0f / sqrtf(sq / (float)c + 1e-5f);
+#pragma unroll
+  for (int q = 0; q < 2; q++) {
+    const int k = lane + 64 * q;
+    if (k < chunks) {
+      float o[8];
+#pragma unroll
+      for (int e = 0; e < 8; e++)
+        o[e] = (v[8 * q + e] - mean) * inv * gamma[8 * k + e] + beta[8 * k + e];
+      *(u32x4 *)(dst + 8 * k) = pack8(o);
+    }
+  }
+}
+
+// Attention of one window and head per workgroup; wave q computes queries
+// 32 q .. 32 q + 31 of the window (NP: the tokens rounded up to 32).
+//  - S^T = K Q^T on v_mfma_f32_32x32x16_f16 (A: keys x dims, B: dims x
+//    queries, both 16-byte loads of qkv rows), so lane l holds query l % 32
+//    and, in register r of key block b, key 32 b + 8 (r / 4) + 4 (l / 32) +
+//    r % 4: the softmax over keys is in-register plus one exchange with
+//    lane l ^ 32.
+//  - The probabilities (already divided by the sum) are the B operand of
+//    O^T = V^T P^T as they lie: for the 16 keys of step (b, s) lane half h
+//    holds keys 32 b + 16 s + 4 h + {0..3, 8..11}, and the A operand (V^T,
+//    staged in LDS as [dim][key]) reads the same keys for its dim.
+//  - Keys past N get -inf; V rows past N are zero in LDS.
+// Scores are (q . k) / sqrt(32) + bias, the reference's (q / sqrt(32)) . k
+// up to rounding (attention.rs:66-111).
+template <int NP>
+__global__ __launch_bounds__(NP * 2) void k_window_attention(WinGeo g, const uint16_t *__restrict__ qkv,
+                                                             int c, int heads,
+                                                             const float *__restrict__ tables,
+                                                             uint16_t *__restrict__ out) {
+  constexpr int KB = NP / 32;
+  constexpr int PITCH = NP + 4;  // halves: 32 dims' rows on distinct banks
+  __shared__ __attribute__((aligned(16))) uint16_t vt[32 * PITCH];
+  const long w = blockIdx.x / heads;
+  const int head = (int)(blockIdx.x - w * heads);
+  const int n = g.n;
+  const long row3 = 3L * c;
+  const uint16_t *base = qkv + w * n * row3;
+
+  // V^T: item (key j, 8-dim chunk q).
+  for (int it = threadIdx.x; it < NP * 4; it += NP * 2) {
+    const int j = it >> 2, q = it & 3;
+    // Unconditional load from a row inside the window, zero past N.
+    u32x4 raw = *(const u32x4 *)(base + min(j, n - 1) * row3 + 2 * c + head * 32 + 8 * q);
+    if (j >= n) raw = u32x4{0u, 0u, 0u, 0u};
+    uint16_t h[8];
+    __builtin_memcpy(h, &raw, 16);
+#pragma unroll
+    for (int e = 0; e < 8; e++) vt[(8 * q + e) * PITCH + j] = h[e];
+  }
+
+  const int lane = threadIdx.x & 63, hf = lane >> 5, l32 = lane & 31;
+  const int qi = (threadIdx.x >> 6) * 32 + l32;
+  const int qc = qi < n ? qi : n - 1;
+  const half8 q0 = *(const half8 *)(base + qc * row3 + head * 32 + 8 * hf);
+  const half8 q1 = *(const half8 *)(base + qc * row3 + head * 32 + 16 + 8 * hf);
+  floatx16 st[KB];
+#pragma unroll
+  for (int b = 0; b < KB; b++) {
+    const int kj = min(32 * b + l32, n - 1);
+    const half8 k0 = *(const half8 *)(base + kj * row3 + c + head * 32 + 8 * hf);
+    const half8 k1 = *(const half8 *)(base + kj * row3 + c + head * 32 + 16 + 8 * hf);
+    floatx16 z = {};
+    z = __builtin_amdgcn_mfma_f32_32x32x16_f16(k0, q0, z, 0, 0, 0);
+    st[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(k1, q1, z, 0, 0, 0);
+  }
+
+  const float scale = 0.17677669529663688f;  // 1 / sqrt(32)
+  const int cls = win_class(g, w);
+  const float *tb = tables + ((long)(cls * heads + head) * n + qc) * n;
+  float mx = -__builtin_inff();
+#pragma unroll
+  for (int b = 0; b < KB; b++)
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      const int j = 32 * b + 8 * (r >> 2) + 4 * hf + (r & 3);
+      const float bj = tb[min(j, n - 1)];  // in bounds for every j
+      const float s = j < n ? st[b][r] * scale + bj : -__builtin_inff();
+      st[b][r] = s;
+      mx = fmaxf(mx, s);
+    }
+  mx = fmaxf(mx, __shfl_xor(mx, 32));
+  float sum = 0.0f;
+#pragma unroll
+  for (int b = 0; b < KB; b++)
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      const float p = __expf(st[b][r] - mx);
+      st[b][r] = p;
+      sum += p;
+    }
+  sum += __shfl_xor(sum, 32);
+  const float inv = 1.0f / sum;
+
+  __syncthreads();  // V^T staged
+  floatx16 ot = {};
+#pragma unroll
+  for (int b = 0; b < KB; b++)
+#pragma unroll
+    for (int s = 0; s < 2; s++) {
+      half8 pb;
+#pragma unroll
+      for (int e = 0; e < 8; e++) pb[e] = (_Float16)(st[b][8 * s + e] * inv);
+      const int kb0 = 32 * b + 16 * s + 4 * hf;
+      const uint2 lo = *(const uint2 *)(vt + l32 * PITCH + kb0);
+      const uint2 hi = *(const uint2 *)(vt + l32 * PITCH + kb0 + 8);
+      u32x4 raw = {lo.x, lo.y, hi.x, hi.y};
+      half8 va;
+      __builtin_memcpy(&va, &raw, 16);
+      ot = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb, ot, 0, 0, 0);
+    }
+  if (qi < n) {
+    uint16_t *o = out + (w * n + qi) * (long)c + head * 32 + 4 * hf;
+#pragma unroll
+    for (int gq = 0; gq < 4; gq++) {
+      uint16_t h[4];
+#pragma unroll
+      for (int e = 0; e < 4; e++) h[e] = f2h(ot[4 * gq + e]);
+      uint2 v;
+      __builtin_memcpy(&v, h, 8);
+      *(uint2 *)(o + 8 * gq) = v;
+    }
+  }
+}
+
+// One thread per 8-channel chunk of a window row: map[source] += row.
+__global__ __launch_bounds__(256) void k_window_scatter_add(WinGeo g, const uint16_t *__restrict__ rows,
+                                                            int c, uint16_t *__restrict__ map,
+                                                            long stride) {
+  const int chunks = c >> 3;
+  const long item = (long)blockIdx.x * 256 + threadIdx.x;
+  if (item >= g.windows * g.n * chunks) return;
+  const long row = item / chunks;
+  const int k = (int)(item - row * chunks);
+  const long src = win_source(g, row / g.n, (int)(row % g.n));
+  if (src < 0) return;
+  float a[8], b[8];
+  unpack8(*(const u32x4 *)(rows + row * c + 8 * k), a);
+  uint16_t *m = map + src * stride + 8 * k;
+  unpack8(*(const u32x4 *)m, b);
+#pragma unroll
+  for (int e = 0; e < 8; e++) b[e] += a[e];
+  *(u32x4 *)m = pack8(b);
+}
+
+ien_status geometry(const ien_windows *w, WinGeo *g) {
+  IEN_CHECK(w, IEN_ERR_INPUT, "null windows");
+  IEN_CHECK(w->window >= 1 && w->window * w->window <= 256, IEN_ERR_INPUT,
+            "window %d (at most 16 x 16 tokens)", w->window);
+  IEN_CHECK(w->shift >= 0 && w->shift < w->window, IEN_ERR_INPUT, "shift %d of window %d",
+            w->shift, w->window);
+  IEN_CHECK(w->height >= 1 && w->width >= 1, IEN_ERR_INPUT, "map %d x %d", w->height, w->width);
+  g->window = w->window;
+  g->shift = w->shift;
+  g->height = w->height;
+  g->width = w->width;
+  g->ph = (w->height + w->window - 1) / w->window * w->window;
+  g->pw = (w->width + w->window - 1) / w->window * w->window;
+  g->wx = g->pw / w->window;
+  g->n = w->window * w->window;
+  g->windows = (long)(g->ph / w->window) * g->wx;
+  return IEN_OK;
+}
+
+bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
+
+}  // namespace
+}  // namespace ien
+
+using namespace ien;
+
+extern "C" {
+
+long ien_window_count(const ien_windows *w) {
+  WinGeo g;
+  if (geometry(w, &g) != IEN_OK) return -1;
+  return g.windows;
+}
+
+ien_status ien_position_bias(const float *table, int heads, int window,
+                             ien_position_layout layout, float *out) {
+  IEN_CHECK(table && out, IEN_ERR_INPUT, "null argument");
+  IEN_CHECK(heads >= 1 && window >= 1 && window <= 16, IEN_ERR_INPUT, "%d heads, window %d", heads,
+            window);
+  IEN_CHECK(layout == IEN_POS_SCUNET || layout == IEN_POS_SWIN, IEN_ERR_INPUT, "layout %d",
+            (int)layout);
+  const int n = window * window, side = 2 * window - 1;
+  for (int h = 0; h < heads; h++)
+    for (int i = 0; i < n; i++)
+      for (int j = 0; j < n; j++) {
+        // Offsets (yi - yj, xi - xj), each shifted into 0 .. 2W - 2.
+        const int cell = (i / window - j / window + window - 1) * side +
+                         (i % window - j % window + window - 1);
+        out[((size_t)h * n + i) * n + j] =
+            layout == IEN_POS_SCUNET ? table[(size_t)h * side * side + cell]
+                                     : table[(size_t)cell * heads + h];
+      }
+  return IEN_OK;
+}
+
+int ien_bias_tables(const float *position, int heads, int window, int shift, float masked,
+                    float *out) {
+  if (!position || !out || heads < 1 || window < 1 || window > 16 || shift < 0 ||
+      shift >= window) {
+    set_error("input: bias tables of %d heads, window %d, shift %d", heads, window, shift);
+    return -1;
+  }
+  const size_t n = (size_t)window * window, per = (size_t)heads * n * n;
+  if (shift == 0) {
+    std::memcpy(out, position, sizeof(float) * per);
+    return 1;
+  }
+  for (int cls = 0; cls < 4; cls++) {
+    // Region of a token in a window of this class: its row (last-column
+    // class: column) in the part the roll brought from the far side.
+    auto region = [&](size_t t) {
+      const bool row = (cls & 2) && (int)(t / window) >= window - shift;
+      const bool col = (cls & 1) && (int)(t % window) >= window - shift;
+      return 2 * (int)row + (int)col;
+    };
+    for (int h = 0; h < heads; h++)
+      for (size_t i = 0; i < n; i++)
+        for (size_t j = 0; j < n; j++) {
+          const size_t at = ((size_t)h * n + i) * n + j;
+          out[cls * per + at] = position[at] + (region(i) == region(j) ? 0.0f : masked);
+        }
+  }
+  return 4;
+}
+
+ien_status ien_window_gather(ien_ctx *ctx, const ien_windows *w, const uint16_t *d_map,
+                             size_t stride, int c, const float *d_gamma, const float *d_beta,
+                             uint16_t *d_tokens) {
+  IEN_CHECK(ctx && d_map && d_gamma && d_beta && d_tokens, IEN_ERR_INPUT, "null argument");
+  WinGeo g;
+  ien_status st = geometry(w, &g);
+  if (st != IEN_OK) return st;
+  IEN_CHECK(c >= 8 && c <= 1024 && c % 8 == 0, IEN_ERR_INPUT, "%d channels (8 .. 1024, by 8)", c);
+  IEN_CHECK(stride >= (size_t)c && stride % 8 == 0 && aligned16(d_map) && aligned16(d_tokens),
+            IEN_ERR_INPUT, "map stride %zu / alignment (16-byte rows)", stride);
+  const long rows = g.windows * g.n;
+  hipLaunchKernelGGL(k_window_gather, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, ctx->stream,
+                     g, d_map, (long)stride, c, d_gamma, d_beta, d_tokens);
+  IEN_HIP(hipGetLastError());
+  return IEN_OK;
+}
+
+ien_status ien_window_attention(ien_ctx *ctx, const ien_windows *w, const uint16_t *d_qkv, int c,
+                                const float *d_tables, uint16_t *d_out) {
+  IEN_CHECK(ctx && d_qkv && d_tables && d_out, IEN_ERR_INPUT, "null argument");
+  WinGeo g;
+  ien_status st = geometry(w, &g);
+  if (st != IEN_OK) return st;
+  IEN_CHECK(c >= 32 && c % 32 == 0, IEN_ERR_INPUT, "%d channels (heads of 32)", c);
+  IEN_CHECK(aligned16(d_qkv) && ((uintptr_t)d_out & 7) == 0, IEN_ERR_INPUT, "alignment");
+  const int heads = c / 32;
+  const long blocks = g.windows * heads;
+  IEN_CHECK(blocks < (1L << 31), IEN_ERR_INPUT, "%ld windows x heads", blocks);
+  const int np = (g.n + 31) / 32 * 32;
+  void (*k)(WinGeo, const uint16_t *, int, int, const float *, uint16_t *) = nullptr;
+  switch (np) {
+    case 32: k = k_window_attention<32>; break;
+    case 64: k = k_window_attention<64>; break;
+    case 96: k = k_window_attention<96>; break;
+    case 128: k = k_window_attention<128>; break;
+    case 160: k = k_window_attention<160>; break;
+    case 192: k = k_window_attention<192>; break;
+    case 224: k = k_window_attention<224>; break;
+    default: k = k_window_attention<256>; break;
+  }
+  hipLaunchKernelGGL(k, dim3((unsigned)blocks), dim3(np * 2), 0, ctx->stream, g, d_qkv, c, heads,
+                     d_tables, d_out);
+  IEN_HIP(hipGetLastError());
+  return IEN_OK;
+}
+
+ien_status ien_window_scatter_add(ien_ctx *ctx, const ien_windows *w, const uint16_t *d_rows,
+                                  int c, uint16_t *d_map, size_t stride) {
+  IEN_CHECK(ctx && d_rows && d_map, IEN_ERR_INPUT, "null argument");
+  WinGeo g;
+  ien_status st = geometry(w, &g);
+  if (st != IEN_OK) return st;
+  IEN_CHECK(c >= 8 && c % 8 == 0, IEN_ERR_INPUT, "%d channels (by 8)", c);
+  IEN_CHECK(stride >= (size_t)c && stride % 8 == 0 && aligned16(d_map) && aligned16(d_rows),
+            IEN_ERR_INPUT, "map stride %zu / alignment (16-byte rows)", stride);
+  const long items = g.windows * g.n * (c / 8);
+  hipLaunchKernelGGL(k_window_scatter_add, dim3((unsigned)((items + 255) / 256)), dim3(256), 0,
+                     ctx->stream, g, d_rows, c, d_map, (long)stride);
+  IEN_HIP(hipGetLastError());
+  return IEN_OK;
+}
+
+}  // extern "C"

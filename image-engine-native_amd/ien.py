@@ -32,7 +32,18 @@ EXPORTS = (
     "ien_layer_norm", "ien_gelu", "ien_sigmoid", "ien_pixel_shuffle_add", "ien_depthwise",
     "ien_model_load", "ien_model_from_tensors", "ien_model_free", "ien_model_run",
     "ien_model_run_device", "ien_model_set_graph",
+    "ien_window_count", "ien_position_bias", "ien_bias_tables", "ien_window_gather",
+    "ien_window_attention", "ien_window_scatter_add",
 )
+
+
+class Windows(ctypes.Structure):
+    """ien_windows: a Swin block's windows over a height x width token map."""
+    _fields_ = [("window", ctypes.c_int), ("shift", ctypes.c_int), ("height", ctypes.c_int),
+                ("width", ctypes.c_int)]
+
+
+POS_SCUNET, POS_SWIN = 0, 1
 
 
 class IenError(RuntimeError):
@@ -124,6 +135,15 @@ def load():
         L.ien_model_run.argtypes = [vp, vp, vp, sz, sz, vp, vp, vp]
         L.ien_model_run_device.argtypes = [vp, vp, vp, sz, sz, vp]
         L.ien_model_set_graph.argtypes = [vp, i]
+        wp = ctypes.POINTER(Windows)
+        L.ien_window_count.argtypes = [wp]
+        L.ien_window_count.restype = ctypes.c_long
+        L.ien_position_bias.argtypes = [vp, i, i, i, vp]
+        L.ien_bias_tables.argtypes = [vp, i, i, i, ctypes.c_float, vp]
+        L.ien_bias_tables.restype = i
+        L.ien_window_gather.argtypes = [vp, wp, vp, sz, i, vp, vp, vp]
+        L.ien_window_attention.argtypes = [vp, wp, vp, i, vp, vp]
+        L.ien_window_scatter_add.argtypes = [vp, wp, vp, i, vp, sz]
         for name in EXPORTS:
             getattr(L, name)
         _lib = L
@@ -278,6 +298,57 @@ def pixel_shuffle_add(ctx, last, last_stride, image, width, height, out):
 def depthwise(ctx, x, height, width, channels, layout, w, size, bias, y):
     check(load().ien_depthwise(ctx.h, _ptr(x), height, width, channels, layout, _ptr(w), size, _ptr(bias),
                                _ptr(y)))
+
+
+def windows(window, shift, height, width):
+    return Windows(window, shift, height, width)
+
+
+def window_count(w):
+    n = load().ien_window_count(ctypes.byref(w))
+    if n < 0:
+        check(ERR_INPUT)
+    return n
+
+
+def _np_ptr(a):
+    return ctypes.c_void_p(a.ctypes.data)
+
+
+def position_bias(table, heads, window, layout):
+    """[heads, N, N] from a SCUNet [heads, 2W-1, 2W-1] or Swin [(2W-1)^2, heads] table (host)."""
+    import numpy as np
+
+    table = np.ascontiguousarray(table, dtype=np.float32)
+    out = np.zeros((heads, window * window, window * window), np.float32)
+    check(load().ien_position_bias(_np_ptr(table), heads, window, layout, _np_ptr(out)))
+    return out
+
+
+def bias_tables(position, window, shift, masked):
+    """[classes, heads, N, N] (host): swin.rs bias_tables."""
+    import numpy as np
+
+    position = np.ascontiguousarray(position, dtype=np.float32)
+    heads, n = position.shape[0], window * window
+    out = np.zeros((4, heads, n, n), np.float32)
+    k = load().ien_bias_tables(_np_ptr(position), heads, window, shift, masked, _np_ptr(out))
+    if k < 0:
+        check(ERR_INPUT)
+    return out[:k]
+
+
+def window_gather(ctx, w, map_, stride, c, gamma, beta, tokens):
+    check(load().ien_window_gather(ctx.h, ctypes.byref(w), _ptr(map_), stride, c, _ptr(gamma), _ptr(beta),
+                                   _ptr(tokens)))
+
+
+def window_attention(ctx, w, qkv, c, tables, out):
+    check(load().ien_window_attention(ctx.h, ctypes.byref(w), _ptr(qkv), c, _ptr(tables), _ptr(out)))
+
+
+def window_scatter_add(ctx, w, rows, c, map_, stride):
+    check(load().ien_window_scatter_add(ctx.h, ctypes.byref(w), _ptr(rows), c, _ptr(map_), stride))
 
 
 class Model:

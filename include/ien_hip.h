@@ -179,6 +179,63 @@ ien_status ien_depthwise(ien_ctx *ctx, const uint16_t *d_x, size_t height, size_
                          size_t channels, ien_layout layout, const float *d_w, size_t size,
                          const float *d_bias, uint16_t *d_y);
 
+/* ---- Swin window attention: scunet-native/src/swin.rs,
+ *      birefnet-native/src/swin.rs, native-engine attention.rs ---------- */
+
+/* The windows of a Swin block over a height x width map of tokens: window x
+ * window tokens each (N = window^2 <= 256), over the map padded to whole
+ * windows and rolled by `shift` (0 for W-MSA, window / 2 for SW-MSA; SCUNet
+ * swin.rs:153-158, BiRefNet swin.rs:240-247).  Window w covers rows
+ * w / ceil(width / window) and columns w % ceil(width / window). */
+typedef struct {
+  int window;
+  int shift;
+  int height, width;
+} ien_windows;
+
+/* ceil(height / window) * ceil(width / window), or -1 if `w` is invalid. */
+long ien_window_count(const ien_windows *w);
+
+/* Relative-position bias [heads][N][N] of a window from its learned table
+ * (host memory): IEN_POS_SCUNET [heads][2W-1][2W-1] as
+ * tools/scunet/export_weights.py:61-67 gathers it, IEN_POS_SWIN
+ * [(2W-1)^2][heads] indexed (dy + W - 1)(2W - 1) + (dx + W - 1). */
+typedef enum { IEN_POS_SCUNET = 0, IEN_POS_SWIN = 1 } ien_position_layout;
+ien_status ien_position_bias(const float *table, int heads, int window,
+                             ien_position_layout layout, float *out);
+
+/* swin.rs bias_tables (scunet :26-50, birefnet :31-51), host memory: out
+ * receives [classes][heads][N][N]: the bias itself when shift is 0 (1
+ * class), else 4 classes (1: window last in its row, 2: last in its column)
+ * with `masked` (-inf for SCUNet, -100 for BiRefNet) between tokens of
+ * different regions.  Returns the class count, or -1. */
+int ien_bias_tables(const float *position, int heads, int window, int shift, float masked,
+                    float *out);
+
+/* The gather of swin.rs attend (scunet :147-161, birefnet :238-254): token
+ * rows [windows * N][c] (f16) from the map (f16, token t at d_map + t *
+ * stride), each LayerNorm'd with gamma, beta (device f32, eps 1e-5,
+ * math.rs:95-116); rows past the map's edge are zero (the padding follows
+ * the normalisation).  c a multiple of 8, at most 1024. */
+ien_status ien_window_gather(ien_ctx *ctx, const ien_windows *w, const uint16_t *d_map,
+                             size_t stride, int c, const float *d_gamma, const float *d_beta,
+                             uint16_t *d_tokens);
+
+/* attention.rs:25-111 attention for every window and head at once: qkv
+ * rows [windows * N][3c] (f16; queries, keys, values), tables the device
+ * copy (f32) of ien_bias_tables' output for the block, window w using
+ * class (shift ? [last column] + 2 [last row] : 0) as swin.rs:171-176
+ * picks it; out rows [windows * N][c] (f16).  c a multiple of 32 (heads of
+ * 32 channels), N <= 256. */
+ien_status ien_window_attention(ien_ctx *ctx, const ien_windows *w, const uint16_t *d_qkv, int c,
+                                const float *d_tables, uint16_t *d_out);
+
+/* The residual of swin.rs attend (scunet :218-230, birefnet :291-303): each
+ * window row is added onto its source token of the map (f16; rows past the
+ * edge are dropped).  c a multiple of 8. */
+ien_status ien_window_scatter_add(ien_ctx *ctx, const ien_windows *w, const uint16_t *d_rows,
+                                  int c, uint16_t *d_map, size_t stride);
+
 /* ---- models: crates/<model>-native/src/lib.rs Model ------------------- */
 typedef enum { IEN_MODEL_REALESRGAN = 0 } ien_model_kind;
 
