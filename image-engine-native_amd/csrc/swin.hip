@@ -1,0 +1,160 @@
+// swin.hip -- the Swin transformer block (crates/scunet-native/src/swin.rs
+// Transformer, crates/birefnet-native/src/swin.rs Block) composed from the
+// window ops and the row products on the context's stream.
+
+#include <cmath>
+#include <cstring>
+
+#include "ien_internal.h"
+
+struct ien_swin {
+  ien_ctx *ctx = nullptr;
+  int c = 0, window = 0, shift = 0, heads = 0, classes = 0;
+  float *d_ln = nullptr;  // ln1 gamma, beta, ln2 gamma, beta (4 c floats)
+  float *d_tables = nullptr;
+  ien_matrix *qkv = nullptr, *proj = nullptr, *fc1 = nullptr, *fc2 = nullptr;
+  // Scratch: `rows` window rows (at least the map's tokens) of 4c, c, c.
+  uint16_t *d_wide = nullptr, *d_tok = nullptr, *d_att = nullptr;
+  size_t rows = 0;
+};
+
+namespace {
+
+void release(ien_swin *b) {
+  if (!b) return;
+  ien_matrix_free(b->qkv);
+  ien_matrix_free(b->proj);
+  ien_matrix_free(b->fc1);
+  ien_matrix_free(b->fc2);
+  (void)hipFree(b->d_ln);
+  (void)hipFree(b->d_tables);
+  (void)hipFree(b->d_wide);
+  (void)hipFree(b->d_tok);
+  (void)hipFree(b->d_att);
+  delete b;
+}
+
+// Grow the scratch to `rows` rows (the stream drains first: kernels may
+// still use the old buffers).
+ien_status reserve(ien_swin *b, size_t rows) {
+  if (rows <= b->rows) return IEN_OK;
+  IEN_HIP(hipStreamSynchronize(b->ctx->stream));
+  (void)hipFree(b->d_wide);
+  (void)hipFree(b->d_tok);
+  (void)hipFree(b->d_att);
+  b->d_wide = b->d_tok = b->d_att = nullptr;
+  b->rows = 0;
+  const size_t c = (size_t)b->c;
+  IEN_HIP(hipMalloc((void **)&b->d_wide, rows * 4 * c * 2));
+  IEN_HIP(hipMalloc((void **)&b->d_tok, rows * c * 2));
+  IEN_HIP(hipMalloc((void **)&b->d_att, rows * c * 2));
+  b->rows = rows;
+  return IEN_OK;
+}
+
+ien_status rows_product(ien_ctx *ctx, const uint16_t *in, size_t k, size_t rows,
+                        const ien_matrix *m, uint16_t *out, size_t stride, ien_act act,
+                        int accumulate) {
+  ien_input x{};
+  x.kind = IEN_INPUT_ROWS;
+  x.data = in;
+  x.stride = k;
+  ien_output o{};
+  o.data = out;
+  o.stride = stride;
+  o.layout = IEN_LAYOUT_NHWC;
+  o.type = IEN_OUT_F16;
+  return ien_multiply_ex(ctx, &x, 0, rows, m, &o, act, nullptr, accumulate);
+}
+
+}  // namespace
+
+using namespace ien;
+
+extern "C" {
+
+ien_status ien_swin_new(ien_ctx *ctx, const ien_swin_weights *w, ien_swin **out) {
+  IEN_CHECK(ctx && w && out, IEN_ERR_INPUT, "null argument");
+  *out = nullptr;
+  const ien_swin_weights &W = *w;
+  IEN_CHECK(W.c >= 32 && W.c % 32 == 0 && W.c <= 1024, IEN_ERR_INPUT,
+            "%d channels (heads of 32, at most 1024)", W.c);
+  IEN_CHECK(W.window >= 1 && W.window <= 16 && W.shift >= 0 && W.shift < W.window,
+            IEN_ERR_INPUT, "window %d, shift %d", W.window, W.shift);
+  IEN_CHECK(W.ln1_gamma && W.ln1_beta && W.qkv_w && W.qkv_b && W.position && W.proj_w &&
+                W.proj_b && W.ln2_gamma && W.ln2_beta && W.fc1_w && W.fc1_b && W.fc2_w && W.fc2_b,
+            IEN_ERR_INPUT, "missing weights");
+  ien_swin *b = new ien_swin;
+  b->ctx = ctx;
+  b->c = W.c;
+  b->window = W.window;
+  b->shift = W.shift;
+  b->heads = W.c / 32;
+  const size_t c = (size_t)W.c, n = (size_t)W.window * W.window;
+  auto fail_with = [&](ien_status st) {
+    release(b);
+    return st;
+  };
+  std::vector<float> tables(4 * (size_t)b->heads * n * n);
+  b->classes = ien_bias_tables(W.position, b->heads, W.window, W.shift, W.masked, tables.data());
+  if (b->classes < 0) return fail_with(IEN_ERR_INPUT);
+  const size_t tbytes = (size_t)b->classes * b->heads * n * n * sizeof(float);
+  std::vector<float> ln(4 * c);
+  std::memcpy(ln.data(), W.ln1_gamma, c * 4);
+  std::memcpy(ln.data() + c, W.ln1_beta, c * 4);
+  std::memcpy(ln.data() + 2 * c, W.ln2_gamma, c * 4);
+  std::memcpy(ln.data() + 3 * c, W.ln2_beta, c * 4);
+  hipError_t e = hipMalloc((void **)&b->d_ln, 4 * c * 4);
+  if (e == hipSuccess) e = hipMalloc((void **)&b->d_tables, tbytes);
+  if (e == hipSuccess) e = hipMemcpy(b->d_ln, ln.data(), 4 * c * 4, hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = hipMemcpy(b->d_tables, tables.data(), tbytes, hipMemcpyHostToDevice);
+  if (e != hipSuccess) {
+    release(b);
+    return fail(IEN_ERR_GPU, "swin upload: %s", hipGetErrorString(e));
+  }
+  ien_status st = ien_matrix_new(ctx, W.qkv_w, IEN_W_F32, c, 3 * c, W.qkv_b, &b->qkv);
+  if (st == IEN_OK) st = ien_matrix_new(ctx, W.proj_w, IEN_W_F32, c, c, W.proj_b, &b->proj);
+  if (st == IEN_OK) st = ien_matrix_new(ctx, W.fc1_w, IEN_W_F32, c, 4 * c, W.fc1_b, &b->fc1);
+  if (st == IEN_OK) st = ien_matrix_new(ctx, W.fc2_w, IEN_W_F32, 4 * c, c, W.fc2_b, &b->fc2);
+  if (st != IEN_OK) return fail_with(st);
+  *out = b;
+  return IEN_OK;
+}
+
+void ien_swin_free(ien_swin *block) { release(block); }
+
+ien_status ien_swin_run(ien_swin *b, uint16_t *d_map, size_t stride, int height, int width) {
+  IEN_CHECK(b && d_map, IEN_ERR_INPUT, "null argument");
+  ien_ctx *ctx = b->ctx;
+  const size_t c = (size_t)b->c;
+  ien_windows w{b->window, b->shift, height, width};
+  const long wins = ien_window_count(&w);
+  IEN_CHECK(wins > 0, IEN_ERR_INPUT, "map %d x %d", height, width);
+  const size_t rows = (size_t)wins * b->window * b->window;
+  const size_t tokens = (size_t)height * width;
+  ien_status st = reserve(b, rows > tokens ? rows : tokens);
+  if (st != IEN_OK) return st;
+  const float *g1 = b->d_ln, *b1 = b->d_ln + c, *g2 = b->d_ln + 2 * c, *b2 = b->d_ln + 3 * c;
+  // attend (scunet swin.rs:131-232): the window rows, qkv, attention,
+  // projection over the token rows, added back onto the map.
+  if ((st = ien_window_gather(ctx, &w, d_map, stride, b->c, g1, b1, b->d_tok)) != IEN_OK) return st;
+  if ((st = rows_product(ctx, b->d_tok, c, rows, b->qkv, b->d_wide, 3 * c, IEN_ACT_NONE, 0)) !=
+      IEN_OK)
+    return st;
+  if ((st = ien_window_attention(ctx, &w, b->d_wide, b->c, b->d_tables, b->d_att)) != IEN_OK)
+    return st;
+  if ((st = rows_product(ctx, b->d_att, c, rows, b->proj, b->d_tok, c, IEN_ACT_NONE, 0)) != IEN_OK)
+    return st;
+  if ((st = ien_window_scatter_add(ctx, &w, b->d_tok, b->c, d_map, stride)) != IEN_OK) return st;
+  // mlp (scunet swin.rs:236-275): every token normalised (a 1 x 1 window
+  // gather is the copy with its LayerNorm), fc1 + GELU, fc2 added back.
+  ien_windows one{1, 0, height, width};
+  if ((st = ien_window_gather(ctx, &one, d_map, stride, b->c, g2, b2, b->d_tok)) != IEN_OK)
+    return st;
+  if ((st = rows_product(ctx, b->d_tok, c, tokens, b->fc1, b->d_wide, 4 * c, IEN_ACT_GELU, 0)) !=
+      IEN_OK)
+    return st;
+  return rows_product(ctx, b->d_wide, 4 * c, tokens, b->fc2, d_map, stride, IEN_ACT_NONE, 1);
+}
+
+}  // extern "C"

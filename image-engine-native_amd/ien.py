@@ -33,7 +33,7 @@ EXPORTS = (
     "ien_model_load", "ien_model_from_tensors", "ien_model_free", "ien_model_run",
     "ien_model_run_device", "ien_model_set_graph",
     "ien_window_count", "ien_position_bias", "ien_bias_tables", "ien_window_gather",
-    "ien_window_attention", "ien_window_scatter_add",
+    "ien_window_attention", "ien_window_scatter_add", "ien_swin_new", "ien_swin_free", "ien_swin_run",
 )
 
 
@@ -44,6 +44,15 @@ class Windows(ctypes.Structure):
 
 
 POS_SCUNET, POS_SWIN = 0, 1
+
+
+class SwinWeights(ctypes.Structure):
+    """ien_swin_weights (host f32 pointers)."""
+    _fields_ = [("c", ctypes.c_int), ("window", ctypes.c_int), ("shift", ctypes.c_int),
+                ("masked", ctypes.c_float)] + [
+        (name, ctypes.c_void_p) for name in (
+            "ln1_gamma", "ln1_beta", "qkv_w", "qkv_b", "position", "proj_w", "proj_b", "ln2_gamma",
+            "ln2_beta", "fc1_w", "fc1_b", "fc2_w", "fc2_b")]
 
 
 class IenError(RuntimeError):
@@ -144,6 +153,10 @@ def load():
         L.ien_window_gather.argtypes = [vp, wp, vp, sz, i, vp, vp, vp]
         L.ien_window_attention.argtypes = [vp, wp, vp, i, vp, vp]
         L.ien_window_scatter_add.argtypes = [vp, wp, vp, i, vp, sz]
+        L.ien_swin_new.argtypes = [vp, ctypes.POINTER(SwinWeights), ctypes.POINTER(vp)]
+        L.ien_swin_free.argtypes = [vp]
+        L.ien_swin_free.restype = None
+        L.ien_swin_run.argtypes = [vp, vp, sz, i, i]
         for name in EXPORTS:
             getattr(L, name)
         _lib = L
@@ -349,6 +362,38 @@ def window_attention(ctx, w, qkv, c, tables, out):
 
 def window_scatter_add(ctx, w, rows, c, map_, stride):
     check(load().ien_window_scatter_add(ctx.h, ctypes.byref(w), _ptr(rows), c, _ptr(map_), stride))
+
+
+class Swin:
+    """ien_swin: one Swin transformer block (attend then MLP, in place).
+    `weights`: dict of host arrays ln1_gamma, ln1_beta, qkv_w (c x 3c),
+    qkv_b, position ([heads, N, N]), proj_w, proj_b, ln2_gamma, ln2_beta,
+    fc1_w (c x 4c), fc1_b, fc2_w (4c x c), fc2_b."""
+
+    def __init__(self, ctx, c, window, shift, masked, weights):
+        import numpy as np
+
+        keep = {k: np.ascontiguousarray(v, dtype=np.float32) for k, v in weights.items()}
+        sw = SwinWeights(c, window, shift, masked)
+        for name, _ in SwinWeights._fields_[4:]:
+            setattr(sw, name, keep[name].ctypes.data)
+        h = ctypes.c_void_p()
+        check(load().ien_swin_new(ctx.h, ctypes.byref(sw), ctypes.byref(h)))
+        self.h = h
+
+    def run(self, map_, stride, height, width):
+        check(load().ien_swin_run(self.h, _ptr(map_), stride, height, width))
+
+    def free(self):
+        if self.h:
+            load().ien_swin_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
 
 
 class Model:

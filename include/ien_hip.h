@@ -236,6 +236,34 @@ ien_status ien_window_attention(ien_ctx *ctx, const ien_windows *w, const uint16
 ien_status ien_window_scatter_add(ien_ctx *ctx, const ien_windows *w, const uint16_t *d_rows,
                                   int c, uint16_t *d_map, size_t stride);
 
+/* A Swin transformer block (scunet swin.rs:85-276 Transformer, birefnet
+ * swin.rs:87-347 Block): weights as host f32, row-major k x n matrices in
+ * the order the weights files hold them. */
+typedef struct {
+  int c;          /* channels: heads of 32 */
+  int window;     /* 8 (SCUNet), 7 or 12 (BiRefNet) */
+  int shift;      /* 0, or window / 2 for a shifted block */
+  float masked;   /* -inf (SCUNet) or -100 (BiRefNet) */
+  const float *ln1_gamma, *ln1_beta;  /* c */
+  const float *qkv_w, *qkv_b;         /* c x 3c, 3c */
+  const float *position;              /* [heads][N][N] relative-position bias */
+  const float *proj_w, *proj_b;       /* c x c, c */
+  const float *ln2_gamma, *ln2_beta;  /* c */
+  const float *fc1_w, *fc1_b;         /* c x 4c, 4c (GELU) */
+  const float *fc2_w, *fc2_b;         /* 4c x c, c */
+} ien_swin_weights;
+typedef struct ien_swin ien_swin;
+
+/* Transformer::load: upload the products, the norms and the class tables
+ * (ien_bias_tables) once. */
+ien_status ien_swin_new(ien_ctx *ctx, const ien_swin_weights *weights, ien_swin **out);
+void ien_swin_free(ien_swin *block);
+/* Transformer::attend then Transformer::mlp, in place on the height x width
+ * token map (f16, token t at d_map + t * stride): windows gathered, rolled
+ * and normalised, attention, projection added back; then LayerNorm, fc1 +
+ * GELU, fc2 added back.  Scratch is the block's own, grown on demand. */
+ien_status ien_swin_run(ien_swin *block, uint16_t *d_map, size_t stride, int height, int width);
+
 /* ---- models: crates/<model>-native/src/lib.rs Model ------------------- */
 typedef enum { IEN_MODEL_REALESRGAN = 0 } ien_model_kind;
 

@@ -1,0 +1,57 @@
+"""GPU parity of a whole Swin transformer block (ien_swin: scunet swin.rs
+Transformer::attend + mlp, birefnet swin.rs Block) against the oracle's
+or_swin_attend followed by or_swin_mlp, on f16-rounded maps; a second run
+on a larger map reuses the block (scratch grown on demand)."""
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+def block_weights(rng, c, window):
+    n, heads = window * window, c // 32
+    r = lambda *s, scale=1.0: (scale * rng.standard_normal(s)).astype(np.float32)
+    return dict(ln1_gamma=1 + r(c, scale=0.1), ln1_beta=r(c, scale=0.1),
+                qkv_w=r(c, 3 * c, scale=1 / np.sqrt(c)), qkv_b=r(3 * c, scale=0.1),
+                position=r(heads, n, n), proj_w=r(c, c, scale=1 / np.sqrt(c)), proj_b=r(c, scale=0.1),
+                ln2_gamma=1 + r(c, scale=0.1), ln2_beta=r(c, scale=0.1),
+                fc1_w=r(c, 4 * c, scale=1 / np.sqrt(c)), fc1_b=r(4 * c, scale=0.1),
+                fc2_w=r(4 * c, c, scale=0.5 / np.sqrt(4 * c)), fc2_b=r(c, scale=0.1))
+
+
+def oracle_block(oracle, x, window, shift, masked, wt):
+    tables = oracle.bias_tables(wt["position"], window, shift, masked)
+    y = oracle.swin_attend(x, window, shift, wt["ln1_gamma"], wt["ln1_beta"], wt["qkv_w"], wt["qkv_b"], tables,
+                           wt["proj_w"], wt["proj_b"])
+    return oracle.swin_mlp(y, wt["ln2_gamma"], wt["ln2_beta"], wt["fc1_w"], wt["fc1_b"], wt["fc2_w"], wt["fc2_b"])
+
+
+@pytest.mark.parametrize("c,window,shift,masked,sizes", [
+    (64, 8, 4, -np.inf, [(16, 24), (32, 40)]),    # SCUNet SW-MSA
+    (64, 8, 0, -np.inf, [(16, 16)]),              # SCUNet W-MSA
+    (96, 7, 3, -100.0, [(10, 10), (14, 21)]),     # the reference's BiRefNet window
+    (32, 12, 6, -100.0, [(15, 13), (24, 24)]),    # the configuration's BiRefNet window
+])
+def test_swin_block(ctx, oracle, c, window, shift, masked, sizes):
+    import torch
+    import ien
+
+    rng = np.random.default_rng(c + window)
+    wt = block_weights(rng, c, window)
+    blk = ien.Swin(ctx, c, window, shift, masked, wt)
+    for h, w in sizes:
+        x = rng.standard_normal((h, w, c)).astype(np.float16)
+        stride = c + 32
+        md = torch.zeros((h * w, stride), dtype=torch.float16, device="cuda")
+        md[:, :c] = torch.from_numpy(x.reshape(h * w, c)).cuda()
+        md[:, c:] = 3.0
+        blk.run(md, stride, h, w)
+        torch.cuda.synchronize()
+        got = md.float().cpu().numpy()
+        assert np.all(got[:, c:] == 3.0)  # channels past c untouched
+        want = oracle_block(oracle, x.astype(np.float32), window, shift, masked, wt)
+        err = np.abs(got[:, :c].reshape(h, w, c) - want)
+        assert err.max() < 5e-2, (h, w, err.max())
+        assert np.sqrt(np.mean(err ** 2)) < 6e-3, (h, w)
+    blk.free()
