@@ -34,6 +34,7 @@ EXPORTS = (
     "ien_model_run_device", "ien_model_set_graph",
     "ien_window_count", "ien_position_bias", "ien_bias_tables", "ien_window_gather",
     "ien_window_attention", "ien_window_scatter_add", "ien_swin_new", "ien_swin_free", "ien_swin_run",
+    "ien_resize", "ien_pad_image", "ien_crop",
 )
 
 
@@ -44,6 +45,7 @@ class Windows(ctypes.Structure):
 
 
 POS_SCUNET, POS_SWIN = 0, 1
+PAD_REPLICATE, PAD_SYMMETRIC_MASKED = 0, 1
 
 
 class SwinWeights(ctypes.Structure):
@@ -157,6 +159,9 @@ def load():
         L.ien_swin_free.argtypes = [vp]
         L.ien_swin_free.restype = None
         L.ien_swin_run.argtypes = [vp, vp, sz, i, i]
+        L.ien_resize.argtypes = [vp, vp, sz, sz, sz, sz, vp, sz, sz, sz, i, i]
+        L.ien_pad_image.argtypes = [vp, i, vp, vp, sz, sz, sz, vp, sz]
+        L.ien_crop.argtypes = [vp, vp, sz, sz, sz, sz, sz, vp]
         for name in EXPORTS:
             getattr(L, name)
         _lib = L
@@ -362,6 +367,20 @@ def window_attention(ctx, w, qkv, c, tables, out):
 
 def window_scatter_add(ctx, w, rows, c, map_, stride):
     check(load().ien_window_scatter_add(ctx.h, ctypes.byref(w), _ptr(rows), c, _ptr(map_), stride))
+
+
+def resize(ctx, src, sh, sw, src_stride, c, dst, dh, dw, dst_stride, out_f32=False, add=False):
+    check(load().ien_resize(ctx.h, _ptr(src), sh, sw, src_stride, c, _ptr(dst), dh, dw, dst_stride,
+                            OUT_F32 if out_f32 else OUT_F16, int(add)))
+
+
+def pad_image(ctx, mode, image, mask, width, height, multiple, out, stride):
+    check(load().ien_pad_image(ctx.h, mode, _ptr(image), _ptr(mask), width, height, multiple, _ptr(out),
+                               stride))
+
+
+def crop(ctx, map_, map_width, stride, width, height, channels, out):
+    check(load().ien_crop(ctx.h, _ptr(map_), map_width, stride, width, height, channels, _ptr(out)))
 
 
 class Swin:

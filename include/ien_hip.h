@@ -179,6 +179,35 @@ ien_status ien_depthwise(ien_ctx *ctx, const uint16_t *d_x, size_t height, size_
                          size_t channels, ien_layout layout, const float *d_w, size_t size,
                          const float *d_bias, uint16_t *d_y);
 
+/* ---- resampling and padding ------------------------------------------- */
+
+/* birefnet-native decoder.rs:436-522 resize: bilinear with aligned corners
+ * as ONNX Runtime computes it (source position out (in - 1) / (out - 1);
+ * when both taps are the same pixel, weights 0.5 and 0.5): the sh x sw map
+ * (f16 NHWC, `c` channels, pixel stride src_stride) into columns 0..c of
+ * the dh x dw map at d_dst (pixel stride dst_stride, f16 or f32 by
+ * out_type), added to what is there when `add`. */
+ien_status ien_resize(ien_ctx *ctx, const uint16_t *d_src, size_t sh, size_t sw, size_t src_stride,
+                      size_t c, void *d_dst, size_t dh, size_t dw, size_t dst_stride,
+                      ien_out_type out_type, int add);
+
+/* A model's input padded to whole multiples of `multiple` (device f32 RGB
+ * image, height x width x 3, in; f16 NHWC out with pixel stride `stride`):
+ * IEN_PAD_REPLICATE repeats the last row and column (scunet-native
+ * network.rs:356-379, 3 channels); IEN_PAD_SYMMETRIC_MASKED mirrors past the
+ * bottom and right edges (2n - 1 - i) and writes image * (1 - mask), then the
+ * mask (lama-native network.rs:336-370, 4 channels; d_mask height x width). */
+typedef enum { IEN_PAD_REPLICATE = 0, IEN_PAD_SYMMETRIC_MASKED = 1 } ien_pad_mode;
+ien_status ien_pad_image(ien_ctx *ctx, ien_pad_mode mode, const float *d_image,
+                         const float *d_mask, size_t width, size_t height, size_t multiple,
+                         uint16_t *d_out, size_t stride);
+
+/* The crop back (scunet-native network.rs:347-351): the top-left width x
+ * height pixels of an f16 NHWC map `map_width` pixels wide (pixel stride
+ * `stride`), `channels` values each, to f32 height x width x channels. */
+ien_status ien_crop(ien_ctx *ctx, const uint16_t *d_map, size_t map_width, size_t stride,
+                    size_t width, size_t height, size_t channels, float *d_out);
+
 /* ---- Swin window attention: scunet-native/src/swin.rs,
  *      birefnet-native/src/swin.rs, native-engine attention.rs ---------- */
 

@@ -141,3 +141,81 @@ void or_depthwise(int threads, const float *x, size_t height, size_t width,
   dw_job j = {x, w, bias, y, height, width, channels, size};
   or_parallel(threads, height * width, 1, 256, dw_task, &j);
 }
+
+/* birefnet-native decoder.rs:467-488 axis: source pixels and weights of
+ * output coordinate `out` for aligned corners, as ONNX Runtime computes
+ * them (i0 == i1: 0.5 and 0.5). */
+static void resize_axis(size_t out, size_t len_in, size_t len_out, size_t *i0, size_t *i1,
+                        float *d1, float *d2) {
+  float pos = len_out == 1 ? 0.0f : (float)out * (float)(len_in - 1) / (float)(len_out - 1);
+  if (pos < 0.0f) pos = 0.0f;
+  if (pos > (float)(len_in - 1)) pos = (float)(len_in - 1);
+  *i0 = (size_t)pos;
+  *i1 = *i0 + 1 < len_in ? *i0 + 1 : len_in - 1;
+  if (*i0 == *i1) {
+    *d1 = 0.5f;
+    *d2 = 0.5f;
+  } else {
+    *d1 = fabsf(pos - (float)*i0);
+    *d2 = fabsf(pos - (float)*i1);
+  }
+}
+
+/* decoder.rs:436-522 resize: the sh x sw x c map (NHWC) bilinearly to
+ * dh x dw, into columns 0..c of rows `stride` apart, added when `add`. */
+void or_resize(const float *src, size_t sh, size_t sw, size_t c, float *dst, size_t dh,
+               size_t dw, size_t stride, int add) {
+  for (size_t y = 0; y < dh; y++) {
+    size_t y1, y2;
+    float dy1, dy2;
+    resize_axis(y, sh, dh, &y1, &y2, &dy1, &dy2);
+    for (size_t x = 0; x < dw; x++) {
+      size_t x1, x2;
+      float dx1, dx2;
+      resize_axis(x, sw, dw, &x1, &x2, &dx1, &dx2);
+      const float *p11 = src + (y1 * sw + x1) * c, *p21 = src + (y1 * sw + x2) * c;
+      const float *p12 = src + (y2 * sw + x1) * c, *p22 = src + (y2 * sw + x2) * c;
+      float *d = dst + (y * dw + x) * stride;
+      for (size_t j = 0; j < c; j++) {
+        const float v = dx2 * dy2 * p11[j] + dx1 * dy2 * p21[j] + dx2 * dy1 * p12[j] +
+                        dx1 * dy1 * p22[j];
+        d[j] = add ? d[j] + v : v;
+      }
+    }
+  }
+}
+
+/* scunet-native network.rs:356-379 pad: the RGB image to the next multiples
+ * of `multiple`, the last row and column repeated; out ph x pw x 3. */
+void or_pad_replicate(const float *image, size_t width, size_t height, size_t multiple,
+                      float *out) {
+  const size_t ph = (height + multiple - 1) / multiple * multiple;
+  const size_t pw = (width + multiple - 1) / multiple * multiple;
+  for (size_t y = 0; y < ph; y++) {
+    const size_t sy = y < height ? y : height - 1;
+    for (size_t x = 0; x < pw; x++) {
+      const size_t sx = x < width ? x : width - 1;
+      for (size_t ch = 0; ch < 3; ch++) out[(y * pw + x) * 3 + ch] = image[(sy * width + sx) * 3 + ch];
+    }
+  }
+}
+
+/* lama-native network.rs:336-370 masked_rows: image * (1 - mask) and the
+ * mask, mirrored past the bottom and right edges (2n - 1 - i), padded to the
+ * next multiples of `multiple`; out ph x pw x 4. */
+void or_masked_rows(const float *image, const float *mask, size_t width, size_t height,
+                    size_t multiple, float *out) {
+  const size_t ph = (height + multiple - 1) / multiple * multiple;
+  const size_t pw = (width + multiple - 1) / multiple * multiple;
+  for (size_t y = 0; y < ph; y++) {
+    const size_t sy = y < height ? y : 2 * height - 1 - y;
+    for (size_t x = 0; x < pw; x++) {
+      const size_t sx = x < width ? x : 2 * width - 1 - x;
+      const size_t p = sy * width + sx;
+      const float m = mask[p];
+      float *o = out + (y * pw + x) * 4;
+      for (size_t ch = 0; ch < 3; ch++) o[ch] = image[p * 3 + ch] * (1.0f - m);
+      o[3] = m;
+    }
+  }
+}

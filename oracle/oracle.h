@@ -128,6 +128,19 @@ int or_realesrgan_run(int threads, const float *const *w,
 void or_pixel_shuffle_add(const float *last, const float *image, size_t width,
                           size_t height, float *out);
 
+/* ---- resize and padding helpers ---------------------------------------- */
+/* birefnet-native decoder.rs:436-522: bilinear, aligned corners, ONNX
+ * Runtime weights (i0 == i1: 0.5, 0.5); NHWC in, columns 0..c of rows
+ * `stride` apart out, added when `add`. */
+void or_resize(const float *src, size_t sh, size_t sw, size_t c, float *dst, size_t dh,
+               size_t dw, size_t stride, int add);
+/* scunet-native network.rs:356-379: replicate-pad RGB to multiples of `multiple`. */
+void or_pad_replicate(const float *image, size_t width, size_t height, size_t multiple,
+                      float *out);
+/* lama-native network.rs:336-370: symmetric pad of image * (1 - m) | m. */
+void or_masked_rows(const float *image, const float *mask, size_t width, size_t height,
+                    size_t multiple, float *out);
+
 /* ---- depthwise (no reference implementation) -------------------------- */
 /* y[p][c] = bias[c] + sum_{ky,kx} w[(ky*size+kx)][c] * x[p + tap][c], NHWC,
  * zero padding, stride 1: the 192 single-channel products of the reference

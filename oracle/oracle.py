@@ -87,6 +87,9 @@ def lib():
         L.or_realesrgan_run.argtypes = [ctypes.c_int, vp, vp, vp, vp, sz, sz, vp]
         L.or_pixel_shuffle_add.argtypes = [vp, vp, sz, sz, vp]
         L.or_depthwise.argtypes = [ctypes.c_int, vp, sz, sz, sz, vp, sz, vp, vp]
+        L.or_resize.argtypes = [vp, sz, sz, sz, vp, sz, sz, sz, ctypes.c_int]
+        L.or_pad_replicate.argtypes = [vp, sz, sz, sz, vp]
+        L.or_masked_rows.argtypes = [vp, vp, sz, sz, sz, vp]
         _lib = L
     return _lib
 
@@ -318,3 +321,31 @@ def depthwise(x, w, bias=None, threads=1):
     y = np.zeros_like(x)
     lib().or_depthwise(threads, _p(x), h, wd, c, _p(w), size, _p(bias), _p(y))
     return y
+
+
+# ---- resize and padding helpers -------------------------------------------
+def resize(src, dh, dw, out=None, add=False):
+    """src [sh, sw, c] -> [dh, dw, c] (into a copy of `out` when adding)."""
+    src = _f32(src)
+    sh, sw, c = src.shape
+    dst = np.zeros((dh, dw, c), np.float32) if out is None else _f32(out).copy()
+    lib().or_resize(_p(src), sh, sw, c, _p(dst), dh, dw, c, int(add))
+    return dst
+
+
+def pad_replicate(image, multiple):
+    image = _f32(image)
+    h, w, _ = image.shape
+    ph, pw = -(-h // multiple) * multiple, -(-w // multiple) * multiple
+    out = np.zeros((ph, pw, 3), np.float32)
+    lib().or_pad_replicate(_p(image), w, h, multiple, _p(out))
+    return out
+
+
+def masked_rows(image, mask, multiple):
+    image, mask = _f32(image), _f32(mask)
+    h, w, _ = image.shape
+    ph, pw = -(-h // multiple) * multiple, -(-w // multiple) * multiple
+    out = np.zeros((ph, pw, 4), np.float32)
+    lib().or_masked_rows(_p(image), _p(mask), w, h, multiple, _p(out))
+    return out
