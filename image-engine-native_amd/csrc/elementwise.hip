@@ -13,6 +13,8 @@ namespace ien {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef float float4v __attribute__((ext_vector_type(4)));
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 __device__ __forceinline__ float h2f_e(uint16_t h) {
   _Float16 v;
@@ -159,66 +161,243 @@ __global__ void k_unary(uint16_t *__restrict__ x, size_t n, int op) {
 }
 
 // ---- depthwise size x size convolution (no reference implementation) ----
-// NCHW: one block per 32-row band of one channel plane; the band's input
-// halo is staged in LDS as floats, and each thread computes 16 outputs of
-// one row from a register window, so each input value is read from HBM
-// once (plus the halo) and from LDS (size + 15) / 16 times per output row.
-template <int KSZ>
+// NCHW: one block per 32-row band of one channel plane (rows up to 256).
+//  - The band plus its halo rows go to LDS as f32 with KSZ / 2 zero columns
+//    each side: every thread first issues all of its 16-byte loads
+//    (addresses clamped into the plane, padding decided at the store), then
+//    converts and stores them.
+//  - Each thread computes a 4 x 4 block of outputs: for each of the
+//    4 + KSZ - 1 input rows it reads 4 + KSZ - 1 floats once and does the
+//    4 x KSZ multiply-adds of that row per output row; the weights are
+//    uniform per block (scalar registers).
+template <int KSZ, bool VEC>
 __global__ __launch_bounds__(256) void k_depthwise_nchw(const uint16_t *__restrict__ x, int H,
                                                         int W, int C,
                                                         const float *__restrict__ w,
                                                         const float *__restrict__ bias,
                                                         uint16_t *__restrict__ y) {
-  constexpr int BR = 32, P = KSZ / 2;
-  constexpr int MAXW = 256;  // widest supported row
-  __shared__ float tile[(BR + KSZ - 1) * (MAXW + KSZ - 1)];
+  constexpr int BR = 32, P = KSZ / 2, MAXW = 256;
+  constexpr int TH = BR + KSZ - 1;             // tile rows
+  constexpr int TW = MAXW + KSZ - 1 + 1;       // tile pitch (floats), odd: banks spread
+  __shared__ float tile[TH * TW];
   const int bands = (H + BR - 1) / BR;
-  const int c = blockIdx.x / bands, band = blockIdx.x % bands;
+  const int c = blockIdx.x / bands, band = blockIdx.x - c * bands;
   const int y0 = band * BR;
-  const int TW = W + KSZ - 1;
   const uint16_t *plane = x + (long)c * H * W;
-  for (int e = threadIdx.x; e < (BR + KSZ - 1) * TW; e += 256) {
-    int ty = e / TW, tx = e - ty * TW;
-    int iy = y0 + ty - P, ix = tx - P;
-    tile[e] = (iy >= 0 && iy < H && ix >= 0 && ix < W) ? h2f_e(plane[(long)iy * W + ix]) : 0.0f;
+
+  // Stage: rows y0 - P .. y0 + BR + P - 1 of the plane, 8 pixels per item
+  // (VEC: rows of whole 16-byte groups) or one.
+  if constexpr (VEC) {
+    const int chunks = W / 8;
+    const int items = TH * chunks;
+    constexpr int PER = (TH * (MAXW / 8) + 255) / 256;
+    u32x4 raw[PER];
+#pragma unroll
+    for (int k = 0; k < PER; k++) {
+      const int e = min(threadIdx.x + 256 * k, items - 1);
+      const int ty = e / chunks, ch = e - ty * chunks;
+      const int iy = min(max(y0 + ty - P, 0), H - 1);
+      raw[k] = *(const u32x4 *)(plane + (long)iy * W + 8 * ch);
+    }
+#pragma unroll
+    for (int k = 0; k < PER; k++) {
+      const int e = threadIdx.x + 256 * k;
+      if (e >= items) break;
+      const int ty = e / chunks, ch = e - ty * chunks;
+      const int iy = y0 + ty - P;
+      const bool row_ok = iy >= 0 && iy < H;
+      uint16_t h[8];
+      __builtin_memcpy(h, &raw[k], 16);
+      float *dst = tile + ty * TW + P + 8 * ch;
+#pragma unroll
+      for (int q = 0; q < 8; q++) dst[q] = row_ok ? h2f_e(h[q]) : 0.0f;
+    }
+  } else {
+    for (int e = threadIdx.x; e < TH * W; e += 256) {
+      const int ty = e / W, xx = e - ty * W;
+      const int iy = y0 + ty - P;
+      tile[ty * TW + P + xx] = iy >= 0 && iy < H ? h2f_e(plane[(long)iy * W + xx]) : 0.0f;
+    }
+  }
+  // Zero columns left and right of the plane's row (P each).
+  for (int e = threadIdx.x; e < TH * 2 * P; e += 256) {
+    const int ty = e / (2 * P), q = e - ty * 2 * P;
+    tile[ty * TW + (q < P ? q : W + q)] = 0.0f;
   }
   float wk[KSZ * KSZ];
 #pragma unroll
   for (int t = 0; t < KSZ * KSZ; t++) wk[t] = w[t * C + c];
   const float b = bias ? bias[c] : 0.0f;
   __syncthreads();
-  const int groups = (W + 15) / 16;
-  for (int item = threadIdx.x; item < BR * groups; item += 256) {
-    int r = item / groups, g = item - r * groups;
-    int oy = y0 + r;
-    if (oy >= H) continue;
-    int x0 = g * 16;
-    float acc[16];
+
+  // Compute: 4 x 4 output blocks, (BR / 4) x (W / 4) of them.
+  const int gx = (W + 3) / 4;
+  for (int item = threadIdx.x; item < (BR / 4) * gx; item += 256) {
+    const int r0 = 4 * (item / gx), x0 = 4 * (item - (item / gx) * gx);
+    if (y0 + r0 >= H) continue;
+    float acc[4][4];
 #pragma unroll
-    for (int q = 0; q < 16; q++) acc[q] = b;
+    for (int i = 0; i < 4; i++)
 #pragma unroll
-    for (int ky = 0; ky < KSZ; ky++) {
-      float win[16 + KSZ - 1];
-      const float *row = tile + (r + ky) * TW + x0;
+      for (int j = 0; j < 4; j++) acc[i][j] = b;
 #pragma unroll
-      for (int q = 0; q < 16 + KSZ - 1; q++) win[q] = (x0 + q < TW) ? row[q] : 0.0f;
+    for (int ry = 0; ry < 4 + KSZ - 1; ry++) {
+      float win[4 + KSZ - 1];
+      const float *row = tile + (r0 + ry) * TW + x0;
 #pragma unroll
-      for (int kx = 0; kx < KSZ; kx++)
+      for (int q = 0; q < 4 + KSZ - 1; q++) win[q] = row[q];
 #pragma unroll
-        for (int q = 0; q < 16; q++) acc[q] += win[q + kx] * wk[ky * KSZ + kx];
+      for (int i = 0; i < 4; i++) {
+        const int ky = ry - i;
+        if (ky < 0 || ky >= KSZ) continue;
+#pragma unroll
+        for (int kx = 0; kx < KSZ; kx++)
+#pragma unroll
+          for (int j = 0; j < 4; j++) acc[i][j] += win[j + kx] * wk[ky * KSZ + kx];
+      }
     }
-    uint16_t *out = y + (long)c * H * W + (long)oy * W + x0;
-    if (x0 + 16 <= W && (((uintptr_t)out) & 15) == 0) {
-      uint16_t h[16];
 #pragma unroll
-      for (int q = 0; q < 16; q++) h[q] = f2h_e(acc[q]);
-      u32x4 v0, v1;
-      __builtin_memcpy(&v0, h, 16);
-      __builtin_memcpy(&v1, h + 8, 16);
-      *(u32x4 *)out = v0;
-      *(u32x4 *)(out + 8) = v1;
+    for (int i = 0; i < 4; i++) {
+      const int oy = y0 + r0 + i;
+      if (oy >= H) break;
+      uint16_t *out = y + (long)c * H * W + (long)oy * W + x0;
+      if (VEC && x0 + 4 <= W) {
+        uint16_t h[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) h[j] = f2h_e(acc[i][j]);
+        uint2 v;
+        __builtin_memcpy(&v, h, 8);
+        *(uint2 *)out = v;
+      } else {
+        for (int j = 0; j < 4 && x0 + j < W; j++) out[j] = f2h_e(acc[i][j]);
+      }
+    }
+  }
+}
+
+// NCHW depthwise on MFMA, for rows of a multiple of 32 pixels (<= 256):
+// per channel and kernel row ky, the 1-D convolution of an input row is a
+// banded (Toeplitz) product, so a 32 x 32 output tile (32 rows y, 32
+// columns x from x0) is
+//   out[y][x] = sum_ky sum_{j < 48} in[y + ky - P][x0 - 8 + j] T_ky[j][x],
+//   T_ky[j][x] = w[ky][j - 8 - x + P] (zero outside the kernel),
+// 3 v_mfma_f32_32x32x16_f16 per ky: A = the input rows (16-byte reads of the
+// f16 band staged in LDS, 8 zero columns left and 16 right), B = T_ky in
+// registers (the weights rounded to f16; products are exact and sums f32).
+// The B fragments depend on the lane's column only: each block puts its
+// channel's 49 weights in LDS (loaded in the same batch as the input band:
+// one memory latency per block), spreads them into a zero-padded band per
+// ky, and every lane reads its 8 values of T_ky[16 s + 8 h + i][x] from
+// there.  The 8 values start at any half, so the band is kept in 8 copies
+// shifted by one half each: the lane reads copy (start mod 8) at a 16-byte
+// aligned address (unaligned LDS reads stall).  A block covers 32 rows, one
+// tile per wave.  C lane l holds column
+// x = l % 32 (coalesced 2-byte stores), register r row 8 (r / 4) + 4 (l / 32)
+// + r % 4.  Wave w takes columns 32 w .. 32 w + 31.
+template <int KSZ>
+__global__ __launch_bounds__(512) void k_depthwise_mfma(const uint16_t *__restrict__ x, int H,
+                                                        int W, int C,
+                                                        const float *__restrict__ w,
+                                                        const float *__restrict__ bias,
+                                                        uint16_t *__restrict__ y) {
+  constexpr int P = KSZ / 2, BR = 32, TH = BR + KSZ - 1, MAXW = 256;
+  constexpr int WB = 96, WOFF = 40;  // weight band: T value at kx sits at kx + WOFF
+  constexpr int BATCH = 8;           // loads in flight per thread (covers TH rows of MAXW)
+  __shared__ __attribute__((aligned(16))) uint16_t tile[TH * (MAXW + 24)];
+  __shared__ __attribute__((aligned(16))) uint16_t wband[8 * KSZ * WB];
+  __shared__ float wl[KSZ * KSZ];
+  const int pitch = W + 24;  // halves; input column x sits at x + 8
+  const int bands = (H + BR - 1) / BR;
+  const int c = blockIdx.x / bands, band = blockIdx.x - c * bands, y0 = band * BR;
+  const uint16_t *plane = x + (long)c * H * W;
+  const int nt = blockDim.x;
+
+  // Stage rows y0 - P .. y0 + BR + P - 1, 16-byte chunks (chunk k of an LDS
+  // row is input columns 8 k - 8 .. 8 k - 1), and the weights: all loads of
+  // a thread first, from clamped addresses, zeros decided at the store.
+  const int chunks = pitch / 8, items = TH * chunks;
+  const float wmine = w[min((int)threadIdx.x, KSZ * KSZ - 1) * C + c];
+  for (int base = threadIdx.x; base < items; base += BATCH * nt) {
+    u32x4 raw[BATCH];
+#pragma unroll
+    for (int b = 0; b < BATCH; b++) {
+      const int e = min(base + b * nt, items - 1);
+      const int ty = e / chunks, k = e - ty * chunks;
+      const int iy = min(max(y0 + ty - P, 0), H - 1);
+      const int ix = min(max(8 * k - 8, 0), W - 8);
+      raw[b] = *(const u32x4 *)(plane + (long)iy * W + ix);
+    }
+#pragma unroll
+    for (int b = 0; b < BATCH; b++) {
+      const int e = base + b * nt;
+      if (e >= items) break;
+      const int ty = e / chunks, k = e - ty * chunks;
+      const int iy = y0 + ty - P;
+      const bool ok = iy >= 0 && iy < H && k >= 1 && 8 * k <= W;
+      const u32x4 zero = {0u, 0u, 0u, 0u};
+      *(u32x4 *)(tile + ty * pitch + 8 * k) = ok ? raw[b] : zero;
+    }
+  }
+  if (threadIdx.x < KSZ * KSZ) wl[threadIdx.x] = wmine;
+  const float b = bias ? bias[c] : 0.0f;
+  __syncthreads();
+  // The weight band (kx outside the kernel: zero), every entry of every
+  // copy written, 8 per thread and item: copy k holds at t the band value of
+  // t + k.
+  for (int e = threadIdx.x; e < KSZ * WB; e += nt) {  // e = (k, ky, 8-entry group)
+    const int k = e / (KSZ * WB / 8), rest = e - k * (KSZ * WB / 8);
+    const int ky = rest / (WB / 8), q = rest - ky * (WB / 8);
+    const int kx0 = 8 * q + k - WOFF;
+    uint16_t h[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      const int kx = kx0 + j;
+      h[j] = f2h_e(kx >= 0 && kx < KSZ ? wl[ky * KSZ + min(max(kx, 0), KSZ - 1)] : 0.0f);
+    }
+    u32x4 v;
+    __builtin_memcpy(&v, h, 16);
+    *(u32x4 *)(wband + (k * KSZ + ky) * WB + 8 * q) = v;
+  }
+  __syncthreads();
+
+  const int lane = threadIdx.x & 63, hf = lane >> 5, l32 = lane & 31;
+  const int x0 = 32 * (threadIdx.x >> 6);
+  // B fragments: element i of step s is T_ky at kx = 16 s + 8 h + i - 8 - x + P.
+  half8 tb[KSZ][3];
+#pragma unroll
+  for (int ky = 0; ky < KSZ; ky++)
+#pragma unroll
+    for (int s = 0; s < 3; s++) {
+      const int t0 = WOFF + 16 * s + 8 * hf - 8 - l32 + P;  // 1 + P .. 79 + P
+      const int k = t0 & 7;
+      tb[ky][s] = *(const half8 *)(wband + (k * KSZ + ky) * WB + (t0 - k));
+    }
+
+  uint16_t *out = y + (long)c * H * W + x0 + l32;
+  const bool full = y0 + BR <= H;
+#pragma unroll
+  for (int t = 0; t < BR / 32; t++) {
+    floatx16 acc;
+#pragma unroll
+    for (int r = 0; r < 16; r++) acc[r] = b;
+#pragma unroll
+    for (int ky = 0; ky < KSZ; ky++)
+#pragma unroll
+      for (int s = 0; s < 3; s++) {
+        const half8 a =
+            *(const half8 *)(tile + (32 * t + l32 + ky) * pitch + x0 + 16 * s + 8 * hf);
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, tb[ky][s], acc, 0, 0, 0);
+      }
+    if (full) {
+#pragma unroll
+      for (int r = 0; r < 16; r++)
+        out[(long)(y0 + 32 * t + 8 * (r >> 2) + 4 * hf + (r & 3)) * W] = f2h_e(acc[r]);
     } else {
-      for (int q = 0; q < 16 && x0 + q < W; q++) out[q] = f2h_e(acc[q]);
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const int oy = y0 + 32 * t + 8 * (r >> 2) + 4 * hf + (r & 3);
+        if (oy < H) out[(long)oy * W] = f2h_e(acc[r]);
+      }
     }
   }
 }
@@ -312,17 +491,26 @@ ien_status ien_depthwise(ien_ctx *ctx, const uint16_t *d_x, size_t height, size_
   IEN_CHECK(ctx && d_x && d_w && d_y, IEN_ERR_INPUT, "null argument");
   IEN_CHECK(height > 0 && width > 0 && channels > 0, IEN_ERR_INPUT, "empty input");
   IEN_CHECK(size % 2 == 1 && size <= 7, IEN_ERR_INPUT, "depthwise size %zu", size);
-  if (layout == IEN_LAYOUT_NCHW && size == 7 && width <= 256) {
+  // The band kernel: 16-byte loads and 8-byte stores for rows of a multiple
+  // of 8 pixels in 16-byte aligned planes, element by element otherwise.
+  const bool bands = layout == IEN_LAYOUT_NCHW && width <= 256 && (size == 7 || size == 3);
+  const bool vec = width % 8 == 0 && ((uintptr_t)d_x & 15) == 0 && ((uintptr_t)d_y & 7) == 0;
+  if (bands && vec && width % 32 == 0) {
+    // Toeplitz products on MFMA: one wave per 32 columns of a 32-row band.
     unsigned blocks = (unsigned)(channels * ((height + 31) / 32));
-    hipLaunchKernelGGL(k_depthwise_nchw<7>, dim3(blocks), dim3(256), 0, ctx->stream, d_x,
-                       (int)height, (int)width, (int)channels, d_w, d_bias, d_y);
-  } else if (layout == IEN_LAYOUT_NCHW && size == 3 && width <= 256) {
+    hipLaunchKernelGGL(size == 7 ? k_depthwise_mfma<7> : k_depthwise_mfma<3>, dim3(blocks),
+                       dim3((unsigned)(2 * width)), 0, ctx->stream, d_x, (int)height, (int)width,
+                       (int)channels, d_w, d_bias, d_y);
+  } else if (bands) {
+    void (*k)(const uint16_t *, int, int, int, const float *, const float *, uint16_t *) =
+        size == 7 ? (vec ? k_depthwise_nchw<7, true> : k_depthwise_nchw<7, false>)
+                  : (vec ? k_depthwise_nchw<3, true> : k_depthwise_nchw<3, false>);
     unsigned blocks = (unsigned)(channels * ((height + 31) / 32));
-    hipLaunchKernelGGL(k_depthwise_nchw<3>, dim3(blocks), dim3(256), 0, ctx->stream, d_x,
-                       (int)height, (int)width, (int)channels, d_w, d_bias, d_y);
+    hipLaunchKernelGGL(k, dim3(blocks), dim3(256), 0, ctx->stream, d_x, (int)height, (int)width,
+                       (int)channels, d_w, d_bias, d_y);
   } else {
     IEN_CHECK(layout == IEN_LAYOUT_NHWC, IEN_ERR_INPUT,
-              "NCHW depthwise of size %zu or rows over 256 pixels", size);
+              "NCHW depthwise of size %zu, rows over 256 pixels or not a multiple of 8", size);
     size_t total = height * width * channels;
     hipLaunchKernelGGL(k_depthwise_nhwc, dim3(grid_for(total, 256)), dim3(256), 0, ctx->stream,
                        d_x, (int)height, (int)width, (int)channels, d_w, (int)size, d_bias, d_y);
