@@ -18,6 +18,7 @@
 #include <memory>
 
 #include "ien_internal.h"
+#include "scunet.h"
 
 namespace ien {
 
@@ -139,6 +140,7 @@ struct ien_model {
   ien_ctx *ctx = nullptr;
   ien_model_kind kind = IEN_MODEL_REALESRGAN;
   std::vector<ien::EsrganLayer> layers;
+  std::unique_ptr<ien::Scunet> scunet;  // IEN_MODEL_SCUNET
   ien::Maps maps;
   bool use_graph = false;
   hipGraphExec_t graph = nullptr;
@@ -182,9 +184,6 @@ static ien_status ensure_maps(ien_model *model, size_t pixels, bool host_staging
   }
   return IEN_OK;
 }
-
-using TensorSource = std::function<ien_status(const std::string &, std::vector<size_t>,
-                                              std::vector<float> *)>;
 
 // realesrgan-native network.rs:54-74 Network::load
 static ien_status load_esrgan(ien_model *model, const TensorSource &take) {
@@ -257,6 +256,34 @@ static ien_status enqueue_esrgan(ien_model *model, const float *d_image, size_t 
   return IEN_OK;
 }
 
+// Steps of a run (progress reports) and output floats per input pixel.
+static int model_steps(const ien_model *m) {
+  return m->kind == IEN_MODEL_SCUNET ? SCUNET_STEPS : STEPS;
+}
+static size_t out_per_pixel(const ien_model *m) {
+  return m->kind == IEN_MODEL_SCUNET ? 3 : 3 * SCALE * SCALE;
+}
+
+// Maps for an image of this size, then its launches.
+static ien_status prepare(ien_model *model, size_t width, size_t height) {
+  if (model->kind == IEN_MODEL_SCUNET) {
+    size_t pw, ph;
+    scunet_padded(width, height, &pw, &ph);
+    const size_t before = model->scunet->pixels;
+    ien_status st = scunet_reserve(model->scunet.get(), pw * ph);
+    if (st == IEN_OK && model->scunet->pixels != before) drop_graph(model);
+    return st;
+  }
+  return ensure_maps(model, width * height, false);
+}
+
+static ien_status enqueue(ien_model *model, const float *d_image, size_t width, size_t height,
+                          float *d_out, hipEvent_t *events) {
+  if (model->kind == IEN_MODEL_SCUNET)
+    return scunet_enqueue(model->scunet.get(), d_image, width, height, d_out, events);
+  return enqueue_esrgan(model, d_image, width, height, d_out, events);
+}
+
 static ien_status check_size(size_t width, size_t height) {
   // realesrgan-native lib.rs:302-316
   if (width == 0 || height == 0) return fail(IEN_ERR_INPUT, "empty %zu x %zu image", width, height);
@@ -274,12 +301,19 @@ extern "C" {
 static ien_status model_new(ien_ctx *ctx, ien_model_kind kind, const TensorSource &take,
                             ien_model **out) {
   IEN_CHECK(ctx && out, IEN_ERR_INPUT, "null argument");
-  IEN_CHECK(kind == IEN_MODEL_REALESRGAN, IEN_ERR_INPUT, "model kind %d", (int)kind);
+  IEN_CHECK(kind == IEN_MODEL_REALESRGAN || kind == IEN_MODEL_SCUNET, IEN_ERR_INPUT,
+            "model kind %d", (int)kind);
   IEN_HIP(hipSetDevice(ctx->device));
   std::unique_ptr<ien_model> model(new ien_model);
   model->ctx = ctx;
   model->kind = kind;
-  ien_status st = load_esrgan(model.get(), take);
+  ien_status st;
+  if (kind == IEN_MODEL_SCUNET) {
+    model->scunet.reset(new Scunet);
+    st = scunet_load(ctx, take, model->scunet.get());
+  } else {
+    st = load_esrgan(model.get(), take);
+  }
   if (st != IEN_OK) {
     ien_model_free(model.release());
     return st;
@@ -292,7 +326,9 @@ ien_status ien_model_load(ien_ctx *ctx, ien_model_kind kind, const char *weights
                           ien_model **out) {
   IEN_CHECK(weights_path, IEN_ERR_INPUT, "no weights path");
   WeightFile file;
-  ien_status st = file.read(weights_path, "REALESRG");
+  // The weights files' magics (realesrgan-native lib.rs:124, scunet-native
+  // lib.rs:101).
+  ien_status st = file.read(weights_path, kind == IEN_MODEL_SCUNET ? "SCUNET\0\0" : "REALESRG");
   if (st != IEN_OK) return st;
   st = model_new(
       ctx, kind,
@@ -352,6 +388,7 @@ void ien_model_free(ien_model *model) {
     ien_matrix_free(l.conv);
     (void)hipFree(l.d_slope);
   }
+  if (model->scunet) scunet_free(model->scunet.get());
   free_maps(model->maps);
   delete model;
 }
@@ -366,20 +403,20 @@ ien_status ien_model_set_graph(ien_model *model, int enabled) {
 ien_status ien_model_run_device(ien_model *model, const float *d_image, const float *d_mask,
                                 size_t width, size_t height, float *d_out) {
   IEN_CHECK(model && d_image && d_out, IEN_ERR_INPUT, "null argument");
-  IEN_CHECK(d_mask == nullptr, IEN_ERR_INPUT, "Real-ESRGAN takes no mask");
+  IEN_CHECK(d_mask == nullptr, IEN_ERR_INPUT, "this model takes no mask");
   ien_status st = check_size(width, height);
   if (st != IEN_OK) return st;
   ien_ctx *ctx = model->ctx;
   IEN_HIP(hipSetDevice(ctx->device));
-  st = ensure_maps(model, width * height, false);
+  st = prepare(model, width, height);
   if (st != IEN_OK) return st;
-  if (!model->use_graph) return enqueue_esrgan(model, d_image, width, height, d_out, nullptr);
+  if (!model->use_graph) return enqueue(model, d_image, width, height, d_out, nullptr);
   if (!model->graph || model->graph_in != d_image || model->graph_out != d_out ||
       model->graph_w != width || model->graph_h != height) {
     drop_graph(model);
     hipGraph_t graph = nullptr;
     IEN_HIP(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
-    st = enqueue_esrgan(model, d_image, width, height, d_out, nullptr);
+    st = enqueue(model, d_image, width, height, d_out, nullptr);
     hipError_t e = hipStreamEndCapture(ctx->stream, &graph);
     if (st != IEN_OK) {
       if (graph) (void)hipGraphDestroy(graph);
@@ -404,33 +441,55 @@ ien_status ien_model_run_device(ien_model *model, const float *d_image, const fl
 ien_status ien_model_run(ien_model *model, const float *image, const float *mask, size_t width,
                          size_t height, float *out, ien_progress progress, void *user) {
   IEN_CHECK(model && image && out, IEN_ERR_INPUT, "null argument");
-  IEN_CHECK(mask == nullptr, IEN_ERR_INPUT, "Real-ESRGAN takes no mask");
+  IEN_CHECK(mask == nullptr, IEN_ERR_INPUT, "this model takes no mask");
   ien_status st = check_size(width, height);
   if (st != IEN_OK) return st;
   ien_ctx *ctx = model->ctx;
   IEN_HIP(hipSetDevice(ctx->device));
   const size_t pixels = width * height;
-  st = ensure_maps(model, pixels, true);
-  if (st != IEN_OK) return st;
-  Maps &m = model->maps;
-  IEN_HIP(hipMemcpyAsync(m.d_in, image, pixels * 3 * 4, hipMemcpyHostToDevice, ctx->stream));
+  float *d_in = nullptr, *d_out = nullptr;
+  if (model->kind == IEN_MODEL_SCUNET) {
+    Scunet &s = *model->scunet;
+    st = prepare(model, width, height);
+    if (st != IEN_OK) return st;
+    if (s.staged < pixels) {
+      IEN_HIP(hipStreamSynchronize(ctx->stream));
+      (void)hipFree(s.d_in);
+      (void)hipFree(s.d_out);
+      s.d_in = s.d_out = nullptr;
+      s.staged = 0;
+      IEN_HIP(hipMalloc(&s.d_in, pixels * 3 * 4));
+      IEN_HIP(hipMalloc(&s.d_out, pixels * 3 * 4));
+      s.staged = pixels;
+    }
+    d_in = s.d_in;
+    d_out = s.d_out;
+  } else {
+    st = ensure_maps(model, pixels, true);
+    if (st != IEN_OK) return st;
+    d_in = model->maps.d_in;
+    d_out = model->maps.d_out;
+  }
+  IEN_HIP(hipMemcpyAsync(d_in, image, pixels * 3 * 4, hipMemcpyHostToDevice, ctx->stream));
+  const int steps = model_steps(model);
   std::vector<hipEvent_t> events;
   if (progress) {
-    events.resize(STEPS);
+    events.resize(steps);
     for (auto &e : events) IEN_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
   }
-  st = enqueue_esrgan(model, m.d_in, width, height, m.d_out, progress ? events.data() : nullptr);
+  st = enqueue(model, d_in, width, height, d_out, progress ? events.data() : nullptr);
   bool cancelled = false;
   if (st == IEN_OK && progress) {
-    // lib.rs:168-188: progress after each layer, in order; a break stops
-    // the run with Cancelled and leaves the model usable.
-    for (int i = 0; i < STEPS && !cancelled; i++) {
+    // lib.rs:168-188 (SCUNet lib.rs:205-215): progress after each layer or
+    // block, in order; a break stops the run with Cancelled and leaves the
+    // model usable.
+    for (int i = 0; i < steps && !cancelled; i++) {
       hipError_t e = hipEventSynchronize(events[i]);
       if (e != hipSuccess) {
-        st = fail(IEN_ERR_GPU, "layer %d: %s", i, hipGetErrorString(e));
+        st = fail(IEN_ERR_GPU, "step %d: %s", i, hipGetErrorString(e));
         break;
       }
-      if (progress((float)(i + 1) / STEPS, user) != 0) cancelled = true;
+      if (progress((float)(i + 1) / steps, user) != 0) cancelled = true;
     }
   }
   hipError_t e = hipStreamSynchronize(ctx->stream);
@@ -438,7 +497,7 @@ ien_status ien_model_run(ien_model *model, const float *image, const float *mask
   if (st != IEN_OK) return st;
   if (e != hipSuccess) return fail(IEN_ERR_GPU, "run: %s", hipGetErrorString(e));
   if (cancelled) return fail(IEN_ERR_CANCELLED, "the progress callback stopped the run");
-  IEN_HIP(hipMemcpy(out, m.d_out, pixels * 3 * SCALE * SCALE * 4, hipMemcpyDeviceToHost));
+  IEN_HIP(hipMemcpy(out, d_out, pixels * out_per_pixel(model) * 4, hipMemcpyDeviceToHost));
   return IEN_OK;
 }
 

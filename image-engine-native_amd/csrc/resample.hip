@@ -123,7 +123,57 @@ __global__ __launch_bounds__(256) void k_crop(const uint16_t *__restrict__ map, 
   out[item] = h2f(map[((long)y * map_width + x) * stride + ch]);
 }
 
+// 2 x 2 gather: one thread per output row and 8-channel chunk of one of
+// the four pixels.
+__global__ __launch_bounds__(256) void k_gather_2x2(const uint16_t *__restrict__ map, int h2,
+                                                    int w2, int width, int c, long stride,
+                                                    int col_major, uint16_t *__restrict__ rows) {
+  const int chunks = c >> 3;
+  const long item = (long)blockIdx.x * 256 + threadIdx.x;
+  if (item >= (long)h2 * w2 * 4 * chunks) return;
+  const long r = item / (4 * chunks);
+  const int rest = (int)(item - r * 4 * chunks), q = rest / chunks, k = rest - q * chunks;
+  const int yy = 2 * (int)(r / w2), xx = 2 * (int)(r - (r / w2) * w2);
+  const int dy = col_major ? (q & 1) : (q >> 1), dx = col_major ? (q >> 1) : (q & 1);
+  *(u32x4 *)(rows + (r * 4 + q) * c + 8 * k) =
+      *(const u32x4 *)(map + ((long)(yy + dy) * width + xx + dx) * stride + 8 * k);
+}
+
+// 2 x 2 scatter: one thread per input pixel, sub-pixel and 8-channel chunk.
+__global__ __launch_bounds__(256) void k_scatter_2x2(const uint16_t *__restrict__ rows,
+                                                     long row_stride, int h, int w, int c,
+                                                     uint16_t *__restrict__ map, long stride) {
+  const int chunks = c >> 3;
+  const long item = (long)blockIdx.x * 256 + threadIdx.x;
+  if (item >= (long)h * w * 4 * chunks) return;
+  const long r = item / (4 * chunks);
+  const int rest = (int)(item - r * 4 * chunks), q = rest / chunks, k = rest - q * chunks;
+  const int y = (int)(r / w), x = (int)(r - (r / w) * w);
+  const long pixel = (long)(2 * y + (q >> 1)) * (2 * w) + 2 * x + (q & 1);
+  *(u32x4 *)(map + pixel * stride + 8 * k) = *(const u32x4 *)(rows + r * row_stride + q * c + 8 * k);
+}
+
+// x += y, 8 halves per thread (a scalar tail).
+__global__ __launch_bounds__(256) void k_add(uint16_t *__restrict__ x,
+                                             const uint16_t *__restrict__ y, long n) {
+  const long i = ((long)blockIdx.x * 256 + threadIdx.x) * 8;
+  if (i + 8 <= n) {
+    u32x4 a = *(const u32x4 *)(x + i), b = *(const u32x4 *)(y + i);
+    uint16_t ha[8], hb[8];
+    __builtin_memcpy(ha, &a, 16);
+    __builtin_memcpy(hb, &b, 16);
+#pragma unroll
+    for (int e = 0; e < 8; e++) ha[e] = f2h(h2f(ha[e]) + h2f(hb[e]));
+    __builtin_memcpy(&a, ha, 16);
+    *(u32x4 *)(x + i) = a;
+  } else {
+    for (long j = i; j < n; j++) x[j] = f2h(h2f(x[j]) + h2f(y[j]));
+  }
+}
+
 unsigned grid256(long items) { return (unsigned)((items + 255) / 256); }
+
+bool a16(const void *p) { return ((uintptr_t)p & 15) == 0; }
 
 }  // namespace
 }  // namespace ien
@@ -189,6 +239,50 @@ ien_status ien_crop(ien_ctx *ctx, const uint16_t *d_map, size_t map_width, size_
   hipLaunchKernelGGL(k_crop, dim3(grid256((long)(height * width * channels))), dim3(256), 0,
                      ctx->stream, d_map, (int)map_width, (long)stride, (int)width, (int)height,
                      (int)channels, d_out);
+  IEN_HIP(hipGetLastError());
+  return IEN_OK;
+}
+
+ien_status ien_gather_2x2(ien_ctx *ctx, const uint16_t *d_map, size_t height, size_t width,
+                          size_t c, size_t stride, ien_order order, uint16_t *d_rows) {
+  IEN_CHECK(ctx && d_map && d_rows, IEN_ERR_INPUT, "null argument");
+  IEN_CHECK(height >= 2 && width >= 2 && height % 2 == 0 && width % 2 == 0 && height < (1u << 30) &&
+                width < (1u << 30),
+            IEN_ERR_INPUT, "2 x 2 gather of a %zu x %zu map", width, height);
+  IEN_CHECK(c >= 8 && c % 8 == 0 && stride >= c && stride % 8 == 0 && a16(d_map) && a16(d_rows),
+            IEN_ERR_INPUT, "%zu channels, stride %zu (multiples of 8, 16-byte aligned)", c, stride);
+  IEN_CHECK(order == IEN_ORDER_ROW_MAJOR || order == IEN_ORDER_COLUMN_MAJOR, IEN_ERR_INPUT,
+            "order %d", (int)order);
+  const long items = (long)(height / 2) * (width / 2) * 4 * (c / 8);
+  hipLaunchKernelGGL(k_gather_2x2, dim3(grid256(items)), dim3(256), 0, ctx->stream, d_map,
+                     (int)(height / 2), (int)(width / 2), (int)width, (int)c, (long)stride,
+                     order == IEN_ORDER_COLUMN_MAJOR ? 1 : 0, d_rows);
+  IEN_HIP(hipGetLastError());
+  return IEN_OK;
+}
+
+ien_status ien_scatter_2x2(ien_ctx *ctx, const uint16_t *d_rows, size_t row_stride,
+                           size_t height, size_t width, size_t c, uint16_t *d_map,
+                           size_t stride) {
+  IEN_CHECK(ctx && d_rows && d_map, IEN_ERR_INPUT, "null argument");
+  IEN_CHECK(height >= 1 && width >= 1 && height < (1u << 29) && width < (1u << 29), IEN_ERR_INPUT,
+            "2 x 2 scatter of a %zu x %zu grid", width, height);
+  IEN_CHECK(c >= 8 && c % 8 == 0 && row_stride >= 4 * c && row_stride % 8 == 0 && stride >= c &&
+                stride % 8 == 0 && a16(d_map) && a16(d_rows),
+            IEN_ERR_INPUT, "%zu channels, strides %zu / %zu", c, row_stride, stride);
+  const long items = (long)height * width * 4 * (c / 8);
+  hipLaunchKernelGGL(k_scatter_2x2, dim3(grid256(items)), dim3(256), 0, ctx->stream, d_rows,
+                     (long)row_stride, (int)height, (int)width, (int)c, d_map, (long)stride);
+  IEN_HIP(hipGetLastError());
+  return IEN_OK;
+}
+
+ien_status ien_add(ien_ctx *ctx, uint16_t *d_x, const uint16_t *d_y, size_t n) {
+  IEN_CHECK(ctx && (n == 0 || (d_x && d_y)), IEN_ERR_INPUT, "null argument");
+  IEN_CHECK(a16(d_x) && a16(d_y), IEN_ERR_INPUT, "alignment (16 bytes)");
+  if (n == 0) return IEN_OK;
+  hipLaunchKernelGGL(k_add, dim3(grid256((long)((n + 7) / 8))), dim3(256), 0, ctx->stream, d_x,
+                     d_y, (long)n);
   IEN_HIP(hipGetLastError());
   return IEN_OK;
 }

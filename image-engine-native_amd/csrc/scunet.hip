@@ -1,0 +1,270 @@
+// scunet.hip -- the SCUNet U-Net on the GPU (crates/scunet-native/src/
+// network.rs:113-354): f16 NHWC maps, the block's 3x3 convolutions and the
+// head and tail through the implicit-GEMM kernels, 1x1 products over pixel
+// rows, the Swin half through ien_swin, the 2x2 halving and doubling
+// convolutions as gathers / scatters around row products.  One event is
+// recorded after each of the 28 blocks for progress reports.
+
+#include <string>
+
+#include "ien_internal.h"
+#include "scunet.h"
+
+namespace ien {
+
+namespace {
+
+constexpr int DIM = 64, BLOCKS = 4, WINDOW = 8, MULTIPLE = 64;
+
+ien_status rows_product(ien_ctx *ctx, const uint16_t *in, size_t k, size_t rows,
+                        const ien_matrix *m, uint16_t *out, size_t stride, int accumulate) {
+  ien_input x{};
+  x.kind = IEN_INPUT_ROWS;
+  x.data = in;
+  x.stride = k;
+  ien_output o{};
+  o.data = out;
+  o.stride = stride;
+  o.layout = IEN_LAYOUT_NHWC;
+  o.type = IEN_OUT_F16;
+  return ien_multiply_ex(ctx, &x, 0, rows, m, &o, IEN_ACT_NONE, nullptr, accumulate);
+}
+
+// A 3x3 zero-padded convolution of an h x w f16 NHWC map.
+ien_status conv3(ien_ctx *ctx, const uint16_t *x, int h, int w, int c, long xs,
+                 const ien_matrix *m, void *y, long ys, ien_act act, int accumulate) {
+  ConvCall cc;
+  cc.x = x;
+  cc.H = h;
+  cc.W = w;
+  cc.C = c;
+  cc.xs = xs;
+  cc.ks = 3;
+  cc.stride = 1;
+  cc.OH = h;
+  cc.OW = w;
+  cc.row0 = 0;
+  cc.rows = (long)h * w;
+  cc.w = m;
+  cc.y = y;
+  cc.ys = ys;
+  cc.act = act;
+  cc.accumulate = accumulate;
+  return launch_conv(ctx, cc);
+}
+
+ien_status matrix(ien_ctx *ctx, const TensorSource &take, const std::string &name, size_t k,
+                  size_t n, bool bias, ien_matrix **out) {
+  std::vector<float> w, b;
+  ien_status st = take(name + ".weight", {k, n}, &w);
+  if (st == IEN_OK && bias) st = take(name + ".bias", {n}, &b);
+  if (st != IEN_OK) return st;
+  return ien_matrix_new(ctx, w.data(), IEN_W_F32, k, n, bias ? b.data() : nullptr, out);
+}
+
+// swin.rs:98-120 Transformer::load and network.rs:122-134 Block::load.
+ien_status load_block(ien_ctx *ctx, const TensorSource &take, const std::string &name, int c,
+                      bool shifted, ScunetBlock *b) {
+  const size_t h = (size_t)c / 2;
+  b->c = c;
+  ien_status st = matrix(ctx, take, name + ".conv1_1", c, c, true, &b->split);
+  if (st == IEN_OK) st = matrix(ctx, take, name + ".conv_block.0", 9 * h, h, false, &b->conv1);
+  if (st == IEN_OK) st = matrix(ctx, take, name + ".conv_block.2", 9 * h, h, false, &b->conv2);
+  if (st == IEN_OK) st = matrix(ctx, take, name + ".conv1_2", c, c, true, &b->join);
+  if (st != IEN_OK) return st;
+  const std::string t = name + ".trans_block";
+  std::vector<float> g1, b1, qw, qb, pos, pw, pb, g2, b2, f1w, f1b, f2w, f2b;
+  const size_t heads = h / 32;
+  if ((st = take(t + ".ln1.weight", {h}, &g1)) != IEN_OK) return st;
+  if ((st = take(t + ".ln1.bias", {h}, &b1)) != IEN_OK) return st;
+  if ((st = take(t + ".msa.embedding_layer.weight", {h, 3 * h}, &qw)) != IEN_OK) return st;
+  if ((st = take(t + ".msa.embedding_layer.bias", {3 * h}, &qb)) != IEN_OK) return st;
+  if ((st = take(t + ".msa.position_bias", {heads, 64, 64}, &pos)) != IEN_OK) return st;
+  if ((st = take(t + ".msa.linear.weight", {h, h}, &pw)) != IEN_OK) return st;
+  if ((st = take(t + ".msa.linear.bias", {h}, &pb)) != IEN_OK) return st;
+  if ((st = take(t + ".ln2.weight", {h}, &g2)) != IEN_OK) return st;
+  if ((st = take(t + ".ln2.bias", {h}, &b2)) != IEN_OK) return st;
+  if ((st = take(t + ".mlp.0.weight", {h, 4 * h}, &f1w)) != IEN_OK) return st;
+  if ((st = take(t + ".mlp.0.bias", {4 * h}, &f1b)) != IEN_OK) return st;
+  if ((st = take(t + ".mlp.2.weight", {4 * h, h}, &f2w)) != IEN_OK) return st;
+  if ((st = take(t + ".mlp.2.bias", {h}, &f2b)) != IEN_OK) return st;
+  ien_swin_weights sw{};
+  sw.c = (int)h;
+  sw.window = WINDOW;
+  sw.shift = shifted ? WINDOW / 2 : 0;
+  sw.masked = -__builtin_inff();
+  sw.ln1_gamma = g1.data();
+  sw.ln1_beta = b1.data();
+  sw.qkv_w = qw.data();
+  sw.qkv_b = qb.data();
+  sw.position = pos.data();
+  sw.proj_w = pw.data();
+  sw.proj_b = pb.data();
+  sw.ln2_gamma = g2.data();
+  sw.ln2_beta = b2.data();
+  sw.fc1_w = f1w.data();
+  sw.fc1_b = f1b.data();
+  sw.fc2_w = f2w.data();
+  sw.fc2_b = f2b.data();
+  return ien_swin_new(ctx, &sw, &b->swin);
+}
+
+void free_block(ScunetBlock &b) {
+  ien_matrix_free(b.split);
+  ien_matrix_free(b.conv1);
+  ien_matrix_free(b.conv2);
+  ien_matrix_free(b.join);
+  ien_swin_free(b.swin);
+  b = ScunetBlock();
+}
+
+void free_maps(Scunet &s) {
+  for (uint16_t **p : {&s.img, &s.x, &s.y, &s.t, &s.rows, &s.skip[0], &s.skip[1], &s.skip[2],
+                       &s.out16}) {
+    (void)hipFree(*p);
+    *p = nullptr;
+  }
+  s.pixels = 0;
+}
+
+// network.rs:158-208 run_level on the h x w map x of c channels (y, t:
+// the block's buffers).
+ien_status run_level(Scunet &s, ScunetBlock *blocks, int h, int w, int c, hipEvent_t *events,
+                     int *step) {
+  ien_ctx *ctx = s.ctx;
+  const size_t pixels = (size_t)h * w, half = (size_t)c / 2;
+  ien_status st = rows_product(ctx, s.x, c, pixels, blocks[0].split, s.y, c, 0);
+  for (int b = 0; b < BLOCKS && st == IEN_OK; b++) {
+    ScunetBlock &B = blocks[b];
+    // network.rs:135-153 convolve: conv3 + ReLU into t, conv3 added back.
+    st = conv3(ctx, s.y, h, w, (int)half, c, B.conv1, s.t, (long)half, IEN_ACT_RELU, 0);
+    if (st == IEN_OK)
+      st = conv3(ctx, s.t, h, w, (int)half, (long)half, B.conv2, s.y, c, IEN_ACT_NONE, 1);
+    if (st == IEN_OK) st = ien_swin_run(B.swin, s.y + half, c, h, w);
+    if (st == IEN_OK) st = rows_product(ctx, s.y, c, pixels, B.join, s.x, c, 1);
+    if (st == IEN_OK && b + 1 < BLOCKS)
+      st = rows_product(ctx, s.x, c, pixels, blocks[b + 1].split, s.y, c, 0);
+    if (st == IEN_OK && events) IEN_HIP(hipEventRecord(events[*step], ctx->stream));
+    ++*step;
+  }
+  return st;
+}
+
+}  // namespace
+
+ien_status scunet_load(ien_ctx *ctx, const TensorSource &take, Scunet *s) {
+  s->ctx = ctx;
+  ien_status st = matrix(ctx, take, "m_head.0", 27, DIM, false, &s->head);
+  for (int l = 0; l < 3 && st == IEN_OK; l++) {
+    const int c = DIM << l;
+    const std::string name = "m_down" + std::to_string(l + 1);
+    for (int b = 0; b < BLOCKS && st == IEN_OK; b++)
+      st = load_block(ctx, take, name + "." + std::to_string(b), c, b % 2 == 1, &s->down[l][b]);
+    if (st == IEN_OK)
+      st = matrix(ctx, take, name + "." + std::to_string(BLOCKS), 4 * c, 2 * c, false, &s->halve[l]);
+  }
+  for (int b = 0; b < BLOCKS && st == IEN_OK; b++)
+    st = load_block(ctx, take, "m_body." + std::to_string(b), 8 * DIM, b % 2 == 1, &s->body[b]);
+  for (int l = 0; l < 3 && st == IEN_OK; l++) {
+    const int c = DIM << (2 - l);
+    const std::string name = "m_up" + std::to_string(3 - l);
+    st = matrix(ctx, take, name + ".0", 2 * c, 4 * c, false, &s->dbl[l]);
+    for (int b = 0; b < BLOCKS && st == IEN_OK; b++)
+      st = load_block(ctx, take, name + "." + std::to_string(b + 1), c, b % 2 == 1, &s->up[l][b]);
+  }
+  if (st == IEN_OK) st = matrix(ctx, take, "m_tail.0", 9 * DIM, 3, false, &s->tail);
+  return st;
+}
+
+void scunet_free(Scunet *s) {
+  ien_matrix_free(s->head);
+  ien_matrix_free(s->tail);
+  for (int l = 0; l < 3; l++) {
+    for (int b = 0; b < BLOCKS; b++) {
+      free_block(s->down[l][b]);
+      free_block(s->up[l][b]);
+    }
+    ien_matrix_free(s->halve[l]);
+    ien_matrix_free(s->dbl[l]);
+  }
+  for (int b = 0; b < BLOCKS; b++) free_block(s->body[b]);
+  free_maps(*s);
+  (void)hipFree(s->d_in);
+  (void)hipFree(s->d_out);
+}
+
+void scunet_padded(size_t width, size_t height, size_t *pw, size_t *ph) {
+  *pw = (width + MULTIPLE - 1) / MULTIPLE * MULTIPLE;
+  *ph = (height + MULTIPLE - 1) / MULTIPLE * MULTIPLE;
+}
+
+// The maps grow on demand (never shrink): at the padded size P pixels, x and
+// y hold P x 64 halves (every level's c-channel map has at most that), t
+// P x 32, rows P x 64 (a level's 2 x 2 gather, or the doubling product), the
+// skips P/4 x 128, P/16 x 256, P/64 x 512.
+ien_status scunet_reserve(Scunet *s, size_t padded_pixels) {
+  if (padded_pixels <= s->pixels) return IEN_OK;
+  IEN_HIP(hipStreamSynchronize(s->ctx->stream));
+  free_maps(*s);
+  const size_t P = padded_pixels;
+  auto alloc = [](uint16_t **p, size_t halves) { return hipMalloc((void **)p, halves * 2); };
+  hipError_t e = alloc(&s->img, P * 8);
+  if (e == hipSuccess) e = alloc(&s->x, P * DIM);
+  if (e == hipSuccess) e = alloc(&s->y, P * DIM);
+  if (e == hipSuccess) e = alloc(&s->t, P * DIM / 2);
+  if (e == hipSuccess) e = alloc(&s->rows, P * DIM);
+  for (int l = 0; l < 3 && e == hipSuccess; l++) e = alloc(&s->skip[l], (P >> (2 * l + 2)) * (128 << l));
+  if (e == hipSuccess) e = alloc(&s->out16, P * 4);
+  if (e != hipSuccess) {
+    free_maps(*s);
+    return fail(IEN_ERR_GPU, "SCUNet maps for %zu pixels: %s", P, hipGetErrorString(e));
+  }
+  s->pixels = P;
+  return IEN_OK;
+}
+
+// network.rs:262-354 run: d_image (f32 height x width x 3) to d_out (the
+// same shape); maps reserved for the padded size.
+ien_status scunet_enqueue(Scunet *s, const float *d_image, size_t width, size_t height,
+                          float *d_out, hipEvent_t *events) {
+  ien_ctx *ctx = s->ctx;
+  size_t pw, ph;
+  scunet_padded(width, height, &pw, &ph);
+  ien_status st = ien_pad_image(ctx, IEN_PAD_REPLICATE, d_image, nullptr, width, height,
+                                MULTIPLE, s->img, 8);
+  if (st != IEN_OK) return st;
+  int h = (int)ph, w = (int)pw, c = DIM, step = 0;
+  // The head (no bias); computed again at the end as the skip into the tail.
+  if ((st = conv3(ctx, s->img, h, w, 3, 8, s->head, s->x, DIM, IEN_ACT_NONE, 0)) != IEN_OK) return st;
+  for (int l = 0; l < 3; l++) {
+    if ((st = run_level(*s, s->down[l], h, w, c, events, &step)) != IEN_OK) return st;
+    // network.rs:403-437 halved, kept as the skip of the level up.
+    if ((st = ien_gather_2x2(ctx, s->x, h, w, c, c, IEN_ORDER_ROW_MAJOR, s->rows)) != IEN_OK)
+      return st;
+    const size_t q = (size_t)(h / 2) * (w / 2);
+    if ((st = rows_product(ctx, s->rows, 4 * c, q, s->halve[l], s->skip[l], 2 * c, 0)) != IEN_OK)
+      return st;
+    h /= 2;
+    w /= 2;
+    c *= 2;
+    IEN_HIP(hipMemcpyAsync(s->x, s->skip[l], q * c * 2, hipMemcpyDeviceToDevice, ctx->stream));
+  }
+  if ((st = run_level(*s, s->body, h, w, c, events, &step)) != IEN_OK) return st;
+  for (int l = 0; l < 3; l++) {
+    const size_t pixels = (size_t)h * w;
+    if ((st = ien_add(ctx, s->x, s->skip[2 - l], pixels * c)) != IEN_OK) return st;
+    // network.rs:439-478 doubled.
+    if ((st = rows_product(ctx, s->x, c, pixels, s->dbl[l], s->rows, 2 * c, 0)) != IEN_OK) return st;
+    if ((st = ien_scatter_2x2(ctx, s->rows, 2 * c, h, w, c / 2, s->x, c / 2)) != IEN_OK) return st;
+    h *= 2;
+    w *= 2;
+    c /= 2;
+    if ((st = run_level(*s, s->up[l], h, w, c, events, &step)) != IEN_OK) return st;
+  }
+  if ((st = conv3(ctx, s->img, h, w, 3, 8, s->head, s->x, DIM, IEN_ACT_NONE, 1)) != IEN_OK) return st;
+  if ((st = conv3(ctx, s->x, h, w, DIM, DIM, s->tail, s->out16, 4, IEN_ACT_NONE, 0)) != IEN_OK)
+    return st;
+  return ien_crop(ctx, s->out16, pw, 4, width, height, 3, d_out);
+}
+
+}  // namespace ien

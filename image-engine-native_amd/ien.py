@@ -21,7 +21,7 @@ INPUT_ROWS, INPUT_IMAGE = 0, 1
 NHWC, NCHW = 0, 1
 ACT_NONE, ACT_RELU, ACT_GELU, ACT_PRELU, ACT_SIGMOID = range(5)
 OUT_F16, OUT_F32 = 0, 1
-MODEL_REALESRGAN = 0
+MODEL_REALESRGAN, MODEL_SCUNET = 0, 1
 
 # Every symbol include/ien_hip.h declares.
 EXPORTS = (
@@ -34,7 +34,7 @@ EXPORTS = (
     "ien_model_run_device", "ien_model_set_graph",
     "ien_window_count", "ien_position_bias", "ien_bias_tables", "ien_window_gather",
     "ien_window_attention", "ien_window_scatter_add", "ien_swin_new", "ien_swin_free", "ien_swin_run",
-    "ien_resize", "ien_pad_image", "ien_crop",
+    "ien_resize", "ien_pad_image", "ien_crop", "ien_gather_2x2", "ien_scatter_2x2", "ien_add",
 )
 
 
@@ -46,6 +46,7 @@ class Windows(ctypes.Structure):
 
 POS_SCUNET, POS_SWIN = 0, 1
 PAD_REPLICATE, PAD_SYMMETRIC_MASKED = 0, 1
+ORDER_ROW_MAJOR, ORDER_COLUMN_MAJOR = 0, 1
 
 
 class SwinWeights(ctypes.Structure):
@@ -162,6 +163,9 @@ def load():
         L.ien_resize.argtypes = [vp, vp, sz, sz, sz, sz, vp, sz, sz, sz, i, i]
         L.ien_pad_image.argtypes = [vp, i, vp, vp, sz, sz, sz, vp, sz]
         L.ien_crop.argtypes = [vp, vp, sz, sz, sz, sz, sz, vp]
+        L.ien_gather_2x2.argtypes = [vp, vp, sz, sz, sz, sz, i, vp]
+        L.ien_scatter_2x2.argtypes = [vp, vp, sz, sz, sz, sz, vp, sz]
+        L.ien_add.argtypes = [vp, vp, vp, sz]
         for name in EXPORTS:
             getattr(L, name)
         _lib = L
@@ -383,6 +387,18 @@ def crop(ctx, map_, map_width, stride, width, height, channels, out):
     check(load().ien_crop(ctx.h, _ptr(map_), map_width, stride, width, height, channels, _ptr(out)))
 
 
+def gather_2x2(ctx, map_, height, width, c, stride, order, rows):
+    check(load().ien_gather_2x2(ctx.h, _ptr(map_), height, width, c, stride, order, _ptr(rows)))
+
+
+def scatter_2x2(ctx, rows, row_stride, height, width, c, map_, stride):
+    check(load().ien_scatter_2x2(ctx.h, _ptr(rows), row_stride, height, width, c, _ptr(map_), stride))
+
+
+def add(ctx, x, y):
+    check(load().ien_add(ctx.h, _ptr(x), _ptr(y), x.numel()))
+
+
 class Swin:
     """ien_swin: one Swin transformer block (attend then MLP, in place).
     `weights`: dict of host arrays ln1_gamma, ln1_beta, qkv_w (c x 3c),
@@ -421,6 +437,7 @@ class Model:
     def __init__(self, ctx, kind, tensors=None, path=None):
         import numpy as np
 
+        self.kind = kind
         L = load()
         h = ctypes.c_void_p()
         if path is not None:
@@ -454,12 +471,14 @@ class Model:
         check(load().ien_model_set_graph(self.h, int(enabled)))
 
     def run(self, image, progress=None):
-        """Host f32 H x W x 3 in, host f32 4H x 4W x 3 out (Model::run_float)."""
+        """Host f32 H x W x 3 in, host f32 out (Model::run_float): 4H x 4W x 3
+        for Real-ESRGAN, H x W x 3 for SCUNet."""
         import numpy as np
 
         image = np.ascontiguousarray(image, dtype=np.float32)
         h, w, _ = image.shape
-        out = np.empty((4 * h, 4 * w, 3), np.float32)
+        s = 4 if self.kind == MODEL_REALESRGAN else 1
+        out = np.empty((s * h, s * w, 3), np.float32)
         cb = PROGRESS(progress) if progress else None
         check(load().ien_model_run(self.h, image.ctypes.data_as(ctypes.c_void_p), None, w, h,
                                    out.ctypes.data_as(ctypes.c_void_p),

@@ -8,6 +8,15 @@ as torch.nn.init.kaiming_normal_), biases uniform in +-1/sqrt(fan_in)
 (torch's Conv2d default), PReLU slopes 0.25 (torch's PReLU default); the
 weights file layout of tools/realesrgan/export_weights.py:48-56 (conv
 [o, i, kh, kw] -> [(kh, kw, i), o]).
+
+SCUNet (crates/scunet-native/src/network.rs, swin.rs): the tensor names and
+[k, n] layouts of tools/scunet/export_weights.py (convolutions [(kh, kw, i),
+o], position biases gathered to [heads, 64, 64]).  The configuration's init
+is trunc-normal with std 0.02 for every weight and position table (at that
+std the +-2 cut is never reached: plain N(0, 0.02^2)), zero biases,
+LayerNorm gamma 1 and beta 0.  Parity tests use a fan-in-scaled init instead
+(N(0, 1 / fan_in) weights, small random biases and norms) so that
+activations do not vanish through the network.
 """
 
 import numpy as np
@@ -71,3 +80,79 @@ def sweep_case(name, seed=INPUT_SEED):
         wt = wrng.standard_normal((size * size, cin)).astype(np.float16).astype(np.float32)
     bias = wrng.standard_normal(cout).astype(np.float32)
     return entry, x, wt, bias
+
+
+# ---- SCUNet ------------------------------------------------------------------
+SCUNET_DIM, SCUNET_BLOCKS, SCUNET_WINDOW = 64, 4, 8
+RESIDUAL_GAIN = 0.2
+
+
+def _scunet_block(name, c):
+    h = c // 2
+    t = f"{name}.trans_block"
+    return [(f"{name}.conv1_1.weight", (c, c)), (f"{name}.conv1_1.bias", (c,)),
+            (f"{name}.conv_block.0.weight", (9 * h, h)), (f"{name}.conv_block.2.weight", (9 * h, h)),
+            (f"{t}.ln1.weight", (h,)), (f"{t}.ln1.bias", (h,)),
+            (f"{t}.msa.embedding_layer.weight", (h, 3 * h)), (f"{t}.msa.embedding_layer.bias", (3 * h,)),
+            (f"{t}.msa.position_bias", (h // 32, 64, 64)),
+            (f"{t}.msa.linear.weight", (h, h)), (f"{t}.msa.linear.bias", (h,)),
+            (f"{t}.ln2.weight", (h,)), (f"{t}.ln2.bias", (h,)),
+            (f"{t}.mlp.0.weight", (h, 4 * h)), (f"{t}.mlp.0.bias", (4 * h,)),
+            (f"{t}.mlp.2.weight", (4 * h, h)), (f"{t}.mlp.2.bias", (h,)),
+            (f"{name}.conv1_2.weight", (c, c)), (f"{name}.conv1_2.bias", (c,))]
+
+
+def scunet_names():
+    """(name, shape) of the 540 tensors, in the order the network consumes
+    them (the oracle's or_scunet_run order)."""
+    out = [("m_head.0.weight", (27, SCUNET_DIM))]
+    for i, c in ((1, 64), (2, 128), (3, 256)):
+        for b in range(SCUNET_BLOCKS):
+            out += _scunet_block(f"m_down{i}.{b}", c)
+        out.append((f"m_down{i}.{SCUNET_BLOCKS}.weight", (4 * c, 2 * c)))
+    for b in range(SCUNET_BLOCKS):
+        out += _scunet_block(f"m_body.{b}", 512)
+    for i, c in ((3, 256), (2, 128), (1, 64)):
+        out.append((f"m_up{i}.0.weight", (2 * c, 4 * c)))
+        for b in range(SCUNET_BLOCKS):
+            out += _scunet_block(f"m_up{i}.{b + 1}", c)
+    out.append(("m_tail.0.weight", (9 * SCUNET_DIM, 3)))
+    return out
+
+
+def scunet_tensors(seed=WEIGHT_SEED, init="trunc_normal"):
+    """name -> array for every SCUNet tensor.  init: "trunc_normal" (the
+    configuration's std 0.02) or "fan" (N(0, 1/fan_in) weights, for parity
+    tests)."""
+    rng = np.random.default_rng(seed)
+    out = {}
+    for name, shape in scunet_names():
+        last = name.rsplit(".", 1)[-1]
+        is_norm = ".ln1." in name or ".ln2." in name
+        if init == "trunc_normal":
+            if is_norm:
+                v = np.ones(shape) if last == "weight" else np.zeros(shape)
+            elif last == "bias":
+                v = np.zeros(shape)
+            else:
+                v = 0.02 * rng.standard_normal(shape)
+        else:
+            if is_norm:
+                v = (1 + 0.1 * rng.standard_normal(shape)) if last == "weight" else 0.1 * rng.standard_normal(shape)
+            elif last == "bias":
+                v = 0.05 * rng.standard_normal(shape)
+            elif last == "position_bias":
+                v = rng.standard_normal(shape)
+            else:
+                v = rng.standard_normal(shape) / np.sqrt(shape[0])
+                # Matrices whose output is added onto a residual stream get a
+                # small gain, so the 28 residual blocks keep activations O(1).
+                if any(k in name for k in ("conv_block.2", "msa.linear", "mlp.2", "conv1_2")):
+                    v *= RESIDUAL_GAIN
+        out[name] = np.asarray(v, np.float32)
+    return out
+
+
+def scunet_image(height=512, width=768, seed=INPUT_SEED):
+    """H x W x 3 RGB, uniform [0, 1)."""
+    return np.random.default_rng(seed).random((height, width, 3), dtype=np.float32)

@@ -208,6 +208,29 @@ ien_status ien_pad_image(ien_ctx *ctx, ien_pad_mode mode, const float *d_image,
 ien_status ien_crop(ien_ctx *ctx, const uint16_t *d_map, size_t map_width, size_t stride,
                     size_t width, size_t height, size_t channels, float *d_out);
 
+/* 2 x 2 space-to-depth: row (y, x) of `d_rows` (row stride 4c) holds the
+ * 2 x 2 input pixels of output pixel (y, x) of the (height / 2) x
+ * (width / 2) grid, c channels each, in IEN_ORDER_ROW_MAJOR ((0,0), (0,1),
+ * (1,0), (1,1) by (dy, dx): scunet-native network.rs:403-437 halved) or
+ * IEN_ORDER_COLUMN_MAJOR ((0,0), (1,0), (0,1), (1,1): birefnet-native
+ * swin.rs:372-392 merge).  The map is f16 NHWC, pixel stride `stride`;
+ * height and width even, c a multiple of 8. */
+typedef enum { IEN_ORDER_ROW_MAJOR = 0, IEN_ORDER_COLUMN_MAJOR = 1 } ien_order;
+ien_status ien_gather_2x2(ien_ctx *ctx, const uint16_t *d_map, size_t height, size_t width,
+                          size_t c, size_t stride, ien_order order, uint16_t *d_rows);
+
+/* Its inverse for a transposed 2 x 2 stride-2 convolution (scunet-native
+ * network.rs:439-478 doubled): input pixel (y, x) of the height x width grid
+ * gives output pixels (2y + dy, 2x + dx) of the map, channels = columns
+ * (2 dy + dx) c .. of its row in d_rows (row stride `row_stride`); the map
+ * is f16 NHWC, (2 height) x (2 width), pixel stride `stride`. */
+ien_status ien_scatter_2x2(ien_ctx *ctx, const uint16_t *d_rows, size_t row_stride,
+                           size_t height, size_t width, size_t c, uint16_t *d_map,
+                           size_t stride);
+
+/* x += y over n f16 values (scunet-native network.rs:380-391 add). */
+ien_status ien_add(ien_ctx *ctx, uint16_t *d_x, const uint16_t *d_y, size_t n);
+
 /* ---- Swin window attention: scunet-native/src/swin.rs,
  *      birefnet-native/src/swin.rs, native-engine attention.rs ---------- */
 
@@ -294,11 +317,12 @@ void ien_swin_free(ien_swin *block);
 ien_status ien_swin_run(ien_swin *block, uint16_t *d_map, size_t stride, int height, int width);
 
 /* ---- models: crates/<model>-native/src/lib.rs Model ------------------- */
-typedef enum { IEN_MODEL_REALESRGAN = 0 } ien_model_kind;
+typedef enum { IEN_MODEL_REALESRGAN = 0, IEN_MODEL_SCUNET = 1 } ien_model_kind;
 
-/* Model::load (realesrgan-native lib.rs:120-137 with the GPU engine): read
- * the weights file (weight_file.rs format, magic b"REALESRG"), check every
- * tensor, upload once. */
+/* Model::load (realesrgan-native lib.rs:120-137, scunet-native
+ * lib.rs:79-111, with the GPU engine): read the weights file (weight_file.rs
+ * format, magic b"REALESRG" or b"SCUNET\0\0"), check every tensor, upload
+ * once. */
 ien_status ien_model_load(ien_ctx *ctx, ien_model_kind kind, const char *weights_path,
                           ien_model **out);
 /* The same from weights already in memory: `tensors` name/shape/value
@@ -313,13 +337,15 @@ ien_status ien_model_from_tensors(ien_ctx *ctx, ien_model_kind kind, const ien_t
                                   size_t count, ien_model **out);
 void ien_model_free(ien_model *model);
 
-/* Progress callback: share done in 0..1, after each layer; nonzero return
- * cancels the run with IEN_ERR_CANCELLED (lib.rs:168-188). */
+/* Progress callback: share done in 0..1, after each layer (Real-ESRGAN, 34)
+ * or block (SCUNet, 28); nonzero return cancels the run with
+ * IEN_ERR_CANCELLED (realesrgan lib.rs:168-188, scunet lib.rs:205-215). */
 typedef int (*ien_progress)(float done, void *user);
 
-/* Model::run_float (realesrgan-native lib.rs:194-214): host f32 NHWC image
- * of width x height x 3 in [0, 1], host f32 output (4h x 4w x 3).  `mask` is
- * for LaMa and NULL otherwise. */
+/* Model::run_float (realesrgan-native lib.rs:194-214, scunet-native
+ * lib.rs:151-171): host f32 NHWC image of width x height x 3 in [0, 1], host
+ * f32 output (Real-ESRGAN 4h x 4w x 3, SCUNet h x w x 3).  `mask` is for LaMa
+ * and NULL otherwise. */
 ien_status ien_model_run(ien_model *model, const float *image, const float *mask, size_t width,
                          size_t height, float *out, ien_progress progress, void *user);
 

@@ -116,6 +116,19 @@ void or_swin_mlp(int threads, float *map, size_t stride, size_t rows, size_t c,
                  const float *gamma, const float *beta, const float *w1, const float *b1,
                  const float *w2, const float *b2);
 
+/* ---- scunet-native network.rs ----------------------------------------- */
+/* network.rs:262-354 run: the RGB image (height x width x 3, values 0..1)
+ * through the U-Net, out height x width x 3.  `t` holds 540 tensors in
+ * this order: head [27][64]; per level down (64, 128, 256 channels) four
+ * blocks then the halving matrix [4c][2c]; the body's four blocks (512);
+ * per level up (256, 128, 64) the doubling matrix [2c][4c] then four blocks;
+ * the tail [576][3].  A block of c channels (h = c / 2): split [c][c], [c];
+ * conv1 [9h][h]; conv2 [9h][h]; ln1 [h], [h]; qkv [h][3h], [3h]; position
+ * bias [h/32][64][64]; proj [h][h], [h]; ln2 [h], [h]; fc1 [h][4h], [4h];
+ * fc2 [4h][h], [h]; join [c][c], [c]. */
+int or_scunet_run(int threads, const float *const *t, const float *image, size_t width,
+                  size_t height, float *out);
+
 /* ---- realesrgan-native network.rs ------------------------------------- */
 /* network.rs:80-141: 34 conv3 layers (PReLU on all but the last), then the
  * x4 pixel shuffle plus the input repeated.  w[i] is 9cin x cout row-major

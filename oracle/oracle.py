@@ -83,6 +83,8 @@ def lib():
         L.or_window_class.argtypes = [sz, sz, sz, sz, sz]
         L.or_swin_attend.argtypes = [ctypes.c_int, vp, sz, sz, sz, sz, sz, sz, vp, vp, vp, vp, vp, vp, vp]
         L.or_swin_mlp.argtypes = [ctypes.c_int, vp, sz, sz, sz, vp, vp, vp, vp, vp, vp]
+        L.or_scunet_run.restype = ctypes.c_int
+        L.or_scunet_run.argtypes = [ctypes.c_int, vp, vp, sz, sz, vp]
         L.or_realesrgan_run.restype = ctypes.c_int
         L.or_realesrgan_run.argtypes = [ctypes.c_int, vp, vp, vp, vp, sz, sz, vp]
         L.or_pixel_shuffle_add.argtypes = [vp, vp, sz, sz, vp]
@@ -348,4 +350,19 @@ def masked_rows(image, mask, multiple):
     ph, pw = -(-h // multiple) * multiple, -(-w // multiple) * multiple
     out = np.zeros((ph, pw, 4), np.float32)
     lib().or_masked_rows(_p(image), _p(mask), w, h, multiple, _p(out))
+    return out
+
+
+# ---- scunet-native -----------------------------------------------------------
+def scunet_run(tensors, names, image, threads=None):
+    """tensors: name -> array; names: the canonical order (synthetic.scunet_names)."""
+    image = _f32(image)
+    h, w, _ = image.shape
+    arrs = [_f32(tensors[n]) for n, _ in names]
+    ptrs = (ctypes.c_void_p * len(arrs))(*[a.ctypes.data for a in arrs])
+    out = np.zeros((h, w, 3), np.float32)
+    rc = lib().or_scunet_run(threads or threads_default(), ctypes.cast(ptrs, ctypes.c_void_p), _p(image), w, h,
+                             _p(out))
+    if rc != 0:
+        raise RuntimeError(f"or_scunet_run: {rc}")
     return out
