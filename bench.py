@@ -37,6 +37,7 @@ sys.path.insert(0, str(ROOT / "image-engine-native_amd"))
 
 MFMA_F16_PEAK_TFLOPS = 2516.6  # MI355X dense f16 MFMA
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+SCUNET_GFLOP = 944.9           # 1x3x512x768, incl. 46.7 GFLOP of window attention
 METRIC = "ms/image at 1 MI355X per model; conv/attn GEMM MFMA util % of f16 peak"
 
 
@@ -189,6 +190,36 @@ def traffic_probe(ctx, tensors, H, W):
     print("traffic probe: body layer x10, then a 134217728-byte copy", flush=True)
 
 
+def scunet_leg(ctx, steps, warmup):
+    """SCUNet (configuration 3) at 1 x 3 x 512 x 768 with its trunc-normal
+    random-init weights, graph replay, input and output in HBM."""
+    import torch
+
+    import ien
+    import synthetic
+
+    h, w = 512, 768
+    model = ien.Model(ctx, ien.MODEL_SCUNET, tensors=synthetic.scunet_tensors())
+    d_in = torch.from_numpy(synthetic.scunet_image(h, w)).cuda()
+    d_out = torch.empty((h, w, 3), dtype=torch.float32, device="cuda")
+    model.set_graph(True)
+    for _ in range(warmup):
+        model.run_device(d_in, w, h, d_out)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        model.run_device(d_in, w, h, d_out)
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    ok = bool(torch.isfinite(d_out).all())
+    model.free()
+    if not ok:
+        sys.exit("SCUNet: non-finite output")
+    return {"workload": "SCUNet 1x3x512x768 (28 Swin-Conv blocks, 64/128/256/512)", "ms_per_image": round(ms, 3),
+            "images_per_s": round(1e3 / ms, 2), "gflop_per_image": SCUNET_GFLOP,
+            "tflops": round(SCUNET_GFLOP / ms, 1)}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -197,6 +228,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-sweep", action="store_true", help="skip the conv sweep")
     ap.add_argument("--kernel-reps", type=int, default=100)
+    ap.add_argument("--no-models", action="store_true", help="skip the other models (SCUNet)")
+    ap.add_argument("--scunet-only", action="store_true",
+                    help="only the SCUNet leg (the workload of its kernel profile)")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="only run the dominant layer 10 times and a 128 MiB device copy "
                          "(the workload of the FETCH_SIZE / WRITE_SIZE counter passes)")
@@ -221,6 +255,9 @@ def main():
     tensors = synthetic.esrgan_tensors()
     if args.traffic_probe:
         traffic_probe(ctx, tensors, H, W)
+        return
+    if args.scunet_only:
+        print(json.dumps(scunet_leg(ctx, max(1, args.steps // 10), 2)), flush=True)
         return
     image = synthetic.esrgan_image(H, W)
     model = ien.Model(ctx, ien.MODEL_REALESRGAN, tensors=tensors)
@@ -255,6 +292,7 @@ def main():
     body_free()
 
     gemm_sweep = None if args.no_sweep else sweep(ctx, stream, args.kernel_reps)
+    models = None if args.no_models else {"scunet": scunet_leg(ctx, max(5, args.steps // 20), 2)}
     cpu = None if args.no_cpu else cpu_baseline(tensors, image)
 
     line = {
@@ -277,6 +315,7 @@ def main():
         "roofline": roofline,
         "cpu_baseline": cpu,
         "gemm_sweep": gemm_sweep,
+        "models": models,
         "device": ctx.name,
     }
     model.free()

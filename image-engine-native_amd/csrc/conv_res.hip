@@ -214,7 +214,9 @@ __global__ __launch_bounds__(512) void conv_res8(ConvArgs a) {
   };
 
   // Accumulating, NCHW or ragged outputs: the staged sums (bias included,
-  // no activation when accumulating) element by element.
+  // no activation when accumulating) by whole 16-byte chunks where the
+  // output is f16 NHWC with 8-aligned rows, else element by element.
+  const bool vec8 = !a.out_f32 && !a.out_nchw && a.ys % 8 == 0 && (((uintptr_t)a.y) & 15) == 0;
   auto store_slow = [&](int mts, const unsigned char *stage) {
     int oy0, ox0;
     origin(mts, oy0, ox0);
@@ -228,6 +230,20 @@ __global__ __launch_bounds__(512) void conv_res8(ConvArgs a) {
       u32x4 hv = *(const u32x4 *)(stage + (tp * R::SPX + chunk * 8) * 2);
       uint16_t h[8];
       __builtin_memcpy(h, &hv, 16);
+      if (vec8 && n0 + 8 <= a.N) {
+        u32x4 *yv = (u32x4 *)((uint16_t *)a.y + (long)rel * a.ys + n0);
+        if (a.accumulate) {
+          const u32x4 ov = *yv;
+          uint16_t oh[8];
+          __builtin_memcpy(oh, &ov, 16);
+#pragma unroll
+          for (int e = 0; e < 8; e++)
+            h[e] = f2h(activate(h2f(h[e]) + h2f(oh[e]), a.act, slope_l[chunk * 8 + e]));
+          __builtin_memcpy(&hv, h, 16);
+        }
+        *yv = hv;
+        continue;
+      }
       for (int e = 0; e < 8 && n0 + e < a.N; e++) {
         const long at = a.out_nchw ? (long)(n0 + e) * a.ys + rel : (long)rel * a.ys + n0 + e;
         float o = h2f(h[e]);

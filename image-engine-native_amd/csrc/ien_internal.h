@@ -93,4 +93,7 @@ struct ConvCall {
 
 ien_status launch_conv(ien_ctx *ctx, const ConvCall &c);
 
+// swin.hip: a block's scratch grown for a height x width map in advance.
+ien_status swin_reserve(ien_swin *b, int height, int width);
+
 }  // namespace ien

@@ -270,7 +270,7 @@ static ien_status prepare(ien_model *model, size_t width, size_t height) {
     size_t pw, ph;
     scunet_padded(width, height, &pw, &ph);
     const size_t before = model->scunet->pixels;
-    ien_status st = scunet_reserve(model->scunet.get(), pw * ph);
+    ien_status st = scunet_reserve(model->scunet.get(), pw, ph);
     if (st == IEN_OK && model->scunet->pixels != before) drop_graph(model);
     return st;
   }

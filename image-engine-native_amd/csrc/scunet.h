@@ -35,7 +35,9 @@ constexpr int SCUNET_STEPS = 28;  // blocks of a run (network.rs:27-31)
 ien_status scunet_load(ien_ctx *ctx, const TensorSource &take, Scunet *s);
 void scunet_free(Scunet *s);
 void scunet_padded(size_t width, size_t height, size_t *pw, size_t *ph);
-ien_status scunet_reserve(Scunet *s, size_t padded_pixels);
+// Maps and every block's scratch for a padded pw x ph image (outside graph
+// capture).
+ien_status scunet_reserve(Scunet *s, size_t pw, size_t ph);
 ien_status scunet_enqueue(Scunet *s, const float *d_image, size_t width, size_t height,
                           float *d_out, hipEvent_t *events);
 

@@ -202,7 +202,21 @@ void scunet_padded(size_t width, size_t height, size_t *pw, size_t *ph) {
 // y hold P x 64 halves (every level's c-channel map has at most that), t
 // P x 32, rows P x 64 (a level's 2 x 2 gather, or the doubling product), the
 // skips P/4 x 128, P/16 x 256, P/64 x 512.
-ien_status scunet_reserve(Scunet *s, size_t padded_pixels) {
+ien_status scunet_reserve(Scunet *s, size_t pw, size_t ph) {
+  // Each level's blocks: down l at 1 / 2^l, the body at 1 / 8, up l at
+  // 1 / 2^(2 - l).
+  for (int l = 0; l < 3; l++)
+    for (int b = 0; b < BLOCKS; b++) {
+      ien_status st = swin_reserve(s->down[l][b].swin, (int)(ph >> l), (int)(pw >> l));
+      if (st == IEN_OK)
+        st = swin_reserve(s->up[l][b].swin, (int)(ph >> (2 - l)), (int)(pw >> (2 - l)));
+      if (st != IEN_OK) return st;
+    }
+  for (int b = 0; b < BLOCKS; b++) {
+    ien_status st = swin_reserve(s->body[b].swin, (int)(ph >> 3), (int)(pw >> 3));
+    if (st != IEN_OK) return st;
+  }
+  const size_t padded_pixels = pw * ph;
   if (padded_pixels <= s->pixels) return IEN_OK;
   IEN_HIP(hipStreamSynchronize(s->ctx->stream));
   free_maps(*s);

@@ -38,6 +38,11 @@ void release(ien_swin *b) {
 // still use the old buffers).
 ien_status reserve(ien_swin *b, size_t rows) {
   if (rows <= b->rows) return IEN_OK;
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  IEN_HIP(hipStreamIsCapturing(b->ctx->stream, &cap));
+  IEN_CHECK(cap == hipStreamCaptureStatusNone, IEN_ERR_INPUT,
+            "swin block scratch must grow to %zu rows while the stream is capturing; "
+            "reserve it before capture", rows);
   IEN_HIP(hipStreamSynchronize(b->ctx->stream));
   (void)hipFree(b->d_wide);
   (void)hipFree(b->d_tok);
@@ -68,6 +73,21 @@ ien_status rows_product(ien_ctx *ctx, const uint16_t *in, size_t k, size_t rows,
 }
 
 }  // namespace
+
+namespace ien {
+
+// Scratch for a height x width map ahead of time (outside any graph
+// capture: growing drains the stream).
+ien_status swin_reserve(ien_swin *b, int height, int width) {
+  IEN_CHECK(b, IEN_ERR_INPUT, "no block");
+  ien_windows w{b->window, b->shift, height, width};
+  const long wins = ien_window_count(&w);
+  IEN_CHECK(wins > 0, IEN_ERR_INPUT, "map %d x %d", height, width);
+  const size_t rows = (size_t)wins * b->window * b->window, tokens = (size_t)height * width;
+  return reserve(b, rows > tokens ? rows : tokens);
+}
+
+}  // namespace ien
 
 using namespace ien;
 

@@ -53,31 +53,35 @@ __device__ __forceinline__ u32x4 pack8(const float *v) {
   return raw;
 }
 
-// One wave per window row: gather, LayerNorm (mean, then the mean square
-// deviation, eps 1e-5: math.rs:95-116), or a zero row past the edge.  Each
-// lane holds up to two 8-channel chunks (c <= 1024).
+// L lanes per window row (the row's 8-channel chunks rounded up to a power
+// of two, at most 64), 64 / L rows per wave: gather, LayerNorm (mean, then
+// the mean square deviation, eps 1e-5: math.rs:95-116), or a zero row past
+// the edge.  A lane holds one 8-channel chunk, two when L = 64 and c > 512
+// (c <= 1024).  The reductions stay inside the row's aligned lane group.
+template <int L>
 __global__ __launch_bounds__(256) void k_window_gather(WinGeo g, const uint16_t *__restrict__ map,
                                                        long stride, int c,
                                                        const float *__restrict__ gamma,
                                                        const float *__restrict__ beta,
                                                        uint16_t *__restrict__ tokens) {
-  const int lane = threadIdx.x & 63;
-  const long row = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= g.windows * g.n) return;
+  constexpr int Q = L == 64 ? 2 : 1;
+  const int sub = threadIdx.x & (L - 1);
+  const long row = ((long)blockIdx.x * 256 + threadIdx.x) / L;
+  if (row >= g.windows * g.n) return;  // whole lane groups leave together
   const long src = win_source(g, row / g.n, (int)(row % g.n));
   uint16_t *dst = tokens + row * c;
   const int chunks = c >> 3;
   if (src < 0) {
     const u32x4 zero = {0u, 0u, 0u, 0u};
-    for (int k = lane; k < chunks; k += 64) *(u32x4 *)(dst + 8 * k) = zero;
+    for (int k = sub; k < chunks; k += L) *(u32x4 *)(dst + 8 * k) = zero;
     return;
   }
   const uint16_t *s = map + src * stride;
-  float v[16];
+  float v[8 * Q];
   float sum = 0.0f;
 #pragma unroll
-  for (int q = 0; q < 2; q++) {
-    const int k = lane + 64 * q;
+  for (int q = 0; q < Q; q++) {
+    const int k = sub + L * q;
     if (k < chunks) {
       unpack8(*(const u32x4 *)(s + 8 * k), v + 8 * q);
     } else {
@@ -87,12 +91,13 @@ __global__ __launch_bounds__(256) void k_window_gather(WinGeo g, const uint16_t 
 #pragma unroll
     for (int e = 0; e < 8; e++) sum += v[8 * q + e];
   }
-  for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
+#pragma unroll
+  for (int off = L / 2; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
   const float mean = sum / (float)c;
   float sq = 0.0f;
 #pragma unroll
-  for (int q = 0; q < 2; q++) {
-    if (lane + 64 * q < chunks) {
+  for (int q = 0; q < Q; q++) {
+    if (sub + L * q < chunks) {
 #pragma unroll
       for (int e = 0; e < 8; e++) {
         const float d = v[8 * q + e] - mean;
@@ -100,16 +105,20 @@ __global__ __launch_bounds__(256) void k_window_gather(WinGeo g, const uint16_t 
       }
     }
   }
-  for (int off = 32; off > 0; off >>= 1) sq += __shfl_xor(sq, off);
+#pragma unroll
+  for (int off = L / 2; off > 0; off >>= 1) sq += __shfl_xor(sq, off);
   const float inv = 1.0f / sqrtf(sq / (float)c + 1e-5f);
 #pragma unroll
-  for (int q = 0; q < 2; q++) {
-    const int k = lane + 64 * q;
+  for (int q = 0; q < Q; q++) {
+    const int k = sub + L * q;
     if (k < chunks) {
+      const float4 g0 = *(const float4 *)(gamma + 8 * k), g1 = *(const float4 *)(gamma + 8 * k + 4);
+      const float4 b0 = *(const float4 *)(beta + 8 * k), b1 = *(const float4 *)(beta + 8 * k + 4);
+      const float gg[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+      const float bb[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
       float o[8];
 #pragma unroll
-      for (int e = 0; e < 8; e++)
-        o[e] = (v[8 * q + e] - mean) * inv * gamma[8 * k + e] + beta[8 * k + e];
+      for (int e = 0; e < 8; e++) o[e] = (v[8 * q + e] - mean) * inv * gg[e] + bb[e];
       *(u32x4 *)(dst + 8 * k) = pack8(o);
     }
   }
@@ -344,9 +353,27 @@ ien_status ien_window_gather(ien_ctx *ctx, const ien_windows *w, const uint16_t 
   IEN_CHECK(c >= 8 && c <= 1024 && c % 8 == 0, IEN_ERR_INPUT, "%d channels (8 .. 1024, by 8)", c);
   IEN_CHECK(stride >= (size_t)c && stride % 8 == 0 && aligned16(d_map) && aligned16(d_tokens),
             IEN_ERR_INPUT, "map stride %zu / alignment (16-byte rows)", stride);
+  IEN_CHECK(((uintptr_t)d_gamma & 15) == 0 && ((uintptr_t)d_beta & 15) == 0, IEN_ERR_INPUT,
+            "LayerNorm parameters must be 16-byte aligned");
   const long rows = g.windows * g.n;
-  hipLaunchKernelGGL(k_window_gather, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, ctx->stream,
-                     g, d_map, (long)stride, c, d_gamma, d_beta, d_tokens);
+  const int chunks = c / 8;
+  int lanes = 1;
+  while (lanes < chunks && lanes < 64) lanes *= 2;
+  const long threads = rows * lanes;
+  IEN_CHECK((threads + 255) / 256 < (1L << 31), IEN_ERR_INPUT, "%ld rows", rows);
+  void (*k)(WinGeo, const uint16_t *, long, int, const float *, const float *, uint16_t *) =
+      nullptr;
+  switch (lanes) {
+    case 1: k = k_window_gather<1>; break;
+    case 2: k = k_window_gather<2>; break;
+    case 4: k = k_window_gather<4>; break;
+    case 8: k = k_window_gather<8>; break;
+    case 16: k = k_window_gather<16>; break;
+    case 32: k = k_window_gather<32>; break;
+    default: k = k_window_gather<64>; break;
+  }
+  hipLaunchKernelGGL(k, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, ctx->stream, g,
+                     d_map, (long)stride, c, d_gamma, d_beta, d_tokens);
   IEN_HIP(hipGetLastError());
   return IEN_OK;
 }

@@ -268,7 +268,8 @@ int ien_bias_tables(const float *position, int heads, int window, int shift, flo
  * rows [windows * N][c] (f16) from the map (f16, token t at d_map + t *
  * stride), each LayerNorm'd with gamma, beta (device f32, eps 1e-5,
  * math.rs:95-116); rows past the map's edge are zero (the padding follows
- * the normalisation).  c a multiple of 8, at most 1024. */
+ * the normalisation).  c a multiple of 8, at most 1024; gamma and beta
+ * 16-byte aligned. */
 ien_status ien_window_gather(ien_ctx *ctx, const ien_windows *w, const uint16_t *d_map,
                              size_t stride, int c, const float *d_gamma, const float *d_beta,
                              uint16_t *d_tokens);
