@@ -220,6 +220,51 @@ def scunet_leg(ctx, steps, warmup):
             "tflops": round(SCUNET_GFLOP / ms, 1)}
 
 
+def lama_gflop(h=512, w=512):
+    """Multiply-adds x 2 of Big LaMa's convolutions and products at h x w
+    (the Fourier transforms' own arithmetic not counted)."""
+    p = h * w
+    e = p // 64
+    half = (w // 8) // 2 + 1
+    macs = p * 196 * 64 + (p // 4) * 576 * 128 + (p // 16) * 1152 * 256 + e * 2304 * 512
+    ffc = e * 4608 * 128 + e * 1152 * 384 + e * 384 * 192 + (h // 8) * half * 384 * 384 + e * 192 * 384
+    macs += 36 * ffc
+    macs += e * 9 * 512 * 256 + (p // 16) * 9 * 256 * 128 + (p // 4) * 9 * 128 * 64 + p * 3136 * 3
+    return 2 * macs / 1e9
+
+
+def lama_leg(ctx, steps, warmup):
+    """Big LaMa (configuration 4) at 1 x 4 x 512 x 512 (RGB plus a ~25 %
+    rectangle mask) with He-normal random-init weights, graph replay, inputs
+    and output in HBM."""
+    import torch
+
+    import ien
+    import synthetic
+
+    h, w = 512, 512
+    model = ien.Model(ctx, ien.MODEL_LAMA, tensors=synthetic.lama_tensors())
+    d_in = torch.from_numpy(synthetic.lama_image(h, w)).cuda()
+    d_mask = torch.from_numpy(synthetic.lama_mask(h, w)).cuda()
+    d_out = torch.empty((h, w, 3), dtype=torch.float32, device="cuda")
+    model.set_graph(True)
+    for _ in range(warmup):
+        model.run_device(d_in, w, h, d_out, d_mask=d_mask)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        model.run_device(d_in, w, h, d_out, d_mask=d_mask)
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    ok = bool(torch.isfinite(d_out).all())
+    model.free()
+    if not ok:
+        sys.exit("LaMa: non-finite output")
+    gflop = round(lama_gflop(h, w), 1)
+    return {"workload": "Big LaMa 1x4x512x512 (18 FFC blocks at 64x64x512)", "ms_per_image": round(ms, 3),
+            "images_per_s": round(1e3 / ms, 2), "gflop_per_image": gflop, "tflops": round(gflop / ms, 1)}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -228,7 +273,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-sweep", action="store_true", help="skip the conv sweep")
     ap.add_argument("--kernel-reps", type=int, default=100)
-    ap.add_argument("--no-models", action="store_true", help="skip the other models (SCUNet)")
+    ap.add_argument("--no-models", action="store_true", help="skip the other models (SCUNet, LaMa)")
+    ap.add_argument("--lama-only", action="store_true",
+                    help="only the LaMa leg (the workload of its kernel profile)")
     ap.add_argument("--scunet-only", action="store_true",
                     help="only the SCUNet leg (the workload of its kernel profile)")
     ap.add_argument("--traffic-probe", action="store_true",
@@ -258,6 +305,9 @@ def main():
         return
     if args.scunet_only:
         print(json.dumps(scunet_leg(ctx, max(1, args.steps // 10), 2)), flush=True)
+        return
+    if args.lama_only:
+        print(json.dumps(lama_leg(ctx, max(1, args.steps // 10), 2)), flush=True)
         return
     image = synthetic.esrgan_image(H, W)
     model = ien.Model(ctx, ien.MODEL_REALESRGAN, tensors=tensors)
@@ -292,7 +342,8 @@ def main():
     body_free()
 
     gemm_sweep = None if args.no_sweep else sweep(ctx, stream, args.kernel_reps)
-    models = None if args.no_models else {"scunet": scunet_leg(ctx, max(5, args.steps // 20), 2)}
+    models = None if args.no_models else {"scunet": scunet_leg(ctx, max(5, args.steps // 20), 2),
+                                          "lama": lama_leg(ctx, max(5, args.steps // 20), 2)}
     cpu = None if args.no_cpu else cpu_baseline(tensors, image)
 
     line = {

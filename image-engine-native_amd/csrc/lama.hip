@@ -1,0 +1,323 @@
+// lama.hip -- Big LaMa's generator on the GPU (crates/lama-native/src/
+// network.rs): f16 NHWC maps; every convolution through the implicit-GEMM
+// kernels (7x7 and 3x3 reflect-padded, 3x3 stride 2, the transposed
+// upsamplings as four output-phase products with offset taps, then a 2 x 2
+// scatter); the spectral branch's 1x1 convolutions as products over pixel
+// or spectrum rows around the Fourier units of fourier.hip.  One event is
+// recorded after each of the 26 steps for progress reports.
+
+#include <string>
+
+#include "lama.h"
+
+namespace ien {
+
+namespace {
+
+constexpr int LOCAL = 128, GLOBAL = 384, CHANNELS = 512, SPECTRAL = 192, BLOCKS = 18;
+constexpr int MULTIPLE = 8;
+
+// network.rs:271 PHASE_TAPS: output phase p = 2 py + px reads input offsets
+// (dy, dx) over the taps of py times those of px.
+constexpr int PHASE_COUNT[2] = {1, 2};
+constexpr int PHASE_OFFSET[2][2] = {{0, 0}, {0, 1}};
+
+ien_status matrix(ien_ctx *ctx, const TensorSource &take, const std::string &name, size_t k,
+                  size_t n, bool bias, ien_matrix **out) {
+  std::vector<float> w, b;
+  ien_status st = take(name + ".weight", {k, n}, &w);
+  if (st == IEN_OK && bias) st = take(name + ".bias", {n}, &b);
+  if (st != IEN_OK) return st;
+  return ien_matrix_new(ctx, w.data(), IEN_W_F32, k, n, bias ? b.data() : nullptr, out);
+}
+
+// A size x size convolution (reflect padding) of an h x w f16 NHWC map.
+ien_status conv(ien_ctx *ctx, const uint16_t *x, int h, int w, int c, long xs, int size,
+                int step, const ien_matrix *m, uint16_t *y, long ys, ien_act act,
+                int accumulate) {
+  ConvCall cc;
+  cc.x = x;
+  cc.H = h;
+  cc.W = w;
+  cc.C = c;
+  cc.xs = xs;
+  cc.ks = size;
+  cc.stride = step;
+  cc.pad_reflect = size > 1;
+  cc.OH = (h - 1) / step + 1;
+  cc.OW = (w - 1) / step + 1;
+  cc.row0 = 0;
+  cc.rows = (long)cc.OH * cc.OW;
+  cc.w = m;
+  cc.y = y;
+  cc.ys = ys;
+  cc.act = act;
+  cc.accumulate = accumulate;
+  return launch_conv(ctx, cc);
+}
+
+// out[r] = act((acc ? out[r] : 0) + in[r] m) over `rows` rows of k values.
+ien_status rows_product(ien_ctx *ctx, const uint16_t *in, size_t k, size_t rows,
+                        const ien_matrix *m, uint16_t *out, long ys, ien_act act,
+                        int accumulate) {
+  ConvCall cc;
+  cc.x = in;
+  cc.rows_mode = 1;
+  cc.C = (int)k;
+  cc.xs = (long)k;
+  cc.ks = 1;
+  cc.stride = 1;
+  cc.row0 = 0;
+  cc.rows = (long)rows;
+  cc.w = m;
+  cc.y = out;
+  cc.ys = ys;
+  cc.act = act;
+  cc.accumulate = accumulate;
+  return launch_conv(ctx, cc);
+}
+
+// network.rs:174-249 Ffc::run: out = ffc(x), both h x w maps of 512.
+ien_status ffc_run(Lama *l, const LamaFfc &f, const uint16_t *x, uint16_t *out, int h, int w) {
+  ien_ctx *ctx = l->ctx;
+  const size_t pixels = (size_t)h * w, half = (size_t)w / 2 + 1, spix = (size_t)h * half;
+  // local: all 512 channels -> 128, ReLU.
+  ien_status st = conv(ctx, x, h, w, CHANNELS, CHANNELS, 3, 1, f.local, out, CHANNELS,
+                       IEN_ACT_RELU, 0);
+  // cross: the local part -> the global part, no activation yet.
+  if (st == IEN_OK)
+    st = conv(ctx, x, h, w, LOCAL, CHANNELS, 3, 1, f.cross, out + LOCAL, CHANNELS, IEN_ACT_NONE,
+              0);
+  // spectral_in: 1x1 of the global part -> 192, ReLU.
+  if (st == IEN_OK)
+    st = conv(ctx, x + LOCAL, h, w, GLOBAL, CHANNELS, 1, 1, f.spectral_in, l->spectral, SPECTRAL,
+              IEN_ACT_RELU, 0);
+  if (st == IEN_OK)
+    st = ien_fourier_forward(l->fourier, l->spectral, SPECTRAL, SPECTRAL, l->work, l->spectrum);
+  // fourier: 1x1 over spectrum pixels [re | im] -> the same, ReLU.
+  if (st == IEN_OK)
+    st = rows_product(ctx, l->spectrum, 2 * SPECTRAL, spix, f.fourier, l->filtered,
+                      2 * SPECTRAL, IEN_ACT_RELU, 0);
+  // spectral += irfft(filtered).
+  if (st == IEN_OK)
+    st = ien_fourier_inverse(l->fourier, l->filtered, SPECTRAL, l->work, l->spectral, SPECTRAL);
+  // global = ReLU(cross + spectral_out(spectral)).
+  if (st == IEN_OK)
+    st = rows_product(ctx, l->spectral, SPECTRAL, pixels, f.spectral_out, out + LOCAL, CHANNELS,
+                      IEN_ACT_RELU, 1);
+  return st;
+}
+
+// network.rs:279-335 Up::run: the four phase products into rows of 4 cout
+// values (phase p at columns p cout), then the 2 x 2 scatter into the
+// doubled map.
+ien_status up_run(Lama *l, ien_matrix *const *phases, const uint16_t *x, int h, int w, int cin,
+                  int cout, uint16_t *y) {
+  for (int p = 0; p < 4; p++) {
+    const int py = p / 2, px = p % 2;
+    ConvCall cc;
+    cc.x = x;
+    cc.H = h;
+    cc.W = w;
+    cc.C = cin;
+    cc.xs = cin;
+    cc.noff = 0;
+    for (int a = 0; a < PHASE_COUNT[py]; a++)
+      for (int b = 0; b < PHASE_COUNT[px]; b++) {
+        cc.offy[cc.noff] = PHASE_OFFSET[py][a];
+        cc.offx[cc.noff] = PHASE_OFFSET[px][b];
+        cc.noff++;
+      }
+    cc.ks = 0;
+    cc.stride = 1;
+    cc.OH = h;
+    cc.OW = w;
+    cc.row0 = 0;
+    cc.rows = (long)h * w;
+    cc.w = phases[p];
+    cc.y = l->rows + (size_t)p * cout;
+    cc.ys = 4L * cout;
+    cc.act = IEN_ACT_RELU;
+    ien_status st = launch_conv(l->ctx, cc);
+    if (st != IEN_OK) return st;
+  }
+  return ien_scatter_2x2(l->ctx, l->rows, 4 * (size_t)cout, h, w, cout, y, cout);
+}
+
+void free_maps(Lama &l) {
+  for (uint16_t **p : {&l.in4, &l.m0, &l.m1, &l.m2, &l.a, &l.mid, &l.out, &l.spectral,
+                       &l.spectrum, &l.filtered, &l.rows, &l.rgb}) {
+    (void)hipFree(*p);
+    *p = nullptr;
+  }
+  (void)hipFree(l.work);
+  l.work = nullptr;
+  l.pixels = 0;
+}
+
+}  // namespace
+
+// network.rs:381-413 Network::load (names as tools/lama/export_weights.py
+// writes them).
+ien_status lama_load(ien_ctx *ctx, const TensorSource &take, Lama *l) {
+  l->ctx = ctx;
+  ien_status st = matrix(ctx, take, "first", 49 * 4, 64, true, &l->first);
+  const int dins[3] = {64, 128, 256}, douts[3] = {128, 256, CHANNELS};
+  for (int i = 0; i < 3 && st == IEN_OK; i++)
+    st = matrix(ctx, take, "down" + std::to_string(i), 9 * (size_t)dins[i], douts[i], true,
+                &l->down[i]);
+  for (int b = 0; b < BLOCKS && st == IEN_OK; b++)
+    for (int f = 0; f < 2 && st == IEN_OK; f++) {
+      const std::string n = "block" + std::to_string(b) + ".ffc" + std::to_string(f);
+      LamaFfc &F = l->blocks[b][f];
+      st = matrix(ctx, take, n + ".local", 9 * CHANNELS, LOCAL, true, &F.local);
+      if (st == IEN_OK) st = matrix(ctx, take, n + ".cross", 9 * LOCAL, GLOBAL, true, &F.cross);
+      if (st == IEN_OK)
+        st = matrix(ctx, take, n + ".spectral_in", GLOBAL, SPECTRAL, true, &F.spectral_in);
+      if (st == IEN_OK)
+        st = matrix(ctx, take, n + ".fourier", 2 * SPECTRAL, 2 * SPECTRAL, true, &F.fourier);
+      if (st == IEN_OK)
+        st = matrix(ctx, take, n + ".spectral_out", SPECTRAL, GLOBAL, false, &F.spectral_out);
+    }
+  const int uins[3] = {CHANNELS, 256, 128}, uouts[3] = {256, 128, 64};
+  for (int i = 0; i < 3 && st == IEN_OK; i++)
+    for (int p = 0; p < 4 && st == IEN_OK; p++) {
+      const size_t taps = (size_t)PHASE_COUNT[p / 2] * PHASE_COUNT[p % 2];
+      st = matrix(ctx, take, "up" + std::to_string(i) + ".phase" + std::to_string(p),
+                  taps * uins[i], uouts[i], true, &l->up[i][p]);
+    }
+  if (st == IEN_OK) st = matrix(ctx, take, "last", 49 * 64, 3, true, &l->last);
+  return st;
+}
+
+void lama_free(Lama *l) {
+  ien_matrix_free(l->first);
+  ien_matrix_free(l->last);
+  for (int i = 0; i < 3; i++) {
+    ien_matrix_free(l->down[i]);
+    for (int p = 0; p < 4; p++) ien_matrix_free(l->up[i][p]);
+  }
+  for (auto &pair : l->blocks)
+    for (LamaFfc &f : pair) {
+      ien_matrix_free(f.local);
+      ien_matrix_free(f.cross);
+      ien_matrix_free(f.spectral_in);
+      ien_matrix_free(f.fourier);
+      ien_matrix_free(f.spectral_out);
+    }
+  ien_fourier_free(l->fourier);
+  l->fourier = nullptr;
+  free_maps(*l);
+  (void)hipFree(l->d_in);
+  (void)hipFree(l->d_mask);
+  (void)hipFree(l->d_out);
+}
+
+// network.rs:337-344 padded: sides to multiples of 8.
+void lama_padded(size_t width, size_t height, size_t *pw, size_t *ph) {
+  *pw = (width + MULTIPLE - 1) / MULTIPLE * MULTIPLE;
+  *ph = (height + MULTIPLE - 1) / MULTIPLE * MULTIPLE;
+}
+
+// At P padded pixels: in4 P x 4; m0 P x 64, m1 P/4 x 128, m2 P/16 x 256
+// (the downs, then the ups' outputs); a, mid, out P/64 x 512; spectral
+// P/64 x 192; spectrum and filtered (h/8)(w/16 + 1) <= P/64 pixels of 384
+// values and the f32 work as large; rows P x 64 (the largest phase product, 4 x 64 channels at
+// P/4); rgb P x 3.  Maps grow and never shrink; the Fourier plan follows
+// the size.
+ien_status lama_reserve(Lama *l, size_t pw, size_t ph, bool *grew) {
+  *grew = false;
+  IEN_CHECK(pw >= 16 && ph >= 16 && pw % MULTIPLE == 0 && ph % MULTIPLE == 0, IEN_ERR_INPUT,
+            "padded %zu x %zu", pw, ph);
+  const size_t h8 = ph / 8, w8 = pw / 8;
+  if (!l->fourier || l->pw != pw || l->ph != ph) {
+    IEN_HIP(hipStreamSynchronize(l->ctx->stream));
+    ien_fourier_free(l->fourier);
+    l->fourier = nullptr;
+    ien_status st = ien_fourier_new(l->ctx, h8, w8, &l->fourier);
+    if (st != IEN_OK) return st;
+    l->pw = pw;
+    l->ph = ph;
+    *grew = true;
+  }
+  const size_t P = pw * ph;
+  if (P <= l->pixels) return IEN_OK;
+  IEN_HIP(hipStreamSynchronize(l->ctx->stream));
+  free_maps(*l);
+  *grew = true;
+  // A spectrum has h8 (w8 / 2 + 1) <= h8 w8 = P / 64 pixels (w8 >= 2).
+  const size_t S = P / 64;
+  auto alloc = [](uint16_t **p, size_t halves) { return hipMalloc((void **)p, halves * 2); };
+  hipError_t e = alloc(&l->in4, P * 4);
+  if (e == hipSuccess) e = alloc(&l->m0, P * 64);
+  if (e == hipSuccess) e = alloc(&l->m1, P / 4 * 128);
+  if (e == hipSuccess) e = alloc(&l->m2, P / 16 * 256);
+  if (e == hipSuccess) e = alloc(&l->a, P / 64 * CHANNELS);
+  if (e == hipSuccess) e = alloc(&l->mid, P / 64 * CHANNELS);
+  if (e == hipSuccess) e = alloc(&l->out, P / 64 * CHANNELS);
+  if (e == hipSuccess) e = alloc(&l->spectral, P / 64 * SPECTRAL);
+  if (e == hipSuccess) e = alloc(&l->spectrum, S * 2 * SPECTRAL);
+  if (e == hipSuccess) e = alloc(&l->filtered, S * 2 * SPECTRAL);
+  if (e == hipSuccess) e = alloc(&l->rows, P * 64);
+  if (e == hipSuccess) e = alloc(&l->rgb, P * 3);
+  if (e == hipSuccess) e = hipMalloc((void **)&l->work, S * 2 * SPECTRAL * 4);
+  if (e != hipSuccess) {
+    free_maps(*l);
+    return fail(IEN_ERR_GPU, "LaMa maps for %zu pixels: %s", P, hipGetErrorString(e));
+  }
+  l->pixels = P;
+  return IEN_OK;
+}
+
+// network.rs:415-489 Network::run.
+ien_status lama_enqueue(Lama *l, const float *d_image, const float *d_mask, size_t width,
+                        size_t height, float *d_out, hipEvent_t *events) {
+  ien_ctx *ctx = l->ctx;
+  size_t pw, ph;
+  lama_padded(width, height, &pw, &ph);
+  IEN_CHECK(l->fourier && l->pw == pw && l->ph == ph && l->pixels >= pw * ph, IEN_ERR_INPUT,
+            "LaMa maps not reserved for %zu x %zu", pw, ph);
+  int step = 0;
+  auto done = [&]() -> ien_status {
+    if (events) IEN_HIP(hipEventRecord(events[step], ctx->stream));
+    step++;
+    return IEN_OK;
+  };
+  // network.rs:346-370 masked_rows: image (1 - m) | m, mirrored to x 8.
+  ien_status st = ien_pad_image(ctx, IEN_PAD_SYMMETRIC_MASKED, d_image, d_mask, width, height,
+                                MULTIPLE, l->in4, 4);
+  int h = (int)ph, w = (int)pw;
+  if (st == IEN_OK)
+    st = conv(ctx, l->in4, h, w, 4, 4, 7, 1, l->first, l->m0, 64, IEN_ACT_RELU, 0);
+  if (st == IEN_OK) st = done();
+  uint16_t *maps[4] = {l->m0, l->m1, l->m2, l->a};
+  const int chans[4] = {64, 128, 256, CHANNELS};
+  for (int i = 0; i < 3 && st == IEN_OK; i++) {
+    st = conv(ctx, maps[i], h, w, chans[i], chans[i], 3, 2, l->down[i], maps[i + 1],
+              chans[i + 1], IEN_ACT_RELU, 0);
+    h = (h - 1) / 2 + 1;
+    w = (w - 1) / 2 + 1;
+    if (st == IEN_OK) st = done();
+  }
+  const size_t eighth = (size_t)h * w;
+  for (int b = 0; b < BLOCKS && st == IEN_OK; b++) {
+    st = ffc_run(l, l->blocks[b][0], l->a, l->mid, h, w);
+    if (st == IEN_OK) st = ffc_run(l, l->blocks[b][1], l->mid, l->out, h, w);
+    if (st == IEN_OK) st = ien_add(ctx, l->a, l->out, eighth * CHANNELS);
+    if (st == IEN_OK) st = done();
+  }
+  // The ups write the quarter, half and full-scale maps again.
+  for (int i = 0; i < 3 && st == IEN_OK; i++) {
+    st = up_run(l, l->up[i], maps[3 - i], h, w, chans[3 - i], chans[2 - i], maps[2 - i]);
+    h *= 2;
+    w *= 2;
+    if (st == IEN_OK) st = done();
+  }
+  if (st == IEN_OK)
+    st = conv(ctx, l->m0, h, w, 64, 64, 7, 1, l->last, l->rgb, 3, IEN_ACT_SIGMOID, 0);
+  if (st == IEN_OK) st = ien_crop(ctx, l->rgb, pw, 3, width, height, 3, d_out);
+  if (st == IEN_OK) st = done();
+  return st;
+}
+
+}  // namespace ien

@@ -10,6 +10,9 @@
 // into f32.  The whole run is one stream of launches; with graphs enabled it
 // is captured once per image size and replayed, so the 36 launches cost one
 // submission.
+//
+// SCUNet and LaMa are objects of their own (scunet.hip, lama.hip) that this
+// file loads, sizes and runs the same way.
 
 #include <cstring>
 #include <fstream>
@@ -18,6 +21,7 @@
 #include <memory>
 
 #include "ien_internal.h"
+#include "lama.h"
 #include "scunet.h"
 
 namespace ien {
@@ -141,10 +145,11 @@ struct ien_model {
   ien_model_kind kind = IEN_MODEL_REALESRGAN;
   std::vector<ien::EsrganLayer> layers;
   std::unique_ptr<ien::Scunet> scunet;  // IEN_MODEL_SCUNET
+  std::unique_ptr<ien::Lama> lama;      // IEN_MODEL_LAMA
   ien::Maps maps;
   bool use_graph = false;
   hipGraphExec_t graph = nullptr;
-  const float *graph_in = nullptr;
+  const float *graph_in = nullptr, *graph_mask = nullptr;
   float *graph_out = nullptr;
   size_t graph_w = 0, graph_h = 0;
 };
@@ -258,10 +263,10 @@ static ien_status enqueue_esrgan(ien_model *model, const float *d_image, size_t 
 
 // Steps of a run (progress reports) and output floats per input pixel.
 static int model_steps(const ien_model *m) {
-  return m->kind == IEN_MODEL_SCUNET ? SCUNET_STEPS : STEPS;
+  return m->kind == IEN_MODEL_SCUNET ? SCUNET_STEPS : m->kind == IEN_MODEL_LAMA ? LAMA_STEPS : STEPS;
 }
 static size_t out_per_pixel(const ien_model *m) {
-  return m->kind == IEN_MODEL_SCUNET ? 3 : 3 * SCALE * SCALE;
+  return m->kind == IEN_MODEL_REALESRGAN ? 3 * SCALE * SCALE : 3;
 }
 
 // Maps for an image of this size, then its launches.
@@ -274,19 +279,33 @@ static ien_status prepare(ien_model *model, size_t width, size_t height) {
     if (st == IEN_OK && model->scunet->pixels != before) drop_graph(model);
     return st;
   }
+  if (model->kind == IEN_MODEL_LAMA) {
+    size_t pw, ph;
+    lama_padded(width, height, &pw, &ph);
+    bool grew = false;
+    ien_status st = lama_reserve(model->lama.get(), pw, ph, &grew);
+    if (grew) drop_graph(model);
+    return st;
+  }
   return ensure_maps(model, width * height, false);
 }
 
-static ien_status enqueue(ien_model *model, const float *d_image, size_t width, size_t height,
-                          float *d_out, hipEvent_t *events) {
+static ien_status enqueue(ien_model *model, const float *d_image, const float *d_mask,
+                          size_t width, size_t height, float *d_out, hipEvent_t *events) {
+  if (model->kind == IEN_MODEL_LAMA)
+    return lama_enqueue(model->lama.get(), d_image, d_mask, width, height, d_out, events);
   if (model->kind == IEN_MODEL_SCUNET)
     return scunet_enqueue(model->scunet.get(), d_image, width, height, d_out, events);
   return enqueue_esrgan(model, d_image, width, height, d_out, events);
 }
 
-static ien_status check_size(size_t width, size_t height) {
+static ien_status check_size(const ien_model *model, size_t width, size_t height) {
   // realesrgan-native lib.rs:302-316
   if (width == 0 || height == 0) return fail(IEN_ERR_INPUT, "empty %zu x %zu image", width, height);
+  // lama-native lib.rs:180-187: sides of at least 9.
+  if (model->kind == IEN_MODEL_LAMA && (width < LAMA_MIN_SIDE || height < LAMA_MIN_SIDE))
+    return fail(IEN_ERR_INPUT, "%zu x %zu image: sides of at least %zu pixels", width, height,
+                LAMA_MIN_SIDE);
   if (width > (1u << 15) || height > (1u << 15) || width * height > (1ull << 28))
     return fail(IEN_ERR_INPUT, "%zu x %zu image is too large", width, height);
   return IEN_OK;
@@ -301,8 +320,8 @@ extern "C" {
 static ien_status model_new(ien_ctx *ctx, ien_model_kind kind, const TensorSource &take,
                             ien_model **out) {
   IEN_CHECK(ctx && out, IEN_ERR_INPUT, "null argument");
-  IEN_CHECK(kind == IEN_MODEL_REALESRGAN || kind == IEN_MODEL_SCUNET, IEN_ERR_INPUT,
-            "model kind %d", (int)kind);
+  IEN_CHECK(kind == IEN_MODEL_REALESRGAN || kind == IEN_MODEL_SCUNET || kind == IEN_MODEL_LAMA,
+            IEN_ERR_INPUT, "model kind %d", (int)kind);
   IEN_HIP(hipSetDevice(ctx->device));
   std::unique_ptr<ien_model> model(new ien_model);
   model->ctx = ctx;
@@ -311,6 +330,9 @@ static ien_status model_new(ien_ctx *ctx, ien_model_kind kind, const TensorSourc
   if (kind == IEN_MODEL_SCUNET) {
     model->scunet.reset(new Scunet);
     st = scunet_load(ctx, take, model->scunet.get());
+  } else if (kind == IEN_MODEL_LAMA) {
+    model->lama.reset(new Lama);
+    st = lama_load(ctx, take, model->lama.get());
   } else {
     st = load_esrgan(model.get(), take);
   }
@@ -327,8 +349,10 @@ ien_status ien_model_load(ien_ctx *ctx, ien_model_kind kind, const char *weights
   IEN_CHECK(weights_path, IEN_ERR_INPUT, "no weights path");
   WeightFile file;
   // The weights files' magics (realesrgan-native lib.rs:124, scunet-native
-  // lib.rs:101).
-  ien_status st = file.read(weights_path, kind == IEN_MODEL_SCUNET ? "SCUNET\0\0" : "REALESRG");
+  // lib.rs:101, lama-native lib.rs:96).
+  ien_status st = file.read(weights_path, kind == IEN_MODEL_SCUNET ? "SCUNET\0\0"
+                                          : kind == IEN_MODEL_LAMA ? "LAMA\0\0\0\0"
+                                                                   : "REALESRG");
   if (st != IEN_OK) return st;
   st = model_new(
       ctx, kind,
@@ -389,6 +413,7 @@ void ien_model_free(ien_model *model) {
     (void)hipFree(l.d_slope);
   }
   if (model->scunet) scunet_free(model->scunet.get());
+  if (model->lama) lama_free(model->lama.get());
   free_maps(model->maps);
   delete model;
 }
@@ -403,20 +428,23 @@ ien_status ien_model_set_graph(ien_model *model, int enabled) {
 ien_status ien_model_run_device(ien_model *model, const float *d_image, const float *d_mask,
                                 size_t width, size_t height, float *d_out) {
   IEN_CHECK(model && d_image && d_out, IEN_ERR_INPUT, "null argument");
-  IEN_CHECK(d_mask == nullptr, IEN_ERR_INPUT, "this model takes no mask");
-  ien_status st = check_size(width, height);
+  if (model->kind == IEN_MODEL_LAMA)
+    IEN_CHECK(d_mask != nullptr, IEN_ERR_INPUT, "LaMa needs a mask");
+  else
+    IEN_CHECK(d_mask == nullptr, IEN_ERR_INPUT, "this model takes no mask");
+  ien_status st = check_size(model, width, height);
   if (st != IEN_OK) return st;
   ien_ctx *ctx = model->ctx;
   IEN_HIP(hipSetDevice(ctx->device));
   st = prepare(model, width, height);
   if (st != IEN_OK) return st;
-  if (!model->use_graph) return enqueue(model, d_image, width, height, d_out, nullptr);
-  if (!model->graph || model->graph_in != d_image || model->graph_out != d_out ||
-      model->graph_w != width || model->graph_h != height) {
+  if (!model->use_graph) return enqueue(model, d_image, d_mask, width, height, d_out, nullptr);
+  if (!model->graph || model->graph_in != d_image || model->graph_mask != d_mask ||
+      model->graph_out != d_out || model->graph_w != width || model->graph_h != height) {
     drop_graph(model);
     hipGraph_t graph = nullptr;
     IEN_HIP(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
-    st = enqueue(model, d_image, width, height, d_out, nullptr);
+    st = enqueue(model, d_image, d_mask, width, height, d_out, nullptr);
     hipError_t e = hipStreamEndCapture(ctx->stream, &graph);
     if (st != IEN_OK) {
       if (graph) (void)hipGraphDestroy(graph);
@@ -430,6 +458,7 @@ ien_status ien_model_run_device(ien_model *model, const float *d_image, const fl
       return fail(IEN_ERR_GPU, "graph instantiate: %s", hipGetErrorString(e));
     }
     model->graph_in = d_image;
+    model->graph_mask = d_mask;
     model->graph_out = d_out;
     model->graph_w = width;
     model->graph_h = height;
@@ -441,14 +470,37 @@ ien_status ien_model_run_device(ien_model *model, const float *d_image, const fl
 ien_status ien_model_run(ien_model *model, const float *image, const float *mask, size_t width,
                          size_t height, float *out, ien_progress progress, void *user) {
   IEN_CHECK(model && image && out, IEN_ERR_INPUT, "null argument");
-  IEN_CHECK(mask == nullptr, IEN_ERR_INPUT, "this model takes no mask");
-  ien_status st = check_size(width, height);
+  if (model->kind == IEN_MODEL_LAMA)
+    IEN_CHECK(mask != nullptr, IEN_ERR_INPUT, "LaMa needs a mask");
+  else
+    IEN_CHECK(mask == nullptr, IEN_ERR_INPUT, "this model takes no mask");
+  ien_status st = check_size(model, width, height);
   if (st != IEN_OK) return st;
   ien_ctx *ctx = model->ctx;
   IEN_HIP(hipSetDevice(ctx->device));
   const size_t pixels = width * height;
-  float *d_in = nullptr, *d_out = nullptr;
-  if (model->kind == IEN_MODEL_SCUNET) {
+  float *d_in = nullptr, *d_out = nullptr, *d_mask = nullptr;
+  if (model->kind == IEN_MODEL_LAMA) {
+    Lama &l = *model->lama;
+    st = prepare(model, width, height);
+    if (st != IEN_OK) return st;
+    if (l.staged < pixels) {
+      IEN_HIP(hipStreamSynchronize(ctx->stream));
+      (void)hipFree(l.d_in);
+      (void)hipFree(l.d_mask);
+      (void)hipFree(l.d_out);
+      l.d_in = l.d_mask = l.d_out = nullptr;
+      l.staged = 0;
+      IEN_HIP(hipMalloc(&l.d_in, pixels * 3 * 4));
+      IEN_HIP(hipMalloc(&l.d_mask, pixels * 4));
+      IEN_HIP(hipMalloc(&l.d_out, pixels * 3 * 4));
+      l.staged = pixels;
+    }
+    d_in = l.d_in;
+    d_mask = l.d_mask;
+    d_out = l.d_out;
+    IEN_HIP(hipMemcpyAsync(d_mask, mask, pixels * 4, hipMemcpyHostToDevice, ctx->stream));
+  } else if (model->kind == IEN_MODEL_SCUNET) {
     Scunet &s = *model->scunet;
     st = prepare(model, width, height);
     if (st != IEN_OK) return st;
@@ -477,7 +529,7 @@ ien_status ien_model_run(ien_model *model, const float *image, const float *mask
     events.resize(steps);
     for (auto &e : events) IEN_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
   }
-  st = enqueue(model, d_in, width, height, d_out, progress ? events.data() : nullptr);
+  st = enqueue(model, d_in, d_mask, width, height, d_out, progress ? events.data() : nullptr);
   bool cancelled = false;
   if (st == IEN_OK && progress) {
     // lib.rs:168-188 (SCUNet lib.rs:205-215): progress after each layer or

@@ -21,7 +21,7 @@ INPUT_ROWS, INPUT_IMAGE = 0, 1
 NHWC, NCHW = 0, 1
 ACT_NONE, ACT_RELU, ACT_GELU, ACT_PRELU, ACT_SIGMOID = range(5)
 OUT_F16, OUT_F32 = 0, 1
-MODEL_REALESRGAN, MODEL_SCUNET = 0, 1
+MODEL_REALESRGAN, MODEL_SCUNET, MODEL_LAMA = 0, 1, 2
 
 # Every symbol include/ien_hip.h declares.
 EXPORTS = (
@@ -35,6 +35,8 @@ EXPORTS = (
     "ien_window_count", "ien_position_bias", "ien_bias_tables", "ien_window_gather",
     "ien_window_attention", "ien_window_scatter_add", "ien_swin_new", "ien_swin_free", "ien_swin_run",
     "ien_resize", "ien_pad_image", "ien_crop", "ien_gather_2x2", "ien_scatter_2x2", "ien_add",
+    "ien_fourier_new", "ien_fourier_free", "ien_fourier_half", "ien_fourier_forward",
+    "ien_fourier_inverse",
 )
 
 
@@ -166,6 +168,13 @@ def load():
         L.ien_gather_2x2.argtypes = [vp, vp, sz, sz, sz, sz, i, vp]
         L.ien_scatter_2x2.argtypes = [vp, vp, sz, sz, sz, sz, vp, sz]
         L.ien_add.argtypes = [vp, vp, vp, sz]
+        L.ien_fourier_new.argtypes = [vp, sz, sz, ctypes.POINTER(vp)]
+        L.ien_fourier_free.argtypes = [vp]
+        L.ien_fourier_free.restype = None
+        L.ien_fourier_half.argtypes = [vp]
+        L.ien_fourier_half.restype = sz
+        L.ien_fourier_forward.argtypes = [vp, vp, sz, sz, vp, vp]
+        L.ien_fourier_inverse.argtypes = [vp, vp, sz, vp, vp, sz]
         for name in EXPORTS:
             getattr(L, name)
         _lib = L
@@ -399,6 +408,33 @@ def add(ctx, x, y):
     check(load().ien_add(ctx.h, _ptr(x), _ptr(y), x.numel()))
 
 
+class Fourier:
+    """ien_fourier: the 2-D real transforms of height x width maps."""
+
+    def __init__(self, ctx, height, width):
+        h = ctypes.c_void_p()
+        check(load().ien_fourier_new(ctx.h, height, width, ctypes.byref(h)))
+        self.h, self.height, self.width = h, height, width
+        self.half = load().ien_fourier_half(h)
+
+    def forward(self, x, stride, channels, work, spectrum):
+        check(load().ien_fourier_forward(self.h, _ptr(x), stride, channels, _ptr(work), _ptr(spectrum)))
+
+    def inverse(self, spectrum, channels, work, out, stride):
+        check(load().ien_fourier_inverse(self.h, _ptr(spectrum), channels, _ptr(work), _ptr(out), stride))
+
+    def free(self):
+        if self.h:
+            load().ien_fourier_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
 class Swin:
     """ien_swin: one Swin transformer block (attend then MLP, in place).
     `weights`: dict of host arrays ln1_gamma, ln1_beta, qkv_w (c x 3c),
@@ -470,20 +506,24 @@ class Model:
     def set_graph(self, enabled):
         check(load().ien_model_set_graph(self.h, int(enabled)))
 
-    def run(self, image, progress=None):
+    def run(self, image, progress=None, mask=None):
         """Host f32 H x W x 3 in, host f32 out (Model::run_float): 4H x 4W x 3
-        for Real-ESRGAN, H x W x 3 for SCUNet."""
+        for Real-ESRGAN, H x W x 3 for SCUNet and LaMa (which takes the
+        H x W mask, 1 = fill)."""
         import numpy as np
 
         image = np.ascontiguousarray(image, dtype=np.float32)
         h, w, _ = image.shape
         s = 4 if self.kind == MODEL_REALESRGAN else 1
         out = np.empty((s * h, s * w, 3), np.float32)
+        m = None if mask is None else np.ascontiguousarray(mask, dtype=np.float32)
         cb = PROGRESS(progress) if progress else None
-        check(load().ien_model_run(self.h, image.ctypes.data_as(ctypes.c_void_p), None, w, h,
+        check(load().ien_model_run(self.h, image.ctypes.data_as(ctypes.c_void_p),
+                                   None if m is None else m.ctypes.data_as(ctypes.c_void_p), w, h,
                                    out.ctypes.data_as(ctypes.c_void_p),
                                    ctypes.cast(cb, ctypes.c_void_p) if cb else None, None))
         return out
 
-    def run_device(self, d_image, width, height, d_out):
-        check(load().ien_model_run_device(self.h, _ptr(d_image), None, width, height, _ptr(d_out)))
+    def run_device(self, d_image, width, height, d_out, d_mask=None):
+        check(load().ien_model_run_device(self.h, _ptr(d_image), None if d_mask is None else _ptr(d_mask),
+                                          width, height, _ptr(d_out)))

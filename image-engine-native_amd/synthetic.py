@@ -85,6 +85,7 @@ def sweep_case(name, seed=INPUT_SEED):
 # ---- SCUNet ------------------------------------------------------------------
 SCUNET_DIM, SCUNET_BLOCKS, SCUNET_WINDOW = 64, 4, 8
 RESIDUAL_GAIN = 0.2
+LAMA_RESIDUAL_GAIN = 0.05
 
 
 def _scunet_block(name, c):
@@ -156,3 +157,78 @@ def scunet_tensors(seed=WEIGHT_SEED, init="trunc_normal"):
 def scunet_image(height=512, width=768, seed=INPUT_SEED):
     """H x W x 3 RGB, uniform [0, 1)."""
     return np.random.default_rng(seed).random((height, width, 3), dtype=np.float32)
+
+
+# Big LaMa (crates/lama-native/src/network.rs): 4 -> 64 -> 128 -> 256 -> 512
+# channels, 18 blocks of two fast Fourier convolutions at an eighth of the
+# size, three transposed upsamplings, 7x7 to RGB.
+LAMA_LOCAL, LAMA_GLOBAL, LAMA_BLOCKS = 128, 384, 18
+
+
+def lama_names():
+    """(name, shape) of every LaMa tensor in the weights file's order
+    (tools/lama/export_weights.py export)."""
+    c = LAMA_LOCAL + LAMA_GLOBAL
+    spectral = LAMA_GLOBAL // 2
+    names = [("first.weight", (49 * 4, 64)), ("first.bias", (64,))]
+    for i, (cin, cout) in enumerate(((64, 128), (128, 256), (256, c))):
+        names += [(f"down{i}.weight", (9 * cin, cout)), (f"down{i}.bias", (cout,))]
+    for b in range(LAMA_BLOCKS):
+        for f in range(2):
+            n = f"block{b}.ffc{f}"
+            names += [
+                (f"{n}.local.weight", (9 * c, LAMA_LOCAL)), (f"{n}.local.bias", (LAMA_LOCAL,)),
+                (f"{n}.cross.weight", (9 * LAMA_LOCAL, LAMA_GLOBAL)), (f"{n}.cross.bias", (LAMA_GLOBAL,)),
+                (f"{n}.spectral_in.weight", (LAMA_GLOBAL, spectral)), (f"{n}.spectral_in.bias", (spectral,)),
+                (f"{n}.fourier.weight", (2 * spectral, 2 * spectral)), (f"{n}.fourier.bias", (2 * spectral,)),
+                (f"{n}.spectral_out.weight", (spectral, LAMA_GLOBAL)),
+            ]
+    for i, (cin, cout) in enumerate(((c, 256), (256, 128), (128, 64))):
+        for p in range(4):
+            taps = (1, 2, 2, 4)[p]
+            names += [(f"up{i}.phase{p}.weight", (taps * cin, cout)), (f"up{i}.phase{p}.bias", (cout,))]
+    names += [("last.weight", (49 * 64, 3)), ("last.bias", (3,))]
+    return names
+
+
+def lama_tensors(seed=WEIGHT_SEED):
+    """name -> array for every LaMa tensor: He-normal matrices (N(0, 2 /
+    fan_in), the ReLU networks' init with every batch norm folded as the
+    identity), small biases; the second FFC of each block, whose output is
+    added onto the residual stream, scaled by LAMA_RESIDUAL_GAIN so 18
+    blocks keep activations O(1) and the sigmoid out of saturation."""
+    rng = np.random.default_rng(seed)
+    out = {}
+    for name, shape in lama_names():
+        if ".phase" in name and name.endswith(".bias") and ".phase0." not in name:
+            # One transposed convolution's bias, shared by its four phases
+            # (export_weights.py puts the same bias on each).
+            out[name] = out[name.split(".phase")[0] + ".phase0.bias"]
+            continue
+        if name.endswith(".bias"):
+            v = 0.02 * rng.standard_normal(shape)
+        else:
+            v = rng.standard_normal(shape) * np.sqrt(2.0 / shape[0])
+            if ".ffc1." in name and not name.endswith(("spectral_in.weight", "fourier.weight")):
+                v *= LAMA_RESIDUAL_GAIN
+        out[name] = np.asarray(v, np.float32)
+    return out
+
+
+def lama_image(height=512, width=512, seed=INPUT_SEED):
+    """H x W x 3 RGB, uniform [0, 1)."""
+    return np.random.default_rng(seed).random((height, width, 3), dtype=np.float32)
+
+
+def lama_mask(height=512, width=512, seed=INPUT_SEED + 1, cover=0.25):
+    """H x W binary mask (1 = fill) of random rectangles, added until about
+    `cover` of the pixels are set."""
+    rng = np.random.default_rng(seed)
+    m = np.zeros((height, width), np.float32)
+    while m.mean() < cover:
+        rh = int(rng.integers(max(1, height // 16), max(2, height // 3)))
+        rw = int(rng.integers(max(1, width // 16), max(2, width // 3)))
+        y = int(rng.integers(0, height - rh + 1))
+        x = int(rng.integers(0, width - rw + 1))
+        m[y:y + rh, x:x + rw] = 1.0
+    return m

@@ -317,13 +317,35 @@ void ien_swin_free(ien_swin *block);
  * GELU, fc2 added back.  Scratch is the block's own, grown on demand. */
 ien_status ien_swin_run(ien_swin *block, uint16_t *d_map, size_t stride, int height, int width);
 
+/* ---- Fourier units: crates/lama-native/src/fourier.rs ----------------- */
+/* fourier.rs:262-288 Fourier::new: the transforms of height x width maps
+ * (sides 1 .. 1024); a spectrum has half = width / 2 + 1 columns. */
+typedef struct ien_fourier ien_fourier;
+ien_status ien_fourier_new(ien_ctx *ctx, size_t height, size_t width, ien_fourier **out);
+void ien_fourier_free(ien_fourier *f);
+size_t ien_fourier_half(const ien_fourier *f);
+/* fourier.rs:291-344 forward: the spectrum of the map d_x (f16 NHWC, pixel
+ * stride `stride`, `channels` values), rfftn over both axes with "ortho"
+ * scale, into d_spectrum (f16, height x half pixels of 2 channels values:
+ * the real parts, then the imaginary parts).  d_work: height x half x 2
+ * channels f32 of scratch. */
+ien_status ien_fourier_forward(const ien_fourier *f, const uint16_t *d_x, size_t stride,
+                               size_t channels, float *d_work, uint16_t *d_spectrum);
+/* fourier.rs:347-403 inverse: the map whose spectrum is d_spectrum (irfftn,
+ * "ortho": the complex transform down the columns, then each row's real
+ * transform, which drops the imaginary parts of column 0 and, for an even
+ * width, of column width / 2), ADDED to d_out (f16 NHWC, pixel stride
+ * `stride`).  d_work as for the forward transform. */
+ien_status ien_fourier_inverse(const ien_fourier *f, const uint16_t *d_spectrum, size_t channels,
+                               float *d_work, uint16_t *d_out, size_t stride);
+
 /* ---- models: crates/<model>-native/src/lib.rs Model ------------------- */
-typedef enum { IEN_MODEL_REALESRGAN = 0, IEN_MODEL_SCUNET = 1 } ien_model_kind;
+typedef enum { IEN_MODEL_REALESRGAN = 0, IEN_MODEL_SCUNET = 1, IEN_MODEL_LAMA = 2 } ien_model_kind;
 
 /* Model::load (realesrgan-native lib.rs:120-137, scunet-native
- * lib.rs:79-111, with the GPU engine): read the weights file (weight_file.rs
- * format, magic b"REALESRG" or b"SCUNET\0\0"), check every tensor, upload
- * once. */
+ * lib.rs:79-111, lama-native lib.rs:75-108, with the GPU engine): read the
+ * weights file (weight_file.rs format, magic b"REALESRG", b"SCUNET\0\0" or
+ * b"LAMA\0\0\0\0"), check every tensor, upload once. */
 ien_status ien_model_load(ien_ctx *ctx, ien_model_kind kind, const char *weights_path,
                           ien_model **out);
 /* The same from weights already in memory: `tensors` name/shape/value
@@ -338,15 +360,17 @@ ien_status ien_model_from_tensors(ien_ctx *ctx, ien_model_kind kind, const ien_t
                                   size_t count, ien_model **out);
 void ien_model_free(ien_model *model);
 
-/* Progress callback: share done in 0..1, after each layer (Real-ESRGAN, 34)
- * or block (SCUNet, 28); nonzero return cancels the run with
- * IEN_ERR_CANCELLED (realesrgan lib.rs:168-188, scunet lib.rs:205-215). */
+/* Progress callback: share done in 0..1, after each layer (Real-ESRGAN, 34),
+ * block (SCUNet, 28) or step (LaMa, 26: lama-native lib.rs:128-157); nonzero
+ * return cancels the run with IEN_ERR_CANCELLED (realesrgan lib.rs:168-188,
+ * scunet lib.rs:205-215). */
 typedef int (*ien_progress)(float done, void *user);
 
 /* Model::run_float (realesrgan-native lib.rs:194-214, scunet-native
- * lib.rs:151-171): host f32 NHWC image of width x height x 3 in [0, 1], host
- * f32 output (Real-ESRGAN 4h x 4w x 3, SCUNet h x w x 3).  `mask` is for LaMa
- * and NULL otherwise. */
+ * lib.rs:151-171, lama-native lib.rs:159-178): host f32 NHWC image of width x
+ * height x 3 in [0, 1], host f32 output (Real-ESRGAN 4h x 4w x 3, SCUNet and
+ * LaMa h x w x 3).  `mask` (height x width, 1 = fill) for LaMa, whose sides
+ * are at least 9; NULL for the others. */
 ien_status ien_model_run(ien_model *model, const float *image, const float *mask, size_t width,
                          size_t height, float *out, ien_progress progress, void *user);
 

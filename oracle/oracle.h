@@ -129,6 +129,24 @@ void or_swin_mlp(int threads, float *map, size_t stride, size_t rows, size_t c,
 int or_scunet_run(int threads, const float *const *t, const float *image, size_t width,
                   size_t height, float *out);
 
+/* ---- lama-native fourier.rs and network.rs ---------------------------- */
+/* fourier.rs:291-344 forward: the "ortho" rfftn of x (h x w x c, NHWC) into
+ * out (h x (w/2+1) pixels of [re x c | im x c]). */
+void or_rfft2(const float *x, size_t h, size_t w, size_t c, float *out);
+/* fourier.rs:347-403 inverse: the "ortho" irfftn of s ADDED to out. */
+void or_irfft2_add(const float *s, size_t h, size_t w, size_t c, float *out);
+/* network.rs:271-335 Up::run: a stride-2 transposed 3x3 convolution as four
+ * output-phase products (PHASE_TAPS), through a ReLU: x (h x w x cin) to out
+ * (2h x 2w x cout); phase_w[p] [(taps) cin][cout] row-major, phase_b[p]. */
+void or_lama_up(int threads, const float *const *phase_w, const float *const *phase_b,
+                const float *x, size_t h, size_t w, size_t cin, size_t cout, float *out);
+/* network.rs:415-489 run: image (height x width x 3 in 0..1) and mask
+ * (height x width, 1 = fill) through Big LaMa's generator; out height x
+ * width x 3.  `t` holds the 358 tensors in the weights file's order
+ * (lama.c). */
+int or_lama_run(int threads, const float *const *t, const float *image, const float *mask,
+                size_t width, size_t height, float *out);
+
 /* ---- realesrgan-native network.rs ------------------------------------- */
 /* network.rs:80-141: 34 conv3 layers (PReLU on all but the last), then the
  * x4 pixel shuffle plus the input repeated.  w[i] is 9cin x cout row-major

@@ -92,6 +92,11 @@ def lib():
         L.or_resize.argtypes = [vp, sz, sz, sz, vp, sz, sz, sz, ctypes.c_int]
         L.or_pad_replicate.argtypes = [vp, sz, sz, sz, vp]
         L.or_masked_rows.argtypes = [vp, vp, sz, sz, sz, vp]
+        L.or_rfft2.argtypes = [vp, sz, sz, sz, vp]
+        L.or_irfft2_add.argtypes = [vp, sz, sz, sz, vp]
+        L.or_lama_run.argtypes = [ctypes.c_int, vp, vp, vp, sz, sz, vp]
+        L.or_lama_run.restype = ctypes.c_int
+        L.or_lama_up.argtypes = [ctypes.c_int, vp, vp, vp, sz, sz, sz, sz, vp]
         _lib = L
     return _lib
 
@@ -365,4 +370,54 @@ def scunet_run(tensors, names, image, threads=None):
                              _p(out))
     if rc != 0:
         raise RuntimeError(f"or_scunet_run: {rc}")
+    return out
+
+
+def rfft2(x):
+    """fourier.rs forward: x (h, w, c) -> spectrum (h, w // 2 + 1, 2c) as [re | im]."""
+    x = _f32(x)
+    h, w, c = x.shape
+    out = np.zeros((h, w // 2 + 1, 2 * c), np.float32)
+    lib().or_rfft2(_p(x), h, w, c, _p(out))
+    return out
+
+
+def irfft2_add(spectrum, out):
+    """fourier.rs inverse: out (h, w, c) += irfftn(spectrum), in place; returns out."""
+    s = _f32(spectrum)
+    assert out.dtype == np.float32 and out.flags["C_CONTIGUOUS"]
+    h, w, c = out.shape
+    assert s.shape == (h, w // 2 + 1, 2 * c)
+    lib().or_irfft2_add(_p(s), h, w, c, _p(out))
+    return out
+
+
+def lama_run(tensors, names, image, mask, threads=None):
+    """tensors: name -> array; names: the weights file's order (synthetic.lama_names)."""
+    image = _f32(image)
+    mask = _f32(mask)
+    h, w, _ = image.shape
+    assert mask.shape == (h, w)
+    arrs = [_f32(tensors[n]) for n, _ in names]
+    ptrs = (ctypes.c_void_p * len(arrs))(*[a.ctypes.data for a in arrs])
+    out = np.zeros((h, w, 3), np.float32)
+    rc = lib().or_lama_run(threads or threads_default(), ctypes.cast(ptrs, ctypes.c_void_p), _p(image),
+                           _p(mask), w, h, _p(out))
+    if rc != 0:
+        raise RuntimeError(f"or_lama_run: {rc}")
+    return out
+
+
+def lama_up(phase_w, phase_b, x, threads=1):
+    """network.rs Up::run: x (h, w, cin) -> (2h, 2w, cout), ReLU."""
+    x = _f32(x)
+    h, w, cin = x.shape
+    ws = [_f32(m) for m in phase_w]
+    bs = [_f32(b) for b in phase_b]
+    cout = ws[0].shape[1]
+    pw = (ctypes.c_void_p * 4)(*[m.ctypes.data for m in ws])
+    pb = (ctypes.c_void_p * 4)(*[b.ctypes.data for b in bs])
+    out = np.zeros((2 * h, 2 * w, cout), np.float32)
+    lib().or_lama_up(threads, ctypes.cast(pw, ctypes.c_void_p), ctypes.cast(pb, ctypes.c_void_p), _p(x), h, w,
+                     cin, cout, _p(out))
     return out

@@ -35,3 +35,10 @@ def oracle():
 
     O.lib()
     return O
+
+
+@pytest.fixture(scope="session")
+def golden():
+    import numpy as np
+
+    return np.load(ROOT / "tests" / "golden" / "golden.npz")

@@ -231,6 +231,33 @@ def main():
     out["esrgan_img"] = img
     out["esrgan_y"] = x[0].numpy().transpose(1, 2, 0)
 
+    # lama-native fourier.rs: rfftn / irfftn over the two spatial axes with
+    # "ortho" scale; spectra as [re | im] per pixel.  The inverse inputs are
+    # not Hermitian: irfftn reads only the real parts of column 0 and (even
+    # widths) of the last column.
+    x = f32(rng.standard_normal((12, 10, 3)))
+    z = torch.fft.rfftn(torch.from_numpy(x.astype(np.float64)), dim=(0, 1), norm="ortho")
+    out["rfft_x"] = x
+    out["rfft_y"] = torch.cat([z.real, z.imag], dim=-1).numpy()
+    for name, (h, w) in (("irfft_odd", (9, 7)), ("irfft_even", (8, 6))):
+        s = f32(rng.standard_normal((h, w // 2 + 1, 4)))
+        zc = torch.complex(torch.from_numpy(s[..., :2].astype(np.float64)),
+                           torch.from_numpy(s[..., 2:].astype(np.float64)))
+        out[f"{name}_s"] = s
+        out[f"{name}_y"] = torch.fft.irfftn(zc, s=(h, w), dim=(0, 1), norm="ortho").numpy()
+
+    # lama-native network.rs:271-335: a stride-2 transposed 3x3 convolution
+    # (padding 1, output padding 1) and ReLU, the layer the four phase
+    # products restate; kernel in torch's [in, out, ky, kx] layout.
+    x = f32(rng.standard_normal((5, 6, 8)))
+    wt = f32(rng.standard_normal((8, 4, 3, 3)) / 6)
+    bt = f32(0.1 * rng.standard_normal(4))
+    y = F.conv_transpose2d(torch.from_numpy(x.astype(np.float64).transpose(2, 0, 1)[None].copy()),
+                           torch.from_numpy(wt.astype(np.float64)), torch.from_numpy(bt.astype(np.float64)),
+                           stride=2, padding=1, output_padding=1)
+    out.update(up_x=x, up_w=wt, up_b=bt)
+    out["up_y"] = F.relu(y)[0].numpy().transpose(1, 2, 0)
+
     packed = {k: (v.astype(np.float32) if v.dtype == np.float64 else v) for k, v in out.items()}
     np.savez_compressed(HERE / "golden.npz", **packed)
     print(f"wrote {len(packed)} arrays, {sum(v.nbytes for v in packed.values())} bytes")
