@@ -232,3 +232,113 @@ def lama_mask(height=512, width=512, seed=INPUT_SEED + 1, cover=0.25):
         x = int(rng.integers(0, width - rw + 1))
         m[y:y + rh, x:x + rw] = 1.0
     return m
+
+
+# BiRefNet-lite (crates/birefnet-native/src/swin.rs, decoder.rs): Swin-T
+# backbone (96..768 channels, depths 2/2/6/2, head dim 32) and the decoder;
+# the configured network uses windows of 12 (shift 6) and a deformable-free
+# ASPP (all-zero offset and modulator convolutions).
+BIREFNET_STAGES = ((96, 2), (192, 2), (384, 6), (768, 2))
+BIREFNET_WINDOW = 12
+BIREFNET_LEVELS = ((1728, 768), (960, 384), (480, 192), (240, 96))  # decoder.rs:776
+BIREFNET_ASPP_SIZES = (1, 1, 3, 7)
+
+
+def birefnet_names(window=BIREFNET_WINDOW):
+    """(name, shape) of every BiRefNet tensor in the reference's load order
+    (swin.rs Backbone::load, then decoder.rs Decoder::load)."""
+    n = window * window
+    names = [("patch_embed.weight", (48, 96)), ("patch_embed.bias", (96,)),
+             ("patch_embed.norm.weight", (96,)), ("patch_embed.norm.bias", (96,))]
+    for s, (c, depth) in enumerate(BIREFNET_STAGES):
+        for b in range(depth):
+            p = f"stage{s}.block{b}."
+            names += [(p + "norm1.weight", (c,)), (p + "norm1.bias", (c,)),
+                      (p + "qkv.weight", (c, 3 * c)), (p + "qkv.bias", (3 * c,)),
+                      (p + "position_bias", (c // 32, n, n)),
+                      (p + "proj.weight", (c, c)), (p + "proj.bias", (c,)),
+                      (p + "norm2.weight", (c,)), (p + "norm2.bias", (c,)),
+                      (p + "fc1.weight", (c, 4 * c)), (p + "fc1.bias", (4 * c,)),
+                      (p + "fc2.weight", (4 * c, c)), (p + "fc2.bias", (c,))]
+        if s < 3:
+            names += [(f"stage{s}.merge.norm.weight", (4 * c,)), (f"stage{s}.merge.norm.bias", (4 * c,)),
+                      (f"stage{s}.merge.weight", (4 * c, 2 * c))]
+        names += [(f"stage{s}.norm.weight", (c,)), (f"stage{s}.norm.bias", (c,))]
+    blocks = [("squeeze", 2880, 1536, False)] + [
+        (f"block{4 - i}", cin, cout, i < 3) for i, (cin, cout) in enumerate(BIREFNET_LEVELS)]
+    for q, cin, cout, gate in blocks:
+        names += [(f"{q}.conv_in.weight", (9 * cin, 64)), (f"{q}.conv_in.bias", (64,)),
+                  (f"{q}.conv_out.weight", (9 * 64, cout)), (f"{q}.conv_out.bias", (cout,))]
+        if gate:
+            names += [(f"{q}.gdt.weight", (9 * cout, 16)), (f"{q}.gdt.bias", (16,)),
+                      (f"{q}.gdt_attn.weight", (16, 1)), (f"{q}.gdt_attn.bias", (1,))]
+        for i, k in enumerate(BIREFNET_ASPP_SIZES):
+            taps = k * k
+            names += [(f"{q}.aspp.branch{i}.offset.weight", (taps * 64, 3 * taps)),
+                      (f"{q}.aspp.branch{i}.offset.bias", (3 * taps,)),
+                      (f"{q}.aspp.branch{i}.weight", (taps * 64, 256)),
+                      (f"{q}.aspp.branch{i}.bias", (256,))]
+        names += [(f"{q}.aspp.pool.weight", (64, 256)), (f"{q}.aspp.pool.bias", (256,)),
+                  (f"{q}.aspp.conv1.weight", (1280, 64)), (f"{q}.aspp.conv1.bias", (64,))]
+    for nn_, c in ((4, 768), (3, 384), (2, 192)):
+        names += [(f"lateral{nn_}.weight", (c, c)), (f"lateral{nn_}.bias", (c,))]
+    for nn_, cin, cout in ((5, 3072, 192), (4, 768, 192), (3, 192, 96), (2, 48, 48)):
+        names += [(f"patches{nn_}.conv1.weight", (9 * cin, 64)), (f"patches{nn_}.conv1.bias", (64,)),
+                  (f"patches{nn_}.conv_out.weight", (9 * 64, cout)), (f"patches{nn_}.conv_out.bias", (cout,))]
+    names += [("head.weight", (96, 1)), ("head.bias", (1,)),
+              ("patches1.conv1.weight", (27, 64)), ("patches1.conv1.bias", (64,)),
+              ("patches1.conv_out.weight", (576, 1)), ("patches1.conv_out.bias", (1,))]
+    return names
+
+
+def _relu_followed(name):
+    """Matrices whose output goes through a ReLU (He gain)."""
+    return any(k in name for k in (".conv_in.", ".aspp.branch", ".aspp.pool.", ".aspp.conv1.", ".gdt."))
+
+
+def birefnet_tensors(seed=WEIGHT_SEED, window=BIREFNET_WINDOW, init="trunc_normal", offsets=0.0):
+    """name -> array for every BiRefNet tensor.  The Swin backbone: "trunc_normal"
+    (timm's std 0.02, LayerNorms 1 / 0, zero biases: the configuration's
+    random init) or "fan" (N(0, 1 / fan_in), residual writers scaled by
+    RESIDUAL_GAIN, position biases N(0, 1): attention far from uniform, for
+    parity tests).  The decoder: N(0, g^2 / fan_in) matrices (g = sqrt 2
+    before a ReLU), small biases.  The ASPP's offset and modulator
+    convolutions are zero (the deformable-free network) unless `offsets`
+    sets their standard deviation."""
+    rng = np.random.default_rng(seed)
+    out = {}
+    for name, shape in birefnet_names(window):
+        last = name.rsplit(".", 1)[-1]
+        is_norm = ".norm" in name and not name.endswith("merge.weight")
+        if name.startswith("stage") or name.startswith("patch_embed"):
+            if is_norm and last in ("weight", "bias") and name.split(".")[-2].startswith("norm"):
+                if init == "trunc_normal":
+                    v = np.ones(shape) if last == "weight" else np.zeros(shape)
+                else:
+                    v = (1 + 0.1 * rng.standard_normal(shape)) if last == "weight" else 0.1 * rng.standard_normal(shape)
+            elif name.endswith("position_bias"):
+                v = (np.clip(rng.standard_normal(shape), -2, 2) * 0.02 if init == "trunc_normal"
+                     else rng.standard_normal(shape))
+            elif last == "bias":
+                v = np.zeros(shape) if init == "trunc_normal" else 0.05 * rng.standard_normal(shape)
+            elif init == "trunc_normal" and not name.startswith("patch_embed"):
+                v = np.clip(rng.standard_normal(shape), -2, 2) * 0.02
+            else:
+                v = rng.standard_normal(shape) / np.sqrt(shape[0])
+                if init == "fan" and (name.endswith("proj.weight") or name.endswith("fc2.weight")):
+                    v *= RESIDUAL_GAIN
+        elif ".offset." in name:
+            v = offsets * rng.standard_normal(shape) if offsets else np.zeros(shape)
+        elif last == "bias":
+            v = 0.02 * rng.standard_normal(shape)
+        else:
+            gain = np.sqrt(2.0) if _relu_followed(name) else 1.0
+            v = gain * rng.standard_normal(shape) / np.sqrt(shape[0])
+        out[name] = np.asarray(v, np.float32)
+    return out
+
+
+def birefnet_image(side=1024, seed=INPUT_SEED):
+    """side x side x 3, N(0, 1): an image already normalised with ImageNet's
+    statistics (the reference's run_normalized input)."""
+    return np.random.default_rng(seed).standard_normal((side, side, 3)).astype(np.float32)

@@ -147,6 +147,15 @@ void or_lama_up(int threads, const float *const *phase_w, const float *const *ph
 int or_lama_run(int threads, const float *const *t, const float *image, const float *mask,
                 size_t width, size_t height, float *out);
 
+/* ---- birefnet-native swin.rs and decoder.rs --------------------------- */
+/* lib.rs:144-171 run_normalized: logits (side x side) of a normalised RGB
+ * image (side x side x 3, side a multiple of 64) through the Swin-T backbone
+ * (windows of `window`, shift window / 2, at the full and the half size) and
+ * the decoder.  `t` holds the tensors in the reference's load order
+ * (Backbone::load then Decoder::load: birefnet.c). */
+int or_birefnet_run(int threads, const float *const *t, size_t window, const float *image,
+                    size_t side, float *logits);
+
 /* ---- realesrgan-native network.rs ------------------------------------- */
 /* network.rs:80-141: 34 conv3 layers (PReLU on all but the last), then the
  * x4 pixel shuffle plus the input repeated.  w[i] is 9cin x cout row-major

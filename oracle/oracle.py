@@ -97,6 +97,8 @@ def lib():
         L.or_lama_run.argtypes = [ctypes.c_int, vp, vp, vp, sz, sz, vp]
         L.or_lama_run.restype = ctypes.c_int
         L.or_lama_up.argtypes = [ctypes.c_int, vp, vp, vp, sz, sz, sz, sz, vp]
+        L.or_birefnet_run.argtypes = [ctypes.c_int, vp, sz, vp, sz, vp]
+        L.or_birefnet_run.restype = ctypes.c_int
         _lib = L
     return _lib
 
@@ -420,4 +422,19 @@ def lama_up(phase_w, phase_b, x, threads=1):
     out = np.zeros((2 * h, 2 * w, cout), np.float32)
     lib().or_lama_up(threads, ctypes.cast(pw, ctypes.c_void_p), ctypes.cast(pb, ctypes.c_void_p), _p(x), h, w,
                      cin, cout, _p(out))
+    return out
+
+
+def birefnet_run(tensors, names, image, window, threads=None):
+    """tensors: name -> array; names: the load order (synthetic.birefnet_names).
+    image: (side, side, 3) normalised; returns (side, side) logits."""
+    image = _f32(image)
+    side = image.shape[0]
+    arrs = [_f32(tensors[n]) for n, _ in names]
+    ptrs = (ctypes.c_void_p * len(arrs))(*[a.ctypes.data for a in arrs])
+    out = np.zeros((side, side), np.float32)
+    rc = lib().or_birefnet_run(threads or threads_default(), ctypes.cast(ptrs, ctypes.c_void_p), window,
+                               _p(image), side, _p(out))
+    if rc != 0:
+        raise RuntimeError(f"or_birefnet_run: {rc}")
     return out
