@@ -265,6 +265,76 @@ def lama_leg(ctx, steps, warmup):
             "images_per_s": round(1e3 / ms, 2), "gflop_per_image": gflop, "tflops": round(gflop / ms, 1)}
 
 
+def birefnet_gflop(side=1024, window=12, padded=True):
+    """Multiply-adds x 2 of BiRefNet-lite at side x side: both backbone runs
+    (the window products over the grids padded to whole windows, as the
+    kernels compute them, or over the tokens alone), the decoder's
+    convolutions and products, the head and the full-resolution branch's two
+    convolutions."""
+    n = window * window
+    macs = 0
+    for s0 in (side, side // 2):
+        g = s0 // 4
+        macs += g * g * 48 * 96
+        for s, (c, depth) in enumerate(((96, 2), (192, 2), (384, 6), (768, 2))):
+            gp = -(-g // window) * window if padded else g
+            tp = gp * gp
+            macs += depth * (tp * c * 3 * c + tp * 2 * n * c + tp * c * c + g * g * 8 * c * c)
+            if s < 3:
+                macs += (g // 2) ** 2 * 4 * c * 2 * c
+                g //= 2
+
+    def block(g, cin, cout, gate):
+        m = g * g * (9 * cin * 64 + 64 * 256 * (1 + 1 + 9 + 49) + 1024 * 64 + 9 * 64 * cout)
+        return m + (g * g * (9 * cout * 16 + 16) if gate else 0)
+
+    g4 = side >> 5
+    macs += block(g4, 2880, 1536, False)
+    for i, ((cin, cout), (pc_in, pc_out)) in enumerate(zip(((1728, 768), (960, 384), (480, 192), (240, 96)),
+                                                           ((3072, 192), (768, 192), (192, 96), (48, 48)))):
+        g = side >> (3 - i + 2)
+        macs += block(g, cin, cout, i < 3)
+        if i:
+            c = (768, 384, 192)[i - 1]
+            macs += g * g * c * c
+        macs += g * g * 9 * pc_in * 64 + g * g * 9 * 64 * pc_out
+    macs += (side // 4) ** 2 * 96 + side * side * (27 * 64 + 576)
+    return 2 * macs / 1e9
+
+
+def birefnet_leg(ctx, steps, warmup):
+    """BiRefNet-lite (configuration 5) at 1 x 3 x 1024 x 1024 N(0, 1),
+    window 12, deformable-free ASPP, trunc-normal Swin init, graph replay,
+    input and logits in HBM."""
+    import torch
+
+    import ien
+    import synthetic
+
+    side = 1024
+    model = ien.Model(ctx, ien.MODEL_BIREFNET, tensors=synthetic.birefnet_tensors())
+    d_in = torch.from_numpy(synthetic.birefnet_image(side)).cuda()
+    d_out = torch.empty((side, side), dtype=torch.float32, device="cuda")
+    model.set_graph(True)
+    for _ in range(warmup):
+        model.run_device(d_in, side, side, d_out)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        model.run_device(d_in, side, side, d_out)
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    ok = bool(torch.isfinite(d_out).all())
+    model.free()
+    if not ok:
+        sys.exit("BiRefNet: non-finite output")
+    gflop = round(birefnet_gflop(side, 12), 1)
+    return {"workload": "BiRefNet-lite 1x3x1024x1024 (Swin-T window 12, deformable-free ASPP)",
+            "ms_per_image": round(ms, 3), "images_per_s": round(1e3 / ms, 2), "gflop_per_image": gflop,
+            "gflop_unpadded_windows": round(birefnet_gflop(side, 12, padded=False), 1),
+            "tflops": round(gflop / ms, 1)}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -273,7 +343,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-sweep", action="store_true", help="skip the conv sweep")
     ap.add_argument("--kernel-reps", type=int, default=100)
-    ap.add_argument("--no-models", action="store_true", help="skip the other models (SCUNet, LaMa)")
+    ap.add_argument("--no-models", action="store_true", help="skip the other models (SCUNet, LaMa, BiRefNet)")
+    ap.add_argument("--birefnet-only", action="store_true",
+                    help="only the BiRefNet leg (the workload of its kernel profile)")
     ap.add_argument("--lama-only", action="store_true",
                     help="only the LaMa leg (the workload of its kernel profile)")
     ap.add_argument("--scunet-only", action="store_true",
@@ -309,6 +381,9 @@ def main():
     if args.lama_only:
         print(json.dumps(lama_leg(ctx, max(1, args.steps // 10), 2)), flush=True)
         return
+    if args.birefnet_only:
+        print(json.dumps(birefnet_leg(ctx, max(1, args.steps // 10), 2)), flush=True)
+        return
     image = synthetic.esrgan_image(H, W)
     model = ien.Model(ctx, ien.MODEL_REALESRGAN, tensors=tensors)
     d_in = torch.from_numpy(image).cuda()
@@ -343,7 +418,8 @@ def main():
 
     gemm_sweep = None if args.no_sweep else sweep(ctx, stream, args.kernel_reps)
     models = None if args.no_models else {"scunet": scunet_leg(ctx, max(5, args.steps // 20), 2),
-                                          "lama": lama_leg(ctx, max(5, args.steps // 20), 2)}
+                                          "lama": lama_leg(ctx, max(5, args.steps // 20), 2),
+                                          "birefnet": birefnet_leg(ctx, max(5, args.steps // 20), 2)}
     cpu = None if args.no_cpu else cpu_baseline(tensors, image)
 
     line = {

@@ -1,0 +1,742 @@
+// birefnet.hip -- BiRefNet-lite on the GPU (crates/birefnet-native/src/
+// lib.rs:144-171 run_normalized, swin.rs, decoder.rs): f16 NHWC maps.
+//  - Backbone: the 4x4 patch embedding as rows (ky, kx, c) through a
+//    product and a LayerNorm; the Swin blocks through ien_swin (windows of
+//    7 or 12, shift window / 2, -100 between regions, zero rows past the
+//    edge); stage outputs normalised into the decoder's level maps; 2x2
+//    merges as column-major gathers, LayerNorm over 4c and a product.
+//  - Decoder: 3x3 convolutions through the implicit-GEMM kernels; the ASPP's
+//    pooling branch as a two-pass column mean and a one-workgroup pass of
+//    its two small products (a bias for conv1), its four branches as k x k
+//    convolutions into the columns of one 1024-channel map (the network is
+//    deformable-free: all-zero offset and modulator convolutions sample the
+//    integer taps with modulator 2 sigmoid(0) = 1, decoder.rs:254-313), and
+//    conv1 accumulated onto that bias; the gate as a 3x3 convolution to 16
+//    channels and a per-pixel sigmoid scale; the image-to-patches stacks;
+//    the head before the final resize; the full-resolution branch as its
+//    composed 5x5 convolution inside the edge ring and both convolutions on
+//    the ring (decoder.rs:594-757).
+// One event is recorded after each of 14 steps (the 2 x 4 backbone stages,
+// the squeeze and the four decoder blocks, the head) for progress reports.
+
+#include <cmath>
+#include <string>
+
+#include "birefnet.h"
+#include "conv_common.h"
+
+namespace ien {
+
+namespace {
+
+constexpr int INTER = 64, BRANCH = 256;
+constexpr int STAGE_C[4] = {96, 192, 384, 768};
+constexpr int STAGE_DEPTH[4] = {2, 2, 6, 2};
+constexpr int ASPP_SIZES[4] = {1, 1, 3, 7};
+constexpr int LEVEL_CIN[4] = {1728, 960, 480, 240};   // decoder.rs:776
+constexpr int LEVEL_COUT[4] = {768, 384, 192, 96};
+constexpr int PATCH_CIN[4] = {3072, 768, 192, 48};   // patches5..2
+constexpr int PATCH_COUT[4] = {192, 192, 96, 48};
+constexpr int SQUEEZE_CIN = 2880, SQUEEZE_COUT = 1536;
+constexpr float MASKED = -100.0f;  // swin.rs:21-23
+constexpr int POOL_PARTS = 256;    // partial sums of the ASPP's column mean
+
+unsigned blocks_for(long items, int per) { return (unsigned)((items + per - 1) / per); }
+
+// swin.rs:190-196: token r's row of 48 values, (ky, kx, c) over its 4 x 4
+// patch of the f16 image; one thread per (token, ky): 12 halves.
+__global__ __launch_bounds__(256) void k_patch_rows(const uint16_t *__restrict__ img, int side,
+                                                    uint16_t *__restrict__ rows) {
+  const int grid = side / 4;
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (long)grid * grid * 4) return;
+  const long r = i / 4;
+  const int ky = (int)(i % 4);
+  const int ty = (int)(r / grid), tx = (int)(r % grid);
+  const uint16_t *s = img + ((long)(ty * 4 + ky) * side + tx * 4) * 3;
+  uint16_t *d = rows + r * 48 + ky * 12;
+#pragma unroll
+  for (int e = 0; e < 12; e++) d[e] = s[e];
+}
+
+// Columns 0..c of `rows` rows, src rows `ss` halves apart, into dst rows
+// `ds` apart (decoder.rs:523-533 place); 8 halves per thread.
+__global__ __launch_bounds__(256) void k_copy_cols(const uint16_t *__restrict__ src, long rows,
+                                                   int c, long ss, uint16_t *__restrict__ dst,
+                                                   long ds) {
+  const int chunks = c / 8;
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= rows * chunks) return;
+  const long r = i / chunks;
+  const int k = (int)(i % chunks);
+  *(u32x4 *)(dst + r * ds + 8 * k) = *(const u32x4 *)(src + r * ss + 8 * k);
+}
+
+// ASPP pooling, pass 1 (decoder.rs:140-150): part b of POOL_PARTS sums the
+// 64 channels over its rows in f32 (4 row groups of 64 lanes, combined in
+// a fixed order: the result does not depend on timing).
+__global__ __launch_bounds__(256) void k_pool_partial(const uint16_t *__restrict__ t, long rows,
+                                                      float *__restrict__ partial) {
+  __shared__ float part[4][INTER];
+  const int ch = threadIdx.x % INTER, g = threadIdx.x / INTER;
+  const long per = (rows + POOL_PARTS - 1) / POOL_PARTS;
+  const long r0 = (long)blockIdx.x * per, r1 = r0 + per < rows ? r0 + per : rows;
+  float s = 0.0f;
+  for (long r = r0 + g; r < r1; r += 4) s += h2f(t[r * INTER + ch]);
+  part[g][ch] = s;
+  __syncthreads();
+  if (g == 0) partial[blockIdx.x * INTER + ch] = ((part[0][ch] + part[1][ch]) + part[2][ch]) + part[3][ch];
+}
+
+// Pass 2, one workgroup: the mean, the pooling product (64 -> 256) + ReLU,
+// and its share of conv1 (256 -> 64) plus conv1's bias: the bias every
+// pixel of conv1 gets (decoder.rs:150-170).  pool: [64][256] weight, [256]
+// bias, [256][64] conv1 rows, [64] conv1 bias.
+__global__ __launch_bounds__(256) void k_pool_finish(const float *__restrict__ partial, long rows,
+                                                     const float *__restrict__ pool,
+                                                     float *__restrict__ bias) {
+  __shared__ float mean[INTER];
+  __shared__ float pooled[BRANCH];
+  const int tid = threadIdx.x;
+  if (tid < INTER) {
+    double s = 0.0;
+    for (int b = 0; b < POOL_PARTS; b++) s += (double)partial[b * INTER + tid];
+    mean[tid] = (float)(s / (double)rows);
+  }
+  __syncthreads();
+  const float *pw = pool, *pb = pool + INTER * BRANCH, *cw = pb + BRANCH, *cb = cw + BRANCH * INTER;
+  {
+    float p = pb[tid];
+    for (int c = 0; c < INTER; c++) p += mean[c] * pw[c * BRANCH + tid];
+    pooled[tid] = p > 0.0f ? p : 0.0f;
+  }
+  __syncthreads();
+  if (tid < INTER) {
+    float b = cb[tid];
+    for (int j = 0; j < BRANCH; j++) b += pooled[j] * cw[j * INTER + tid];
+    bias[tid] = b;
+  }
+}
+
+// Every row of a rows x 64 map set to the (f16-rounded) bias.
+__global__ __launch_bounds__(256) void k_fill_rows(uint16_t *__restrict__ x, long rows,
+                                                   const float *__restrict__ bias) {
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= rows * INTER) return;
+  x[i] = f2h(bias[i % INTER]);
+}
+
+// decoder.rs:378-401 the gate: out[p] *= sigmoid(b + sum_k g[p][k] w[k]),
+// one thread per 8 channels of a pixel.
+struct GateW {
+  float w[16];
+  float b;
+};
+__global__ __launch_bounds__(256) void k_gate(uint16_t *__restrict__ out, long rows, int c,
+                                              const uint16_t *__restrict__ g, GateW gw) {
+  const int chunks = c / 8;
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= rows * chunks) return;
+  const long p = i / chunks;
+  const int k = (int)(i % chunks);
+  float s = gw.b;
+#pragma unroll
+  for (int j = 0; j < 16; j++) s = s + h2f(g[p * 16 + j]) * gw.w[j];
+  s = sigmoid_f(s);
+  u32x4 *o = (u32x4 *)(out + p * c + 8 * k);
+  u32x4 v = *o;
+  uint16_t h[8];
+  __builtin_memcpy(h, &v, 16);
+#pragma unroll
+  for (int e = 0; e < 8; e++) h[e] = f2h(h2f(h[e]) * s);
+  __builtin_memcpy(&v, h, 16);
+  *o = v;
+}
+
+// decoder.rs:546-577 image2patches: pixel (y, x) of the size x size stack,
+// channel (c grid + gy) grid + gx = image pixel (gy size + y, gx size + x),
+// colour c.
+__global__ __launch_bounds__(256) void k_image_patches(const uint16_t *__restrict__ img, int side,
+                                                       int size, uint16_t *__restrict__ out) {
+  const int grid = side / size, channels = 3 * grid * grid;
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (long)size * size * channels) return;
+  const long p = i / channels;
+  const int ch = (int)(i % channels);
+  const int y = (int)(p / size), x = (int)(p % size);
+  const int c = ch / (grid * grid), gy = (ch / grid) % grid, gx = ch % grid;
+  out[i] = img[((long)(gy * size + y) * side + gx * size + x) * 3 + c];
+}
+
+// decoder.rs:737-757: head bias plus the composed 5x5 convolution of the f32
+// image at every pixel inside the edge ring (the bias, then each tap's three
+// products in order; zero outside the image).  full: [25][3] weights, bias.
+__global__ __launch_bounds__(256) void k_full_interior(const float *__restrict__ image, int side,
+                                                       const float *__restrict__ full,
+                                                       float head_bias, float *__restrict__ out) {
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (long)side * side) return;
+  const int y = (int)(i / side), x = (int)(i % side);
+  if (y == 0 || x == 0 || y == side - 1 || x == side - 1) return;
+  float s = full[75];
+  for (int e = 0; e < 25; e++) {
+    const int py = y + e / 5 - 2, px = x + e % 5 - 2;
+    float p0 = 0.0f, p1 = 0.0f, p2 = 0.0f;
+    if (py >= 0 && px >= 0 && py < side && px < side) {
+      const float *p = image + ((long)py * side + px) * 3;
+      p0 = p[0];
+      p1 = p[1];
+      p2 = p[2];
+    }
+    s += full[3 * e] * p0 + full[3 * e + 1] * p1 + full[3 * e + 2] * p2;
+  }
+  out[i] = head_bias + s;
+}
+
+// decoder.rs:700-734 on the edge ring: both 3x3 convolutions one after the
+// other (the intermediate map's zero padding is reached).  One wave per
+// ring pixel, lane k = intermediate channel k.  full + 76: conv1 [27][64],
+// bias1 [64], conv_out [9][64], bias_out.
+__global__ __launch_bounds__(64) void k_full_ring(const float *__restrict__ image, int side,
+                                                  const float *__restrict__ full, float head_bias,
+                                                  float *__restrict__ out) {
+  const int ring = blockIdx.x, k = threadIdx.x;
+  // Ring pixel -> (y, x): the top row, the bottom row, then the left and
+  // right columns between them.
+  int y, x;
+  if (ring < side) {
+    y = 0;
+    x = ring;
+  } else if (ring < 2 * side) {
+    y = side - 1;
+    x = ring - side;
+  } else {
+    const int r = ring - 2 * side;  // < 2 (side - 2)
+    y = 1 + r / 2;
+    x = (r & 1) ? side - 1 : 0;
+  }
+  const float *c1 = full + 76, *b1 = c1 + 27 * INTER, *co = b1 + INTER, *bo = co + 9 * INTER;
+  float s = 0.0f;
+  for (int d = 0; d < 9; d++) {
+    const int qy = y + d / 3 - 1, qx = x + d % 3 - 1;
+    if (qy < 0 || qx < 0 || qy >= side || qx >= side) continue;
+    float m = b1[k];
+    for (int e = 0; e < 9; e++) {
+      const int py = qy + e / 3 - 1, px = qx + e % 3 - 1;
+      if (py < 0 || px < 0 || py >= side || px >= side) continue;
+      const float *p = image + ((long)py * side + px) * 3;
+      for (int c = 0; c < 3; c++) m += p[c] * c1[(e * 3 + c) * INTER + k];
+    }
+    float v = m * co[d * INTER + k];
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+    s += v;
+  }
+  if (k == 0) out[(long)y * side + x] = head_bias + (bo[0] + s);
+}
+
+ien_status matrix(ien_ctx *ctx, const TensorSource &take, const std::string &name, size_t k,
+                  size_t n, bool bias, ien_matrix **out) {
+  std::vector<float> w, b;
+  ien_status st = take(name + ".weight", {k, n}, &w);
+  if (st == IEN_OK && bias) st = take(name + ".bias", {n}, &b);
+  if (st != IEN_OK) return st;
+  return ien_matrix_new(ctx, w.data(), IEN_W_F32, k, n, bias ? b.data() : nullptr, out);
+}
+
+ien_status upload(const std::vector<float> &v, float **d) {
+  IEN_HIP(hipMalloc((void **)d, v.size() * 4));
+  IEN_HIP(hipMemcpy(*d, v.data(), v.size() * 4, hipMemcpyHostToDevice));
+  return IEN_OK;
+}
+
+// gamma then beta of a LayerNorm over c, onto the device.
+ien_status norm(const TensorSource &take, const std::string &name, size_t c, float **d) {
+  std::vector<float> g, b;
+  ien_status st = take(name + ".weight", {c}, &g);
+  if (st == IEN_OK) st = take(name + ".bias", {c}, &b);
+  if (st != IEN_OK) return st;
+  g.insert(g.end(), b.begin(), b.end());
+  return upload(g, d);
+}
+
+// decoder.rs:316-343 Block::load and :102-136 Aspp::load.
+ien_status load_block(ien_ctx *ctx, const TensorSource &take, const std::string &q, int cin,
+                      int cout, bool gate, BirefnetBlock *B) {
+  B->cin = cin;
+  B->cout = cout;
+  B->gate = gate;
+  ien_status st = matrix(ctx, take, q + ".conv_in", 9 * (size_t)cin, INTER, true, &B->conv_in);
+  if (st == IEN_OK) st = matrix(ctx, take, q + ".conv_out", 9 * INTER, cout, true, &B->conv_out);
+  if (st == IEN_OK && gate) {
+    st = matrix(ctx, take, q + ".gdt", 9 * (size_t)cout, 16, true, &B->gdt);
+    std::vector<float> w, b;
+    if (st == IEN_OK) st = take(q + ".gdt_attn.weight", {16, 1}, &w);
+    if (st == IEN_OK) st = take(q + ".gdt_attn.bias", {1}, &b);
+    if (st == IEN_OK) {
+      for (int j = 0; j < 16; j++) B->gdt_w[j] = w[j];
+      B->gdt_b = b[0];
+    }
+  }
+  for (int i = 0; i < 4 && st == IEN_OK; i++) {
+    const size_t taps = (size_t)ASPP_SIZES[i] * ASPP_SIZES[i];
+    const std::string p = q + ".aspp.branch" + std::to_string(i);
+    std::vector<float> ow, ob;
+    st = take(p + ".offset.weight", {taps * INTER, 3 * taps}, &ow);
+    if (st == IEN_OK) st = take(p + ".offset.bias", {3 * taps}, &ob);
+    if (st != IEN_OK) break;
+    // The deformable-free network: zero offsets and modulator logits.
+    for (float v : ow)
+      if (v != 0.0f) return fail(IEN_ERR_WEIGHTS, "%s: deformable offsets are not supported", p.c_str());
+    for (float v : ob)
+      if (v != 0.0f) return fail(IEN_ERR_WEIGHTS, "%s: deformable offsets are not supported", p.c_str());
+    st = matrix(ctx, take, p, taps * INTER, BRANCH, true, &B->branch[i]);
+  }
+  if (st != IEN_OK) return st;
+  std::vector<float> pw, pb, cw, cb;
+  st = take(q + ".aspp.pool.weight", {INTER, BRANCH}, &pw);
+  if (st == IEN_OK) st = take(q + ".aspp.pool.bias", {BRANCH}, &pb);
+  if (st == IEN_OK) st = take(q + ".aspp.conv1.weight", {5 * BRANCH, INTER}, &cw);
+  if (st == IEN_OK) st = take(q + ".aspp.conv1.bias", {INTER}, &cb);
+  if (st != IEN_OK) return st;
+  // conv1's first 4 x 256 rows read the branches; its last 256 the pooling.
+  st = ien_matrix_new(ctx, cw.data(), IEN_W_F32, 4 * BRANCH, INTER, nullptr, &B->conv1);
+  if (st != IEN_OK) return st;
+  std::vector<float> pool(pw);
+  pool.insert(pool.end(), pb.begin(), pb.end());
+  pool.insert(pool.end(), cw.begin() + 4 * BRANCH * INTER, cw.end());
+  pool.insert(pool.end(), cb.begin(), cb.end());
+  return upload(pool, &B->d_pool);
+}
+
+void free_block(BirefnetBlock &B) {
+  ien_matrix_free(B.conv_in);
+  ien_matrix_free(B.conv_out);
+  ien_matrix_free(B.conv1);
+  ien_matrix_free(B.gdt);
+  for (auto *m : B.branch) ien_matrix_free(m);
+  (void)hipFree(B.d_pool);
+}
+
+void free_maps(Birefnet &b) {
+  for (uint16_t **p : {&b.img16, &b.half16, &b.prow, &b.x, &b.mrows, &b.level[0], &b.level[1],
+                       &b.level[2], &b.level[3], &b.tmp, &b.x4, &b.in, &b.t, &b.a, &b.cat, &b.g,
+                       &b.prev, &b.stacked, &b.mid, &b.low}) {
+    (void)hipFree(*p);
+    *p = nullptr;
+  }
+  (void)hipFree(b.partial);
+  (void)hipFree(b.d_bias);
+  b.partial = b.d_bias = nullptr;
+  b.side = 0;
+}
+
+// A size x size stride-1 convolution (zero padding) of an h x w f16 map.
+ien_status conv(ien_ctx *ctx, const uint16_t *x, int h, int w, int c, long xs, int size,
+                const ien_matrix *m, uint16_t *y, long ys, ien_act act, int accumulate) {
+  ConvCall cc;
+  cc.x = x;
+  cc.H = h;
+  cc.W = w;
+  cc.C = c;
+  cc.xs = xs;
+  cc.ks = size;
+  cc.stride = 1;
+  cc.OH = h;
+  cc.OW = w;
+  cc.row0 = 0;
+  cc.rows = (long)h * w;
+  cc.w = m;
+  cc.y = y;
+  cc.ys = ys;
+  cc.act = act;
+  cc.accumulate = accumulate;
+  return launch_conv(ctx, cc);
+}
+
+ien_status rows_product(ien_ctx *ctx, const uint16_t *in, size_t k, long xs, size_t rows,
+                        const ien_matrix *m, uint16_t *out, long ys, ien_act act, int accumulate) {
+  ConvCall cc;
+  cc.x = in;
+  cc.rows_mode = 1;
+  cc.C = (int)k;
+  cc.xs = xs;
+  cc.ks = 1;
+  cc.stride = 1;
+  cc.row0 = 0;
+  cc.rows = (long)rows;
+  cc.w = m;
+  cc.y = out;
+  cc.ys = ys;
+  cc.act = act;
+  cc.accumulate = accumulate;
+  return launch_conv(ctx, cc);
+}
+
+ien_status copy_cols(ien_ctx *ctx, const uint16_t *src, long rows, int c, long ss, uint16_t *dst,
+                     long ds) {
+  IEN_CHECK(c % 8 == 0 && ss % 8 == 0 && ds % 8 == 0 && ((uintptr_t)src & 15) == 0 &&
+                ((uintptr_t)dst & 15) == 0,
+            IEN_ERR_INPUT, "column copy of %d of %ld / %ld", c, ss, ds);
+  hipLaunchKernelGGL(k_copy_cols, dim3(blocks_for(rows * (c / 8), 256)), dim3(256), 0,
+                     ctx->stream, src, rows, c, ss, dst, ds);
+  IEN_HIP(hipGetLastError());
+  return IEN_OK;
+}
+
+// decoder.rs:346-413 Block::run: in (h x w x cin) -> out (h x w x cout).
+ien_status block_run(Birefnet *b, const BirefnetBlock &B, const uint16_t *in, int h, int w,
+                     uint16_t *out) {
+  ien_ctx *ctx = b->ctx;
+  const long pixels = (long)h * w;
+  ien_status st = conv(ctx, in, h, w, B.cin, B.cin, 3, B.conv_in, b->t, INTER, IEN_ACT_RELU, 0);
+  if (st != IEN_OK) return st;
+  hipLaunchKernelGGL(k_pool_partial, dim3(POOL_PARTS), dim3(256), 0, ctx->stream, b->t, pixels,
+                     b->partial);
+  hipLaunchKernelGGL(k_pool_finish, dim3(1), dim3(256), 0, ctx->stream, b->partial, pixels,
+                     B.d_pool, b->d_bias);
+  IEN_HIP(hipGetLastError());
+  for (int i = 0; i < 4 && st == IEN_OK; i++)
+    st = conv(ctx, b->t, h, w, INTER, INTER, ASPP_SIZES[i], B.branch[i], b->cat + i * BRANCH,
+              4 * BRANCH, IEN_ACT_RELU, 0);
+  if (st != IEN_OK) return st;
+  hipLaunchKernelGGL(k_fill_rows, dim3(blocks_for(pixels * INTER, 256)), dim3(256), 0, ctx->stream,
+                     b->a, pixels, b->d_bias);
+  IEN_HIP(hipGetLastError());
+  st = rows_product(ctx, b->cat, 4 * BRANCH, 4 * BRANCH, pixels, B.conv1, b->a, INTER,
+                    IEN_ACT_RELU, 1);
+  if (st == IEN_OK)
+    st = conv(ctx, b->a, h, w, INTER, INTER, 3, B.conv_out, out, B.cout, IEN_ACT_NONE, 0);
+  if (st == IEN_OK && B.gate) {
+    st = conv(ctx, out, h, w, B.cout, B.cout, 3, B.gdt, b->g, 16, IEN_ACT_RELU, 0);
+    if (st != IEN_OK) return st;
+    GateW gw;
+    for (int j = 0; j < 16; j++) gw.w[j] = B.gdt_w[j];
+    gw.b = B.gdt_b;
+    hipLaunchKernelGGL(k_gate, dim3(blocks_for(pixels * (B.cout / 8), 256)), dim3(256), 0,
+                       ctx->stream, out, pixels, B.cout, b->g, gw);
+    IEN_HIP(hipGetLastError());
+  }
+  return st;
+}
+
+// swin.rs:171-215 Backbone::run on the f16 image `img` (side x side x 3):
+// each stage's normalised output into level buffer s (columns `col` of
+// rows 2 c wide) directly for the full size, through `tmp` and a resize for
+// the half size.
+ien_status backbone_run(Birefnet *b, const uint16_t *img, int side, bool half,
+                        hipEvent_t *events, int *step) {
+  ien_ctx *ctx = b->ctx;
+  int grid = side / 4;
+  const long tokens = (long)grid * grid;
+  hipLaunchKernelGGL(k_patch_rows, dim3(blocks_for(tokens * 4, 256)), dim3(256), 0, ctx->stream,
+                     img, side, b->prow);
+  IEN_HIP(hipGetLastError());
+  ien_status st = rows_product(ctx, b->prow, 48, 48, tokens, b->embed, b->x, 96, IEN_ACT_NONE, 0);
+  if (st == IEN_OK) st = ien_layer_norm(ctx, b->x, tokens, 96, 96, b->d_embed_ln, b->d_embed_ln + 96);
+  for (int s = 0; s < 4 && st == IEN_OK; s++) {
+    const int c = STAGE_C[s];
+    for (ien_swin *blk : b->blocks[s]) {
+      st = ien_swin_run(blk, b->x, c, grid, grid);
+      if (st != IEN_OK) return st;
+    }
+    const long n = (long)grid * grid;
+    if (!half) {
+      st = copy_cols(ctx, b->x, n, c, c, b->level[s], 2L * c);
+      if (st == IEN_OK)
+        st = ien_layer_norm(ctx, b->level[s], n, c, 2 * c, b->d_norm[s], b->d_norm[s] + c);
+    } else {
+      // The half-size map, normalised, then resized to the full grid.
+      st = copy_cols(ctx, b->x, n, c, c, b->tmp, c);
+      if (st == IEN_OK) st = ien_layer_norm(ctx, b->tmp, n, c, c, b->d_norm[s], b->d_norm[s] + c);
+      if (st == IEN_OK)
+        st = ien_resize(ctx, b->tmp, grid, grid, c, c, b->level[s] + c, 2 * grid, 2 * grid, 2 * c,
+                        IEN_OUT_F16, 0);
+    }
+    if (st == IEN_OK && s < 3) {
+      // swin.rs:377-405 merge: (0,0), (1,0), (0,1), (1,1) by (row, column).
+      st = ien_gather_2x2(ctx, b->x, grid, grid, c, c, IEN_ORDER_COLUMN_MAJOR, b->mrows);
+      const long half_tokens = n / 4;
+      if (st == IEN_OK)
+        st = ien_layer_norm(ctx, b->mrows, half_tokens, 4 * c, 4 * c, b->d_merge_ln[s],
+                            b->d_merge_ln[s] + 4 * c);
+      if (st == IEN_OK)
+        st = rows_product(ctx, b->mrows, 4 * c, 4 * c, half_tokens, b->merge[s], b->x, 2 * c,
+                          IEN_ACT_NONE, 0);
+      grid /= 2;
+    }
+    if (st == IEN_OK && events) IEN_HIP(hipEventRecord(events[*step], ctx->stream));
+    ++*step;
+  }
+  return st;
+}
+
+}  // namespace
+
+// swin.rs:110-169 Backbone::load, decoder.rs:779-811 Decoder::load.
+ien_status birefnet_load(ien_ctx *ctx, const TensorSource &take, const ShapeOf &shape,
+                         Birefnet *b) {
+  b->ctx = ctx;
+  std::vector<size_t> ps;
+  if (!shape("stage0.block0.position_bias", &ps) || ps.size() != 3 || ps[1] != ps[2])
+    return fail(IEN_ERR_WEIGHTS, "stage0.block0.position_bias: missing or not [heads][N][N]");
+  int window = 1;
+  while ((size_t)(window * window) < ps[1]) window++;
+  IEN_CHECK((size_t)(window * window) == ps[1] && window >= 2 && window <= 16, IEN_ERR_WEIGHTS,
+            "position bias of %zu tokens: not a square window of at most 16", ps[1]);
+  b->window = window;
+  const size_t N = (size_t)window * window;
+  ien_status st = matrix(ctx, take, "patch_embed", 48, 96, true, &b->embed);
+  if (st == IEN_OK) st = norm(take, "patch_embed.norm", 96, &b->d_embed_ln);
+  for (int s = 0; s < 4 && st == IEN_OK; s++) {
+    const size_t c = STAGE_C[s], heads = c / 32;
+    for (int k = 0; k < STAGE_DEPTH[s] && st == IEN_OK; k++) {
+      const std::string p = "stage" + std::to_string(s) + ".block" + std::to_string(k) + ".";
+      std::vector<float> g1, b1, qw, qb, pos, pw, pb, g2, b2, f1w, f1b, f2w, f2b;
+      if ((st = take(p + "norm1.weight", {c}, &g1)) != IEN_OK) break;
+      if ((st = take(p + "norm1.bias", {c}, &b1)) != IEN_OK) break;
+      if ((st = take(p + "qkv.weight", {c, 3 * c}, &qw)) != IEN_OK) break;
+      if ((st = take(p + "qkv.bias", {3 * c}, &qb)) != IEN_OK) break;
+      if ((st = take(p + "position_bias", {heads, N, N}, &pos)) != IEN_OK) break;
+      if ((st = take(p + "proj.weight", {c, c}, &pw)) != IEN_OK) break;
+      if ((st = take(p + "proj.bias", {c}, &pb)) != IEN_OK) break;
+      if ((st = take(p + "norm2.weight", {c}, &g2)) != IEN_OK) break;
+      if ((st = take(p + "norm2.bias", {c}, &b2)) != IEN_OK) break;
+      if ((st = take(p + "fc1.weight", {c, 4 * c}, &f1w)) != IEN_OK) break;
+      if ((st = take(p + "fc1.bias", {4 * c}, &f1b)) != IEN_OK) break;
+      if ((st = take(p + "fc2.weight", {4 * c, c}, &f2w)) != IEN_OK) break;
+      if ((st = take(p + "fc2.bias", {c}, &f2b)) != IEN_OK) break;
+      ien_swin_weights sw{};
+      sw.c = (int)c;
+      sw.window = window;
+      sw.shift = k % 2 == 1 ? window / 2 : 0;
+      sw.masked = MASKED;
+      sw.ln1_gamma = g1.data();
+      sw.ln1_beta = b1.data();
+      sw.qkv_w = qw.data();
+      sw.qkv_b = qb.data();
+      sw.position = pos.data();
+      sw.proj_w = pw.data();
+      sw.proj_b = pb.data();
+      sw.ln2_gamma = g2.data();
+      sw.ln2_beta = b2.data();
+      sw.fc1_w = f1w.data();
+      sw.fc1_b = f1b.data();
+      sw.fc2_w = f2w.data();
+      sw.fc2_b = f2b.data();
+      ien_swin *blk = nullptr;
+      st = ien_swin_new(ctx, &sw, &blk);
+      if (st == IEN_OK) b->blocks[s].push_back(blk);
+    }
+    if (st == IEN_OK && s < 3) {
+      const std::string p = "stage" + std::to_string(s) + ".merge";
+      st = norm(take, p + ".norm", 4 * c, &b->d_merge_ln[s]);
+      if (st == IEN_OK) st = matrix(ctx, take, p, 4 * c, 2 * c, false, &b->merge[s]);
+    }
+    if (st == IEN_OK) st = norm(take, "stage" + std::to_string(s) + ".norm", c, &b->d_norm[s]);
+  }
+  if (st == IEN_OK)
+    st = load_block(ctx, take, "squeeze", SQUEEZE_CIN, SQUEEZE_COUT, false, &b->dec[0]);
+  for (int i = 0; i < 4 && st == IEN_OK; i++)
+    st = load_block(ctx, take, "block" + std::to_string(4 - i), LEVEL_CIN[i], LEVEL_COUT[i], i < 3,
+                    &b->dec[i + 1]);
+  const int lat_c[3] = {768, 384, 192};
+  for (int i = 0; i < 3 && st == IEN_OK; i++)
+    st = matrix(ctx, take, "lateral" + std::to_string(4 - i), lat_c[i], lat_c[i], true,
+                &b->lateral[i]);
+  for (int i = 0; i < 4 && st == IEN_OK; i++) {
+    const std::string p = "patches" + std::to_string(5 - i);
+    st = matrix(ctx, take, p + ".conv1", 9 * (size_t)PATCH_CIN[i], INTER, true, &b->patch_conv1[i]);
+    if (st == IEN_OK)
+      st = matrix(ctx, take, p + ".conv_out", 9 * INTER, PATCH_COUT[i], true, &b->patch_out[i]);
+  }
+  if (st == IEN_OK) st = matrix(ctx, take, "head", 96, 1, false, &b->head);
+  if (st == IEN_OK) {
+    std::vector<float> hb, c1, b1, co, bo;
+    st = take("head.bias", {1}, &hb);
+    if (st == IEN_OK) st = take("patches1.conv1.weight", {27, INTER}, &c1);
+    if (st == IEN_OK) st = take("patches1.conv1.bias", {INTER}, &b1);
+    if (st == IEN_OK) st = take("patches1.conv_out.weight", {9 * INTER, 1}, &co);
+    if (st == IEN_OK) st = take("patches1.conv_out.bias", {1}, &bo);
+    if (st != IEN_OK) return st;
+    b->head_bias = hb[0];
+    // decoder.rs:604-630: the composed 5x5 weights and bias, summed in f64.
+    double composed[75] = {0};
+    double cb = bo[0];
+    for (int d = 0; d < 9; d++)
+      for (int k = 0; k < INTER; k++) {
+        const double w2 = co[d * INTER + k];
+        cb += w2 * b1[k];
+        for (int e = 0; e < 9; e++) {
+          const int ey = d / 3 + e / 3, ex = d % 3 + e % 3;
+          for (int c = 0; c < 3; c++) composed[(ey * 5 + ex) * 3 + c] += w2 * c1[(e * 3 + c) * INTER + k];
+        }
+      }
+    std::vector<float> full(76);
+    for (int i = 0; i < 75; i++) full[i] = (float)composed[i];
+    full[75] = (float)cb;
+    full.insert(full.end(), c1.begin(), c1.end());
+    full.insert(full.end(), b1.begin(), b1.end());
+    full.insert(full.end(), co.begin(), co.end());
+    full.push_back(bo[0]);
+    st = upload(full, &b->d_full);
+  }
+  return st;
+}
+
+void birefnet_free(Birefnet *b) {
+  ien_matrix_free(b->embed);
+  (void)hipFree(b->d_embed_ln);
+  for (int s = 0; s < 4; s++) {
+    for (ien_swin *blk : b->blocks[s]) ien_swin_free(blk);
+    b->blocks[s].clear();
+    (void)hipFree(b->d_norm[s]);
+  }
+  for (int s = 0; s < 3; s++) {
+    (void)hipFree(b->d_merge_ln[s]);
+    ien_matrix_free(b->merge[s]);
+    ien_matrix_free(b->lateral[s]);
+  }
+  for (auto &B : b->dec) free_block(B);
+  for (int i = 0; i < 4; i++) {
+    ien_matrix_free(b->patch_conv1[i]);
+    ien_matrix_free(b->patch_out[i]);
+  }
+  ien_matrix_free(b->head);
+  (void)hipFree(b->d_full);
+  free_maps(*b);
+  (void)hipFree(b->d_in);
+  (void)hipFree(b->d_out);
+}
+
+// At side S (P = S^2 pixels): img16 3P, half16 3P/4; patch rows P/16 x 48;
+// token map x and merge rows P/16 x 96 (every stage's map holds at most
+// that); level s (S/2^(s+2))^2 x 2 c_s; tmp P/64 x 96 (the half run's
+// stage maps); x4 (S/32)^2 x 2880; the decoder's input P/16 x 240 (every
+// level's g^2 cin is at most that), t and a P/16 x 64, cat P/16 x 1024,
+// g P/16 x 16, prev P/16 x 96 (every block's g^2 cout is at most that),
+// stacked 3P, mid P/16 x 64, low P/16.
+ien_status birefnet_reserve(Birefnet *b, size_t side, bool *grew) {
+  *grew = false;
+  IEN_CHECK(side >= 64 && side % 64 == 0 && side <= 8192, IEN_ERR_INPUT,
+            "side %zu: a multiple of 64 (at most 8192)", side);
+  for (int s = 0; s < 4; s++)
+    for (ien_swin *blk : b->blocks[s]) {
+      ien_status st = swin_reserve(blk, (int)(side >> (s + 2)), (int)(side >> (s + 2)));
+      if (st != IEN_OK) return st;
+    }
+  if (side <= b->side) return IEN_OK;
+  IEN_HIP(hipStreamSynchronize(b->ctx->stream));
+  free_maps(*b);
+  *grew = true;
+  const size_t P = side * side, Q = P / 16;
+  auto alloc = [](uint16_t **p, size_t halves) { return hipMalloc((void **)p, halves * 2); };
+  hipError_t e = alloc(&b->img16, 3 * P);
+  if (e == hipSuccess) e = alloc(&b->half16, 3 * P / 4);
+  if (e == hipSuccess) e = alloc(&b->prow, Q * 48);
+  if (e == hipSuccess) e = alloc(&b->x, Q * 96);
+  if (e == hipSuccess) e = alloc(&b->mrows, Q * 96);
+  for (int s = 0; s < 4 && e == hipSuccess; s++) {
+    const size_t g = side >> (s + 2);
+    e = alloc(&b->level[s], g * g * 2 * STAGE_C[s]);
+  }
+  if (e == hipSuccess) e = alloc(&b->tmp, P / 64 * 96);
+  if (e == hipSuccess) e = alloc(&b->x4, (side / 32) * (side / 32) * SQUEEZE_CIN);
+  if (e == hipSuccess) e = alloc(&b->in, Q * 240);
+  if (e == hipSuccess) e = alloc(&b->t, Q * INTER);
+  if (e == hipSuccess) e = alloc(&b->a, Q * INTER);
+  if (e == hipSuccess) e = alloc(&b->cat, Q * 4 * BRANCH);
+  if (e == hipSuccess) e = alloc(&b->g, Q * 16);
+  if (e == hipSuccess) e = alloc(&b->prev, Q * 96);
+  if (e == hipSuccess) e = alloc(&b->stacked, 3 * P);
+  if (e == hipSuccess) e = alloc(&b->mid, Q * INTER);
+  if (e == hipSuccess) e = alloc(&b->low, Q);
+  if (e == hipSuccess) e = hipMalloc((void **)&b->partial, POOL_PARTS * INTER * 4);
+  if (e == hipSuccess) e = hipMalloc((void **)&b->d_bias, INTER * 4);
+  if (e != hipSuccess) {
+    free_maps(*b);
+    return fail(IEN_ERR_GPU, "BiRefNet maps for side %zu: %s", side, hipGetErrorString(e));
+  }
+  b->side = side;
+  return IEN_OK;
+}
+
+// lib.rs:144-171 run_normalized and decoder.rs:813-926 Decoder::run.
+ien_status birefnet_enqueue(Birefnet *b, const float *d_image, size_t side_, float *d_logits,
+                            hipEvent_t *events) {
+  ien_ctx *ctx = b->ctx;
+  IEN_CHECK(b->side >= side_ && side_ % 64 == 0, IEN_ERR_INPUT, "maps not reserved for side %zu",
+            side_);
+  const int side = (int)side_;
+  int step = 0;
+  ien_status st = ien_floats_to_halves(ctx, d_image, b->img16, (size_t)side * side * 3);
+  if (st == IEN_OK)
+    st = ien_resize(ctx, b->img16, side, side, 3, 3, b->half16, side / 2, side / 2, 3, IEN_OUT_F16,
+                    0);
+  if (st == IEN_OK) st = backbone_run(b, b->img16, side, false, events, &step);
+  if (st == IEN_OK) st = backbone_run(b, b->half16, side / 2, true, events, &step);
+  if (st != IEN_OK) return st;
+  // The squeeze block's input: levels 1..3 resized to level 4's grid, then
+  // level 4 (decoder.rs:840-859).
+  const int g4 = side >> 5;
+  int offset = 0;
+  for (int s = 0; s < 3 && st == IEN_OK; s++) {
+    const int g = side >> (s + 2), c = 2 * STAGE_C[s];
+    st = ien_resize(ctx, b->level[s], g, g, c, c, b->x4 + offset, g4, g4, SQUEEZE_CIN, IEN_OUT_F16,
+                    0);
+    offset += c;
+  }
+  if (st == IEN_OK)
+    st = copy_cols(ctx, b->level[3], (long)g4 * g4, 2 * STAGE_C[3], 2 * STAGE_C[3], b->x4 + offset,
+                   SQUEEZE_CIN);
+  if (st == IEN_OK) st = block_run(b, b->dec[0], b->x4, g4, g4, b->prev);
+  if (st == IEN_OK && events) IEN_HIP(hipEventRecord(events[step], ctx->stream));
+  step++;
+  int prev_grid = g4;
+  for (int i = 0; i < 4 && st == IEN_OK; i++) {
+    const int level = 3 - i, cin = LEVEL_CIN[i], g = side >> (level + 2);
+    const int main_c = i == 0 ? SQUEEZE_COUT : LEVEL_COUT[i - 1];
+    const long pixels = (long)g * g;
+    if (i == 0) {
+      st = copy_cols(ctx, b->prev, pixels, main_c, main_c, b->in, cin);
+    } else {
+      const int c = 2 * STAGE_C[level];
+      st = rows_product(ctx, b->level[level], c, c, pixels, b->lateral[i - 1], b->in, cin,
+                        IEN_ACT_NONE, 0);
+      if (st == IEN_OK)
+        st = ien_resize(ctx, b->prev, prev_grid, prev_grid, main_c, main_c, b->in, g, g, cin,
+                        IEN_OUT_F16, 1);
+    }
+    // decoder.rs:535-591: the image as patches of g x g, both convolutions.
+    if (st == IEN_OK) {
+      const int gp = side / g;
+      hipLaunchKernelGGL(k_image_patches, dim3(blocks_for(pixels * 3 * gp * gp, 256)), dim3(256), 0,
+                         ctx->stream, b->img16, side, g, b->stacked);
+      IEN_HIP(hipGetLastError());
+      st = conv(ctx, b->stacked, g, g, 3 * gp * gp, 3 * gp * gp, 3, b->patch_conv1[i], b->mid,
+                INTER, IEN_ACT_NONE, 0);
+    }
+    if (st == IEN_OK)
+      st = conv(ctx, b->mid, g, g, INTER, INTER, 3, b->patch_out[i], b->in + main_c, cin,
+                IEN_ACT_NONE, 0);
+    if (st == IEN_OK) st = block_run(b, b->dec[i + 1], b->in, g, g, b->prev);
+    if (st == IEN_OK && events) IEN_HIP(hipEventRecord(events[step], ctx->stream));
+    step++;
+    prev_grid = g;
+  }
+  if (st != IEN_OK) return st;
+  // The head before the final resize, then the full-resolution branch
+  // (decoder.rs:885-926).
+  const long low_pixels = (long)prev_grid * prev_grid;
+  st = rows_product(ctx, b->prev, 96, 96, low_pixels, b->head, b->low, 1, IEN_ACT_NONE, 0);
+  if (st != IEN_OK) return st;
+  hipLaunchKernelGGL(k_full_interior, dim3(blocks_for((long)side * side, 256)), dim3(256), 0,
+                     ctx->stream, d_image, side, b->d_full, b->head_bias, d_logits);
+  hipLaunchKernelGGL(k_full_ring, dim3((unsigned)(4 * side - 4)), dim3(64), 0, ctx->stream,
+                     d_image, side, b->d_full, b->head_bias, d_logits);
+  IEN_HIP(hipGetLastError());
+  st = ien_resize(ctx, b->low, prev_grid, prev_grid, 1, 1, d_logits, side, side, 1, IEN_OUT_F32, 1);
+  if (st == IEN_OK && events) IEN_HIP(hipEventRecord(events[step], ctx->stream));
+  return st;
+}
+
+}  // namespace ien

@@ -11,8 +11,8 @@
 // is captured once per image size and replayed, so the 36 launches cost one
 // submission.
 //
-// SCUNet and LaMa are objects of their own (scunet.hip, lama.hip) that this
-// file loads, sizes and runs the same way.
+// SCUNet, LaMa and BiRefNet are objects of their own (scunet.hip, lama.hip,
+// birefnet.hip) that this file loads, sizes and runs the same way.
 
 #include <cstring>
 #include <fstream>
@@ -20,6 +20,7 @@
 #include <map>
 #include <memory>
 
+#include "birefnet.h"
 #include "ien_internal.h"
 #include "lama.h"
 #include "scunet.h"
@@ -116,6 +117,14 @@ class WeightFile {
     return IEN_OK;
   }
 
+  // The shape of a stored tensor, without taking it.
+  bool shape_of(const std::string &name, std::vector<size_t> *shape) const {
+    auto it = tensors.find(name);
+    if (it == tensors.end()) return false;
+    *shape = it->second.shape;
+    return true;
+  }
+
   // weight_file.rs:139-145 finish
   ien_status finish() {
     if (!tensors.empty())
@@ -146,6 +155,7 @@ struct ien_model {
   std::vector<ien::EsrganLayer> layers;
   std::unique_ptr<ien::Scunet> scunet;  // IEN_MODEL_SCUNET
   std::unique_ptr<ien::Lama> lama;      // IEN_MODEL_LAMA
+  std::unique_ptr<ien::Birefnet> birefnet;  // IEN_MODEL_BIREFNET
   ien::Maps maps;
   bool use_graph = false;
   hipGraphExec_t graph = nullptr;
@@ -263,10 +273,17 @@ static ien_status enqueue_esrgan(ien_model *model, const float *d_image, size_t 
 
 // Steps of a run (progress reports) and output floats per input pixel.
 static int model_steps(const ien_model *m) {
-  return m->kind == IEN_MODEL_SCUNET ? SCUNET_STEPS : m->kind == IEN_MODEL_LAMA ? LAMA_STEPS : STEPS;
+  switch (m->kind) {
+    case IEN_MODEL_SCUNET: return SCUNET_STEPS;
+    case IEN_MODEL_LAMA: return LAMA_STEPS;
+    case IEN_MODEL_BIREFNET: return BIREFNET_STEPS;
+    default: return STEPS;
+  }
 }
 static size_t out_per_pixel(const ien_model *m) {
-  return m->kind == IEN_MODEL_REALESRGAN ? 3 * SCALE * SCALE : 3;
+  return m->kind == IEN_MODEL_REALESRGAN ? 3 * SCALE * SCALE
+         : m->kind == IEN_MODEL_BIREFNET ? 1
+                                         : 3;
 }
 
 // Maps for an image of this size, then its launches.
@@ -277,6 +294,12 @@ static ien_status prepare(ien_model *model, size_t width, size_t height) {
     const size_t before = model->scunet->pixels;
     ien_status st = scunet_reserve(model->scunet.get(), pw, ph);
     if (st == IEN_OK && model->scunet->pixels != before) drop_graph(model);
+    return st;
+  }
+  if (model->kind == IEN_MODEL_BIREFNET) {
+    bool grew = false;
+    ien_status st = birefnet_reserve(model->birefnet.get(), width, &grew);
+    if (grew) drop_graph(model);
     return st;
   }
   if (model->kind == IEN_MODEL_LAMA) {
@@ -294,6 +317,8 @@ static ien_status enqueue(ien_model *model, const float *d_image, const float *d
                           size_t width, size_t height, float *d_out, hipEvent_t *events) {
   if (model->kind == IEN_MODEL_LAMA)
     return lama_enqueue(model->lama.get(), d_image, d_mask, width, height, d_out, events);
+  if (model->kind == IEN_MODEL_BIREFNET)
+    return birefnet_enqueue(model->birefnet.get(), d_image, width, d_out, events);
   if (model->kind == IEN_MODEL_SCUNET)
     return scunet_enqueue(model->scunet.get(), d_image, width, height, d_out, events);
   return enqueue_esrgan(model, d_image, width, height, d_out, events);
@@ -302,6 +327,11 @@ static ien_status enqueue(ien_model *model, const float *d_image, const float *d
 static ien_status check_size(const ien_model *model, size_t width, size_t height) {
   // realesrgan-native lib.rs:302-316
   if (width == 0 || height == 0) return fail(IEN_ERR_INPUT, "empty %zu x %zu image", width, height);
+  // birefnet-native lib.rs:175-187: a square side x side image, side a
+  // positive multiple of 64.
+  if (model->kind == IEN_MODEL_BIREFNET && (width != height || width % 64 != 0))
+    return fail(IEN_ERR_INPUT, "%zu x %zu image: BiRefNet takes a square side, a multiple of 64",
+                width, height);
   // lama-native lib.rs:180-187: sides of at least 9.
   if (model->kind == IEN_MODEL_LAMA && (width < LAMA_MIN_SIDE || height < LAMA_MIN_SIDE))
     return fail(IEN_ERR_INPUT, "%zu x %zu image: sides of at least %zu pixels", width, height,
@@ -318,9 +348,10 @@ using namespace ien;
 extern "C" {
 
 static ien_status model_new(ien_ctx *ctx, ien_model_kind kind, const TensorSource &take,
-                            ien_model **out) {
+                            const ShapeOf &shape, ien_model **out) {
   IEN_CHECK(ctx && out, IEN_ERR_INPUT, "null argument");
-  IEN_CHECK(kind == IEN_MODEL_REALESRGAN || kind == IEN_MODEL_SCUNET || kind == IEN_MODEL_LAMA,
+  IEN_CHECK(kind == IEN_MODEL_REALESRGAN || kind == IEN_MODEL_SCUNET || kind == IEN_MODEL_LAMA ||
+                kind == IEN_MODEL_BIREFNET,
             IEN_ERR_INPUT, "model kind %d", (int)kind);
   IEN_HIP(hipSetDevice(ctx->device));
   std::unique_ptr<ien_model> model(new ien_model);
@@ -333,6 +364,9 @@ static ien_status model_new(ien_ctx *ctx, ien_model_kind kind, const TensorSourc
   } else if (kind == IEN_MODEL_LAMA) {
     model->lama.reset(new Lama);
     st = lama_load(ctx, take, model->lama.get());
+  } else if (kind == IEN_MODEL_BIREFNET) {
+    model->birefnet.reset(new Birefnet);
+    st = birefnet_load(ctx, take, shape, model->birefnet.get());
   } else {
     st = load_esrgan(model.get(), take);
   }
@@ -350,16 +384,18 @@ ien_status ien_model_load(ien_ctx *ctx, ien_model_kind kind, const char *weights
   WeightFile file;
   // The weights files' magics (realesrgan-native lib.rs:124, scunet-native
   // lib.rs:101, lama-native lib.rs:96).
-  ien_status st = file.read(weights_path, kind == IEN_MODEL_SCUNET ? "SCUNET\0\0"
-                                          : kind == IEN_MODEL_LAMA ? "LAMA\0\0\0\0"
-                                                                   : "REALESRG");
+  // birefnet-native lib.rs:84
+  ien_status st = file.read(weights_path, kind == IEN_MODEL_SCUNET     ? "SCUNET\0\0"
+                                          : kind == IEN_MODEL_LAMA     ? "LAMA\0\0\0\0"
+                                          : kind == IEN_MODEL_BIREFNET ? "BIREFNET"
+                                                                       : "REALESRG");
   if (st != IEN_OK) return st;
   st = model_new(
       ctx, kind,
       [&](const std::string &n, std::vector<size_t> s, std::vector<float> *o) {
         return file.take(n, s, o);
       },
-      out);
+      [&](const std::string &n, std::vector<size_t> *s) { return file.shape_of(n, s); }, out);
   if (st != IEN_OK) return st;
   st = file.finish();
   if (st != IEN_OK) {
@@ -391,7 +427,7 @@ ien_status ien_model_from_tensors(ien_ctx *ctx, ien_model_kind kind, const ien_t
       [&](const std::string &n, std::vector<size_t> s, std::vector<float> *o) {
         return file.take(n, s, o);
       },
-      out);
+      [&](const std::string &n, std::vector<size_t> *s) { return file.shape_of(n, s); }, out);
   if (st != IEN_OK) return st;
   st = file.finish();
   if (st != IEN_OK) {
@@ -414,6 +450,7 @@ void ien_model_free(ien_model *model) {
   }
   if (model->scunet) scunet_free(model->scunet.get());
   if (model->lama) lama_free(model->lama.get());
+  if (model->birefnet) birefnet_free(model->birefnet.get());
   free_maps(model->maps);
   delete model;
 }
@@ -500,6 +537,22 @@ ien_status ien_model_run(ien_model *model, const float *image, const float *mask
     d_mask = l.d_mask;
     d_out = l.d_out;
     IEN_HIP(hipMemcpyAsync(d_mask, mask, pixels * 4, hipMemcpyHostToDevice, ctx->stream));
+  } else if (model->kind == IEN_MODEL_BIREFNET) {
+    Birefnet &b = *model->birefnet;
+    st = prepare(model, width, height);
+    if (st != IEN_OK) return st;
+    if (b.staged < pixels) {
+      IEN_HIP(hipStreamSynchronize(ctx->stream));
+      (void)hipFree(b.d_in);
+      (void)hipFree(b.d_out);
+      b.d_in = b.d_out = nullptr;
+      b.staged = 0;
+      IEN_HIP(hipMalloc(&b.d_in, pixels * 3 * 4));
+      IEN_HIP(hipMalloc(&b.d_out, pixels * 4));
+      b.staged = pixels;
+    }
+    d_in = b.d_in;
+    d_out = b.d_out;
   } else if (model->kind == IEN_MODEL_SCUNET) {
     Scunet &s = *model->scunet;
     st = prepare(model, width, height);

@@ -21,7 +21,7 @@ INPUT_ROWS, INPUT_IMAGE = 0, 1
 NHWC, NCHW = 0, 1
 ACT_NONE, ACT_RELU, ACT_GELU, ACT_PRELU, ACT_SIGMOID = range(5)
 OUT_F16, OUT_F32 = 0, 1
-MODEL_REALESRGAN, MODEL_SCUNET, MODEL_LAMA = 0, 1, 2
+MODEL_REALESRGAN, MODEL_SCUNET, MODEL_LAMA, MODEL_BIREFNET = 0, 1, 2, 3
 
 # Every symbol include/ien_hip.h declares.
 EXPORTS = (
@@ -509,13 +509,15 @@ class Model:
     def run(self, image, progress=None, mask=None):
         """Host f32 H x W x 3 in, host f32 out (Model::run_float): 4H x 4W x 3
         for Real-ESRGAN, H x W x 3 for SCUNet and LaMa (which takes the
-        H x W mask, 1 = fill)."""
+        H x W mask, 1 = fill), H x W logits for BiRefNet (whose input is
+        already normalised)."""
         import numpy as np
 
         image = np.ascontiguousarray(image, dtype=np.float32)
         h, w, _ = image.shape
         s = 4 if self.kind == MODEL_REALESRGAN else 1
-        out = np.empty((s * h, s * w, 3), np.float32)
+        shape = (h, w) if self.kind == MODEL_BIREFNET else (s * h, s * w, 3)
+        out = np.empty(shape, np.float32)
         m = None if mask is None else np.ascontiguousarray(mask, dtype=np.float32)
         cb = PROGRESS(progress) if progress else None
         check(load().ien_model_run(self.h, image.ctypes.data_as(ctypes.c_void_p),

@@ -340,12 +340,20 @@ ien_status ien_fourier_inverse(const ien_fourier *f, const uint16_t *d_spectrum,
                                float *d_work, uint16_t *d_out, size_t stride);
 
 /* ---- models: crates/<model>-native/src/lib.rs Model ------------------- */
-typedef enum { IEN_MODEL_REALESRGAN = 0, IEN_MODEL_SCUNET = 1, IEN_MODEL_LAMA = 2 } ien_model_kind;
+typedef enum {
+  IEN_MODEL_REALESRGAN = 0,
+  IEN_MODEL_SCUNET = 1,
+  IEN_MODEL_LAMA = 2,
+  IEN_MODEL_BIREFNET = 3
+} ien_model_kind;
 
 /* Model::load (realesrgan-native lib.rs:120-137, scunet-native
- * lib.rs:79-111, lama-native lib.rs:75-108, with the GPU engine): read the
- * weights file (weight_file.rs format, magic b"REALESRG", b"SCUNET\0\0" or
- * b"LAMA\0\0\0\0"), check every tensor, upload once. */
+ * lib.rs:79-111, lama-native lib.rs:75-108, birefnet-native lib.rs:63-96,
+ * with the GPU engine): read the weights file (weight_file.rs format, magic
+ * b"REALESRG", b"SCUNET\0\0", b"LAMA\0\0\0\0" or b"BIREFNET"), check every
+ * tensor, upload once.  BiRefNet's window (7 as exported, 12 in the
+ * configured network) follows from its position-bias tensors; its ASPP must
+ * be deformable-free (all-zero offset convolutions, else IEN_ERR_WEIGHTS). */
 ien_status ien_model_load(ien_ctx *ctx, ien_model_kind kind, const char *weights_path,
                           ien_model **out);
 /* The same from weights already in memory: `tensors` name/shape/value
@@ -361,16 +369,20 @@ ien_status ien_model_from_tensors(ien_ctx *ctx, ien_model_kind kind, const ien_t
 void ien_model_free(ien_model *model);
 
 /* Progress callback: share done in 0..1, after each layer (Real-ESRGAN, 34),
- * block (SCUNet, 28) or step (LaMa, 26: lama-native lib.rs:128-157); nonzero
- * return cancels the run with IEN_ERR_CANCELLED (realesrgan lib.rs:168-188,
- * scunet lib.rs:205-215). */
+ * block (SCUNet, 28) or step (LaMa, 26: lama-native lib.rs:128-157; BiRefNet,
+ * 14: the 2 x 4 backbone stages, the five decoder blocks and the head, which
+ * the reference does not report); nonzero return cancels the run with
+ * IEN_ERR_CANCELLED (realesrgan lib.rs:168-188, scunet lib.rs:205-215). */
 typedef int (*ien_progress)(float done, void *user);
 
 /* Model::run_float (realesrgan-native lib.rs:194-214, scunet-native
- * lib.rs:151-171, lama-native lib.rs:159-178): host f32 NHWC image of width x
- * height x 3 in [0, 1], host f32 output (Real-ESRGAN 4h x 4w x 3, SCUNet and
- * LaMa h x w x 3).  `mask` (height x width, 1 = fill) for LaMa, whose sides
- * are at least 9; NULL for the others. */
+ * lib.rs:151-171, lama-native lib.rs:159-178) and BiRefNet's run_normalized
+ * (birefnet-native lib.rs:144-171): host f32 NHWC image of width x height x
+ * 3 (in [0, 1]; for BiRefNet already normalised with ImageNet's mean and
+ * deviation, square, sides a multiple of 64), host f32 output (Real-ESRGAN
+ * 4h x 4w x 3, SCUNet and LaMa h x w x 3, BiRefNet h x w logits).  `mask`
+ * (height x width, 1 = fill) for LaMa, whose sides are at least 9; NULL for
+ * the others. */
 ien_status ien_model_run(ien_model *model, const float *image, const float *mask, size_t width,
                          size_t height, float *out, ien_progress progress, void *user);
 
