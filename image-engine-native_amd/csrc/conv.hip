@@ -107,10 +107,11 @@ __global__ __launch_bounds__(256) void conv_mfma(ConvArgs a) {
   // Bias and PReLU slope of this lane's accumulator column, per N-block:
   // loaded now, used after the products.
   float bias_r[NBW], slope_r[NBW];
+  if (a.ksplit > 1) a.y = (float *)a.y + (long)blockIdx.y * (a.p_end - a.p_begin) * a.ys;
 #pragma unroll
   for (int j = 0; j < NBW; j++) {
     const int n = (nblk0 + j) * 32 + (lane & 31);  // < NB * 32: the bias is padded
-    bias_r[j] = a.bias[n];
+    bias_r[j] = a.ksplit > 1 ? 0.0f : a.bias[n];
     slope_r[j] = a.act == IEN_ACT_PRELU ? a.slope[min(n, a.N - 1)] : 0.0f;
   }
 
@@ -154,7 +155,9 @@ __global__ __launch_bounds__(256) void conv_mfma(ConvArgs a) {
     abase[i] = apix[i] * CKP + (VEC ? 8 * (lane >> 5) : 0);
   }
 
-  for (int c0 = 0; c0 < a.C; c0 += CK) {
+  const int c_begin = (int)blockIdx.y * a.kchunks * CK;
+  const int c_end = min(a.C, c_begin + a.kchunks * CK);
+  for (int c0 = c_begin; c0 < c_end; c0 += CK) {
     const int cc = min(CK, a.C - c0);  // == CK when VEC
     __syncthreads();
     // ---- global -> LDS: the halo of this channel chunk ----
@@ -419,6 +422,12 @@ __global__ __launch_bounds__(256) void conv_mfma(ConvArgs a) {
       const long base = (long)(p - a.p_begin) * a.ys + n;
       if (a.out_f32) {
         float *yo = (float *)a.y + base;
+        if (nv == 8 && !a.accumulate && (((uintptr_t)yo) & 15) == 0) {
+          // Two 16-byte stores (split-K partial sums take this path).
+          *(float4v *)yo = float4v{v[0], v[1], v[2], v[3]};
+          *(float4v *)(yo + 4) = float4v{v[4], v[5], v[6], v[7]};
+          continue;
+        }
         for (int e = 0; e < nv; e++) {
           float o = v[e];
           if (a.accumulate)
@@ -516,6 +525,32 @@ __global__ __launch_bounds__(256) void conv_mfma(ConvArgs a) {
   }
 }
 
+// Split-K finish: out(p, n) = act((acc ? out : 0) + bias[n] + sum over the
+// ksplit partial sums in order), the epilogue's order.
+__global__ __launch_bounds__(256) void k_splitk_finish(const float *__restrict__ part, int ksplit,
+                                                       long rows, int pitch, int N,
+                                                       const float *__restrict__ bias,
+                                                       const float *__restrict__ slope, int act,
+                                                       int accumulate, void *y, long ys,
+                                                       int out_f32, int out_nchw) {
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= rows * N) return;
+  const long p = i / N;
+  const int n = (int)(i % N);
+  float s = 0.0f;
+  for (int z = 0; z < ksplit; z++) s += part[((long)z * rows + p) * pitch + n];
+  float v = s + bias[n];
+  const float sl = act == IEN_ACT_PRELU ? slope[n] : 0.0f;
+  const long at = out_nchw ? (long)n * ys + p : p * ys + n;
+  if (out_f32) {
+    float *yo = (float *)y + at;
+    *yo = accumulate ? activate(v + *yo, act, sl) : activate(v, act, sl);
+  } else {
+    uint16_t *yo = (uint16_t *)y + at;
+    *yo = f2h(accumulate ? activate(v + h2f(*yo), act, sl) : activate(v, act, sl));
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Host dispatch.
 
@@ -532,8 +567,44 @@ static ien_status run_cfg(ien_ctx *ctx, ConvArgs a) {
   IEN_CHECK(blocks > 0 && blocks < (1L << 31), IEN_ERR_INPUT, "grid of %ld tiles", blocks);
   // The packed weights must cover every fragment the tiles touch.
   IEN_CHECK(a.tiles_n * Cfg::NBT <= a.NB, IEN_ERR_INPUT, "weights narrower than the tile");
+  // Split-K when the tiles leave three quarters of the CUs idle: about two
+  // workgroups per CU, each split at least 512 deep in K (the partial sums
+  // cost an f32 write and read of the output per split), partial sums in
+  // the context's workspace, then the finishing pass.
+  const int chunks = (a.C + CK - 1) / CK;
+  const long rows = a.p_end - a.p_begin;
+  const int pitch = a.tiles_n * Cfg::BN;
+  const int T = KS == 0 ? a.noff : KS * KS;
+  const int min_chunks = (512 + T * CK - 1) / (T * CK);
+  int ksplit = 1;
+  if (VEC && chunks >= 2 * min_chunks && 4 * blocks <= ctx->cus) {
+    ksplit = (int)std::min<long>(chunks / min_chunks, (2L * ctx->cus + blocks - 1) / blocks);
+    while (ksplit > 1 && (size_t)ksplit * rows * pitch > ctx->splitk_floats) ksplit--;
+  }
+  a.kchunks = (chunks + ksplit - 1) / ksplit;
+  a.ksplit = (chunks + a.kchunks - 1) / a.kchunks;
+  if (a.ksplit <= 1) {
+    a.ksplit = 1;
+    a.kchunks = chunks;
+    hipLaunchKernelGGL((conv_mfma<KS, S, TR, TC, MSPLIT, NBW, CK, VEC, IN_NCHW>),
+                       dim3((unsigned)blocks), dim3(256), 0, ctx->stream, a);
+    IEN_HIP(hipGetLastError());
+    return IEN_OK;
+  }
+  ConvArgs pa = a;
+  pa.y = ctx->splitk;
+  pa.ys = pitch;
+  pa.out_f32 = 1;
+  pa.out_nchw = 0;
+  pa.act = IEN_ACT_NONE;
+  pa.accumulate = 0;
   hipLaunchKernelGGL((conv_mfma<KS, S, TR, TC, MSPLIT, NBW, CK, VEC, IN_NCHW>),
-                     dim3((unsigned)blocks), dim3(256), 0, ctx->stream, a);
+                     dim3((unsigned)blocks, (unsigned)a.ksplit), dim3(256), 0, ctx->stream, pa);
+  IEN_HIP(hipGetLastError());
+  const long items = rows * a.N;
+  hipLaunchKernelGGL(k_splitk_finish, dim3((unsigned)((items + 255) / 256)), dim3(256), 0,
+                     ctx->stream, (const float *)ctx->splitk, a.ksplit, rows, pitch, a.N, a.bias,
+                     a.slope, a.act, a.accumulate, a.y, (long)a.ys, a.out_f32, a.out_nchw);
   IEN_HIP(hipGetLastError());
   return IEN_OK;
 }

@@ -36,6 +36,10 @@ struct ConvArgs {
   void *y;
   int ys;
   int out_nchw, out_f32, act, accumulate;
+  // Split-K: blockIdx.y takes channel chunks [kchunks y, kchunks (y + 1)),
+  // and with ksplit > 1 the launch writes raw f32 sums (no bias) to
+  // y + y_index * (p_end - p_begin) * ys, NHWC; a finishing pass adds them.
+  int ksplit, kchunks;
 };
 
 __device__ __forceinline__ int reflect_idx(int i, int n) {

@@ -43,6 +43,10 @@ struct ien_ctx {
   // 4 KiB of zeros in device memory: the source of padding pixels for
   // loads that write LDS directly (they cannot write a constant).
   uint16_t *zeros = nullptr;
+  // Split-K partial sums of the convolution kernels (f32), allocated once
+  // with the context so that no launch allocates (graph capture).
+  float *splitk = nullptr;
+  size_t splitk_floats = 0;
 };
 
 // Packed weights (gemm.rs Matrix): k x n padded to whole 16 x 32 MFMA

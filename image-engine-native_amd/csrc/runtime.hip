@@ -109,10 +109,15 @@ ien_status ien_open(int device, ien_ctx **out) {
   ctx->stream = ctx->own;
   e = hipMalloc(&ctx->zeros, 4096);
   if (e == hipSuccess) e = hipMemset(ctx->zeros, 0, 4096);
+  // 32 MiB of split-K partial sums.
+  ctx->splitk_floats = (size_t)8 << 20;
+  if (e == hipSuccess) e = hipMalloc((void **)&ctx->splitk, ctx->splitk_floats * 4);
   if (e != hipSuccess) {
+    (void)hipFree(ctx->zeros);
+    (void)hipFree(ctx->splitk);
     (void)hipStreamDestroy(ctx->own);
     delete ctx;
-    return fail(IEN_ERR_GPU, "zero page: %s", hipGetErrorString(e));
+    return fail(IEN_ERR_GPU, "context buffers: %s", hipGetErrorString(e));
   }
   *out = ctx;
   return IEN_OK;
@@ -124,6 +129,7 @@ void ien_close(ien_ctx *ctx) {
   (void)hipStreamSynchronize(ctx->stream);
   (void)hipStreamDestroy(ctx->own);
   (void)hipFree(ctx->zeros);
+  (void)hipFree(ctx->splitk);
   delete ctx;
 }
 

@@ -188,6 +188,49 @@ def test_rows(ctx, oracle, m, k, n):
     close(out.float().cpu().numpy(), want)
 
 
+# Split-K: few output tiles and several channel chunks, so the reduction is
+# spread over workgroups, summed by the finishing pass, then bias,
+# accumulate and activation.
+@pytest.mark.parametrize("act", [0, 1, 3])
+def test_splitk_conv3_accumulate(ctx, oracle, act):
+    x, wt, b = case(14, 6, 32, 512, 64, 9)
+    slope = np.linspace(0.05, 0.5, 64).astype(np.float32)
+    init = f16(np.random.default_rng(15).standard_normal((6 * 32, 64)))
+    got = run_gpu(ctx, x, wt, b, act=act, slope=slope, init=init)
+    close(got, want_cpu(oracle, x, wt, b, act=act, slope=slope, init=init))
+
+
+def test_splitk_nchw_f32_reflect_rows(ctx, oracle):
+    x, wt, b = case(16, 8, 32, 256, 96, 9)
+    want = want_cpu(oracle, x, wt, b)
+    close(run_gpu(ctx, x, wt, b, nchw_in=True, nchw_out=True), want)
+    close(run_gpu(ctx, x, wt, b, out_f32=True, stride_pad=8), want, f32=True)
+    close(run_gpu(ctx, x, wt, b, pad=1), want_cpu(oracle, x, wt, b, pad=1))
+    close(run_gpu(ctx, x, wt, b, row0=37, rows=150), want[37:187])
+
+
+def test_splitk_offsets_and_rows(ctx, oracle):
+    import torch
+    import ien
+
+    offsets = [(0, 0), (1, 0), (0, 1), (1, 1)]
+    x, wt, b = case(17, 8, 16, 512, 64, 4)
+    close(run_gpu(ctx, x, wt, b, offsets=offsets), want_cpu(oracle, x, wt, b, offsets=offsets))
+    rng = np.random.default_rng(18)
+    m, k, n = 100, 1024, 96
+    a = f16(rng.standard_normal((m, k)))
+    wt = f16(rng.standard_normal((k, n)) / np.sqrt(k))
+    bias = rng.standard_normal(n).astype(np.float32)
+    init = f16(rng.standard_normal((m, n)))
+    want = oracle.multiply_rows(a, wt, bias, out=init.copy(), accumulate=True)
+    mat = ien.Matrix(ctx, wt, bias)
+    out = torch.from_numpy(init).half().cuda()
+    ien.multiply(ctx, ien.rows_input(torch.from_numpy(a).half().cuda(), k), 0, m, mat, out, n,
+                 accumulate=True)
+    torch.cuda.synchronize()
+    close(out.float().cpu().numpy(), want)
+
+
 def test_conv3_finish_prelu(ctx, oracle):
     import torch
     import ien
