@@ -125,6 +125,72 @@ __global__ __launch_bounds__(256) void k_layer_norm(uint16_t *__restrict__ x, lo
   }
 }
 
+// The same with L lanes per row (the row's 8-channel chunks rounded up to a
+// power of two, at most 64) and Q chunks per lane, 16-byte loads and
+// stores: rows of 8-aligned channels at 8-aligned strides.  The reductions
+// stay inside the row's aligned lane group.
+template <int L, int Q>
+__global__ __launch_bounds__(256) void k_layer_norm_vec(uint16_t *__restrict__ x, long rows, int c,
+                                                        long stride,
+                                                        const float *__restrict__ gamma,
+                                                        const float *__restrict__ beta) {
+  const int sub = threadIdx.x & (L - 1);
+  const long row = ((long)blockIdx.x * 256 + threadIdx.x) / L;
+  if (row >= rows) return;  // whole lane groups leave together
+  uint16_t *r = x + row * stride;
+  const int chunks = c >> 3;
+  float v[8 * Q];
+  float sum = 0.0f;
+#pragma unroll
+  for (int q = 0; q < Q; q++) {
+    const int k = sub + L * q;
+    if (k < chunks) {
+      const u32x4 raw = *(const u32x4 *)(r + 8 * k);
+      uint16_t h[8];
+      __builtin_memcpy(h, &raw, 16);
+#pragma unroll
+      for (int e = 0; e < 8; e++) v[8 * q + e] = h2f_e(h[e]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; e++) v[8 * q + e] = 0.0f;
+    }
+#pragma unroll
+    for (int e = 0; e < 8; e++) sum += v[8 * q + e];
+  }
+#pragma unroll
+  for (int off = L / 2; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
+  const float mean = sum / (float)c;
+  float sq = 0.0f;
+#pragma unroll
+  for (int q = 0; q < Q; q++)
+    if (sub + L * q < chunks) {
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        const float d = v[8 * q + e] - mean;
+        sq += d * d;
+      }
+    }
+#pragma unroll
+  for (int off = L / 2; off > 0; off >>= 1) sq += __shfl_xor(sq, off);
+  const float inv = 1.0f / sqrtf(sq / (float)c + 1e-5f);
+#pragma unroll
+  for (int q = 0; q < Q; q++) {
+    const int k = sub + L * q;
+    if (k < chunks) {
+      const float4 g0 = *(const float4 *)(gamma + 8 * k), g1 = *(const float4 *)(gamma + 8 * k + 4);
+      const float4 b0 = *(const float4 *)(beta + 8 * k), b1 = *(const float4 *)(beta + 8 * k + 4);
+      const float gg[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+      const float bb[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+      uint16_t h[8];
+#pragma unroll
+      for (int e = 0; e < 8; e++) h[e] = f2h_e((v[8 * q + e] - mean) * inv * gg[e] + bb[e]);
+      u32x4 raw;
+      __builtin_memcpy(&raw, h, 16);
+      *(u32x4 *)(r + 8 * k) = raw;
+    }
+  }
+}
+
 // ---- math.rs:136-152 GELU and the logistic function in place -------------
 __device__ __forceinline__ float gelu_e(float x) {
   // math.rs:41-75 (Eigen's generic_fast_erf_float coefficients).
@@ -463,6 +529,33 @@ ien_status ien_layer_norm(ien_ctx *ctx, uint16_t *d_x, size_t rows, size_t c, si
   IEN_CHECK(ctx && d_x && d_gamma && d_beta, IEN_ERR_INPUT, "null argument");
   IEN_CHECK(c > 0 && c <= 3072 && stride >= c, IEN_ERR_INPUT, "rows of %zu values", c);
   if (rows == 0) return IEN_OK;
+  const bool vec = c % 8 == 0 && stride % 8 == 0 && ((uintptr_t)d_x & 15) == 0 &&
+                   ((uintptr_t)d_gamma & 15) == 0 && ((uintptr_t)d_beta & 15) == 0;
+  if (vec) {
+    const int chunks = (int)(c / 8);
+    int lanes = 1;
+    while (lanes < chunks && lanes < 64) lanes *= 2;
+    const int q = (chunks + lanes - 1) / lanes;  // at most 6 (c <= 3072)
+    const size_t threads = rows * (size_t)lanes;
+    const dim3 grid((unsigned)((threads + 255) / 256));
+    void (*k)(uint16_t *, long, int, long, const float *, const float *) = nullptr;
+    switch (lanes) {
+      case 1: k = k_layer_norm_vec<1, 1>; break;
+      case 2: k = k_layer_norm_vec<2, 1>; break;
+      case 4: k = k_layer_norm_vec<4, 1>; break;
+      case 8: k = k_layer_norm_vec<8, 1>; break;
+      case 16: k = k_layer_norm_vec<16, 1>; break;
+      case 32: k = k_layer_norm_vec<32, 1>; break;
+      default:
+        k = q == 1 ? k_layer_norm_vec<64, 1> : q == 2 ? k_layer_norm_vec<64, 2>
+            : q <= 3 ? k_layer_norm_vec<64, 3> : k_layer_norm_vec<64, 6>;
+        break;
+    }
+    hipLaunchKernelGGL(k, grid, dim3(256), 0, ctx->stream, d_x, (long)rows, (int)c, (long)stride,
+                       d_gamma, d_beta);
+    IEN_HIP(hipGetLastError());
+    return IEN_OK;
+  }
   hipLaunchKernelGGL(k_layer_norm, dim3(grid_for(rows, 4)), dim3(256), 0, ctx->stream, d_x,
                      (long)rows, (int)c, (long)stride, d_gamma, d_beta);
   IEN_HIP(hipGetLastError());

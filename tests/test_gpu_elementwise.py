@@ -47,7 +47,8 @@ def test_pixel_shuffle_add_bit_exact(ctx, oracle, h, w):
     assert np.array_equal(out.cpu().numpy(), want)
 
 
-@pytest.mark.parametrize("rows,c", [(1, 32), (77, 96), (300, 768), (5, 3072), (9, 37)])
+@pytest.mark.parametrize("rows,c", [(1, 32), (77, 96), (300, 768), (5, 3072), (9, 37), (40, 8),
+                                    (33, 1536), (7, 2048), (130, 2304)])
 def test_layer_norm(ctx, oracle, rows, c):
     import torch
     import ien
@@ -62,6 +63,26 @@ def test_layer_norm(ctx, oracle, rows, c):
     torch.cuda.synchronize()
     got = xt.float().cpu().numpy()
     assert np.abs(got - want).max() <= 2e-3 * np.abs(want).max() + 2e-3
+
+
+def test_layer_norm_strided_columns(ctx, oracle):
+    """Columns 0..c of rows `stride` apart: normalised in place, the others
+    untouched (the level maps of the BiRefNet decoder)."""
+    import torch
+    import ien
+
+    rows, c, stride = 50, 192, 384
+    rng = np.random.default_rng(3)
+    x = (rng.standard_normal((rows, stride)) * 2).astype(np.float16)
+    gamma = (1 + 0.1 * rng.standard_normal(c)).astype(np.float32)
+    beta = (0.1 * rng.standard_normal(c)).astype(np.float32)
+    want = oracle.layer_norm(x[:, :c].astype(np.float32), gamma, beta).reshape(rows, c)
+    xt = torch.from_numpy(x).cuda()
+    ien.layer_norm(ctx, xt, rows, c, stride, torch.from_numpy(gamma).cuda(), torch.from_numpy(beta).cuda())
+    torch.cuda.synchronize()
+    got = xt.float().cpu().numpy()
+    assert np.abs(got[:, :c] - want).max() <= 2e-3 * np.abs(want).max() + 2e-3
+    assert np.array_equal(got[:, c:], x[:, c:].astype(np.float32))
 
 
 def test_gelu_sigmoid(ctx, oracle):
