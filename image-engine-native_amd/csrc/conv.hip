@@ -407,6 +407,77 @@ __global__ __launch_bounds__(256) void conv_mfma(ConvArgs a) {
     __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes done
     __builtin_amdgcn_wave_barrier();
     constexpr int GROUPS = NBW * 4;  // 8-channel groups per staged pixel
+    constexpr int ITEMS = MBW * 32 * GROUPS / 64;  // per lane
+    // Item t of this lane: its output offset, or -1 outside the output.
+    auto item_at = [&](int t, int &g) -> long {
+      const int item = lane + 64 * t;
+      const int q = item / GROUPS;
+      g = item % GROUPS;
+      const int mb = mg * MBW + q / 32;
+      const int r = mb / (TC / 32), cx = (mb % (TC / 32)) * 32 + (q & 31);
+      const int oy = oy0 + r, ox = ox0 + cx;
+      const int p = oy * a.OW + ox;
+      const int n = nblk0 * 32 + 8 * g;
+      if (oy >= a.OH || ox >= a.OW || p < a.p_begin || p >= a.p_end || n >= a.N) return -1;
+      return (long)(p - a.p_begin) * a.ys + n;
+    };
+    // f16 outputs in whole 16-byte groups: the old values (when
+    // accumulating) are all loaded first, unconditionally, so one memory
+    // latency covers them; then one loop per activation (picked once).
+    const bool groups16 = !a.out_f32 && (a.ys & 7) == 0 && (a.N & 7) == 0 &&
+                          (((uintptr_t)a.y) & 15) == 0;
+    if (groups16) {
+      uint16_t *yh = (uint16_t *)a.y;
+      u32x4 old[ITEMS];
+      if (a.accumulate) {
+#pragma unroll
+        for (int t = 0; t < ITEMS; t++) {
+          int g;
+          const long at = item_at(t, g);
+          old[t] = *(const u32x4 *)(yh + (at >= 0 ? at : 0));
+        }
+      }
+      auto store = [&](auto actf) {
+#pragma unroll
+        for (int t = 0; t < ITEMS; t++) {
+          int g;
+          const long at = item_at(t, g);
+          if (at < 0) continue;
+          const int q = (lane + 64 * t) / GROUPS;
+          const float4v s0 = *(const float4v *)(stage + q * SP + 8 * g);
+          const float4v s1 = *(const float4v *)(stage + q * SP + 8 * g + 4);
+          float v[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
+          uint16_t o[8];
+          if (a.accumulate) {
+            uint16_t oh[8];
+            __builtin_memcpy(oh, &old[t], 16);
+            const int n = nblk0 * 32 + 8 * g;
+#pragma unroll
+            for (int e = 0; e < 8; e++) o[e] = f2h(actf(v[e] + h2f(oh[e]), n + e));
+          } else {
+#pragma unroll
+            for (int e = 0; e < 8; e++) o[e] = f2h(v[e]);  // activated in the accumulators
+          }
+          u32x4 ov;
+          __builtin_memcpy(&ov, o, 16);
+          *(u32x4 *)(yh + at) = ov;
+        }
+      };
+      const int act = a.accumulate ? a.act : IEN_ACT_NONE;
+      if (act == IEN_ACT_RELU)
+        store([](float v, int) { return v > 0.0f ? v : 0.0f; });
+      else if (act == IEN_ACT_GELU)
+        store([](float v, int) { return gelu_f(v); });
+      else if (act == IEN_ACT_SIGMOID)
+        store([](float v, int) { return sigmoid_f(v); });
+      else if (act == IEN_ACT_PRELU) {
+        const float *sl = a.slope;
+        store([sl](float v, int n) { return v < 0.0f ? v * sl[n] : v; });
+      } else {
+        store([](float v, int) { return v; });
+      }
+      return;
+    }
     for (int item = lane; item < MBW * 32 * GROUPS; item += 64) {
       const int q = item / GROUPS, g = item % GROUPS;
       const int mb = mg * MBW + q / 32;
