@@ -3,6 +3,7 @@
 // window ops and the row products on the context's stream.
 
 #include <cmath>
+#include <cstdint>
 #include <cstring>
 
 #include "ien_internal.h"
@@ -166,8 +167,11 @@ ien_status ien_swin_run(ien_swin *b, uint16_t *d_map, size_t stride, int height,
   if ((st = rows_product(ctx, b->d_att, c, rows, b->proj, b->d_tok, c, IEN_ACT_NONE, 0)) != IEN_OK)
     return st;
   if ((st = ien_window_scatter_add(ctx, &w, b->d_tok, b->c, d_map, stride)) != IEN_OK) return st;
-  // mlp (scunet swin.rs:236-275): every token normalised (a 1 x 1 window
-  // gather is the copy with its LayerNorm), fc1 + GELU, fc2 added back.
+  // mlp (scunet swin.rs:236-275): every token normalised, fc1 + GELU, fc2
+  // added back; one fused pass where its kernel takes the width, else a
+  // 1 x 1 window gather (the copy with its LayerNorm) and two products.
+  if (swin_mlp_supported(b->c) && stride % 8 == 0 && ((uintptr_t)d_map & 15) == 0)
+    return swin_mlp(ctx, d_map, stride, (long)tokens, b->c, g2, b2, b->fc1, b->fc2);
   ien_windows one{1, 0, height, width};
   if ((st = ien_window_gather(ctx, &one, d_map, stride, b->c, g2, b2, b->d_tok)) != IEN_OK)
     return st;

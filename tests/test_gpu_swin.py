@@ -32,6 +32,10 @@ def oracle_block(oracle, x, window, shift, masked, wt):
     (64, 8, 0, -np.inf, [(16, 16)]),              # SCUNet W-MSA
     (96, 7, 3, -100.0, [(10, 10), (14, 21)]),     # the reference's BiRefNet window
     (32, 12, 6, -100.0, [(15, 13), (24, 24)]),    # the configuration's BiRefNet window
+    (128, 8, 4, -np.inf, [(16, 24)]),             # SCUNet level 3
+    (256, 8, 0, -np.inf, [(8, 16), (9, 13)]),     # SCUNet body; a ragged last row block
+    (192, 12, 6, -100.0, [(12, 24)]),             # Swin-T stage 2
+    (384, 12, 0, -100.0, [(12, 12)]),             # Swin-T stage 3 (MLP through the row products)
 ])
 def test_swin_block(ctx, oracle, c, window, shift, masked, sizes):
     import torch
