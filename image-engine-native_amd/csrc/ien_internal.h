@@ -107,4 +107,15 @@ ien_status swin_mlp(ien_ctx *ctx, uint16_t *d_map, size_t stride, long rows, int
                     const float *gamma, const float *beta, const ien_matrix *fc1,
                     const ien_matrix *fc2);
 
+// swin_attend.hip: a Swin block's attention half (gather, LayerNorm, qkv,
+// attention, projection, residual) in one pass per window, for window 8
+// and 32, 64 or 128 channels; its projection fragments and bias tables are
+// packed once per block by the two helpers.
+bool swin_attend_supported(int c, int window);
+std::vector<uint16_t> swin_attend_proj(const float *proj_w, int c);
+std::vector<float> swin_attend_tables(const float *tables, int classes, int heads);
+ien_status swin_attend(ien_ctx *ctx, const ien_windows *win, uint16_t *d_map, size_t stride,
+                       int c, const float *gamma, const float *beta, const ien_matrix *qkv,
+                       const uint16_t *d_proj, const float *bproj, const float *d_tables);
+
 }  // namespace ien

@@ -13,6 +13,10 @@ struct ien_swin {
   int c = 0, window = 0, shift = 0, heads = 0, classes = 0;
   float *d_ln = nullptr;  // ln1 gamma, beta, ln2 gamma, beta (4 c floats)
   float *d_tables = nullptr;
+  // The fused attention's projection fragments and bias tables (when it
+  // takes the block's width and window).
+  uint16_t *d_attn_proj = nullptr;
+  float *d_attn_tables = nullptr;
   ien_matrix *qkv = nullptr, *proj = nullptr, *fc1 = nullptr, *fc2 = nullptr;
   // Scratch: `rows` window rows (at least the map's tokens) of 4c, c, c.
   uint16_t *d_wide = nullptr, *d_tok = nullptr, *d_att = nullptr;
@@ -29,6 +33,8 @@ void release(ien_swin *b) {
   ien_matrix_free(b->fc2);
   (void)hipFree(b->d_ln);
   (void)hipFree(b->d_tables);
+  (void)hipFree(b->d_attn_proj);
+  (void)hipFree(b->d_attn_tables);
   (void)hipFree(b->d_wide);
   (void)hipFree(b->d_tok);
   (void)hipFree(b->d_att);
@@ -129,6 +135,16 @@ ien_status ien_swin_new(ien_ctx *ctx, const ien_swin_weights *w, ien_swin **out)
   if (e == hipSuccess) e = hipMalloc((void **)&b->d_tables, tbytes);
   if (e == hipSuccess) e = hipMemcpy(b->d_ln, ln.data(), 4 * c * 4, hipMemcpyHostToDevice);
   if (e == hipSuccess) e = hipMemcpy(b->d_tables, tables.data(), tbytes, hipMemcpyHostToDevice);
+  if (e == hipSuccess && swin_attend_supported(W.c, W.window)) {
+    const std::vector<uint16_t> proj = swin_attend_proj(W.proj_w, W.c);
+    const std::vector<float> packed = swin_attend_tables(tables.data(), b->classes, b->heads);
+    e = hipMalloc((void **)&b->d_attn_proj, proj.size() * 2);
+    if (e == hipSuccess) e = hipMalloc((void **)&b->d_attn_tables, packed.size() * 4);
+    if (e == hipSuccess)
+      e = hipMemcpy(b->d_attn_proj, proj.data(), proj.size() * 2, hipMemcpyHostToDevice);
+    if (e == hipSuccess)
+      e = hipMemcpy(b->d_attn_tables, packed.data(), packed.size() * 4, hipMemcpyHostToDevice);
+  }
   if (e != hipSuccess) {
     release(b);
     return fail(IEN_ERR_GPU, "swin upload: %s", hipGetErrorString(e));
@@ -156,21 +172,27 @@ ien_status ien_swin_run(ien_swin *b, uint16_t *d_map, size_t stride, int height,
   ien_status st = reserve(b, rows > tokens ? rows : tokens);
   if (st != IEN_OK) return st;
   const float *g1 = b->d_ln, *b1 = b->d_ln + c, *g2 = b->d_ln + 2 * c, *b2 = b->d_ln + 3 * c;
-  // attend (scunet swin.rs:131-232): the window rows, qkv, attention,
-  // projection over the token rows, added back onto the map.
-  if ((st = ien_window_gather(ctx, &w, d_map, stride, b->c, g1, b1, b->d_tok)) != IEN_OK) return st;
-  if ((st = rows_product(ctx, b->d_tok, c, rows, b->qkv, b->d_wide, 3 * c, IEN_ACT_NONE, 0)) !=
-      IEN_OK)
-    return st;
-  if ((st = ien_window_attention(ctx, &w, b->d_wide, b->c, b->d_tables, b->d_att)) != IEN_OK)
-    return st;
-  if ((st = rows_product(ctx, b->d_att, c, rows, b->proj, b->d_tok, c, IEN_ACT_NONE, 0)) != IEN_OK)
-    return st;
-  if ((st = ien_window_scatter_add(ctx, &w, b->d_tok, b->c, d_map, stride)) != IEN_OK) return st;
+  const bool rows16 = stride % 8 == 0 && ((uintptr_t)d_map & 15) == 0;
+  // attend (scunet swin.rs:131-232): one fused pass per window where its
+  // kernel takes the width and window, else the window rows, qkv,
+  // attention, projection over the token rows, added back onto the map.
+  if (b->d_attn_proj && rows16) {
+    st = swin_attend(ctx, &w, d_map, stride, b->c, g1, b1, b->qkv, b->d_attn_proj,
+                     b->proj->d_bias, b->d_attn_tables);
+  } else {
+    st = ien_window_gather(ctx, &w, d_map, stride, b->c, g1, b1, b->d_tok);
+    if (st == IEN_OK)
+      st = rows_product(ctx, b->d_tok, c, rows, b->qkv, b->d_wide, 3 * c, IEN_ACT_NONE, 0);
+    if (st == IEN_OK) st = ien_window_attention(ctx, &w, b->d_wide, b->c, b->d_tables, b->d_att);
+    if (st == IEN_OK)
+      st = rows_product(ctx, b->d_att, c, rows, b->proj, b->d_tok, c, IEN_ACT_NONE, 0);
+    if (st == IEN_OK) st = ien_window_scatter_add(ctx, &w, b->d_tok, b->c, d_map, stride);
+  }
+  if (st != IEN_OK) return st;
   // mlp (scunet swin.rs:236-275): every token normalised, fc1 + GELU, fc2
   // added back; one fused pass where its kernel takes the width, else a
   // 1 x 1 window gather (the copy with its LayerNorm) and two products.
-  if (swin_mlp_supported(b->c) && stride % 8 == 0 && ((uintptr_t)d_map & 15) == 0)
+  if (swin_mlp_supported(b->c) && rows16)
     return swin_mlp(ctx, d_map, stride, (long)tokens, b->c, g2, b2, b->fc1, b->fc2);
   ien_windows one{1, 0, height, width};
   if ((st = ien_window_gather(ctx, &one, d_map, stride, b->c, g2, b2, b->d_tok)) != IEN_OK)

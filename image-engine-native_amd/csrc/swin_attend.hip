@@ -1,0 +1,366 @@
+// swin_attend.hip -- the attention half of a Swin block in one pass per
+// window (crates/scunet-native/src/swin.rs:131-232 Transformer::attend):
+// gather of the rolled window, LayerNorm, q k v, attention with the
+// position bias and shift mask, projection and residual, written back to
+// the window's own tokens.  Window 8 (64 tokens), c = 32, 64 or 128
+// (heads of 32).
+//
+// Everything between the load of x and the store stays in registers:
+//  - x is loaded as MFMA fragments (lane l: token l % 32 of a 32-token
+//    block, channels 16 s + 8 (l / 32) + 0..7) and normalised in place;
+//    those registers are both the B operand of K^T = Wk^T x^T, Q^T = Wq^T
+//    x^T and the A operand of V = x Wv (v_mfma_f32_32x32x16_f16).  The
+//    packed qkv weights serve as A (for W^T) and B fragments unchanged.
+//  - An accumulator tile holds row 8 (r / 4) + 4 (l / 32) + r % 4 in
+//    register r and column l % 32.  Read in pairs of registers 8 s .. 8 s
+//    + 7 it is an operand whose 16-wide k step holds rows 16 s + 4 (l / 32)
+//    + {0..3, 8..11}: a fixed permutation of that step's k.  K^T and Q^T
+//    tiles are then the A and B operands of S^T = K Q^T (same dims on both
+//    sides), V and S^T tiles those of O^T = V^T P^T (same keys), and O^T
+//    the B operand of Y^T = Wp^T O^T, whose A fragments are packed on the
+//    host with the head dims in that permuted order.
+//  - S^T has keys in rows and queries in columns: the softmax over keys is
+//    in-register plus one exchange with lane l ^ 32.  The bias tables
+//    (position bias plus the shift mask of the window's class) are packed
+//    on the host in the accumulator layout, so a lane reads 16-byte runs.
+//  - Y^T's rows are output channels: the residual is read and the result
+//    written 4 channels (8 bytes) at a time per token.
+// Rounding points are the unfused path's: normalised x, q, k, v, the
+// probabilities and the attention output are f16; products accumulate in
+// f32; the result is rounded once after bias and residual.
+// With two waves per window (c = 64, 128) each wave takes 32 queries and
+// both compute K and V for all 64 keys; a barrier separates every read of
+// the window from the first write.
+
+#include "conv_common.h"
+#include "window_geo.h"
+
+namespace ien {
+namespace {
+
+struct AttendArgs {
+  WinGeo g;
+  uint16_t *map;
+  long stride;
+  const float *gamma, *beta;  // LayerNorm 1 (c each, 16-byte aligned)
+  const uint16_t *wqkv;       // packed fragments of the c x 3c qkv weights
+  const float *bqkv;          // 3c
+  const uint16_t *wproj;      // Wp^T A fragments [c / 32][heads][2][512]
+  const float *bproj;         // c
+  const float *bias;          // [class][head][key block][query block][4][64][4]
+};
+
+__device__ __forceinline__ half8 frag(const uint16_t *p, int idx, int lane) {
+  return *(const half8 *)(p + (size_t)idx * 512 + lane * 8);
+}
+
+// Registers 8 s .. 8 s + 7 of an accumulator tile (+ per-register add) as
+// an f16 operand.
+__device__ __forceinline__ half8 operand(const floatx16 &t, int s, float scale) {
+  half8 h;
+#pragma unroll
+  for (int i = 0; i < 8; i++) h[i] = (_Float16)(t[8 * s + i] * scale);
+  return h;
+}
+
+// The heads, the projection and the store for query blocks Q0 .. Q0 + QB
+// - 1 of window w (Q0 a constant, so that no register array is indexed by
+// a variable).
+template <int C, int QB, int Q0>
+__device__ __forceinline__ void attend_heads(const AttendArgs &a, const half8 (&xn)[2][C / 16],
+                                             const long (&src)[2], long w, bool live) {
+  constexpr int H = C / 32, CB = C / 32, KS = C / 16;
+  const int lane = threadIdx.x & 63, hf = lane >> 5, l32 = lane & 31;
+  floatx16 y[CB][QB];
+#pragma unroll
+  for (int cb = 0; cb < CB; cb++)
+#pragma unroll
+    for (int qb = 0; qb < QB; qb++) y[cb][qb] = floatx16{};
+  const int cls = win_class(a.g, w);
+  const float scale = 0.17677669529663688f;  // 1 / sqrt(32)
+
+  for (int h = 0; h < H; h++) {
+    floatx16 kt[2] = {}, vv[2] = {}, qt[QB];
+#pragma unroll
+    for (int qb = 0; qb < QB; qb++) qt[qb] = floatx16{};
+#pragma unroll
+    for (int s = 0; s < KS; s++) {
+      const half8 wq = frag(a.wqkv, h * KS + s, lane);
+      const half8 wk = frag(a.wqkv, (CB + h) * KS + s, lane);
+      const half8 wv = frag(a.wqkv, (2 * CB + h) * KS + s, lane);
+#pragma unroll
+      for (int kb = 0; kb < 2; kb++) {
+        kt[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wk, xn[kb][s], kt[kb], 0, 0, 0);
+        vv[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(xn[kb][s], wv, vv[kb], 0, 0, 0);
+      }
+#pragma unroll
+      for (int qb = 0; qb < QB; qb++) {
+        const half8 xq = xn[Q0 + qb][s];
+        qt[qb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wq, xq, qt[qb], 0, 0, 0);
+      }
+    }
+    // Biases: K^T, Q^T rows are dims 8 (r / 4) + 4 hf + r % 4; V columns
+    // are dims l32.
+    const float bv = a.bqkv[2 * C + 32 * h + l32];
+#pragma unroll
+    for (int q4 = 0; q4 < 4; q4++) {
+      const float4 bq = *(const float4 *)(a.bqkv + 32 * h + 8 * q4 + 4 * hf);
+      const float4 bk = *(const float4 *)(a.bqkv + C + 32 * h + 8 * q4 + 4 * hf);
+      const float bqa[4] = {bq.x, bq.y, bq.z, bq.w}, bka[4] = {bk.x, bk.y, bk.z, bk.w};
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+#pragma unroll
+        for (int kb = 0; kb < 2; kb++) {
+          kt[kb][4 * q4 + e] += bka[e];
+          vv[kb][4 * q4 + e] += bv;
+        }
+#pragma unroll
+        for (int qb = 0; qb < QB; qb++) qt[qb][4 * q4 + e] += bqa[e];
+      }
+    }
+    half8 ka[2][2], qo[QB][2], va[2][2];
+#pragma unroll
+    for (int s = 0; s < 2; s++) {
+#pragma unroll
+      for (int kb = 0; kb < 2; kb++) {
+        ka[kb][s] = operand(kt[kb], s, 1.0f);
+        va[kb][s] = operand(vv[kb], s, 1.0f);
+      }
+#pragma unroll
+      for (int qb = 0; qb < QB; qb++) qo[qb][s] = operand(qt[qb], s, 1.0f);
+    }
+    // S^T (keys x queries), bias, softmax over keys.
+    const float *tbl = a.bias + (size_t)(cls * H + h) * 4 * 4 * 256;
+    floatx16 o[QB];
+#pragma unroll
+    for (int qb = 0; qb < QB; qb++) {
+      floatx16 st[2];
+      float mx = -__builtin_inff();
+#pragma unroll
+      for (int kb = 0; kb < 2; kb++) {
+        st[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[kb][0], qo[qb][0], floatx16{}, 0, 0, 0);
+        st[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[kb][1], qo[qb][1], st[kb], 0, 0, 0);
+        const float *tq = tbl + ((kb * 2 + Q0 + qb) * 4) * 256 + lane * 4;
+#pragma unroll
+        for (int q4 = 0; q4 < 4; q4++) {
+          const float4 bt = *(const float4 *)(tq + q4 * 256);
+          const float bta[4] = {bt.x, bt.y, bt.z, bt.w};
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            const float v = st[kb][4 * q4 + e] * scale + bta[e];
+            st[kb][4 * q4 + e] = v;
+            mx = fmaxf(mx, v);
+          }
+        }
+      }
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      float sum = 0.0f;
+#pragma unroll
+      for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+          const float p = __expf(st[kb][r] - mx);
+          st[kb][r] = p;
+          sum += p;
+        }
+      sum += __shfl_xor(sum, 32);
+      const float inv = 1.0f / sum;
+      o[qb] = floatx16{};
+#pragma unroll
+      for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+        for (int s = 0; s < 2; s++)
+          o[qb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va[kb][s], operand(st[kb], s, inv), o[qb], 0, 0, 0);
+    }
+    // Projection of this head's dims onto every output channel.
+#pragma unroll
+    for (int qb = 0; qb < QB; qb++) {
+      const half8 o0 = operand(o[qb], 0, 1.0f), o1 = operand(o[qb], 1, 1.0f);
+#pragma unroll
+      for (int cb = 0; cb < CB; cb++) {
+        y[cb][qb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(frag(a.wproj, (cb * H + h) * 2, lane), o0,
+                                                           y[cb][qb], 0, 0, 0);
+        y[cb][qb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(frag(a.wproj, (cb * H + h) * 2 + 1, lane),
+                                                           o1, y[cb][qb], 0, 0, 0);
+      }
+    }
+  }
+
+  // Bias, old token, rounded once; rows of Y^T are output channels.
+#pragma unroll
+  for (int qb = 0; qb < QB; qb++) {
+    const long t = src[Q0 + qb];
+    if (!live || t < 0) continue;
+    uint16_t *row = a.map + t * a.stride;
+#pragma unroll
+    for (int cb = 0; cb < CB; cb++)
+#pragma unroll
+      for (int q4 = 0; q4 < 4; q4++) {
+        const int ch = 32 * cb + 8 * q4 + 4 * hf;
+        const float4 bp = *(const float4 *)(a.bproj + ch);
+        const float bpa[4] = {bp.x, bp.y, bp.z, bp.w};
+        uint2 old = *(const uint2 *)(row + ch);
+        uint16_t hv[4];
+        __builtin_memcpy(hv, &old, 8);
+#pragma unroll
+        for (int e = 0; e < 4; e++) hv[e] = f2h(y[cb][qb][4 * q4 + e] + bpa[e] + h2f(hv[e]));
+        __builtin_memcpy(&old, hv, 8);
+        *(uint2 *)(row + ch) = old;
+      }
+  }
+}
+
+template <int C, int QB>
+__global__ __launch_bounds__(256) void k_swin_attend(AttendArgs a) {
+  constexpr int KS = C / 16;
+  constexpr int WPB = QB == 2 ? 4 : 2;  // windows per workgroup
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, hf = lane >> 5, l32 = lane & 31;
+  const long wr = (long)blockIdx.x * WPB + (QB == 2 ? wave : wave >> 1);
+  const bool live = wr < a.g.windows;
+  const long w = live ? wr : a.g.windows - 1;
+
+  long src[2];
+#pragma unroll
+  for (int tb = 0; tb < 2; tb++) src[tb] = win_source(a.g, w, 32 * tb + l32);
+
+  // x fragments, then LayerNorm (mean, then the mean square deviation,
+  // eps 1e-5: math.rs:95-116); tokens past the map's edge are zero rows.
+  half8 xn[2][KS];
+  {
+    u32x4 xr[2][KS];
+#pragma unroll
+    for (int tb = 0; tb < 2; tb++)
+#pragma unroll
+      for (int s = 0; s < KS; s++)
+        xr[tb][s] = *(const u32x4 *)(a.map + (src[tb] < 0 ? 0 : src[tb]) * a.stride + 16 * s + 8 * hf);
+#pragma unroll
+    for (int tb = 0; tb < 2; tb++) {
+      float v[KS][8];
+      float sum = 0.0f;
+#pragma unroll
+      for (int s = 0; s < KS; s++) {
+        uint16_t h[8];
+        __builtin_memcpy(h, &xr[tb][s], 16);
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+          v[s][e] = h2f(h[e]);
+          sum += v[s][e];
+        }
+      }
+      sum += __shfl_xor(sum, 32);
+      const float mean = sum / (float)C;
+      float sq = 0.0f;
+#pragma unroll
+      for (int s = 0; s < KS; s++)
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+          const float d = v[s][e] - mean;
+          sq += d * d;
+        }
+      sq += __shfl_xor(sq, 32);
+      const float inv = 1.0f / sqrtf(sq / (float)C + 1e-5f);
+      const float keep = src[tb] < 0 ? 0.0f : 1.0f;
+#pragma unroll
+      for (int s = 0; s < KS; s++) {
+        const float4 g0 = *(const float4 *)(a.gamma + 16 * s + 8 * hf);
+        const float4 g1 = *(const float4 *)(a.gamma + 16 * s + 8 * hf + 4);
+        const float4 b0 = *(const float4 *)(a.beta + 16 * s + 8 * hf);
+        const float4 b1 = *(const float4 *)(a.beta + 16 * s + 8 * hf + 4);
+        const float gg[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+        const float bb[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+#pragma unroll
+        for (int e = 0; e < 8; e++)
+          xn[tb][s][e] = (_Float16)(((v[s][e] - mean) * inv * gg[e] + bb[e]) * keep);
+      }
+    }
+  }
+  if constexpr (QB == 1) __syncthreads();  // both waves of the window have read it
+
+  if constexpr (QB == 2)
+    attend_heads<C, 2, 0>(a, xn, src, w, live);
+  else if (wave & 1)
+    attend_heads<C, 1, 1>(a, xn, src, w, live);
+  else
+    attend_heads<C, 1, 0>(a, xn, src, w, live);
+}
+
+template <int C, int QB>
+ien_status launch(ien_ctx *ctx, const AttendArgs &a) {
+  constexpr int WPB = QB == 2 ? 4 : 2;
+  const long blocks = (a.g.windows + WPB - 1) / WPB;
+  IEN_CHECK(blocks < (1L << 31), IEN_ERR_INPUT, "%ld windows", a.g.windows);
+  hipLaunchKernelGGL((k_swin_attend<C, QB>), dim3((unsigned)blocks), dim3(256), 0, ctx->stream, a);
+  IEN_HIP(hipGetLastError());
+  return IEN_OK;
+}
+
+}  // namespace
+
+bool swin_attend_supported(int c, int window) {
+  return window == 8 && (c == 32 || c == 64 || c == 128);
+}
+
+std::vector<uint16_t> swin_attend_proj(const float *proj_w, int c) {
+  // Fragment (cb, head, s): lane l, slot i -> output channel 32 cb + l % 32,
+  // head dim 16 s + 4 (l / 32) + (i & 3) + 8 (i >> 2).
+  const int heads = c / 32;
+  std::vector<uint16_t> out((size_t)c * c);
+  for (int cb = 0; cb < c / 32; cb++)
+    for (int h = 0; h < heads; h++)
+      for (int s = 0; s < 2; s++)
+        for (int l = 0; l < 64; l++)
+          for (int i = 0; i < 8; i++) {
+            const int o = 32 * cb + l % 32;
+            const int j = 32 * h + 16 * s + 4 * (l / 32) + (i & 3) + 8 * (i >> 2);
+            out[(((size_t)(cb * heads + h) * 2 + s) * 64 + l) * 8 + i] =
+                f32_to_half(proj_w[(size_t)j * c + o]);
+          }
+  return out;
+}
+
+std::vector<float> swin_attend_tables(const float *tables, int classes, int heads) {
+  // [class][head][kb][qb][q4][lane][e] = table[query 32 qb + lane % 32]
+  // [key 32 kb + 8 q4 + 4 (lane / 32) + e] of a 64-token window.
+  const int n = 64;
+  std::vector<float> out((size_t)classes * heads * 4 * 4 * 256);
+  for (int cls = 0; cls < classes; cls++)
+    for (int h = 0; h < heads; h++) {
+      const float *t = tables + (size_t)(cls * heads + h) * n * n;
+      for (int kb = 0; kb < 2; kb++)
+        for (int qb = 0; qb < 2; qb++)
+          for (int q4 = 0; q4 < 4; q4++)
+            for (int l = 0; l < 64; l++)
+              for (int e = 0; e < 4; e++) {
+                const int i = 32 * qb + l % 32, j = 32 * kb + 8 * q4 + 4 * (l / 32) + e;
+                out[(((((size_t)(cls * heads + h) * 2 + kb) * 2 + qb) * 4 + q4) * 64 + l) * 4 + e] =
+                    t[(size_t)i * n + j];
+              }
+    }
+  return out;
+}
+
+ien_status swin_attend(ien_ctx *ctx, const ien_windows *win, uint16_t *d_map, size_t stride,
+                       int c, const float *gamma, const float *beta, const ien_matrix *qkv,
+                       const uint16_t *d_proj, const float *bproj, const float *d_tables) {
+  IEN_CHECK(ctx && win && d_map && gamma && beta && qkv && d_proj && bproj && d_tables,
+            IEN_ERR_INPUT, "null argument");
+  WinGeo g;
+  ien_status st = geometry(win, &g);
+  if (st != IEN_OK) return st;
+  IEN_CHECK(swin_attend_supported(c, g.window), IEN_ERR_INPUT, "%d channels, window %d", c,
+            g.window);
+  IEN_CHECK(stride >= (size_t)c && stride % 8 == 0 && aligned16(d_map) && aligned16(gamma) &&
+                aligned16(beta),
+            IEN_ERR_INPUT, "map stride %zu / alignment", stride);
+  IEN_CHECK(qkv->k == (size_t)c && qkv->n == 3 * (size_t)c && qkv->kb == c / 16, IEN_ERR_INPUT,
+            "qkv weights %zu x %zu for %d channels", qkv->k, qkv->n, c);
+  AttendArgs a{g, d_map, (long)stride, gamma, beta, qkv->d_packed, qkv->d_bias, d_proj, bproj,
+               d_tables};
+  switch (c) {
+    case 32: return launch<32, 2>(ctx, a);
+    case 64: return launch<64, 1>(ctx, a);
+    default: return launch<128, 1>(ctx, a);
+  }
+}
+
+}  // namespace ien

@@ -5,37 +5,10 @@
 // crates/native-engine/src/attention.rs).
 
 #include "conv_common.h"
+#include "window_geo.h"
 
 namespace ien {
 namespace {
-
-// A block's window geometry (ien_windows plus what follows from it).
-struct WinGeo {
-  int window, shift, height, width;
-  int ph, pw;  // the map padded to whole windows
-  int wx;      // windows per row of windows
-  int n;       // tokens per window
-  long windows;
-};
-
-// Source token of window token i of window w, or -1 past the map's edge:
-// ((wy W + i / W + shift) mod ph, (wx W + i % W + shift) mod pw).
-__device__ __forceinline__ long win_source(const WinGeo &g, long w, int i) {
-  const int wy = (int)(w / g.wx), wxi = (int)(w - (long)wy * g.wx);
-  int y = wy * g.window + i / g.window + g.shift;
-  int x = wxi * g.window + i % g.window + g.shift;
-  if (y >= g.ph) y -= g.ph;  // shift < window <= ph: one wrap at most
-  if (x >= g.pw) x -= g.pw;
-  if (y >= g.height || x >= g.width) return -1;
-  return (long)y * g.width + x;
-}
-
-// swin.rs:171-176: 1 for a window last in its row, 2 last in its column.
-__device__ __forceinline__ int win_class(const WinGeo &g, long w) {
-  if (g.shift == 0) return 0;
-  const long rows = g.windows / g.wx;
-  return (int)(w % g.wx == g.wx - 1) + 2 * (int)(w / g.wx == rows - 1);
-}
 
 __device__ __forceinline__ void unpack8(const u32x4 &raw, float *v) {
   uint16_t h[8];
@@ -258,26 +231,6 @@ __global__ __launch_bounds__(256) void k_window_scatter_add(WinGeo g, const uint
   *(u32x4 *)m = pack8(b);
 }
 
-ien_status geometry(const ien_windows *w, WinGeo *g) {
-  IEN_CHECK(w, IEN_ERR_INPUT, "null windows");
-  IEN_CHECK(w->window >= 1 && w->window * w->window <= 256, IEN_ERR_INPUT,
-            "window %d (at most 16 x 16 tokens)", w->window);
-  IEN_CHECK(w->shift >= 0 && w->shift < w->window, IEN_ERR_INPUT, "shift %d of window %d",
-            w->shift, w->window);
-  IEN_CHECK(w->height >= 1 && w->width >= 1, IEN_ERR_INPUT, "map %d x %d", w->height, w->width);
-  g->window = w->window;
-  g->shift = w->shift;
-  g->height = w->height;
-  g->width = w->width;
-  g->ph = (w->height + w->window - 1) / w->window * w->window;
-  g->pw = (w->width + w->window - 1) / w->window * w->window;
-  g->wx = g->pw / w->window;
-  g->n = w->window * w->window;
-  g->windows = (long)(g->ph / w->window) * g->wx;
-  return IEN_OK;
-}
-
-bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
 
 }  // namespace
 }  // namespace ien

@@ -1,7 +1,9 @@
 """GPU parity of a whole Swin transformer block (ien_swin: scunet swin.rs
 Transformer::attend + mlp, birefnet swin.rs Block) against the oracle's
 or_swin_attend followed by or_swin_mlp, on f16-rounded maps; a second run
-on a larger map reuses the block (scratch grown on demand)."""
+on a larger map reuses the block (scratch grown on demand).  Window 8 with
+32, 64 or 128 channels runs the fused per-window attention, 32..256
+channels the fused MLP; the other widths and windows the unfused path."""
 
 import numpy as np
 import pytest
@@ -32,7 +34,9 @@ def oracle_block(oracle, x, window, shift, masked, wt):
     (64, 8, 0, -np.inf, [(16, 16)]),              # SCUNet W-MSA
     (96, 7, 3, -100.0, [(10, 10), (14, 21)]),     # the reference's BiRefNet window
     (32, 12, 6, -100.0, [(15, 13), (24, 24)]),    # the configuration's BiRefNet window
-    (128, 8, 4, -np.inf, [(16, 24)]),             # SCUNet level 3
+    (32, 8, 4, -np.inf, [(16, 24), (12, 20)]),    # SCUNet level 1; windows past the map's edge
+    (32, 8, 0, -np.inf, [(8, 8), (24, 16)]),      # one window, then several
+    (128, 8, 4, -np.inf, [(16, 24), (20, 12)]),   # SCUNet level 3
     (256, 8, 0, -np.inf, [(8, 16), (9, 13)]),     # SCUNet body; a ragged last row block
     (192, 12, 6, -100.0, [(12, 24)]),             # Swin-T stage 2
     (384, 12, 0, -100.0, [(12, 12)]),             # Swin-T stage 3 (MLP through the row products)
