@@ -93,7 +93,12 @@ struct Res8 {
   static constexpr int STG = 3 * HALO;
   static constexpr int PARAM = STG + 2 * STAGE;
   static constexpr int WOFF = 2 * HALO;
-  static constexpr int LDS = PARAM + 2048;
+  // When they fit: two buffers for the old outputs of an accumulating tile
+  // (its 16-byte store items, in item order).
+  static constexpr int OLDB = TR * TC * 8 * 16;
+  static constexpr int OLD = PARAM + 2048;
+  static constexpr bool OLD_LDS = OLD + 2 * OLDB <= 160 * 1024;
+  static constexpr int LDS = OLD_LDS ? OLD + 2 * OLDB : PARAM + 2048;
   static constexpr int SITEMS = TR * TC * 8 / 512;  // 16-byte stores per thread and tile
   static constexpr int DEPTH = 3;                   // fragment prefetch
   static_assert(C == 16 || C == 32 || C == 64, "channels");
@@ -191,10 +196,16 @@ __global__ __launch_bounds__(512) void conv_res8(ConvArgs a) {
   // Plain f16 NHWC outputs of whole 16-byte chunks below 2 GiB go out as
   // buffer stores; anything else element by element (store_slow).
   const long out_bytes = (long)(a.p_end - a.p_begin) * a.ys * 2;
-  const bool fast = !a.accumulate && !a.out_f32 && !a.out_nchw && a.N % 8 == 0 &&
-                    a.ys % 8 == 0 && (((uintptr_t)a.y) & 15) == 0 && out_bytes <= 0x7fff0000L;
+  const bool plain = !a.out_f32 && !a.out_nchw && a.N % 8 == 0 && a.ys % 8 == 0 &&
+                     (((uintptr_t)a.y) & 15) == 0 && out_bytes <= 0x7fff0000L;
+  // Accumulating into such outputs: the old items of tile t-1 are loaded
+  // straight into LDS in iteration t (before its halo loads, so the wait at
+  // the end of the iteration covers them) and added in iteration t+1.
+  const bool accum = plain && a.accumulate && R::OLD_LDS;
+  const bool fast = plain && (!a.accumulate || accum);
   const __amdgpu_buffer_rsrc_t yr =
       __builtin_amdgcn_make_buffer_rsrc(a.y, 0, fast ? (int)out_bytes : 0, 0x00020000);
+  const int4v yl = buffer_rsrc(a.y, accum ? (int)out_bytes : 0);
 
   // Byte offset of output item j of this thread (16 bytes: 8 channels of
   // one pixel; 8 consecutive threads write one pixel's 128 bytes), or OOB.
@@ -211,6 +222,27 @@ __global__ __launch_bounds__(512) void conv_res8(ConvArgs a) {
   auto item_src = [&](int j, const unsigned char *stage) {
     const int v = tid + 512 * j;
     return *(const u32x4 *)(stage + ((v >> 3) * R::SPX + (v & 7) * 8) * 2);
+  };
+  auto old_buf = [&](int k) { return lds + R::OLD + k * R::OLDB; };
+  // Old items of tile mts into old buffer k (8 KiB per round of items).
+  auto load_old = [&](int mts, int k) {
+#pragma unroll
+    for (int j = 0; j < R::SITEMS; j++)
+      dma_lds(yl, __builtin_amdgcn_readfirstlane(lds0 + R::OLD + k * R::OLDB + (512 * j + 64 * wave) * 16),
+              item_off(j, mts, true));
+  };
+  // Staged sum + old item, activated, for an accumulating store.
+  auto add_old = [&](int j, u32x4 sv, const unsigned char *ob) {
+    const int v = tid + 512 * j, chunk = v & 7;
+    const u32x4 ov = *(const u32x4 *)(ob + 16 * v);
+    uint16_t h[8], o[8];
+    __builtin_memcpy(h, &sv, 16);
+    __builtin_memcpy(o, &ov, 16);
+#pragma unroll
+    for (int e = 0; e < 8; e++)
+      h[e] = f2h(activate(h2f(h[e]) + h2f(o[e]), a.act, slope_l[chunk * 8 + e]));
+    __builtin_memcpy(&sv, h, 16);
+    return sv;
   };
 
   // Accumulating, NCHW or ragged outputs: the staged sums (bias included,
@@ -284,7 +316,8 @@ __global__ __launch_bounds__(512) void conv_res8(ConvArgs a) {
   // loads into buffer `nxt` and (unless FIRST: no earlier tile) tile t-1's
   // epilogue and tile t-2's stores spread over the steps.
   auto mma = [&](auto first, int cur, int nxt, int nmt, bool dma, const floatx16 &acc1,
-                 unsigned char *stage1, const int *soff, const unsigned char *stage2) {
+                 unsigned char *stage1, const int *soff, const unsigned char *stage2,
+                 int old_mt, int old_wr, const unsigned char *old_rd) {
     constexpr bool FIRST = decltype(first)::value;
     int noy0, nox0;
     origin(nmt, noy0, nox0);
@@ -303,7 +336,9 @@ __global__ __launch_bounds__(512) void conv_res8(ConvArgs a) {
         if (dma) load_halo(e, noy0, nox0, nxt);
       } else {
         if (e < NS) {
+          if (e == 0 && accum) load_old(old_mt, old_wr);  // before this tile's halo loads
           sv[e] = item_src(e, stage2);
+          if (accum) sv[e] = add_old(e, sv[e], old_rd);
         } else if (e == NS) {
           if (dma) load_halo(0, noy0, nox0, nxt);
         } else if (e < 2 * NS + 1) {
@@ -346,7 +381,7 @@ __global__ __launch_bounds__(512) void conv_res8(ConvArgs a) {
     const int h2 = h == 0 ? 2 : h - 1;  // (t + 2) % 3
     floatx16 acc;
     if (t == 0) {
-      acc = mma(std::true_type{}, h, h2, far, dma, acc1, nullptr, nullptr, nullptr);
+      acc = mma(std::true_type{}, h, h2, far, dma, acc1, nullptr, nullptr, nullptr, 0, 0, nullptr);
     } else {
       const int par = t & 1;
       unsigned char *st1 = stage_buf(par);
@@ -356,7 +391,8 @@ __global__ __launch_bounds__(512) void conv_res8(ConvArgs a) {
 #pragma unroll
       for (int j = 0; j < R::SITEMS; j++)
         soff[j] = item_off(j, mt2 < 0 ? mt : mt2, mt2 >= 0 && fast);
-      acc = mma(std::false_type{}, h, h2, far, dma, acc1, st1, soff, st2);
+      acc = mma(std::false_type{}, h, h2, far, dma, acc1, st1, soff, st2, mt1, t & 1,
+                old_buf((t - 1) & 1));
     }
     acc1 = acc;
     mt2 = mt1;
@@ -378,24 +414,30 @@ __global__ __launch_bounds__(512) void conv_res8(ConvArgs a) {
   if (mt2 >= 0) {
     if (fast) {
 #pragma unroll
-      for (int j = 0; j < R::SITEMS; j++)
-        __builtin_amdgcn_raw_buffer_store_b128(item_src(j, stage_buf(par ^ 1)), yr,
-                                               item_off(j, mt2, true), 0, 0);
+      for (int j = 0; j < R::SITEMS; j++) {
+        u32x4 sv = item_src(j, stage_buf(par ^ 1));
+        if (accum) sv = add_old(j, sv, old_buf((t - 1) & 1));
+        __builtin_amdgcn_raw_buffer_store_b128(sv, yr, item_off(j, mt2, true), 0, 0);
+      }
     } else {
       store_slow(mt2, stage_buf(par ^ 1));
     }
   }
   if (mt1 >= 0) {
+    if (accum) load_old(mt1, t & 1);
 #pragma unroll
     for (int g = 0; g < 4; g++) epilogue(acc1, g, stage_buf(par));
   }
+  if (accum) wait_vm<0>();  // tile t-1's old items
   __syncthreads();
   if (mt1 >= 0) {
     if (fast) {
 #pragma unroll
-      for (int j = 0; j < R::SITEMS; j++)
-        __builtin_amdgcn_raw_buffer_store_b128(item_src(j, stage_buf(par)), yr,
-                                               item_off(j, mt1, true), 0, 0);
+      for (int j = 0; j < R::SITEMS; j++) {
+        u32x4 sv = item_src(j, stage_buf(par));
+        if (accum) sv = add_old(j, sv, old_buf(t & 1));
+        __builtin_amdgcn_raw_buffer_store_b128(sv, yr, item_off(j, mt1, true), 0, 0);
+      }
     } else {
       store_slow(mt1, stage_buf(par));
     }

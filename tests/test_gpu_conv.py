@@ -117,6 +117,21 @@ def test_activations_and_accumulate(ctx, oracle, act):
     close(got, want)
 
 
+# The resident kernel's accumulating path for 16 and 32 input channels (old
+# outputs staged one tile ahead): ragged tiles, several tiles per CU (the
+# last case), activations after the sum, a padded output stride.
+@pytest.mark.parametrize("c,n,h,w,act,pad", [(32, 32, 7, 130, 0, 0), (32, 64, 33, 64, 1, 8),
+                                            (16, 48, 20, 100, 3, 0), (32, 32, 320, 330, 0, 0),
+                                            (16, 16, 65, 63, 2, 8)])
+def test_resident_accumulate(ctx, oracle, c, n, h, w, act, pad):
+    x, wt, b = case(11 + c + n, h, w, c, n, 9)
+    slope = np.linspace(0.05, 0.5, n).astype(np.float32)
+    init = f16(np.random.default_rng(h + w).standard_normal((h * w, n)))
+    got = run_gpu(ctx, x, wt, b, act=act, slope=slope, init=init, stride_pad=pad)
+    want = want_cpu(oracle, x, wt, b, act=act, slope=slope, init=init)
+    close(got, want)
+
+
 def test_nchw_in_and_out(ctx, oracle):
     import ien
 
