@@ -5,7 +5,8 @@
 // the window's own tokens.  Window 8 (64 tokens), c = 32, 64 or 128
 // (heads of 32).
 //
-// Everything between the load of x and the store stays in registers:
+// Everything between the load of x and the store stays in registers (but
+// for the exchange of head outputs):
 //  - x is loaded as MFMA fragments (lane l: token l % 32 of a 32-token
 //    block, channels 16 s + 8 (l / 32) + 0..7) and normalised in place;
 //    those registers are both the B operand of K^T = Wk^T x^T, Q^T = Wq^T
@@ -28,9 +29,8 @@
 // Rounding points are the unfused path's: normalised x, q, k, v, the
 // probabilities and the attention output are f16; products accumulate in
 // f32; the result is rounded once after bias and residual.
-// With two waves per window (c = 64, 128) each wave takes 32 queries and
-// both compute K and V for all 64 keys; a barrier separates every read of
-// the window from the first write.
+// One wave per window and head of 32 dims; with several heads the waves of
+// a window exchange their outputs through LDS before the projection.
 
 #include "conv_common.h"
 #include "window_geo.h"
@@ -63,233 +63,252 @@ __device__ __forceinline__ half8 operand(const floatx16 &t, int s, float scale) 
   return h;
 }
 
-// The heads, the projection and the store for query blocks Q0 .. Q0 + QB
-// - 1 of window w (Q0 a constant, so that no register array is indexed by
-// a variable).
-template <int C, int QB, int Q0>
-__device__ __forceinline__ void attend_heads(const AttendArgs &a, const half8 (&xn)[2][C / 16],
-                                             const long (&src)[2], long w, bool live) {
-  constexpr int H = C / 32, CB = C / 32, KS = C / 16;
-  const int lane = threadIdx.x & 63, hf = lane >> 5, l32 = lane & 31;
-  floatx16 y[CB][QB];
+// x of window w's 64 tokens as normalised fragments (LayerNorm: mean, then
+// the mean square deviation, eps 1e-5: math.rs:95-116); tokens past the
+// map's edge are zero rows.
+template <int C>
+__device__ __forceinline__ void load_norm(const AttendArgs &a, const long (&src)[2],
+                                          half8 (&xn)[2][C / 16]) {
+  constexpr int KS = C / 16;
+  const int hf = (threadIdx.x & 63) >> 5;
+  u32x4 xr[2][KS];
 #pragma unroll
-  for (int cb = 0; cb < CB; cb++)
+  for (int tb = 0; tb < 2; tb++)
 #pragma unroll
-    for (int qb = 0; qb < QB; qb++) y[cb][qb] = floatx16{};
-  const int cls = win_class(a.g, w);
-  const float scale = 0.17677669529663688f;  // 1 / sqrt(32)
-
-  for (int h = 0; h < H; h++) {
-    floatx16 kt[2] = {}, vv[2] = {}, qt[QB];
+    for (int s = 0; s < KS; s++)
+      xr[tb][s] = *(const u32x4 *)(a.map + (src[tb] < 0 ? 0 : src[tb]) * a.stride + 16 * s + 8 * hf);
 #pragma unroll
-    for (int qb = 0; qb < QB; qb++) qt[qb] = floatx16{};
+  for (int tb = 0; tb < 2; tb++) {
+    float v[KS][8];
+    float sum = 0.0f;
 #pragma unroll
     for (int s = 0; s < KS; s++) {
-      const half8 wq = frag(a.wqkv, h * KS + s, lane);
+      uint16_t h[8];
+      __builtin_memcpy(h, &xr[tb][s], 16);
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        v[s][e] = h2f(h[e]);
+        sum += v[s][e];
+      }
+    }
+    sum += __shfl_xor(sum, 32);
+    const float mean = sum / (float)C;
+    float sq = 0.0f;
+#pragma unroll
+    for (int s = 0; s < KS; s++)
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        const float d = v[s][e] - mean;
+        sq += d * d;
+      }
+    sq += __shfl_xor(sq, 32);
+    const float inv = 1.0f / sqrtf(sq / (float)C + 1e-5f);
+    const float keep = src[tb] < 0 ? 0.0f : 1.0f;
+#pragma unroll
+    for (int s = 0; s < KS; s++) {
+      const float4 g0 = *(const float4 *)(a.gamma + 16 * s + 8 * hf);
+      const float4 g1 = *(const float4 *)(a.gamma + 16 * s + 8 * hf + 4);
+      const float4 b0 = *(const float4 *)(a.beta + 16 * s + 8 * hf);
+      const float4 b1 = *(const float4 *)(a.beta + 16 * s + 8 * hf + 4);
+      const float gg[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+      const float bb[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+#pragma unroll
+      for (int e = 0; e < 8; e++)
+        xn[tb][s][e] = (_Float16)(((v[s][e] - mean) * inv * gg[e] + bb[e]) * keep);
+    }
+  }
+}
+
+// Head h of the window: q, k, v of all 64 tokens, S^T, softmax, O^T; the
+// result as the B operands of the projection, ob[query block][k step]
+// (head dims 16 s + 4 hf + {0..3, 8..11}).
+template <int C>
+__device__ __forceinline__ void head_attention(const AttendArgs &a, const half8 (&xn)[2][C / 16],
+                                               int cls, int h, half8 (&ob)[2][2]) {
+  constexpr int H = C / 32, KS = C / 16, CB = C / 32;
+  const int lane = threadIdx.x & 63, hf = lane >> 5, l32 = lane & 31;
+  const float scale = 0.17677669529663688f;  // 1 / sqrt(32)
+  // K and V first, then Q: fewer accumulators live at once.
+  half8 ka[2][2], qo[2][2], va[2][2];
+  {
+    floatx16 kt[2] = {}, vv[2] = {};
+#pragma unroll
+    for (int s = 0; s < KS; s++) {
       const half8 wk = frag(a.wqkv, (CB + h) * KS + s, lane);
       const half8 wv = frag(a.wqkv, (2 * CB + h) * KS + s, lane);
 #pragma unroll
-      for (int kb = 0; kb < 2; kb++) {
-        kt[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wk, xn[kb][s], kt[kb], 0, 0, 0);
-        vv[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(xn[kb][s], wv, vv[kb], 0, 0, 0);
-      }
-#pragma unroll
-      for (int qb = 0; qb < QB; qb++) {
-        const half8 xq = xn[Q0 + qb][s];
-        qt[qb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wq, xq, qt[qb], 0, 0, 0);
+      for (int tb = 0; tb < 2; tb++) {
+        kt[tb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wk, xn[tb][s], kt[tb], 0, 0, 0);
+        vv[tb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(xn[tb][s], wv, vv[tb], 0, 0, 0);
       }
     }
-    // Biases: K^T, Q^T rows are dims 8 (r / 4) + 4 hf + r % 4; V columns
-    // are dims l32.
+    // Biases: K^T rows are dims 8 (r / 4) + 4 hf + r % 4; V columns are
+    // dims l32.
     const float bv = a.bqkv[2 * C + 32 * h + l32];
 #pragma unroll
     for (int q4 = 0; q4 < 4; q4++) {
-      const float4 bq = *(const float4 *)(a.bqkv + 32 * h + 8 * q4 + 4 * hf);
       const float4 bk = *(const float4 *)(a.bqkv + C + 32 * h + 8 * q4 + 4 * hf);
-      const float bqa[4] = {bq.x, bq.y, bq.z, bq.w}, bka[4] = {bk.x, bk.y, bk.z, bk.w};
+      const float bka[4] = {bk.x, bk.y, bk.z, bk.w};
 #pragma unroll
-      for (int e = 0; e < 4; e++) {
+      for (int e = 0; e < 4; e++)
 #pragma unroll
-        for (int kb = 0; kb < 2; kb++) {
-          kt[kb][4 * q4 + e] += bka[e];
-          vv[kb][4 * q4 + e] += bv;
+        for (int tb = 0; tb < 2; tb++) {
+          kt[tb][4 * q4 + e] += bka[e];
+          vv[tb][4 * q4 + e] += bv;
         }
-#pragma unroll
-        for (int qb = 0; qb < QB; qb++) qt[qb][4 * q4 + e] += bqa[e];
-      }
     }
-    half8 ka[2][2], qo[QB][2], va[2][2];
 #pragma unroll
-    for (int s = 0; s < 2; s++) {
+    for (int s = 0; s < 2; s++)
 #pragma unroll
-      for (int kb = 0; kb < 2; kb++) {
-        ka[kb][s] = operand(kt[kb], s, 1.0f);
-        va[kb][s] = operand(vv[kb], s, 1.0f);
+      for (int tb = 0; tb < 2; tb++) {
+        ka[tb][s] = operand(kt[tb], s, 1.0f);
+        va[tb][s] = operand(vv[tb], s, 1.0f);
       }
+  }
+  {
+    floatx16 qt[2] = {};
 #pragma unroll
-      for (int qb = 0; qb < QB; qb++) qo[qb][s] = operand(qt[qb], s, 1.0f);
+    for (int s = 0; s < KS; s++) {
+      const half8 wq = frag(a.wqkv, h * KS + s, lane);
+#pragma unroll
+      for (int tb = 0; tb < 2; tb++)
+        qt[tb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wq, xn[tb][s], qt[tb], 0, 0, 0);
     }
-    // S^T (keys x queries), bias, softmax over keys.
-    const float *tbl = a.bias + (size_t)(cls * H + h) * 4 * 4 * 256;
-    floatx16 o[QB];
 #pragma unroll
-    for (int qb = 0; qb < QB; qb++) {
-      floatx16 st[2];
-      float mx = -__builtin_inff();
+    for (int q4 = 0; q4 < 4; q4++) {
+      const float4 bq = *(const float4 *)(a.bqkv + 32 * h + 8 * q4 + 4 * hf);
+      const float bqa[4] = {bq.x, bq.y, bq.z, bq.w};
 #pragma unroll
-      for (int kb = 0; kb < 2; kb++) {
-        st[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[kb][0], qo[qb][0], floatx16{}, 0, 0, 0);
-        st[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[kb][1], qo[qb][1], st[kb], 0, 0, 0);
-        const float *tq = tbl + ((kb * 2 + Q0 + qb) * 4) * 256 + lane * 4;
+      for (int e = 0; e < 4; e++)
 #pragma unroll
-        for (int q4 = 0; q4 < 4; q4++) {
-          const float4 bt = *(const float4 *)(tq + q4 * 256);
-          const float bta[4] = {bt.x, bt.y, bt.z, bt.w};
+        for (int tb = 0; tb < 2; tb++) qt[tb][4 * q4 + e] += bqa[e];
+    }
 #pragma unroll
-          for (int e = 0; e < 4; e++) {
-            const float v = st[kb][4 * q4 + e] * scale + bta[e];
-            st[kb][4 * q4 + e] = v;
-            mx = fmaxf(mx, v);
-          }
+    for (int s = 0; s < 2; s++)
+#pragma unroll
+      for (int tb = 0; tb < 2; tb++) qo[tb][s] = operand(qt[tb], s, 1.0f);
+  }
+  const float *tbl = a.bias + (size_t)(cls * H + h) * 4 * 4 * 256;
+#pragma unroll
+  for (int qb = 0; qb < 2; qb++) {
+    floatx16 st[2];
+    float mx = -__builtin_inff();
+#pragma unroll
+    for (int kb = 0; kb < 2; kb++) {
+      st[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[kb][0], qo[qb][0], floatx16{}, 0, 0, 0);
+      st[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[kb][1], qo[qb][1], st[kb], 0, 0, 0);
+      const float *tq = tbl + ((kb * 2 + qb) * 4) * 256 + lane * 4;
+#pragma unroll
+      for (int q4 = 0; q4 < 4; q4++) {
+        const float4 bt = *(const float4 *)(tq + q4 * 256);
+        const float bta[4] = {bt.x, bt.y, bt.z, bt.w};
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          const float v = st[kb][4 * q4 + e] * scale + bta[e];
+          st[kb][4 * q4 + e] = v;
+          mx = fmaxf(mx, v);
         }
       }
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
-      float sum = 0.0f;
-#pragma unroll
-      for (int kb = 0; kb < 2; kb++)
-#pragma unroll
-        for (int r = 0; r < 16; r++) {
-          const float p = __expf(st[kb][r] - mx);
-          st[kb][r] = p;
-          sum += p;
-        }
-      sum += __shfl_xor(sum, 32);
-      const float inv = 1.0f / sum;
-      o[qb] = floatx16{};
-#pragma unroll
-      for (int kb = 0; kb < 2; kb++)
-#pragma unroll
-        for (int s = 0; s < 2; s++)
-          o[qb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va[kb][s], operand(st[kb], s, inv), o[qb], 0, 0, 0);
     }
-    // Projection of this head's dims onto every output channel.
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    float sum = 0.0f;
 #pragma unroll
-    for (int qb = 0; qb < QB; qb++) {
-      const half8 o0 = operand(o[qb], 0, 1.0f), o1 = operand(o[qb], 1, 1.0f);
+    for (int kb = 0; kb < 2; kb++)
 #pragma unroll
-      for (int cb = 0; cb < CB; cb++) {
-        y[cb][qb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(frag(a.wproj, (cb * H + h) * 2, lane), o0,
-                                                           y[cb][qb], 0, 0, 0);
-        y[cb][qb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(frag(a.wproj, (cb * H + h) * 2 + 1, lane),
-                                                           o1, y[cb][qb], 0, 0, 0);
+      for (int r = 0; r < 16; r++) {
+        const float p = __expf(st[kb][r] - mx);
+        st[kb][r] = p;
+        sum += p;
       }
-    }
+    sum += __shfl_xor(sum, 32);
+    const float inv = 1.0f / sum;
+    floatx16 o = {};
+#pragma unroll
+    for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+      for (int s = 0; s < 2; s++)
+        o = __builtin_amdgcn_mfma_f32_32x32x16_f16(va[kb][s], operand(st[kb], s, inv), o, 0, 0, 0);
+    ob[qb][0] = operand(o, 0, 1.0f);
+    ob[qb][1] = operand(o, 1, 1.0f);
+  }
+}
+
+// One wave per window and head (H = c / 32 waves per window, 4 / H windows
+// per workgroup).  With several heads the waves of a window leave their
+// heads' outputs in LDS (as the operands they are), meet at a barrier, and
+// wave h projects all heads onto output channels 32 h .. 32 h + 31; the
+// barrier also orders every read of the window before the first write.
+template <int C>
+__global__ __launch_bounds__(256, C <= 64 ? 2 : 1) void k_swin_attend(AttendArgs a) {
+  constexpr int H = C / 32, KS = C / 16, WPG = 4 / H;
+  __shared__ half8 xo[H > 1 ? WPG * 2 * H * 2 * 64 : 1];  // [window][query block][head][s][lane]
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, hf = lane >> 5, l32 = lane & 31;
+  const int wl = wave / H, h = wave % H;
+  const long wr = (long)blockIdx.x * WPG + wl;
+  const bool live = wr < a.g.windows;
+  const long w = live ? wr : a.g.windows - 1;
+  long src[2];
+#pragma unroll
+  for (int tb = 0; tb < 2; tb++) src[tb] = win_source(a.g, w, 32 * tb + l32);
+  half8 xn[2][KS];
+  load_norm<C>(a, src, xn);
+  half8 ob[2][2];
+  head_attention<C>(a, xn, win_class(a.g, w), h, ob);
+
+  // Y^T (output channels 32 h + rows, tokens of query block qb).
+  floatx16 y[2] = {};
+  if constexpr (H == 1) {
+#pragma unroll
+    for (int qb = 0; qb < 2; qb++)
+#pragma unroll
+      for (int s = 0; s < 2; s++)
+        y[qb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(frag(a.wproj, s, lane), ob[qb][s], y[qb], 0, 0, 0);
+  } else {
+#pragma unroll
+    for (int qb = 0; qb < 2; qb++)
+#pragma unroll
+      for (int s = 0; s < 2; s++) xo[(((wl * 2 + qb) * H + h) * 2 + s) * 64 + lane] = ob[qb][s];
+    __syncthreads();
+#pragma unroll
+    for (int hh = 0; hh < H; hh++)
+#pragma unroll
+      for (int s = 0; s < 2; s++) {
+        const half8 wp = frag(a.wproj, (h * H + hh) * 2 + s, lane);
+#pragma unroll
+        for (int qb = 0; qb < 2; qb++)
+          y[qb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+              wp, xo[(((wl * 2 + qb) * H + hh) * 2 + s) * 64 + lane], y[qb], 0, 0, 0);
+      }
   }
 
   // Bias, old token, rounded once; rows of Y^T are output channels.
 #pragma unroll
-  for (int qb = 0; qb < QB; qb++) {
-    const long t = src[Q0 + qb];
+  for (int qb = 0; qb < 2; qb++) {
+    const long t = src[qb];
     if (!live || t < 0) continue;
     uint16_t *row = a.map + t * a.stride;
 #pragma unroll
-    for (int cb = 0; cb < CB; cb++)
+    for (int q4 = 0; q4 < 4; q4++) {
+      const int ch = 32 * h + 8 * q4 + 4 * hf;
+      const float4 bp = *(const float4 *)(a.bproj + ch);
+      const float bpa[4] = {bp.x, bp.y, bp.z, bp.w};
+      uint2 old = *(const uint2 *)(row + ch);
+      uint16_t hv[4];
+      __builtin_memcpy(hv, &old, 8);
 #pragma unroll
-      for (int q4 = 0; q4 < 4; q4++) {
-        const int ch = 32 * cb + 8 * q4 + 4 * hf;
-        const float4 bp = *(const float4 *)(a.bproj + ch);
-        const float bpa[4] = {bp.x, bp.y, bp.z, bp.w};
-        uint2 old = *(const uint2 *)(row + ch);
-        uint16_t hv[4];
-        __builtin_memcpy(hv, &old, 8);
-#pragma unroll
-        for (int e = 0; e < 4; e++) hv[e] = f2h(y[cb][qb][4 * q4 + e] + bpa[e] + h2f(hv[e]));
-        __builtin_memcpy(&old, hv, 8);
-        *(uint2 *)(row + ch) = old;
-      }
-  }
-}
-
-template <int C, int QB>
-__global__ __launch_bounds__(256) void k_swin_attend(AttendArgs a) {
-  constexpr int KS = C / 16;
-  constexpr int WPB = QB == 2 ? 4 : 2;  // windows per workgroup
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, hf = lane >> 5, l32 = lane & 31;
-  const long wr = (long)blockIdx.x * WPB + (QB == 2 ? wave : wave >> 1);
-  const bool live = wr < a.g.windows;
-  const long w = live ? wr : a.g.windows - 1;
-
-  long src[2];
-#pragma unroll
-  for (int tb = 0; tb < 2; tb++) src[tb] = win_source(a.g, w, 32 * tb + l32);
-
-  // x fragments, then LayerNorm (mean, then the mean square deviation,
-  // eps 1e-5: math.rs:95-116); tokens past the map's edge are zero rows.
-  half8 xn[2][KS];
-  {
-    u32x4 xr[2][KS];
-#pragma unroll
-    for (int tb = 0; tb < 2; tb++)
-#pragma unroll
-      for (int s = 0; s < KS; s++)
-        xr[tb][s] = *(const u32x4 *)(a.map + (src[tb] < 0 ? 0 : src[tb]) * a.stride + 16 * s + 8 * hf);
-#pragma unroll
-    for (int tb = 0; tb < 2; tb++) {
-      float v[KS][8];
-      float sum = 0.0f;
-#pragma unroll
-      for (int s = 0; s < KS; s++) {
-        uint16_t h[8];
-        __builtin_memcpy(h, &xr[tb][s], 16);
-#pragma unroll
-        for (int e = 0; e < 8; e++) {
-          v[s][e] = h2f(h[e]);
-          sum += v[s][e];
-        }
-      }
-      sum += __shfl_xor(sum, 32);
-      const float mean = sum / (float)C;
-      float sq = 0.0f;
-#pragma unroll
-      for (int s = 0; s < KS; s++)
-#pragma unroll
-        for (int e = 0; e < 8; e++) {
-          const float d = v[s][e] - mean;
-          sq += d * d;
-        }
-      sq += __shfl_xor(sq, 32);
-      const float inv = 1.0f / sqrtf(sq / (float)C + 1e-5f);
-      const float keep = src[tb] < 0 ? 0.0f : 1.0f;
-#pragma unroll
-      for (int s = 0; s < KS; s++) {
-        const float4 g0 = *(const float4 *)(a.gamma + 16 * s + 8 * hf);
-        const float4 g1 = *(const float4 *)(a.gamma + 16 * s + 8 * hf + 4);
-        const float4 b0 = *(const float4 *)(a.beta + 16 * s + 8 * hf);
-        const float4 b1 = *(const float4 *)(a.beta + 16 * s + 8 * hf + 4);
-        const float gg[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
-        const float bb[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
-#pragma unroll
-        for (int e = 0; e < 8; e++)
-          xn[tb][s][e] = (_Float16)(((v[s][e] - mean) * inv * gg[e] + bb[e]) * keep);
-      }
+      for (int e = 0; e < 4; e++) hv[e] = f2h(y[qb][4 * q4 + e] + bpa[e] + h2f(hv[e]));
+      __builtin_memcpy(&old, hv, 8);
+      *(uint2 *)(row + ch) = old;
     }
   }
-  if constexpr (QB == 1) __syncthreads();  // both waves of the window have read it
-
-  if constexpr (QB == 2)
-    attend_heads<C, 2, 0>(a, xn, src, w, live);
-  else if (wave & 1)
-    attend_heads<C, 1, 1>(a, xn, src, w, live);
-  else
-    attend_heads<C, 1, 0>(a, xn, src, w, live);
 }
 
-template <int C, int QB>
+template <int C>
 ien_status launch(ien_ctx *ctx, const AttendArgs &a) {
-  constexpr int WPB = QB == 2 ? 4 : 2;
-  const long blocks = (a.g.windows + WPB - 1) / WPB;
+  constexpr int WPG = 4 / (C / 32);
+  const long blocks = (a.g.windows + WPG - 1) / WPG;
   IEN_CHECK(blocks < (1L << 31), IEN_ERR_INPUT, "%ld windows", a.g.windows);
-  hipLaunchKernelGGL((k_swin_attend<C, QB>), dim3((unsigned)blocks), dim3(256), 0, ctx->stream, a);
+  hipLaunchKernelGGL(k_swin_attend<C>, dim3((unsigned)blocks), dim3(256), 0, ctx->stream, a);
   IEN_HIP(hipGetLastError());
   return IEN_OK;
 }
@@ -357,9 +376,9 @@ ien_status swin_attend(ien_ctx *ctx, const ien_windows *win, uint16_t *d_map, si
   AttendArgs a{g, d_map, (long)stride, gamma, beta, qkv->d_packed, qkv->d_bias, d_proj, bproj,
                d_tables};
   switch (c) {
-    case 32: return launch<32, 2>(ctx, a);
-    case 64: return launch<64, 1>(ctx, a);
-    default: return launch<128, 1>(ctx, a);
+    case 32: return launch<32>(ctx, a);
+    case 64: return launch<64>(ctx, a);
+    default: return launch<128>(ctx, a);
   }
 }
 
