@@ -101,7 +101,7 @@ ien_status launch_conv(ien_ctx *ctx, const ConvCall &c);
 ien_status swin_reserve(ien_swin *b, int height, int width);
 
 // swin_mlp.hip: map rows += fc2(GELU(fc1(LayerNorm(rows)))) in one pass,
-// for c a multiple of 32 up to 256 (16-byte aligned rows).
+// for c = 32, 64 and 96 (16-byte aligned rows).
 bool swin_mlp_supported(int c);
 ien_status swin_mlp(ien_ctx *ctx, uint16_t *d_map, size_t stride, long rows, int c,
                     const float *gamma, const float *beta, const ien_matrix *fc1,

@@ -1,6 +1,6 @@
 // swin_mlp.hip -- the Swin block's MLP half in one pass over the token rows
 // (crates/scunet-native/src/swin.rs:236-275, crates/birefnet-native/src/
-// swin.rs Mlp): x += fc2(GELU(fc1(LayerNorm(x)))), for c = 32 .. 256.
+// swin.rs Mlp): x += fc2(GELU(fc1(LayerNorm(x)))), for c = 32, 64 and 96.
 //
 // One workgroup of 4 waves per 64 token rows:
 //  - LayerNorm (mean, then the mean square deviation, eps 1e-5: math.rs:
@@ -215,7 +215,10 @@ ien_status launch(ien_ctx *ctx, const MlpArgs &a) {
 
 }  // namespace
 
-bool swin_mlp_supported(int c) { return c % 32 == 0 && c >= 32 && c <= 256; }
+// Up to 96 channels: wider blocks have too few rows per token map at the
+// networks' sizes to fill the chip with 64-row workgroups, and their
+// weights no longer stay close; the row products serve them better.
+bool swin_mlp_supported(int c) { return c == 32 || c == 64 || c == 96; }
 
 ien_status swin_mlp(ien_ctx *ctx, uint16_t *d_map, size_t stride, long rows, int c,
                     const float *gamma, const float *beta, const ien_matrix *fc1,
@@ -236,12 +239,7 @@ ien_status swin_mlp(ien_ctx *ctx, uint16_t *d_map, size_t stride, long rows, int
   switch (c) {
     case 32: return launch<32>(ctx, a);
     case 64: return launch<64>(ctx, a);
-    case 96: return launch<96>(ctx, a);
-    case 128: return launch<128>(ctx, a);
-    case 160: return launch<160>(ctx, a);
-    case 192: return launch<192>(ctx, a);
-    case 224: return launch<224>(ctx, a);
-    default: return launch<256>(ctx, a);
+    default: return launch<96>(ctx, a);
   }
 }
 
