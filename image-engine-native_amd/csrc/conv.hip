@@ -638,17 +638,19 @@ static ien_status run_cfg(ien_ctx *ctx, ConvArgs a) {
   IEN_CHECK(blocks > 0 && blocks < (1L << 31), IEN_ERR_INPUT, "grid of %ld tiles", blocks);
   // The packed weights must cover every fragment the tiles touch.
   IEN_CHECK(a.tiles_n * Cfg::NBT <= a.NB, IEN_ERR_INPUT, "weights narrower than the tile");
-  // Split-K when the tiles leave three quarters of the CUs idle: about two
-  // workgroups per CU, each split at least 512 deep in K (the partial sums
-  // cost an f32 write and read of the output per split), partial sums in
-  // the context's workspace, then the finishing pass.
+  // Split-K when the tiles leave three quarters of the CUs idle, or any CU
+  // idle for a 1 x 1 product at least 1536 deep: about two workgroups per
+  // CU, each split at least 512 deep in K (the partial sums cost an f32
+  // write and read of the output per split), partial sums in the context's
+  // workspace, then the finishing pass.
   const int chunks = (a.C + CK - 1) / CK;
   const long rows = a.p_end - a.p_begin;
   const int pitch = a.tiles_n * Cfg::BN;
   const int T = KS == 0 ? a.noff : KS * KS;
   const int min_chunks = (512 + T * CK - 1) / (T * CK);
   int ksplit = 1;
-  if (VEC && chunks >= 2 * min_chunks && 4 * blocks <= ctx->cus) {
+  const bool idle = 4 * blocks <= ctx->cus || (KS == 1 && T * a.C >= 1536 && blocks < ctx->cus);
+  if (VEC && chunks >= 2 * min_chunks && idle) {
     ksplit = (int)std::min<long>(chunks / min_chunks, (2L * ctx->cus + blocks - 1) / blocks);
     while (ksplit > 1 && (size_t)ksplit * rows * pitch > ctx->splitk_floats) ksplit--;
   }
