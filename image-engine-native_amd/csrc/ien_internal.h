@@ -102,6 +102,14 @@ ien_status swin_reserve(ien_swin *b, int height, int width);
 
 // swin_mlp.hip: map rows += fc2(GELU(fc1(LayerNorm(rows)))) in one pass,
 // for c = 32, 64 and 96 (16-byte aligned rows).
+// window.hip: [class][head][query][key] bias tables of n-token windows in
+// the attention kernels' accumulator layout, [class][head][query block]
+// [key block][4][64 lanes][4] (keys past n -inf); the attention over
+// windows with tables in that layout (packed) or the plain one.
+std::vector<float> pack_bias_tables(const float *tables, int classes, int heads, int n);
+ien_status window_attention(ien_ctx *ctx, const ien_windows *w, const uint16_t *d_qkv, int c,
+                            const float *d_tables, bool packed, uint16_t *d_out);
+
 bool swin_mlp_supported(int c);
 ien_status swin_mlp(ien_ctx *ctx, uint16_t *d_map, size_t stride, long rows, int c,
                     const float *gamma, const float *beta, const ien_matrix *fc1,
@@ -109,11 +117,10 @@ ien_status swin_mlp(ien_ctx *ctx, uint16_t *d_map, size_t stride, long rows, int
 
 // swin_attend.hip: a Swin block's attention half (gather, LayerNorm, qkv,
 // attention, projection, residual) in one pass per window, for window 8
-// and 32, 64 or 128 channels; its projection fragments and bias tables are
-// packed once per block by the two helpers.
+// and 32, 64 or 128 channels; its projection fragments are packed once per
+// block by swin_attend_proj, its bias tables by pack_bias_tables.
 bool swin_attend_supported(int c, int window);
 std::vector<uint16_t> swin_attend_proj(const float *proj_w, int c);
-std::vector<float> swin_attend_tables(const float *tables, int classes, int heads);
 ien_status swin_attend(ien_ctx *ctx, const ien_windows *win, uint16_t *d_map, size_t stride,
                        int c, const float *gamma, const float *beta, const ien_matrix *qkv,
                        const uint16_t *d_proj, const float *bproj, const float *d_tables);

@@ -12,11 +12,10 @@ struct ien_swin {
   ien_ctx *ctx = nullptr;
   int c = 0, window = 0, shift = 0, heads = 0, classes = 0;
   float *d_ln = nullptr;  // ln1 gamma, beta, ln2 gamma, beta (4 c floats)
-  float *d_tables = nullptr;
-  // The fused attention's projection fragments and bias tables (when it
-  // takes the block's width and window).
+  // The bias tables in the attention kernels' layout; the fused attention's
+  // projection fragments (when it takes the block's width and window).
+  float *d_packed = nullptr;
   uint16_t *d_attn_proj = nullptr;
-  float *d_attn_tables = nullptr;
   ien_matrix *qkv = nullptr, *proj = nullptr, *fc1 = nullptr, *fc2 = nullptr;
   // Scratch: `rows` window rows (at least the map's tokens) of 4c, c, c.
   uint16_t *d_wide = nullptr, *d_tok = nullptr, *d_att = nullptr;
@@ -32,9 +31,8 @@ void release(ien_swin *b) {
   ien_matrix_free(b->fc1);
   ien_matrix_free(b->fc2);
   (void)hipFree(b->d_ln);
-  (void)hipFree(b->d_tables);
+  (void)hipFree(b->d_packed);
   (void)hipFree(b->d_attn_proj);
-  (void)hipFree(b->d_attn_tables);
   (void)hipFree(b->d_wide);
   (void)hipFree(b->d_tok);
   (void)hipFree(b->d_att);
@@ -125,25 +123,24 @@ ien_status ien_swin_new(ien_ctx *ctx, const ien_swin_weights *w, ien_swin **out)
   std::vector<float> tables(4 * (size_t)b->heads * n * n);
   b->classes = ien_bias_tables(W.position, b->heads, W.window, W.shift, W.masked, tables.data());
   if (b->classes < 0) return fail_with(IEN_ERR_INPUT);
-  const size_t tbytes = (size_t)b->classes * b->heads * n * n * sizeof(float);
   std::vector<float> ln(4 * c);
   std::memcpy(ln.data(), W.ln1_gamma, c * 4);
   std::memcpy(ln.data() + c, W.ln1_beta, c * 4);
   std::memcpy(ln.data() + 2 * c, W.ln2_gamma, c * 4);
   std::memcpy(ln.data() + 3 * c, W.ln2_beta, c * 4);
   hipError_t e = hipMalloc((void **)&b->d_ln, 4 * c * 4);
-  if (e == hipSuccess) e = hipMalloc((void **)&b->d_tables, tbytes);
   if (e == hipSuccess) e = hipMemcpy(b->d_ln, ln.data(), 4 * c * 4, hipMemcpyHostToDevice);
-  if (e == hipSuccess) e = hipMemcpy(b->d_tables, tables.data(), tbytes, hipMemcpyHostToDevice);
+  if (e == hipSuccess) {
+    const std::vector<float> packed = pack_bias_tables(tables.data(), b->classes, b->heads, (int)n);
+    e = hipMalloc((void **)&b->d_packed, packed.size() * 4);
+    if (e == hipSuccess)
+      e = hipMemcpy(b->d_packed, packed.data(), packed.size() * 4, hipMemcpyHostToDevice);
+  }
   if (e == hipSuccess && swin_attend_supported(W.c, W.window)) {
     const std::vector<uint16_t> proj = swin_attend_proj(W.proj_w, W.c);
-    const std::vector<float> packed = swin_attend_tables(tables.data(), b->classes, b->heads);
     e = hipMalloc((void **)&b->d_attn_proj, proj.size() * 2);
-    if (e == hipSuccess) e = hipMalloc((void **)&b->d_attn_tables, packed.size() * 4);
     if (e == hipSuccess)
       e = hipMemcpy(b->d_attn_proj, proj.data(), proj.size() * 2, hipMemcpyHostToDevice);
-    if (e == hipSuccess)
-      e = hipMemcpy(b->d_attn_tables, packed.data(), packed.size() * 4, hipMemcpyHostToDevice);
   }
   if (e != hipSuccess) {
     release(b);
@@ -178,12 +175,13 @@ ien_status ien_swin_run(ien_swin *b, uint16_t *d_map, size_t stride, int height,
   // attention, projection over the token rows, added back onto the map.
   if (b->d_attn_proj && rows16) {
     st = swin_attend(ctx, &w, d_map, stride, b->c, g1, b1, b->qkv, b->d_attn_proj,
-                     b->proj->d_bias, b->d_attn_tables);
+                     b->proj->d_bias, b->d_packed);
   } else {
     st = ien_window_gather(ctx, &w, d_map, stride, b->c, g1, b1, b->d_tok);
     if (st == IEN_OK)
       st = rows_product(ctx, b->d_tok, c, rows, b->qkv, b->d_wide, 3 * c, IEN_ACT_NONE, 0);
-    if (st == IEN_OK) st = ien_window_attention(ctx, &w, b->d_wide, b->c, b->d_tables, b->d_att);
+    if (st == IEN_OK)
+      st = window_attention(ctx, &w, b->d_wide, b->c, b->d_packed, true, b->d_att);
     if (st == IEN_OK)
       st = rows_product(ctx, b->d_att, c, rows, b->proj, b->d_tok, c, IEN_ACT_NONE, 0);
     if (st == IEN_OK) st = ien_window_scatter_add(ctx, &w, b->d_tok, b->c, d_map, stride);

@@ -47,7 +47,7 @@ struct AttendArgs {
   const float *bqkv;          // 3c
   const uint16_t *wproj;      // Wp^T A fragments [c / 32][heads][2][512]
   const float *bproj;         // c
-  const float *bias;          // [class][head][key block][query block][4][64][4]
+  const float *bias;          // [class][head][query block][key block][4][64][4]
 };
 
 __device__ __forceinline__ half8 frag(const uint16_t *p, int idx, int lane) {
@@ -197,7 +197,7 @@ __device__ __forceinline__ void head_attention(const AttendArgs &a, const half8 
     for (int kb = 0; kb < 2; kb++) {
       st[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[kb][0], qo[qb][0], floatx16{}, 0, 0, 0);
       st[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[kb][1], qo[qb][1], st[kb], 0, 0, 0);
-      const float *tq = tbl + ((kb * 2 + qb) * 4) * 256 + lane * 4;
+      const float *tq = tbl + ((qb * 2 + kb) * 4) * 256 + lane * 4;
 #pragma unroll
       for (int q4 = 0; q4 < 4; q4++) {
         const float4 bt = *(const float4 *)(tq + q4 * 256);
@@ -334,27 +334,6 @@ std::vector<uint16_t> swin_attend_proj(const float *proj_w, int c) {
             out[(((size_t)(cb * heads + h) * 2 + s) * 64 + l) * 8 + i] =
                 f32_to_half(proj_w[(size_t)j * c + o]);
           }
-  return out;
-}
-
-std::vector<float> swin_attend_tables(const float *tables, int classes, int heads) {
-  // [class][head][kb][qb][q4][lane][e] = table[query 32 qb + lane % 32]
-  // [key 32 kb + 8 q4 + 4 (lane / 32) + e] of a 64-token window.
-  const int n = 64;
-  std::vector<float> out((size_t)classes * heads * 4 * 4 * 256);
-  for (int cls = 0; cls < classes; cls++)
-    for (int h = 0; h < heads; h++) {
-      const float *t = tables + (size_t)(cls * heads + h) * n * n;
-      for (int kb = 0; kb < 2; kb++)
-        for (int qb = 0; qb < 2; qb++)
-          for (int q4 = 0; q4 < 4; q4++)
-            for (int l = 0; l < 64; l++)
-              for (int e = 0; e < 4; e++) {
-                const int i = 32 * qb + l % 32, j = 32 * kb + 8 * q4 + 4 * (l / 32) + e;
-                out[(((((size_t)(cls * heads + h) * 2 + kb) * 2 + qb) * 4 + q4) * 64 + l) * 4 + e] =
-                    t[(size_t)i * n + j];
-              }
-    }
   return out;
 }
 

@@ -109,9 +109,12 @@ __global__ __launch_bounds__(256) void k_window_gather(WinGeo g, const uint16_t 
 //    holds keys 32 b + 16 s + 4 h + {0..3, 8..11}, and the A operand (V^T,
 //    staged in LDS as [dim][key]) reads the same keys for its dim.
 //  - Keys past N get -inf; V rows past N are zero in LDS.
+//  - PACKED: the bias tables come in the accumulator layout of
+//    pack_bias_tables (keys past N already -inf), read as 16-byte runs;
+//    otherwise as [class][head][query][key] rows, a strided read per lane.
 // Scores are (q . k) / sqrt(32) + bias, the reference's (q / sqrt(32)) . k
 // up to rounding (attention.rs:66-111).
-template <int NP>
+template <int NP, bool PACKED>
 __global__ __launch_bounds__(NP * 2) void k_window_attention(WinGeo g, const uint16_t *__restrict__ qkv,
                                                              int c, int heads,
                                                              const float *__restrict__ tables,
@@ -155,18 +158,35 @@ __global__ __launch_bounds__(NP * 2) void k_window_attention(WinGeo g, const uin
 
   const float scale = 0.17677669529663688f;  // 1 / sqrt(32)
   const int cls = win_class(g, w);
-  const float *tb = tables + ((long)(cls * heads + head) * n + qc) * n;
   float mx = -__builtin_inff();
+  if constexpr (PACKED) {
+    const float *tp = tables + ((long)(cls * heads + head) * KB + (threadIdx.x >> 6)) * KB * 1024 + lane * 4;
 #pragma unroll
-  for (int b = 0; b < KB; b++)
+    for (int b = 0; b < KB; b++)
 #pragma unroll
-    for (int r = 0; r < 16; r++) {
-      const int j = 32 * b + 8 * (r >> 2) + 4 * hf + (r & 3);
-      const float bj = tb[min(j, n - 1)];  // in bounds for every j
-      const float s = j < n ? st[b][r] * scale + bj : -__builtin_inff();
-      st[b][r] = s;
-      mx = fmaxf(mx, s);
-    }
+      for (int q4 = 0; q4 < 4; q4++) {
+        const float4 bt = *(const float4 *)(tp + (b * 4 + q4) * 256);
+        const float bta[4] = {bt.x, bt.y, bt.z, bt.w};
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          const float s = st[b][4 * q4 + e] * scale + bta[e];
+          st[b][4 * q4 + e] = s;
+          mx = fmaxf(mx, s);
+        }
+      }
+  } else {
+    const float *tb = tables + ((long)(cls * heads + head) * n + qc) * n;
+#pragma unroll
+    for (int b = 0; b < KB; b++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const int j = 32 * b + 8 * (r >> 2) + 4 * hf + (r & 3);
+        const float bj = tb[min(j, n - 1)];  // in bounds for every j
+        const float s = j < n ? st[b][r] * scale + bj : -__builtin_inff();
+        st[b][r] = s;
+        mx = fmaxf(mx, s);
+      }
+  }
   mx = fmaxf(mx, __shfl_xor(mx, 32));
   float sum = 0.0f;
 #pragma unroll
@@ -233,6 +253,71 @@ __global__ __launch_bounds__(256) void k_window_scatter_add(WinGeo g, const uint
 
 
 }  // namespace
+
+namespace {
+
+ien_status launch_attention(ien_ctx *ctx, const WinGeo &g, const uint16_t *d_qkv, int c,
+                            const float *d_tables, bool packed, uint16_t *d_out) {
+  const int heads = c / 32;
+  const long blocks = g.windows * heads;
+  IEN_CHECK(blocks < (1L << 31), IEN_ERR_INPUT, "%ld windows x heads", blocks);
+  const int np = (g.n + 31) / 32 * 32;
+  void (*k)(WinGeo, const uint16_t *, int, int, const float *, uint16_t *) = nullptr;
+#define IEN_ATT(NP)                                                                \
+  k = packed ? k_window_attention<NP, true> : k_window_attention<NP, false>;      \
+  break
+  switch (np) {
+    case 32: IEN_ATT(32);
+    case 64: IEN_ATT(64);
+    case 96: IEN_ATT(96);
+    case 128: IEN_ATT(128);
+    case 160: IEN_ATT(160);
+    case 192: IEN_ATT(192);
+    case 224: IEN_ATT(224);
+    default: IEN_ATT(256);
+  }
+#undef IEN_ATT
+  hipLaunchKernelGGL(k, dim3((unsigned)blocks), dim3(np * 2), 0, ctx->stream, g, d_qkv, c, heads,
+                     d_tables, d_out);
+  IEN_HIP(hipGetLastError());
+  return IEN_OK;
+}
+
+}  // namespace
+
+std::vector<float> pack_bias_tables(const float *tables, int classes, int heads, int n) {
+  // [class][head][query block][key block][q4][lane][e] = table[query
+  // 32 qb + lane % 32][key 32 kb + 8 q4 + 4 (lane / 32) + e]; keys past n
+  // are -inf, queries past n 0.
+  const int kbs = (n + 31) / 32;
+  std::vector<float> out((size_t)classes * heads * kbs * kbs * 1024);
+  for (int cls = 0; cls < classes; cls++)
+    for (int h = 0; h < heads; h++) {
+      const float *t = tables + (size_t)(cls * heads + h) * n * n;
+      for (int qb = 0; qb < kbs; qb++)
+        for (int kb = 0; kb < kbs; kb++)
+          for (int q4 = 0; q4 < 4; q4++)
+            for (int l = 0; l < 64; l++)
+              for (int e = 0; e < 4; e++) {
+                const int i = 32 * qb + l % 32, j = 32 * kb + 8 * q4 + 4 * (l / 32) + e;
+                const float v = j >= n ? -__builtin_inff() : i >= n ? 0.0f : t[(size_t)i * n + j];
+                out[((((size_t)(cls * heads + h) * kbs + qb) * kbs + kb) * 4 + q4) * 256 + l * 4 + e] = v;
+              }
+    }
+  return out;
+}
+
+ien_status window_attention(ien_ctx *ctx, const ien_windows *w, const uint16_t *d_qkv, int c,
+                            const float *d_tables, bool packed, uint16_t *d_out) {
+  IEN_CHECK(ctx && d_qkv && d_tables && d_out, IEN_ERR_INPUT, "null argument");
+  WinGeo g;
+  ien_status st = geometry(w, &g);
+  if (st != IEN_OK) return st;
+  IEN_CHECK(c >= 32 && c % 32 == 0, IEN_ERR_INPUT, "%d channels (heads of 32)", c);
+  IEN_CHECK(aligned16(d_qkv) && ((uintptr_t)d_out & 7) == 0, IEN_ERR_INPUT, "alignment");
+  return launch_attention(ctx, g, d_qkv, c, d_tables, packed, d_out);
+}
+
 }  // namespace ien
 
 using namespace ien;
@@ -333,31 +418,7 @@ ien_status ien_window_gather(ien_ctx *ctx, const ien_windows *w, const uint16_t 
 
 ien_status ien_window_attention(ien_ctx *ctx, const ien_windows *w, const uint16_t *d_qkv, int c,
                                 const float *d_tables, uint16_t *d_out) {
-  IEN_CHECK(ctx && d_qkv && d_tables && d_out, IEN_ERR_INPUT, "null argument");
-  WinGeo g;
-  ien_status st = geometry(w, &g);
-  if (st != IEN_OK) return st;
-  IEN_CHECK(c >= 32 && c % 32 == 0, IEN_ERR_INPUT, "%d channels (heads of 32)", c);
-  IEN_CHECK(aligned16(d_qkv) && ((uintptr_t)d_out & 7) == 0, IEN_ERR_INPUT, "alignment");
-  const int heads = c / 32;
-  const long blocks = g.windows * heads;
-  IEN_CHECK(blocks < (1L << 31), IEN_ERR_INPUT, "%ld windows x heads", blocks);
-  const int np = (g.n + 31) / 32 * 32;
-  void (*k)(WinGeo, const uint16_t *, int, int, const float *, uint16_t *) = nullptr;
-  switch (np) {
-    case 32: k = k_window_attention<32>; break;
-    case 64: k = k_window_attention<64>; break;
-    case 96: k = k_window_attention<96>; break;
-    case 128: k = k_window_attention<128>; break;
-    case 160: k = k_window_attention<160>; break;
-    case 192: k = k_window_attention<192>; break;
-    case 224: k = k_window_attention<224>; break;
-    default: k = k_window_attention<256>; break;
-  }
-  hipLaunchKernelGGL(k, dim3((unsigned)blocks), dim3(np * 2), 0, ctx->stream, g, d_qkv, c, heads,
-                     d_tables, d_out);
-  IEN_HIP(hipGetLastError());
-  return IEN_OK;
+  return window_attention(ctx, w, d_qkv, c, d_tables, false, d_out);
 }
 
 ien_status ien_window_scatter_add(ien_ctx *ctx, const ien_windows *w, const uint16_t *d_rows,
