@@ -747,6 +747,7 @@ ien_status launch_conv(ien_ctx *ctx, const ConvCall &c) {
     a.W = a.OW = 32;
     a.M = a.p_end;
     a.H = a.OH = (a.M + 31) / 32;
+    if (vec && rows_supported(a, c.rows)) return launch_rows(ctx, a);
     if (vec) IEN_CK(1, 1, 4, 32, false);
     IEN_CHECK(c.C <= 64, IEN_ERR_INPUT, "rows of %d values (not a multiple of 16, over 64)", c.C);
     return run_cfg<1, 1, 4, 32, 4, 2, 64, false, false>(ctx, a);
@@ -786,6 +787,7 @@ ien_status launch_conv(ien_ctx *ctx, const ConvCall &c) {
   }
   if (c.ks == 1 && c.stride == 1) {
     IEN_CHECK(vec, IEN_ERR_INPUT, "1x1 products over %d channels", c.C);
+    if (!nchw && !c.pad_reflect && rows_supported(a, c.rows)) return launch_rows(ctx, a);
     if (nchw) IEN_CK(1, 1, 4, 32, true);
     IEN_CK(1, 1, 4, 32, false);
   }

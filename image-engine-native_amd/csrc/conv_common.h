@@ -153,6 +153,12 @@ __device__ __forceinline__ void dma16(const void *src, void *lds) {
   __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)lds, 16, 0, 0);
 }
 
+// rows.hip: products over rows (1 x 1, NHWC f16 in and out) with K a
+// multiple of 32, N of 8, 16-byte aligned rows and enough tiles to fill
+// the chip.
+bool rows_supported(const ConvArgs &a, long rows);
+ien_status launch_rows(ien_ctx *ctx, const ConvArgs &a);
+
 // conv_res.hip: the resident-weight kernel for NHWC inputs of 16, 32 or 64
 // channels with k x k (k = 1, 3) zero-padded taps and K = k k C <= 640.
 bool resident_supported(int ks, int stride, int c, int nchw, int reflect, int noff, int rows_mode,

@@ -1,0 +1,285 @@
+// rows.hip -- products over rows of pixels (1 x 1 convolutions and
+// Input::Rows, gemm.rs:272-283) on gfx950: out[r] = act(x[r] W + bias
+// (+ old out[r] when accumulating)), x f16 rows `xs` halves apart, W packed
+// as MFMA B fragments (ien_matrix), f16 rows out.
+//
+// A workgroup of 4 waves computes a 128-row x BN-column tile (BN = 128:
+// each wave 64 x 64, 2 x 2 blocks of v_mfma_f32_32x32x16_f16; BN = 64: each
+// wave 32 x 64).  K runs in chunks of KC channels through a 3-stage LDS
+// ring: every wave issues its share of the chunk's direct-to-LDS buffer
+// loads (16 bytes a lane, 1 KiB a wave instruction) two chunks ahead, so
+// one barrier per chunk suffices and the loads of two chunks are always in
+// flight.  The loads are inline assembly the compiler does not see (its
+// own waits after such loads would flush the whole counter); loads
+// complete in order, so waiting until LPC are outstanding means all but
+// the next chunk's have landed.  The buffer range check returns zeros for
+// rows past the end.
+//  - x rows are staged [row][16-byte slot] with the slots XOR-swizzled by
+//    row, so the 32 rows of an A-fragment read fall on distinct banks; the
+//    swizzle is applied to the source address, since a wave's loads fill a
+//    contiguous KiB.
+//  - W fragments are copied as packed (1 KiB per fragment, lane order).
+//  - Epilogue: acc + bias staged as f32 in LDS, 64 rows at a time, then
+//    per 16-byte item (8 channels of a row) the old output (loaded first,
+//    all at once) and the activation, one loop per activation: the order of
+//    gemm.rs:583-666.
+// Chunks of 32 channels keep the ring at 48 KiB (BN = 128), so several
+// workgroups share a CU and hide each other's latency.
+// Tiles are dealt XCD-aware with N fastest, so a tile row's x stays in its
+// XCD's L2 for every column tile.
+
+#include "conv_common.h"
+
+#pragma clang diagnostic ignored "-Winline-asm"  // m0 is written by the loads below
+
+namespace ien {
+namespace {
+
+typedef int int4v __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ int4v rows_rsrc(const void *p, long bytes) {
+  const unsigned long long a = (unsigned long long)p;
+  int4v r;
+  r.x = (int)(unsigned)a;
+  r.y = (int)((a >> 32) & 0xffff);
+  r.z = (int)bytes;
+  r.w = 0x00020000;
+  return r;
+}
+
+__device__ __forceinline__ unsigned rows_lds(const void *p) {
+  return (unsigned)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+}
+
+__device__ __forceinline__ void rows_dma(int4v r, unsigned wave_base, int off) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               :: "s"(wave_base), "v"(off), "s"(r) : "memory", "m0");
+}
+
+template <int N>
+__device__ __forceinline__ void rows_wait() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt(0x0f70 | (N & 15) | ((N >> 4) << 14));
+}
+
+struct RowsArgs {
+  const uint16_t *x;  // row 0 of the range
+  int xs;             // halves between rows
+  int M, K;           // rows, reduction depth (a multiple of KC)
+  const uint16_t *wp;
+  int KB, NB, N;      // packed 16-deep and 32-wide blocks, columns
+  const float *bias, *slope;
+  uint16_t *y;        // output row 0
+  int ys;
+  int act, accumulate;
+  int tiles_n, tiles;
+};
+
+template <int BN, int KC>
+struct RowsCfg {
+  static constexpr int BM = 128;
+  static constexpr int SLOTS = KC / 8;                   // 16-byte slots per staged row
+  static constexpr int A_BYTES = BM * KC * 2;
+  static constexpr int B_BYTES = BN * KC * 2;
+  static constexpr int STAGE = A_BYTES + B_BYTES;
+  static constexpr int STAGES = 3;
+  static constexpr int A_LOADS = A_BYTES / 1024 / 4;     // per wave and chunk
+  static constexpr int B_LOADS = B_BYTES / 1024 / 4;
+  static constexpr int LPC = A_LOADS + B_LOADS;
+  static constexpr int SP = BN + 4;                      // staged f32 row pitch
+  static constexpr int LDS = STAGES * STAGE > 64 * SP * 4 ? STAGES * STAGE : 64 * SP * 4;
+  static constexpr int WM = BN == 128 ? 2 : 1;           // 32-row blocks per wave
+  static constexpr int ITEMS = BM * BN / 8 / 256;        // 16-byte output items per thread
+  static_assert(A_LOADS * 4 * 1024 == A_BYTES && B_LOADS * 4 * 1024 == B_BYTES, "load split");
+};
+
+// Slot of 16-byte chunk g of staged row r.
+template <int SLOTS>
+__device__ __forceinline__ int swz(int r, int g) {
+  return g ^ ((SLOTS == 8 ? r : r >> 1) & (SLOTS - 1));
+}
+
+template <int BN, int KC>
+__global__ __launch_bounds__(256) void k_rows(RowsArgs a) {
+  using R = RowsCfg<BN, KC>;
+  __shared__ __attribute__((aligned(1024))) unsigned char lds[R::LDS];
+  const int tid = threadIdx.x, lane = tid & 63, hf = lane >> 5, l32 = lane & 31;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int t = xcd_remap(blockIdx.x, gridDim.x);
+  const int tm = t / a.tiles_n, tn = t - tm * a.tiles_n;
+  const int m0 = tm * R::BM;
+  const unsigned l0 = rows_lds(lds);
+  const int4v xr = rows_rsrc(a.x, (long)a.M * a.xs * 2);
+  const int4v wr = rows_rsrc(a.wp, (long)a.NB * a.KB * 1024);
+  const int chunks = a.K / KC;
+
+  // Chunk c into stage s: A rows m0 .. m0 + 127, channels c KC .. + KC - 1;
+  // B fragments of column blocks tn BN / 32 .. and k blocks c KC / 16 ...
+  auto issue = [&](int c, int s) {
+    const unsigned base = l0 + s * R::STAGE;
+#pragma unroll
+    for (int i = 0; i < R::A_LOADS; i++) {
+      const int d = wave + 4 * i;                 // KiB of the A stage
+      const int row = d * (1024 / (KC * 2)) + lane / R::SLOTS;
+      const int slot = lane % R::SLOTS;
+      const int g = swz<R::SLOTS>(row, slot);      // the chunk this slot holds
+      rows_dma(xr, __builtin_amdgcn_readfirstlane(base + d * 1024),
+               ((m0 + row) * a.xs + c * KC + 8 * g) * 2);
+    }
+#pragma unroll
+    for (int i = 0; i < R::B_LOADS; i++) {
+      const int f = wave + 4 * i;                 // fragment (j, q) of the chunk
+      const int j = f / (KC / 16), q = f % (KC / 16);
+      const int nb = tn * (BN / 32) + j, kb = c * (KC / 16) + q;
+      rows_dma(wr, __builtin_amdgcn_readfirstlane(base + R::A_BYTES + f * 1024),
+               (nb * a.KB + kb) * 1024 + lane * 16);
+    }
+  };
+
+  const int wm = BN == 128 ? (wave & 1) : wave;   // 64-row (BN 128) or 32-row block
+  const int wn = BN == 128 ? (wave >> 1) : 0;     // 64-column block
+  floatx16 acc[R::WM][2];
+#pragma unroll
+  for (int i = 0; i < R::WM; i++)
+#pragma unroll
+    for (int j = 0; j < 2; j++) acc[i][j] = floatx16{};
+
+  issue(0, 0);
+  if (chunks > 1) issue(1, 1);
+  for (int c = 0; c < chunks; c++) {
+    if (c + 1 < chunks)
+      rows_wait<R::LPC>();  // all but chunk c + 1's loads
+    else
+      rows_wait<0>();
+    __syncthreads();  // chunk c visible; every wave is done with chunk c - 1
+    if (c + 2 < chunks) issue(c + 2, (c + 2) % 3);
+    const unsigned char *sa = lds + (c % 3) * R::STAGE;
+    const unsigned char *sb = sa + R::A_BYTES;
+#pragma unroll
+    for (int q = 0; q < KC / 16; q++) {
+      half8 af[R::WM], bf[2];
+#pragma unroll
+      for (int i = 0; i < R::WM; i++) {
+        const int row = (wm * R::WM + i) * 32 + l32;
+        af[i] = *(const half8 *)(sa + row * KC * 2 + swz<R::SLOTS>(row, 2 * q + hf) * 16);
+      }
+#pragma unroll
+      for (int j = 0; j < 2; j++)
+        bf[j] = *(const half8 *)(sb + ((wn * 2 + j) * (KC / 16) + q) * 1024 + lane * 16);
+#pragma unroll
+      for (int i = 0; i < R::WM; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+    }
+  }
+  __syncthreads();  // every wave is done with the stages
+
+  // 16-byte items: row v / (BN / 8), channels 8 (v % (BN / 8)) ..., items
+  // e < ITEMS / 2 in rows 0..63.  The old outputs are loaded first, so their
+  // latency overlaps the staging.
+  u32x4 old[R::ITEMS];
+  if (a.accumulate) {
+#pragma unroll
+    for (int e = 0; e < R::ITEMS; e++) {
+      const int v = tid + 256 * e, row = v / (BN / 8), col = tn * BN + 8 * (v % (BN / 8));
+      const bool ok = m0 + row < a.M && col < a.N;
+      old[e] = *(const u32x4 *)(a.y + (ok ? (long)(m0 + row) * a.ys + col : 0));
+    }
+  }
+  float *st = (float *)lds;
+  auto store = [&](auto actf, int half) {
+#pragma unroll
+    for (int e = half * R::ITEMS / 2; e < (half + 1) * R::ITEMS / 2; e++) {
+      const int v = tid + 256 * e, row = v / (BN / 8), c8 = 8 * (v % (BN / 8));
+      const int col = tn * BN + c8;
+      if (m0 + row >= a.M || col >= a.N) continue;
+      const float *sr = st + (row - 64 * half) * R::SP + c8;
+      const float4v s0 = *(const float4v *)sr, s1 = *(const float4v *)(sr + 4);
+      float v8[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
+      if (a.accumulate) {
+        uint16_t h[8];
+        __builtin_memcpy(h, &old[e], 16);
+#pragma unroll
+        for (int k = 0; k < 8; k++) v8[k] += h2f(h[k]);
+      }
+      uint16_t o[8];
+#pragma unroll
+      for (int k = 0; k < 8; k++) o[k] = f2h(actf(v8[k], col + k));
+      __builtin_memcpy(a.y + (long)(m0 + row) * a.ys + col, o, 16);
+    }
+  };
+  // acc + bias as f32 rows in LDS, 64 rows at a time.
+  const int owner = BN == 128 ? wm : wm >> 1;  // the 64-row half this wave computed
+#pragma unroll
+  for (int half = 0; half < 2; half++) {
+    if (half) __syncthreads();  // the first half is read
+    if (owner == half) {
+#pragma unroll
+      for (int j = 0; j < 2; j++) {
+        const int col = (wn * 2 + j) * 32 + l32;
+        const float b = a.bias[tn * BN + col];  // padded to whole 32-column blocks
+#pragma unroll
+        for (int i = 0; i < R::WM; i++)
+#pragma unroll
+          for (int r = 0; r < 16; r++)
+            st[((wm * R::WM + i) * 32 - 64 * half + 8 * (r >> 2) + 4 * hf + (r & 3)) * R::SP + col] =
+                acc[i][j][r] + b;
+      }
+    }
+    __syncthreads();
+    switch (a.act) {
+      case IEN_ACT_RELU: store([&](float v, int) { return act_c<IEN_ACT_RELU>(v, 0.0f); }, half); break;
+      case IEN_ACT_GELU: store([&](float v, int) { return act_c<IEN_ACT_GELU>(v, 0.0f); }, half); break;
+      case IEN_ACT_SIGMOID:
+        store([&](float v, int) { return act_c<IEN_ACT_SIGMOID>(v, 0.0f); }, half);
+        break;
+      case IEN_ACT_PRELU:
+        store([&](float v, int col) { return act_c<IEN_ACT_PRELU>(v, a.slope[col]); }, half);
+        break;
+      default: store([&](float v, int) { return v; }, half); break;
+    }
+  }
+}
+
+template <int BN, int KC>
+ien_status launch(ien_ctx *ctx, RowsArgs a) {
+  a.tiles_n = (a.N + BN - 1) / BN;
+  a.tiles = (a.M + 127) / 128 * a.tiles_n;
+  hipLaunchKernelGGL((k_rows<BN, KC>), dim3((unsigned)a.tiles), dim3(256), 0, ctx->stream, a);
+  IEN_HIP(hipGetLastError());
+  return IEN_OK;
+}
+
+}  // namespace
+
+bool rows_supported(const ConvArgs &a, long rows) {
+  const bool aligned = (((uintptr_t)a.x) & 15) == 0 && (((uintptr_t)a.y) & 15) == 0;
+  const long tiles = (rows + 127) / 128 * ((a.N + 127) / 128);
+  return aligned && !a.out_f32 && !a.out_nchw && a.C % 32 == 0 && a.N % 8 == 0 && a.xs % 8 == 0 &&
+         a.ys % 8 == 0 && (long)a.xs * (rows + 128) * 2 <= 0x7fff0000L &&
+         (long)a.NB * a.KB * 1024 <= 0x7fff0000L && tiles >= 128;
+}
+
+// Rows p_begin .. p_end of x (row stride xs) times the packed weights into
+// rows 0 .. of y; a.C is the reduction depth.
+ien_status launch_rows(ien_ctx *ctx, const ConvArgs &c) {
+  RowsArgs a{};
+  a.x = c.x + (long)c.p_begin * c.xs;
+  a.xs = c.xs;
+  a.M = c.p_end - c.p_begin;
+  a.K = c.C;
+  a.wp = c.wp;
+  a.KB = c.KB;
+  a.NB = c.NB;
+  a.N = c.N;
+  a.bias = c.bias;
+  a.slope = c.slope;
+  a.y = (uint16_t *)c.y;
+  a.ys = c.ys;
+  a.act = c.act;
+  a.accumulate = c.accumulate;
+  return c.N > 64 ? launch<128, 32>(ctx, a) : launch<64, 32>(ctx, a);
+}
+
+}  // namespace ien

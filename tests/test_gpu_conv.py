@@ -203,6 +203,48 @@ def test_rows(ctx, oracle, m, k, n):
     close(out.float().cpu().numpy(), want)
 
 
+# Row products with enough 128-row tiles for the pipelined row kernel: both
+# tile widths (N > 64 and <= 64), K a multiple of 64 or only of 32, ragged
+# last tiles in M and N, accumulation, activations, padded strides and a
+# row range that starts past row 0.
+@pytest.mark.parametrize("m,k,n,act,acc,row0,pad", [
+    (16500, 256, 128, 2, False, 0, 8), (33000, 64, 64, 0, True, 0, 0),
+    (20000, 96, 96, 3, True, 0, 8), (17000, 160, 40, 1, False, 0, 0),
+    (17000, 128, 256, 0, True, 1000, 8)])
+def test_rows_tiles(ctx, oracle, m, k, n, act, acc, row0, pad):
+    import torch
+    import ien
+
+    rng = np.random.default_rng(m + k + n)
+    total = row0 + m
+    a = f16(rng.standard_normal((total, k)))
+    wt = f16(rng.standard_normal((k, n)) / np.sqrt(k))
+    b = rng.standard_normal(n).astype(np.float32) * 0.1
+    slope = np.linspace(0.05, 0.5, n).astype(np.float32)
+    init = f16(rng.standard_normal((m, n))) if acc else None
+    oact = {0: oracle.ACT_NONE, 1: oracle.ACT_RELU, 2: oracle.ACT_GELU, 3: oracle.ACT_NONE}[act]
+    want = oracle.multiply_rows(a[row0:], wt, b, act=oact, out=None if init is None else init.copy(),
+                                accumulate=acc, threads=8)
+    if act == 3:
+        want = np.where(want < 0, want * slope[None, :], want)
+    xs, ys = k + pad, n + pad
+    ap = np.zeros((total, xs), np.float32)
+    ap[:, :k] = a
+    at = torch.from_numpy(ap).half().cuda()
+    mat = ien.Matrix(ctx, wt, b)
+    out = torch.zeros((m, ys), dtype=torch.float16, device="cuda")
+    if acc:
+        out[:, :n].copy_(torch.from_numpy(init))
+    sl = torch.from_numpy(slope).cuda()
+    ien.multiply_ex(ctx, ien.rows_input(at, xs), row0, m, mat, out, ys, act=act, slope=sl if act == 3 else None,
+                    accumulate=acc)
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy()
+    mat.free()
+    assert np.all(got[:, n:] == 0)  # padding columns untouched
+    close(got[:, :n], want)
+
+
 # Split-K: few output tiles and several channel chunks, so the reduction is
 # spread over workgroups, summed by the finishing pass, then bias,
 # accumulate and activation.
