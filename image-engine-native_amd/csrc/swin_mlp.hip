@@ -68,11 +68,14 @@ __global__ __launch_bounds__(256) void k_swin_mlp(MlpArgs a) {
   const long row0 = (long)blockIdx.x * MLP_ROWS;
   const long last = a.rows - 1;
 
-  // LayerNorm: L lanes per row, one 8-channel chunk per lane.
+  // LayerNorm: L lanes per row, one 8-channel chunk per lane.  When every
+  // lane holds a chunk (L = c / 8), thread tid's chunk of pass p is its
+  // output item p, so the rows stay in registers for the residual.
+  constexpr bool KEEP = S::L == C / 8;
+  u32x4 raw[S::PASSES];
   {
     const int sub = tid & (S::L - 1), chunks = C / 8;
     const int k = sub < chunks ? sub : chunks - 1;
-    u32x4 raw[S::PASSES];
 #pragma unroll
     for (int p = 0; p < S::PASSES; p++) {
       const long r = min(row0 + p * (256 / S::L) + tid / S::L, last);
@@ -188,7 +191,10 @@ __global__ __launch_bounds__(256) void k_swin_mlp(MlpArgs a) {
 #pragma unroll
   for (int i = 0; i < ITEMS; i++) {
     const int item = tid + 256 * i, r = item / (C / 8), k = item % (C / 8);
-    old[i] = *(const u32x4 *)(a.map + min(row0 + r, last) * a.stride + 8 * k);
+    if constexpr (KEEP)
+      old[i] = raw[i];
+    else
+      old[i] = *(const u32x4 *)(a.map + min(row0 + r, last) * a.stride + 8 * k);
   }
 #pragma unroll
   for (int i = 0; i < ITEMS; i++) {
