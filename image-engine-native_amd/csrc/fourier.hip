@@ -259,18 +259,23 @@ __global__ __launch_bounds__(THREADS) void k_line_mfma(LinePass p) {
 #pragma unroll
     for (int r = 0; r < 16; r++) acc[r] = acc2[r] = 0.0f;
     const float *a = p.at + mb * 32 + cc;
-    // 32 k at a time: the 16 table loads of a lane are issued together, so
-    // one memory latency covers 16 MFMAs.  Lane halves take k of either
-    // parity; KP is even, so a step is valid for both or neither.
+    // 32 k at a time: the 16 table loads of a lane are issued together, and
+    // those of the next 32 k before this batch's MFMAs, so their latency
+    // overlaps the products.  Lane halves take k of either parity; KP is
+    // even, so a step is valid for both or neither.
+    // A[m = 32 mb + lane % 32][k]; steps past KP are never used (clamped to
+    // a valid row so the load needs no branch).
+    auto table = [&](int k0, float *av) {
+#pragma unroll
+      for (int i = 0; i < 16; i++) av[i] = a[(long)min(k0 + 2 * i + (lane >> 5), p.KP - 1) * p.MP];
+    };
+    float nx[16];
+    table(0, nx);
     for (int k0 = 0; k0 < p.KP; k0 += 32) {
       float av[16];
 #pragma unroll
-      for (int i = 0; i < 16; i++) {
-        // A[m = 32 mb + lane % 32][k]; steps past KP are never used (clamped
-        // to a valid row so the load needs no branch).
-        const int k = min(k0 + 2 * i + (lane >> 5), p.KP - 1);
-        av[i] = a[(long)k * p.MP];
-      }
+      for (int i = 0; i < 16; i++) av[i] = nx[i];
+      if (k0 + 32 < p.KP) table(k0 + 32, nx);
 #pragma unroll
       for (int i = 0; i < 16; i += 2) {
         if (k0 + 2 * i >= p.KP) break;
@@ -283,19 +288,28 @@ __global__ __launch_bounds__(THREADS) void k_line_mfma(LinePass p) {
 #pragma unroll
     for (int r = 0; r < 16; r++) acc[r] += acc2[r];
     if (c0 + cc >= p.C) continue;
+    auto out_at = [&](int r) {
+      const int m = min(mb * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3), p.M - 1);
+      const int part = m >= p.M1;  // m < 2 M1
+      return ln * p.out_line + (m - part * p.M1) * p.out_k + part * p.out_part + c0 + cc;
+    };
+    // When adding, the 16 old values are loaded together first (from
+    // clamped, valid positions), so one latency covers them.
+    float old[16];
+#pragma unroll
+    for (int r = 0; r < 16; r++)
+      old[r] = !ADD ? 0.0f
+               : OUT_F16 ? h2f(((const uint16_t *)p.out)[out_at(r)])
+                         : ((const float *)p.out)[out_at(r)];
 #pragma unroll
     for (int r = 0; r < 16; r++) {
       const int m = mb * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
       if (m >= p.M) continue;
-      const int part = m >= p.M1;  // m < 2 M1
-      const long at = ln * p.out_line + (m - part * p.M1) * p.out_k + part * p.out_part + c0 + cc;
-      if (OUT_F16) {
-        uint16_t *o = (uint16_t *)p.out + at;
-        *o = f2h(ADD ? h2f(*o) + acc[r] : acc[r]);
-      } else {
-        float *o = (float *)p.out + at;
-        *o = ADD ? *o + acc[r] : acc[r];
-      }
+      const long at = out_at(r);
+      if (OUT_F16)
+        ((uint16_t *)p.out)[at] = f2h(ADD ? old[r] + acc[r] : acc[r]);
+      else
+        ((float *)p.out)[at] = ADD ? old[r] + acc[r] : acc[r];
     }
   }
 }
