@@ -75,9 +75,9 @@ struct RowsArgs {
   int tiles_n, tiles;
 };
 
-template <int BN, int KC>
+template <int BM_, int BN, int KC>
 struct RowsCfg {
-  static constexpr int BM = 128;
+  static constexpr int BM = BM_;
   static constexpr int SLOTS = KC / 8;                   // 16-byte slots per staged row
   static constexpr int A_BYTES = BM * KC * 2;
   static constexpr int B_BYTES = BN * KC * 2;
@@ -88,7 +88,8 @@ struct RowsCfg {
   static constexpr int LPC = A_LOADS + B_LOADS;
   static constexpr int SP = BN + 4;                      // staged f32 row pitch
   static constexpr int LDS = STAGES * STAGE > 64 * SP * 4 ? STAGES * STAGE : 64 * SP * 4;
-  static constexpr int WM = BN == 128 ? 2 : 1;           // 32-row blocks per wave
+  static constexpr int WM = BN == 128 ? BM / 64 : 1;      // 32-row blocks per wave
+  static constexpr int HALVES = BM / 64;                 // 64-row staging passes
   static constexpr int ITEMS = BM * BN / 8 / 256;        // 16-byte output items per thread
   static_assert(A_LOADS * 4 * 1024 == A_BYTES && B_LOADS * 4 * 1024 == B_BYTES, "load split");
 };
@@ -99,9 +100,10 @@ __device__ __forceinline__ int swz(int r, int g) {
   return g ^ ((SLOTS == 8 ? r : r >> 1) & (SLOTS - 1));
 }
 
-template <int BN, int KC>
+template <int BM, int BN, int KC>
 __global__ __launch_bounds__(256) void k_rows(RowsArgs a) {
-  using R = RowsCfg<BN, KC>;
+  using R = RowsCfg<BM, BN, KC>;
+  static_assert(BM == 128 || BN == 128, "64-row tiles are 128 columns wide");
   __shared__ __attribute__((aligned(1024))) unsigned char lds[R::LDS];
   const int tid = threadIdx.x, lane = tid & 63, hf = lane >> 5, l32 = lane & 31;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -113,7 +115,7 @@ __global__ __launch_bounds__(256) void k_rows(RowsArgs a) {
   const int4v wr = rows_rsrc(a.wp, (long)a.NB * a.KB * 1024);
   const int chunks = a.K / KC;
 
-  // Chunk c into stage s: A rows m0 .. m0 + 127, channels c KC .. + KC - 1;
+  // Chunk c into stage s: A rows m0 .. m0 + BM - 1, channels c KC .. + KC - 1;
   // B fragments of column blocks tn BN / 32 .. and k blocks c KC / 16 ...
   auto issue = [&](int c, int s) {
     const unsigned base = l0 + s * R::STAGE;
@@ -136,7 +138,7 @@ __global__ __launch_bounds__(256) void k_rows(RowsArgs a) {
     }
   };
 
-  const int wm = BN == 128 ? (wave & 1) : wave;   // 64-row (BN 128) or 32-row block
+  const int wm = BN == 128 ? (wave & 1) : wave;   // block of WM 32-row blocks
   const int wn = BN == 128 ? (wave >> 1) : 0;     // 64-column block
   floatx16 acc[R::WM][2];
 #pragma unroll
@@ -176,8 +178,8 @@ __global__ __launch_bounds__(256) void k_rows(RowsArgs a) {
   __syncthreads();  // every wave is done with the stages
 
   // 16-byte items: row v / (BN / 8), channels 8 (v % (BN / 8)) ..., items
-  // e < ITEMS / 2 in rows 0..63.  The old outputs are loaded first, so their
-  // latency overlaps the staging.
+  // of staging pass h in rows 64 h .. 64 h + 63.  The old outputs are loaded
+  // first, so their latency overlaps the staging.
   u32x4 old[R::ITEMS];
   if (a.accumulate) {
 #pragma unroll
@@ -190,7 +192,7 @@ __global__ __launch_bounds__(256) void k_rows(RowsArgs a) {
   float *st = (float *)lds;
   auto store = [&](auto actf, int half) {
 #pragma unroll
-    for (int e = half * R::ITEMS / 2; e < (half + 1) * R::ITEMS / 2; e++) {
+    for (int e = half * R::ITEMS / R::HALVES; e < (half + 1) * R::ITEMS / R::HALVES; e++) {
       const int v = tid + 256 * e, row = v / (BN / 8), c8 = 8 * (v % (BN / 8));
       const int col = tn * BN + c8;
       if (m0 + row >= a.M || col >= a.N) continue;
@@ -210,9 +212,9 @@ __global__ __launch_bounds__(256) void k_rows(RowsArgs a) {
     }
   };
   // acc + bias as f32 rows in LDS, 64 rows at a time.
-  const int owner = BN == 128 ? wm : wm >> 1;  // the 64-row half this wave computed
+  const int owner = BM == 64 ? 0 : BN == 128 ? wm : wm >> 1;  // the 64 rows this wave computed
 #pragma unroll
-  for (int half = 0; half < 2; half++) {
+  for (int half = 0; half < R::HALVES; half++) {
     if (half) __syncthreads();  // the first half is read
     if (owner == half) {
 #pragma unroll
@@ -242,23 +244,27 @@ __global__ __launch_bounds__(256) void k_rows(RowsArgs a) {
   }
 }
 
-template <int BN, int KC>
+template <int BM, int BN, int KC>
 ien_status launch(ien_ctx *ctx, RowsArgs a) {
   a.tiles_n = (a.N + BN - 1) / BN;
-  a.tiles = (a.M + 127) / 128 * a.tiles_n;
-  hipLaunchKernelGGL((k_rows<BN, KC>), dim3((unsigned)a.tiles), dim3(256), 0, ctx->stream, a);
+  a.tiles = (a.M + BM - 1) / BM * a.tiles_n;
+  hipLaunchKernelGGL((k_rows<BM, BN, KC>), dim3((unsigned)a.tiles), dim3(256), 0, ctx->stream, a);
   IEN_HIP(hipGetLastError());
   return IEN_OK;
 }
 
 }  // namespace
 
+// Tiles of 128 rows when they number at least 128, else 64-row tiles when
+// those number at least 96; below that the general kernel's split-K serves.
+static long tiles_of(long rows, int bm, int n) { return (rows + bm - 1) / bm * ((n + 127) / 128); }
+
 bool rows_supported(const ConvArgs &a, long rows) {
   const bool aligned = (((uintptr_t)a.x) & 15) == 0 && (((uintptr_t)a.y) & 15) == 0;
-  const long tiles = (rows + 127) / 128 * ((a.N + 127) / 128);
+  const bool enough = tiles_of(rows, 128, a.N) >= 128 || tiles_of(rows, 64, a.N) >= 96;
   return aligned && !a.out_f32 && !a.out_nchw && a.C % 32 == 0 && a.N % 8 == 0 && a.xs % 8 == 0 &&
          a.ys % 8 == 0 && (long)a.xs * (rows + 128) * 2 <= 0x7fff0000L &&
-         (long)a.NB * a.KB * 1024 <= 0x7fff0000L && tiles >= 128;
+         (long)a.NB * a.KB * 1024 <= 0x7fff0000L && enough;
 }
 
 // Rows p_begin .. p_end of x (row stride xs) times the packed weights into
@@ -279,7 +285,8 @@ ien_status launch_rows(ien_ctx *ctx, const ConvArgs &c) {
   a.ys = c.ys;
   a.act = c.act;
   a.accumulate = c.accumulate;
-  return c.N > 64 ? launch<128, 32>(ctx, a) : launch<64, 32>(ctx, a);
+  if (tiles_of(a.M, 128, a.N) < 128) return launch<64, 128, 32>(ctx, a);
+  return c.N > 64 ? launch<128, 128, 32>(ctx, a) : launch<128, 64, 32>(ctx, a);
 }
 
 }  // namespace ien

@@ -203,14 +203,16 @@ def test_rows(ctx, oracle, m, k, n):
     close(out.float().cpu().numpy(), want)
 
 
-# Row products with enough 128-row tiles for the pipelined row kernel: both
-# tile widths (N > 64 and <= 64), K a multiple of 64 or only of 32, ragged
-# last tiles in M and N, accumulation, activations, padded strides and a
-# row range that starts past row 0.
+# Row products with enough tiles for the pipelined row kernel: 128-row tiles
+# of both widths (N > 64 and <= 64) and 64-row tiles (the last three cases),
+# K a multiple of 64 or only of 32, ragged last tiles in M and N,
+# accumulation, activations, padded strides and row ranges that start past
+# row 0.
 @pytest.mark.parametrize("m,k,n,act,acc,row0,pad", [
     (16500, 256, 128, 2, False, 0, 8), (33000, 64, 64, 0, True, 0, 0),
     (20000, 96, 96, 3, True, 0, 8), (17000, 160, 40, 1, False, 0, 0),
-    (17000, 128, 256, 0, True, 1000, 8)])
+    (17000, 128, 256, 0, True, 1000, 8),
+    (4096, 384, 192, 1, False, 0, 0), (4096, 192, 384, 1, True, 0, 8), (6100, 96, 256, 2, False, 37, 0)])
 def test_rows_tiles(ctx, oracle, m, k, n, act, acc, row0, pad):
     import torch
     import ien
