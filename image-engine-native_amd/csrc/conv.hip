@@ -622,6 +622,64 @@ __global__ __launch_bounds__(256) void k_splitk_finish(const float *__restrict__
   }
 }
 
+// The same for f16 NHWC outputs with 8-aligned widths and strides: 8
+// channels per thread, 16-byte loads and stores, one loop per activation.
+__global__ __launch_bounds__(256) void k_splitk_finish8(const float *__restrict__ part, int ksplit,
+                                                        long rows, int pitch, int N,
+                                                        const float *__restrict__ bias,
+                                                        const float *__restrict__ slope, int act,
+                                                        int accumulate, uint16_t *y, long ys) {
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  const int groups = N >> 3;
+  if (i >= rows * groups) return;
+  const long p = i / groups;
+  const int n = (int)(i - p * groups) * 8;
+  float4v s0 = *(const float4v *)(bias + n), s1 = *(const float4v *)(bias + n + 4);
+  for (int z = 0; z < ksplit; z++) {
+    const float *q = part + ((long)z * rows + p) * pitch + n;
+    s0 += *(const float4v *)q;
+    s1 += *(const float4v *)(q + 4);
+  }
+  float v[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
+  uint16_t *yo = y + p * ys + n;
+  if (accumulate) {
+    uint16_t h[8];
+    *(u32x4 *)h = *(const u32x4 *)yo;
+#pragma unroll
+    for (int e = 0; e < 8; e++) v[e] += h2f(h[e]);
+  }
+  uint16_t o[8];
+  auto out = [&](auto actf) {
+#pragma unroll
+    for (int e = 0; e < 8; e++) o[e] = f2h(actf(v[e], e));
+  };
+  switch (act) {
+    case IEN_ACT_RELU: out([&](float x, int) { return act_c<IEN_ACT_RELU>(x, 0.0f); }); break;
+    case IEN_ACT_GELU: out([&](float x, int) { return act_c<IEN_ACT_GELU>(x, 0.0f); }); break;
+    case IEN_ACT_SIGMOID: out([&](float x, int) { return act_c<IEN_ACT_SIGMOID>(x, 0.0f); }); break;
+    case IEN_ACT_PRELU: out([&](float x, int e) { return act_c<IEN_ACT_PRELU>(x, slope[n + e]); }); break;
+    default: out([&](float x, int) { return x; }); break;
+  }
+  *(u32x4 *)yo = *(const u32x4 *)o;
+}
+
+ien_status splitk_finish(ien_ctx *ctx, int ksplit, long rows, int pitch, const ConvArgs &a) {
+  if (!a.out_f32 && !a.out_nchw && a.N % 8 == 0 && pitch % 8 == 0 && a.ys % 8 == 0 &&
+      (((uintptr_t)a.y) & 15) == 0) {
+    const long items = rows * (a.N / 8);
+    hipLaunchKernelGGL(k_splitk_finish8, dim3((unsigned)((items + 255) / 256)), dim3(256), 0,
+                       ctx->stream, (const float *)ctx->splitk, ksplit, rows, pitch, a.N, a.bias,
+                       a.slope, a.act, a.accumulate, (uint16_t *)a.y, (long)a.ys);
+  } else {
+    const long items = rows * a.N;
+    hipLaunchKernelGGL(k_splitk_finish, dim3((unsigned)((items + 255) / 256)), dim3(256), 0,
+                       ctx->stream, (const float *)ctx->splitk, ksplit, rows, pitch, a.N, a.bias,
+                       a.slope, a.act, a.accumulate, a.y, (long)a.ys, a.out_f32, a.out_nchw);
+  }
+  IEN_HIP(hipGetLastError());
+  return IEN_OK;
+}
+
 // ---------------------------------------------------------------------------
 // Host dispatch.
 
@@ -674,12 +732,7 @@ static ien_status run_cfg(ien_ctx *ctx, ConvArgs a) {
   hipLaunchKernelGGL((conv_mfma<KS, S, TR, TC, MSPLIT, NBW, CK, VEC, IN_NCHW>),
                      dim3((unsigned)blocks, (unsigned)a.ksplit), dim3(256), 0, ctx->stream, pa);
   IEN_HIP(hipGetLastError());
-  const long items = rows * a.N;
-  hipLaunchKernelGGL(k_splitk_finish, dim3((unsigned)((items + 255) / 256)), dim3(256), 0,
-                     ctx->stream, (const float *)ctx->splitk, a.ksplit, rows, pitch, a.N, a.bias,
-                     a.slope, a.act, a.accumulate, a.y, (long)a.ys, a.out_f32, a.out_nchw);
-  IEN_HIP(hipGetLastError());
-  return IEN_OK;
+  return splitk_finish(ctx, a.ksplit, rows, pitch, a);
 }
 
 // Channel chunk of the 16-channel-step kernels: the largest of 64, 32, 16

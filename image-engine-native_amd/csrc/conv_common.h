@@ -153,6 +153,12 @@ __device__ __forceinline__ void dma16(const void *src, void *lds) {
   __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)lds, 16, 0, 0);
 }
 
+// conv.hip: the pass after a split-K product -- the ksplit f32 partial sums
+// of `rows` x a.N outputs (rows `pitch` floats apart, split z after z rows
+// x pitch, in the context's workspace) added in order, then bias, old
+// output when accumulating and activation into a.y.
+ien_status splitk_finish(ien_ctx *ctx, int ksplit, long rows, int pitch, const ConvArgs &a);
+
 // rows.hip: products over rows (1 x 1, NHWC f16 in and out) with K a
 // multiple of 32, N of 8, 16-byte aligned rows and enough tiles to fill
 // the chip.

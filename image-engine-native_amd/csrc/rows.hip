@@ -73,6 +73,10 @@ struct RowsArgs {
   int ys;
   int act, accumulate;
   int tiles_n, tiles;
+  // Split-K (gridDim.y splits of kchunks chunks): raw f32 sums of split z
+  // at part + (z M + row) pitch, no bias, for the finishing pass.
+  float *part;
+  int pitch, kchunks;
 };
 
 template <int BM_, int BN, int KC>
@@ -113,11 +117,13 @@ __global__ __launch_bounds__(256) void k_rows(RowsArgs a) {
   const unsigned l0 = rows_lds(lds);
   const int4v xr = rows_rsrc(a.x, (long)a.M * a.xs * 2);
   const int4v wr = rows_rsrc(a.wp, (long)a.NB * a.KB * 1024);
-  const int chunks = a.K / KC;
+  const int c_begin = blockIdx.y * a.kchunks;
+  const int chunks = min(a.K / KC - c_begin, a.kchunks);  // this split's chunks
 
   // Chunk c into stage s: A rows m0 .. m0 + BM - 1, channels c KC .. + KC - 1;
   // B fragments of column blocks tn BN / 32 .. and k blocks c KC / 16 ...
-  auto issue = [&](int c, int s) {
+  auto issue = [&](int lc, int s) {
+    const int c = c_begin + lc;
     const unsigned base = l0 + s * R::STAGE;
 #pragma unroll
     for (int i = 0; i < R::A_LOADS; i++) {
@@ -148,7 +154,7 @@ __global__ __launch_bounds__(256) void k_rows(RowsArgs a) {
 
   issue(0, 0);
   if (chunks > 1) issue(1, 1);
-  for (int c = 0; c < chunks; c++) {
+  for (int c = 0; c < chunks; c++) {  // c: this split's chunk index
     if (c + 1 < chunks)
       rows_wait<R::LPC>();  // all but chunk c + 1's loads
     else
@@ -176,6 +182,36 @@ __global__ __launch_bounds__(256) void k_rows(RowsArgs a) {
     }
   }
   __syncthreads();  // every wave is done with the stages
+
+  if (a.part) {  // split-K: raw sums, 32 bytes per item
+    float *st = (float *)lds;
+    const int owner = BM == 64 ? 0 : BN == 128 ? wm : wm >> 1;
+#pragma unroll
+    for (int half = 0; half < R::HALVES; half++) {
+      if (half) __syncthreads();
+      if (owner == half) {
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+          for (int i = 0; i < R::WM; i++)
+#pragma unroll
+            for (int r = 0; r < 16; r++)
+              st[((wm * R::WM + i) * 32 - 64 * half + 8 * (r >> 2) + 4 * hf + (r & 3)) * R::SP +
+                 (wn * 2 + j) * 32 + l32] = acc[i][j][r];
+      }
+      __syncthreads();
+#pragma unroll
+      for (int e = half * R::ITEMS / R::HALVES; e < (half + 1) * R::ITEMS / R::HALVES; e++) {
+        const int v = tid + 256 * e, row = v / (BN / 8), c8 = 8 * (v % (BN / 8));
+        if (m0 + row >= a.M) continue;
+        const float *sr = st + (row - 64 * half) * R::SP + c8;
+        float *q = a.part + ((long)blockIdx.y * a.M + m0 + row) * a.pitch + tn * BN + c8;
+        *(float4v *)q = *(const float4v *)sr;
+        *(float4v *)(q + 4) = *(const float4v *)(sr + 4);
+      }
+    }
+    return;
+  }
 
   // 16-byte items: row v / (BN / 8), channels 8 (v % (BN / 8)) ..., items
   // of staging pass h in rows 64 h .. 64 h + 63.  The old outputs are loaded
@@ -244,24 +280,43 @@ __global__ __launch_bounds__(256) void k_rows(RowsArgs a) {
   }
 }
 
+// Split-K when the tiles leave three quarters of the CUs idle, or any CU
+// idle with K at least 1536 deep: about two workgroups per CU, each split at
+// least 256 deep.  (Splitting products that already fill most CUs, such as
+// SCUNet's 1024-deep fc2 over 192 tiles, cost more in partial sums and the
+// finishing pass than it gained.)
 template <int BM, int BN, int KC>
-ien_status launch(ien_ctx *ctx, RowsArgs a) {
+ien_status launch(ien_ctx *ctx, RowsArgs a, const ConvArgs &c) {
   a.tiles_n = (a.N + BN - 1) / BN;
   a.tiles = (a.M + BM - 1) / BM * a.tiles_n;
-  hipLaunchKernelGGL((k_rows<BM, BN, KC>), dim3((unsigned)a.tiles), dim3(256), 0, ctx->stream, a);
+  const int chunks = a.K / KC;
+  a.pitch = a.tiles_n * BN;
+  int ksplit = 1;
+  if (chunks >= 16 && (4 * a.tiles <= ctx->cus || (a.K >= 1536 && a.tiles < ctx->cus))) {
+    ksplit = std::min(chunks / 8, (2 * ctx->cus + a.tiles - 1) / a.tiles);
+    while (ksplit > 1 && (size_t)ksplit * a.M * a.pitch > ctx->splitk_floats) ksplit--;
+  }
+  a.kchunks = (chunks + ksplit - 1) / ksplit;
+  ksplit = (chunks + a.kchunks - 1) / a.kchunks;
+  a.part = ksplit > 1 ? ctx->splitk : nullptr;
+  hipLaunchKernelGGL((k_rows<BM, BN, KC>), dim3((unsigned)a.tiles, (unsigned)ksplit), dim3(256), 0,
+                     ctx->stream, a);
   IEN_HIP(hipGetLastError());
-  return IEN_OK;
+  if (ksplit == 1) return IEN_OK;
+  return splitk_finish(ctx, ksplit, a.M, a.pitch, c);
 }
 
 }  // namespace
 
 // Tiles of 128 rows when they number at least 128, else 64-row tiles when
-// those number at least 96; below that the general kernel's split-K serves.
+// those number at least 96, or at least 8 with K 512 deep (split-K); below
+// that the general kernel serves.
 static long tiles_of(long rows, int bm, int n) { return (rows + bm - 1) / bm * ((n + 127) / 128); }
 
 bool rows_supported(const ConvArgs &a, long rows) {
   const bool aligned = (((uintptr_t)a.x) & 15) == 0 && (((uintptr_t)a.y) & 15) == 0;
-  const bool enough = tiles_of(rows, 128, a.N) >= 128 || tiles_of(rows, 64, a.N) >= 96;
+  const long t64 = tiles_of(rows, 64, a.N);
+  const bool enough = tiles_of(rows, 128, a.N) >= 128 || t64 >= 96 || (t64 >= 8 && a.C >= 512);
   return aligned && !a.out_f32 && !a.out_nchw && a.C % 32 == 0 && a.N % 8 == 0 && a.xs % 8 == 0 &&
          a.ys % 8 == 0 && (long)a.xs * (rows + 128) * 2 <= 0x7fff0000L &&
          (long)a.NB * a.KB * 1024 <= 0x7fff0000L && enough;
@@ -285,8 +340,8 @@ ien_status launch_rows(ien_ctx *ctx, const ConvArgs &c) {
   a.ys = c.ys;
   a.act = c.act;
   a.accumulate = c.accumulate;
-  if (tiles_of(a.M, 128, a.N) < 128) return launch<64, 128, 32>(ctx, a);
-  return c.N > 64 ? launch<128, 128, 32>(ctx, a) : launch<128, 64, 32>(ctx, a);
+  if (tiles_of(a.M, 128, a.N) < 128) return launch<64, 128, 32>(ctx, a, c);
+  return c.N > 64 ? launch<128, 128, 32>(ctx, a, c) : launch<128, 64, 32>(ctx, a, c);
 }
 
 }  // namespace ien

@@ -204,15 +204,17 @@ def test_rows(ctx, oracle, m, k, n):
 
 
 # Row products with enough tiles for the pipelined row kernel: 128-row tiles
-# of both widths (N > 64 and <= 64) and 64-row tiles (the last three cases),
-# K a multiple of 64 or only of 32, ragged last tiles in M and N,
+# of both widths (N > 64 and <= 64), 64-row tiles (cases 6-8) and, with K
+# at least 512 deep and few tiles, split-K into the finishing pass (the last
+# three), K a multiple of 64 or only of 32, ragged last tiles in M and N,
 # accumulation, activations, padded strides and row ranges that start past
 # row 0.
 @pytest.mark.parametrize("m,k,n,act,acc,row0,pad", [
     (16500, 256, 128, 2, False, 0, 8), (33000, 64, 64, 0, True, 0, 0),
     (20000, 96, 96, 3, True, 0, 8), (17000, 160, 40, 1, False, 0, 0),
     (17000, 128, 256, 0, True, 1000, 8),
-    (4096, 384, 192, 1, False, 0, 0), (4096, 192, 384, 1, True, 0, 8), (6100, 96, 256, 2, False, 37, 0)])
+    (4096, 384, 192, 1, False, 0, 0), (4096, 192, 384, 1, True, 0, 8), (6100, 96, 256, 2, False, 37, 0),
+    (1024, 768, 384, 0, False, 0, 0), (2000, 3072, 768, 2, True, 5, 8), (1000, 1536, 96, 3, True, 0, 0)])
 def test_rows_tiles(ctx, oracle, m, k, n, act, acc, row0, pad):
     import torch
     import ien
