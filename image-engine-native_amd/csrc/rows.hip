@@ -340,8 +340,11 @@ ien_status launch_rows(ien_ctx *ctx, const ConvArgs &c) {
   a.ys = c.ys;
   a.act = c.act;
   a.accumulate = c.accumulate;
-  if (tiles_of(a.M, 128, a.N) < 128) return launch<64, 128, 32>(ctx, a, c);
-  return c.N > 64 ? launch<128, 128, 32>(ctx, a, c) : launch<128, 64, 32>(ctx, a, c);
+  // Columns over 64: 64-row tiles (four workgroups a CU, twice the tiles of
+  // 128-row ones; measured faster on every model shape); up to 64 columns:
+  // 128 x 64 tiles.
+  if (c.N > 64 || tiles_of(a.M, 128, a.N) < 128) return launch<64, 128, 32>(ctx, a, c);
+  return launch<128, 64, 32>(ctx, a, c);
 }
 
 }  // namespace ien

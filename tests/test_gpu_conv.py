@@ -203,10 +203,10 @@ def test_rows(ctx, oracle, m, k, n):
     close(out.float().cpu().numpy(), want)
 
 
-# Row products with enough tiles for the pipelined row kernel: 128-row tiles
-# of both widths (N > 64 and <= 64), 64-row tiles (cases 6-8) and, with K
-# at least 512 deep and few tiles, split-K into the finishing pass (the last
-# three), K a multiple of 64 or only of 32, ragged last tiles in M and N,
+# Row products with enough tiles for the pipelined row kernel: 128 x 64
+# tiles (N <= 64), 64 x 128 tiles (wider N) and, with K at least 512 deep
+# and few tiles, split-K into the finishing pass (the last three), K a
+# multiple of 64 or only of 32, ragged last tiles in M and N,
 # accumulation, activations, padded strides and row ranges that start past
 # row 0.
 @pytest.mark.parametrize("m,k,n,act,acc,row0,pad", [
