@@ -825,6 +825,11 @@ ien_status launch_conv(ien_ctx *ctx, const ConvCall &c) {
       if (nchw) return run_cfg<3, 1, 4, 32, 4, 2, 16, false, true>(ctx, a);
       return run_cfg<3, 1, 4, 32, 4, 2, 16, false, false>(ctx, a);
     }
+    // NHWC: 4 x 32 tiles and 32-channel chunks, so that the halo and weight
+    // stages of three workgroups fit a CU's LDS and hide each other's load
+    // latency (same-box A/B against 64-channel chunks and 4 x 96 tiles:
+    // SCUNet 4.49 -> 4.30, LaMa 4.08 -> 4.01 ms).
+    if (!nchw && ck == 64) return run_cfg<3, 1, 4, 32, 4, 2, 32, true, false>(ctx, a);
     if (c.OW % 96 == 0 && ck == 64) {
       if (nchw) return run_cfg<3, 1, 4, 96, 4, 2, 64, true, true>(ctx, a);
       return run_cfg<3, 1, 4, 96, 4, 2, 64, true, false>(ctx, a);
