@@ -47,6 +47,13 @@ struct ien_ctx {
   // with the context so that no launch allocates (graph capture).
   float *splitk = nullptr;
   size_t splitk_floats = 0;
+  // Branch streams (default priority, non-blocking) with their own split-K
+  // workspaces: independent parts of a network run on them between fork()
+  // and join(), so that they overlap on the GPU (and in a captured graph).
+  static constexpr int BRANCHES = 3;
+  hipStream_t branch[BRANCHES] = {};
+  float *branch_splitk[BRANCHES] = {};
+  hipEvent_t fork_ev = nullptr, join_ev[BRANCHES] = {};
 };
 
 // Packed weights (gemm.rs Matrix): k x n padded to whole 16 x 32 MFMA
@@ -63,6 +70,29 @@ struct ien_matrix {
 };
 
 namespace ien {
+
+// fork_branches(ctx, n): branch streams 1..n start after the work already
+// on the context's stream; join_branches(ctx, n): the context's stream
+// continues after the branches' work.  Between them, a Branch object sends
+// the context's launches (and its split-K workspace) to branch i while it
+// lives.
+ien_status fork_branches(ien_ctx *ctx, int n);
+ien_status join_branches(ien_ctx *ctx, int n);
+struct Branch {
+  ien_ctx *ctx;
+  hipStream_t stream;
+  float *splitk;
+  Branch(ien_ctx *c, int i) : ctx(c), stream(c->stream), splitk(c->splitk) {
+    ctx->stream = ctx->branch[i - 1];
+    ctx->splitk = ctx->branch_splitk[i - 1];
+  }
+  ~Branch() {
+    ctx->stream = stream;
+    ctx->splitk = splitk;
+  }
+  Branch(const Branch &) = delete;
+  Branch &operator=(const Branch &) = delete;
+};
 
 // Pack row-major k x n weights (as floats) into the fragment layout above.
 std::vector<uint16_t> pack_fragments(const float *w, size_t k, size_t n, int *kb, int *nb);

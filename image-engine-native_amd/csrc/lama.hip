@@ -81,26 +81,36 @@ ien_status rows_product(ien_ctx *ctx, const uint16_t *in, size_t k, size_t rows,
 ien_status ffc_run(Lama *l, const LamaFfc &f, const uint16_t *x, uint16_t *out, int h, int w) {
   ien_ctx *ctx = l->ctx;
   const size_t pixels = (size_t)h * w, half = (size_t)w / 2 + 1, spix = (size_t)h * half;
+  // The local convolution, the cross convolution and the spectral chain
+  // are independent until the spectral output accumulates onto the cross
+  // part: local on the context's stream, cross on branch 1, the spectral
+  // chain on branch 2, joined before the accumulation.
+  ien_status st = fork_branches(ctx, 2);
   // local: all 512 channels -> 128, ReLU.
-  ien_status st = conv(ctx, x, h, w, CHANNELS, CHANNELS, 3, 1, f.local, out, CHANNELS,
-                       IEN_ACT_RELU, 0);
-  // cross: the local part -> the global part, no activation yet.
   if (st == IEN_OK)
+    st = conv(ctx, x, h, w, CHANNELS, CHANNELS, 3, 1, f.local, out, CHANNELS, IEN_ACT_RELU, 0);
+  // cross: the local part -> the global part, no activation yet.
+  if (st == IEN_OK) {
+    Branch b(ctx, 1);
     st = conv(ctx, x, h, w, LOCAL, CHANNELS, 3, 1, f.cross, out + LOCAL, CHANNELS, IEN_ACT_NONE,
               0);
-  // spectral_in: 1x1 of the global part -> 192, ReLU.
-  if (st == IEN_OK)
+  }
+  if (st == IEN_OK) {
+    Branch b(ctx, 2);
+    // spectral_in: 1x1 of the global part -> 192, ReLU.
     st = conv(ctx, x + LOCAL, h, w, GLOBAL, CHANNELS, 1, 1, f.spectral_in, l->spectral, SPECTRAL,
               IEN_ACT_RELU, 0);
-  if (st == IEN_OK)
-    st = ien_fourier_forward(l->fourier, l->spectral, SPECTRAL, SPECTRAL, l->work, l->spectrum);
-  // fourier: 1x1 over spectrum pixels [re | im] -> the same, ReLU.
-  if (st == IEN_OK)
-    st = rows_product(ctx, l->spectrum, 2 * SPECTRAL, spix, f.fourier, l->filtered,
-                      2 * SPECTRAL, IEN_ACT_RELU, 0);
-  // spectral += irfft(filtered).
-  if (st == IEN_OK)
-    st = ien_fourier_inverse(l->fourier, l->filtered, SPECTRAL, l->work, l->spectral, SPECTRAL);
+    if (st == IEN_OK)
+      st = ien_fourier_forward(l->fourier, l->spectral, SPECTRAL, SPECTRAL, l->work, l->spectrum);
+    // fourier: 1x1 over spectrum pixels [re | im] -> the same, ReLU.
+    if (st == IEN_OK)
+      st = rows_product(ctx, l->spectrum, 2 * SPECTRAL, spix, f.fourier, l->filtered,
+                        2 * SPECTRAL, IEN_ACT_RELU, 0);
+    // spectral += irfft(filtered).
+    if (st == IEN_OK)
+      st = ien_fourier_inverse(l->fourier, l->filtered, SPECTRAL, l->work, l->spectral, SPECTRAL);
+  }
+  if (st == IEN_OK) st = join_branches(ctx, 2);
   // global = ReLU(cross + spectral_out(spectral)).
   if (st == IEN_OK)
     st = rows_product(ctx, l->spectral, SPECTRAL, pixels, f.spectral_out, out + LOCAL, CHANNELS,

@@ -11,6 +11,22 @@
 
 namespace ien {
 
+ien_status fork_branches(ien_ctx *ctx, int n) {
+  IEN_CHECK(n >= 1 && n <= ien_ctx::BRANCHES, IEN_ERR_INPUT, "%d branches", n);
+  IEN_HIP(hipEventRecord(ctx->fork_ev, ctx->stream));
+  for (int i = 0; i < n; i++) IEN_HIP(hipStreamWaitEvent(ctx->branch[i], ctx->fork_ev, 0));
+  return IEN_OK;
+}
+
+ien_status join_branches(ien_ctx *ctx, int n) {
+  IEN_CHECK(n >= 1 && n <= ien_ctx::BRANCHES, IEN_ERR_INPUT, "%d branches", n);
+  for (int i = 0; i < n; i++) {
+    IEN_HIP(hipEventRecord(ctx->join_ev[i], ctx->branch[i]));
+    IEN_HIP(hipStreamWaitEvent(ctx->stream, ctx->join_ev[i], 0));
+  }
+  return IEN_OK;
+}
+
 static thread_local std::string g_error;
 
 void set_error(const char *fmt, ...) {
@@ -112,12 +128,17 @@ ien_status ien_open(int device, ien_ctx **out) {
   // 32 MiB of split-K partial sums.
   ctx->splitk_floats = (size_t)8 << 20;
   if (e == hipSuccess) e = hipMalloc((void **)&ctx->splitk, ctx->splitk_floats * 4);
+  if (e == hipSuccess) e = hipEventCreateWithFlags(&ctx->fork_ev, hipEventDisableTiming);
+  for (int i = 0; i < ien_ctx::BRANCHES && e == hipSuccess; i++) {
+    e = hipStreamCreateWithFlags(&ctx->branch[i], hipStreamNonBlocking);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&ctx->join_ev[i], hipEventDisableTiming);
+    if (e == hipSuccess)
+      e = hipMalloc((void **)&ctx->branch_splitk[i], ctx->splitk_floats * 4);
+  }
   if (e != hipSuccess) {
-    (void)hipFree(ctx->zeros);
-    (void)hipFree(ctx->splitk);
-    (void)hipStreamDestroy(ctx->own);
-    delete ctx;
-    return fail(IEN_ERR_GPU, "context buffers: %s", hipGetErrorString(e));
+    const std::string why = hipGetErrorString(e);
+    ien_close(ctx);
+    return fail(IEN_ERR_GPU, "context buffers: %s", why.c_str());
   }
   *out = ctx;
   return IEN_OK;
@@ -126,8 +147,17 @@ ien_status ien_open(int device, ien_ctx **out) {
 void ien_close(ien_ctx *ctx) {
   if (!ctx) return;
   (void)hipSetDevice(ctx->device);
-  (void)hipStreamSynchronize(ctx->stream);
-  (void)hipStreamDestroy(ctx->own);
+  if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+  for (int i = 0; i < ien_ctx::BRANCHES; i++) {
+    if (ctx->branch[i]) {
+      (void)hipStreamSynchronize(ctx->branch[i]);
+      (void)hipStreamDestroy(ctx->branch[i]);
+    }
+    if (ctx->join_ev[i]) (void)hipEventDestroy(ctx->join_ev[i]);
+    (void)hipFree(ctx->branch_splitk[i]);
+  }
+  if (ctx->fork_ev) (void)hipEventDestroy(ctx->fork_ev);
+  if (ctx->own) (void)hipStreamDestroy(ctx->own);
   (void)hipFree(ctx->zeros);
   (void)hipFree(ctx->splitk);
   delete ctx;

@@ -136,11 +136,18 @@ ien_status run_level(Scunet &s, ScunetBlock *blocks, int h, int w, int c, hipEve
   ien_status st = rows_product(ctx, s.x, c, pixels, blocks[0].split, s.y, c, 0);
   for (int b = 0; b < BLOCKS && st == IEN_OK; b++) {
     ScunetBlock &B = blocks[b];
-    // network.rs:135-153 convolve: conv3 + ReLU into t, conv3 added back.
-    st = conv3(ctx, s.y, h, w, (int)half, c, B.conv1, s.t, (long)half, IEN_ACT_RELU, 0);
-    if (st == IEN_OK)
-      st = conv3(ctx, s.t, h, w, (int)half, (long)half, B.conv2, s.y, c, IEN_ACT_NONE, 1);
+    // The two halves are independent until the join: the convolution half
+    // on branch 1, the Swin half on the context's stream.
+    st = fork_branches(ctx, 1);
+    if (st == IEN_OK) {
+      Branch br(ctx, 1);
+      // network.rs:135-153 convolve: conv3 + ReLU into t, conv3 added back.
+      st = conv3(ctx, s.y, h, w, (int)half, c, B.conv1, s.t, (long)half, IEN_ACT_RELU, 0);
+      if (st == IEN_OK)
+        st = conv3(ctx, s.t, h, w, (int)half, (long)half, B.conv2, s.y, c, IEN_ACT_NONE, 1);
+    }
     if (st == IEN_OK) st = ien_swin_run(B.swin, s.y + half, c, h, w);
+    if (st == IEN_OK) st = join_branches(ctx, 1);
     if (st == IEN_OK) st = rows_product(ctx, s.y, c, pixels, B.join, s.x, c, 1);
     if (st == IEN_OK && b + 1 < BLOCKS)
       st = rows_product(ctx, s.x, c, pixels, blocks[b + 1].split, s.y, c, 0);
