@@ -350,6 +350,8 @@ def main():
                     help="only the LaMa leg (the workload of its kernel profile)")
     ap.add_argument("--scunet-only", action="store_true",
                     help="only the SCUNet leg (the workload of its kernel profile)")
+    ap.add_argument("--sweep-only", action="store_true",
+                    help="only the conv sweep (the workload of its kernel profile)")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="only run the dominant layer 10 times and a 128 MiB device copy "
                          "(the workload of the FETCH_SIZE / WRITE_SIZE counter passes)")
@@ -383,6 +385,9 @@ def main():
         return
     if args.birefnet_only:
         print(json.dumps(birefnet_leg(ctx, max(1, args.steps // 10), 2)), flush=True)
+        return
+    if args.sweep_only:
+        print(json.dumps({"gemm_sweep": sweep(ctx, stream, args.kernel_reps)}), flush=True)
         return
     image = synthetic.esrgan_image(H, W)
     model = ien.Model(ctx, ien.MODEL_REALESRGAN, tensors=tensors)

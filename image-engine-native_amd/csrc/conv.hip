@@ -814,6 +814,12 @@ ien_status launch_conv(ien_ctx *ctx, const ConvCall &c) {
     if (vec) IEN_CK(0, 1, 4, 32, false);
     return run_cfg<0, 1, 4, 32, 4, 2, 16, false, false>(ctx, a);
   }
+  // Four input channels (the models' image inputs) and few outputs (their
+  // last convolutions): the general kernel would pad these to 16-channel
+  // steps and 64-channel tiles.
+  if (narrow_supported(a, c.ks, c.stride, nchw, c.noff, c.rows_mode))
+    return launch_narrow(ctx, a, c.ks);
+  if (few_supported(a, c.ks, c.stride, nchw, c.noff, c.rows_mode)) return launch_few(ctx, a, c.ks);
   // Resident weights: NHWC, zero padding, 16, 32 or 64 channels, K <= 640.
   // Its results are staged as f16: f32 outputs take the general kernel.
   if (vec && !c.out_f32 &&

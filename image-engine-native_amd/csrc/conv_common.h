@@ -171,4 +171,13 @@ bool resident_supported(int ks, int stride, int c, int nchw, int reflect, int no
                         long in_bytes);
 ien_status launch_resident(ien_ctx *ctx, ConvArgs a, int ks);
 
+// conv_small.hip: NHWC convolutions of 4 input channels (dense taps x
+// channels K) and of 64 input channels into N outputs with N x ks <= 32
+// ((output, kx) pairs as the MFMA rows); stride 1, zero or reflect padding,
+// whole output images.
+bool narrow_supported(const ConvArgs &a, int ks, int stride, int nchw, int noff, int rows_mode);
+ien_status launch_narrow(ien_ctx *ctx, ConvArgs a, int ks);
+bool few_supported(const ConvArgs &a, int ks, int stride, int nchw, int noff, int rows_mode);
+ien_status launch_few(ien_ctx *ctx, ConvArgs a, int ks);
+
 }  // namespace ien

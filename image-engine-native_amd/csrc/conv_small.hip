@@ -1,0 +1,354 @@
+// conv_small.hip -- convolutions whose channel counts leave most of an MFMA
+// tile empty in the general kernel (conv.hip), which pads the input to
+// 16-channel steps and the output to 64-channel tiles.
+//
+// conv_narrow: NHWC inputs of 4 channels (LaMa's masked image,
+// lama-native network.rs:46-58 first conv, 7x7 reflect; SCUNet's image
+// with a zero fourth channel, scunet-native network.rs:113-140 head, 3x3).
+// K = taps x 4 is dense: one v_mfma_f32_32x32x16_f16 step covers 4 taps of
+// 4 channels, lane half h reading taps 4s + 2h and 4s + 2h + 1 (two 8-byte
+// LDS reads).  The product is C^T = W^T X^T: the packed weight fragments
+// are the A operand and stay in VGPRs for the whole launch (64 output
+// channels, 2 x ceil(taps / 4) fragments), the pixels are the B operand.
+// Persistent workgroups of 8 waves walk 8 x 32-pixel tiles (wave w: tile
+// row w); the next tile's halo (8 bytes per pixel) is loaded into
+// registers while the current one computes, and written to the other of
+// two LDS halo buffers after it.  Each wave stages its 32 pixels x 64
+// channels in LDS and writes whole 16-byte chunks of pixel rows.
+//
+// conv_few: NHWC inputs of 64 channels into N outputs with N x KS <= 32
+// (LaMa's last conv 64 -> 3 7x7 reflect + sigmoid, network.rs:415-489;
+// SCUNet's tail 64 -> 3 3x3, network.rs:113-140).  The MFMA rows are the
+// (output, kx) pairs and K = (ky, channel): for an output row y and 64
+// consecutive padded input columns q,
+//   Z[(n, kx)][q] = sum_ky sum_c W[ky][kx][c][n] in[y + ky - P][q][c],
+// then out[n][x] = bias[n] + sum_kx Z[(n, kx)][x + kx]: 64 - 2P outputs per
+// 64 columns, the kx sum read back from LDS.  Padding is applied to the
+// input row and column indices (reflect, or zero for rows and columns
+// outside the image).
+// Both: bias, old output when accumulating, activation -- the order of
+// gemm.rs:583-666.
+
+#include "conv_common.h"
+
+namespace ien {
+
+namespace {
+
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// Input row or column i of an n-pixel axis: reflected (valid) or zero
+// padded (valid only inside).  Indices far outside (pixels that only feed
+// outputs past the edge) are clamped so that every address stays inside.
+__device__ __forceinline__ int pad_index(int i, int n, bool reflect, bool &ok) {
+  ok = reflect || (unsigned)i < (unsigned)n;
+  if (reflect) i = reflect_idx(i, n);
+  return min(max(i, 0), n - 1);
+}
+
+template <int KS>
+struct Narrow {
+  static constexpr int P = KS / 2, TAPS = KS * KS;
+  static constexpr int STEPS = (TAPS * 4 + 15) / 16;  // 4 taps of 4 channels a step
+  static constexpr int WAVES = 8, TR = WAVES, TC = 32;
+  static constexpr int HR = TR + KS - 1, HC = TC + KS - 1, HPIX = HR * HC;
+  static constexpr int HLOADS = (HPIX + WAVES * 64 - 1) / (WAVES * 64);  // halo pixels a thread
+  static constexpr int HALO = HPIX * 8;                                  // bytes (4 halves a pixel)
+  static constexpr int SPX = 64 + 8;                                     // staged halves a pixel
+  static constexpr int STAGE = 32 * SPX * 2;                             // bytes a wave
+  static constexpr int PARAM = 2 * HALO;         // 64 biases and 64 slopes (512 bytes)
+  static constexpr int STG = PARAM + 512;
+  static constexpr int LDS = STG + WAVES * STAGE;
+  static_assert(2 * STEPS * 1024 <= WAVES * STAGE, "the prologue's weights fit the staging");
+  static_assert(LDS <= 64 * 1024, "LDS budget");
+};
+
+// Byte offset of tap t's pixel from the tap-(0, 0) pixel of a halo row of
+// HC pixels; the padding taps past KS x KS (zero weights) read tap 0.
+template <int KS>
+__device__ __forceinline__ constexpr int tap_off(int t) {
+  return t < KS * KS ? ((t / KS) * Narrow<KS>::HC + t % KS) * 8 : 0;
+}
+
+template <int KS>
+__global__ __launch_bounds__(512) void conv_narrow(ConvArgs a) {
+  using R = Narrow<KS>;
+  constexpr int STEPS = R::STEPS, P = R::P;
+  __shared__ __attribute__((aligned(16))) unsigned char lds[R::LDS];
+  float *bias_l = (float *)(lds + R::PARAM), *slope_l = bias_l + 64;
+
+  const int tid = threadIdx.x, lane = tid & 63, hf = lane >> 5, l32 = lane & 31;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int tn = blockIdx.x % a.tiles_n;            // this block's 64 output channels
+  const int per_n = gridDim.x / a.tiles_n;          // blocks sharing them
+  const int tiles_x = (a.OW + R::TC - 1) / R::TC;
+  const int tiles_m = tiles_x * ((a.OH + R::TR - 1) / R::TR);
+  const bool reflect = a.pad_reflect != 0;
+
+  // ---- prologue: weights (fragments (2 tn + j, s)) through the staging
+  // area into VGPRs, biases and slopes into LDS ----
+  for (int f = wave; f < 2 * STEPS; f += R::WAVES) {
+    const int j = f / STEPS, s = f - j * STEPS;
+    *(u32x4 *)(lds + R::STG + f * 1024 + lane * 16) =
+        *(const u32x4 *)(a.wp + ((long)(2 * tn + j) * a.KB + s) * 512 + lane * 8);
+  }
+  if (tid < 64) {
+    const int n = tn * 64 + tid;
+    bias_l[tid] = a.bias[n];  // padded to whole 128-column tiles
+    slope_l[tid] = a.act == IEN_ACT_PRELU && n < a.N ? a.slope[n] : 0.0f;
+  }
+  __syncthreads();
+  half8 wr[2][STEPS];
+#pragma unroll
+  for (int j = 0; j < 2; j++)
+#pragma unroll
+    for (int s = 0; s < STEPS; s++)
+      wr[j][s] = *(const half8 *)(lds + R::STG + (j * STEPS + s) * 1024 + lane * 16);
+  // (The staging area is written only after the barrier at the top of the
+  // first tile, when every wave has read its weights.)
+
+  auto origin = [&](int mt, int &oy0, int &ox0) {
+    oy0 = (mt / tiles_x) * R::TR;
+    ox0 = (mt % tiles_x) * R::TC;
+  };
+  // The halo of tile mt into registers: pixel tid + 512 i of the
+  // (TR + KS - 1) x (TC + KS - 1) window, from a valid address always.
+  u32x2 hv[R::HLOADS];
+  auto load_halo = [&](int mt) {
+    int oy0, ox0;
+    origin(mt, oy0, ox0);
+#pragma unroll
+    for (int i = 0; i < R::HLOADS; i++) {
+      const int hp = min(tid + R::WAVES * 64 * i, R::HPIX - 1);
+      const int hy = hp / R::HC, hx = hp - hy * R::HC;
+      bool oky, okx;
+      const int iy = pad_index(oy0 + hy - P, a.H, reflect, oky);
+      const int ix = pad_index(ox0 + hx - P, a.W, reflect, okx);
+      const u32x2 v = *(const u32x2 *)(a.x + ((long)iy * a.W + ix) * a.xs);
+      hv[i] = oky && okx ? v : u32x2{0u, 0u};
+    }
+  };
+  auto store_halo = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < R::HLOADS; i++) {
+      const int hp = tid + R::WAVES * 64 * i;
+      if (hp < R::HPIX) *(u32x2 *)(lds + buf * R::HALO + hp * 8) = hv[i];
+    }
+  };
+
+  const bool accumulate = a.accumulate != 0;
+  unsigned char *stage = lds + R::STG + wave * R::STAGE;
+  uint16_t *yh = (uint16_t *)a.y;
+  int mt = blockIdx.x / a.tiles_n;
+  if (mt < tiles_m) load_halo(mt);
+  for (int it = 0; mt < tiles_m; it++, mt += per_n) {
+    store_halo(it & 1);
+    __syncthreads();  // the halo is in; every wave is past tile it - 2 (same buffer)
+    if (mt + per_n < tiles_m) load_halo(mt + per_n);
+    int oy0, ox0;
+    origin(mt, oy0, ox0);
+    const int oy = oy0 + wave, ox = ox0 + l32;
+    const bool in_out = oy < a.OH && ox < a.OW;
+    const long pix = (long)oy * a.OW + ox;
+
+    // Old outputs (when accumulating): the lane's 4 channels of each group.
+    u32x2 old[2][4];
+    if (accumulate) {
+#pragma unroll
+      for (int j = 0; j < 2; j++)
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+          const int n = tn * 64 + 32 * j + 8 * g + 4 * hf;
+          old[j][g] = in_out && n < a.N ? *(const u32x2 *)(yh + pix * a.ys + n) : u32x2{0u, 0u};
+        }
+    }
+
+    floatx16 acc[2];
+#pragma unroll
+    for (int j = 0; j < 2; j++)
+#pragma unroll
+      for (int g = 0; g < 4; g++) {
+        const float4v b4 = *(const float4v *)(bias_l + 32 * j + 8 * g + 4 * hf);
+#pragma unroll
+        for (int e = 0; e < 4; e++) acc[j][4 * g + e] = b4[e];
+      }
+    const unsigned char *hb = lds + (it & 1) * R::HALO + (wave * R::HC + l32) * 8;
+#pragma unroll
+    for (int s = 0; s < STEPS; s++) {
+      const int o0 = hf ? tap_off<KS>(4 * s + 2) : tap_off<KS>(4 * s);
+      const int o1 = hf ? tap_off<KS>(4 * s + 3) : tap_off<KS>(4 * s + 1);
+      const u32x2 p0 = *(const u32x2 *)(hb + o0), p1 = *(const u32x2 *)(hb + o1);
+      const u32x4 raw = {p0[0], p0[1], p1[0], p1[1]};
+      half8 xb;
+      __builtin_memcpy(&xb, &raw, 16);
+      acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wr[0][s], xb, acc[0], 0, 0, 0);
+      acc[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wr[1][s], xb, acc[1], 0, 0, 0);
+    }
+
+    // C^T: lane pixel l32, register 4 g + e = channel 32 j + 8 g + 4 hf + e.
+#pragma unroll
+    for (int j = 0; j < 2; j++)
+#pragma unroll
+      for (int g = 0; g < 4; g++) {
+        const int ch = 32 * j + 8 * g + 4 * hf;
+        uint16_t oh[4], h[4];
+        __builtin_memcpy(oh, &old[j][g], 8);
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          float v = acc[j][4 * g + e];
+          if (accumulate) v += h2f(oh[e]);
+          h[e] = f2h(activate(v, a.act, slope_l[ch + e]));
+        }
+        u32x2 o;
+        __builtin_memcpy(&o, h, 8);
+        *(u32x2 *)(stage + (l32 * R::SPX + ch) * 2) = o;
+      }
+    __builtin_amdgcn_wave_barrier();
+    // 32 pixels x 8 chunks of 16 bytes: item v = lane + 64 q.
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      const int v = lane + 64 * q, px = v >> 3, chunk = v & 7;
+      const u32x4 val = *(const u32x4 *)(stage + (px * R::SPX + 8 * chunk) * 2);
+      const int sx = ox0 + px, n = tn * 64 + 8 * chunk;
+      if (oy < a.OH && sx < a.OW && n < a.N)
+        *(u32x4 *)(yh + ((long)oy * a.OW + sx) * a.ys + n) = val;
+    }
+    __builtin_amdgcn_wave_barrier();  // the stage is read before the next tile writes it
+  }
+}
+
+template <int KS>
+struct Few {
+  static constexpr int P = KS / 2, C = 64;
+  static constexpr int STEPS = KS * C / 16;  // K = (ky, channel)
+  static constexpr int TW = 64 - 2 * P;     // outputs a 64-column item
+  static constexpr int ZP = 64 + 4;         // floats a staged Z row
+  static constexpr int WAVES = 4;
+  static constexpr int ZBYTES = 32 * ZP * 4;
+  static constexpr int LDS = WAVES * ZBYTES;
+  static_assert(STEPS * 1024 <= LDS, "the prologue's weights fit the Z stages");
+};
+
+template <int KS>
+__global__ __launch_bounds__(256) void conv_few(ConvArgs a) {
+  using R = Few<KS>;
+  constexpr int STEPS = R::STEPS, P = R::P, C = R::C, ZP = R::ZP;
+  __shared__ __attribute__((aligned(16))) unsigned char lds[R::LDS];
+  const int tid = threadIdx.x, lane = tid & 63, hf = lane >> 5, l32 = lane & 31;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int rows_used = a.N * KS;
+  const bool reflect = a.pad_reflect != 0;
+
+  // ---- prologue: the A operand of step s (W^T rows m = (n, kx), k = 16 s +
+  // 8 h + i = (ky, channel)) gathered from the packed fragments: W[k'][n]
+  // for k' = (ky KS + kx) C + c sits in fragment k' / 16, lane
+  // n + 32 ((k' % 16) / 8) ----
+  for (int s = wave; s < STEPS; s += R::WAVES) {
+    const int m = l32, n = m / KS, kx = m - n * KS;
+    const int k0 = 16 * s + 8 * hf, ky = k0 / C, c0 = k0 - ky * C;
+    const int kk = (ky * KS + kx) * C + c0;
+    u32x4 v = {0u, 0u, 0u, 0u};
+    if (m < rows_used) v = *(const u32x4 *)(a.wp + (long)(kk >> 4) * 512 + (n + 32 * ((kk & 15) >> 3)) * 8);
+    *(u32x4 *)(lds + s * 1024 + lane * 16) = v;
+  }
+  __syncthreads();
+  half8 wa[STEPS];
+#pragma unroll
+  for (int s = 0; s < STEPS; s++) wa[s] = *(const half8 *)(lds + s * 1024 + lane * 16);
+  __syncthreads();  // every wave has its weights before the Z stages are written
+
+  float *zs = (float *)(lds + wave * R::ZBYTES);
+  const int tiles_x = (a.OW + R::TW - 1) / R::TW;
+  const long items = (long)a.OH * tiles_x;
+  const int waves_total = gridDim.x * R::WAVES;
+  uint16_t *yh = (uint16_t *)a.y;
+  float *yf = (float *)a.y;
+  for (long item = (long)blockIdx.x * R::WAVES + wave; item < items; item += waves_total) {
+    const int y = (int)(item / tiles_x), x0 = (int)(item - (long)y * tiles_x) * R::TW;
+    // Input rows of the KS kernel rows (uniform).
+    int iy[KS];
+    bool oky[KS];
+#pragma unroll
+    for (int ky = 0; ky < KS; ky++) iy[ky] = pad_index(y + ky - P, a.H, reflect, oky[ky]);
+#pragma unroll
+    for (int cb = 0; cb < 2; cb++) {
+      bool okx;
+      const int ix = pad_index(x0 - P + 32 * cb + l32, a.W, reflect, okx);
+      floatx16 acc = {};
+#pragma unroll
+      for (int s = 0; s < STEPS; s++) {
+        const int k0 = 16 * s, ky = k0 / C, c0 = k0 - ky * C + 8 * hf;
+        const u32x4 raw = *(const u32x4 *)(a.x + ((long)iy[ky] * a.W + ix) * a.xs + c0);
+        const u32x4 v = oky[ky] && okx ? raw : u32x4{0u, 0u, 0u, 0u};
+        half8 xb;
+        __builtin_memcpy(&xb, &v, 16);
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(wa[s], xb, acc, 0, 0, 0);
+      }
+      // C: row 8 (r / 4) + 4 hf + r % 4 = (n, kx), column 32 cb + l32.
+#pragma unroll
+      for (int r = 0; r < 16; r++)
+        zs[(8 * (r >> 2) + 4 * hf + (r & 3)) * ZP + 32 * cb + l32] = acc[r];
+    }
+    __builtin_amdgcn_wave_barrier();
+    const int x = x0 + lane;
+    if (lane < R::TW && x < a.OW) {
+      const long pix = (long)y * a.OW + x;
+      for (int n = 0; n < a.N; n++) {
+        float v = a.bias[n];
+#pragma unroll
+        for (int kx = 0; kx < KS; kx++) v += zs[(n * KS + kx) * ZP + lane + kx];
+        const long at = pix * a.ys + n;
+        if (a.out_f32) {
+          if (a.accumulate) v += yf[at];
+          yf[at] = activate(v, a.act, a.act == IEN_ACT_PRELU ? a.slope[n] : 0.0f);
+        } else {
+          if (a.accumulate) v += h2f(yh[at]);
+          yh[at] = f2h(activate(v, a.act, a.act == IEN_ACT_PRELU ? a.slope[n] : 0.0f));
+        }
+      }
+    }
+    __builtin_amdgcn_wave_barrier();  // Z is read before the next item writes it
+  }
+}
+
+int cus_of(ien_ctx *ctx) { return ctx->cus > 0 ? ctx->cus : 256; }
+
+}  // namespace
+
+bool narrow_supported(const ConvArgs &a, int ks, int stride, int nchw, int noff, int rows_mode) {
+  return !nchw && !noff && !rows_mode && stride == 1 && a.C == 4 &&
+         (ks == 3 || ks == 5 || ks == 7) && a.xs % 4 == 0 && ((uintptr_t)a.x & 7) == 0 &&
+         a.p_begin == 0 && a.p_end == a.OH * a.OW && a.OH == a.H && a.OW == a.W &&
+         !a.out_f32 && !a.out_nchw && a.N % 8 == 0 && a.ys % 8 == 0 &&
+         ((uintptr_t)a.y & 15) == 0;
+}
+
+ien_status launch_narrow(ien_ctx *ctx, ConvArgs a, int ks) {
+  const int tiles_m = ((a.OW + 31) / 32) * ((a.OH + 7) / 8);
+  a.tiles_n = (a.N + 63) / 64;
+  const int per_n = std::max(1, std::min(tiles_m, cus_of(ctx) / a.tiles_n));
+  const dim3 grid(per_n * a.tiles_n), block(512);
+  if (ks == 3) hipLaunchKernelGGL(conv_narrow<3>, grid, block, 0, ctx->stream, a);
+  else if (ks == 5) hipLaunchKernelGGL(conv_narrow<5>, grid, block, 0, ctx->stream, a);
+  else hipLaunchKernelGGL(conv_narrow<7>, grid, block, 0, ctx->stream, a);
+  IEN_HIP(hipGetLastError());
+  return IEN_OK;
+}
+
+bool few_supported(const ConvArgs &a, int ks, int stride, int nchw, int noff, int rows_mode) {
+  return !nchw && !noff && !rows_mode && stride == 1 && a.C == 64 && (ks == 3 || ks == 7) &&
+         a.N * ks <= 32 && a.xs % 8 == 0 && ((uintptr_t)a.x & 15) == 0 && a.p_begin == 0 &&
+         a.p_end == a.OH * a.OW && a.OH == a.H && a.OW == a.W && !a.out_nchw;
+}
+
+ien_status launch_few(ien_ctx *ctx, ConvArgs a, int ks) {
+  const int tw = ks == 3 ? Few<3>::TW : Few<7>::TW;
+  const long items = (long)a.OH * ((a.OW + tw - 1) / tw);
+  const int blocks = (int)std::max(1L, std::min((items + 3) / 4, (long)cus_of(ctx) * 2));
+  if (ks == 3) hipLaunchKernelGGL(conv_few<3>, dim3(blocks), dim3(256), 0, ctx->stream, a);
+  else hipLaunchKernelGGL(conv_few<7>, dim3(blocks), dim3(256), 0, ctx->stream, a);
+  IEN_HIP(hipGetLastError());
+  return IEN_OK;
+}
+
+}  // namespace ien

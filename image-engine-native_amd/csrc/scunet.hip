@@ -5,6 +5,7 @@
 // convolutions as gathers / scatters around row products.  One event is
 // recorded after each of the 28 blocks for progress reports.
 
+#include <algorithm>
 #include <string>
 
 #include "ien_internal.h"
@@ -161,7 +162,18 @@ ien_status run_level(Scunet &s, ScunetBlock *blocks, int h, int w, int c, hipEve
 
 ien_status scunet_load(ien_ctx *ctx, const TensorSource &take, Scunet *s) {
   s->ctx = ctx;
-  ien_status st = matrix(ctx, take, "m_head.0", 27, DIM, false, &s->head);
+  // The head reads the image map's 4 channels (the fourth is zero): its
+  // 27 x DIM weights with a zero row after each tap's 3, so that K = 9 x 4
+  // runs on the four-channel kernel.
+  std::vector<float> head;
+  ien_status st = take("m_head.0.weight", {27, DIM}, &head);
+  if (st == IEN_OK) {
+    std::vector<float> head4((size_t)36 * DIM, 0.0f);
+    for (int t = 0; t < 9; t++)
+      for (int c = 0; c < 3; c++)
+        std::copy_n(&head[(size_t)(t * 3 + c) * DIM], DIM, &head4[(size_t)(t * 4 + c) * DIM]);
+    st = ien_matrix_new(ctx, head4.data(), IEN_W_F32, 36, DIM, nullptr, &s->head);
+  }
   for (int l = 0; l < 3 && st == IEN_OK; l++) {
     const int c = DIM << l;
     const std::string name = "m_down" + std::to_string(l + 1);
@@ -230,6 +242,8 @@ ien_status scunet_reserve(Scunet *s, size_t pw, size_t ph) {
   const size_t P = padded_pixels;
   auto alloc = [](uint16_t **p, size_t halves) { return hipMalloc((void **)p, halves * 2); };
   hipError_t e = alloc(&s->img, P * 8);
+  // Channels 3..7 of the image map stay zero (the head reads channel 3).
+  if (e == hipSuccess) e = hipMemsetAsync(s->img, 0, P * 8 * 2, s->ctx->stream);
   if (e == hipSuccess) e = alloc(&s->x, P * DIM);
   if (e == hipSuccess) e = alloc(&s->y, P * DIM);
   if (e == hipSuccess) e = alloc(&s->t, P * DIM / 2);
@@ -256,7 +270,7 @@ ien_status scunet_enqueue(Scunet *s, const float *d_image, size_t width, size_t 
   if (st != IEN_OK) return st;
   int h = (int)ph, w = (int)pw, c = DIM, step = 0;
   // The head (no bias); computed again at the end as the skip into the tail.
-  if ((st = conv3(ctx, s->img, h, w, 3, 8, s->head, s->x, DIM, IEN_ACT_NONE, 0)) != IEN_OK) return st;
+  if ((st = conv3(ctx, s->img, h, w, 4, 8, s->head, s->x, DIM, IEN_ACT_NONE, 0)) != IEN_OK) return st;
   for (int l = 0; l < 3; l++) {
     if ((st = run_level(*s, s->down[l], h, w, c, events, &step)) != IEN_OK) return st;
     // network.rs:403-437 halved, kept as the skip of the level up.
@@ -282,7 +296,7 @@ ien_status scunet_enqueue(Scunet *s, const float *d_image, size_t width, size_t 
     c /= 2;
     if ((st = run_level(*s, s->up[l], h, w, c, events, &step)) != IEN_OK) return st;
   }
-  if ((st = conv3(ctx, s->img, h, w, 3, 8, s->head, s->x, DIM, IEN_ACT_NONE, 1)) != IEN_OK) return st;
+  if ((st = conv3(ctx, s->img, h, w, 4, 8, s->head, s->x, DIM, IEN_ACT_NONE, 1)) != IEN_OK) return st;
   if ((st = conv3(ctx, s->x, h, w, DIM, DIM, s->tail, s->out16, 4, IEN_ACT_NONE, 0)) != IEN_OK)
     return st;
   return ien_crop(ctx, s->out16, pw, 4, width, height, 3, d_out);

@@ -27,7 +27,7 @@ def case(seed, h, w, c, n, taps):
 
 
 def run_gpu(ctx, x, wt, b, size=3, step=1, pad=0, offsets=None, act=0, slope=None, nchw_in=False,
-            nchw_out=False, out_f32=False, init=None, row0=0, rows=None, stride_pad=0):
+            nchw_out=False, out_f32=False, init=None, row0=0, rows=None, stride_pad=0, out_pad=None):
     import torch
     import ien
 
@@ -56,7 +56,7 @@ def run_gpu(ctx, x, wt, b, size=3, step=1, pad=0, offsets=None, act=0, slope=Non
             out.copy_(torch.from_numpy(init[row0:row0 + rows].T.copy()))
         ostride = rows
     else:
-        ostride = n + stride_pad
+        ostride = n + (stride_pad if out_pad is None else out_pad)
         out = torch.zeros((rows, ostride), dtype=dt, device="cuda")
         if init is not None:
             out[:, :n].copy_(torch.from_numpy(init[row0:row0 + rows]))
@@ -169,6 +169,52 @@ def test_reflect_3x3(ctx, oracle):
 def test_conv7x7(ctx, oracle, c, pad):
     x, wt, b = case(9, 12, 40, c, 64, 49)
     close(run_gpu(ctx, x, wt, b, size=7, pad=pad), want_cpu(oracle, x, wt, b, size=7, pad=pad))
+
+
+# Four input channels (conv_narrow: K = taps x 4 dense on MFMA, the models'
+# image inputs): 3x3, 5x5 and 7x7, zero and reflect padding, ragged 8 x 32
+# tiles, two 64-channel output tiles, 48 outputs, a padded input stride
+# (12 halves), activations after the old output.
+@pytest.mark.parametrize("size,pad,h,w,n,act,acc,sp", [
+    (7, 1, 37, 70, 64, "RELU", False, 0),    # LaMa's first conv
+    (3, 0, 21, 45, 64, "NONE", True, 8),     # SCUNet's head, added a second time
+    (5, 1, 9, 33, 128, "PRELU", False, 0),
+    (3, 1, 64, 96, 48, "GELU", True, 0),
+    (7, 0, 5, 7, 64, "SIGMOID", False, 8),   # smaller than one tile
+])
+def test_conv_four_channels(ctx, oracle, size, pad, h, w, n, act, acc, sp):
+    import ien
+
+    act = getattr(ien, "ACT_" + act)
+    x, wt, b = case(40 + size + n, h, w, 4, n, size * size)
+    slope = np.linspace(-0.3, 0.5, n).astype(np.float32)
+    init = f16(np.random.default_rng(h * w).standard_normal((h * w, n))) if acc else None
+    got = run_gpu(ctx, x, wt, b, size=size, pad=pad, act=act, slope=slope, init=init, stride_pad=sp)
+    close(got, want_cpu(oracle, x, wt, b, size=size, pad=pad, act=act, slope=slope, init=init))
+
+
+# Few outputs (conv_few: (output, kx) pairs as the MFMA rows, the kx sum read
+# back from LDS; the models' last convolutions): 7x7 and 3x3, reflect and
+# zero padding, 1 to 10 outputs, output strides of 3, 4 and 10 halves or f32,
+# images narrower than one 58- or 62-column item and several items a row.
+@pytest.mark.parametrize("size,pad,h,w,n,act,acc,f32,op", [
+    (7, 1, 40, 130, 3, "SIGMOID", False, False, 0),  # LaMa's last conv
+    (3, 0, 33, 70, 3, "NONE", False, False, 1),      # SCUNet's tail (output stride 4)
+    (3, 1, 12, 61, 10, "RELU", True, False, 0),
+    (7, 0, 9, 58, 4, "NONE", True, True, 0),
+    (3, 0, 5, 5, 1, "GELU", False, True, 0),
+    (7, 1, 17, 200, 2, "PRELU", False, False, 0),
+])
+def test_conv_few_outputs(ctx, oracle, size, pad, h, w, n, act, acc, f32, op):
+    import ien
+
+    act = getattr(ien, "ACT_" + act)
+    x, wt, b = case(60 + size + n, h, w, 64, n, size * size)
+    slope = np.linspace(-0.3, 0.5, n).astype(np.float32)
+    init = f16(np.random.default_rng(h + w).standard_normal((h * w, n))) if acc else None
+    got = run_gpu(ctx, x, wt, b, size=size, pad=pad, act=act, slope=slope, init=init, out_f32=f32,
+                  out_pad=op)
+    close(got, want_cpu(oracle, x, wt, b, size=size, pad=pad, act=act, slope=slope, init=init))
 
 
 def test_1x1(ctx, oracle):
