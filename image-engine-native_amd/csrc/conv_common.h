@@ -7,6 +7,8 @@
 
 #include "ien_internal.h"
 
+#pragma clang diagnostic ignored "-Winline-asm"  // m0 is written by the LDS loads
+
 namespace ien {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
@@ -124,6 +126,46 @@ __device__ __forceinline__ uint16_t f2h(float f) {
 __device__ __forceinline__ int xcd_remap(int b, int nblocks) {
   if ((nblocks & 7) != 0) return b;
   return (b & 7) * (nblocks >> 3) + (b >> 3);
+}
+
+typedef int int4v __attribute__((ext_vector_type(4)));
+
+// A raw buffer resource over `bytes` (< 2^31) bytes at `p`: offsets past
+// the end read 0 and drop stores.
+__device__ __forceinline__ int4v buffer_rsrc(const void *p, long bytes) {
+  const unsigned long long a = (unsigned long long)p;
+  int4v r;
+  r.x = (int)(unsigned)a;
+  r.y = (int)((a >> 32) & 0xffff);
+  r.z = (int)bytes;
+  r.w = 0x00020000;
+  return r;
+}
+
+// LDS byte address of a pointer into __shared__ memory.
+__device__ __forceinline__ unsigned lds_addr(const void *p) {
+  return (unsigned)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+}
+
+// Buffer loads straight into LDS, issued from inline assembly: lane l's
+// bytes from buffer offset `off` land at LDS `wave_base` + (16 or 4) l.
+// `wave_base` must be uniform.  Counted by vmcnt but invisible to the
+// compiler (its own waits after such loads flush whole counters), so the
+// kernel waits for them itself (wait_vm).  Loads complete in order.
+__device__ __forceinline__ void dma_lds(int4v rsrc, unsigned wave_base, int off) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               :: "s"(wave_base), "v"(off), "s"(rsrc) : "memory", "m0");
+}
+__device__ __forceinline__ void dma_lds4(int4v rsrc, unsigned wave_base, int off) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dword %1, %2, 0 offen lds"
+               :: "s"(wave_base), "v"(off), "s"(rsrc) : "memory", "m0");
+}
+
+// s_waitcnt vmcnt(n) alone.
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt(0x0f70 | (N & 15) | ((N >> 4) << 14));
 }
 
 // Global -> LDS staging, BATCH independent loads in flight per thread

@@ -34,45 +34,7 @@
 
 #include "conv_common.h"
 
-#pragma clang diagnostic ignored "-Winline-asm"  // m0 is written by the loads below
-
 namespace ien {
-
-namespace {
-
-typedef int int4v __attribute__((ext_vector_type(4)));
-
-// A raw buffer resource over `bytes` bytes at `p` (offsets past it read 0).
-__device__ __forceinline__ int4v buffer_rsrc(const void *p, int bytes) {
-  const unsigned long long a = (unsigned long long)p;
-  int4v r;
-  r.x = (int)(unsigned)a;
-  r.y = (int)((a >> 32) & 0xffff);
-  r.z = bytes;
-  r.w = 0x00020000;
-  return r;
-}
-
-// LDS byte address of a pointer into __shared__ memory.
-__device__ __forceinline__ unsigned lds_addr(const void *p) {
-  return (unsigned)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
-}
-
-// 16 bytes per lane from buffer offset `off` to LDS `wave_base` + 16 lane.
-// `wave_base` must be uniform.  Counted by vmcnt; invisible to the compiler.
-__device__ __forceinline__ void dma_lds(int4v rsrc, unsigned wave_base, int off) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-               :: "s"(wave_base), "v"(off), "s"(rsrc) : "memory", "m0");
-}
-
-// s_waitcnt vmcnt(n) alone.
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt(0x0f70 | (N & 15) | ((N >> 4) << 14));
-}
-
-}  // namespace
 
 template <int KS, int C>
 struct Res8 {

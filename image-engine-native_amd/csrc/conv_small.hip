@@ -11,10 +11,12 @@
 // are the A operand and stay in VGPRs for the whole launch (64 output
 // channels, 2 x ceil(taps / 4) fragments), the pixels are the B operand.
 // Persistent workgroups of 8 waves walk 8 x 32-pixel tiles (wave w: tile
-// row w); the next tile's halo (8 bytes per pixel) is loaded into
-// registers while the current one computes, and written to the other of
-// two LDS halo buffers after it.  Each wave stages its 32 pixels x 64
-// channels in LDS and writes whole 16-byte chunks of pixel rows.
+// row w); two register sets take turns holding the halos (8 bytes per
+// pixel) of the next two tiles while the current one computes, each
+// written to one of two LDS halo buffers when its tile starts.  Each wave
+// stages its 32 pixels x 64 channels in LDS and writes whole 16-byte
+// chunks of pixel rows.  The activation is a template parameter (no
+// branch per value).
 //
 // conv_few: NHWC inputs of 64 channels into N outputs with N x KS <= 32
 // (LaMa's last conv 64 -> 3 7x7 reflect + sigmoid, network.rs:415-489;
@@ -23,7 +25,9 @@
 // consecutive padded input columns q,
 //   Z[(n, kx)][q] = sum_ky sum_c W[ky][kx][c][n] in[y + ky - P][q][c],
 // then out[n][x] = bias[n] + sum_kx Z[(n, kx)][x + kx]: 64 - 2P outputs per
-// 64 columns, the kx sum read back from LDS.  Padding is applied to the
+// 64 columns, the kx sum read back from LDS.  The A operand stays in LDS
+// (the VGPRs hold a column block's loads, all issued before its MFMA
+// steps).  Padding is applied to the
 // input row and column indices (reflect, or zero for rows and columns
 // outside the image).
 // Both: bias, old output when accumulating, activation -- the order of
@@ -52,14 +56,17 @@ struct Narrow {
   static constexpr int STEPS = (TAPS * 4 + 15) / 16;  // 4 taps of 4 channels a step
   static constexpr int WAVES = 8, TR = WAVES, TC = 32;
   static constexpr int HR = TR + KS - 1, HC = TC + KS - 1, HPIX = HR * HC;
-  static constexpr int HLOADS = (HPIX + WAVES * 64 - 1) / (WAVES * 64);  // halo pixels a thread
-  static constexpr int HALO = HPIX * 8;                                  // bytes (4 halves a pixel)
-  static constexpr int SPX = 64 + 8;                                     // staged halves a pixel
-  static constexpr int STAGE = 32 * SPX * 2;                             // bytes a wave
-  static constexpr int PARAM = 2 * HALO;         // 64 biases and 64 slopes (512 bytes)
+  // The halo (HPIX pixels x 8 bytes) as dwords, half a pixel each, loaded
+  // straight into LDS: HL 256-byte loads per wave, whole rounds of 8 waves.
+  static constexpr int HL = (HPIX * 2 + WAVES * 64 - 1) / (WAVES * 64);
+  static constexpr int HALO = HL * WAVES * 256;  // bytes a buffer
+  static constexpr int SPX = 64 + 8;             // staged halves a pixel
+  static constexpr int STAGE = 32 * SPX * 2;     // bytes a wave
+  static constexpr int PARAM = 3 * HALO;         // 64 biases and 64 slopes (512 bytes)
   static constexpr int STG = PARAM + 512;
   static constexpr int LDS = STG + WAVES * STAGE;
   static_assert(2 * STEPS * 1024 <= WAVES * STAGE, "the prologue's weights fit the staging");
+  static_assert(HL < 16, "vmcnt range");
   static_assert(LDS <= 64 * 1024, "LDS budget");
 };
 
@@ -70,11 +77,11 @@ __device__ __forceinline__ constexpr int tap_off(int t) {
   return t < KS * KS ? ((t / KS) * Narrow<KS>::HC + t % KS) * 8 : 0;
 }
 
-template <int KS>
+template <int KS, int ACT>
 __global__ __launch_bounds__(512) void conv_narrow(ConvArgs a) {
   using R = Narrow<KS>;
-  constexpr int STEPS = R::STEPS, P = R::P;
-  __shared__ __attribute__((aligned(16))) unsigned char lds[R::LDS];
+  constexpr int STEPS = R::STEPS, P = R::P, HL = R::HL;
+  __shared__ __attribute__((aligned(1024))) unsigned char lds[R::LDS];
   float *bias_l = (float *)(lds + R::PARAM), *slope_l = bias_l + 64;
 
   const int tid = threadIdx.x, lane = tid & 63, hf = lane >> 5, l32 = lane & 31;
@@ -84,9 +91,36 @@ __global__ __launch_bounds__(512) void conv_narrow(ConvArgs a) {
   const int tiles_x = (a.OW + R::TC - 1) / R::TC;
   const int tiles_m = tiles_x * ((a.OH + R::TR - 1) / R::TR);
   const bool reflect = a.pad_reflect != 0;
+  const unsigned lds0 = lds_addr(lds);
+
+  auto origin = [&](int mt, int &oy0, int &ox0) {
+    oy0 = (mt / tiles_x) * R::TR;
+    ox0 = (mt % tiles_x) * R::TC;
+  };
+  // The halo of tile mt into LDS buffer `buf`: load i of this wave carries
+  // dwords d = 64 (wave + 8 i) + lane, i.e. channels 2 (d % 2), +1 of halo
+  // pixel d / 2.  Zero padding and the dwords past the halo read the
+  // buffer's range check (zeros); reflect padding reads the mirrored pixel.
+  constexpr int OOB = 0x7ffffff0;
+  const int4v xr = buffer_rsrc(a.x, (long)a.H * a.W * a.xs * 2);
+  auto load_halo = [&](int mt, int buf) {
+    int oy0, ox0;
+    origin(mt, oy0, ox0);
+#pragma unroll
+    for (int i = 0; i < HL; i++) {
+      const int d = 64 * (wave + R::WAVES * i) + lane, hp = d >> 1;
+      const int hy = hp / R::HC, hx = hp - hy * R::HC;
+      bool oky, okx;
+      const int iy = pad_index(oy0 + hy - P, a.H, reflect, oky);
+      const int ix = pad_index(ox0 + hx - P, a.W, reflect, okx);
+      const int off = hp < R::HPIX && oky && okx ? ((iy * a.W + ix) * a.xs + 2 * (d & 1)) * 2 : OOB;
+      dma_lds4(xr, __builtin_amdgcn_readfirstlane(lds0 + buf * R::HALO + 256 * (wave + R::WAVES * i)),
+               off);
+    }
+  };
 
   // ---- prologue: weights (fragments (2 tn + j, s)) through the staging
-  // area into VGPRs, biases and slopes into LDS ----
+  // area into VGPRs, biases and slopes into LDS, the first two halos ----
   for (int f = wave; f < 2 * STEPS; f += R::WAVES) {
     const int j = f / STEPS, s = f - j * STEPS;
     *(u32x4 *)(lds + R::STG + f * 1024 + lane * 16) =
@@ -95,8 +129,16 @@ __global__ __launch_bounds__(512) void conv_narrow(ConvArgs a) {
   if (tid < 64) {
     const int n = tn * 64 + tid;
     bias_l[tid] = a.bias[n];  // padded to whole 128-column tiles
-    slope_l[tid] = a.act == IEN_ACT_PRELU && n < a.N ? a.slope[n] : 0.0f;
+    slope_l[tid] = ACT == IEN_ACT_PRELU && n < a.N ? a.slope[n] : 0.0f;
   }
+  int mt = blockIdx.x / a.tiles_n;
+  const bool any = mt < tiles_m, second = mt + per_n < tiles_m;
+  if (any) load_halo(mt, 0);
+  if (second) load_halo(mt + per_n, 1);
+  if (second)
+    wait_vm<HL>();  // the first halo (the second may be in flight)
+  else
+    wait_vm<0>();
   __syncthreads();
   half8 wr[2][STEPS];
 #pragma unroll
@@ -104,107 +146,14 @@ __global__ __launch_bounds__(512) void conv_narrow(ConvArgs a) {
 #pragma unroll
     for (int s = 0; s < STEPS; s++)
       wr[j][s] = *(const half8 *)(lds + R::STG + (j * STEPS + s) * 1024 + lane * 16);
-  // (The staging area is written only after the barrier at the top of the
-  // first tile, when every wave has read its weights.)
+  __syncthreads();  // every wave has its weights before the staging is written
 
-  auto origin = [&](int mt, int &oy0, int &ox0) {
-    oy0 = (mt / tiles_x) * R::TR;
-    ox0 = (mt % tiles_x) * R::TC;
-  };
-  // The halo of tile mt into registers: pixel tid + 512 i of the
-  // (TR + KS - 1) x (TC + KS - 1) window, from a valid address always.
-  u32x2 hv[R::HLOADS];
-  auto load_halo = [&](int mt) {
-    int oy0, ox0;
-    origin(mt, oy0, ox0);
-#pragma unroll
-    for (int i = 0; i < R::HLOADS; i++) {
-      const int hp = min(tid + R::WAVES * 64 * i, R::HPIX - 1);
-      const int hy = hp / R::HC, hx = hp - hy * R::HC;
-      bool oky, okx;
-      const int iy = pad_index(oy0 + hy - P, a.H, reflect, oky);
-      const int ix = pad_index(ox0 + hx - P, a.W, reflect, okx);
-      const u32x2 v = *(const u32x2 *)(a.x + ((long)iy * a.W + ix) * a.xs);
-      hv[i] = oky && okx ? v : u32x2{0u, 0u};
-    }
-  };
-  auto store_halo = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < R::HLOADS; i++) {
-      const int hp = tid + R::WAVES * 64 * i;
-      if (hp < R::HPIX) *(u32x2 *)(lds + buf * R::HALO + hp * 8) = hv[i];
-    }
-  };
-
-  const bool accumulate = a.accumulate != 0;
   unsigned char *stage = lds + R::STG + wave * R::STAGE;
   uint16_t *yh = (uint16_t *)a.y;
-  int mt = blockIdx.x / a.tiles_n;
-  if (mt < tiles_m) load_halo(mt);
-  for (int it = 0; mt < tiles_m; it++, mt += per_n) {
-    store_halo(it & 1);
-    __syncthreads();  // the halo is in; every wave is past tile it - 2 (same buffer)
-    if (mt + per_n < tiles_m) load_halo(mt + per_n);
-    int oy0, ox0;
-    origin(mt, oy0, ox0);
-    const int oy = oy0 + wave, ox = ox0 + l32;
-    const bool in_out = oy < a.OH && ox < a.OW;
-    const long pix = (long)oy * a.OW + ox;
-
-    // Old outputs (when accumulating): the lane's 4 channels of each group.
-    u32x2 old[2][4];
-    if (accumulate) {
-#pragma unroll
-      for (int j = 0; j < 2; j++)
-#pragma unroll
-        for (int g = 0; g < 4; g++) {
-          const int n = tn * 64 + 32 * j + 8 * g + 4 * hf;
-          old[j][g] = in_out && n < a.N ? *(const u32x2 *)(yh + pix * a.ys + n) : u32x2{0u, 0u};
-        }
-    }
-
-    floatx16 acc[2];
-#pragma unroll
-    for (int j = 0; j < 2; j++)
-#pragma unroll
-      for (int g = 0; g < 4; g++) {
-        const float4v b4 = *(const float4v *)(bias_l + 32 * j + 8 * g + 4 * hf);
-#pragma unroll
-        for (int e = 0; e < 4; e++) acc[j][4 * g + e] = b4[e];
-      }
-    const unsigned char *hb = lds + (it & 1) * R::HALO + (wave * R::HC + l32) * 8;
-#pragma unroll
-    for (int s = 0; s < STEPS; s++) {
-      const int o0 = hf ? tap_off<KS>(4 * s + 2) : tap_off<KS>(4 * s);
-      const int o1 = hf ? tap_off<KS>(4 * s + 3) : tap_off<KS>(4 * s + 1);
-      const u32x2 p0 = *(const u32x2 *)(hb + o0), p1 = *(const u32x2 *)(hb + o1);
-      const u32x4 raw = {p0[0], p0[1], p1[0], p1[1]};
-      half8 xb;
-      __builtin_memcpy(&xb, &raw, 16);
-      acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wr[0][s], xb, acc[0], 0, 0, 0);
-      acc[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wr[1][s], xb, acc[1], 0, 0, 0);
-    }
-
-    // C^T: lane pixel l32, register 4 g + e = channel 32 j + 8 g + 4 hf + e.
-#pragma unroll
-    for (int j = 0; j < 2; j++)
-#pragma unroll
-      for (int g = 0; g < 4; g++) {
-        const int ch = 32 * j + 8 * g + 4 * hf;
-        uint16_t oh[4], h[4];
-        __builtin_memcpy(oh, &old[j][g], 8);
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-          float v = acc[j][4 * g + e];
-          if (accumulate) v += h2f(oh[e]);
-          h[e] = f2h(activate(v, a.act, slope_l[ch + e]));
-        }
-        u32x2 o;
-        __builtin_memcpy(&o, h, 8);
-        *(u32x2 *)(stage + (l32 * R::SPX + ch) * 2) = o;
-      }
-    __builtin_amdgcn_wave_barrier();
-    // 32 pixels x 8 chunks of 16 bytes: item v = lane + 64 q.
+  // The staged tile ending at (oy0, ox0): 32 pixels x 8 chunks of 16 bytes,
+  // item v = lane + 64 q.
+  auto store_tile = [&](int oy0, int ox0) {
+    const int oy = oy0 + wave;
 #pragma unroll
     for (int q = 0; q < 4; q++) {
       const int v = lane + 64 * q, px = v >> 3, chunk = v & 7;
@@ -213,8 +162,99 @@ __global__ __launch_bounds__(512) void conv_narrow(ConvArgs a) {
       if (oy < a.OH && sx < a.OW && n < a.N)
         *(u32x4 *)(yh + ((long)oy * a.OW + sx) * a.ys + n) = val;
     }
-    __builtin_amdgcn_wave_barrier();  // the stage is read before the next tile writes it
-  }
+  };
+
+  // Iteration t: buffer t % 3 holds tile t's halo, t + 1's is in flight;
+  // the stores of tile t - 1 go out first, then the loads of tile t + 2's
+  // halo, then tile t's steps and epilogue into this wave's stage.
+  auto run = [&](auto accum) {
+    constexpr bool ACC = decltype(accum)::value;
+    int prev_oy0 = -1, prev_ox0 = 0, buf = 0;
+    while (mt < tiles_m) {
+      if (prev_oy0 >= 0) store_tile(prev_oy0, prev_ox0);
+      const int far = mt + 2 * per_n;
+      const bool dma = far < tiles_m;  // uniform
+      if (dma) load_halo(far, buf == 0 ? 2 : buf - 1);
+      int oy0, ox0;
+      origin(mt, oy0, ox0);
+      const int oy = oy0 + wave, ox = ox0 + l32;
+      const bool in_out = oy < a.OH && ox < a.OW;
+      const long pix = (long)oy * a.OW + ox;
+
+      // Old outputs (when accumulating): the lane's 4 channels of each group.
+      u32x2 old[2][4];
+      if constexpr (ACC) {
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+          for (int g = 0; g < 4; g++) {
+            const int n = tn * 64 + 32 * j + 8 * g + 4 * hf;
+            old[j][g] = in_out && n < a.N ? *(const u32x2 *)(yh + pix * a.ys + n) : u32x2{0u, 0u};
+          }
+      }
+
+      floatx16 acc[2];
+#pragma unroll
+      for (int j = 0; j < 2; j++)
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+          const float4v b4 = *(const float4v *)(bias_l + 32 * j + 8 * g + 4 * hf);
+#pragma unroll
+          for (int e = 0; e < 4; e++) acc[j][4 * g + e] = b4[e];
+        }
+      const unsigned char *hb = lds + buf * R::HALO + (wave * R::HC + l32) * 8;
+#pragma unroll
+      for (int s = 0; s < STEPS; s++) {
+        const int o0 = hf ? tap_off<KS>(4 * s + 2) : tap_off<KS>(4 * s);
+        const int o1 = hf ? tap_off<KS>(4 * s + 3) : tap_off<KS>(4 * s + 1);
+        const u32x2 p0 = *(const u32x2 *)(hb + o0), p1 = *(const u32x2 *)(hb + o1);
+        const u32x4 raw = {p0[0], p0[1], p1[0], p1[1]};
+        half8 xb;
+        __builtin_memcpy(&xb, &raw, 16);
+        acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wr[0][s], xb, acc[0], 0, 0, 0);
+        acc[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wr[1][s], xb, acc[1], 0, 0, 0);
+      }
+
+      // C^T: lane pixel l32, register 4 g + e = channel 32 j + 8 g + 4 hf + e.
+      __builtin_amdgcn_wave_barrier();  // tile t - 1's stage was read above
+#pragma unroll
+      for (int j = 0; j < 2; j++)
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+          const int ch = 32 * j + 8 * g + 4 * hf;
+          const float4v s4 = *(const float4v *)(slope_l + ch);
+          uint16_t oh[4], h[4];
+          if constexpr (ACC) __builtin_memcpy(oh, &old[j][g], 8);
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            float v = acc[j][4 * g + e];
+            if constexpr (ACC) v += h2f(oh[e]);
+            h[e] = f2h(act_c<ACT>(v, s4[e]));
+          }
+          u32x2 o;
+          __builtin_memcpy(&o, h, 8);
+          *(u32x2 *)(stage + (l32 * R::SPX + ch) * 2) = o;
+        }
+      __builtin_amdgcn_wave_barrier();
+      prev_oy0 = oy0;
+      prev_ox0 = ox0;
+      mt += per_n;
+      buf = buf == 2 ? 0 : buf + 1;
+      // Tile t + 1's halo (loaded before this iteration's HL loads, which
+      // may be in flight; stores in between could be counted in their
+      // place, so without them wait for everything).
+      if (dma)
+        wait_vm<HL>();
+      else
+        wait_vm<0>();
+      __syncthreads();  // ... of every wave; buffer t % 3 is free for tile t + 3
+    }
+    if (prev_oy0 >= 0) store_tile(prev_oy0, prev_ox0);
+  };
+  if (a.accumulate)
+    run(std::true_type{});
+  else
+    run(std::false_type{});
 }
 
 template <int KS>
@@ -224,9 +264,9 @@ struct Few {
   static constexpr int TW = 64 - 2 * P;     // outputs a 64-column item
   static constexpr int ZP = 64 + 4;         // floats a staged Z row
   static constexpr int WAVES = 4;
+  static constexpr int ABYTES = STEPS * 1024;
   static constexpr int ZBYTES = 32 * ZP * 4;
-  static constexpr int LDS = WAVES * ZBYTES;
-  static_assert(STEPS * 1024 <= LDS, "the prologue's weights fit the Z stages");
+  static constexpr int LDS = ABYTES + WAVES * ZBYTES;
 };
 
 template <int KS>
@@ -240,9 +280,9 @@ __global__ __launch_bounds__(256) void conv_few(ConvArgs a) {
   const bool reflect = a.pad_reflect != 0;
 
   // ---- prologue: the A operand of step s (W^T rows m = (n, kx), k = 16 s +
-  // 8 h + i = (ky, channel)) gathered from the packed fragments: W[k'][n]
-  // for k' = (ky KS + kx) C + c sits in fragment k' / 16, lane
-  // n + 32 ((k' % 16) / 8) ----
+  // 8 h + i = (ky, channel)), kept in LDS, gathered from the packed
+  // fragments: W[k'][n] for k' = (ky KS + kx) C + c sits in fragment
+  // k' / 16, lane n + 32 ((k' % 16) / 8) ----
   for (int s = wave; s < STEPS; s += R::WAVES) {
     const int m = l32, n = m / KS, kx = m - n * KS;
     const int k0 = 16 * s + 8 * hf, ky = k0 / C, c0 = k0 - ky * C;
@@ -252,12 +292,8 @@ __global__ __launch_bounds__(256) void conv_few(ConvArgs a) {
     *(u32x4 *)(lds + s * 1024 + lane * 16) = v;
   }
   __syncthreads();
-  half8 wa[STEPS];
-#pragma unroll
-  for (int s = 0; s < STEPS; s++) wa[s] = *(const half8 *)(lds + s * 1024 + lane * 16);
-  __syncthreads();  // every wave has its weights before the Z stages are written
 
-  float *zs = (float *)(lds + wave * R::ZBYTES);
+  float *zs = (float *)(lds + R::ABYTES + wave * R::ZBYTES);
   const int tiles_x = (a.OW + R::TW - 1) / R::TW;
   const long items = (long)a.OH * tiles_x;
   const int waves_total = gridDim.x * R::WAVES;
@@ -274,15 +310,22 @@ __global__ __launch_bounds__(256) void conv_few(ConvArgs a) {
     for (int cb = 0; cb < 2; cb++) {
       bool okx;
       const int ix = pad_index(x0 - P + 32 * cb + l32, a.W, reflect, okx);
-      floatx16 acc = {};
+      // All of the column block's loads first, then the MFMA steps.
+      u32x4 xv[STEPS];
 #pragma unroll
       for (int s = 0; s < STEPS; s++) {
         const int k0 = 16 * s, ky = k0 / C, c0 = k0 - ky * C + 8 * hf;
-        const u32x4 raw = *(const u32x4 *)(a.x + ((long)iy[ky] * a.W + ix) * a.xs + c0);
-        const u32x4 v = oky[ky] && okx ? raw : u32x4{0u, 0u, 0u, 0u};
+        // Padding reads the zero buffer: no select waits for the load.
+        const uint16_t *src = oky[ky] && okx ? a.x + ((long)iy[ky] * a.W + ix) * a.xs : a.zeros;
+        xv[s] = *(const u32x4 *)(src + c0);
+      }
+      floatx16 acc = {};
+#pragma unroll
+      for (int s = 0; s < STEPS; s++) {
         half8 xb;
-        __builtin_memcpy(&xb, &v, 16);
-        acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(wa[s], xb, acc, 0, 0, 0);
+        __builtin_memcpy(&xb, &xv[s], 16);
+        const half8 wa = *(const half8 *)(lds + s * 1024 + lane * 16);
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(wa, xb, acc, 0, 0, 0);
       }
       // C: row 8 (r / 4) + 4 hf + r % 4 = (n, kx), column 32 cb + l32.
 #pragma unroll
@@ -298,12 +341,13 @@ __global__ __launch_bounds__(256) void conv_few(ConvArgs a) {
 #pragma unroll
         for (int kx = 0; kx < KS; kx++) v += zs[(n * KS + kx) * ZP + lane + kx];
         const long at = pix * a.ys + n;
+        const float sl = a.act == IEN_ACT_PRELU ? a.slope[n] : 0.0f;
         if (a.out_f32) {
           if (a.accumulate) v += yf[at];
-          yf[at] = activate(v, a.act, a.act == IEN_ACT_PRELU ? a.slope[n] : 0.0f);
+          yf[at] = activate(v, a.act, sl);
         } else {
           if (a.accumulate) v += h2f(yh[at]);
-          yh[at] = f2h(activate(v, a.act, a.act == IEN_ACT_PRELU ? a.slope[n] : 0.0f));
+          yh[at] = f2h(activate(v, a.act, sl));
         }
       }
     }
@@ -312,6 +356,28 @@ __global__ __launch_bounds__(256) void conv_few(ConvArgs a) {
 }
 
 int cus_of(ien_ctx *ctx) { return ctx->cus > 0 ? ctx->cus : 256; }
+
+template <int KS>
+ien_status narrow_act(ien_ctx *ctx, const ConvArgs &a, dim3 grid) {
+  switch (a.act) {
+    case IEN_ACT_RELU:
+      hipLaunchKernelGGL((conv_narrow<KS, IEN_ACT_RELU>), grid, dim3(512), 0, ctx->stream, a);
+      break;
+    case IEN_ACT_PRELU:
+      hipLaunchKernelGGL((conv_narrow<KS, IEN_ACT_PRELU>), grid, dim3(512), 0, ctx->stream, a);
+      break;
+    case IEN_ACT_GELU:
+      hipLaunchKernelGGL((conv_narrow<KS, IEN_ACT_GELU>), grid, dim3(512), 0, ctx->stream, a);
+      break;
+    case IEN_ACT_SIGMOID:
+      hipLaunchKernelGGL((conv_narrow<KS, IEN_ACT_SIGMOID>), grid, dim3(512), 0, ctx->stream, a);
+      break;
+    default:
+      hipLaunchKernelGGL((conv_narrow<KS, IEN_ACT_NONE>), grid, dim3(512), 0, ctx->stream, a);
+  }
+  IEN_HIP(hipGetLastError());
+  return IEN_OK;
+}
 
 }  // namespace
 
@@ -326,13 +392,14 @@ bool narrow_supported(const ConvArgs &a, int ks, int stride, int nchw, int noff,
 ien_status launch_narrow(ien_ctx *ctx, ConvArgs a, int ks) {
   const int tiles_m = ((a.OW + 31) / 32) * ((a.OH + 7) / 8);
   a.tiles_n = (a.N + 63) / 64;
-  const int per_n = std::max(1, std::min(tiles_m, cus_of(ctx) / a.tiles_n));
-  const dim3 grid(per_n * a.tiles_n), block(512);
-  if (ks == 3) hipLaunchKernelGGL(conv_narrow<3>, grid, block, 0, ctx->stream, a);
-  else if (ks == 5) hipLaunchKernelGGL(conv_narrow<5>, grid, block, 0, ctx->stream, a);
-  else hipLaunchKernelGGL(conv_narrow<7>, grid, block, 0, ctx->stream, a);
-  IEN_HIP(hipGetLastError());
-  return IEN_OK;
+  // One workgroup per CU at 7 x 7 (its weights fill the VGPRs), two at
+  // 3 x 3 and 5 x 5.
+  const int per_cu = ks == 7 ? 1 : 2;
+  const int per_n = std::max(1, std::min(tiles_m, per_cu * cus_of(ctx) / a.tiles_n));
+  const dim3 grid(per_n * a.tiles_n);
+  if (ks == 3) return narrow_act<3>(ctx, a, grid);
+  if (ks == 5) return narrow_act<5>(ctx, a, grid);
+  return narrow_act<7>(ctx, a, grid);
 }
 
 bool few_supported(const ConvArgs &a, int ks, int stride, int nchw, int noff, int rows_mode) {

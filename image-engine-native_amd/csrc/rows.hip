@@ -30,37 +30,8 @@
 
 #include "conv_common.h"
 
-#pragma clang diagnostic ignored "-Winline-asm"  // m0 is written by the loads below
-
 namespace ien {
 namespace {
-
-typedef int int4v __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ int4v rows_rsrc(const void *p, long bytes) {
-  const unsigned long long a = (unsigned long long)p;
-  int4v r;
-  r.x = (int)(unsigned)a;
-  r.y = (int)((a >> 32) & 0xffff);
-  r.z = (int)bytes;
-  r.w = 0x00020000;
-  return r;
-}
-
-__device__ __forceinline__ unsigned rows_lds(const void *p) {
-  return (unsigned)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
-}
-
-__device__ __forceinline__ void rows_dma(int4v r, unsigned wave_base, int off) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-               :: "s"(wave_base), "v"(off), "s"(r) : "memory", "m0");
-}
-
-template <int N>
-__device__ __forceinline__ void rows_wait() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt(0x0f70 | (N & 15) | ((N >> 4) << 14));
-}
 
 struct RowsArgs {
   const uint16_t *x;  // row 0 of the range
@@ -114,9 +85,9 @@ __global__ __launch_bounds__(256) void k_rows(RowsArgs a) {
   const int t = xcd_remap(blockIdx.x, gridDim.x);
   const int tm = t / a.tiles_n, tn = t - tm * a.tiles_n;
   const int m0 = tm * R::BM;
-  const unsigned l0 = rows_lds(lds);
-  const int4v xr = rows_rsrc(a.x, (long)a.M * a.xs * 2);
-  const int4v wr = rows_rsrc(a.wp, (long)a.NB * a.KB * 1024);
+  const unsigned l0 = lds_addr(lds);
+  const int4v xr = buffer_rsrc(a.x, (long)a.M * a.xs * 2);
+  const int4v wr = buffer_rsrc(a.wp, (long)a.NB * a.KB * 1024);
   const int c_begin = blockIdx.y * a.kchunks;
   const int chunks = min(a.K / KC - c_begin, a.kchunks);  // this split's chunks
 
@@ -131,7 +102,7 @@ __global__ __launch_bounds__(256) void k_rows(RowsArgs a) {
       const int row = d * (1024 / (KC * 2)) + lane / R::SLOTS;
       const int slot = lane % R::SLOTS;
       const int g = swz<R::SLOTS>(row, slot);      // the chunk this slot holds
-      rows_dma(xr, __builtin_amdgcn_readfirstlane(base + d * 1024),
+      dma_lds(xr, __builtin_amdgcn_readfirstlane(base + d * 1024),
                ((m0 + row) * a.xs + c * KC + 8 * g) * 2);
     }
 #pragma unroll
@@ -139,7 +110,7 @@ __global__ __launch_bounds__(256) void k_rows(RowsArgs a) {
       const int f = wave + 4 * i;                 // fragment (j, q) of the chunk
       const int j = f / (KC / 16), q = f % (KC / 16);
       const int nb = tn * (BN / 32) + j, kb = c * (KC / 16) + q;
-      rows_dma(wr, __builtin_amdgcn_readfirstlane(base + R::A_BYTES + f * 1024),
+      dma_lds(wr, __builtin_amdgcn_readfirstlane(base + R::A_BYTES + f * 1024),
                (nb * a.KB + kb) * 1024 + lane * 16);
     }
   };
@@ -156,9 +127,9 @@ __global__ __launch_bounds__(256) void k_rows(RowsArgs a) {
   if (chunks > 1) issue(1, 1);
   for (int c = 0; c < chunks; c++) {  // c: this split's chunk index
     if (c + 1 < chunks)
-      rows_wait<R::LPC>();  // all but chunk c + 1's loads
+      wait_vm<R::LPC>();  // all but chunk c + 1's loads
     else
-      rows_wait<0>();
+      wait_vm<0>();
     __syncthreads();  // chunk c visible; every wave is done with chunk c - 1
     if (c + 2 < chunks) issue(c + 2, (c + 2) % 3);
     const unsigned char *sa = lds + (c % 3) * R::STAGE;
