@@ -37,7 +37,8 @@
 
 namespace ien {
 
-template <int KS, int S, int TR, int TC, int MSPLIT, int NBW, int CK, bool VEC, bool IN_NCHW>
+template <int KS, int S, int TR, int TC, int MSPLIT, int NBW, int CK, bool VEC, bool IN_NCHW,
+          bool DB = false>
 struct ConvCfg {
   static constexpr int NSPLIT = 4 / MSPLIT;
   static constexpr int BN = 32 * NBW * NSPLIT;
@@ -58,22 +59,32 @@ struct ConvCfg {
   static constexpr int PB = CK * 2;                           // bytes per DMA halo pixel
   static constexpr int NCH = PB / 16;                         // 16-byte chunks per pixel
   static constexpr int RPB = PB >= 256 ? 1 : 256 / PB;        // pixels per 256-byte bank row
-  static constexpr int HALO_BYTES = DMA ? (HR * HC * PB + 1023) / 1024 * 1024 : HR * HC * CKP * 2;
+  // Double-buffered chunks (DB): whole rounds of the 4 waves' 1 KiB loads.
+  static constexpr int HALO_ROUND = DB ? 4096 : 1024;
+  static constexpr int HALO_BYTES =
+      DMA ? (HR * HC * PB + HALO_ROUND - 1) / HALO_ROUND * HALO_ROUND : HR * HC * CKP * 2;
   // 16-deep k steps of one chunk: VEC walks taps x CK/16; otherwise K is
   // flattened over (tap, channel) and rounded up to 16.
   static constexpr int KSTEPS = VEC ? TMAX * (CK / 16) : (TMAX * CK + 15) / 16;
-  static constexpr int B_BYTES = NBT * KSTEPS * 1024;  // B fragments of the chunk
+  static constexpr int BFRAGS = DB ? (NBT * KSTEPS + 3) / 4 * 4 : NBT * KSTEPS;
+  static constexpr int B_BYTES = BFRAGS * 1024;  // B fragments of the chunk
   // Epilogue staging per wave: NHWC [px][NBW*32 + 8] or NCHW [NBW*32][px + 4] floats.
   static constexpr int STAGE_NHWC = MBW * 32 * (NBW * 32 + 8);
   static constexpr int STAGE_NCHW = NBW * 32 * (MBW * 32 + 4);
   static constexpr int STAGE = STAGE_NHWC > STAGE_NCHW ? STAGE_NHWC : STAGE_NCHW;
   static constexpr int MAIN_BYTES = HALO_BYTES + B_BYTES;
-  static constexpr int LDS_BYTES = MAIN_BYTES > 4 * STAGE * 4 ? MAIN_BYTES : 4 * STAGE * 4;
+  static constexpr int BUFS = DB ? 2 : 1;
+  static constexpr int LDS_BYTES =
+      BUFS * MAIN_BYTES > 4 * STAGE * 4 ? BUFS * MAIN_BYTES : 4 * STAGE * 4;
+  // Loads per wave and chunk (DB): the halo's KiBs and the fragments.
+  static constexpr int DW = DB ? HALO_BYTES / 4096 + BFRAGS / 4 : 0;
+  // (Double buffering stages through direct-to-LDS loads only.)
+  static constexpr bool FITS = (!DB || DMA) && LDS_BYTES <= 160 * 1024 && DW < 64;
   static_assert(MB % MSPLIT == 0, "M-blocks must split evenly over waves");
   static_assert(TC % 32 == 0, "tile columns are whole M-blocks");
   static_assert(!VEC || CK % 16 == 0, "16-channel steps");
   static_assert(HALO_BYTES % 16 == 0, "B fragments start 16-byte aligned");
-  static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
+  static_assert(DB || LDS_BYTES <= 160 * 1024, "LDS budget");
 };
 
 // Swizzled chunk slot of 16-byte chunk c of DMA halo pixel p.
@@ -82,9 +93,10 @@ __device__ __forceinline__ int swz_slot(int p, int c) {
   return c ^ ((p / Cfg::RPB) & (Cfg::NCH - 1));
 }
 
-template <int KS, int S, int TR, int TC, int MSPLIT, int NBW, int CK, bool VEC, bool IN_NCHW>
+template <int KS, int S, int TR, int TC, int MSPLIT, int NBW, int CK, bool VEC, bool IN_NCHW,
+          bool DB = false>
 __global__ __launch_bounds__(256) void conv_mfma(ConvArgs a) {
-  using Cfg = ConvCfg<KS, S, TR, TC, MSPLIT, NBW, CK, VEC, IN_NCHW>;
+  using Cfg = ConvCfg<KS, S, TR, TC, MSPLIT, NBW, CK, VEC, IN_NCHW, DB>;
   constexpr int HR = Cfg::HR, HC = Cfg::HC, CKP = Cfg::CKP, MBW = Cfg::MBW, NBT = Cfg::NBT;
   constexpr int KSTEPS = Cfg::KSTEPS;
   constexpr int P = KS == 0 ? 0 : KS / 2;
@@ -157,124 +169,12 @@ __global__ __launch_bounds__(256) void conv_mfma(ConvArgs a) {
 
   const int c_begin = (int)blockIdx.y * a.kchunks * CK;
   const int c_end = min(a.C, c_begin + a.kchunks * CK);
-  for (int c0 = c_begin; c0 < c_end; c0 += CK) {
-    const int cc = min(CK, a.C - c0);  // == CK when VEC
-    __syncthreads();
-    // ---- global -> LDS: the halo of this channel chunk ----
-    if constexpr (Cfg::DMA) {
-      // One KiB per wave instruction: lane l fills byte 16 l of it, which
-      // is chunk slot s of halo pixel p, holding input chunk
-      // s ^ swizzle(p); padding pixels read the zero page.
-      constexpr int G = Cfg::HALO_BYTES / 1024;
-      for (int g = wave; g < G; g += 4) {
-        const int byte = g * 1024 + lane * 16;
-        const int hp = byte / Cfg::PB, slot = (byte % Cfg::PB) / 16;
-        const uint16_t *src = a.zeros;
-        if (hp < HR * HC) {
-          const int hy = hp / HC, hx = hp - hy * HC;
-          const int off = resolve(iy0 + hy, ix0 + hx);
-          if (off >= 0) src = a.x + off + c0 + 8 * swz_slot<Cfg>(hp, slot);
-        }
-        dma16(src, lds_raw + g * 1024);
-      }
-    } else if constexpr (!IN_NCHW) {
-      // Few channels: one half per element.
-      auto where = [&](int e, int &hp, int &c) {
-        hp = e / cc;
-        c = e - hp * cc;
-        const int hy = hp / HC, hx = hp - hy * HC;
-        return resolve(iy0 + hy, ix0 + hx);
-      };
-      staged_copy<8>(
-          HR * HC * cc, tid,
-          [&](int e) -> u32x4 {
-            int hp, c;
-            const int off = where(e, hp, c);
-            return u32x4{(uint32_t)a.x[(off >= 0 ? off : 0) + c0 + c], 0u, 0u, 0u};
-          },
-          [&](int e, u32x4 val) {
-            int hp, c;
-            const int off = where(e, hp, c);
-            halo[hp * CKP + c] = off >= 0 ? (uint16_t)val[0] : (uint16_t)0;
-          });
-    } else {
-      // NCHW.  Fast path (rows of whole 16-byte groups, zero padding): 8
-      // neighbouring pixels of one channel row per load; a group lies wholly
-      // inside or wholly outside the image.  Otherwise one half per element.
-      const bool fast = !a.rows_mode && !a.pad_reflect && (a.W & 7) == 0 && (a.xs & 7) == 0 &&
-                        (((uintptr_t)a.x) & 15) == 0;
-      if (fast) {
-        auto floor8 = [](int v) { return v >= 0 ? v / 8 : -((7 - v) / 8); };
-        const int g0 = floor8(ix0);
-        const int groups = floor8(ix0 + HC - 1) + 1 - g0;
-        auto where = [&](int e, int &hy, int &c, int &gx) {
-          const int g = e % groups, rest = e / groups;
-          hy = rest % HR;
-          c = rest / HR;
-          gx = (g0 + g) * 8;
-          const int iy = iy0 + hy;
-          return iy >= 0 && iy < a.H && gx >= 0 && gx < a.W;
-        };
-        staged_copy<8>(
-            cc * HR * groups, tid,
-            [&](int e) -> u32x4 {
-              int hy, c, gx;
-              const bool ok = where(e, hy, c, gx);
-              const int off = ok ? (c0 + c) * a.xs + (iy0 + hy) * a.W + gx : 0;
-              return *(const u32x4 *)(a.x + off);
-            },
-            [&](int e, u32x4 val) {
-              int hy, c, gx;
-              if (!where(e, hy, c, gx)) val = u32x4{0u, 0u, 0u, 0u};
-              uint16_t v8[8];
-              __builtin_memcpy(v8, &val, 16);
-#pragma unroll
-              for (int q = 0; q < 8; q++) {
-                const int hx = gx + q - ix0;
-                if (hx >= 0 && hx < HC) halo[(hy * HC + hx) * CKP + c] = v8[q];
-              }
-            });
-      } else {
-        auto where = [&](int e, int &hp, int &c) {
-          c = e / (HR * HC);
-          hp = e - c * (HR * HC);
-          const int hy = hp / HC, hx = hp - hy * HC;
-          return resolve(iy0 + hy, ix0 + hx);
-        };
-        staged_copy<8>(
-            cc * HR * HC, tid,
-            [&](int e) -> u32x4 {
-              int hp, c;
-              const int off = where(e, hp, c);
-              return u32x4{(uint32_t)a.x[(c0 + c) * a.xs + (off >= 0 ? off : 0)], 0u, 0u, 0u};
-            },
-            [&](int e, u32x4 val) {
-              int hp, c;
-              const int off = where(e, hp, c);
-              halo[hp * CKP + c] = off >= 0 ? (uint16_t)val[0] : (uint16_t)0;
-            });
-      }
-    }
-
-    // ---- global -> LDS: this chunk's weight fragments, [block][step], ----
-    // one KiB fragment per wave instruction.
-    {
-      const int steps = VEC ? T * (CK / 16) : (T * cc + 15) / 16;
-      for (int f = wave; f < NBT * steps; f += 4) {
-        const int jn = f / steps, s = f - jn * steps;
-        int kb = s;  // one chunk holds all channels: fragments in order
-        if (VEC) {
-          const int tap = s / (CK / 16), kc = s % (CK / 16);
-          kb = tap * (a.C / 16) + c0 / 16 + kc;
-        }
-        dma16(a.wp + ((nblk_tile + jn) * a.KB + kb) * 512 + lane * 8,
-              bl + (jn * KSTEPS + s) * 512);
-      }
-    }
-    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): the direct-to-LDS loads have landed
-    __syncthreads();
-
-    const uint16_t *bw = bl + ng * NBW * KSTEPS * 512 + lane * 8;
+  // The products of one staged channel chunk (its halo and B fragments at
+  // `base`; cc channels).
+  auto compute = [&](const unsigned char *base, int cc) {
+    const uint16_t *halo = (const uint16_t *)base;
+    const uint16_t *bw =
+        (const uint16_t *)(base + Cfg::HALO_BYTES) + ng * NBW * KSTEPS * 512 + lane * 8;
     auto mma = [&](const half8 *av, const half8 *bv) {
 #pragma unroll
       for (int i = 0; i < MBW; i++)
@@ -292,7 +192,7 @@ __global__ __launch_bounds__(256) void conv_mfma(ConvArgs a) {
 #pragma unroll
           for (int i = 0; i < MBW; i++) {
             const int p = apix[i] + dy * HC + dx;
-            av[i] = *(const half8 *)(lds_raw + p * Cfg::PB + 16 * swz_slot<Cfg>(p, c));
+            av[i] = *(const half8 *)(base + p * Cfg::PB + 16 * swz_slot<Cfg>(p, c));
           }
         } else {
           const int off = (dy * HC + dx) * CKP + kc * 16;
@@ -324,7 +224,7 @@ __global__ __launch_bounds__(256) void conv_mfma(ConvArgs a) {
 #pragma unroll
         for (int i = 0; i < MBW; i++) {
           const int p = apix[i] + a.offy[tap] * HC + a.offx[tap];
-          av[i] = *(const half8 *)(lds_raw + p * Cfg::PB + 16 * swz_slot<Cfg>(p, c));
+          av[i] = *(const half8 *)(base + p * Cfg::PB + 16 * swz_slot<Cfg>(p, c));
         }
 #pragma unroll
         for (int j = 0; j < NBW; j++) bv[j] = *(const half8 *)(bw + (j * KSTEPS + s) * 512);
@@ -363,6 +263,181 @@ __global__ __launch_bounds__(256) void conv_mfma(ConvArgs a) {
         }
         mma(av, bv);
       }
+    }
+  };
+
+  if constexpr (DB) {
+    // Double-buffered chunks: chunk i + 1's halo and fragments are loaded
+    // (straight into the other LDS buffer, by loads the compiler does not
+    // see) while chunk i is multiplied; a wait for the chunk's own loads
+    // (all but the DW loads issued after them) and one barrier on each side.
+    // The buffer range checks give the zero padding.
+    constexpr int OOB = 0x7ffffff0;
+    const long in_halves = a.rows_mode ? (long)a.M * a.xs : (long)a.H * a.W * a.xs;
+    const int4v xr = uniform_rsrc(a.x, in_halves * 2);
+    const int4v wrs = uniform_rsrc(a.wp, (long)a.NB * a.KB * 1024);
+    const unsigned lds0 = lds_addr(lds_raw);
+    const int steps = T * (CK / 16);
+    auto issue = [&](int c0, int buf) {
+      const unsigned bb = lds0 + buf * Cfg::MAIN_BYTES;
+#pragma unroll
+      for (int gi = 0; gi < Cfg::HALO_BYTES / 4096; gi++) {
+        const int g = wave + 4 * gi;
+        const int byte = g * 1024 + lane * 16;
+        const int hp = byte / Cfg::PB, slot = (byte % Cfg::PB) / 16;
+        int off = OOB;
+        if (hp < HR * HC) {
+          const int hy = hp / HC, hx = hp - hy * HC;
+          const int o = resolve(iy0 + hy, ix0 + hx);
+          if (o >= 0) off = (o + c0 + 8 * swz_slot<Cfg>(hp, slot)) * 2;
+        }
+        dma_lds(xr, __builtin_amdgcn_readfirstlane(bb + g * 1024), off);
+      }
+#pragma unroll
+      for (int fi = 0; fi < Cfg::BFRAGS / 4; fi++) {
+        const int f = wave + 4 * fi;
+        const int jn = f / KSTEPS, st = f - jn * KSTEPS;
+        int off = OOB;
+        if (jn < NBT && st < steps) {
+          const int tap = st / (CK / 16), kc = st % (CK / 16);
+          const int kb = tap * (a.C / 16) + c0 / 16 + kc;
+          off = (((nblk_tile + jn) * a.KB + kb) * 512 + lane * 8) * 2;
+        }
+        dma_lds(wrs, __builtin_amdgcn_readfirstlane(bb + Cfg::HALO_BYTES + f * 1024), off);
+      }
+    };
+    if (c_begin < c_end) issue(c_begin, 0);
+    int i = 0;
+    for (int c0 = c_begin; c0 < c_end; c0 += CK, i++) {
+      const bool next = c0 + CK < c_end;  // uniform
+      if (next) issue(c0 + CK, (i + 1) & 1);
+      if (next)
+        wait_vm<Cfg::DW>();
+      else
+        wait_vm<0>();
+      __syncthreads();  // chunk i is in every wave's view
+      compute(lds_raw + (i & 1) * Cfg::MAIN_BYTES, CK);
+      __syncthreads();  // every wave is done with buffer i % 2 before chunk i + 2 fills it
+    }
+  } else {
+    for (int c0 = c_begin; c0 < c_end; c0 += CK) {
+      const int cc = min(CK, a.C - c0);  // == CK when VEC
+      __syncthreads();
+      // ---- global -> LDS: the halo of this channel chunk ----
+      if constexpr (Cfg::DMA) {
+        // One KiB per wave instruction: lane l fills byte 16 l of it, which
+        // is chunk slot s of halo pixel p, holding input chunk
+        // s ^ swizzle(p); padding pixels read the zero page.
+        constexpr int G = Cfg::HALO_BYTES / 1024;
+        for (int g = wave; g < G; g += 4) {
+          const int byte = g * 1024 + lane * 16;
+          const int hp = byte / Cfg::PB, slot = (byte % Cfg::PB) / 16;
+          const uint16_t *src = a.zeros;
+          if (hp < HR * HC) {
+            const int hy = hp / HC, hx = hp - hy * HC;
+            const int off = resolve(iy0 + hy, ix0 + hx);
+            if (off >= 0) src = a.x + off + c0 + 8 * swz_slot<Cfg>(hp, slot);
+          }
+          dma16(src, lds_raw + g * 1024);
+        }
+      } else if constexpr (!IN_NCHW) {
+        // Few channels: one half per element.
+        auto where = [&](int e, int &hp, int &c) {
+          hp = e / cc;
+          c = e - hp * cc;
+          const int hy = hp / HC, hx = hp - hy * HC;
+          return resolve(iy0 + hy, ix0 + hx);
+        };
+        staged_copy<8>(
+            HR * HC * cc, tid,
+            [&](int e) -> u32x4 {
+              int hp, c;
+              const int off = where(e, hp, c);
+              return u32x4{(uint32_t)a.x[(off >= 0 ? off : 0) + c0 + c], 0u, 0u, 0u};
+            },
+            [&](int e, u32x4 val) {
+              int hp, c;
+              const int off = where(e, hp, c);
+              halo[hp * CKP + c] = off >= 0 ? (uint16_t)val[0] : (uint16_t)0;
+            });
+      } else {
+        // NCHW.  Fast path (rows of whole 16-byte groups, zero padding): 8
+        // neighbouring pixels of one channel row per load; a group lies wholly
+        // inside or wholly outside the image.  Otherwise one half per element.
+        const bool fast = !a.rows_mode && !a.pad_reflect && (a.W & 7) == 0 && (a.xs & 7) == 0 &&
+                          (((uintptr_t)a.x) & 15) == 0;
+        if (fast) {
+          auto floor8 = [](int v) { return v >= 0 ? v / 8 : -((7 - v) / 8); };
+          const int g0 = floor8(ix0);
+          const int groups = floor8(ix0 + HC - 1) + 1 - g0;
+          auto where = [&](int e, int &hy, int &c, int &gx) {
+            const int g = e % groups, rest = e / groups;
+            hy = rest % HR;
+            c = rest / HR;
+            gx = (g0 + g) * 8;
+            const int iy = iy0 + hy;
+            return iy >= 0 && iy < a.H && gx >= 0 && gx < a.W;
+          };
+          staged_copy<8>(
+              cc * HR * groups, tid,
+              [&](int e) -> u32x4 {
+                int hy, c, gx;
+                const bool ok = where(e, hy, c, gx);
+                const int off = ok ? (c0 + c) * a.xs + (iy0 + hy) * a.W + gx : 0;
+                return *(const u32x4 *)(a.x + off);
+              },
+              [&](int e, u32x4 val) {
+                int hy, c, gx;
+                if (!where(e, hy, c, gx)) val = u32x4{0u, 0u, 0u, 0u};
+                uint16_t v8[8];
+                __builtin_memcpy(v8, &val, 16);
+#pragma unroll
+                for (int q = 0; q < 8; q++) {
+                  const int hx = gx + q - ix0;
+                  if (hx >= 0 && hx < HC) halo[(hy * HC + hx) * CKP + c] = v8[q];
+                }
+              });
+        } else {
+          auto where = [&](int e, int &hp, int &c) {
+            c = e / (HR * HC);
+            hp = e - c * (HR * HC);
+            const int hy = hp / HC, hx = hp - hy * HC;
+            return resolve(iy0 + hy, ix0 + hx);
+          };
+          staged_copy<8>(
+              cc * HR * HC, tid,
+              [&](int e) -> u32x4 {
+                int hp, c;
+                const int off = where(e, hp, c);
+                return u32x4{(uint32_t)a.x[(c0 + c) * a.xs + (off >= 0 ? off : 0)], 0u, 0u, 0u};
+              },
+              [&](int e, u32x4 val) {
+                int hp, c;
+                const int off = where(e, hp, c);
+                halo[hp * CKP + c] = off >= 0 ? (uint16_t)val[0] : (uint16_t)0;
+              });
+        }
+      }
+
+      // ---- global -> LDS: this chunk's weight fragments, [block][step], ----
+      // one KiB fragment per wave instruction.
+      {
+        const int steps = VEC ? T * (CK / 16) : (T * cc + 15) / 16;
+        for (int f = wave; f < NBT * steps; f += 4) {
+          const int jn = f / steps, s = f - jn * steps;
+          int kb = s;  // one chunk holds all channels: fragments in order
+          if (VEC) {
+            const int tap = s / (CK / 16), kc = s % (CK / 16);
+            kb = tap * (a.C / 16) + c0 / 16 + kc;
+          }
+          dma16(a.wp + ((nblk_tile + jn) * a.KB + kb) * 512 + lane * 8,
+                bl + (jn * KSTEPS + s) * 512);
+        }
+      }
+      __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): the direct-to-LDS loads have landed
+      __syncthreads();
+
+      compute(lds_raw, cc);
     }
   }
 
@@ -706,21 +781,49 @@ static ien_status run_cfg(ien_ctx *ctx, ConvArgs a) {
   const int pitch = a.tiles_n * Cfg::BN;
   const int T = KS == 0 ? a.noff : KS * KS;
   const int min_chunks = (512 + T * CK - 1) / (T * CK);
+  // Double-buffered chunks when the tiles (and their splits) fill the CUs
+  // at most once: then no other workgroup hides a chunk's load latency.
+  // Each split keeps at least two chunks to overlap; the buffer loads take
+  // 32-bit byte offsets.  Not for offset taps (the transposed phases ran
+  // slower double-buffered: 36 -> 44 and 23 -> 35 us at LaMa's first two
+  // upsamplings), nor when the context asks for compact launches.
+  bool db = false;
+  if constexpr (Cfg::DMA && KS > 0) {
+    if constexpr (ConvCfg<KS, S, TR, TC, MSPLIT, NBW, CK, VEC, IN_NCHW, true>::FITS) {
+      const long in_bytes = (a.rows_mode ? (long)a.M : (long)a.H * a.W) * a.xs * 2;
+      db = !ctx->compact && blocks <= ctx->cus && chunks >= 2 && in_bytes < (1L << 31) &&
+           (long)a.NB * a.KB * 1024 < (1L << 31);
+    }
+  }
   int ksplit = 1;
   const bool idle = 4 * blocks <= ctx->cus || (KS == 1 && T * a.C >= 1536 && blocks < ctx->cus);
   if (VEC && chunks >= 2 * min_chunks && idle) {
     ksplit = (int)std::min<long>(chunks / min_chunks, (2L * ctx->cus + blocks - 1) / blocks);
+    if (db) ksplit = (int)std::min<long>({(long)ksplit, ctx->cus / blocks, chunks / 2L});
+    ksplit = std::max(ksplit, 1);
     while (ksplit > 1 && (size_t)ksplit * rows * pitch > ctx->splitk_floats) ksplit--;
   }
   a.kchunks = (chunks + ksplit - 1) / ksplit;
   a.ksplit = (chunks + a.kchunks - 1) / a.kchunks;
+  auto launch = [&](const ConvArgs &la, dim3 grid) -> ien_status {
+    if constexpr (Cfg::DMA && KS > 0 &&
+                  ConvCfg<KS, S, TR, TC, MSPLIT, NBW, CK, VEC, IN_NCHW, true>::FITS) {
+      if (db) {
+        hipLaunchKernelGGL((conv_mfma<KS, S, TR, TC, MSPLIT, NBW, CK, VEC, IN_NCHW, true>), grid,
+                           dim3(256), 0, ctx->stream, la);
+        IEN_HIP(hipGetLastError());
+        return IEN_OK;
+      }
+    }
+    hipLaunchKernelGGL((conv_mfma<KS, S, TR, TC, MSPLIT, NBW, CK, VEC, IN_NCHW>), grid, dim3(256),
+                       0, ctx->stream, la);
+    IEN_HIP(hipGetLastError());
+    return IEN_OK;
+  };
   if (a.ksplit <= 1) {
     a.ksplit = 1;
     a.kchunks = chunks;
-    hipLaunchKernelGGL((conv_mfma<KS, S, TR, TC, MSPLIT, NBW, CK, VEC, IN_NCHW>),
-                       dim3((unsigned)blocks), dim3(256), 0, ctx->stream, a);
-    IEN_HIP(hipGetLastError());
-    return IEN_OK;
+    return launch(a, dim3((unsigned)blocks));
   }
   ConvArgs pa = a;
   pa.y = ctx->splitk;
@@ -729,9 +832,8 @@ static ien_status run_cfg(ien_ctx *ctx, ConvArgs a) {
   pa.out_nchw = 0;
   pa.act = IEN_ACT_NONE;
   pa.accumulate = 0;
-  hipLaunchKernelGGL((conv_mfma<KS, S, TR, TC, MSPLIT, NBW, CK, VEC, IN_NCHW>),
-                     dim3((unsigned)blocks, (unsigned)a.ksplit), dim3(256), 0, ctx->stream, pa);
-  IEN_HIP(hipGetLastError());
+  const ien_status st = launch(pa, dim3((unsigned)blocks, (unsigned)a.ksplit));
+  if (st != IEN_OK) return st;
   return splitk_finish(ctx, a.ksplit, rows, pitch, a);
 }
 

@@ -142,6 +142,17 @@ __device__ __forceinline__ int4v buffer_rsrc(const void *p, long bytes) {
   return r;
 }
 
+// The same, read from lane 0: for callers whose pointer and size the
+// compiler cannot prove uniform, so that the inline assembly below gets the
+// resource in SGPRs.
+__device__ __forceinline__ int4v uniform_rsrc(const void *p, long bytes) {
+  int4v r = buffer_rsrc(p, bytes);
+  r.x = __builtin_amdgcn_readfirstlane(r.x);
+  r.y = __builtin_amdgcn_readfirstlane(r.y);
+  r.z = __builtin_amdgcn_readfirstlane(r.z);
+  return r;
+}
+
 // LDS byte address of a pointer into __shared__ memory.
 __device__ __forceinline__ unsigned lds_addr(const void *p) {
   return (unsigned)(uintptr_t)(const __attribute__((address_space(3))) void *)p;

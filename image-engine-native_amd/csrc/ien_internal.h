@@ -54,6 +54,10 @@ struct ien_ctx {
   hipStream_t branch[BRANCHES] = {};
   float *branch_splitk[BRANCHES] = {};
   hipEvent_t fork_ev = nullptr, join_ev[BRANCHES] = {};
+  // Convolutions keep a single chunk buffer in LDS (no double-buffered
+  // chunks): set by a driver around work that runs beside LDS-hungry
+  // kernels of another branch.
+  bool compact = false;
 };
 
 // Packed weights (gemm.rs Matrix): k x n padded to whole 16 x 32 MFMA

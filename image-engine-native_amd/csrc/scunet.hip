@@ -143,9 +143,13 @@ ien_status run_level(Scunet &s, ScunetBlock *blocks, int h, int w, int c, hipEve
     if (st == IEN_OK) {
       Branch br(ctx, 1);
       // network.rs:135-153 convolve: conv3 + ReLU into t, conv3 added back.
+      // Single-buffered: double-buffered chunks (one workgroup of 104 KiB
+      // LDS a CU) crowded out the Swin half's kernels (1% slower per image).
+      ctx->compact = true;
       st = conv3(ctx, s.y, h, w, (int)half, c, B.conv1, s.t, (long)half, IEN_ACT_RELU, 0);
       if (st == IEN_OK)
         st = conv3(ctx, s.t, h, w, (int)half, (long)half, B.conv2, s.y, c, IEN_ACT_NONE, 1);
+      ctx->compact = false;
     }
     if (st == IEN_OK) st = ien_swin_run(B.swin, s.y + half, c, h, w);
     if (st == IEN_OK) st = join_branches(ctx, 1);

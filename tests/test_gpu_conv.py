@@ -99,6 +99,14 @@ def test_conv3x3_nhwc(ctx, oracle, h, w, c, n):
     close(run_gpu(ctx, x, wt, b), want_cpu(oracle, x, wt, b))
 
 
+# Launches that fill the CUs at most once stage their channel chunks
+# double-buffered (the small cases above); a grid of 384 tiles takes the
+# single-buffered kernel.
+def test_conv3x3_large_grid(ctx, oracle):
+    x, wt, b = case(12, 128, 192, 128, 128, 9)
+    close(run_gpu(ctx, x, wt, b, pad=1), want_cpu(oracle, x, wt, b, pad=1))
+
+
 @pytest.mark.parametrize("c", [3, 4, 8, 16])
 def test_conv3x3_few_channels(ctx, oracle, c):
     x, wt, b = case(2, 11, 37, c, 64, 9)
