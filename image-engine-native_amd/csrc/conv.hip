@@ -76,10 +76,16 @@ struct ConvCfg {
   static constexpr int BUFS = DB ? 2 : 1;
   static constexpr int LDS_BYTES =
       BUFS * MAIN_BYTES > 4 * STAGE * 4 ? BUFS * MAIN_BYTES : 4 * STAGE * 4;
-  // Loads per wave and chunk (DB): the halo's KiBs and the fragments.
-  static constexpr int DW = DB ? HALO_BYTES / 4096 + BFRAGS / 4 : 0;
-  // (Double buffering stages through direct-to-LDS loads only.)
-  static constexpr bool FITS = (!DB || DMA) && LDS_BYTES <= 160 * 1024 && DW < 64;
+  // Direct-to-LDS loads per wave and chunk (DB): the halo's KiBs (NHWC)
+  // and the fragments.
+  static constexpr int DW = DB ? (DMA ? HALO_BYTES / 4096 : 0) + BFRAGS / 4 : 0;
+  // NCHW (DB): 16-byte groups of 8 pixels of one channel row a chunk's halo
+  // spans, and per thread.
+  static constexpr int NGROUPS = CK * HR * ((HC + 14) / 8);
+  static constexpr int NITEMS = (NGROUPS + 255) / 256;
+  // (Double buffering takes 16-channel steps: NHWC through direct-to-LDS
+  // loads, NCHW through registers.)
+  static constexpr bool FITS = (!DB || VEC) && LDS_BYTES <= 160 * 1024 && DW < 64;
   static_assert(MB % MSPLIT == 0, "M-blocks must split evenly over waves");
   static_assert(TC % 32 == 0, "tile columns are whole M-blocks");
   static_assert(!VEC || CK % 16 == 0, "16-channel steps");
@@ -266,7 +272,89 @@ __global__ __launch_bounds__(256) void conv_mfma(ConvArgs a) {
     }
   };
 
-  if constexpr (DB) {
+  if constexpr (DB && !Cfg::DMA) {
+    // Double-buffered NCHW chunks (zero padding, rows of whole 16-byte
+    // groups): chunk i + 1's halo groups are loaded into registers and its
+    // fragments straight into the other LDS buffer while chunk i is
+    // multiplied; the groups are written (transposed to pixel-major) after
+    // the products, then one barrier.
+    constexpr int OOB = 0x7ffffff0;
+    const int4v wrs = uniform_rsrc(a.wp, (long)a.NB * a.KB * 1024);
+    const unsigned lds0 = lds_addr(lds_raw);
+    auto floor8 = [](int v) { return v >= 0 ? v / 8 : -((7 - v) / 8); };
+    const int g0 = floor8(ix0);
+    const int groups = floor8(ix0 + HC - 1) + 1 - g0;
+    const int items = CK * HR * groups;  // <= Cfg::NGROUPS
+    auto where = [&](int e, int &hy, int &c, int &gx) {
+      const int g = e % groups, rest = e / groups;
+      hy = rest % HR;
+      c = rest / HR;
+      gx = (g0 + g) * 8;
+      const int iy = iy0 + hy;
+      return e < items && iy >= 0 && iy < a.H && gx >= 0 && gx < a.W;
+    };
+    u32x4 hv[Cfg::NITEMS];
+    auto load_groups = [&](int c0) {
+#pragma unroll
+      for (int j = 0; j < Cfg::NITEMS; j++) {
+        int hy, c, gx;
+        const bool ok = where(tid + 256 * j, hy, c, gx);
+        hv[j] = *(const u32x4 *)(a.x + (ok ? (c0 + c) * a.xs + (iy0 + hy) * a.W + gx : 0));
+      }
+    };
+    auto store_groups = [&](unsigned char *base) {
+      uint16_t *hl = (uint16_t *)base;
+#pragma unroll
+      for (int j = 0; j < Cfg::NITEMS; j++) {
+        const int e = tid + 256 * j;
+        if (e >= items) break;
+        int hy, c, gx;
+        const bool ok = where(e, hy, c, gx);
+        uint16_t v8[8];
+        const u32x4 val = ok ? hv[j] : u32x4{0u, 0u, 0u, 0u};
+        __builtin_memcpy(v8, &val, 16);
+#pragma unroll
+        for (int q = 0; q < 8; q++) {
+          const int hx = gx + q - ix0;
+          if (hx >= 0 && hx < HC) hl[(hy * HC + hx) * CKP + c] = v8[q];
+        }
+      }
+    };
+    auto issue_weights = [&](int c0, int buf) {
+      const unsigned bb = lds0 + buf * Cfg::MAIN_BYTES + Cfg::HALO_BYTES;
+#pragma unroll
+      for (int fi = 0; fi < Cfg::BFRAGS / 4; fi++) {
+        const int f = wave + 4 * fi;
+        const int jn = f / KSTEPS, st = f - jn * KSTEPS;
+        int off = OOB;
+        if (jn < NBT) {
+          const int tap = st / (CK / 16), kc = st % (CK / 16);
+          const int kb = tap * (a.C / 16) + c0 / 16 + kc;
+          off = (((nblk_tile + jn) * a.KB + kb) * 512 + lane * 8) * 2;
+        }
+        dma_lds(wrs, __builtin_amdgcn_readfirstlane(bb + f * 1024), off);
+      }
+    };
+    if (c_begin < c_end) {
+      load_groups(c_begin);
+      issue_weights(c_begin, 0);
+      store_groups(lds_raw);
+      wait_vm<0>();
+      __syncthreads();
+    }
+    int i = 0;
+    for (int c0 = c_begin; c0 < c_end; c0 += CK, i++) {
+      const bool next = c0 + CK < c_end;  // uniform
+      if (next) {
+        load_groups(c0 + CK);
+        issue_weights(c0 + CK, (i + 1) & 1);
+      }
+      compute(lds_raw + (i & 1) * Cfg::MAIN_BYTES, CK);
+      if (next) store_groups(lds_raw + ((i + 1) & 1) * Cfg::MAIN_BYTES);
+      wait_vm<0>();     // chunk i + 1's fragments
+      __syncthreads();  // chunk i + 1 is in; every wave is done with buffer i % 2
+    }
+  } else if constexpr (DB) {
     // Double-buffered chunks: chunk i + 1's halo and fragments are loaded
     // (straight into the other LDS buffer, by loads the compiler does not
     // see) while chunk i is multiplied; a wait for the chunk's own loads
@@ -697,6 +785,98 @@ __global__ __launch_bounds__(256) void k_splitk_finish(const float *__restrict__
   }
 }
 
+// The same for NCHW outputs: a workgroup sums 32 pixels x 32 channels
+// (reading the partial sums along channels, the 4 loads of a split issued
+// together from valid addresses), transposes them through LDS and writes 4
+// consecutive pixels of one channel per thread (8 or 16 bytes when
+// aligned).
+__global__ __launch_bounds__(256) void k_splitk_finish_nchw(const float *__restrict__ part,
+                                                            int ksplit, long rows, int pitch, int N,
+                                                            const float *__restrict__ bias,
+                                                            const float *__restrict__ slope,
+                                                            int act, int accumulate, void *y,
+                                                            long ys, int out_f32) {
+  __shared__ float tile[32][32 + 1];
+  const long p0 = (long)blockIdx.x * 32;
+  const int n0 = blockIdx.y * 32, tid = threadIdx.x;
+  // Sum: thread (pixel group pg, channel nn): pixels pg + 8 k, channel n0 + nn.
+  const int nn = tid & 31, pg = tid >> 5;
+  long at_in[4];
+  bool ok[4];
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    const long p = p0 + pg + 8 * k;
+    ok[k] = p < rows && n0 + nn < N;
+    at_in[k] = ok[k] ? p * pitch + n0 + nn : 0;
+  }
+  float sum[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int z = 0; z < ksplit; z++) {
+    const float *pz = part + (long)z * rows * pitch;
+    float v[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) v[k] = pz[at_in[k]];
+#pragma unroll
+    for (int k = 0; k < 4; k++) sum[k] += v[k];
+  }
+#pragma unroll
+  for (int k = 0; k < 4; k++) tile[nn][pg + 8 * k] = ok[k] ? sum[k] : 0.0f;
+  __syncthreads();
+  // Write: thread (channel row r, 4-pixel chunk q).
+  const int r = tid >> 3, q = (tid & 7) * 4, n = n0 + r;
+  if (n >= N) return;
+  const float b = bias[n], sl = act == IEN_ACT_PRELU ? slope[n] : 0.0f;
+  const long at = (long)n * ys + p0 + q;
+  const bool whole = p0 + q + 4 <= rows;
+  float v[4], old[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int e = 0; e < 4; e++) v[e] = tile[r][q + e] + b;
+  if (out_f32) {
+    float *yo = (float *)y + at;
+    const bool vec = whole && ((((uintptr_t)yo) & 15) == 0);
+    if (accumulate) {
+      if (vec) {
+        const float4v o = *(const float4v *)yo;
+#pragma unroll
+        for (int e = 0; e < 4; e++) old[e] = o[e];
+      } else {
+        for (int e = 0; e < 4; e++) old[e] = p0 + q + e < rows ? yo[e] : 0.0f;
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 4; e++) v[e] = activate(accumulate ? v[e] + old[e] : v[e], act, sl);
+    if (vec) {
+      *(float4v *)yo = float4v{v[0], v[1], v[2], v[3]};
+    } else {
+      for (int e = 0; e < 4; e++)
+        if (p0 + q + e < rows) yo[e] = v[e];
+    }
+  } else {
+    uint16_t *yo = (uint16_t *)y + at;
+    const bool vec = whole && ((((uintptr_t)yo) & 7) == 0);
+    uint16_t h[4];
+    if (accumulate) {
+      if (vec) {
+        const uint2 o = *(const uint2 *)yo;
+        __builtin_memcpy(h, &o, 8);
+      } else {
+        for (int e = 0; e < 4; e++) h[e] = p0 + q + e < rows ? yo[e] : (uint16_t)0;
+      }
+#pragma unroll
+      for (int e = 0; e < 4; e++) old[e] = h2f(h[e]);
+    }
+#pragma unroll
+    for (int e = 0; e < 4; e++) h[e] = f2h(activate(accumulate ? v[e] + old[e] : v[e], act, sl));
+    if (vec) {
+      uint2 o;
+      __builtin_memcpy(&o, h, 8);
+      *(uint2 *)yo = o;
+    } else {
+      for (int e = 0; e < 4; e++)
+        if (p0 + q + e < rows) yo[e] = h[e];
+    }
+  }
+}
+
 // The same for f16 NHWC outputs with 8-aligned widths and strides: 8
 // channels per thread, 16-byte loads and stores, one loop per activation.
 __global__ __launch_bounds__(256) void k_splitk_finish8(const float *__restrict__ part, int ksplit,
@@ -745,6 +925,11 @@ ien_status splitk_finish(ien_ctx *ctx, int ksplit, long rows, int pitch, const C
     hipLaunchKernelGGL(k_splitk_finish8, dim3((unsigned)((items + 255) / 256)), dim3(256), 0,
                        ctx->stream, (const float *)ctx->splitk, ksplit, rows, pitch, a.N, a.bias,
                        a.slope, a.act, a.accumulate, (uint16_t *)a.y, (long)a.ys);
+  } else if (a.out_nchw) {
+    const dim3 grid((unsigned)((rows + 31) / 32), (unsigned)((a.N + 31) / 32));
+    hipLaunchKernelGGL(k_splitk_finish_nchw, grid, dim3(256), 0, ctx->stream,
+                       (const float *)ctx->splitk, ksplit, rows, pitch, a.N, a.bias, a.slope, a.act,
+                       a.accumulate, a.y, (long)a.ys, a.out_f32);
   } else {
     const long items = rows * a.N;
     hipLaunchKernelGGL(k_splitk_finish, dim3((unsigned)((items + 255) / 256)), dim3(256), 0,
@@ -788,11 +973,15 @@ static ien_status run_cfg(ien_ctx *ctx, ConvArgs a) {
   // slower double-buffered: 36 -> 44 and 23 -> 35 us at LaMa's first two
   // upsamplings), nor when the context asks for compact launches.
   bool db = false;
-  if constexpr (Cfg::DMA && KS > 0) {
+  if constexpr (VEC && KS > 0) {
     if constexpr (ConvCfg<KS, S, TR, TC, MSPLIT, NBW, CK, VEC, IN_NCHW, true>::FITS) {
       const long in_bytes = (a.rows_mode ? (long)a.M : (long)a.H * a.W) * a.xs * 2;
-      db = !ctx->compact && blocks <= ctx->cus && chunks >= 2 && in_bytes < (1L << 31) &&
-           (long)a.NB * a.KB * 1024 < (1L << 31);
+      // NCHW: the fast halo path only (zero padding, whole 16-byte groups).
+      const bool layout_ok =
+          !IN_NCHW || (!a.rows_mode && !a.pad_reflect && (a.W & 7) == 0 && (a.xs & 7) == 0 &&
+                       (((uintptr_t)a.x) & 15) == 0);
+      db = layout_ok && !ctx->compact && blocks <= ctx->cus && chunks >= 2 &&
+           (IN_NCHW || in_bytes < (1L << 31)) && (long)a.NB * a.KB * 1024 < (1L << 31);
     }
   }
   int ksplit = 1;
@@ -806,7 +995,7 @@ static ien_status run_cfg(ien_ctx *ctx, ConvArgs a) {
   a.kchunks = (chunks + ksplit - 1) / ksplit;
   a.ksplit = (chunks + a.kchunks - 1) / a.kchunks;
   auto launch = [&](const ConvArgs &la, dim3 grid) -> ien_status {
-    if constexpr (Cfg::DMA && KS > 0 &&
+    if constexpr (VEC && KS > 0 &&
                   ConvCfg<KS, S, TR, TC, MSPLIT, NBW, CK, VEC, IN_NCHW, true>::FITS) {
       if (db) {
         hipLaunchKernelGGL((conv_mfma<KS, S, TR, TC, MSPLIT, NBW, CK, VEC, IN_NCHW, true>), grid,

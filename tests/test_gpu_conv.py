@@ -149,6 +149,15 @@ def test_nchw_in_and_out(ctx, oracle):
     close(run_gpu(ctx, x, wt, b, nchw_in=True, nchw_out=True, out_f32=True), want, f32=False)
 
 
+# NCHW 1 x 1 (the conv sweep's 256 -> 512): four 64-channel chunks over 64
+# tiles, double-buffered through registers; NCHW and NHWC outputs.
+def test_nchw_1x1(ctx, oracle):
+    x, wt, b = case(13, 16, 64, 256, 512, 1)
+    want = want_cpu(oracle, x, wt, b, size=1)
+    close(run_gpu(ctx, x, wt, b, size=1, nchw_in=True, nchw_out=True), want)
+    close(run_gpu(ctx, x, wt, b, size=1, nchw_in=True), want)
+
+
 def test_f32_output_and_strides(ctx, oracle):
     x, wt, b = case(5, 9, 50, 32, 40, 9)
     want = want_cpu(oracle, x, wt, b)
@@ -322,6 +331,21 @@ def test_splitk_nchw_f32_reflect_rows(ctx, oracle):
     close(run_gpu(ctx, x, wt, b, out_f32=True, stride_pad=8), want, f32=True)
     close(run_gpu(ctx, x, wt, b, pad=1), want_cpu(oracle, x, wt, b, pad=1))
     close(run_gpu(ctx, x, wt, b, row0=37, rows=150), want[37:187])
+
+
+# The NCHW finishing pass (32 pixels x 32 channels a workgroup, transposed
+# through LDS): ragged pixel blocks and channel groups, accumulating, f16
+# and f32 outputs.
+@pytest.mark.parametrize("f32", [False, True])
+def test_splitk_nchw_out_accumulate(ctx, oracle, f32):
+    import ien
+
+    x, wt, b = case(19, 7, 30, 512, 80, 9)
+    slope = np.linspace(-0.2, 0.4, 80).astype(np.float32)
+    init = f16(np.random.default_rng(20).standard_normal((7 * 30, 80)))
+    got = run_gpu(ctx, x, wt, b, act=ien.ACT_PRELU, slope=slope, init=init, nchw_in=True,
+                  nchw_out=True, out_f32=f32)
+    close(got, want_cpu(oracle, x, wt, b, act=ien.ACT_PRELU, slope=slope, init=init))
 
 
 def test_splitk_offsets_and_rows(ctx, oracle):
