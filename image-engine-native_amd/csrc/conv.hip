@@ -980,7 +980,9 @@ static ien_status run_cfg(ien_ctx *ctx, ConvArgs a) {
       const bool layout_ok =
           !IN_NCHW || (!a.rows_mode && !a.pad_reflect && (a.W & 7) == 0 && (a.xs & 7) == 0 &&
                        (((uintptr_t)a.x) & 15) == 0);
-      db = layout_ok && !ctx->compact && blocks <= ctx->cus && chunks >= 2 &&
+      constexpr int FIT =
+          160 * 1024 / ConvCfg<KS, S, TR, TC, MSPLIT, NBW, CK, VEC, IN_NCHW, true>::LDS_BYTES;
+      db = layout_ok && !ctx->compact && blocks <= (long)ctx->cus * FIT && chunks >= 2 &&
            (IN_NCHW || in_bytes < (1L << 31)) && (long)a.NB * a.KB * 1024 < (1L << 31);
     }
   }
@@ -1129,6 +1131,13 @@ ien_status launch_conv(ien_ctx *ctx, const ConvCall &c) {
     // NCHW likewise (the conv sweep: 3x3 64 at 256 x 384 25.4 -> 22.5 us,
     // 128 at 128 x 192 38.1 -> 27.1 us, 512 at 32 x 32 35.7 -> 25.9 us).
     if (ck == 64) {
+      // Between one and two tiles a CU: 16-channel chunks, double-buffered
+      // two workgroups a CU.
+      const long tiles = (long)((c.OH + 3) / 4) * ((c.OW + 31) / 32) * ((w->n + 63) / 64);
+      if (tiles > ctx->cus && tiles <= 2L * ctx->cus && !ctx->compact) {
+        if (nchw) return run_cfg<3, 1, 4, 32, 4, 2, 16, true, true>(ctx, a);
+        return run_cfg<3, 1, 4, 32, 4, 2, 16, true, false>(ctx, a);
+      }
       if (nchw) return run_cfg<3, 1, 4, 32, 4, 2, 32, true, true>(ctx, a);
       return run_cfg<3, 1, 4, 32, 4, 2, 32, true, false>(ctx, a);
     }
