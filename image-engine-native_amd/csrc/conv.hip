@@ -93,6 +93,17 @@ struct ConvCfg {
   static_assert(DB || LDS_BYTES <= 160 * 1024, "LDS budget");
 };
 
+// Offset tap t (< 4; offsets of 0 or 1 pixel, as launch_conv checks) from
+// bit masks built with constant indices: indexing the argument arrays at
+// run time (or selects the compiler turns back into such indexing) copies
+// the whole argument block to scratch memory.
+__device__ __forceinline__ void offset_tap(const ConvArgs &a, int t, int &dy, int &dx) {
+  const int ybits = a.offy[0] | a.offy[1] << 1 | a.offy[2] << 2 | a.offy[3] << 3;
+  const int xbits = a.offx[0] | a.offx[1] << 1 | a.offx[2] << 2 | a.offx[3] << 3;
+  dy = (ybits >> t) & 1;
+  dx = (xbits >> t) & 1;
+}
+
 // Swizzled chunk slot of 16-byte chunk c of DMA halo pixel p.
 template <class Cfg>
 __device__ __forceinline__ int swz_slot(int p, int c) {
@@ -229,7 +240,9 @@ __global__ __launch_bounds__(256) void conv_mfma(ConvArgs a) {
         const int c = 2 * kc + (lane >> 5);
 #pragma unroll
         for (int i = 0; i < MBW; i++) {
-          const int p = apix[i] + a.offy[tap] * HC + a.offx[tap];
+          int ody, odx;
+          offset_tap(a, tap, ody, odx);
+          const int p = apix[i] + ody * HC + odx;
           av[i] = *(const half8 *)(base + p * Cfg::PB + 16 * swz_slot<Cfg>(p, c));
         }
 #pragma unroll
@@ -252,8 +265,7 @@ __global__ __launch_bounds__(256) void conv_mfma(ConvArgs a) {
           const int tap = kk / cc, c = kk - tap * cc;
           int dy, dx;
           if constexpr (KS == 0) {
-            dy = a.offy[tap];
-            dx = a.offx[tap];
+            offset_tap(a, tap, dy, dx);
           } else {
             dy = tap / KS;
             dx = tap - dy * KS;

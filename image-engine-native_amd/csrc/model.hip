@@ -14,6 +14,7 @@
 // SCUNet, LaMa and BiRefNet are objects of their own (scunet.hip, lama.hip,
 // birefnet.hip) that this file loads, sizes and runs the same way.
 
+#include <algorithm>
 #include <cstring>
 #include <fstream>
 #include <functional>
@@ -188,7 +189,10 @@ static ien_status ensure_maps(ien_model *model, size_t pixels, bool host_staging
   if (m.pixels < pixels) {
     drop_graph(model);
     free_maps(m);
-    IEN_HIP(hipMalloc(&m.image, pixels * 3 * 2));
+    // The f16 image, 4 halves a pixel: the fourth stays zero (the first
+    // layer reads 4 channels).
+    IEN_HIP(hipMalloc(&m.image, pixels * 4 * 2));
+    IEN_HIP(hipMemsetAsync(m.image, 0, pixels * 4 * 2, model->ctx->stream));
     IEN_HIP(hipMalloc(&m.a, pixels * FEATURES * 2));
     IEN_HIP(hipMalloc(&m.b, pixels * FEATURES * 2));
     m.pixels = pixels;
@@ -215,7 +219,18 @@ static ien_status load_esrgan(ien_model *model, const TensorSource &take) {
     EsrganLayer layer;
     layer.cin = cin;
     layer.cout = cout;
-    st = ien_matrix_new(model->ctx, w.data(), IEN_W_F32, 9 * cin, cout, b.data(), &layer.conv);
+    if (i == 0) {
+      // The image map has 4 channels (the fourth zero): a zero weight row
+      // after each tap's 3, so that K = 9 x 4 runs on the four-channel kernel.
+      std::vector<float> w4((size_t)36 * cout, 0.0f);
+      for (int t = 0; t < 9; t++)
+        for (int c = 0; c < 3; c++)
+          std::copy_n(&w[(size_t)(t * 3 + c) * cout], cout, &w4[(size_t)(t * 4 + c) * cout]);
+      w.swap(w4);
+      layer.cin = 4;
+    }
+    st = ien_matrix_new(model->ctx, w.data(), IEN_W_F32, 9 * layer.cin, cout, b.data(),
+                        &layer.conv);
     if (st != IEN_OK) return st;
     model->layers.push_back(layer);
     if (!last) {
@@ -236,7 +251,8 @@ static ien_status enqueue_esrgan(ien_model *model, const float *d_image, size_t 
   ien_ctx *ctx = model->ctx;
   Maps &m = model->maps;
   const size_t pixels = width * height;
-  ien_status st = ien_floats_to_halves(ctx, d_image, m.image, pixels * 3);
+  ien_status st = ien_pad_image(ctx, IEN_PAD_REPLICATE, d_image, nullptr, width, height, 1,
+                                m.image, 4);
   if (st != IEN_OK) return st;
   for (int i = 0; i < STEPS; i++) {
     const EsrganLayer &l = model->layers[i];
