@@ -981,9 +981,9 @@ static ien_status run_cfg(ien_ctx *ctx, ConvArgs a) {
   // Double-buffered chunks when the tiles (and their splits) fill the CUs
   // at most once: then no other workgroup hides a chunk's load latency.
   // Each split keeps at least two chunks to overlap; the buffer loads take
-  // 32-bit byte offsets.  Not for offset taps (the transposed phases ran
-  // slower double-buffered: 36 -> 44 and 23 -> 35 us at LaMa's first two
-  // upsamplings), nor when the context asks for compact launches.
+  // 32-bit byte offsets.  Not for offset taps (LaMa's transposed phases:
+  // no gain, 3.25 against 3.23 ms per image), nor when the context asks for
+  // compact launches.
   bool db = false;
   if constexpr (VEC && KS > 0) {
     if constexpr (ConvCfg<KS, S, TR, TC, MSPLIT, NBW, CK, VEC, IN_NCHW, true>::FITS) {
