@@ -155,8 +155,18 @@ ien_status swin_mlp(ien_ctx *ctx, uint16_t *d_map, size_t stride, long rows, int
 // block by swin_attend_proj, its bias tables by pack_bias_tables.
 bool swin_attend_supported(int c, int window);
 std::vector<uint16_t> swin_attend_proj(const float *proj_w, int c);
+// The MLP half fused after the attention (c = 32): LayerNorm 2, the fc1
+// and fc2 A fragments from swin_attend_mlp (fc1's 8 KiB, then fc2's), the
+// biases (4c and c floats); all 16-byte aligned.
+struct AttendMlp {
+  const float *gamma, *beta;
+  const uint16_t *w;
+  const float *b1, *b2;
+};
+std::vector<uint16_t> swin_attend_mlp(const float *fc1_w, const float *fc2_w);
 ien_status swin_attend(ien_ctx *ctx, const ien_windows *win, uint16_t *d_map, size_t stride,
                        int c, const float *gamma, const float *beta, const ien_matrix *qkv,
-                       const uint16_t *d_proj, const float *bproj, const float *d_tables);
+                       const uint16_t *d_proj, const float *bproj, const float *d_tables,
+                       const AttendMlp *mlp = nullptr);
 
 }  // namespace ien

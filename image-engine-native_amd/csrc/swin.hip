@@ -16,6 +16,8 @@ struct ien_swin {
   // projection fragments (when it takes the block's width and window).
   float *d_packed = nullptr;
   uint16_t *d_attn_proj = nullptr;
+  // At 32 channels: the fc1 / fc2 fragments of the MLP fused after it.
+  uint16_t *d_attn_mlp = nullptr;
   ien_matrix *qkv = nullptr, *proj = nullptr, *fc1 = nullptr, *fc2 = nullptr;
   // Scratch: `rows` window rows (at least the map's tokens) of 4c, c, c.
   uint16_t *d_wide = nullptr, *d_tok = nullptr, *d_att = nullptr;
@@ -33,6 +35,7 @@ void release(ien_swin *b) {
   (void)hipFree(b->d_ln);
   (void)hipFree(b->d_packed);
   (void)hipFree(b->d_attn_proj);
+  (void)hipFree(b->d_attn_mlp);
   (void)hipFree(b->d_wide);
   (void)hipFree(b->d_tok);
   (void)hipFree(b->d_att);
@@ -141,6 +144,12 @@ ien_status ien_swin_new(ien_ctx *ctx, const ien_swin_weights *w, ien_swin **out)
     e = hipMalloc((void **)&b->d_attn_proj, proj.size() * 2);
     if (e == hipSuccess)
       e = hipMemcpy(b->d_attn_proj, proj.data(), proj.size() * 2, hipMemcpyHostToDevice);
+    if (e == hipSuccess && W.c == 32) {
+      const std::vector<uint16_t> mlp = swin_attend_mlp(W.fc1_w, W.fc2_w);
+      e = hipMalloc((void **)&b->d_attn_mlp, mlp.size() * 2);
+      if (e == hipSuccess)
+        e = hipMemcpy(b->d_attn_mlp, mlp.data(), mlp.size() * 2, hipMemcpyHostToDevice);
+    }
   }
   if (e != hipSuccess) {
     release(b);
@@ -173,6 +182,12 @@ ien_status ien_swin_run(ien_swin *b, uint16_t *d_map, size_t stride, int height,
   // attend (scunet swin.rs:131-232): one fused pass per window where its
   // kernel takes the width and window, else the window rows, qkv,
   // attention, projection over the token rows, added back onto the map.
+  if (b->d_attn_mlp && rows16) {
+    // Both halves in one pass per window (32 channels).
+    const AttendMlp mlp{g2, b2, b->d_attn_mlp, b->fc1->d_bias, b->fc2->d_bias};
+    return swin_attend(ctx, &w, d_map, stride, b->c, g1, b1, b->qkv, b->d_attn_proj,
+                       b->proj->d_bias, b->d_packed, &mlp);
+  }
   if (b->d_attn_proj && rows16) {
     st = swin_attend(ctx, &w, d_map, stride, b->c, g1, b1, b->qkv, b->d_attn_proj,
                      b->proj->d_bias, b->d_packed);

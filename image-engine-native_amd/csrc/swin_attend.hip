@@ -31,6 +31,16 @@
 // f32; the result is rounded once after bias and residual.
 // One wave per window and head of 32 dims; with several heads the waves of
 // a window exchange their outputs through LDS before the projection.
+//
+// At c = 32 the block's MLP half (swin.rs:236-275) can follow in the same
+// wave: the result rounded to f16 (as the map would hold it) is
+// normalised per token (each lane holds 16 of its token's channels, the
+// lane l ^ 32 the other 16), and its registers are the permuted-k B
+// operand of H^T = W1^T x^T.  The fc1 accumulators, GELU'd and rounded to
+// f16, are in turn the permuted-k B operand of Z^T = W2^T H^T; both A
+// operands are packed on the host in those permuted orders.  The MLP is
+// per token and every token of the map lies in one window, so the fused
+// order gives the separate passes' results.
 
 #include "conv_common.h"
 #include "window_geo.h"
@@ -48,6 +58,11 @@ struct AttendArgs {
   const uint16_t *wproj;      // Wp^T A fragments [c / 32][heads][2][512]
   const float *bproj;         // c
   const float *bias;          // [class][head][query block][key block][4][64][4]
+  // The MLP half (c = 32): LayerNorm 2, permuted fc1 / fc2 A fragments
+  // [4 unit blocks][2 k steps][64 lanes][8], biases (4c, c).
+  const float *gamma2, *beta2;
+  const uint16_t *w1, *w2;
+  const float *b1, *b2;
 };
 
 __device__ __forceinline__ half8 frag(const uint16_t *p, int idx, int lane) {
@@ -238,8 +253,9 @@ __device__ __forceinline__ void head_attention(const AttendArgs &a, const half8 
 // heads' outputs in LDS (as the operands they are), meet at a barrier, and
 // wave h projects all heads onto output channels 32 h .. 32 h + 31; the
 // barrier also orders every read of the window before the first write.
-template <int C>
+template <int C, bool MLP>
 __global__ __launch_bounds__(256, C <= 64 ? 2 : 1) void k_swin_attend(AttendArgs a) {
+  static_assert(!MLP || C == 32, "the fused MLP takes one head");
   constexpr int H = C / 32, KS = C / 16, WPG = 4 / H;
   __shared__ half8 xo[H > 1 ? WPG * 2 * H * 2 * 64 : 1];  // [window][query block][head][s][lane]
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, hf = lane >> 5, l32 = lane & 31;
@@ -281,6 +297,109 @@ __global__ __launch_bounds__(256, C <= 64 ? 2 : 1) void k_swin_attend(AttendArgs
       }
   }
 
+  if constexpr (MLP) {
+    // x1 = the attention half's result, rounded as the map would hold it.
+    float x1[2][16];
+#pragma unroll
+    for (int qb = 0; qb < 2; qb++) {
+      const long t = src[qb];
+      const bool real = live && t >= 0;
+      const uint16_t *row = a.map + (real ? t : 0) * a.stride;
+#pragma unroll
+      for (int q4 = 0; q4 < 4; q4++) {
+        const int ch = 8 * q4 + 4 * hf;
+        const float4 bp = *(const float4 *)(a.bproj + ch);
+        const float bpa[4] = {bp.x, bp.y, bp.z, bp.w};
+        const uint2 old = real ? *(const uint2 *)(row + ch) : uint2{0u, 0u};
+        uint16_t hv[4];
+        __builtin_memcpy(hv, &old, 8);
+#pragma unroll
+        for (int e = 0; e < 4; e++) x1[qb][4 * q4 + e] = h2f(f2h(y[qb][4 * q4 + e] + bpa[e] + h2f(hv[e])));
+      }
+    }
+    // LayerNorm 2 per token; register 8 s + i is channel 16 s + 4 hf +
+    // (i & 3) + 8 (i >> 2): the permuted-k operand of fc1.
+    half8 xn[2][2];
+#pragma unroll
+    for (int qb = 0; qb < 2; qb++) {
+      float sum = 0.0f;
+#pragma unroll
+      for (int r = 0; r < 16; r++) sum += x1[qb][r];
+      sum += __shfl_xor(sum, 32);
+      const float mean = sum / 32.0f;
+      float sq = 0.0f;
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const float d = x1[qb][r] - mean;
+        sq += d * d;
+      }
+      sq += __shfl_xor(sq, 32);
+      const float inv = 1.0f / sqrtf(sq / 32.0f + 1e-5f);
+#pragma unroll
+      for (int q4 = 0; q4 < 4; q4++) {
+        const int ch = 8 * q4 + 4 * hf;
+        const float4 g = *(const float4 *)(a.gamma2 + ch);
+        const float4 b = *(const float4 *)(a.beta2 + ch);
+        const float ga[4] = {g.x, g.y, g.z, g.w}, ba[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          const int r = 4 * q4 + e;
+          xn[qb][r >> 3][r & 7] = (_Float16)((x1[qb][r] - mean) * inv * ga[e] + ba[e]);
+        }
+      }
+    }
+    // fc1 + GELU + fc2, 32 hidden units at a time.
+    floatx16 z[2] = {};
+#pragma unroll
+    for (int ub = 0; ub < 4; ub++) {
+      floatx16 hacc[2] = {};
+#pragma unroll
+      for (int s = 0; s < 2; s++) {
+        const half8 w1 = frag(a.w1, ub * 2 + s, lane);
+#pragma unroll
+        for (int qb = 0; qb < 2; qb++)
+          hacc[qb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(w1, xn[qb][s], hacc[qb], 0, 0, 0);
+      }
+#pragma unroll
+      for (int q4 = 0; q4 < 4; q4++) {
+        const float4 bu = *(const float4 *)(a.b1 + 32 * ub + 8 * q4 + 4 * hf);
+        const float bua[4] = {bu.x, bu.y, bu.z, bu.w};
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+#pragma unroll
+          for (int qb = 0; qb < 2; qb++)
+            hacc[qb][4 * q4 + e] = gelu_f(hacc[qb][4 * q4 + e] + bua[e]);
+      }
+#pragma unroll
+      for (int s = 0; s < 2; s++) {
+        const half8 w2 = frag(a.w2, ub * 2 + s, lane);
+#pragma unroll
+        for (int qb = 0; qb < 2; qb++)
+          z[qb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(w2, operand(hacc[qb], s, 1.0f), z[qb], 0, 0, 0);
+      }
+    }
+    // x1 + fc2 + bias, rounded once.
+#pragma unroll
+    for (int qb = 0; qb < 2; qb++) {
+      const long t = src[qb];
+      if (!live || t < 0) continue;
+      uint16_t *row = a.map + t * a.stride;
+#pragma unroll
+      for (int q4 = 0; q4 < 4; q4++) {
+        const int ch = 8 * q4 + 4 * hf;
+        const float4 bz = *(const float4 *)(a.b2 + ch);
+        const float bza[4] = {bz.x, bz.y, bz.z, bz.w};
+        uint16_t hv[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) hv[e] = f2h(x1[qb][4 * q4 + e] + (z[qb][4 * q4 + e] + bza[e]));
+        uint2 o;
+        __builtin_memcpy(&o, hv, 8);
+        *(uint2 *)(row + ch) = o;
+      }
+    }
+    return;
+  }
+
   // Bias, old token, rounded once; rows of Y^T are output channels.
 #pragma unroll
   for (int qb = 0; qb < 2; qb++) {
@@ -303,12 +422,12 @@ __global__ __launch_bounds__(256, C <= 64 ? 2 : 1) void k_swin_attend(AttendArgs
   }
 }
 
-template <int C>
+template <int C, bool MLP = false>
 ien_status launch(ien_ctx *ctx, const AttendArgs &a) {
   constexpr int WPG = 4 / (C / 32);
   const long blocks = (a.g.windows + WPG - 1) / WPG;
   IEN_CHECK(blocks < (1L << 31), IEN_ERR_INPUT, "%ld windows", a.g.windows);
-  hipLaunchKernelGGL(k_swin_attend<C>, dim3((unsigned)blocks), dim3(256), 0, ctx->stream, a);
+  hipLaunchKernelGGL((k_swin_attend<C, MLP>), dim3((unsigned)blocks), dim3(256), 0, ctx->stream, a);
   IEN_HIP(hipGetLastError());
   return IEN_OK;
 }
@@ -337,9 +456,31 @@ std::vector<uint16_t> swin_attend_proj(const float *proj_w, int c) {
   return out;
 }
 
+std::vector<uint16_t> swin_attend_mlp(const float *fc1_w, const float *fc2_w) {
+  // c = 32.  fc1 fragment (ub, s): lane l, slot i -> hidden unit 32 ub + l % 32,
+  // channel 16 s + 4 (l / 32) + (i & 3) + 8 (i >> 2); then fc2 fragment
+  // (ub, s): output channel l % 32, unit 32 ub + 16 s + 4 (l / 32) + (i & 3)
+  // + 8 (i >> 2).
+  constexpr int c = 32, units = 4 * c;
+  std::vector<uint16_t> out((size_t)2 * 8 * 512);
+  for (int ub = 0; ub < 4; ub++)
+    for (int s = 0; s < 2; s++)
+      for (int l = 0; l < 64; l++)
+        for (int i = 0; i < 8; i++) {
+          const int perm = 16 * s + 4 * (l / 32) + (i & 3) + 8 * (i >> 2);
+          const size_t at = (((size_t)(ub * 2 + s)) * 64 + l) * 8 + i;
+          const int unit1 = 32 * ub + l % 32, ch1 = perm;
+          out[at] = f32_to_half(fc1_w[(size_t)ch1 * units + unit1]);
+          const int ch2 = l % 32, unit2 = 32 * ub + perm;
+          out[8 * 512 + at] = f32_to_half(fc2_w[(size_t)unit2 * c + ch2]);
+        }
+  return out;
+}
+
 ien_status swin_attend(ien_ctx *ctx, const ien_windows *win, uint16_t *d_map, size_t stride,
                        int c, const float *gamma, const float *beta, const ien_matrix *qkv,
-                       const uint16_t *d_proj, const float *bproj, const float *d_tables) {
+                       const uint16_t *d_proj, const float *bproj, const float *d_tables,
+                       const AttendMlp *mlp) {
   IEN_CHECK(ctx && win && d_map && gamma && beta && qkv && d_proj && bproj && d_tables,
             IEN_ERR_INPUT, "null argument");
   WinGeo g;
@@ -352,8 +493,22 @@ ien_status swin_attend(ien_ctx *ctx, const ien_windows *win, uint16_t *d_map, si
             IEN_ERR_INPUT, "map stride %zu / alignment", stride);
   IEN_CHECK(qkv->k == (size_t)c && qkv->n == 3 * (size_t)c && qkv->kb == c / 16, IEN_ERR_INPUT,
             "qkv weights %zu x %zu for %d channels", qkv->k, qkv->n, c);
-  AttendArgs a{g, d_map, (long)stride, gamma, beta, qkv->d_packed, qkv->d_bias, d_proj, bproj,
-               d_tables};
+  AttendArgs a{g,      d_map,   (long)stride, gamma,   beta,    qkv->d_packed, qkv->d_bias,
+               d_proj, bproj,   d_tables,     nullptr, nullptr, nullptr,       nullptr,
+               nullptr, nullptr};
+  if (mlp) {
+    IEN_CHECK(c == 32 && mlp->gamma && mlp->beta && mlp->w && mlp->b1 && mlp->b2 &&
+                  aligned16(mlp->gamma) && aligned16(mlp->beta) && aligned16(mlp->b1) &&
+                  aligned16(mlp->b2),
+              IEN_ERR_INPUT, "fused MLP: 32 channels, aligned parameters");
+    a.gamma2 = mlp->gamma;
+    a.beta2 = mlp->beta;
+    a.w1 = mlp->w;
+    a.w2 = mlp->w + 8 * 512;
+    a.b1 = mlp->b1;
+    a.b2 = mlp->b2;
+    return launch<32, true>(ctx, a);
+  }
   switch (c) {
     case 32: return launch<32>(ctx, a);
     case 64: return launch<64>(ctx, a);
