@@ -91,31 +91,45 @@ __global__ __launch_bounds__(256) void k_pool_partial(const uint16_t *__restrict
 // Pass 2, one workgroup: the mean, the pooling product (64 -> 256) + ReLU,
 // and its share of conv1 (256 -> 64) plus conv1's bias: the bias every
 // pixel of conv1 gets (decoder.rs:150-170).  pool: [64][256] weight, [256]
-// bias, [256][64] conv1 rows, [64] conv1 bias.
+// bias, [256][64] conv1 rows, [64] conv1 bias.  The 64-wide sums are split
+// over the 4 lane groups (parts g, g + 4, ...; conv1 rows 64 g ..) and
+// combined in a fixed order, the loops unrolled so that loads go out in
+// batches.
 __global__ __launch_bounds__(256) void k_pool_finish(const float *__restrict__ partial, long rows,
                                                      const float *__restrict__ pool,
                                                      float *__restrict__ bias) {
+  static_assert(INTER == 64 && BRANCH == 256 && POOL_PARTS % 4 == 0, "pool shapes");
+  __shared__ double msum[4][INTER];
   __shared__ float mean[INTER];
   __shared__ float pooled[BRANCH];
-  const int tid = threadIdx.x;
-  if (tid < INTER) {
+  __shared__ float bsum[4][INTER];
+  const int tid = threadIdx.x, ch = tid % INTER, g = tid / INTER;
+  {
     double s = 0.0;
-    for (int b = 0; b < POOL_PARTS; b++) s += (double)partial[b * INTER + tid];
-    mean[tid] = (float)(s / (double)rows);
+#pragma unroll 16
+    for (int b = g; b < POOL_PARTS; b += 4) s += (double)partial[b * INTER + ch];
+    msum[g][ch] = s;
   }
+  __syncthreads();
+  if (tid < INTER)
+    mean[tid] = (float)((((msum[0][tid] + msum[1][tid]) + msum[2][tid]) + msum[3][tid]) / (double)rows);
   __syncthreads();
   const float *pw = pool, *pb = pool + INTER * BRANCH, *cw = pb + BRANCH, *cb = cw + BRANCH * INTER;
   {
     float p = pb[tid];
+#pragma unroll 16
     for (int c = 0; c < INTER; c++) p += mean[c] * pw[c * BRANCH + tid];
     pooled[tid] = p > 0.0f ? p : 0.0f;
   }
   __syncthreads();
-  if (tid < INTER) {
-    float b = cb[tid];
-    for (int j = 0; j < BRANCH; j++) b += pooled[j] * cw[j * INTER + tid];
-    bias[tid] = b;
+  {
+    float b = 0.0f;
+#pragma unroll 16
+    for (int j = INTER * g; j < INTER * g + INTER; j++) b += pooled[j] * cw[j * INTER + ch];
+    bsum[g][ch] = b;
   }
+  __syncthreads();
+  if (tid < INTER) bias[tid] = cb[tid] + (((bsum[0][tid] + bsum[1][tid]) + bsum[2][tid]) + bsum[3][tid]);
 }
 
 // Every row of a rows x 64 map set to the (f16-rounded) bias.
