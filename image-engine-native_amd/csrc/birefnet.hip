@@ -169,9 +169,14 @@ __global__ __launch_bounds__(256) void k_gate(uint16_t *__restrict__ out, long r
 
 // decoder.rs:546-577 image2patches: pixel (y, x) of the size x size stack,
 // channel (c grid + gy) grid + gx = image pixel (gy size + y, gx size + x),
-// colour c.
-__global__ __launch_bounds__(256) void k_image_patches(const uint16_t *__restrict__ img, int side,
-                                                       int size, uint16_t *__restrict__ out) {
+// colour c.  One thread per output element (any grid), or for grids of 4,
+// 8, 16 and 32 one thread per (gy, c, output pixel), pixels fastest: it reads
+// the GRID image pixels of its run (neighbouring threads read neighbouring
+// pixels) and writes the run's GRID consecutive channels as 16-byte (8 when
+// GRID is 4) stores.
+__global__ __launch_bounds__(256) void k_image_patches_any(const uint16_t *__restrict__ img,
+                                                           int side, int size,
+                                                           uint16_t *__restrict__ out) {
   const int grid = side / size, channels = 3 * grid * grid;
   const long i = (long)blockIdx.x * 256 + threadIdx.x;
   if (i >= (long)size * size * channels) return;
@@ -180,6 +185,36 @@ __global__ __launch_bounds__(256) void k_image_patches(const uint16_t *__restric
   const int y = (int)(p / size), x = (int)(p % size);
   const int c = ch / (grid * grid), gy = (ch / grid) % grid, gx = ch % grid;
   out[i] = img[((long)(gy * size + y) * side + gx * size + x) * 3 + c];
+}
+
+template <int GRID>
+__global__ __launch_bounds__(256) void k_image_patches(const uint16_t *__restrict__ img, int side,
+                                                       uint16_t *__restrict__ out) {
+  const int size = side / GRID, channels = 3 * GRID * GRID;
+  const long pixels = (long)size * size;
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= pixels * 3 * GRID) return;
+  const long p = i % pixels;
+  const int run = (int)(i / pixels), c = run / GRID, gy = run % GRID;
+  const int y = (int)(p / size), x = (int)(p % size);
+  const uint16_t *src = img + ((long)(gy * size + y) * side + x) * 3 + c;
+  uint16_t v[GRID];
+#pragma unroll
+  for (int gx = 0; gx < GRID; gx++) v[gx] = src[(long)gx * size * 3];
+  uint16_t *dst = out + p * channels + (c * GRID + gy) * GRID;
+  if constexpr (GRID % 8 == 0) {
+#pragma unroll
+    for (int q = 0; q < GRID / 8; q++) {
+      u32x4 o;
+      __builtin_memcpy(&o, v + 8 * q, 16);
+      *(u32x4 *)(dst + 8 * q) = o;
+    }
+  } else {
+    static_assert(GRID == 4, "runs of 4 or a multiple of 8");
+    uint2 o;
+    __builtin_memcpy(&o, v, 8);
+    *(uint2 *)dst = o;
+  }
 }
 
 // decoder.rs:737-757: head bias plus the composed 5x5 convolution of the f32
@@ -723,8 +758,22 @@ ien_status birefnet_enqueue(Birefnet *b, const float *d_image, size_t side_, flo
     // decoder.rs:535-591: the image as patches of g x g, both convolutions.
     if (st == IEN_OK) {
       const int gp = side / g;
-      hipLaunchKernelGGL(k_image_patches, dim3(blocks_for(pixels * 3 * gp * gp, 256)), dim3(256), 0,
-                         ctx->stream, b->img16, side, g, b->stacked);
+      const dim3 grid(blocks_for(pixels * 3 * gp, 256));
+      if (gp == 4)
+        hipLaunchKernelGGL(k_image_patches<4>, grid, dim3(256), 0, ctx->stream, b->img16, side,
+                           b->stacked);
+      else if (gp == 8)
+        hipLaunchKernelGGL(k_image_patches<8>, grid, dim3(256), 0, ctx->stream, b->img16, side,
+                           b->stacked);
+      else if (gp == 16)
+        hipLaunchKernelGGL(k_image_patches<16>, grid, dim3(256), 0, ctx->stream, b->img16, side,
+                           b->stacked);
+      else if (gp == 32)
+        hipLaunchKernelGGL(k_image_patches<32>, grid, dim3(256), 0, ctx->stream, b->img16, side,
+                           b->stacked);
+      else
+        hipLaunchKernelGGL(k_image_patches_any, dim3(blocks_for(pixels * 3 * gp * gp, 256)),
+                           dim3(256), 0, ctx->stream, b->img16, side, g, b->stacked);
       IEN_HIP(hipGetLastError());
       st = conv(ctx, b->stacked, g, g, 3 * gp * gp, 3 * gp * gp, 3, b->patch_conv1[i], b->mid,
                 INTER, IEN_ACT_NONE, 0);
