@@ -3,8 +3,8 @@ Transformer::attend + mlp, birefnet swin.rs Block) against the oracle's
 or_swin_attend followed by or_swin_mlp, on f16-rounded maps; a second run
 on a larger map reuses the block (scratch grown on demand).  Window 8 with
 32, 64 or 128 channels runs the fused per-window attention (at 32 with the
-MLP in the same pass), 64..96 channels the fused MLP; the other widths and
-windows the unfused path."""
+MLP in the same pass); 32, 64 and 96 channels otherwise the fused MLP pass;
+the other widths and windows the unfused path."""
 
 import numpy as np
 import pytest
