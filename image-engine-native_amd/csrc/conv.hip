@@ -1171,7 +1171,9 @@ ien_status launch_conv(ien_ctx *ctx, const ConvCall &c) {
   if (c.ks == 7 && c.stride == 1) {
     IEN_CHECK(!nchw, IEN_ERR_INPUT, "7x7 convolutions read NHWC");
     if (!vec) return run_cfg<7, 1, 4, 32, 4, 2, 16, false, false>(ctx, a);
-    return run_cfg<7, 1, 4, 32, 4, 2, 16, true, false>(ctx, a);
+    // 8 x 32 tiles (two M-blocks a wave): each chunk's 49-tap fragments
+    // (98 KiB at 64 output channels) are staged for twice the pixels.
+    return run_cfg<7, 1, 8, 32, 4, 2, 16, true, false>(ctx, a);
   }
 #undef IEN_CK
   return fail(IEN_ERR_INPUT, "no kernel for %dx%d stride %d convolutions", c.ks, c.ks, c.stride);
