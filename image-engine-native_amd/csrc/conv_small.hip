@@ -11,12 +11,14 @@
 // are the A operand and stay in VGPRs for the whole launch (64 output
 // channels, 2 x ceil(taps / 4) fragments), the pixels are the B operand.
 // Persistent workgroups of 8 waves walk 8 x 32-pixel tiles (wave w: tile
-// row w); two register sets take turns holding the halos (8 bytes per
-// pixel) of the next two tiles while the current one computes, each
-// written to one of two LDS halo buffers when its tile starts.  Each wave
-// stages its 32 pixels x 64 channels in LDS and writes whole 16-byte
-// chunks of pixel rows.  The activation is a template parameter (no
-// branch per value).
+// row w).  Halos (8 bytes a pixel) are loaded straight into LDS as 4-byte
+// items by buffer loads the compiler does not see, two tiles ahead into
+// three buffers; the range check of the buffer loads supplies the zero
+// padding.  Each iteration issues the previous tile's stores first, then
+// the loads, so the end-of-tile vmcnt wait for the next halo rarely waits
+// for stores.  Each wave stages its 32 pixels x 64 channels in LDS and
+// writes whole 16-byte chunks of pixel rows.  The activation is a template
+// parameter (no branch per value).
 //
 // conv_few: NHWC inputs of 64 channels into N outputs with N x KS <= 32
 // (LaMa's last conv 64 -> 3 7x7 reflect + sigmoid, network.rs:415-489;
@@ -27,9 +29,9 @@
 // then out[n][x] = bias[n] + sum_kx Z[(n, kx)][x + kx]: 64 - 2P outputs per
 // 64 columns, the kx sum read back from LDS.  The A operand stays in LDS
 // (the VGPRs hold a column block's loads, all issued before its MFMA
-// steps).  Padding is applied to the
-// input row and column indices (reflect, or zero for rows and columns
-// outside the image).
+// steps).  Padding is applied to the input row and column indices
+// (reflect, or zero for rows and columns outside the image: those read the
+// context's zero buffer, so no select waits for a load).
 // Both: bias, old output when accumulating, activation -- the order of
 // gemm.rs:583-666.
 
