@@ -29,6 +29,14 @@
 // order of gemm.rs:583-666), stages f32 results per wave in LDS and writes
 // 16-byte vectors.
 //
+// Launches whose workgroups fill the CUs at most once (counting the
+// double-buffered workgroups that fit a CU) keep two chunk buffers (DB):
+// chunk i + 1 is loaded while chunk i is multiplied -- NHWC halo and
+// fragments by buffer loads straight into LDS that the compiler does not
+// see (waited for with vmcnt(loads per wave)), NCHW halo groups through
+// registers written after the products.  No other workgroup would hide the
+// load latency there.
+//
 // Block ids are remapped so that each XCD (blocks are dealt round-robin to
 // the 8 XCDs) gets a contiguous band of tiles: neighbouring tiles share halo
 // rows, which then stay in that XCD's L2.
