@@ -36,9 +36,13 @@
 
 namespace ien {
 
-template <int KS, int C>
+// H32: outputs of at most 32 channels, not accumulating -- every wave on
+// the one 32-channel half, over tiles of 4 rows of 64 pixels.
+template <int KS, int C, bool H32 = false>
 struct Res8 {
-  static constexpr int TR = 2, TC = 64;  // output tile: 2 rows of 64 pixels
+  static constexpr int TR = H32 ? 4 : 2, TC = 64;  // output tile: TR rows of 64 pixels
+  static constexpr int CH = H32 ? 32 : 64;         // output channels of a tile
+  static constexpr int IPX = CH / 8;               // 16-byte items of a staged pixel
   static constexpr int STEPS = KS * KS * C / 16;
   static constexpr int HR = TR + KS - 1, HC = TC + KS - 1, HPIX = HR * HC;
   // Halo pixel stride: the channels plus one 16-byte pad chunk.
@@ -47,9 +51,9 @@ struct Res8 {
   // 1 KiB loads per halo.
   static constexpr int HALO = (HPIX * PB + 8191) / 8192 * 8192;
   static constexpr int HIT = HALO / 8192;     // halo loads per wave
-  static constexpr int SPX = 64 + 8;          // staged halves per pixel (padded)
+  static constexpr int SPX = CH + 8;          // staged halves per pixel (padded)
   static constexpr int STAGE = TR * TC * SPX * 2;
-  static constexpr int WBYTES = 2 * STEPS * 1024;  // B fragments of 64 channels
+  static constexpr int WBYTES = CH / 32 * STEPS * 1024;  // B fragments of the tile's channels
   // LDS: 3 halo buffers | 2 staging buffers | bias (1 KiB) | slopes (1 KiB).
   // In the prologue the weights sit over halo 2 and the staging buffers.
   static constexpr int STG = 3 * HALO;
@@ -57,23 +61,24 @@ struct Res8 {
   static constexpr int WOFF = 2 * HALO;
   // When they fit: two buffers for the old outputs of an accumulating tile
   // (its 16-byte store items, in item order).
-  static constexpr int OLDB = TR * TC * 8 * 16;
+  static constexpr int OLDB = TR * TC * IPX * 16;
   static constexpr int OLD = PARAM + 2048;
   static constexpr bool OLD_LDS = OLD + 2 * OLDB <= 160 * 1024;
   static constexpr int LDS = OLD_LDS ? OLD + 2 * OLDB : PARAM + 2048;
-  static constexpr int SITEMS = TR * TC * 8 / 512;  // 16-byte stores per thread and tile
+  static constexpr int SITEMS = TR * TC * IPX / 512;  // 16-byte stores per thread and tile
   static constexpr int DEPTH = 3;                   // fragment prefetch
   static_assert(C == 16 || C == 32 || C == 64, "channels");
   static_assert(STEPS <= 36, "weights must fit in registers");
   static_assert(WOFF + WBYTES <= PARAM, "prologue weights overlap the parameters");
   static_assert(LDS <= 160 * 1024, "LDS budget");
-  static_assert(SITEMS * 512 == TR * TC * 8, "store split");
+  static_assert(SITEMS * 512 == TR * TC * IPX, "store split");
   static_assert(2 * HIT < 64, "vmcnt range");
 };
 
-template <int KS, int C, int ACT>
+template <int KS, int C, int ACT, bool H32 = false>
 __global__ __launch_bounds__(512) void conv_res8(ConvArgs a) {
-  using R = Res8<KS, C>;
+  using R = Res8<KS, C, H32>;
+  constexpr int IPX = R::IPX, CH = R::CH, NJ = CH / 32;
   constexpr int STEPS = R::STEPS, HC = R::HC, PB = R::PB, P = KS / 2, DEPTH = R::DEPTH;
   constexpr int HIT = R::HIT;
   __shared__ __attribute__((aligned(1024))) unsigned char lds[R::LDS];
@@ -81,9 +86,10 @@ __global__ __launch_bounds__(512) void conv_res8(ConvArgs a) {
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int mg = wave & 3, ng = wave >> 2;  // 32-pixel block, 32-channel half
+  // 32-pixel block, 32-channel half
+  const int mg = H32 ? wave : wave & 3, ng = H32 ? 0 : wave >> 2;
   const int lb = xcd_remap(blockIdx.x, gridDim.x);
-  const int tn = lb % a.tiles_n;            // this block's 64-channel tile
+  const int tn = lb % a.tiles_n;            // this block's CH-channel tile
   const int per_n = gridDim.x / a.tiles_n;  // blocks sharing it
   const int tiles_m = a.tiles_x * a.tiles_y;
   const unsigned lds0 = lds_addr(lds);
@@ -120,18 +126,18 @@ __global__ __launch_bounds__(512) void conv_res8(ConvArgs a) {
   // tiles (the second is the first again when there is none) ----
   if (wave == 0) {  // lanes 0-15: the 64 biases of the tile (padded to NB * 32)
     dma_lds(buffer_rsrc(a.bias, a.NB * 32 * 4), __builtin_amdgcn_readfirstlane(lds0 + R::PARAM),
-            lane < 16 ? (tn * 64 + 4 * lane) * 4 : OOB);
+            lane < 16 ? (tn * CH + 4 * lane) * 4 : OOB);
   } else if (wave == 1) {  // lanes 0-15: the slopes (zeros unless PReLU)
     dma_lds(buffer_rsrc(a.slope, a.act == IEN_ACT_PRELU ? a.N * 4 : 0),
             __builtin_amdgcn_readfirstlane(lds0 + R::PARAM + 1024),
-            lane < 16 ? (tn * 64 + 4 * lane) * 4 : OOB);
+            lane < 16 ? (tn * CH + 4 * lane) * 4 : OOB);
   }
   {
     const int4v wrs = buffer_rsrc(a.wp, a.NB * a.KB * 1024);
-    for (int f = wave; f < 2 * STEPS; f += 8) {
+    for (int f = wave; f < NJ * STEPS; f += 8) {
       const int jn = f / STEPS, s = f - jn * STEPS;
       dma_lds(wrs, __builtin_amdgcn_readfirstlane(lds0 + R::WOFF + f * 1024),
-              ((tn * 2 + jn) * a.KB + s) * 1024 + lane * 16);
+              ((tn * NJ + jn) * a.KB + s) * 1024 + lane * 16);
     }
   }
   int mt = lb / a.tiles_n;
@@ -174,16 +180,16 @@ __global__ __launch_bounds__(512) void conv_res8(ConvArgs a) {
   auto item_off = [&](int j, int mts, bool valid) -> int {
     int oy0, ox0;
     origin(mts, oy0, ox0);
-    const int v = tid + 512 * j, tp = v >> 3, chunk = v & 7;
+    const int v = tid + 512 * j, tp = v / IPX, chunk = v % IPX;
     const int oy = oy0 + tp / R::TC, ox = ox0 + tp % R::TC;
     const int p = oy * a.OW + ox;
-    const int n0 = tn * 64 + chunk * 8;
+    const int n0 = tn * CH + chunk * 8;
     const bool ok = valid && oy < a.OH && ox < a.OW && p >= a.p_begin && p < a.p_end && n0 < a.N;
     return ok ? ((p - a.p_begin) * a.ys + n0) * 2 : OOB;
   };
   auto item_src = [&](int j, const unsigned char *stage) {
     const int v = tid + 512 * j;
-    return *(const u32x4 *)(stage + ((v >> 3) * R::SPX + (v & 7) * 8) * 2);
+    return *(const u32x4 *)(stage + ((v / IPX) * R::SPX + (v % IPX) * 8) * 2);
   };
   auto old_buf = [&](int k) { return lds + R::OLD + k * R::OLDB; };
   // Old items of tile mts into old buffer k (8 KiB per round of items).
@@ -195,7 +201,7 @@ __global__ __launch_bounds__(512) void conv_res8(ConvArgs a) {
   };
   // Staged sum + old item, activated, for an accumulating store.
   auto add_old = [&](int j, u32x4 sv, const unsigned char *ob) {
-    const int v = tid + 512 * j, chunk = v & 7;
+    const int v = tid + 512 * j, chunk = v % IPX;
     const u32x4 ov = *(const u32x4 *)(ob + 16 * v);
     uint16_t h[8], o[8];
     __builtin_memcpy(h, &sv, 16);
@@ -214,11 +220,11 @@ __global__ __launch_bounds__(512) void conv_res8(ConvArgs a) {
   auto store_slow = [&](int mts, const unsigned char *stage) {
     int oy0, ox0;
     origin(mts, oy0, ox0);
-    for (int v = tid; v < R::TR * R::TC * 8; v += 512) {
-      const int tp = v >> 3, chunk = v & 7;
+    for (int v = tid; v < R::TR * R::TC * IPX; v += 512) {
+      const int tp = v / IPX, chunk = v % IPX;
       const int oy = oy0 + tp / R::TC, ox = ox0 + tp % R::TC;
       const int p = oy * a.OW + ox;
-      const int n0 = tn * 64 + chunk * 8;
+      const int n0 = tn * CH + chunk * 8;
       if (oy >= a.OH || ox >= a.OW || p < a.p_begin || p >= a.p_end || n0 >= a.N) continue;
       const int rel = p - a.p_begin;
       u32x4 hv = *(const u32x4 *)(stage + (tp * R::SPX + chunk * 8) * 2);
@@ -413,24 +419,24 @@ bool resident_supported(int ks, int stride, int c, int nchw, int reflect, int no
          !reflect && noff == 0 && !rows_mode && ks * ks * c / 16 <= 36 && in_bytes <= 0x7fff0000L;
 }
 
-template <int KS, int C>
+template <int KS, int C, bool H32 = false>
 static ien_status run_res8(ien_ctx *ctx, ConvArgs a) {
-  using R = Res8<KS, C>;
+  using R = Res8<KS, C, H32>;
   void (*kernel)(ConvArgs) = nullptr;
   // Accumulating: the sums are staged and activated after the old output.
   switch (a.accumulate ? IEN_ACT_NONE : a.act) {
-    case IEN_ACT_RELU: kernel = conv_res8<KS, C, IEN_ACT_RELU>; break;
-    case IEN_ACT_PRELU: kernel = conv_res8<KS, C, IEN_ACT_PRELU>; break;
-    case IEN_ACT_GELU: kernel = conv_res8<KS, C, IEN_ACT_GELU>; break;
-    case IEN_ACT_SIGMOID: kernel = conv_res8<KS, C, IEN_ACT_SIGMOID>; break;
-    default: kernel = conv_res8<KS, C, IEN_ACT_NONE>; break;
+    case IEN_ACT_RELU: kernel = conv_res8<KS, C, IEN_ACT_RELU, H32>; break;
+    case IEN_ACT_PRELU: kernel = conv_res8<KS, C, IEN_ACT_PRELU, H32>; break;
+    case IEN_ACT_GELU: kernel = conv_res8<KS, C, IEN_ACT_GELU, H32>; break;
+    case IEN_ACT_SIGMOID: kernel = conv_res8<KS, C, IEN_ACT_SIGMOID, H32>; break;
+    default: kernel = conv_res8<KS, C, IEN_ACT_NONE, H32>; break;
   }
   const int first_row = a.p_begin / a.OW, last_row = (a.p_end - 1) / a.OW;
   a.ty_begin = first_row / R::TR;
   a.tiles_y = last_row / R::TR + 1 - a.ty_begin;
   a.tiles_x = (a.OW + R::TC - 1) / R::TC;
-  a.tiles_n = (a.N + 63) / 64;
-  IEN_CHECK(a.tiles_n * 2 <= a.NB, IEN_ERR_INPUT, "weights narrower than the tile");
+  a.tiles_n = (a.N + R::CH - 1) / R::CH;
+  IEN_CHECK(a.tiles_n * (R::CH / 32) <= a.NB, IEN_ERR_INPUT, "weights narrower than the tile");
   const long tiles_m = (long)a.tiles_y * a.tiles_x;
   // One workgroup per CU; every channel tile gets as many, a multiple of 8
   // (the XCDs) where there are that many.
@@ -447,7 +453,12 @@ ien_status launch_resident(ien_ctx *ctx, ConvArgs a, int ks) {
   if (ks == 3) {
     switch (a.C) {
       case 16: return run_res8<3, 16>(ctx, a);
-      case 32: return run_res8<3, 32>(ctx, a);
+      case 32:
+        // At most 32 outputs, not accumulating: every wave on them, tiles
+        // of 4 rows (the old-output buffers of accumulating tiles would not
+        // fit beside the larger halos).
+        if (a.N <= 32 && !a.accumulate) return run_res8<3, 32, true>(ctx, a);
+        return run_res8<3, 32>(ctx, a);
       default: return run_res8<3, 64>(ctx, a);
     }
   }

@@ -140,6 +140,18 @@ def test_resident_accumulate(ctx, oracle, c, n, h, w, act, pad):
     close(got, want)
 
 
+# The resident kernel's half mode (32 input channels, at most 32 outputs,
+# not accumulating: every wave on the 32 channels, 4-row tiles): ragged
+# tiles, fewer outputs, activations, padded strides, several tiles a CU.
+@pytest.mark.parametrize("n,h,w,act,pad", [(32, 33, 70, 1, 0), (24, 9, 64, 3, 8), (16, 5, 130, 0, 0),
+                                           (32, 200, 260, 1, 8)])
+def test_resident_half(ctx, oracle, n, h, w, act, pad):
+    x, wt, b = case(21 + n + h, h, w, 32, n, 9)
+    slope = np.linspace(-0.2, 0.4, n).astype(np.float32)
+    got = run_gpu(ctx, x, wt, b, act=act, slope=slope, stride_pad=pad)
+    close(got, want_cpu(oracle, x, wt, b, act=act, slope=slope))
+
+
 def test_nchw_in_and_out(ctx, oracle):
     import ien
 
