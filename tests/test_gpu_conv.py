@@ -125,12 +125,14 @@ def test_activations_and_accumulate(ctx, oracle, act):
     close(got, want)
 
 
-# The resident kernel's accumulating path for 16 and 32 input channels (old
-# outputs staged one tile ahead): ragged tiles, several tiles per CU (the
-# last case), activations after the sum, a padded output stride.
+# The resident kernel's accumulating path (old outputs staged one tile
+# ahead for 16 and 32 input channels; element-wise stores at 64): ragged
+# tiles, several tiles per CU, activations after the sum, a padded output
+# stride.
 @pytest.mark.parametrize("c,n,h,w,act,pad", [(32, 32, 7, 130, 0, 0), (32, 64, 33, 64, 1, 8),
                                             (16, 48, 20, 100, 3, 0), (32, 32, 320, 330, 0, 0),
-                                            (16, 16, 65, 63, 2, 8)])
+                                            (16, 16, 65, 63, 2, 8), (64, 64, 7, 130, 0, 0),
+                                            (64, 48, 33, 64, 1, 8), (64, 64, 200, 260, 2, 0)])
 def test_resident_accumulate(ctx, oracle, c, n, h, w, act, pad):
     x, wt, b = case(11 + c + n, h, w, c, n, 9)
     slope = np.linspace(0.05, 0.5, n).astype(np.float32)
