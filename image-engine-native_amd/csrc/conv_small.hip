@@ -384,7 +384,9 @@ ien_status narrow_act(ien_ctx *ctx, const ConvArgs &a, dim3 grid) {
 }  // namespace
 
 bool narrow_supported(const ConvArgs &a, int ks, int stride, int nchw, int noff, int rows_mode) {
+  // The halo loads take 32-bit byte offsets: inputs below 2 GiB.
   return !nchw && !noff && !rows_mode && stride == 1 && a.C == 4 &&
+         (long)a.H * a.W * a.xs * 2 <= 0x7fff0000L &&
          (ks == 3 || ks == 5 || ks == 7) && a.xs % 4 == 0 && ((uintptr_t)a.x & 7) == 0 &&
          a.p_begin == 0 && a.p_end == a.OH * a.OW && a.OH == a.H && a.OW == a.W &&
          !a.out_f32 && !a.out_nchw && a.N % 8 == 0 && a.ys % 8 == 0 &&
