@@ -27,11 +27,13 @@
 // consecutive padded input columns q,
 //   Z[(n, kx)][q] = sum_ky sum_c W[ky][kx][c][n] in[y + ky - P][q][c],
 // then out[n][x] = bias[n] + sum_kx Z[(n, kx)][x + kx]: 64 - 2P outputs per
-// 64 columns, the kx sum read back from LDS.  The A operand stays in LDS
-// (the VGPRs hold a column block's loads, all issued before its MFMA
-// steps).  Padding is applied to the input row and column indices
+// 64 columns, the kx sum read back from LDS.  A workgroup of 4 waves (one
+// output row each) stages the item's KS + 3 input rows x 64 columns in LDS
+// (a ring: going down a column tile, an item loads only its 4 new rows)
+// with whole 128-byte pixels, loaded into registers while the previous
+// item computes; the A operand stays in LDS too.  Padding is applied to the input row and column indices
 // (reflect, or zero for rows and columns outside the image: those read the
-// context's zero buffer, so no select waits for a load).
+// context's zero buffer).
 // Both: bias, old output when accumulating, activation -- the order of
 // gemm.rs:583-666.
 
@@ -262,22 +264,28 @@ __global__ __launch_bounds__(512) void conv_narrow(ConvArgs a) {
 template <int KS>
 struct Few {
   static constexpr int P = KS / 2, C = 64;
-  static constexpr int STEPS = KS * C / 16;  // K = (ky, channel)
-  static constexpr int TW = 64 - 2 * P;     // outputs a 64-column item
-  static constexpr int ZP = 64 + 4;         // floats a staged Z row
-  static constexpr int WAVES = 4;
+  static constexpr int STEPS = KS * C / 16;   // K = (ky, channel)
+  static constexpr int TW = 64 - 2 * P;       // outputs of a 64-column item
+  static constexpr int WAVES = 4, RB = WAVES;  // output rows of an item, one a wave
+  static constexpr int IR = RB + KS - 1;      // staged input rows
+  static constexpr int PXB = C * 2 + 16;      // bytes a staged pixel (one pad chunk)
+  static constexpr int IN = IR * 64 * PXB;    // staged input bytes
+  static constexpr int ZP = 64 + 4;           // floats a staged Z row
   static constexpr int ABYTES = STEPS * 1024;
   static constexpr int ZBYTES = 32 * ZP * 4;
-  static constexpr int LDS = ABYTES + WAVES * ZBYTES;
+  static constexpr int LDS = IN + ABYTES + WAVES * ZBYTES + 64 * 4;  // + bias, slope
+  static_assert(LDS <= 160 * 1024, "LDS budget");
 };
 
 template <int KS>
 __global__ __launch_bounds__(256) void conv_few(ConvArgs a) {
   using R = Few<KS>;
-  constexpr int STEPS = R::STEPS, P = R::P, C = R::C, ZP = R::ZP;
+  constexpr int STEPS = R::STEPS, P = R::P, C = R::C, ZP = R::ZP, PXB = R::PXB;
   __shared__ __attribute__((aligned(16))) unsigned char lds[R::LDS];
+  unsigned char *in_l = lds, *a_l = lds + R::IN;
   const int tid = threadIdx.x, lane = tid & 63, hf = lane >> 5, l32 = lane & 31;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  float *zs = (float *)(lds + R::IN + R::ABYTES) + wave * (32 * ZP);
   const int rows_used = a.N * KS;
   const bool reflect = a.pad_reflect != 0;
 
@@ -291,59 +299,92 @@ __global__ __launch_bounds__(256) void conv_few(ConvArgs a) {
     const int kk = (ky * KS + kx) * C + c0;
     u32x4 v = {0u, 0u, 0u, 0u};
     if (m < rows_used) v = *(const u32x4 *)(a.wp + (long)(kk >> 4) * 512 + (n + 32 * ((kk & 15) >> 3)) * 8);
-    *(u32x4 *)(lds + s * 1024 + lane * 16) = v;
+    *(u32x4 *)(a_l + s * 1024 + lane * 16) = v;
   }
-  __syncthreads();
 
-  float *zs = (float *)(lds + R::ABYTES + wave * R::ZBYTES);
-  const int tiles_x = (a.OW + R::TW - 1) / R::TW;
-  const long items = (long)a.OH * tiles_x;
-  const int waves_total = gridDim.x * R::WAVES;
+  float *bs = (float *)(lds + R::IN + R::ABYTES + R::WAVES * R::ZBYTES);  // bias, slope
+  if (tid < a.N) {
+    bs[tid] = a.bias[tid];
+    bs[32 + tid] = a.act == IEN_ACT_PRELU ? a.slope[tid] : 0.0f;
+  }
+
+  // Items are (column tile, group of RB output rows), numbered down each
+  // column tile; a workgroup takes a contiguous run of them.  The staged
+  // input rows form a ring of IR rows in LDS (input row y0 - P + r of item
+  // y0 sits in slot (y0 + r) % IR), so an item that continues the previous
+  // one down its tile loads only its RB new rows.
+  const int tiles_x = (a.OW + R::TW - 1) / R::TW, groups = (a.OH + R::RB - 1) / R::RB;
+  const long items = (long)groups * tiles_x;
+  const long per = (items + gridDim.x - 1) / gridDim.x;
+  const long first = blockIdx.x * per, last = min(items, first + per);
   uint16_t *yh = (uint16_t *)a.y;
   float *yf = (float *)a.y;
-  for (long item = (long)blockIdx.x * R::WAVES + wave; item < items; item += waves_total) {
-    const int y = (int)(item / tiles_x), x0 = (int)(item - (long)y * tiles_x) * R::TW;
-    // Input rows of the KS kernel rows (uniform).
-    int iy[KS];
-    bool oky[KS];
+  // Whole 128-byte pixels as 16-byte pieces (padding pixels read the zero
+  // buffer), up to PER of them a thread, loaded into registers while the
+  // previous item computes.
+  constexpr int PER = R::IR * 64 * 8 / 256, NEW = R::RB * 64 * 8 / 256;
+  static_assert(PER * 256 == R::IR * 64 * 8 && NEW * 256 == R::RB * 64 * 8, "whole pieces a thread");
+  u32x4 pre[PER];
+  auto load_item = [&](long item, bool full) {
+    const int y0 = (int)(item % groups) * R::RB, x0 = (int)(item / groups) * R::TW;
+    const int r0 = full ? 0 : KS - 1, n = full ? PER : NEW;
 #pragma unroll
-    for (int ky = 0; ky < KS; ky++) iy[ky] = pad_index(y + ky - P, a.H, reflect, oky[ky]);
-#pragma unroll
-    for (int cb = 0; cb < 2; cb++) {
-      bool okx;
-      const int ix = pad_index(x0 - P + 32 * cb + l32, a.W, reflect, okx);
-      // All of the column block's loads first, then the MFMA steps.
-      u32x4 xv[STEPS];
-#pragma unroll
-      for (int s = 0; s < STEPS; s++) {
-        const int k0 = 16 * s, ky = k0 / C, c0 = k0 - ky * C + 8 * hf;
-        // Padding reads the zero buffer: no select waits for the load.
-        const uint16_t *src = oky[ky] && okx ? a.x + ((long)iy[ky] * a.W + ix) * a.xs : a.zeros;
-        xv[s] = *(const u32x4 *)(src + c0);
+    for (int b = 0; b < PER; b++) {
+      if (b < n) {
+        const int e = tid + 256 * b, r = r0 + (e >> 9), j = (e >> 3) & 63, ch = e & 7;
+        bool oky, okx;
+        const int iy = pad_index(y0 - P + r, a.H, reflect, oky);
+        const int ix = pad_index(x0 - P + j, a.W, reflect, okx);
+        const uint16_t *src = oky && okx ? a.x + ((long)iy * a.W + ix) * a.xs + 8 * ch : a.zeros;
+        pre[b] = *(const u32x4 *)src;
       }
-      floatx16 acc = {};
+    }
+  };
+  auto continues = [&](long item) { return item != first && item % groups != 0; };
+  if (first < last) load_item(first, true);
+  for (long item = first; item < last; item++) {  // uniform in the block
+    const int y0 = (int)(item % groups) * R::RB, x0 = (int)(item / groups) * R::TW;
+    {
+      const bool full = !continues(item);
+      const int r0 = full ? 0 : KS - 1, n = full ? PER : NEW;
 #pragma unroll
-      for (int s = 0; s < STEPS; s++) {
-        half8 xb;
-        __builtin_memcpy(&xb, &xv[s], 16);
-        const half8 wa = *(const half8 *)(lds + s * 1024 + lane * 16);
-        acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(wa, xb, acc, 0, 0, 0);
+      for (int b = 0; b < PER; b++) {
+        if (b < n) {
+          const int e = tid + 256 * b, r = r0 + (e >> 9), j = (e >> 3) & 63, ch = e & 7;
+          *(u32x4 *)(in_l + (((y0 + r) % R::IR) * 64 + j) * PXB + 16 * ch) = pre[b];
+        }
       }
-      // C: row 8 (r / 4) + 4 hf + r % 4 = (n, kx), column 32 cb + l32.
+    }
+    __syncthreads();  // the rows (and, the first time, the A operand and bias) are in
+    if (item + 1 < last) load_item(item + 1, !continues(item + 1));
+    const int y = y0 + wave;
+    floatx16 acc[2] = {};  // the two 32-column blocks: independent chains
+#pragma unroll
+    for (int s = 0; s < STEPS; s++) {
+      const int k0 = 16 * s, ky = k0 / C, c0 = k0 - ky * C + 8 * hf;
+      const half8 wa = *(const half8 *)(a_l + s * 1024 + lane * 16);
+#pragma unroll
+      for (int cb = 0; cb < 2; cb++) {
+        const half8 xb = *(const half8 *)(in_l + (((y0 + wave + ky) % R::IR) * 64 + 32 * cb + l32) * PXB + c0 * 2);
+        acc[cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wa, xb, acc[cb], 0, 0, 0);
+      }
+    }
+    // C: row 8 (r / 4) + 4 hf + r % 4 = (n, kx), column 32 cb + l32.
+#pragma unroll
+    for (int cb = 0; cb < 2; cb++)
 #pragma unroll
       for (int r = 0; r < 16; r++)
-        zs[(8 * (r >> 2) + 4 * hf + (r & 3)) * ZP + 32 * cb + l32] = acc[r];
-    }
+        zs[(8 * (r >> 2) + 4 * hf + (r & 3)) * ZP + 32 * cb + l32] = acc[cb][r];
     __builtin_amdgcn_wave_barrier();
     const int x = x0 + lane;
-    if (lane < R::TW && x < a.OW) {
+    if (y < a.OH && lane < R::TW && x < a.OW) {
       const long pix = (long)y * a.OW + x;
       for (int n = 0; n < a.N; n++) {
-        float v = a.bias[n];
+        float v = bs[n];
 #pragma unroll
         for (int kx = 0; kx < KS; kx++) v += zs[(n * KS + kx) * ZP + lane + kx];
         const long at = pix * a.ys + n;
-        const float sl = a.act == IEN_ACT_PRELU ? a.slope[n] : 0.0f;
+        const float sl = bs[32 + n];
         if (a.out_f32) {
           if (a.accumulate) v += yf[at];
           yf[at] = activate(v, a.act, sl);
@@ -353,7 +394,7 @@ __global__ __launch_bounds__(256) void conv_few(ConvArgs a) {
         }
       }
     }
-    __builtin_amdgcn_wave_barrier();  // Z is read before the next item writes it
+    __syncthreads();  // every wave is done with the rows and its Z before the next item
   }
 }
 
@@ -414,8 +455,11 @@ bool few_supported(const ConvArgs &a, int ks, int stride, int nchw, int noff, in
 
 ien_status launch_few(ien_ctx *ctx, ConvArgs a, int ks) {
   const int tw = ks == 3 ? Few<3>::TW : Few<7>::TW;
-  const long items = (long)a.OH * ((a.OW + tw - 1) / tw);
-  const int blocks = (int)std::max(1L, std::min((items + 3) / 4, (long)cus_of(ctx) * 2));
+  // One workgroup a CU (its staged rows fill the LDS), each over a run of
+  // `per` items of 4 output rows x tw columns; no workgroup's run is empty.
+  const long items = (long)((a.OH + 3) / 4) * ((a.OW + tw - 1) / tw);
+  const long per = (items + cus_of(ctx) - 1) / cus_of(ctx);
+  const int blocks = (int)std::max(1L, (items + per - 1) / per);
   if (ks == 3) hipLaunchKernelGGL(conv_few<3>, dim3(blocks), dim3(256), 0, ctx->stream, a);
   else hipLaunchKernelGGL(conv_few<7>, dim3(blocks), dim3(256), 0, ctx->stream, a);
   IEN_HIP(hipGetLastError());

@@ -227,8 +227,13 @@ def test_conv_four_channels(ctx, oracle, size, pad, h, w, n, act, acc, sp):
 # Few outputs (conv_few: (output, kx) pairs as the MFMA rows, the kx sum read
 # back from LDS; the models' last convolutions): 7x7 and 3x3, reflect and
 # zero padding, 1 to 10 outputs, output strides of 3, 4 and 10 halves or f32,
-# images narrower than one 58- or 62-column item and several items a row.
+# images narrower than one 58- or 62-column item and several items a row,
+# and images of more items than the GPU has CUs (a workgroup then goes down
+# its column tile reusing staged rows; the odd row-group counts put runs
+# across tile boundaries).
 @pytest.mark.parametrize("size,pad,h,w,n,act,acc,f32,op", [
+    (7, 1, 500, 130, 3, "SIGMOID", False, False, 0),
+    (3, 0, 402, 200, 3, "NONE", True, False, 1),
     (7, 1, 40, 130, 3, "SIGMOID", False, False, 0),  # LaMa's last conv
     (3, 0, 33, 70, 3, "NONE", False, False, 1),      # SCUNet's tail (output stride 4)
     (3, 1, 12, 61, 10, "RELU", True, False, 0),
