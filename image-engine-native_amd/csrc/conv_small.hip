@@ -31,9 +31,9 @@
 // output row each) stages the item's KS + 3 input rows x 64 columns in LDS
 // (a ring: going down a column tile, an item loads only its 4 new rows)
 // with whole 128-byte pixels, loaded into registers while the previous
-// item computes; the A operand stays in LDS too.  Padding is applied to the input row and column indices
-// (reflect, or zero for rows and columns outside the image: those read the
-// context's zero buffer).
+// item computes; the A operand stays in LDS too.  Padding is applied to the
+// input row and column indices (reflect, or zero for rows and columns
+// outside the image: those read the context's zero buffer).
 // Both: bias, old output when accumulating, activation -- the order of
 // gemm.rs:583-666.
 
