@@ -32,17 +32,19 @@ def test_half_conversions_bit_exact(ctx, oracle):
     assert np.array_equal(np.isnan(g), nan) and np.array_equal(g[~nan].view(np.uint32), want[~nan].view(np.uint32))
 
 
-@pytest.mark.parametrize("h,w", [(3, 5), (64, 96), (256, 384)])
-def test_pixel_shuffle_add_bit_exact(ctx, oracle, h, w):
+# Last-layer strides of 64, 48 (the network's) and 50 halves; a 1 x 1 image.
+@pytest.mark.parametrize("h,w,stride", [(3, 5, 64), (64, 96, 64), (256, 384, 48), (1, 1, 48),
+                                        (7, 33, 50)])
+def test_pixel_shuffle_add_bit_exact(ctx, oracle, h, w, stride):
     import torch
     import ien
 
     rng = np.random.default_rng(h)
-    last = rng.standard_normal((h * w, 64)).astype(np.float16)
+    last = rng.standard_normal((h * w, stride)).astype(np.float16)
     image = rng.random((h, w, 3), dtype=np.float32)
     want = oracle.pixel_shuffle_add(last[:, :48].astype(np.float32), image)
     out = torch.empty((4 * h, 4 * w, 3), dtype=torch.float32, device="cuda")
-    ien.pixel_shuffle_add(ctx, torch.from_numpy(last).cuda(), 64, torch.from_numpy(image).cuda(), w, h, out)
+    ien.pixel_shuffle_add(ctx, torch.from_numpy(last).cuda(), stride, torch.from_numpy(image).cuda(), w, h, out)
     torch.cuda.synchronize()
     assert np.array_equal(out.cpu().numpy(), want)
 
