@@ -1002,8 +1002,10 @@ static ien_status run_cfg(ien_ctx *ctx, ConvArgs a) {
                        (((uintptr_t)a.x) & 15) == 0);
       constexpr int FIT =
           160 * 1024 / ConvCfg<KS, S, TR, TC, MSPLIT, NBW, CK, VEC, IN_NCHW, true>::LDS_BYTES;
+      // Buffer ranges stay below the padding loads' out-of-range offset
+      // (0x7ffffff0), so a padding load never lands inside the buffer.
       db = layout_ok && !ctx->compact && blocks <= (long)ctx->cus * FIT && chunks >= 2 &&
-           (IN_NCHW || in_bytes < (1L << 31)) && (long)a.NB * a.KB * 1024 < (1L << 31);
+           (IN_NCHW || in_bytes <= 0x7fff0000L) && (long)a.NB * a.KB * 1024 <= 0x7fff0000L;
     }
   }
   int ksplit = 1;

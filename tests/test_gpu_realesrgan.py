@@ -12,6 +12,7 @@ import numpy as np
 import pytest
 
 import synthetic
+from parity import assert_spread
 
 pytestmark = pytest.mark.gpu
 
@@ -61,6 +62,10 @@ def test_config_size_device_path_and_graph(ctx, oracle, tensors):
     err = np.abs(eager - want).max()
     print(f"256x384: max err {err:.3g}, PSNR {psnr(eager, want):.1f} dB")
     assert err <= 2e-2 and psnr(eager, want) >= 45
+    # The network's own part (output minus the repeated input) against its
+    # spread: error RMS <= 1 % of its std, max <= 5 % of its peak.
+    up = np.repeat(np.repeat(image, 4, axis=0), 4, axis=1)
+    assert_spread(eager - up, want - up, what="256x384 residual")
     model.set_graph(True)
     for replay in range(3):
         d_out.zero_()
