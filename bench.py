@@ -21,7 +21,12 @@ profiles/conv3x3_64_256x384_hbm_traffic.txt when that summary exists.
 cpu_baseline: the oracle -- the C restatement of the reference's CPU f32
 path (crates/realesrgan-native/src/network.rs over native-engine's
 Winograd F(4x4, 3x3) and indirect GEMM) -- timed on this host's cores on
-the same image, median of 3 runs after a warm-up.
+the same image, median of 5 runs after a warm-up (README.md:26-27).  Every
+other configuration carries its own cpu_baseline from the same protocol
+(models[*].cpu_baseline, gemm_sweep_cpu).
+
+host_path_ms: ien_model_run with host buffers (upload, launches, download
+of the f32 output, synchronisation) beside the device-resident `value`.
 """
 
 import argparse
@@ -39,6 +44,10 @@ MFMA_F16_PEAK_TFLOPS = 2516.6  # MI355X dense f16 MFMA
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 SCUNET_GFLOP = 944.9           # 1x3x512x768, incl. 46.7 GFLOP of window attention
 METRIC = "ms/image at 1 MI355X per model; conv/attn GEMM MFMA util % of f16 peak"
+
+
+def log(msg):
+    print(f"bench: {msg}", file=sys.stderr, flush=True)
 
 
 def conv_flops(h, w, cin, cout, size):
@@ -65,19 +74,24 @@ def event_time(fn, reps, stream):
     return start.elapsed_time(end) / reps
 
 
-def sweep(ctx, stream, reps):
-    """Each conv-sweep shape (NCHW, f16, N(0,1)) through the library."""
-    import numpy as np
-    import torch
+class SweepCase:
+    """One conv-sweep shape (NCHW, f16, N(0, 1)) set up on the device the
+    way the benchmark times it: `launch()` runs the product (or the
+    depthwise pass) through the library into `out` (C x H*W f16);
+    `x`, `wt`, `bias` are the host inputs (x C x H x W)."""
 
-    import ien
-    import synthetic
+    def __init__(self, ctx, name):
+        import torch
 
-    results = []
-    for entry in synthetic.SWEEP:
-        (name, kind, cin, cout, size, h, w), x, wt, bias = synthetic.sweep_case(entry[0])
+        import ien
+        import synthetic
+
+        (self.name, self.kind, cin, cout, size, h, w), x, wt, bias = synthetic.sweep_case(name)
+        self.cin, self.cout, self.size, self.h, self.w = cin, cout, size, h, w
+        self.x, self.wt, self.bias = x, wt, bias
         xt = torch.from_numpy(x).half().cuda()
-        if kind == "conv":
+        self._m = None
+        if self.kind == "conv":
             m = ien.Matrix(ctx, wt, bias)
             inp = ien.image_input(xt, h, w, cin, layout=ien.NCHW, size=size)
             out = torch.empty((cout, h * w), dtype=torch.float16, device="cuda")
@@ -85,29 +99,45 @@ def sweep(ctx, stream, reps):
             def launch():
                 ien.multiply_ex(ctx, inp, 0, h * w, m, out, h * w, layout=ien.NCHW)
 
-            flops = conv_flops(h, w, cin, cout, size)
-            nbytes = 2.0 * (cin + cout) * h * w + 2.0 * wt.size
+            self._m = m
+            self.flops = conv_flops(h, w, cin, cout, size)
+            self.nbytes = 2.0 * (cin + cout) * h * w + 2.0 * wt.size
         else:
             wd = torch.from_numpy(wt).cuda()
             bd = torch.from_numpy(bias).cuda()
-            out = torch.empty_like(xt)
+            out = torch.empty((cin, h * w), dtype=torch.float16, device="cuda")
 
             def launch():
                 ien.depthwise(ctx, xt, h, w, cin, ien.NCHW, wd, size, bd, out)
 
-            flops = 2.0 * h * w * cin * size * size
-            nbytes = 2.0 * 2 * cin * h * w + 4.0 * wt.size
+            self.flops = 2.0 * h * w * cin * size * size
+            self.nbytes = 2.0 * 2 * cin * h * w + 4.0 * wt.size
+        self.out = out
+        self.launch = launch
+
+    def free(self):
+        if self._m is not None:
+            self._m.free()
+            self._m = None
+
+
+def sweep(ctx, stream, reps):
+    """Each conv-sweep shape (NCHW, f16, N(0,1)) through the library."""
+    import synthetic
+
+    results = []
+    for entry in synthetic.SWEEP:
+        case = SweepCase(ctx, entry[0])
         for _ in range(5):
-            launch()
-        ms = event_time(launch, reps, stream)
-        tflops = flops / (ms * 1e-3) / 1e12
-        gbs = nbytes / (ms * 1e-3) / 1e9
-        row = {"shape": name, "us": round(ms * 1e3, 2), "tflops": round(tflops, 1),
+            case.launch()
+        ms = event_time(case.launch, reps, stream)
+        tflops = case.flops / (ms * 1e-3) / 1e12
+        gbs = case.nbytes / (ms * 1e-3) / 1e9
+        row = {"shape": case.name, "us": round(ms * 1e3, 2), "tflops": round(tflops, 1),
                "mfma_util_pct": round(100 * tflops / MFMA_F16_PEAK_TFLOPS, 1),
                "hbm_gbs": round(gbs, 0), "hbm_pct": round(100 * gbs / HBM_PEAK_GBS, 1)}
         results.append(row)
-        if kind == "conv":
-            m.free()
+        case.free()
     return results
 
 
@@ -119,32 +149,82 @@ def traffic_from_profiles():
     return float(m.group(1)) if m else None
 
 
-def cpu_baseline(tensors, image):
-    sys.path.insert(0, str(ROOT))
-    from oracle import oracle as O
-
-    import synthetic
-
-    layers = synthetic.esrgan_layers(tensors)
-    threads = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
-    O.realesrgan_run(layers, image, threads=threads)  # warm-up
-    times = []
-    for _ in range(3):
-        t0 = time.perf_counter()
-        O.realesrgan_run(layers, image, threads=threads)
-        times.append(time.perf_counter() - t0)
-    times.sort()
-    cpu = "unknown"
+def cpu_model():
     try:
         for line in open("/proc/cpuinfo"):
             if line.startswith("model name"):
-                cpu = line.split(":", 1)[1].strip()
-                break
+                return line.split(":", 1)[1].strip()
     except OSError:
         pass
-    return {"value": round(times[1] * 1e3, 1), "unit": "ms/image", "cores": threads, "kind": "port",
-            "sample": f"one full 1x3x256x384 image, median of 3 runs after a warm-up, {threads} threads "
-                      f"on {cpu}; the oracle (C restatement of the reference CPU f32 path)"}
+    return "unknown"
+
+
+def cpu_threads():
+    return len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+
+
+def cpu_time(fn, runs):
+    """Median seconds of `runs` calls of fn after one warm-up call (the
+    reference's protocol, README.md:26-27)."""
+    fn()
+    times = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    return times[len(times) // 2]
+
+
+def oracle_module():
+    sys.path.insert(0, str(ROOT))
+    from oracle import oracle as O
+
+    return O
+
+
+def cpu_leg(fn, runs, what):
+    """cpu_baseline of one configuration: the oracle (C restatement of the
+    reference CPU f32 path) on this host's cores."""
+    threads = cpu_threads()
+    sec = cpu_time(lambda: fn(threads), runs)
+    return {"value": round(sec * 1e3, 1), "unit": "ms/image", "cores": threads, "kind": "port",
+            "sample": f"{what}, median of {runs} runs after a warm-up, {threads} threads on {cpu_model()}; "
+                      f"the oracle (C restatement of the reference CPU f32 path, not the reference's "
+                      f"AVX2 build: a conservative baseline)"}
+
+
+def cpu_baseline(tensors, image, runs):
+    O = oracle_module()
+    import synthetic
+
+    layers = synthetic.esrgan_layers(tensors)
+    return cpu_leg(lambda t: O.realesrgan_run(layers, image, threads=t), runs, "one full 1x3x256x384 image")
+
+
+def cpu_sweep(runs):
+    """The conv sweep's shapes on the oracle: conv3 (Winograd, the
+    reference's 3x3 path), multiply (1x1) and the direct depthwise sum."""
+    import numpy as np
+
+    O = oracle_module()
+    import synthetic
+
+    out = []
+    threads = cpu_threads()
+    for entry in synthetic.SWEEP:
+        (name, kind, cin, cout, size, h, w), x, wt, bias = synthetic.sweep_case(entry[0])
+        x = np.ascontiguousarray(x.transpose(1, 2, 0))
+        if kind == "depthwise":
+            fn = lambda: O.depthwise(x, wt, bias, threads=threads)
+        elif size == 3:
+            fn = lambda: O.conv3(x, wt, bias, threads=threads)
+        else:
+            fn = lambda: O.multiply_conv(x, wt, bias, size=size, threads=threads)
+        out.append({"shape": name, "ms": round(cpu_time(fn, runs) * 1e3, 2)})
+    return {"shapes": out, "cores": threads, "kind": "port",
+            "sample": f"each shape once per run, median of {runs} runs after a warm-up, {threads} threads "
+                      f"on {cpu_model()}; the oracle (conv3 F(4x4)/F(2x2) for 3x3, multiply for 1x1)"}
 
 
 def body_layer(ctx, tensors, H, W):
@@ -190,7 +270,13 @@ def traffic_probe(ctx, tensors, H, W):
     print("traffic probe: body layer x10, then a 134217728-byte copy", flush=True)
 
 
-def scunet_leg(ctx, steps, warmup):
+def host_path_ms(run, reps=3):
+    """Median milliseconds of ien_model_run (host buffers: upload, the
+    launches, download and synchronisation), after a warm-up."""
+    return round(cpu_time(run, reps) * 1e3, 3)
+
+
+def scunet_leg(ctx, steps, warmup, cpu_runs=0):
     """SCUNet (configuration 3) at 1 x 3 x 512 x 768 with its trunc-normal
     random-init weights, graph replay, input and output in HBM."""
     import torch
@@ -199,8 +285,11 @@ def scunet_leg(ctx, steps, warmup):
     import synthetic
 
     h, w = 512, 768
-    model = ien.Model(ctx, ien.MODEL_SCUNET, tensors=synthetic.scunet_tensors())
-    d_in = torch.from_numpy(synthetic.scunet_image(h, w)).cuda()
+    tensors = synthetic.scunet_tensors()
+    image = synthetic.scunet_image(h, w)
+    model = ien.Model(ctx, ien.MODEL_SCUNET, tensors=tensors)
+    host_ms = host_path_ms(lambda: model.run(image))
+    d_in = torch.from_numpy(image).cuda()
     d_out = torch.empty((h, w, 3), dtype=torch.float32, device="cuda")
     model.set_graph(True)
     for _ in range(warmup):
@@ -215,9 +304,16 @@ def scunet_leg(ctx, steps, warmup):
     model.free()
     if not ok:
         sys.exit("SCUNet: non-finite output")
-    return {"workload": "SCUNet 1x3x512x768 (28 Swin-Conv blocks, 64/128/256/512)", "ms_per_image": round(ms, 3),
-            "images_per_s": round(1e3 / ms, 2), "gflop_per_image": SCUNET_GFLOP,
-            "tflops": round(SCUNET_GFLOP / ms, 1)}
+    leg = {"workload": "SCUNet 1x3x512x768 (28 Swin-Conv blocks, 64/128/256/512)", "ms_per_image": round(ms, 3),
+           "images_per_s": round(1e3 / ms, 2), "gflop_per_image": SCUNET_GFLOP,
+           "tflops": round(SCUNET_GFLOP / ms, 1), "mfma_frac": round(SCUNET_GFLOP / ms / MFMA_F16_PEAK_TFLOPS, 4),
+           "host_path_ms": host_ms}
+    if cpu_runs:
+        O = oracle_module()
+        names = synthetic.scunet_names()
+        leg["cpu_baseline"] = cpu_leg(lambda t: O.scunet_run(tensors, names, image, threads=t), cpu_runs,
+                                      "one full 1x3x512x768 image")
+    return leg
 
 
 def lama_gflop(h=512, w=512):
@@ -233,7 +329,7 @@ def lama_gflop(h=512, w=512):
     return 2 * macs / 1e9
 
 
-def lama_leg(ctx, steps, warmup):
+def lama_leg(ctx, steps, warmup, cpu_runs=0):
     """Big LaMa (configuration 4) at 1 x 4 x 512 x 512 (RGB plus a ~25 %
     rectangle mask) with He-normal random-init weights, graph replay, inputs
     and output in HBM."""
@@ -243,9 +339,12 @@ def lama_leg(ctx, steps, warmup):
     import synthetic
 
     h, w = 512, 512
-    model = ien.Model(ctx, ien.MODEL_LAMA, tensors=synthetic.lama_tensors())
-    d_in = torch.from_numpy(synthetic.lama_image(h, w)).cuda()
-    d_mask = torch.from_numpy(synthetic.lama_mask(h, w)).cuda()
+    tensors = synthetic.lama_tensors()
+    image, mask = synthetic.lama_image(h, w), synthetic.lama_mask(h, w)
+    model = ien.Model(ctx, ien.MODEL_LAMA, tensors=tensors)
+    host_ms = host_path_ms(lambda: model.run(image, mask=mask))
+    d_in = torch.from_numpy(image).cuda()
+    d_mask = torch.from_numpy(mask).cuda()
     d_out = torch.empty((h, w, 3), dtype=torch.float32, device="cuda")
     model.set_graph(True)
     for _ in range(warmup):
@@ -261,8 +360,15 @@ def lama_leg(ctx, steps, warmup):
     if not ok:
         sys.exit("LaMa: non-finite output")
     gflop = round(lama_gflop(h, w), 1)
-    return {"workload": "Big LaMa 1x4x512x512 (18 FFC blocks at 64x64x512)", "ms_per_image": round(ms, 3),
-            "images_per_s": round(1e3 / ms, 2), "gflop_per_image": gflop, "tflops": round(gflop / ms, 1)}
+    leg = {"workload": "Big LaMa 1x4x512x512 (18 FFC blocks at 64x64x512)", "ms_per_image": round(ms, 3),
+           "images_per_s": round(1e3 / ms, 2), "gflop_per_image": gflop, "tflops": round(gflop / ms, 1),
+           "mfma_frac": round(gflop / ms / MFMA_F16_PEAK_TFLOPS, 4), "host_path_ms": host_ms}
+    if cpu_runs:
+        O = oracle_module()
+        names = synthetic.lama_names()
+        leg["cpu_baseline"] = cpu_leg(lambda t: O.lama_run(tensors, names, image, mask, threads=t), cpu_runs,
+                                      "one full 1x4x512x512 image and mask")
+    return leg
 
 
 def birefnet_gflop(side=1024, window=12, padded=True):
@@ -302,7 +408,7 @@ def birefnet_gflop(side=1024, window=12, padded=True):
     return 2 * macs / 1e9
 
 
-def birefnet_leg(ctx, steps, warmup):
+def birefnet_leg(ctx, steps, warmup, cpu_runs=0):
     """BiRefNet-lite (configuration 5) at 1 x 3 x 1024 x 1024 N(0, 1),
     window 12, deformable-free ASPP, trunc-normal Swin init, graph replay,
     input and logits in HBM."""
@@ -312,8 +418,11 @@ def birefnet_leg(ctx, steps, warmup):
     import synthetic
 
     side = 1024
-    model = ien.Model(ctx, ien.MODEL_BIREFNET, tensors=synthetic.birefnet_tensors())
-    d_in = torch.from_numpy(synthetic.birefnet_image(side)).cuda()
+    tensors = synthetic.birefnet_tensors()
+    image = synthetic.birefnet_image(side)
+    model = ien.Model(ctx, ien.MODEL_BIREFNET, tensors=tensors)
+    host_ms = host_path_ms(lambda: model.run(image))
+    d_in = torch.from_numpy(image).cuda()
     d_out = torch.empty((side, side), dtype=torch.float32, device="cuda")
     model.set_graph(True)
     for _ in range(warmup):
@@ -329,10 +438,17 @@ def birefnet_leg(ctx, steps, warmup):
     if not ok:
         sys.exit("BiRefNet: non-finite output")
     gflop = round(birefnet_gflop(side, 12), 1)
-    return {"workload": "BiRefNet-lite 1x3x1024x1024 (Swin-T window 12, deformable-free ASPP)",
-            "ms_per_image": round(ms, 3), "images_per_s": round(1e3 / ms, 2), "gflop_per_image": gflop,
-            "gflop_unpadded_windows": round(birefnet_gflop(side, 12, padded=False), 1),
-            "tflops": round(gflop / ms, 1)}
+    leg = {"workload": "BiRefNet-lite 1x3x1024x1024 (Swin-T window 12, deformable-free ASPP)",
+           "ms_per_image": round(ms, 3), "images_per_s": round(1e3 / ms, 2), "gflop_per_image": gflop,
+           "gflop_unpadded_windows": round(birefnet_gflop(side, 12, padded=False), 1),
+           "tflops": round(gflop / ms, 1), "mfma_frac": round(gflop / ms / MFMA_F16_PEAK_TFLOPS, 4),
+           "host_path_ms": host_ms}
+    if cpu_runs:
+        O = oracle_module()
+        names = synthetic.birefnet_names(12)
+        leg["cpu_baseline"] = cpu_leg(lambda t: O.birefnet_run(tensors, names, image, 12, threads=t), cpu_runs,
+                                      "one full 1x3x1024x1024 image")
+    return leg
 
 
 def main():
@@ -340,7 +456,9 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
+    ap.add_argument("--cpu-runs", type=int, default=5,
+                    help="timed oracle runs per configuration (median, after one warm-up)")
     ap.add_argument("--no-sweep", action="store_true", help="skip the conv sweep")
     ap.add_argument("--kernel-reps", type=int, default=100)
     ap.add_argument("--no-models", action="store_true", help="skip the other models (SCUNet, LaMa, BiRefNet)")
@@ -421,11 +539,19 @@ def main():
                 "kernel_us": round(kms * 1e3, 2), "flop_per_launch": flops}
     body_free()
 
+    host_ms = host_path_ms(lambda: model.run(image))
+    cpu_runs = 0 if args.no_cpu else args.cpu_runs
+    log("Real-ESRGAN timed")
     gemm_sweep = None if args.no_sweep else sweep(ctx, stream, args.kernel_reps)
-    models = None if args.no_models else {"scunet": scunet_leg(ctx, max(5, args.steps // 20), 2),
-                                          "lama": lama_leg(ctx, max(5, args.steps // 20), 2),
-                                          "birefnet": birefnet_leg(ctx, max(5, args.steps // 20), 2)}
-    cpu = None if args.no_cpu else cpu_baseline(tensors, image)
+    log("conv sweep timed")
+    models = None
+    if not args.no_models:
+        models = {}
+        for name, leg in (("scunet", scunet_leg), ("lama", lama_leg), ("birefnet", birefnet_leg)):
+            models[name] = leg(ctx, max(5, args.steps // 20), 2, cpu_runs)
+            log(f"{name} timed")
+    cpu = cpu_baseline(tensors, image, cpu_runs) if cpu_runs else None
+    sweep_cpu = cpu_sweep(cpu_runs) if cpu_runs and not args.no_sweep else None
 
     line = {
         "metric": METRIC,
@@ -444,9 +570,11 @@ def main():
                    "global_batch": 1, "height": H, "width": W, "layers": 34, "parallelism": "none",
                    "execution": "one HIP graph per image"},
         "images_per_s": round(1e3 / ms_per_step, 1),
+        "host_path_ms": host_ms,
         "roofline": roofline,
         "cpu_baseline": cpu,
         "gemm_sweep": gemm_sweep,
+        "gemm_sweep_cpu": sweep_cpu,
         "models": models,
         "device": ctx.name,
     }
