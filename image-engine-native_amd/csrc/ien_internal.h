@@ -145,6 +145,9 @@ ien_status window_attention(ien_ctx *ctx, const ien_windows *w, const uint16_t *
                             const float *d_tables, bool packed, uint16_t *d_out);
 
 bool swin_mlp_supported(int c);
+// The device address of ien_swin_run_static's static scratch on `device`
+// (current), looked up once per device.
+hipError_t swin_static_setup(int device);
 ien_status swin_mlp(ien_ctx *ctx, uint16_t *d_map, size_t stride, long rows, int c,
                     const float *gamma, const float *beta, const ien_matrix *fc1,
                     const ien_matrix *fc2);

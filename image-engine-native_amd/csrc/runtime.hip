@@ -129,6 +129,7 @@ ien_status ien_open(int device, ien_ctx **out) {
   ctx->splitk_floats = (size_t)8 << 20;
   if (e == hipSuccess) e = hipMalloc((void **)&ctx->splitk, ctx->splitk_floats * 4);
   if (e == hipSuccess) e = hipEventCreateWithFlags(&ctx->fork_ev, hipEventDisableTiming);
+  if (e == hipSuccess) e = swin_static_setup(device);
   for (int i = 0; i < ien_ctx::BRANCHES && e == hipSuccess; i++) {
     e = hipStreamCreateWithFlags(&ctx->branch[i], hipStreamNonBlocking);
     if (e == hipSuccess) e = hipEventCreateWithFlags(&ctx->join_ev[i], hipEventDisableTiming);

@@ -5,8 +5,19 @@
 #include <cmath>
 #include <cstdint>
 #include <cstring>
+#include <mutex>
+#include <vector>
 
 #include "ien_internal.h"
+
+using namespace ien;
+
+// Scratch of ien_swin_run_static: the unfused path's window rows (4c wide
+// for qkv and the MLP's hidden layer, then c and c) in device memory the
+// library never allocates.  Each device holds its own copy for the life of
+// the process.  In host code `scratch` names a host-side stand-in; the
+// device address comes from hipGetSymbolAddress (swin_static_setup).
+static __device__ __align__(256) uint16_t scratch[IEN_SWIN_STATIC_SCRATCH_BYTES / 2];
 
 struct ien_swin {
   ien_ctx *ctx = nullptr;
@@ -65,6 +76,15 @@ ien_status reserve(ien_swin *b, size_t rows) {
   return IEN_OK;
 }
 
+// The device address of `scratch`, per device (swin_static_setup).
+std::mutex g_scratch_mu;
+std::vector<uint16_t *> g_scratch;
+
+uint16_t *static_scratch(int device) {
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  return device >= 0 && (size_t)device < g_scratch.size() ? g_scratch[device] : nullptr;
+}
+
 ien_status rows_product(ien_ctx *ctx, const uint16_t *in, size_t k, size_t rows,
                         const ien_matrix *m, uint16_t *out, size_t stride, ien_act act,
                         int accumulate) {
@@ -78,6 +98,81 @@ ien_status rows_product(ien_ctx *ctx, const uint16_t *in, size_t k, size_t rows,
   o.layout = IEN_LAYOUT_NHWC;
   o.type = IEN_OUT_F16;
   return ien_multiply_ex(ctx, &x, 0, rows, m, &o, act, nullptr, accumulate);
+}
+
+
+bool rows16_map(const uint16_t *d_map, size_t stride) {
+  return stride % 8 == 0 && ((uintptr_t)d_map & 15) == 0;
+}
+
+// Window rows of a block's scratch for a height x width map (at least the
+// map's tokens), or 0 for an invalid map.
+size_t block_rows(const ien_swin *b, int height, int width) {
+  ien_windows w{b->window, b->shift, height, width};
+  const long wins = ien_window_count(&w);
+  if (wins <= 0) return 0;
+  const size_t rows = (size_t)wins * b->window * b->window, tokens = (size_t)height * width;
+  return rows > tokens ? rows : tokens;
+}
+
+// Whether run_block touches its scratch: the fused passes do not.
+bool needs_scratch(const ien_swin *b, const uint16_t *d_map, size_t stride) {
+  const bool rows16 = rows16_map(d_map, stride);
+  if (b->d_attn_mlp && rows16) return false;
+  const bool attend_fused = b->d_attn_proj && rows16;
+  const bool mlp_fused = swin_mlp_supported(b->c) && rows16;
+  return !(attend_fused && mlp_fused);
+}
+
+// One block (attend, then mlp) with the unfused path's scratch at wide
+// (rows x 4c), tok and att (rows x c each).
+ien_status run_block(ien_swin *b, uint16_t *d_map, size_t stride, int height, int width,
+                     uint16_t *wide, uint16_t *tok, uint16_t *att) {
+  ien_ctx *ctx = b->ctx;
+  const size_t c = (size_t)b->c;
+  ien_windows w{b->window, b->shift, height, width};
+  const long wins = ien_window_count(&w);
+  IEN_CHECK(wins > 0, IEN_ERR_INPUT, "map %d x %d", height, width);
+  const size_t rows = (size_t)wins * b->window * b->window;
+  const size_t tokens = (size_t)height * width;
+  ien_status st = IEN_OK;
+  const float *g1 = b->d_ln, *b1 = b->d_ln + c, *g2 = b->d_ln + 2 * c, *b2 = b->d_ln + 3 * c;
+  const bool rows16 = rows16_map(d_map, stride);
+  // attend (scunet swin.rs:131-232): one fused pass per window where its
+  // kernel takes the width and window, else the window rows, qkv,
+  // attention, projection over the token rows, added back onto the map.
+  if (b->d_attn_mlp && rows16) {
+    // Both halves in one pass per window (32 channels).
+    const AttendMlp mlp{g2, b2, b->d_attn_mlp, b->fc1->d_bias, b->fc2->d_bias};
+    return swin_attend(ctx, &w, d_map, stride, b->c, g1, b1, b->qkv, b->d_attn_proj,
+                       b->proj->d_bias, b->d_packed, &mlp);
+  }
+  if (b->d_attn_proj && rows16) {
+    st = swin_attend(ctx, &w, d_map, stride, b->c, g1, b1, b->qkv, b->d_attn_proj,
+                     b->proj->d_bias, b->d_packed);
+  } else {
+    st = ien_window_gather(ctx, &w, d_map, stride, b->c, g1, b1, tok);
+    if (st == IEN_OK)
+      st = rows_product(ctx, tok, c, rows, b->qkv, wide, 3 * c, IEN_ACT_NONE, 0);
+    if (st == IEN_OK)
+      st = window_attention(ctx, &w, wide, b->c, b->d_packed, true, att);
+    if (st == IEN_OK)
+      st = rows_product(ctx, att, c, rows, b->proj, tok, c, IEN_ACT_NONE, 0);
+    if (st == IEN_OK) st = ien_window_scatter_add(ctx, &w, tok, b->c, d_map, stride);
+  }
+  if (st != IEN_OK) return st;
+  // mlp (scunet swin.rs:236-275): every token normalised, fc1 + GELU, fc2
+  // added back; one fused pass where its kernel takes the width, else a
+  // 1 x 1 window gather (the copy with its LayerNorm) and two products.
+  if (swin_mlp_supported(b->c) && rows16)
+    return swin_mlp(ctx, d_map, stride, (long)tokens, b->c, g2, b2, b->fc1, b->fc2);
+  ien_windows one{1, 0, height, width};
+  if ((st = ien_window_gather(ctx, &one, d_map, stride, b->c, g2, b2, tok)) != IEN_OK)
+    return st;
+  if ((st = rows_product(ctx, tok, c, tokens, b->fc1, wide, 4 * c, IEN_ACT_GELU, 0)) !=
+      IEN_OK)
+    return st;
+  return rows_product(ctx, wide, 4 * c, tokens, b->fc2, d_map, stride, IEN_ACT_NONE, 1);
 }
 
 }  // namespace
@@ -95,9 +190,21 @@ ien_status swin_reserve(ien_swin *b, int height, int width) {
   return reserve(b, rows > tokens ? rows : tokens);
 }
 
+// Once per device, with that device current (ien_open): the device
+// address of `scratch` for ien_swin_run_static.
+hipError_t swin_static_setup(int device) {
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if ((size_t)device < g_scratch.size() && g_scratch[device]) return hipSuccess;
+  void *ptr = nullptr;
+  hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+  if (e != hipSuccess) return e;
+  if ((size_t)device >= g_scratch.size()) g_scratch.resize(device + 1, nullptr);
+  g_scratch[device] = (uint16_t *)ptr;
+  return hipSuccess;
+}
+
 }  // namespace ien
 
-using namespace ien;
 
 extern "C" {
 
@@ -168,52 +275,32 @@ void ien_swin_free(ien_swin *block) { release(block); }
 
 ien_status ien_swin_run(ien_swin *b, uint16_t *d_map, size_t stride, int height, int width) {
   IEN_CHECK(b && d_map, IEN_ERR_INPUT, "null argument");
-  ien_ctx *ctx = b->ctx;
-  const size_t c = (size_t)b->c;
-  ien_windows w{b->window, b->shift, height, width};
-  const long wins = ien_window_count(&w);
-  IEN_CHECK(wins > 0, IEN_ERR_INPUT, "map %d x %d", height, width);
-  const size_t rows = (size_t)wins * b->window * b->window;
-  const size_t tokens = (size_t)height * width;
-  ien_status st = reserve(b, rows > tokens ? rows : tokens);
+  const size_t rows = block_rows(b, height, width);
+  IEN_CHECK(rows > 0, IEN_ERR_INPUT, "map %d x %d", height, width);
+  ien_status st = reserve(b, rows);
   if (st != IEN_OK) return st;
-  const float *g1 = b->d_ln, *b1 = b->d_ln + c, *g2 = b->d_ln + 2 * c, *b2 = b->d_ln + 3 * c;
-  const bool rows16 = stride % 8 == 0 && ((uintptr_t)d_map & 15) == 0;
-  // attend (scunet swin.rs:131-232): one fused pass per window where its
-  // kernel takes the width and window, else the window rows, qkv,
-  // attention, projection over the token rows, added back onto the map.
-  if (b->d_attn_mlp && rows16) {
-    // Both halves in one pass per window (32 channels).
-    const AttendMlp mlp{g2, b2, b->d_attn_mlp, b->fc1->d_bias, b->fc2->d_bias};
-    return swin_attend(ctx, &w, d_map, stride, b->c, g1, b1, b->qkv, b->d_attn_proj,
-                       b->proj->d_bias, b->d_packed, &mlp);
+  return run_block(b, d_map, stride, height, width, b->d_wide, b->d_tok, b->d_att);
+}
+
+ien_status ien_swin_run_static(ien_swin *b, uint16_t *d_map, size_t stride, int height,
+                               int width) {
+  IEN_CHECK(b && d_map, IEN_ERR_INPUT, "null argument");
+  const size_t rows = block_rows(b, height, width);
+  IEN_CHECK(rows > 0, IEN_ERR_INPUT, "map %d x %d", height, width);
+  uint16_t *wide = nullptr, *tok = nullptr, *att = nullptr;
+  if (needs_scratch(b, d_map, stride)) {
+    const size_t c = (size_t)b->c, bytes = rows * 6 * c * 2;
+    IEN_CHECK(bytes <= IEN_SWIN_STATIC_SCRATCH_BYTES, IEN_ERR_INPUT,
+              "a %d x %d map of %d channels needs %zu bytes of scratch; the static scratch "
+              "holds %zu",
+              height, width, b->c, bytes, (size_t)IEN_SWIN_STATIC_SCRATCH_BYTES);
+    uint16_t *base = static_scratch(b->ctx->device);
+    IEN_CHECK(base, IEN_ERR_GPU, "no static scratch on device %d", b->ctx->device);
+    wide = base;
+    tok = wide + rows * 4 * c;
+    att = tok + rows * c;
   }
-  if (b->d_attn_proj && rows16) {
-    st = swin_attend(ctx, &w, d_map, stride, b->c, g1, b1, b->qkv, b->d_attn_proj,
-                     b->proj->d_bias, b->d_packed);
-  } else {
-    st = ien_window_gather(ctx, &w, d_map, stride, b->c, g1, b1, b->d_tok);
-    if (st == IEN_OK)
-      st = rows_product(ctx, b->d_tok, c, rows, b->qkv, b->d_wide, 3 * c, IEN_ACT_NONE, 0);
-    if (st == IEN_OK)
-      st = window_attention(ctx, &w, b->d_wide, b->c, b->d_packed, true, b->d_att);
-    if (st == IEN_OK)
-      st = rows_product(ctx, b->d_att, c, rows, b->proj, b->d_tok, c, IEN_ACT_NONE, 0);
-    if (st == IEN_OK) st = ien_window_scatter_add(ctx, &w, b->d_tok, b->c, d_map, stride);
-  }
-  if (st != IEN_OK) return st;
-  // mlp (scunet swin.rs:236-275): every token normalised, fc1 + GELU, fc2
-  // added back; one fused pass where its kernel takes the width, else a
-  // 1 x 1 window gather (the copy with its LayerNorm) and two products.
-  if (swin_mlp_supported(b->c) && rows16)
-    return swin_mlp(ctx, d_map, stride, (long)tokens, b->c, g2, b2, b->fc1, b->fc2);
-  ien_windows one{1, 0, height, width};
-  if ((st = ien_window_gather(ctx, &one, d_map, stride, b->c, g2, b2, b->d_tok)) != IEN_OK)
-    return st;
-  if ((st = rows_product(ctx, b->d_tok, c, tokens, b->fc1, b->d_wide, 4 * c, IEN_ACT_GELU, 0)) !=
-      IEN_OK)
-    return st;
-  return rows_product(ctx, b->d_wide, 4 * c, tokens, b->fc2, d_map, stride, IEN_ACT_NONE, 1);
+  return run_block(b, d_map, stride, height, width, wide, tok, att);
 }
 
 }  // extern "C"

@@ -34,6 +34,7 @@ EXPORTS = (
     "ien_model_run_device", "ien_model_set_graph",
     "ien_window_count", "ien_position_bias", "ien_bias_tables", "ien_window_gather",
     "ien_window_attention", "ien_window_scatter_add", "ien_swin_new", "ien_swin_free", "ien_swin_run",
+    "ien_swin_run_static",
     "ien_resize", "ien_pad_image", "ien_crop", "ien_gather_2x2", "ien_scatter_2x2", "ien_add",
     "ien_fourier_new", "ien_fourier_free", "ien_fourier_half", "ien_fourier_forward",
     "ien_fourier_inverse",
@@ -162,6 +163,7 @@ def load():
         L.ien_swin_free.argtypes = [vp]
         L.ien_swin_free.restype = None
         L.ien_swin_run.argtypes = [vp, vp, sz, i, i]
+        L.ien_swin_run_static.argtypes = [vp, vp, sz, i, i]
         L.ien_resize.argtypes = [vp, vp, sz, sz, sz, sz, vp, sz, sz, sz, i, i]
         L.ien_pad_image.argtypes = [vp, i, vp, vp, sz, sz, sz, vp, sz]
         L.ien_crop.argtypes = [vp, vp, sz, sz, sz, sz, sz, vp]
@@ -454,6 +456,11 @@ class Swin:
 
     def run(self, map_, stride, height, width):
         check(load().ien_swin_run(self.h, _ptr(map_), stride, height, width))
+
+    def run_static(self, map_, stride, height, width):
+        """ien_swin_run_static: the same block with the library's static
+        scratch (allocates nothing)."""
+        check(load().ien_swin_run_static(self.h, _ptr(map_), stride, height, width))
 
     def free(self):
         if self.h:

@@ -317,6 +317,20 @@ void ien_swin_free(ien_swin *block);
  * GELU, fc2 added back.  Scratch is the block's own, grown on demand. */
 ien_status ien_swin_run(ien_swin *block, uint16_t *d_map, size_t stride, int height, int width);
 
+/* No counterpart in the reference: ien_swin_run for callers that cannot
+ * allocate device memory (code under HIP graph capture, serving loops that
+ * forbid hipMalloc).  The same kernels and results as ien_swin_run, but the
+ * unfused path's scratch (window rows of 6c halves, at least height x width
+ * of them) lives in a static device array of IEN_SWIN_STATIC_SCRATCH_BYTES
+ * per GPU, held until the process ends; this call allocates and frees
+ * nothing.  A map whose scratch would not fit is refused with
+ * IEN_ERR_INPUT.  Every call on one GPU shares that GPU's array (its
+ * contents are overwritten before they are read), so calls that overlap on
+ * one GPU, from any context or stream, race. */
+#define IEN_SWIN_STATIC_SCRATCH_BYTES ((size_t)32 << 20)
+ien_status ien_swin_run_static(ien_swin *block, uint16_t *d_map, size_t stride, int height,
+                               int width);
+
 /* ---- Fourier units: crates/lama-native/src/fourier.rs ----------------- */
 /* fourier.rs:262-288 Fourier::new: the transforms of height x width maps
  * (sides 1 .. 1024); a spectrum has half = width / 2 + 1 columns. */
