@@ -58,6 +58,6 @@ void birefnet_free(Birefnet *b);
 // graph capture); *grew is set when buffers were replaced.
 ien_status birefnet_reserve(Birefnet *b, size_t side, bool *grew);
 ien_status birefnet_enqueue(Birefnet *b, const float *d_image, size_t side, float *d_logits,
-                            hipEvent_t *events);
+                            Steps *steps);
 
 }  // namespace ien

@@ -473,7 +473,7 @@ ien_status block_run(Birefnet *b, const BirefnetBlock &B, const uint16_t *in, in
 // rows 2 c wide) directly for the full size, through `tmp` and a resize for
 // the half size.
 ien_status backbone_run(Birefnet *b, const uint16_t *img, int side, bool half,
-                        hipEvent_t *events, int *step) {
+                        Steps *steps, int *step) {
   ien_ctx *ctx = b->ctx;
   int grid = side / 4;
   const long tokens = (long)grid * grid;
@@ -513,7 +513,7 @@ ien_status backbone_run(Birefnet *b, const uint16_t *img, int side, bool half,
                           IEN_ACT_NONE, 0);
       grid /= 2;
     }
-    if (st == IEN_OK && events) IEN_HIP(hipEventRecord(events[*step], ctx->stream));
+    if (st == IEN_OK && steps) st = steps->step(ctx->stream);
     ++*step;
   }
   return st;
@@ -711,7 +711,7 @@ ien_status birefnet_reserve(Birefnet *b, size_t side, bool *grew) {
 
 // lib.rs:144-171 run_normalized and decoder.rs:813-926 Decoder::run.
 ien_status birefnet_enqueue(Birefnet *b, const float *d_image, size_t side_, float *d_logits,
-                            hipEvent_t *events) {
+                            Steps *steps) {
   ien_ctx *ctx = b->ctx;
   IEN_CHECK(b->side >= side_ && side_ % 64 == 0, IEN_ERR_INPUT, "maps not reserved for side %zu",
             side_);
@@ -721,8 +721,8 @@ ien_status birefnet_enqueue(Birefnet *b, const float *d_image, size_t side_, flo
   if (st == IEN_OK)
     st = ien_resize(ctx, b->img16, side, side, 3, 3, b->half16, side / 2, side / 2, 3, IEN_OUT_F16,
                     0);
-  if (st == IEN_OK) st = backbone_run(b, b->img16, side, false, events, &step);
-  if (st == IEN_OK) st = backbone_run(b, b->half16, side / 2, true, events, &step);
+  if (st == IEN_OK) st = backbone_run(b, b->img16, side, false, steps, &step);
+  if (st == IEN_OK) st = backbone_run(b, b->half16, side / 2, true, steps, &step);
   if (st != IEN_OK) return st;
   // The squeeze block's input: levels 1..3 resized to level 4's grid, then
   // level 4 (decoder.rs:840-859).
@@ -738,7 +738,7 @@ ien_status birefnet_enqueue(Birefnet *b, const float *d_image, size_t side_, flo
     st = copy_cols(ctx, b->level[3], (long)g4 * g4, 2 * STAGE_C[3], 2 * STAGE_C[3], b->x4 + offset,
                    SQUEEZE_CIN);
   if (st == IEN_OK) st = block_run(b, b->dec[0], b->x4, g4, g4, b->prev);
-  if (st == IEN_OK && events) IEN_HIP(hipEventRecord(events[step], ctx->stream));
+  if (st == IEN_OK && steps) st = steps->step(ctx->stream);
   step++;
   int prev_grid = g4;
   for (int i = 0; i < 4 && st == IEN_OK; i++) {
@@ -782,7 +782,7 @@ ien_status birefnet_enqueue(Birefnet *b, const float *d_image, size_t side_, flo
       st = conv(ctx, b->mid, g, g, INTER, INTER, 3, b->patch_out[i], b->in + main_c, cin,
                 IEN_ACT_NONE, 0);
     if (st == IEN_OK) st = block_run(b, b->dec[i + 1], b->in, g, g, b->prev);
-    if (st == IEN_OK && events) IEN_HIP(hipEventRecord(events[step], ctx->stream));
+    if (st == IEN_OK && steps) st = steps->step(ctx->stream);
     step++;
     prev_grid = g;
   }
@@ -798,7 +798,7 @@ ien_status birefnet_enqueue(Birefnet *b, const float *d_image, size_t side_, flo
                      d_image, side, b->d_full, b->head_bias, d_logits);
   IEN_HIP(hipGetLastError());
   st = ien_resize(ctx, b->low, prev_grid, prev_grid, 1, 1, d_logits, side, side, 1, IEN_OUT_F32, 1);
-  if (st == IEN_OK && events) IEN_HIP(hipEventRecord(events[step], ctx->stream));
+  if (st == IEN_OK && steps) st = steps->step(ctx->stream);
   return st;
 }
 

@@ -98,6 +98,31 @@ struct Branch {
   Branch &operator=(const Branch &) = delete;
 };
 
+// Progress of a run (realesrgan-native lib.rs:168-188, scunet-native
+// lib.rs:205-215): a model driver calls step() after issuing each step's
+// work (a layer, block or stage).  step() records an event for that step,
+// then waits for the previous step and reports it, so one step stays
+// queued on the GPU while the callback runs.  When the callback asks to
+// stop, step() returns IEN_ERR_CANCELLED and the driver issues nothing
+// more; the run ends after the step already queued.  `total` counts the
+// steps of the whole call (tiles x steps per image).
+struct Steps {
+  ien_progress progress = nullptr;
+  void *user = nullptr;
+  int total = 0, issued = 0, reported = 0;
+  hipEvent_t ev[2] = {nullptr, nullptr};
+  Steps(ien_progress p, void *u, int t) : progress(p), user(u), total(t) {}
+  ~Steps();
+  Steps(const Steps &) = delete;
+  Steps &operator=(const Steps &) = delete;
+  ien_status step(hipStream_t stream);
+  // Wait for the last issued step and report it.
+  ien_status drain();
+
+ private:
+  ien_status report_through(int done);
+};
+
 // Pack row-major k x n weights (as floats) into the fragment layout above.
 std::vector<uint16_t> pack_fragments(const float *w, size_t k, size_t n, int *kb, int *nb);
 
@@ -130,6 +155,17 @@ struct ConvCall {
 };
 
 ien_status launch_conv(ien_ctx *ctx, const ConvCall &c);
+
+// io.hip: the 8-bit image passes of the models' u8 entry points, on the
+// context's stream (to_float, to_byte, LaMa's mask and compositing,
+// BiRefNet's normalisation of interleaved RGB).
+ien_status bytes_to_floats(ien_ctx *ctx, const uint8_t *src, float *dst, size_t n);
+ien_status floats_to_bytes(ien_ctx *ctx, const float *src, uint8_t *dst, size_t n);
+ien_status mask_bytes(ien_ctx *ctx, const uint8_t *src, float *dst, size_t n);
+ien_status normalize_bytes(ien_ctx *ctx, const uint8_t *src, size_t pixels, const float mean[3],
+                           const float deviation[3], float *dst);
+ien_status composite_bytes(ien_ctx *ctx, const uint8_t *rgb, const uint8_t *mask,
+                           const float *pred, size_t pixels, uint8_t *out);
 
 // swin.hip: a block's scratch grown for a height x width map in advance.
 ien_status swin_reserve(ien_swin *b, int height, int width);

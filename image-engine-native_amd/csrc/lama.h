@@ -39,6 +39,6 @@ void lama_padded(size_t width, size_t height, size_t *pw, size_t *ph);
 // capture); *grew is set when buffers or the plan were replaced.
 ien_status lama_reserve(Lama *l, size_t pw, size_t ph, bool *grew);
 ien_status lama_enqueue(Lama *l, const float *d_image, const float *d_mask, size_t width,
-                        size_t height, float *d_out, hipEvent_t *events);
+                        size_t height, float *d_out, Steps *steps);
 
 }  // namespace ien

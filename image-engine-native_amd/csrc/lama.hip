@@ -281,7 +281,7 @@ ien_status lama_reserve(Lama *l, size_t pw, size_t ph, bool *grew) {
 
 // network.rs:415-489 Network::run.
 ien_status lama_enqueue(Lama *l, const float *d_image, const float *d_mask, size_t width,
-                        size_t height, float *d_out, hipEvent_t *events) {
+                        size_t height, float *d_out, Steps *steps) {
   ien_ctx *ctx = l->ctx;
   size_t pw, ph;
   lama_padded(width, height, &pw, &ph);
@@ -289,9 +289,8 @@ ien_status lama_enqueue(Lama *l, const float *d_image, const float *d_mask, size
             "LaMa maps not reserved for %zu x %zu", pw, ph);
   int step = 0;
   auto done = [&]() -> ien_status {
-    if (events) IEN_HIP(hipEventRecord(events[step], ctx->stream));
     step++;
-    return IEN_OK;
+    return steps ? steps->step(ctx->stream) : IEN_OK;
   };
   // network.rs:346-370 masked_rows: image (1 - m) | m, mirrored to x 8.
   ien_status st = ien_pad_image(ctx, IEN_PAD_SYMMETRIC_MASKED, d_image, d_mask, width, height,

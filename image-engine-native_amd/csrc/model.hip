@@ -163,11 +163,18 @@ struct ien_model {
   const float *graph_in = nullptr, *graph_mask = nullptr;
   float *graph_out = nullptr;
   size_t graph_w = 0, graph_h = 0;
+  // 8-bit images of the u8 entry point on the device (ien_model_run_u8).
+  uint8_t *d_bytes = nullptr;
+  size_t bytes_cap = 0;
 };
 
 namespace ien {
 
 static constexpr int FEATURES = 64, STEPS = 34, SCALE = 4;
+// realesrgan-native lib.rs:34-41 GPU_TILE, MARGIN (= network::REACH, the 34
+// layers' reach); scunet-native lib.rs:33-38 TILE, MARGIN.
+static constexpr size_t ESRGAN_GPU_TILE = 768, ESRGAN_MARGIN = 34;
+static constexpr size_t SCUNET_TILE = 896, SCUNET_MARGIN = 64;
 
 static void free_maps(Maps &m) {
   (void)hipFree(m.image);
@@ -245,9 +252,9 @@ static ien_status load_esrgan(ien_model *model, const TensorSource &take) {
 }
 
 // The launches of one run: input to f16, 34 convolutions, shuffle.  With
-// `events`, one event is recorded after each layer for progress reports.
+// `steps`, progress is reported after each layer.
 static ien_status enqueue_esrgan(ien_model *model, const float *d_image, size_t width,
-                                 size_t height, float *d_out, hipEvent_t *events) {
+                                 size_t height, float *d_out, Steps *steps) {
   ien_ctx *ctx = model->ctx;
   Maps &m = model->maps;
   const size_t pixels = width * height;
@@ -282,7 +289,7 @@ static ien_status enqueue_esrgan(ien_model *model, const float *d_image, size_t 
       st = ien_pixel_shuffle_add(ctx, dst, (size_t)l.cout, d_image, width, height, d_out);
       if (st != IEN_OK) return st;
     }
-    if (events) IEN_HIP(hipEventRecord(events[i], ctx->stream));
+    if (steps && (st = steps->step(ctx->stream)) != IEN_OK) return st;
   }
   return IEN_OK;
 }
@@ -330,14 +337,14 @@ static ien_status prepare(ien_model *model, size_t width, size_t height) {
 }
 
 static ien_status enqueue(ien_model *model, const float *d_image, const float *d_mask,
-                          size_t width, size_t height, float *d_out, hipEvent_t *events) {
+                          size_t width, size_t height, float *d_out, Steps *steps) {
   if (model->kind == IEN_MODEL_LAMA)
-    return lama_enqueue(model->lama.get(), d_image, d_mask, width, height, d_out, events);
+    return lama_enqueue(model->lama.get(), d_image, d_mask, width, height, d_out, steps);
   if (model->kind == IEN_MODEL_BIREFNET)
-    return birefnet_enqueue(model->birefnet.get(), d_image, width, d_out, events);
+    return birefnet_enqueue(model->birefnet.get(), d_image, width, d_out, steps);
   if (model->kind == IEN_MODEL_SCUNET)
-    return scunet_enqueue(model->scunet.get(), d_image, width, height, d_out, events);
-  return enqueue_esrgan(model, d_image, width, height, d_out, events);
+    return scunet_enqueue(model->scunet.get(), d_image, width, height, d_out, steps);
+  return enqueue_esrgan(model, d_image, width, height, d_out, steps);
 }
 
 static ien_status check_size(const ien_model *model, size_t width, size_t height) {
@@ -355,6 +362,179 @@ static ien_status check_size(const ien_model *model, size_t width, size_t height
   if (width > (1u << 15) || height > (1u << 15) || width * height > (1ull << 28))
     return fail(IEN_ERR_INPUT, "%zu x %zu image is too large", width, height);
   return IEN_OK;
+}
+
+static ien_status check_mask(const ien_model *model, bool has_mask) {
+  if (model->kind == IEN_MODEL_LAMA)
+    IEN_CHECK(has_mask, IEN_ERR_INPUT, "LaMa needs a mask");
+  else
+    IEN_CHECK(!has_mask, IEN_ERR_INPUT, "this model takes no mask");
+  return IEN_OK;
+}
+
+// Device buffers of a run through host buffers: the f32 input, mask and
+// output of a width x height image, grown on demand and never shrunk, with
+// the model's maps reserved for that size.
+struct Staging {
+  float *in = nullptr, *mask = nullptr, *out = nullptr;
+};
+
+static ien_status grow(float **p, size_t floats) {
+  (void)hipFree(*p);
+  *p = nullptr;
+  IEN_HIP(hipMalloc((void **)p, floats * 4));
+  return IEN_OK;
+}
+
+static ien_status stage(ien_model *model, size_t width, size_t height, Staging *io) {
+  ien_ctx *ctx = model->ctx;
+  const size_t pixels = width * height;
+  ien_status st = prepare(model, width, height);
+  if (st != IEN_OK) return st;
+  size_t *staged = nullptr;
+  float **in = nullptr, **mask = nullptr, **out = nullptr;
+  if (model->kind == IEN_MODEL_LAMA) {
+    Lama &l = *model->lama;
+    staged = &l.staged;
+    in = &l.d_in, mask = &l.d_mask, out = &l.d_out;
+  } else if (model->kind == IEN_MODEL_BIREFNET) {
+    Birefnet &b = *model->birefnet;
+    staged = &b.staged;
+    in = &b.d_in, out = &b.d_out;
+  } else if (model->kind == IEN_MODEL_SCUNET) {
+    Scunet &s = *model->scunet;
+    staged = &s.staged;
+    in = &s.d_in, out = &s.d_out;
+  } else {
+    if ((st = ensure_maps(model, pixels, true)) != IEN_OK) return st;
+    io->in = model->maps.d_in;
+    io->out = model->maps.d_out;
+    return IEN_OK;
+  }
+  if (*staged < pixels) {
+    IEN_HIP(hipStreamSynchronize(ctx->stream));
+    *staged = 0;
+    if ((st = grow(in, pixels * 3)) != IEN_OK) return st;
+    if (mask && (st = grow(mask, pixels)) != IEN_OK) return st;
+    if ((st = grow(out, pixels * out_per_pixel(model))) != IEN_OK) return st;
+    *staged = pixels;
+  }
+  io->in = *in;
+  io->mask = mask ? *mask : nullptr;
+  io->out = *out;
+  return IEN_OK;
+}
+
+// Device copies of 8-bit images (input, mask, output), 256-byte aligned
+// parts of one buffer grown on demand.
+struct Bytes {
+  uint8_t *in = nullptr, *mask = nullptr, *out = nullptr;
+};
+
+static size_t round256(size_t n) { return (n + 255) & ~(size_t)255; }
+
+static ien_status stage_bytes(ien_model *model, size_t in, size_t mask, size_t out, Bytes *b) {
+  const size_t need = round256(in) + round256(mask) + round256(out);
+  if (model->bytes_cap < need) {
+    IEN_HIP(hipStreamSynchronize(model->ctx->stream));
+    (void)hipFree(model->d_bytes);
+    model->d_bytes = nullptr;
+    model->bytes_cap = 0;
+    IEN_HIP(hipMalloc((void **)&model->d_bytes, need));
+    model->bytes_cap = need;
+  }
+  b->in = model->d_bytes;
+  b->mask = b->in + round256(in);
+  b->out = b->mask + round256(mask);
+  return IEN_OK;
+}
+
+// After a run's launches: the last step reported, then the stream drained
+// (a cancelled run still finishes the work already queued, and the model
+// stays usable).
+static ien_status finish_run(ien_model *model, ien_status st, Steps *steps) {
+  if (st == IEN_OK && steps) st = steps->drain();
+  const hipError_t e = hipStreamSynchronize(model->ctx->stream);
+  if (st != IEN_OK) return st;
+  if (e != hipSuccess) return fail(IEN_ERR_GPU, "run: %s", hipGetErrorString(e));
+  return IEN_OK;
+}
+
+// realesrgan-native lib.rs:230-289 / scunet-native lib.rs:192-247 tiled:
+// a grid of equal tiles at most `tile` pixels on a side, each run with up
+// to `margin` pixels of its surroundings, only the tile's own output kept.
+// T is float (run_float_tiled) or uint8_t (Model::run: to_float on the way
+// in, to_byte on the way out, both on the device).
+template <typename T>
+static ien_status run_tiled(ien_model *model, const T *image, size_t width, size_t height,
+                            size_t tile, size_t margin, T *out, ien_progress progress, void *user) {
+  IEN_CHECK(model->kind == IEN_MODEL_REALESRGAN || model->kind == IEN_MODEL_SCUNET,
+            IEN_ERR_INPUT, "only Real-ESRGAN and SCUNet run in tiles");
+  ien_status st = check_size(model, width, height);
+  if (st != IEN_OK) return st;
+  IEN_CHECK(tile > 0, IEN_ERR_INPUT, "tile size 0");
+  ien_ctx *ctx = model->ctx;
+  IEN_HIP(hipSetDevice(ctx->device));
+  constexpr bool bytes = sizeof(T) == 1;
+  const size_t scale = model->kind == IEN_MODEL_REALESRGAN ? SCALE : 1, ow = width * scale;
+  const size_t cols = (width + tile - 1) / tile, rows = (height + tile - 1) / tile;
+  auto region = [&](size_t j, size_t i, size_t r[8]) {
+    const size_t y0 = j * height / rows, y1 = (j + 1) * height / rows;
+    const size_t x0 = i * width / cols, x1 = (i + 1) * width / cols;
+    const size_t rx0 = x0 > margin ? x0 - margin : 0, ry0 = y0 > margin ? y0 - margin : 0;
+    const size_t rx1 = std::min(x1 + margin, width), ry1 = std::min(y1 + margin, height);
+    const size_t v[8] = {x0, x1, y0, y1, rx0, rx1, ry0, ry1};
+    std::copy_n(v, 8, r);
+  };
+  // The largest region first, so that the buffers grow once.
+  size_t big_w = 0, big_h = 0;
+  for (size_t j = 0; j < rows; j++)
+    for (size_t i = 0; i < cols; i++) {
+      size_t r[8];
+      region(j, i, r);
+      if ((r[5] - r[4]) * (r[7] - r[6]) > big_w * big_h) big_w = r[5] - r[4], big_h = r[7] - r[6];
+    }
+  Staging io;
+  if ((st = stage(model, big_w, big_h, &io)) != IEN_OK) return st;
+  Bytes b;
+  if (bytes && (st = stage_bytes(model, big_w * big_h * 3, 0,
+                                 big_w * big_h * 3 * scale * scale, &b)) != IEN_OK)
+    return st;
+  const int per_tile = model_steps(model);
+  Steps steps(progress, user, (int)(cols * rows) * per_tile);
+  Steps *sp = progress ? &steps : nullptr;
+  for (size_t j = 0; j < rows && st == IEN_OK; j++) {
+    for (size_t i = 0; i < cols && st == IEN_OK; i++) {
+      size_t r[8];
+      region(j, i, r);
+      const size_t x0 = r[0], x1 = r[1], y0 = r[2], y1 = r[3], rx0 = r[4], ry0 = r[6];
+      const size_t rw = r[5] - r[4], rh = r[7] - r[6];
+      if ((st = stage(model, rw, rh, &io)) != IEN_OK) break;
+      const T *src = image + (ry0 * width + rx0) * 3;
+      if (bytes) {
+        IEN_HIP(hipMemcpy2DAsync(b.in, rw * 3, src, width * 3, rw * 3, rh, hipMemcpyHostToDevice,
+                                 ctx->stream));
+        if ((st = bytes_to_floats(ctx, b.in, io.in, rw * rh * 3)) != IEN_OK) break;
+      } else {
+        IEN_HIP(hipMemcpy2DAsync(io.in, rw * 3 * 4, src, width * 3 * 4, rw * 3 * 4, rh,
+                                 hipMemcpyHostToDevice, ctx->stream));
+      }
+      if ((st = enqueue(model, io.in, nullptr, rw, rh, io.out, sp)) != IEN_OK) break;
+      // The tile's own output: rows y0 .. y1, columns x0 .. x1 (scaled).
+      const size_t rws = rw * scale, cw = (x1 - x0) * scale;
+      const size_t from = ((y0 - ry0) * scale * rws + (x0 - rx0) * scale) * 3;
+      T *dst = out + (y0 * scale * ow + x0 * scale) * 3;
+      if (bytes) {
+        if ((st = floats_to_bytes(ctx, io.out, b.out, rws * rh * scale * 3)) != IEN_OK) break;
+        IEN_HIP(hipMemcpy2DAsync(dst, ow * 3, b.out + from, rws * 3, cw * 3, (y1 - y0) * scale,
+                                 hipMemcpyDeviceToHost, ctx->stream));
+      } else {
+        IEN_HIP(hipMemcpy2DAsync(dst, ow * 3 * 4, io.out + from, rws * 3 * 4, cw * 3 * 4,
+                                 (y1 - y0) * scale, hipMemcpyDeviceToHost, ctx->stream));
+      }
+    }
+  }
+  return finish_run(model, st, sp);
 }
 
 }  // namespace ien
@@ -468,6 +648,7 @@ void ien_model_free(ien_model *model) {
   if (model->lama) lama_free(model->lama.get());
   if (model->birefnet) birefnet_free(model->birefnet.get());
   free_maps(model->maps);
+  (void)hipFree(model->d_bytes);
   delete model;
 }
 
@@ -523,102 +704,76 @@ ien_status ien_model_run_device(ien_model *model, const float *d_image, const fl
 ien_status ien_model_run(ien_model *model, const float *image, const float *mask, size_t width,
                          size_t height, float *out, ien_progress progress, void *user) {
   IEN_CHECK(model && image && out, IEN_ERR_INPUT, "null argument");
-  if (model->kind == IEN_MODEL_LAMA)
-    IEN_CHECK(mask != nullptr, IEN_ERR_INPUT, "LaMa needs a mask");
-  else
-    IEN_CHECK(mask == nullptr, IEN_ERR_INPUT, "this model takes no mask");
-  ien_status st = check_size(model, width, height);
+  ien_status st = check_mask(model, mask != nullptr);
+  if (st == IEN_OK) st = check_size(model, width, height);
   if (st != IEN_OK) return st;
   ien_ctx *ctx = model->ctx;
   IEN_HIP(hipSetDevice(ctx->device));
   const size_t pixels = width * height;
-  float *d_in = nullptr, *d_out = nullptr, *d_mask = nullptr;
-  if (model->kind == IEN_MODEL_LAMA) {
-    Lama &l = *model->lama;
-    st = prepare(model, width, height);
-    if (st != IEN_OK) return st;
-    if (l.staged < pixels) {
-      IEN_HIP(hipStreamSynchronize(ctx->stream));
-      (void)hipFree(l.d_in);
-      (void)hipFree(l.d_mask);
-      (void)hipFree(l.d_out);
-      l.d_in = l.d_mask = l.d_out = nullptr;
-      l.staged = 0;
-      IEN_HIP(hipMalloc(&l.d_in, pixels * 3 * 4));
-      IEN_HIP(hipMalloc(&l.d_mask, pixels * 4));
-      IEN_HIP(hipMalloc(&l.d_out, pixels * 3 * 4));
-      l.staged = pixels;
-    }
-    d_in = l.d_in;
-    d_mask = l.d_mask;
-    d_out = l.d_out;
-    IEN_HIP(hipMemcpyAsync(d_mask, mask, pixels * 4, hipMemcpyHostToDevice, ctx->stream));
-  } else if (model->kind == IEN_MODEL_BIREFNET) {
-    Birefnet &b = *model->birefnet;
-    st = prepare(model, width, height);
-    if (st != IEN_OK) return st;
-    if (b.staged < pixels) {
-      IEN_HIP(hipStreamSynchronize(ctx->stream));
-      (void)hipFree(b.d_in);
-      (void)hipFree(b.d_out);
-      b.d_in = b.d_out = nullptr;
-      b.staged = 0;
-      IEN_HIP(hipMalloc(&b.d_in, pixels * 3 * 4));
-      IEN_HIP(hipMalloc(&b.d_out, pixels * 4));
-      b.staged = pixels;
-    }
-    d_in = b.d_in;
-    d_out = b.d_out;
-  } else if (model->kind == IEN_MODEL_SCUNET) {
-    Scunet &s = *model->scunet;
-    st = prepare(model, width, height);
-    if (st != IEN_OK) return st;
-    if (s.staged < pixels) {
-      IEN_HIP(hipStreamSynchronize(ctx->stream));
-      (void)hipFree(s.d_in);
-      (void)hipFree(s.d_out);
-      s.d_in = s.d_out = nullptr;
-      s.staged = 0;
-      IEN_HIP(hipMalloc(&s.d_in, pixels * 3 * 4));
-      IEN_HIP(hipMalloc(&s.d_out, pixels * 3 * 4));
-      s.staged = pixels;
-    }
-    d_in = s.d_in;
-    d_out = s.d_out;
-  } else {
-    st = ensure_maps(model, pixels, true);
-    if (st != IEN_OK) return st;
-    d_in = model->maps.d_in;
-    d_out = model->maps.d_out;
-  }
-  IEN_HIP(hipMemcpyAsync(d_in, image, pixels * 3 * 4, hipMemcpyHostToDevice, ctx->stream));
-  const int steps = model_steps(model);
-  std::vector<hipEvent_t> events;
-  if (progress) {
-    events.resize(steps);
-    for (auto &e : events) IEN_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
-  }
-  st = enqueue(model, d_in, d_mask, width, height, d_out, progress ? events.data() : nullptr);
-  bool cancelled = false;
-  if (st == IEN_OK && progress) {
-    // lib.rs:168-188 (SCUNet lib.rs:205-215): progress after each layer or
-    // block, in order; a break stops the run with Cancelled and leaves the
-    // model usable.
-    for (int i = 0; i < steps && !cancelled; i++) {
-      hipError_t e = hipEventSynchronize(events[i]);
-      if (e != hipSuccess) {
-        st = fail(IEN_ERR_GPU, "step %d: %s", i, hipGetErrorString(e));
-        break;
-      }
-      if (progress((float)(i + 1) / steps, user) != 0) cancelled = true;
-    }
-  }
-  hipError_t e = hipStreamSynchronize(ctx->stream);
-  for (auto &ev : events) (void)hipEventDestroy(ev);
+  Staging io;
+  if ((st = stage(model, width, height, &io)) != IEN_OK) return st;
+  if (mask) IEN_HIP(hipMemcpyAsync(io.mask, mask, pixels * 4, hipMemcpyHostToDevice, ctx->stream));
+  IEN_HIP(hipMemcpyAsync(io.in, image, pixels * 3 * 4, hipMemcpyHostToDevice, ctx->stream));
+  Steps steps(progress, user, model_steps(model));
+  Steps *sp = progress ? &steps : nullptr;
+  st = enqueue(model, io.in, mask ? io.mask : nullptr, width, height, io.out, sp);
+  if ((st = finish_run(model, st, sp)) != IEN_OK) return st;
+  IEN_HIP(hipMemcpy(out, io.out, pixels * out_per_pixel(model) * 4, hipMemcpyDeviceToHost));
+  return IEN_OK;
+}
+
+ien_status ien_model_run_tiled(ien_model *model, const float *image, size_t width,
+                               size_t height, size_t tile, size_t margin, float *out,
+                               ien_progress progress, void *user) {
+  IEN_CHECK(model && image && out, IEN_ERR_INPUT, "null argument");
+  return run_tiled(model, image, width, height, tile, margin, out, progress, user);
+}
+
+ien_status ien_model_run_u8(ien_model *model, const uint8_t *rgb, const uint8_t *mask,
+                            size_t width, size_t height, void *out, ien_progress progress,
+                            void *user) {
+  IEN_CHECK(model && rgb && out, IEN_ERR_INPUT, "null argument");
+  ien_status st = check_mask(model, mask != nullptr);
   if (st != IEN_OK) return st;
-  if (e != hipSuccess) return fail(IEN_ERR_GPU, "run: %s", hipGetErrorString(e));
-  if (cancelled) return fail(IEN_ERR_CANCELLED, "the progress callback stopped the run");
-  IEN_HIP(hipMemcpy(out, d_out, pixels * out_per_pixel(model) * 4, hipMemcpyDeviceToHost));
+  // realesrgan-native lib.rs:164-188 and scunet-native lib.rs:123-148:
+  // tiles of the engine's size with the model's margin, bytes in and out.
+  if (model->kind == IEN_MODEL_REALESRGAN)
+    return run_tiled(model, rgb, width, height, ESRGAN_GPU_TILE, ESRGAN_MARGIN, (uint8_t *)out,
+                     progress, user);
+  if (model->kind == IEN_MODEL_SCUNET)
+    return run_tiled(model, rgb, width, height, SCUNET_TILE, SCUNET_MARGIN, (uint8_t *)out,
+                     progress, user);
+  if ((st = check_size(model, width, height)) != IEN_OK) return st;
+  ien_ctx *ctx = model->ctx;
+  IEN_HIP(hipSetDevice(ctx->device));
+  const size_t pixels = width * height;
+  Staging io;
+  if ((st = stage(model, width, height, &io)) != IEN_OK) return st;
+  const bool lama = model->kind == IEN_MODEL_LAMA;
+  Bytes b;
+  if ((st = stage_bytes(model, pixels * 3, lama ? pixels : 0, lama ? pixels * 3 : 0, &b)) != IEN_OK)
+    return st;
+  IEN_HIP(hipMemcpyAsync(b.in, rgb, pixels * 3, hipMemcpyHostToDevice, ctx->stream));
+  if (lama) {
+    // lama-native lib.rs:138-142: the image / 255 and the mask as 0 or 1.
+    IEN_HIP(hipMemcpyAsync(b.mask, mask, pixels, hipMemcpyHostToDevice, ctx->stream));
+    st = bytes_to_floats(ctx, b.in, io.in, pixels * 3);
+    if (st == IEN_OK) st = mask_bytes(ctx, b.mask, io.mask, pixels);
+  } else {
+    // birefnet-native lib.rs:111-116: ImageNet's mean and deviation.
+    static const float mean[3] = {0.485f, 0.456f, 0.406f}, deviation[3] = {0.229f, 0.224f, 0.225f};
+    st = normalize_bytes(ctx, b.in, pixels, mean, deviation, io.in);
+  }
+  Steps steps(progress, user, model_steps(model));
+  Steps *sp = progress ? &steps : nullptr;
+  if (st == IEN_OK) st = enqueue(model, io.in, lama ? io.mask : nullptr, width, height, io.out, sp);
+  // lama-native lib.rs:147-155: the holes take the prediction as bytes.
+  if (st == IEN_OK && lama) st = composite_bytes(ctx, b.in, b.mask, io.out, pixels, b.out);
+  if ((st = finish_run(model, st, sp)) != IEN_OK) return st;
+  if (lama)
+    IEN_HIP(hipMemcpy(out, b.out, pixels * 3, hipMemcpyDeviceToHost));
+  else
+    IEN_HIP(hipMemcpy(out, io.out, pixels * 4, hipMemcpyDeviceToHost));
   return IEN_OK;
 }
 

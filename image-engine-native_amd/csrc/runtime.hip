@@ -93,6 +93,37 @@ std::vector<uint16_t> pack_fragments(const float *w, size_t k, size_t n, int *kb
   return out;
 }
 
+Steps::~Steps() {
+  for (hipEvent_t &e : ev)
+    if (e) (void)hipEventDestroy(e);
+}
+
+ien_status Steps::report_through(int done) {
+  while (reported < done) {
+    reported++;
+    if (progress((float)reported / (float)total, user) != 0)
+      return fail(IEN_ERR_CANCELLED, "the progress callback stopped the run");
+  }
+  return IEN_OK;
+}
+
+ien_status Steps::step(hipStream_t stream) {
+  hipEvent_t &mine = ev[issued % 2];
+  if (!mine) IEN_HIP(hipEventCreateWithFlags(&mine, hipEventDisableTiming));
+  IEN_HIP(hipEventRecord(mine, stream));
+  issued++;
+  if (issued < 2) return IEN_OK;
+  // The previous step: its event is the other one of the pair.
+  IEN_HIP(hipEventSynchronize(ev[issued % 2]));
+  return report_through(issued - 1);
+}
+
+ien_status Steps::drain() {
+  if (issued == 0) return IEN_OK;
+  IEN_HIP(hipEventSynchronize(ev[(issued - 1) % 2]));
+  return report_through(issued);
+}
+
 }  // namespace ien
 
 using namespace ien;

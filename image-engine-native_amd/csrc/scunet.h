@@ -39,6 +39,6 @@ void scunet_padded(size_t width, size_t height, size_t *pw, size_t *ph);
 // capture).
 ien_status scunet_reserve(Scunet *s, size_t pw, size_t ph);
 ien_status scunet_enqueue(Scunet *s, const float *d_image, size_t width, size_t height,
-                          float *d_out, hipEvent_t *events);
+                          float *d_out, Steps *steps);
 
 }  // namespace ien

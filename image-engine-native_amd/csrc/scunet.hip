@@ -130,7 +130,7 @@ void free_maps(Scunet &s) {
 
 // network.rs:158-208 run_level on the h x w map x of c channels (y, t:
 // the block's buffers).
-ien_status run_level(Scunet &s, ScunetBlock *blocks, int h, int w, int c, hipEvent_t *events,
+ien_status run_level(Scunet &s, ScunetBlock *blocks, int h, int w, int c, Steps *steps,
                      int *step) {
   ien_ctx *ctx = s.ctx;
   const size_t pixels = (size_t)h * w, half = (size_t)c / 2;
@@ -156,7 +156,7 @@ ien_status run_level(Scunet &s, ScunetBlock *blocks, int h, int w, int c, hipEve
     if (st == IEN_OK) st = rows_product(ctx, s.y, c, pixels, B.join, s.x, c, 1);
     if (st == IEN_OK && b + 1 < BLOCKS)
       st = rows_product(ctx, s.x, c, pixels, blocks[b + 1].split, s.y, c, 0);
-    if (st == IEN_OK && events) IEN_HIP(hipEventRecord(events[*step], ctx->stream));
+    if (st == IEN_OK && steps) st = steps->step(ctx->stream);
     ++*step;
   }
   return st;
@@ -265,7 +265,7 @@ ien_status scunet_reserve(Scunet *s, size_t pw, size_t ph) {
 // network.rs:262-354 run: d_image (f32 height x width x 3) to d_out (the
 // same shape); maps reserved for the padded size.
 ien_status scunet_enqueue(Scunet *s, const float *d_image, size_t width, size_t height,
-                          float *d_out, hipEvent_t *events) {
+                          float *d_out, Steps *steps) {
   ien_ctx *ctx = s->ctx;
   size_t pw, ph;
   scunet_padded(width, height, &pw, &ph);
@@ -276,7 +276,7 @@ ien_status scunet_enqueue(Scunet *s, const float *d_image, size_t width, size_t 
   // The head (no bias); computed again at the end as the skip into the tail.
   if ((st = conv3(ctx, s->img, h, w, 4, 8, s->head, s->x, DIM, IEN_ACT_NONE, 0)) != IEN_OK) return st;
   for (int l = 0; l < 3; l++) {
-    if ((st = run_level(*s, s->down[l], h, w, c, events, &step)) != IEN_OK) return st;
+    if ((st = run_level(*s, s->down[l], h, w, c, steps, &step)) != IEN_OK) return st;
     // network.rs:403-437 halved, kept as the skip of the level up.
     if ((st = ien_gather_2x2(ctx, s->x, h, w, c, c, IEN_ORDER_ROW_MAJOR, s->rows)) != IEN_OK)
       return st;
@@ -288,7 +288,7 @@ ien_status scunet_enqueue(Scunet *s, const float *d_image, size_t width, size_t 
     c *= 2;
     IEN_HIP(hipMemcpyAsync(s->x, s->skip[l], q * c * 2, hipMemcpyDeviceToDevice, ctx->stream));
   }
-  if ((st = run_level(*s, s->body, h, w, c, events, &step)) != IEN_OK) return st;
+  if ((st = run_level(*s, s->body, h, w, c, steps, &step)) != IEN_OK) return st;
   for (int l = 0; l < 3; l++) {
     const size_t pixels = (size_t)h * w;
     if ((st = ien_add(ctx, s->x, s->skip[2 - l], pixels * c)) != IEN_OK) return st;
@@ -298,7 +298,7 @@ ien_status scunet_enqueue(Scunet *s, const float *d_image, size_t width, size_t 
     h *= 2;
     w *= 2;
     c /= 2;
-    if ((st = run_level(*s, s->up[l], h, w, c, events, &step)) != IEN_OK) return st;
+    if ((st = run_level(*s, s->up[l], h, w, c, steps, &step)) != IEN_OK) return st;
   }
   if ((st = conv3(ctx, s->img, h, w, 4, 8, s->head, s->x, DIM, IEN_ACT_NONE, 1)) != IEN_OK) return st;
   if ((st = conv3(ctx, s->x, h, w, DIM, DIM, s->tail, s->out16, 4, IEN_ACT_NONE, 0)) != IEN_OK)

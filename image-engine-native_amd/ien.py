@@ -31,7 +31,9 @@ EXPORTS = (
     "ien_matrix_new", "ien_matrix_free", "ien_multiply", "ien_multiply_ex", "ien_conv3",
     "ien_layer_norm", "ien_gelu", "ien_sigmoid", "ien_pixel_shuffle_add", "ien_depthwise",
     "ien_model_load", "ien_model_from_tensors", "ien_model_free", "ien_model_run",
-    "ien_model_run_device", "ien_model_set_graph",
+    "ien_model_run_device", "ien_model_set_graph", "ien_model_run_tiled", "ien_model_run_u8",
+    "ien_bytes_to_floats", "ien_floats_to_bytes", "ien_mask_bytes", "ien_normalize_bytes",
+    "ien_composite_bytes",
     "ien_window_count", "ien_position_bias", "ien_bias_tables", "ien_window_gather",
     "ien_window_attention", "ien_window_scatter_add", "ien_swin_new", "ien_swin_free", "ien_swin_run",
     "ien_swin_run_static",
@@ -148,6 +150,13 @@ def load():
         L.ien_model_free.argtypes = [vp]
         L.ien_model_free.restype = None
         L.ien_model_run.argtypes = [vp, vp, vp, sz, sz, vp, vp, vp]
+        L.ien_model_run_tiled.argtypes = [vp, vp, sz, sz, sz, sz, vp, vp, vp]
+        L.ien_model_run_u8.argtypes = [vp, vp, vp, sz, sz, vp, vp, vp]
+        L.ien_bytes_to_floats.argtypes = [vp, vp, vp, sz]
+        L.ien_floats_to_bytes.argtypes = [vp, vp, vp, sz]
+        L.ien_mask_bytes.argtypes = [vp, vp, vp, sz]
+        L.ien_normalize_bytes.argtypes = [vp, vp, sz, vp, vp, vp]
+        L.ien_composite_bytes.argtypes = [vp, vp, vp, vp, sz, vp]
         L.ien_model_run_device.argtypes = [vp, vp, vp, sz, sz, vp]
         L.ien_model_set_graph.argtypes = [vp, i]
         wp = ctypes.POINTER(Windows)
@@ -474,6 +483,31 @@ class Swin:
             pass
 
 
+def bytes_to_floats(ctx, src, dst):
+    """to_float on device: uint8 tensor to float32 tensor of the same size."""
+    check(load().ien_bytes_to_floats(ctx.h, _ptr(src), _ptr(dst), src.numel()))
+
+
+def floats_to_bytes(ctx, src, dst):
+    """to_byte on device: float32 tensor to uint8 tensor of the same size."""
+    check(load().ien_floats_to_bytes(ctx.h, _ptr(src), _ptr(dst), src.numel()))
+
+
+def mask_bytes(ctx, mask, dst):
+    check(load().ien_mask_bytes(ctx.h, _ptr(mask), _ptr(dst), mask.numel()))
+
+
+def normalize_bytes(ctx, rgb, mean, std, dst):
+    """rgb: uint8 tensor of pixels x 3 values; mean, std: three floats."""
+    m = (ctypes.c_float * 3)(*mean)
+    d = (ctypes.c_float * 3)(*std)
+    check(load().ien_normalize_bytes(ctx.h, _ptr(rgb), rgb.numel() // 3, m, d, _ptr(dst)))
+
+
+def composite_bytes(ctx, rgb, mask, pred, out):
+    check(load().ien_composite_bytes(ctx.h, _ptr(rgb), _ptr(mask), _ptr(pred), mask.numel(), _ptr(out)))
+
+
 class Model:
     """ien_model: the reference's Model with the HIP engine."""
 
@@ -531,6 +565,42 @@ class Model:
                                    None if m is None else m.ctypes.data_as(ctypes.c_void_p), w, h,
                                    out.ctypes.data_as(ctypes.c_void_p),
                                    ctypes.cast(cb, ctypes.c_void_p) if cb else None, None))
+        return out
+
+    def run_tiled(self, image, tile, margin, progress=None):
+        """Model::run_float_tiled (Real-ESRGAN, SCUNet): host f32 H x W x 3
+        in, the run's output shape out."""
+        import numpy as np
+
+        image = np.ascontiguousarray(image, dtype=np.float32)
+        h, w, _ = image.shape
+        s = 4 if self.kind == MODEL_REALESRGAN else 1
+        out = np.empty((s * h, s * w, 3), np.float32)
+        cb = PROGRESS(progress) if progress else None
+        check(load().ien_model_run_tiled(self.h, image.ctypes.data_as(ctypes.c_void_p), w, h, tile, margin,
+                                         out.ctypes.data_as(ctypes.c_void_p),
+                                         ctypes.cast(cb, ctypes.c_void_p) if cb else None, None))
+        return out
+
+    def run_u8(self, rgb, mask=None, progress=None):
+        """Model::run on 8-bit RGB H x W x 3 (uint8): bytes out (4H x 4W x 3
+        for Real-ESRGAN, H x W x 3 for SCUNet and LaMa, which takes the
+        H x W byte mask), H x W f32 logits for BiRefNet."""
+        import numpy as np
+
+        rgb = np.ascontiguousarray(rgb, dtype=np.uint8)
+        h, w, _ = rgb.shape
+        if self.kind == MODEL_BIREFNET:
+            out = np.empty((h, w), np.float32)
+        else:
+            s = 4 if self.kind == MODEL_REALESRGAN else 1
+            out = np.empty((s * h, s * w, 3), np.uint8)
+        m = None if mask is None else np.ascontiguousarray(mask, dtype=np.uint8)
+        cb = PROGRESS(progress) if progress else None
+        check(load().ien_model_run_u8(self.h, rgb.ctypes.data_as(ctypes.c_void_p),
+                                      None if m is None else m.ctypes.data_as(ctypes.c_void_p), w, h,
+                                      out.ctypes.data_as(ctypes.c_void_p),
+                                      ctypes.cast(cb, ctypes.c_void_p) if cb else None, None))
         return out
 
     def run_device(self, d_image, width, height, d_out, d_mask=None):

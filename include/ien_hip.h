@@ -179,6 +179,25 @@ ien_status ien_depthwise(ien_ctx *ctx, const uint16_t *d_x, size_t height, size_
                          size_t channels, ien_layout layout, const float *d_w, size_t size,
                          const float *d_bias, uint16_t *d_y);
 
+/* ---- 8-bit images: the models' Model::run byte I/O -------------------- */
+/* realesrgan-native lib.rs:292-295 to_float: n bytes to f32 v / 255. */
+ien_status ien_bytes_to_floats(ien_ctx *ctx, const uint8_t *d_src, float *d_dst, size_t n);
+/* realesrgan-native lib.rs:297-300 to_byte: n floats to bytes,
+ * round(clamp(v, 0, 1) * 255) with halves away from zero (NaN to 0). */
+ien_status ien_floats_to_bytes(ien_ctx *ctx, const float *d_src, uint8_t *d_dst, size_t n);
+/* lama-native lib.rs:142: a byte mask as f32 holes, 1 where the byte is
+ * not 0, else 0. */
+ien_status ien_mask_bytes(ien_ctx *ctx, const uint8_t *d_mask, float *d_dst, size_t n);
+/* birefnet-native lib.rs:111-116: interleaved 8-bit RGB (pixels x 3) to
+ * f32 (v / 255 - mean[c]) / deviation[c] (host mean and deviation). */
+ien_status ien_normalize_bytes(ien_ctx *ctx, const uint8_t *d_rgb, size_t pixels,
+                               const float mean[3], const float deviation[3], float *d_dst);
+/* lama-native lib.rs:147-155: out = the RGB bytes where the mask byte is 0,
+ * to_byte(prediction) where it is not (pixels x 3 values, one mask byte a
+ * pixel). */
+ien_status ien_composite_bytes(ien_ctx *ctx, const uint8_t *d_rgb, const uint8_t *d_mask,
+                               const float *d_pred, size_t pixels, uint8_t *d_out);
+
 /* ---- resampling and padding ------------------------------------------- */
 
 /* birefnet-native decoder.rs:436-522 resize: bilinear with aligned corners
@@ -399,6 +418,31 @@ typedef int (*ien_progress)(float done, void *user);
  * the others. */
 ien_status ien_model_run(ien_model *model, const float *image, const float *mask, size_t width,
                          size_t height, float *out, ien_progress progress, void *user);
+
+/* Model::run_float_tiled (realesrgan-native lib.rs:216-229, scunet-native
+ * lib.rs:172-185), Real-ESRGAN and SCUNet: the image cut into a grid of
+ * equal tiles at most `tile` pixels on a side, each run with up to `margin`
+ * pixels of its surroundings on every side, only the tile's own output
+ * kept.  Real-ESRGAN with a margin of at least 34 (the 34 layers' reach)
+ * gives the whole image's result bit for bit.  Progress counts the steps
+ * of every tile; a cancel stops issuing work and returns
+ * IEN_ERR_CANCELLED. */
+ien_status ien_model_run_tiled(ien_model *model, const float *image, size_t width,
+                               size_t height, size_t tile, size_t margin, float *out,
+                               ien_progress progress, void *user);
+
+/* Model::run / run_with_progress on 8-bit RGB (host, width x height x 3):
+ * Real-ESRGAN (realesrgan-native lib.rs:161-189: tiles of 768 with margin
+ * 34, out 4h x 4w x 3 bytes) and SCUNet (scunet-native lib.rs:120-148:
+ * tiles of 896 with margin 64, out h x w x 3 bytes) take to_float in and
+ * to_byte out; LaMa (lama-native lib.rs:114-156) takes `mask` (width x
+ * height bytes, not 0 = fill) and returns the image with only the holes
+ * replaced (h x w x 3 bytes); BiRefNet (birefnet-native lib.rs:107-141,
+ * square sides a multiple of 64) normalises with ImageNet's statistics and
+ * returns f32 logits (h x w floats) in `out`. */
+ien_status ien_model_run_u8(ien_model *model, const uint8_t *rgb, const uint8_t *mask,
+                            size_t width, size_t height, void *out, ien_progress progress,
+                            void *user);
 
 /* The same on device buffers (f32 NHWC in and out), no host copies and no
  * synchronisation: the hot path a serving loop or a benchmark times. */

@@ -32,6 +32,18 @@ float or_half_to_f32(uint16_t h);              /* half.rs:125-140 */
 void or_floats_to_halves(const float *src, uint16_t *dst, size_t n);
 void or_halves_to_f32(const uint16_t *src, float *dst, size_t n);
 
+/* ---- 8-bit image I/O and tiling (io.c) -------------------------------- */
+float or_to_float(uint8_t v);                  /* realesrgan lib.rs:292-295 */
+uint8_t or_to_byte(float v);                   /* realesrgan lib.rs:297-300 */
+void or_bytes_to_floats(const uint8_t *src, float *dst, size_t n);
+void or_floats_to_bytes(const float *src, uint8_t *dst, size_t n);
+void or_normalize_bytes(const uint8_t *rgb, size_t pixels, float *dst); /* birefnet lib.rs:111-116 */
+void or_mask_bytes(const uint8_t *mask, float *dst, size_t n);         /* lama lib.rs:142 */
+void or_composite_bytes(const uint8_t *rgb, const uint8_t *mask, const float *pred,
+                        size_t pixels, uint8_t *out);                   /* lama lib.rs:147-155 */
+size_t or_tile_regions(size_t width, size_t height, size_t tile, size_t margin,
+                       size_t *out);                                    /* realesrgan lib.rs:251-265 */
+
 /* ---- math.rs ---------------------------------------------------------- */
 float or_exp_neg(float z);                     /* math.rs:21-31 */
 void or_sigmoid(float *x, size_t n);           /* math.rs:33-39,145-152 */

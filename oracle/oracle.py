@@ -99,6 +99,17 @@ def lib():
         L.or_lama_up.argtypes = [ctypes.c_int, vp, vp, vp, sz, sz, sz, sz, vp]
         L.or_birefnet_run.argtypes = [ctypes.c_int, vp, sz, vp, sz, vp]
         L.or_birefnet_run.restype = ctypes.c_int
+        L.or_to_float.restype = f
+        L.or_to_float.argtypes = [ctypes.c_uint8]
+        L.or_to_byte.restype = ctypes.c_uint8
+        L.or_to_byte.argtypes = [f]
+        L.or_bytes_to_floats.argtypes = [vp, vp, sz]
+        L.or_floats_to_bytes.argtypes = [vp, vp, sz]
+        L.or_normalize_bytes.argtypes = [vp, sz, vp]
+        L.or_mask_bytes.argtypes = [vp, vp, sz]
+        L.or_composite_bytes.argtypes = [vp, vp, vp, sz, vp]
+        L.or_tile_regions.restype = sz
+        L.or_tile_regions.argtypes = [sz, sz, sz, sz, vp]
         _lib = L
     return _lib
 
@@ -113,6 +124,63 @@ def _f32(a):
 
 def threads_default():
     return os.cpu_count() or 1
+
+
+# ---- 8-bit image I/O and tiling (io.c) --------------------------------------
+def _u8(a):
+    return np.ascontiguousarray(a, dtype=np.uint8)
+
+
+def bytes_to_floats(b):
+    """realesrgan-native lib.rs:292-295 to_float over an array of bytes."""
+    b = _u8(b)
+    out = np.empty(b.shape, np.float32)
+    lib().or_bytes_to_floats(_p(b), _p(out), b.size)
+    return out
+
+
+def floats_to_bytes(x):
+    """realesrgan-native lib.rs:297-300 to_byte over an array of floats."""
+    x = _f32(x)
+    out = np.empty(x.shape, np.uint8)
+    lib().or_floats_to_bytes(_p(x), _p(out), x.size)
+    return out
+
+
+def normalize_bytes(rgb):
+    """birefnet-native lib.rs:111-116: interleaved RGB bytes (..., 3) to the
+    ImageNet-normalised floats."""
+    rgb = _u8(rgb)
+    out = np.empty(rgb.shape, np.float32)
+    lib().or_normalize_bytes(_p(rgb), rgb.size // 3, _p(out))
+    return out
+
+
+def mask_bytes(mask):
+    mask = _u8(mask)
+    out = np.empty(mask.shape, np.float32)
+    lib().or_mask_bytes(_p(mask), _p(out), mask.size)
+    return out
+
+
+def composite_bytes(rgb, mask, pred):
+    """lama-native lib.rs:147-155 over H x W x 3 bytes, an H x W byte mask
+    and H x W x 3 predicted floats."""
+    rgb, mask, pred = _u8(rgb), _u8(mask), _f32(pred)
+    out = np.empty(rgb.shape, np.uint8)
+    lib().or_composite_bytes(_p(rgb), _p(mask), _p(pred), mask.size, _p(out))
+    return out
+
+
+def tile_regions(width, height, tile, margin):
+    """realesrgan-native lib.rs:251-265: rows of (x0, x1, y0, y1, rx0, rx1,
+    ry0, ry1), one per tile in row-major order."""
+    if tile == 0:
+        return np.zeros((0, 8), np.uint64)
+    n = -(-width // tile) * -(-height // tile)
+    out = np.zeros((n, 8), np.uint64)
+    k = lib().or_tile_regions(width, height, tile, margin, _p(out))
+    return out[:k].astype(np.int64)
 
 
 # ---- half.rs ---------------------------------------------------------------
