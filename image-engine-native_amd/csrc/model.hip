@@ -34,6 +34,30 @@ struct Tensor {
   std::vector<float> values;
 };
 
+// Whether `s` is well-formed UTF-8 (as str::from_utf8 accepts it: no
+// overlong forms, no surrogates, nothing past U+10FFFF).
+static bool utf8(const std::string &s) {
+  const unsigned char *p = (const unsigned char *)s.data(), *end = p + s.size();
+  while (p < end) {
+    const unsigned c = *p;
+    if (c < 0x80) {
+      p++;
+      continue;
+    }
+    const int n = (c & 0xe0) == 0xc0 ? 1 : (c & 0xf0) == 0xe0 ? 2 : (c & 0xf8) == 0xf0 ? 3 : -1;
+    if (n < 0 || end - p <= n) return false;
+    unsigned cp = c & (0x3f >> n);
+    for (int i = 1; i <= n; i++) {
+      if ((p[i] & 0xc0) != 0x80) return false;
+      cp = (cp << 6) | (p[i] & 0x3f);
+    }
+    static const unsigned least[4] = {0, 0x80, 0x800, 0x10000};
+    if (cp < least[n] || cp > 0x10ffff || (cp >= 0xd800 && cp <= 0xdfff)) return false;
+    p += n + 1;
+  }
+  return true;
+}
+
 class WeightFile {
  public:
   std::map<std::string, Tensor> tensors;
@@ -69,6 +93,7 @@ class WeightFile {
       if (!take(&name_len, 2)) return fail(IEN_ERR_WEIGHTS, "weights file is truncated");
       std::string name(name_len, '\0');
       if (!take(name.data(), name_len)) return fail(IEN_ERR_WEIGHTS, "weights file is truncated");
+      if (!utf8(name)) return fail(IEN_ERR_WEIGHTS, "tensor name is not UTF-8");
       uint8_t dr[2];
       if (!take(dr, 2)) return fail(IEN_ERR_WEIGHTS, "weights file is truncated");
       size_t width = dr[0] == 0 ? 4 : dr[0] == 1 ? 2 : 0;
