@@ -36,9 +36,11 @@ struct Birefnet {
   ien_matrix *patch_conv1[4] = {}, *patch_out[4] = {};  // patches5..2
   ien_matrix *head = nullptr;
   float head_bias = 0.0f;
-  // Full-resolution branch: the composed 5x5 weights [25][3] and bias, then
-  // conv1 [27][64], bias1 [64], conv_out [9][64], bias_out (f32, device).
+  // Full-resolution branch (f32, device): the composed 5x5 weights [25][3]
+  // and their bias, conv1 [27][64], bias1 [64], conv_out [9][64]; its
+  // output bias on the host.
   float *d_full = nullptr;
+  float bias_out = 0.0f;
   size_t side = 0;  // the side the maps are reserved for
   uint16_t *img16 = nullptr, *half16 = nullptr, *prow = nullptr, *x = nullptr, *mrows = nullptr,
            *level[4] = {}, *tmp = nullptr, *x4 = nullptr, *in = nullptr, *t = nullptr,

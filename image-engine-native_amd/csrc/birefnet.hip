@@ -13,9 +13,9 @@
 //    integer taps with modulator 2 sigmoid(0) = 1, decoder.rs:254-313), and
 //    conv1 accumulated onto that bias; the gate as a 3x3 convolution to 16
 //    channels and a per-pixel sigmoid scale; the image-to-patches stacks;
-//    the head before the final resize; the full-resolution branch as its
-//    composed 5x5 convolution inside the edge ring and both convolutions on
-//    the ring (decoder.rs:594-757).
+//    the head before the final resize; the full-resolution branch in 16 x 16
+//    tiles, its composed 5x5 convolution off the edge ring and, in the
+//    border tiles, both convolutions on the ring (decoder.rs:594-757).
 // One event is recorded after each of 14 steps (the 2 x 4 backbone stages,
 // the squeeze and the four decoder blocks, the head) for progress reports.
 
@@ -217,70 +217,97 @@ __global__ __launch_bounds__(256) void k_image_patches(const uint16_t *__restric
   }
 }
 
-// decoder.rs:737-757: head bias plus the composed 5x5 convolution of the f32
-// image at every pixel inside the edge ring (the bias, then each tap's three
-// products in order; zero outside the image).  full: [25][3] weights, bias.
-__global__ __launch_bounds__(256) void k_full_interior(const float *__restrict__ image, int side,
-                                                       const float *__restrict__ full,
-                                                       float head_bias, float *__restrict__ out) {
-  const long i = (long)blockIdx.x * 256 + threadIdx.x;
-  if (i >= (long)side * side) return;
-  const int y = (int)(i / side), x = (int)(i % side);
-  if (y == 0 || x == 0 || y == side - 1 || x == side - 1) return;
-  float s = full[75];
-  for (int e = 0; e < 25; e++) {
-    const int py = y + e / 5 - 2, px = x + e % 5 - 2;
-    float p0 = 0.0f, p1 = 0.0f, p2 = 0.0f;
-    if (py >= 0 && px >= 0 && py < side && px < side) {
-      const float *p = image + ((long)py * side + px) * 3;
-      p0 = p[0];
-      p1 = p[1];
-      p2 = p[2];
-    }
-    s += full[3 * e] * p0 + full[3 * e + 1] * p1 + full[3 * e + 2] * p2;
-  }
-  out[i] = head_bias + s;
-}
+// The full-resolution branch's weights (decoder.rs:604-635 FullResolution):
+// the composed 5x5 weights [25][3] with their bias after them, and the two
+// convolutions it composes (conv1 [27][64] + bias1, conv_out [9][64] +
+// bias_out), all device f32.
+struct FullParams {
+  const float *composed, *conv1, *bias1, *conv_out;
+  float bias_out, head_bias;
+};
 
-// decoder.rs:700-734 on the edge ring: both 3x3 convolutions one after the
-// other (the intermediate map's zero padding is reached).  One wave per
-// ring pixel, lane k = intermediate channel k.  full + 76: conv1 [27][64],
-// bias1 [64], conv_out [9][64], bias_out.
-__global__ __launch_bounds__(64) void k_full_ring(const float *__restrict__ image, int side,
-                                                  const float *__restrict__ full, float head_bias,
-                                                  float *__restrict__ out) {
-  const int ring = blockIdx.x, k = threadIdx.x;
-  // Ring pixel -> (y, x): the top row, the bottom row, then the left and
-  // right columns between them.
-  int y, x;
-  if (ring < side) {
-    y = 0;
-    x = ring;
-  } else if (ring < 2 * side) {
-    y = side - 1;
-    x = ring - side;
-  } else {
-    const int r = ring - 2 * side;  // < 2 (side - 2)
-    y = 1 + r / 2;
-    x = (r & 1) ? side - 1 : 0;
+// decoder.rs:637-757 FullResolution::add with the head bias: 16 x 16 pixel
+// tiles, one thread a pixel, the tile's image patch with two pixels around
+// it (zeros outside the image) staged in LDS as three planes.
+//  - Pixels off the image's edge ring: the composed 5x5 convolution
+//    (composed_row: the bias, then each tap's three products in order).
+//  - Tiles on the image's border then compute their ring pixels exactly
+//    (decoder.rs:700-734 exact: conv1 + bias1 at each in-image neighbour,
+//    the intermediate map's zero padding reached, then conv_out): the ring
+//    pixels are numbered within the tile, and 16 threads take one, each
+//    holding 4 of the 64 intermediate channels over the neighbours; a
+//    16-lane sum adds them.
+constexpr int FT = 16, FP = FT + 4;
+__global__ __launch_bounds__(256) void k_full_res(const float *__restrict__ image, int side,
+                                                  FullParams f, float *__restrict__ out) {
+  __shared__ float patch[3][FP][FP];
+  __shared__ int ring_count[4];
+  __shared__ short ring_pixel[2 * FT];
+  const int t = threadIdx.x, ly = t / FT, lx = t % FT;
+  const int y0 = blockIdx.y * FT, x0 = blockIdx.x * FT;
+  for (int i = t; i < FP * FP; i += 256) {
+    const int py = y0 - 2 + i / FP, px = x0 - 2 + i % FP;
+    const bool in = py >= 0 && px >= 0 && py < side && px < side;
+    const float *p = image + ((long)(in ? py : 0) * side + (in ? px : 0)) * 3;
+#pragma unroll
+    for (int c = 0; c < 3; c++) patch[c][i / FP][i % FP] = in ? p[c] : 0.0f;
   }
-  const float *c1 = full + 76, *b1 = c1 + 27 * INTER, *co = b1 + INTER, *bo = co + 9 * INTER;
-  float s = 0.0f;
-  for (int d = 0; d < 9; d++) {
-    const int qy = y + d / 3 - 1, qx = x + d % 3 - 1;
-    if (qy < 0 || qx < 0 || qy >= side || qx >= side) continue;
-    float m = b1[k];
-    for (int e = 0; e < 9; e++) {
-      const int py = qy + e / 3 - 1, px = qx + e % 3 - 1;
-      if (py < 0 || px < 0 || py >= side || px >= side) continue;
-      const float *p = image + ((long)py * side + px) * 3;
-      for (int c = 0; c < 3; c++) m += p[c] * c1[(e * 3 + c) * INTER + k];
+  __syncthreads();
+  const int y = y0 + ly, x = x0 + lx;
+  const bool ring = y == 0 || x == 0 || y == side - 1 || x == side - 1;
+  if (!ring) {
+    float s = f.composed[75];
+    for (int e = 0; e < 25; e++) {
+      const int py = ly + e / 5, px = lx + e % 5;
+      s += f.composed[3 * e] * patch[0][py][px] + f.composed[3 * e + 1] * patch[1][py][px] +
+           f.composed[3 * e + 2] * patch[2][py][px];
     }
-    float v = m * co[d * INTER + k];
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
-    s += v;
+    out[(long)y * side + x] = f.head_bias + s;
   }
-  if (k == 0) out[(long)y * side + x] = head_bias + (bo[0] + s);
+  if (blockIdx.x != 0 && blockIdx.y != 0 && blockIdx.x + 1 != gridDim.x && blockIdx.y + 1 != gridDim.y)
+    return;  // the whole tile is off the ring
+  const int wave = t / 64, lane = t % 64;
+  const unsigned long long mask = __ballot(ring);
+  if (lane == 0) ring_count[wave] = __popcll(mask);
+  __syncthreads();
+  int before = 0, rings = 0;
+  for (int w = 0; w < 4; w++) {
+    before += w < wave ? ring_count[w] : 0;
+    rings += ring_count[w];
+  }
+  if (ring) ring_pixel[before + __popcll(mask & ((1ull << lane) - 1))] = (short)t;
+  __syncthreads();
+  const int g = t % 16;
+  for (int r0 = 0; r0 < rings; r0 += 16) {
+    const int r = r0 + t / 16;
+    float v = 0.0f;
+    int ry = 0, rx = 0;
+    if (r < rings) {
+      const int pt = ring_pixel[r], py = pt / FT, px = pt % FT;
+      ry = y0 + py;
+      rx = x0 + px;
+      for (int d = 0; d < 9; d++) {
+        const int qy = ry + d / 3 - 1, qx = rx + d % 3 - 1;
+        if (qy < 0 || qx < 0 || qy >= side || qx >= side) continue;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          const int k = g + 16 * j;
+          float m = f.bias1[k];
+          for (int e = 0; e < 9; e++) {
+            const int sy = py + d / 3 + e / 3, sx = px + d % 3 + e % 3;
+#pragma unroll
+            for (int c = 0; c < 3; c++) m += patch[c][sy][sx] * f.conv1[(e * 3 + c) * INTER + k];
+          }
+          v += m * f.conv_out[d * INTER + k];
+        }
+      }
+    }
+    v += __shfl_xor(v, 8);
+    v += __shfl_xor(v, 4);
+    v += __shfl_xor(v, 2);
+    v += __shfl_xor(v, 1);
+    if (r < rings && g == 0) out[(long)ry * side + rx] = f.head_bias + (f.bias_out + v);
+  }
 }
 
 ien_status matrix(ien_ctx *ctx, const TensorSource &take, const std::string &name, size_t k,
@@ -626,7 +653,7 @@ ien_status birefnet_load(ien_ctx *ctx, const TensorSource &take, const ShapeOf &
     full.insert(full.end(), c1.begin(), c1.end());
     full.insert(full.end(), b1.begin(), b1.end());
     full.insert(full.end(), co.begin(), co.end());
-    full.push_back(bo[0]);
+    b->bias_out = bo[0];
     st = upload(full, &b->d_full);
   }
   return st;
@@ -792,10 +819,10 @@ ien_status birefnet_enqueue(Birefnet *b, const float *d_image, size_t side_, flo
   const long low_pixels = (long)prev_grid * prev_grid;
   st = rows_product(ctx, b->prev, 96, 96, low_pixels, b->head, b->low, 1, IEN_ACT_NONE, 0);
   if (st != IEN_OK) return st;
-  hipLaunchKernelGGL(k_full_interior, dim3(blocks_for((long)side * side, 256)), dim3(256), 0,
-                     ctx->stream, d_image, side, b->d_full, b->head_bias, d_logits);
-  hipLaunchKernelGGL(k_full_ring, dim3((unsigned)(4 * side - 4)), dim3(64), 0, ctx->stream,
-                     d_image, side, b->d_full, b->head_bias, d_logits);
+  const FullParams fp{b->d_full, b->d_full + 76, b->d_full + 76 + 27 * INTER,
+                      b->d_full + 76 + 28 * INTER, b->bias_out, b->head_bias};
+  hipLaunchKernelGGL(k_full_res, dim3((unsigned)(side / FT), (unsigned)(side / FT)), dim3(256), 0,
+                     ctx->stream, d_image, side, fp, d_logits);
   IEN_HIP(hipGetLastError());
   st = ien_resize(ctx, b->low, prev_grid, prev_grid, 1, 1, d_logits, side, side, 1, IEN_OUT_F32, 1);
   if (st == IEN_OK && steps) st = steps->step(ctx->stream);

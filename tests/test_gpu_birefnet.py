@@ -43,6 +43,11 @@ def check(got, want, what):
     assert_config_tolerance(got, want, peak=max(1.0, float(np.abs(want).max())), what=what + " logits")
     assert_spread(got, want, what=what + " logits")
     assert_config_tolerance(sigmoid(got), sigmoid(want), what=what + " mask")
+    # The edge ring, where the full-resolution branch runs its two
+    # convolutions instead of the composed one, on its own.
+    ring = np.zeros(got.shape, bool)
+    ring[0], ring[-1], ring[:, 0], ring[:, -1] = True, True, True, True
+    assert_spread(got[ring], want[ring], what=what + " ring logits")
 
 
 def test_birefnet_rejects_deformable_offsets_and_bad_sizes(ctx):
