@@ -15,6 +15,10 @@ struct BirefnetBlock {
   int cin = 0, cout = 0;
   ien_matrix *conv_in = nullptr, *conv_out = nullptr, *branch[4] = {}, *conv1 = nullptr,
              *gdt = nullptr;
+  // A deformable branch's offset convolution (2 taps offsets, then taps
+  // modulator logits); null where they are all zero, which makes the
+  // branch a plain size x size convolution.
+  ien_matrix *offset[4] = {};
   // pool weight [64][256], pool bias [256], conv1's pooling rows [256][64],
   // conv1's bias [64]: f32 on the device for the pooling kernel.
   float *d_pool = nullptr;
@@ -41,6 +45,11 @@ struct Birefnet {
   // output bias on the host.
   float *d_full = nullptr;
   float bias_out = 0.0f;
+  // Deformable branches: their offsets (f32, 3 taps a pixel) and the
+  // bilinear samples of one chunk of rows (f16, taps x 64 a row).
+  bool deformable = false;
+  float *offs = nullptr;
+  uint16_t *samples = nullptr;
   size_t side = 0;  // the side the maps are reserved for
   uint16_t *img16 = nullptr, *half16 = nullptr, *prow = nullptr, *x = nullptr, *mrows = nullptr,
            *level[4] = {}, *tmp = nullptr, *x4 = nullptr, *in = nullptr, *t = nullptr,

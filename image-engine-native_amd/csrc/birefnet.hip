@@ -10,7 +10,9 @@
 //    its two small products (a bias for conv1), its four branches as k x k
 //    convolutions into the columns of one 1024-channel map (the network is
 //    deformable-free: all-zero offset and modulator convolutions sample the
-//    integer taps with modulator 2 sigmoid(0) = 1, decoder.rs:254-313), and
+//    integer taps with modulator 2 sigmoid(0) = 1, decoder.rs:254-313) or,
+//    where a branch's offsets are not zero, its offset convolution, the
+//    bilinear samples and their product in chunks of rows; and
 //    conv1 accumulated onto that bias; the gate as a 3x3 convolution to 16
 //    channels and a per-pixel sigmoid scale; the image-to-patches stacks;
 //    the head before the final resize; the full-resolution branch in 16 x 16
@@ -40,6 +42,9 @@ constexpr int PATCH_COUT[4] = {192, 192, 96, 48};
 constexpr int SQUEEZE_CIN = 2880, SQUEEZE_COUT = 1536;
 constexpr float MASKED = -100.0f;  // swin.rs:21-23
 constexpr int POOL_PARTS = 256;    // partial sums of the ASPP's column mean
+// Bilinear samples of a deformable branch are built this many bytes of rows
+// at a time (the 7 x 7 branch: about 10k pixels of 49 x 64 halves).
+constexpr size_t SAMPLE_BYTES = (size_t)64 << 20;
 
 unsigned blocks_for(long items, int per) { return (unsigned)((items + per - 1) / per); }
 
@@ -360,12 +365,15 @@ ien_status load_block(ien_ctx *ctx, const TensorSource &take, const std::string 
     st = take(p + ".offset.weight", {taps * INTER, 3 * taps}, &ow);
     if (st == IEN_OK) st = take(p + ".offset.bias", {3 * taps}, &ob);
     if (st != IEN_OK) break;
-    // The deformable-free network: zero offsets and modulator logits.
-    for (float v : ow)
-      if (v != 0.0f) return fail(IEN_ERR_WEIGHTS, "%s: deformable offsets are not supported", p.c_str());
-    for (float v : ob)
-      if (v != 0.0f) return fail(IEN_ERR_WEIGHTS, "%s: deformable offsets are not supported", p.c_str());
-    st = matrix(ctx, take, p, taps * INTER, BRANCH, true, &B->branch[i]);
+    // All-zero offsets and modulator logits sample the integer taps with
+    // modulator 2 sigmoid(0) = 1: the branch is then a plain convolution.
+    bool zero = true;
+    for (float v : ow) zero = zero && v == 0.0f;
+    for (float v : ob) zero = zero && v == 0.0f;
+    if (!zero)
+      st = ien_matrix_new(ctx, ow.data(), IEN_W_F32, taps * INTER, 3 * taps, ob.data(),
+                          &B->offset[i]);
+    if (st == IEN_OK) st = matrix(ctx, take, p, taps * INTER, BRANCH, true, &B->branch[i]);
   }
   if (st != IEN_OK) return st;
   std::vector<float> pw, pb, cw, cb;
@@ -390,6 +398,7 @@ void free_block(BirefnetBlock &B) {
   ien_matrix_free(B.conv1);
   ien_matrix_free(B.gdt);
   for (auto *m : B.branch) ien_matrix_free(m);
+  for (auto *m : B.offset) ien_matrix_free(m);
   (void)hipFree(B.d_pool);
 }
 
@@ -402,7 +411,10 @@ void free_maps(Birefnet &b) {
   }
   (void)hipFree(b.partial);
   (void)hipFree(b.d_bias);
-  b.partial = b.d_bias = nullptr;
+  (void)hipFree(b.offs);
+  (void)hipFree(b.samples);
+  b.partial = b.d_bias = b.offs = nullptr;
+  b.samples = nullptr;
   b.side = 0;
 }
 
@@ -459,6 +471,92 @@ ien_status copy_cols(ien_ctx *ctx, const uint16_t *src, long rows, int c, long s
   return IEN_OK;
 }
 
+// decoder.rs:239-313 sample_rows / sample: the deformable input of rows
+// row0 .. row0 + rows of an h x w map t (f16, 64 channels): for each tap of
+// a size x size kernel, the 64 channels bilinearly sampled at the tap moved
+// by its offset, times twice the sigmoid of its modulator logit; a point
+// more than a pixel outside the map reads zero and corners outside it count
+// as zero (torchvision's deform_conv2d).  offs: 3 taps f32 a pixel (y, x
+// offsets per tap, then the logits).  One thread per (row, tap, 8-channel
+// group): four 16-byte corner loads, blended in f32 in the reference's
+// corner order, one 16-byte store into row r's taps x 64 halves.
+__global__ __launch_bounds__(256) void k_deform_sample(const uint16_t *__restrict__ t, int h, int w,
+                                                       const float *__restrict__ offs, int size,
+                                                       long row0, long rows,
+                                                       uint16_t *__restrict__ samples) {
+  const int taps = size * size;
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= rows * taps * 8) return;
+  const int grp = (int)(i % 8), tap = (int)(i / 8 % taps);
+  const long r = i / 8 / taps, p = row0 + r;
+  const int y = (int)(p / w), x = (int)(p % w);
+  const float *o = offs + p * 3 * taps;
+  const float half = (float)(size / 2);
+  const float py = ((float)y - half + (float)(tap / size)) + o[2 * tap];
+  const float px = ((float)x - half + (float)(tap % size)) + o[2 * tap + 1];
+  const float m = 2.0f * sigmoid_f(o[2 * taps + tap]);
+  float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  if (!(py <= -1.0f || py >= (float)h || px <= -1.0f || px >= (float)w)) {
+    const float y0f = floorf(py), x0f = floorf(px);
+    const float ly = py - y0f, lx = px - x0f, hy = 1.0f - ly, hx = 1.0f - lx;
+    const int y0 = (int)y0f, x0 = (int)x0f;
+    const float cw[4] = {hy * hx, hy * lx, ly * hx, ly * lx};
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const int cy = y0 + k / 2, cx = x0 + k % 2;
+      if (cy < 0 || cx < 0 || cy >= h || cx >= w) continue;
+      const u32x4 v = *(const u32x4 *)(t + ((long)cy * w + cx) * INTER + grp * 8);
+      uint16_t hv[8];
+      __builtin_memcpy(hv, &v, 16);
+#pragma unroll
+      for (int j = 0; j < 8; j++) acc[j] += cw[k] * h2f(hv[j]);
+    }
+  }
+  uint16_t out[8];
+#pragma unroll
+  for (int j = 0; j < 8; j++) out[j] = f2h(acc[j] * m);
+  u32x4 ov;
+  __builtin_memcpy(&ov, out, 16);
+  *(u32x4 *)(samples + (r * taps + tap) * INTER + grp * 8) = ov;
+}
+
+// One deformable ASPP branch (decoder.rs:176-218): the offset convolution
+// into f32, then per chunk of rows the samples and their product with the
+// branch weights (ReLU) into columns i x 256 of the concatenated map.
+ien_status deformable_branch(Birefnet *b, const BirefnetBlock &B, int i, int h, int w) {
+  ien_ctx *ctx = b->ctx;
+  const int size = ASPP_SIZES[i], taps = size * size;
+  const long pixels = (long)h * w;
+  ConvCall cc;
+  cc.x = b->t;
+  cc.H = h;
+  cc.W = w;
+  cc.C = INTER;
+  cc.xs = INTER;
+  cc.ks = size;
+  cc.stride = 1;
+  cc.OH = h;
+  cc.OW = w;
+  cc.row0 = 0;
+  cc.rows = pixels;
+  cc.w = B.offset[i];
+  cc.y = b->offs;
+  cc.ys = 3 * taps;
+  cc.out_f32 = 1;
+  ien_status st = launch_conv(ctx, cc);
+  const long chunk = std::max<long>(64, (long)(SAMPLE_BYTES / ((size_t)taps * INTER * 2)) / 64 * 64);
+  for (long row0 = 0; row0 < pixels && st == IEN_OK; row0 += chunk) {
+    const long rows = std::min(chunk, pixels - row0);
+    hipLaunchKernelGGL(k_deform_sample, dim3(blocks_for(rows * taps * 8, 256)), dim3(256), 0,
+                       ctx->stream, b->t, h, w, b->offs, size, row0, rows, b->samples);
+    IEN_HIP(hipGetLastError());
+    st = rows_product(ctx, b->samples, (size_t)taps * INTER, (long)taps * INTER, (size_t)rows,
+                      B.branch[i], b->cat + row0 * 4 * BRANCH + i * BRANCH, 4 * BRANCH,
+                      IEN_ACT_RELU, 0);
+  }
+  return st;
+}
+
 // decoder.rs:346-413 Block::run: in (h x w x cin) -> out (h x w x cout).
 ien_status block_run(Birefnet *b, const BirefnetBlock &B, const uint16_t *in, int h, int w,
                      uint16_t *out) {
@@ -472,8 +570,9 @@ ien_status block_run(Birefnet *b, const BirefnetBlock &B, const uint16_t *in, in
                      B.d_pool, b->d_bias);
   IEN_HIP(hipGetLastError());
   for (int i = 0; i < 4 && st == IEN_OK; i++)
-    st = conv(ctx, b->t, h, w, INTER, INTER, ASPP_SIZES[i], B.branch[i], b->cat + i * BRANCH,
-              4 * BRANCH, IEN_ACT_RELU, 0);
+    st = B.offset[i] ? deformable_branch(b, B, i, h, w)
+                     : conv(ctx, b->t, h, w, INTER, INTER, ASPP_SIZES[i], B.branch[i],
+                            b->cat + i * BRANCH, 4 * BRANCH, IEN_ACT_RELU, 0);
   if (st != IEN_OK) return st;
   hipLaunchKernelGGL(k_fill_rows, dim3(blocks_for(pixels * INTER, 256)), dim3(256), 0, ctx->stream,
                      b->a, pixels, b->d_bias);
@@ -615,6 +714,8 @@ ien_status birefnet_load(ien_ctx *ctx, const TensorSource &take, const ShapeOf &
   for (int i = 0; i < 4 && st == IEN_OK; i++)
     st = load_block(ctx, take, "block" + std::to_string(4 - i), LEVEL_CIN[i], LEVEL_COUT[i], i < 3,
                     &b->dec[i + 1]);
+  for (const BirefnetBlock &B : b->dec)
+    for (ien_matrix *m : B.offset) b->deformable = b->deformable || m != nullptr;
   const int lat_c[3] = {768, 384, 192};
   for (int i = 0; i < 3 && st == IEN_OK; i++)
     st = matrix(ctx, take, "lateral" + std::to_string(4 - i), lat_c[i], lat_c[i], true,
@@ -728,6 +829,10 @@ ien_status birefnet_reserve(Birefnet *b, size_t side, bool *grew) {
   if (e == hipSuccess) e = alloc(&b->low, Q);
   if (e == hipSuccess) e = hipMalloc((void **)&b->partial, POOL_PARTS * INTER * 4);
   if (e == hipSuccess) e = hipMalloc((void **)&b->d_bias, INTER * 4);
+  if (e == hipSuccess && b->deformable) {
+    e = hipMalloc((void **)&b->offs, Q * 3 * 49 * 4);
+    if (e == hipSuccess) e = hipMalloc((void **)&b->samples, SAMPLE_BYTES);
+  }
   if (e != hipSuccess) {
     free_maps(*b);
     return fail(IEN_ERR_GPU, "BiRefNet maps for side %zu: %s", side, hipGetErrorString(e));

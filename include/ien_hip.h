@@ -385,8 +385,9 @@ typedef enum {
  * with the GPU engine): read the weights file (weight_file.rs format, magic
  * b"REALESRG", b"SCUNET\0\0", b"LAMA\0\0\0\0" or b"BIREFNET"), check every
  * tensor, upload once.  BiRefNet's window (7 as exported, 12 in the
- * configured network) follows from its position-bias tensors; its ASPP must
- * be deformable-free (all-zero offset convolutions, else IEN_ERR_WEIGHTS). */
+ * configured network) follows from its position-bias tensors; an ASPP
+ * branch with all-zero offset convolutions runs as a plain convolution,
+ * any other as the deformable convolution (decoder.rs:176-313). */
 ien_status ien_model_load(ien_ctx *ctx, ien_model_kind kind, const char *weights_path,
                           ien_model **out);
 /* The same from weights already in memory: `tensors` name/shape/value

@@ -4,7 +4,7 @@ against the oracle's or_birefnet_run: the configured window 12 (padded
 grids at every stage) and the reference's window 7, the fan-in and the
 configuration's trunc-normal inits; the mask compared after the sigmoid
 (max-abs 2e-2, PSNR 45 dB) and the logits within 2 % of their range; the
-deformable-offset and size checks; progress and graph replay; the
+deformable ASPP at three offset scales; the size checks; progress and graph replay; the
 configuration's 1024 x 1024 size against the oracle with both inits.  The
 logits are also held to the spread bounds (error RMS <= 1 % of their std,
 max <= 5 % of their peak)."""
@@ -50,13 +50,25 @@ def check(got, want, what):
     assert_spread(got[ring], want[ring], what=what + " ring logits")
 
 
-def test_birefnet_rejects_deformable_offsets_and_bad_sizes(ctx):
+@pytest.mark.parametrize("window,side,offsets", [(7, 64, 0.002), (7, 64, 0.3), (12, 128, 0.01)])
+def test_birefnet_deformable_matches_oracle(ctx, oracle, window, side, offsets):
+    """The deformable ASPP (decoder.rs:176-313): non-zero offset and
+    modulator convolutions, sample points moved within a pixel (0.002),
+    a few pixels (0.01) and far outside the map (0.3)."""
     import ien
 
-    t = synthetic.birefnet_tensors(offsets=0.1)
-    with pytest.raises(ien.IenError) as e:
-        ien.Model(ctx, ien.MODEL_BIREFNET, tensors=t)
-    assert e.value.status == ien.ERR_WEIGHTS
+    t = synthetic.birefnet_tensors(window=window, init="fan", offsets=offsets)
+    img = synthetic.birefnet_image(side, seed=side + 3)
+    want = oracle.birefnet_run(t, synthetic.birefnet_names(window), img, window)
+    model = ien.Model(ctx, ien.MODEL_BIREFNET, tensors=t)
+    got = model.run(img)
+    model.free()
+    check(got, want, f"deformable window {window} side {side} offsets {offsets}")
+
+
+def test_birefnet_rejects_bad_sizes(ctx):
+    import ien
+
     model = ien.Model(ctx, ien.MODEL_BIREFNET, tensors=synthetic.birefnet_tensors())
     for h, w in ((96, 96), (64, 128)):
         with pytest.raises(ien.IenError) as e:
