@@ -156,6 +156,19 @@ struct ConvCall {
 
 ien_status launch_conv(ien_ctx *ctx, const ConvCall &c);
 
+// conv_pair.hip: two 3x3 64 -> 64 convolutions with bias and PReLU in one
+// launch (x -> w1 -> w2 -> y, the intermediate map never stored): NHWC f16
+// maps of H x W x 64, 16-byte aligned, x and y not overlapping.
+struct PairCall {
+  const uint16_t *x = nullptr;
+  uint16_t *y = nullptr;
+  int H = 0, W = 0;
+  const ien_matrix *w1 = nullptr, *w2 = nullptr;
+  const float *s1 = nullptr, *s2 = nullptr;  // PReLU slopes
+};
+bool pair_supported(const PairCall &p);
+ien_status launch_pair(ien_ctx *ctx, const PairCall &p);
+
 // io.hip: the 8-bit image passes of the models' u8 entry points, on the
 // context's stream (to_float, to_byte, LaMa's mask and compositing,
 // BiRefNet's normalisation of interleaved RGB).

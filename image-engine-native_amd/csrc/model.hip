@@ -286,11 +286,35 @@ static ien_status enqueue_esrgan(ien_model *model, const float *d_image, size_t 
   ien_status st = ien_pad_image(ctx, IEN_PAD_REPLICATE, d_image, nullptr, width, height, 1,
                                 m.image, 4);
   if (st != IEN_OK) return st;
+  // Layer i writes `a` when i is even, `b` when odd (gpu.rs:163-169); two
+  // body layers in one launch where the pair kernel takes them, from one
+  // map to the other (so that a pair of layers 2k - 1, 2k also ends in `a`).
+  uint16_t *ma = m.a, *mb = m.b;
   for (int i = 0; i < STEPS; i++) {
     const EsrganLayer &l = model->layers[i];
-    // Layer i writes `a` when i is even, `b` when odd (gpu.rs:163-169).
-    const uint16_t *src = i == 0 ? m.image : (i % 2 == 1 ? m.a : m.b);
-    uint16_t *dst = i % 2 == 0 ? m.a : m.b;
+    const uint16_t *src = i == 0 ? m.image : (i % 2 == 1 ? ma : mb);
+    uint16_t *dst = i % 2 == 0 ? ma : mb;
+    if (i % 2 == 1 && i + 1 < STEPS - 1) {
+      PairCall pc;
+      pc.x = ma;
+      pc.y = mb;
+      pc.H = (int)height;
+      pc.W = (int)width;
+      pc.w1 = l.conv;
+      pc.s1 = l.d_slope;
+      pc.w2 = model->layers[i + 1].conv;
+      pc.s2 = model->layers[i + 1].d_slope;
+      if (pair_supported(pc)) {
+        // Layers i and i + 1 from `a` into `b`, then the roles swap back:
+        // the next layer reads what this pair wrote.
+        if ((st = launch_pair(ctx, pc)) != IEN_OK) return st;
+        std::swap(ma, mb);
+        for (int k = 0; k < 2; k++)
+          if (steps && (st = steps->step(ctx->stream)) != IEN_OK) return st;
+        i++;
+        continue;
+      }
+    }
     ConvCall c;
     c.x = src;
     c.H = (int)height;

@@ -76,6 +76,61 @@ def test_config_size_device_path_and_graph(ctx, oracle, tensors):
     model.free()
 
 
+def unfused_network(ctx, tensors, image):
+    """The network from one-layer products through the C ABI: the input as
+    the model stages it (an f16 map of 4 channels, the fourth zero), the
+    first layer with its weights expanded to 4 channels (the four-channel
+    kernel), the 32 body layers and the last through ien_multiply_ex (the
+    resident kernel), then the pixel shuffle."""
+    import torch
+    import ien
+
+    h, w, _ = image.shape
+    layers = synthetic.esrgan_layers(tensors)
+    d_img = torch.from_numpy(image).cuda()
+    x = torch.zeros((h * w, 4), dtype=torch.float16, device="cuda")
+    ien.pad_image(ctx, ien.PAD_REPLICATE, d_img, None, w, h, 1, x, 4)
+    maps = [torch.empty((h * w, 64), dtype=torch.float16, device="cuda") for _ in range(2)]
+    last = torch.empty((h * w, 48), dtype=torch.float16, device="cuda")
+    keep = []
+    for i, (wt, b, slope) in enumerate(layers):
+        if i == 0:
+            w4 = np.zeros((36, wt.shape[1]), np.float32)
+            for t in range(9):
+                w4[4 * t:4 * t + 3] = wt[3 * t:3 * t + 3]
+            wt, src, cin = w4, x, 4
+        else:
+            src, cin = maps[(i - 1) % 2], 64
+        m = ien.Matrix(ctx, wt, b)
+        sl = None if slope is None else torch.from_numpy(slope).cuda()
+        keep += [m, sl]
+        dst = last if i == len(layers) - 1 else maps[i % 2]
+        inp = ien.image_input(src, h, w, cin)
+        ien.multiply_ex(ctx, inp, 0, h * w, m, dst, dst.shape[1],
+                        act=ien.ACT_PRELU if slope is not None else ien.ACT_NONE, slope=sl)
+    out = torch.empty((4 * h, 4 * w, 3), dtype=torch.float32, device="cuda")
+    ien.pixel_shuffle_add(ctx, last, 48, d_img, w, h, out)
+    torch.cuda.synchronize()
+    for m in keep[::2]:
+        m.free()
+    return out.cpu().numpy()
+
+
+@pytest.mark.parametrize("h,w", [(256, 384), (50, 70), (16, 24), (37, 100)])
+def test_body_pairs_equal_single_layers(ctx, tensors, h, w):
+    """The model runs its body two layers per launch; the same network from
+    one-layer launches gives the same bits (tiles of 16 x 24 at the
+    configured size, ragged edge tiles, a single tile)."""
+    import ien
+
+    image = synthetic.esrgan_image(h, w, seed=h + w)
+    model = ien.Model(ctx, ien.MODEL_REALESRGAN, tensors=tensors)
+    got = model.run(image)
+    model.free()
+    want = unfused_network(ctx, tensors, image)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), float(np.abs(got - want).max())
+
+
 def test_progress_and_cancel(ctx, tensors):
     """lib.rs:168-188: progress after each of the 34 layers, monotone, ending
     at 1; breaking cancels, the model stays usable and the next run is
