@@ -326,3 +326,34 @@ ien_status launch_pair(ien_ctx *ctx, const PairCall &p) {
 }
 
 }  // namespace ien
+
+using namespace ien;
+
+extern "C" ien_status ien_conv3_pair(ien_ctx *ctx, const uint16_t *d_x, uint16_t *d_y,
+                                     size_t height, size_t width, const ien_matrix *w1,
+                                     const float *d_slope1, const ien_matrix *w2,
+                                     const float *d_slope2) {
+  IEN_CHECK(ctx && d_x && d_y && w1 && w2 && d_slope1 && d_slope2, IEN_ERR_INPUT,
+            "null argument");
+  IEN_CHECK(height > 0 && width > 0 && height < (1u << 20) && width < (1u << 20), IEN_ERR_INPUT,
+            "map of %zu x %zu", height, width);
+  for (const ien_matrix *m : {w1, w2})
+    IEN_CHECK(m->k == 9 * C && m->n == C, IEN_ERR_INPUT,
+              "pair layers are 3x3 64->64 (k 576, n 64), not k %zu, n %zu", m->k, m->n);
+  const size_t bytes = height * width * C * 2;
+  IEN_CHECK(bytes <= 0x7fff0000UL, IEN_ERR_INPUT, "map of %zu bytes over 2 GiB", bytes);
+  IEN_CHECK((((uintptr_t)d_x | (uintptr_t)d_y) & 15) == 0, IEN_ERR_INPUT,
+            "maps must be 16-byte aligned");
+  const uintptr_t x = (uintptr_t)d_x, y = (uintptr_t)d_y;
+  IEN_CHECK(x + bytes <= y || y + bytes <= x, IEN_ERR_INPUT, "input and output maps overlap");
+  PairCall p;
+  p.x = d_x;
+  p.y = d_y;
+  p.H = (int)height;
+  p.W = (int)width;
+  p.w1 = w1;
+  p.s1 = d_slope1;
+  p.w2 = w2;
+  p.s2 = d_slope2;
+  return launch_pair(ctx, p);
+}

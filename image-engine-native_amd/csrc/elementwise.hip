@@ -89,6 +89,49 @@ __global__ void k_shuffle_add(const uint16_t *__restrict__ last, long last_strid
   }
 }
 
+// The same sums a workgroup per run of up to 64 input pixels of one row:
+// their 48-half records come in as 16-byte loads (staged in LDS), each
+// thread (pixel, sub-row i) builds its 12 output floats into the LDS copy
+// of the 4 output rows (4 x 3 KiB), and those go out as 16-byte stores,
+// consecutive threads on consecutive chunks of a row.  Grid: x over runs
+// of 64 pixels, y over input rows.  Needs 16-byte aligned pixel records
+// and output.
+constexpr int SHUF_PX = 64;
+__global__ __launch_bounds__(256) void k_shuffle_add16(const uint16_t *__restrict__ last,
+                                                       long last_stride,
+                                                       const float *__restrict__ image, int width,
+                                                       float *__restrict__ out) {
+  __shared__ uint4 rec[SHUF_PX * 6];          // 48 halves a pixel
+  __shared__ float4v rows[4 * SHUF_PX * 3];   // 4 rows of 4 SHUF_PX pixels x RGB
+  const int t = threadIdx.x, y = blockIdx.y, x0 = blockIdx.x * SHUF_PX;
+  const int n = min(SHUF_PX, width - x0);  // pixels in this run
+  const long p0 = (long)y * width + x0;
+  for (int q = t; q < n * 6; q += 256)
+    rec[q] = *(const uint4 *)(last + (p0 + q / 6) * last_stride + 8 * (q % 6));
+  __syncthreads();
+  {
+    const int px = t >> 2, i = t & 3;
+    if (px < n) {
+      const uint16_t *h = (const uint16_t *)(rec + px * 6);
+      const float im[3] = {image[3 * (p0 + px)], image[3 * (p0 + px) + 1],
+                           image[3 * (p0 + px) + 2]};
+      float v[12];
+#pragma unroll
+      for (int j = 0; j < 4; j++)
+#pragma unroll
+        for (int c = 0; c < 3; c++) v[3 * j + c] = h2f_e(h[16 * c + 4 * i + j]) + im[c];
+#pragma unroll
+      for (int k = 0; k < 3; k++)
+        rows[(i * SHUF_PX + px) * 3 + k] = float4v{v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]};
+    }
+  }
+  __syncthreads();
+  for (int q = t; q < 4 * n * 3; q += 256) {
+    const int i = q / (3 * n), c = q - i * 3 * n;
+    *(float4v *)(out + 12L * width * (4L * y + i) + 12L * x0 + 4 * c) = rows[i * SHUF_PX * 3 + c];
+  }
+}
+
 // ---- math.rs:95-116 LayerNorm: one wave per row, two passes over ---------
 // registers, f32 statistics, epsilon 1e-5.
 __global__ __launch_bounds__(256) void k_layer_norm(uint16_t *__restrict__ x, long rows, int c,
@@ -517,9 +560,18 @@ ien_status ien_pixel_shuffle_add(ien_ctx *ctx, const uint16_t *d_last, size_t la
   IEN_CHECK(ctx && d_last && d_image && d_out, IEN_ERR_INPUT, "null argument");
   IEN_CHECK(width > 0 && height > 0, IEN_ERR_INPUT, "empty %zu x %zu image", width, height);
   IEN_CHECK(last_stride >= 48, IEN_ERR_INPUT, "last layer stride %zu under 48", last_stride);
-  size_t total = width * height * 16;
-  hipLaunchKernelGGL(k_shuffle_add, dim3(grid_for(total, 256)), dim3(256), 0, ctx->stream, d_last,
-                     (long)last_stride, d_image, (int)width, (int)height, d_out);
+  IEN_CHECK(width < (1u << 28) && height < (1u << 28), IEN_ERR_INPUT, "image of %zu x %zu",
+            width, height);
+  if (last_stride % 8 == 0 && (((uintptr_t)d_last | (uintptr_t)d_out) & 15) == 0 &&
+      height <= 65535) {  // input rows on the grid's y
+    const dim3 grid((unsigned)((width + SHUF_PX - 1) / SHUF_PX), (unsigned)height);
+    hipLaunchKernelGGL(k_shuffle_add16, grid, dim3(256), 0, ctx->stream, d_last, (long)last_stride,
+                       d_image, (int)width, d_out);
+  } else {
+    size_t total = width * height * 16;
+    hipLaunchKernelGGL(k_shuffle_add, dim3(grid_for(total, 256)), dim3(256), 0, ctx->stream, d_last,
+                       (long)last_stride, d_image, (int)width, (int)height, d_out);
+  }
   IEN_HIP(hipGetLastError());
   return IEN_OK;
 }

@@ -155,6 +155,17 @@ ien_status ien_multiply_ex(ien_ctx *ctx, const ien_input *input, size_t row0, si
 ien_status ien_conv3(ien_ctx *ctx, const ien_input *input, const ien_matrix *w, void *d_out,
                      size_t stride, int accumulate, ien_act finish, const float *d_slope);
 
+/* realesrgan-native network.rs:96-109, two consecutive body steps in one
+ * launch: y = prelu(conv3(prelu(conv3(x, w1), s1), w2), s2) on an
+ * H x W x 64 f16 NHWC map (pixels 64 halves apart, zero padding), both
+ * layers 3x3 64->64 with their bias and PReLU slopes (device f32, 64
+ * each).  The first layer's results stay on chip as f16, so y is bit for
+ * bit what two ien_multiply_ex launches of the layers give.  x and y are
+ * 16-byte aligned and do not overlap. */
+ien_status ien_conv3_pair(ien_ctx *ctx, const uint16_t *d_x, uint16_t *d_y, size_t height,
+                          size_t width, const ien_matrix *w1, const float *d_slope1,
+                          const ien_matrix *w2, const float *d_slope2);
+
 /* ---- elementwise: crates/native-engine/src/math.rs --------------------- */
 /* math.rs:154-170 layer_norm over rows of c values (f16 in place, f32
  * statistics, epsilon 1e-5); gamma/beta device f32. */

@@ -131,6 +131,66 @@ def test_body_pairs_equal_single_layers(ctx, tensors, h, w):
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), float(np.abs(got - want).max())
 
 
+def pair_inputs(ctx, tensors, h, w, seed):
+    import torch
+    import ien
+
+    (w1, b1, s1), (w2, b2, s2) = synthetic.esrgan_layers(tensors)[1:3]
+    x = np.random.default_rng(seed).standard_normal((h, w, 64)).astype(np.float16)
+    m1, m2 = ien.Matrix(ctx, w1, b1), ien.Matrix(ctx, w2, b2)
+    sl1, sl2 = torch.from_numpy(s1).cuda(), torch.from_numpy(s2).cuda()
+    return x, (w1, b1, s1, w2, b2, s2), m1, sl1, m2, sl2
+
+
+@pytest.mark.parametrize("h,w", [(256, 384), (33, 49), (16, 24), (1, 1)])
+def test_conv3_pair_op(ctx, oracle, tensors, h, w):
+    """ien_conv3_pair (two body steps of network.rs:96-109 in one launch):
+    bit for bit two single-layer ien_multiply_ex launches, and close to the
+    oracle's two conv3 + PReLU steps with the intermediate map rounded to
+    f16 as the GPU stores it (error RMS <= 0.2 % of the output's spread)."""
+    import torch
+    import ien
+
+    x, (w1, b1, s1, w2, b2, s2), m1, sl1, m2, sl2 = pair_inputs(ctx, tensors, h, w, seed=h * w)
+    dx = torch.from_numpy(x).cuda()
+    dy = torch.empty_like(dx)
+    mid = torch.empty_like(dx)
+    ref = torch.empty_like(dx)
+    ien.conv3_pair(ctx, dx, dy, h, w, m1, sl1, m2, sl2)
+    ien.multiply_ex(ctx, ien.image_input(dx, h, w, 64), 0, h * w, m1, mid, 64, act=ien.ACT_PRELU, slope=sl1)
+    ien.multiply_ex(ctx, ien.image_input(mid, h, w, 64), 0, h * w, m2, ref, 64, act=ien.ACT_PRELU, slope=sl2)
+    torch.cuda.synchronize()
+    got = dy.cpu().numpy()
+    assert np.array_equal(got.view(np.uint16), ref.cpu().numpy().view(np.uint16))
+    first = oracle.conv3(x, w1, b1, finish=oracle.FINISH_PRELU, slope=s1, threads=8)
+    want = oracle.conv3(first.astype(np.float16), w2, b2, finish=oracle.FINISH_PRELU, slope=s2, threads=8)
+    assert_spread(got.astype(np.float32), want, rms_frac=2e-3, max_frac=1e-2, what=f"pair {h}x{w}")
+    m1.free()
+    m2.free()
+
+
+def test_conv3_pair_refusals(ctx, tensors):
+    """Overlapping maps, misaligned maps and layers that are not 3x3 64->64
+    are refused before anything is launched."""
+    import torch
+    import ien
+
+    h, w = 8, 8
+    x, _, m1, sl1, m2, sl2 = pair_inputs(ctx, tensors, h, w, seed=1)
+    buf = torch.zeros(3 * h * w * 64, dtype=torch.float16, device="cuda")
+    last_w, last_b, _ = synthetic.esrgan_layers(tensors)[-1]
+    m_last = ien.Matrix(ctx, last_w, last_b)
+    cases = ((buf[: h * w * 64], buf[h * w * 32: h * w * 96], m2, "overlap"),
+             (buf[1: 1 + h * w * 64], buf[2 * h * w * 64:], m2, "aligned"),
+             (buf[: h * w * 64], buf[2 * h * w * 64:], m_last, "k 576, n 48"))
+    for src, dst, second, message in cases:
+        with pytest.raises(ien.IenError) as e:
+            ien.conv3_pair(ctx, src, dst, h, w, m1, sl1, second, sl2)
+        assert e.value.status == ien.ERR_INPUT and message in str(e.value), str(e.value)
+    for m in (m1, m2, m_last):
+        m.free()
+
+
 def test_progress_and_cancel(ctx, tensors):
     """lib.rs:168-188: progress after each of the 34 layers, monotone, ending
     at 1; breaking cancels, the model stays usable and the next run is
