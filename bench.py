@@ -10,15 +10,15 @@ A step is one forward pass of the whole network over one synthetic image
 input already resident in HBM: the 36 launches of a step are replayed from
 one HIP graph.  Prints one JSON line.
 
-roofline: the dominant kernel is conv_pair, two consecutive body layers
-(3x3 64->64 + PReLU each) per launch, 16 of the 36 launches of a step and
-32 of its 34 layers.  Its algorithmic work per launch is
-2 layers * 2 * 98304 px * 64 * 576 = 14.496 GFLOP (the halo recomputed by
+roofline: the dominant kernel is the body chain, the 32 body layers (3x3
+64->64 + PReLU each, 16 pairs) in one launch, 32 of the 34 layers of a
+step.  Its algorithmic work per launch is
+32 layers * 2 * 98304 px * 64 * 576 = 231.9 GFLOP (the halo recomputed by
 neighbouring tiles is not counted); its average duration is measured with
 HIP events on the library's stream over back-to-back launches
-(ien_conv3_pair).  `traffic` (HBM bytes per launch from rocprofv3
+(ien_conv3_chain, each after the clear of its flags, as in the model).  `traffic` (HBM bytes per launch from rocprofv3
 FETCH_SIZE / WRITE_SIZE, scaled by a copy kernel of known size) is read
-from profiles/conv_pair_256x384_hbm_traffic.txt when that summary exists.
+from profiles/conv_chain_256x384_hbm_traffic.txt when that summary exists.
 
 cpu_baseline: the oracle -- the C restatement of the reference's CPU f32
 path (crates/realesrgan-native/src/network.rs over native-engine's
@@ -144,7 +144,7 @@ def sweep(ctx, stream, reps):
 
 
 def traffic_from_profiles():
-    path = ROOT / "profiles" / "conv_pair_256x384_hbm_traffic.txt"
+    path = ROOT / "profiles" / "conv_chain_256x384_hbm_traffic.txt"
     if not path.exists():
         return None
     m = re.search(r"^traffic_bytes_per_launch:\s*([0-9.eE+]+)", path.read_text(), re.M)
@@ -229,28 +229,29 @@ def cpu_sweep(runs):
                       f"on {cpu_model()}; the oracle (conv3 F(4x4)/F(2x2) for 3x3, multiply for 1x1)"}
 
 
-def body_pair(ctx, tensors, H, W):
-    """The dominant launch: two body layers (3x3 64->64 + PReLU each, body
-    weights 1 and 2) at H x W on a seeded N(0, 1) f16 NHWC map, through
-    ien_conv3_pair; returns (launch, free)."""
+def body_chain(ctx, tensors, H, W):
+    """The dominant launch: the 32 body layers (3x3 64->64 + PReLU each, the
+    model's body weights) at H x W on a seeded N(0, 1) f16 NHWC map, through
+    ien_conv3_chain; returns (launch, free)."""
     import numpy as np
     import torch
 
     import ien
     import synthetic
 
-    (w1, b1, s1), (w2, b2, s2) = synthetic.esrgan_layers(tensors)[1:3]
-    m1, m2 = ien.Matrix(ctx, w1, b1), ien.Matrix(ctx, w2, b2)
-    sl1, sl2 = torch.from_numpy(s1).cuda(), torch.from_numpy(s2).cuda()
+    layers = synthetic.esrgan_layers(tensors)[1:33]
+    mats = [ien.Matrix(ctx, w, b) for w, b, _ in layers]
+    slopes = [torch.from_numpy(s).cuda() for _, _, s in layers]
     src = torch.from_numpy(np.random.default_rng(3).standard_normal((H * W, 64))).half().cuda()
-    dst = torch.empty((H * W, 64), dtype=torch.float16, device="cuda")
+    other = torch.empty((H * W, 64), dtype=torch.float16, device="cuda")
 
     def launch():
-        ien.conv3_pair(ctx, src, dst, H, W, m1, sl1, m2, sl2)
+        ien.conv3_chain(ctx, src, other, H, W, mats, slopes)
 
     def free():
-        m1.free()
-        m2.free()
+        ien.conv3_chain_status(ctx)
+        for m in mats:
+            m.free()
 
     return launch, free
 
@@ -260,7 +261,7 @@ def traffic_probe(ctx, tensors, H, W):
     (a kernel of known traffic, for scaling FETCH_SIZE and WRITE_SIZE)."""
     import torch
 
-    launch, free = body_pair(ctx, tensors, H, W)
+    launch, free = body_chain(ctx, tensors, H, W)
     for _ in range(10):
         launch()
     torch.cuda.synchronize()
@@ -270,7 +271,7 @@ def traffic_probe(ctx, tensors, H, W):
     c.copy_(a)
     torch.cuda.synchronize()
     free()
-    print("traffic probe: body pair x10, then a 134217728-byte copy", flush=True)
+    print("traffic probe: body chain x10, then a 134217728-byte copy", flush=True)
 
 
 def host_path_ms(run, reps=3):
@@ -528,17 +529,17 @@ def main():
     if not bool(torch.isfinite(d_out).all()):
         sys.exit("non-finite output")
 
-    # Dominant kernel: two body layers (3x3 64->64 + PReLU) per launch at 256x384.
-    body, body_free = body_pair(ctx, tensors, H, W)
+    # Dominant kernel: the 32 body layers (3x3 64->64 + PReLU) in one launch at 256x384.
+    body, body_free = body_chain(ctx, tensors, H, W)
     for _ in range(5):
         body()
-    kms = event_time(body, args.kernel_reps, stream)
-    flops = 2 * conv_flops(H, W, 64, 64, 3)
+    kms = event_time(body, max(10, args.kernel_reps // 10), stream)
+    flops = 32 * conv_flops(H, W, 64, 64, 3)
     achieved = flops / (kms * 1e-3) / 1e12
     roofline = {"bound": "mfma", "achieved": round(achieved, 1), "peak": MFMA_F16_PEAK_TFLOPS,
                 "unit": "TFLOP/s", "frac": round(achieved / MFMA_F16_PEAK_TFLOPS, 4),
                 "traffic": traffic_from_profiles(),
-                "kernel": "conv_pair (two 3x3 64->64 + PReLU body layers per launch, 256x384)",
+                "kernel": "conv_pair<chain> (the 32 3x3 64->64 + PReLU body layers in one launch, 256x384)",
                 "kernel_us": round(kms * 1e3, 2), "flop_per_launch": flops}
     body_free()
 

@@ -1,13 +1,14 @@
-// conv_pair.hip -- two consecutive 3x3 64 -> 64 convolutions, each with
-// bias and PReLU, in one launch: a pair of Real-ESRGAN's body layers
+// conv_pair.hip -- consecutive 3x3 64 -> 64 convolutions, each with bias
+// and PReLU, two per tile pass: pairs of Real-ESRGAN's body layers
 // (crates/realesrgan-native/src/network.rs:96-109; gemm.rs multiply order).
 //
 // A launch of one such layer at 256 x 384 spends about as long on fixed
 // costs (the gap after the previous kernel, the weights landing, the last
-// stores draining) as on its products; a pair pays them once.
+// stores draining) as on its products; a pair pays them once, and a chain
+// of pairs (the whole body in one launch) once for all of them.
 //
-// One workgroup of 8 waves (two per SIMD) computes a 16 x 24 tile of the
-// second layer's outputs:
+// One workgroup of 8 waves (two per SIMD) computes a 16 x 24 tile of a
+// pair's second layer:
 //  - The input halo, 20 x 28 pixels of 64 channels, is loaded straight into
 //    LDS (zeros outside the image, from the buffer range check), each pixel
 //    followed by a 16-byte pad chunk and each row by 224 bytes, so that
@@ -18,18 +19,33 @@
 //    twice).  Pixels outside the image are stored as zeros: the second
 //    layer's zero padding.  The results go to LDS as f16, rounded as the
 //    map between two separate launches would hold them.
-//  - Phase 2: the second layer on the 16 x 24 output pixels (12 blocks),
-//    each wave storing its own results as they are finished.
+//  - Phase 2: the second layer on the 16 x 24 output pixels (12 blocks).
 // Wave w takes the 32 output channels of half w / 4 and the blocks w % 4,
 // w % 4 + 4, ...; it holds that half of one layer's packed weights in
 // registers (36 fragments, the A operand of v_mfma_f32_32x32x16_f16, so the
-// product is C^T = W^T X^T): the first layer's loaded once per workgroup
-// into LDS beside the halo, the second's straight from memory, each
-// fragment as soon as the first layer's last product with it has been
-// issued.  Every
-// accumulator is seeded with the bias and sums the 36 steps (9 taps x 16
-// channels, taps first) in the order of the one-layer resident kernel, so
-// a pair gives the same bits as two launches of it.
+// product is C^T = W^T X^T), each layer's loaded once per workgroup into
+// LDS and from there into registers.  Every accumulator is seeded with the
+// bias and sums the 36 steps (9 taps x 16 channels, taps first) in the
+// order of the one-layer resident kernel, so a pair gives the same bits as
+// two launches of it.
+//
+// A chain runs P pairs in one launch with one workgroup per tile, all
+// resident at once (at most one per CU).  A tile keeps its pair output in
+// LDS as the centre of the next pair's halo and exchanges only the 2-pixel
+// ring with its 8 neighbours: after pair k it stores the outer 2 rows and
+// columns of its output to border map k % 2 and, once those stores are
+// complete, publishes epoch k + 1; pair k + 1 waits until each neighbour's
+// epoch reaches k + 1 and loads its ring from that map.  The neighbours may
+// run on other XCDs, whose L2 caches are not kept coherent with this one:
+// the border stores, the ring loads and the epoch words all use device
+// scope (the sc1 cache policy: written through to, and read from, the
+// device's point of coherence), so no cache-wide write-back or invalidate
+// is needed.  A neighbour only publishes after it has
+// read its own ring from the other map, so a border map is never rewritten
+// while a reader still needs it.  Every wait is bounded by a wall-clock
+// limit; a tile that runs out sets an abort word that every other waiting
+// tile sees, so all workgroups end (the run reports the failure).  The last
+// pair stores the whole tile.
 
 #include "conv_common.h"
 
@@ -41,92 +57,141 @@ constexpr int OTR = 16, OTC = 24;          // output tile
 constexpr int MR = OTR + 2, MC = OTC + 2;  // first layer's pixels: 18 x 26
 constexpr int IR = OTR + 4, IC = OTC + 4;  // input halo: 20 x 28
 constexpr int PB = 2 * C + 16;             // bytes of a staged pixel
-// Staged rows end with 224 bytes of padding: 144-byte pixels put 16
-// consecutive pixels on disjoint banks, and with the padding a block's step
-// from the last pixel of a row to the first of the next (3 pixels on in the
-// staged row) lands on the banks of a one-pixel step, so no B-fragment read
-// conflicts even where a block spans rows.
-constexpr int RPAD = 224;
-constexpr int HROW = IC * PB + RPAD, MROW = MC * PB + RPAD;  // bytes a staged row
+// Staged rows end with padding, which with 144-byte pixels (16
+// consecutive pixels on disjoint banks) makes a block's step from the last
+// pixel of one of its rows to the first of the next land on the banks of a
+// one-pixel step, so no B-fragment read conflicts even where a block spans
+// rows: the first layer's results are read in rows of 24 (of 26), the halo
+// in rows of 26 (of 28) by a single pair and, interior first, in rows of
+// 22 by a chain.
+constexpr int MROW = MC * PB + 224;  // bytes a staged row of the first layer's results
 constexpr int MPIX = MR * MC, OPIX = OTR * OTC;
-constexpr int HALO = IR * HROW;
-constexpr int MID = HALO;  // first layer's results; its weights before them
 constexpr int WBYTES = 2 * (9 * C / 16) * 1024;  // both halves of a layer
-constexpr int MIDSZ = std::max(MR * MROW, WBYTES);
-constexpr int PARAM = MID + MIDSZ;
-constexpr int LDS = PARAM + 4 * C * 4;                  // bias 1, slope 1, bias 2, slope 2
 constexpr int STEPS = 9 * C / 16;
 constexpr int MBLK = (MPIX + 31) / 32, OBLK = OPIX / 32;
 constexpr int WAVES = 8, THREADS = 64 * WAVES;
-constexpr int HLOADS = (HALO + 1024 * WAVES - 1) / (1024 * WAVES);  // 1 KiB halo loads per wave
 constexpr int WLOADS = WBYTES / (1024 * WAVES);  // 1 KiB weight loads per wave
-static_assert(LDS <= 160 * 1024, "LDS budget");
-static_assert(HALO % 16 == 0 && (RPAD + 2 * PB) % 256 == 0, "row padding");
-static_assert(MBLK <= 16 && OBLK == 12, "block split over the waves");
-static_assert(HLOADS + WLOADS < 64 && WLOADS * 1024 * WAVES == WBYTES, "load split");
-static_assert((WAVES - 1 + WAVES * (HLOADS - 2)) * 1024 + 1024 <= HALO, "halo loads before the last");
+constexpr int BORDER = 4 * OTC + 4 * (OTR - 4);  // output pixels in the outer 2 rows / columns
+constexpr int INNER = (MR - 4) * (MC - 4);       // first-layer pixels that read no halo ring
+constexpr int MAXPAIRS = 16;
+static_assert((MROW - 23 * PB) % 256 == PB, "first layer's rows");
+static_assert(MBLK <= 16 && OBLK == 12 && INNER >= 8 * 32, "block split over the waves");
+static_assert(WLOADS * 1024 * WAVES == WBYTES, "weight loads");
+
+// LDS layout: the halo, then the first layer's results (its weights before
+// them), then the biases and slopes of both layers.
+template <bool CHAIN>
+struct Geo {
+  static constexpr int HROW = IC * PB + (CHAIN ? 160 : 224);  // bytes a staged halo row
+  static constexpr int HALO = IR * HROW;
+  static constexpr int MID = HALO;
+  static constexpr int PARAM = MID + std::max(MR * MROW, WBYTES);
+  static constexpr int LDS = PARAM + 4 * C * 4;
+  static constexpr int HLOADS = (HALO + 1024 * WAVES - 1) / (1024 * WAVES);  // 1 KiB loads a wave
+  static constexpr int RSPAN = (2 * HROW + 1023) / 1024;  // 1 KiB loads of two ring rows
+  static_assert(LDS <= 160 * 1024 && HALO % 16 == 0, "LDS budget");
+  static_assert((HROW - ((CHAIN ? MC - 4 : MC) - 1) * PB) % 256 == PB, "halo rows");
+  static_assert(HLOADS + WLOADS < 64, "load split");
+  static_assert((WAVES - 1 + WAVES * (HLOADS - 2)) * 1024 + 1024 <= HALO, "halo loads before the last");
+  static_assert(WBYTES <= HALO, "second layer's weights in the halo");
+};
+
+// The first layer's pixel i (of MPIX) in a pass order: row-major, or for a
+// chain the INNER pixels that read only the halo's centre first (rows 2 ..
+// 15, columns 2 .. 23, row-major), then rows 0, 1, then columns 0, 1, 24,
+// 25 of rows 2 .. 15, then rows 16, 17.
+template <bool CHAIN>
+__device__ __forceinline__ int first_pixel(int i) {
+  if (!CHAIN) return i;
+  if (i < INNER) return (2 + i / (MC - 4)) * MC + 2 + i % (MC - 4);
+  i -= INNER;
+  if (i < 2 * MC) return i;
+  i -= 2 * MC;
+  if (i < 4 * (MR - 4)) {
+    const int c = i & 3;
+    return (2 + (i >> 2)) * MC + (c < 2 ? c : c + MC - 4);
+  }
+  return (MR - 2) * MC + i - 4 * (MR - 4);
+}
 
 struct PairArgs {
-  const uint16_t *x;  // H x W x 64 f16 (pixels 64 halves apart)
-  uint16_t *y;        // the same shape; must not overlap x
-  int H, W, tiles_x;
-  const uint16_t *w1, *w2;  // packed weights (fragment (kb, nb) at (nb KB + kb) 512 halves)
-  int KB;
-  const float *b1, *s1, *b2, *s2;  // biases and PReLU slopes (64 each)
+  const uint16_t *x;  // H x W x 64 f16 input (pixels 64 halves apart)
+  uint16_t *y;        // the same shape: the last pair's output
+  int H, W, tiles_x, tiles_y;
+  int KB;     // fragments along k of each layer (36)
+  int pairs;  // 1, or the chain's length
+  // Layer 2 k and 2 k + 1 of pair k: packed weights (fragment (kb, nb) at
+  // (nb KB + kb) 512 halves), biases and PReLU slopes (64 each).
+  const uint16_t *w[2 * MAXPAIRS];
+  const float *b[2 * MAXPAIRS], *s[2 * MAXPAIRS];
+  // Chain only: the border maps (pair k stores to border[k % 2]); the
+  // flags: the abort word (zero at launch), the failure word (set with it,
+  // kept until the host reads it), then the tile epochs (tiles_x tiles_y
+  // words, zero at launch); and the wall-clock ticks (100 MHz) a wait for
+  // neighbours may take.
+  uint16_t *border[2];
+  int *flags;
+  long spin_limit;
 };
 
 constexpr int OOB = 0x7ffffff0;
+constexpr int SC1 = 16;  // cache policy bits of a device-scope buffer access
 
+// dma_lds at device scope (sc1): the load bypasses copies in this XCD's
+// caches that another XCD's device-scope stores may have made stale.
+__device__ __forceinline__ void dma_lds_device(int4v rsrc, unsigned wave_base, int off) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen sc1 lds"
+               :: "s"(wave_base), "v"(off), "s"(rsrc) : "memory", "m0");
+}
+
+template <bool CHAIN>
 __global__ __launch_bounds__(THREADS) void conv_pair(PairArgs a) {
-  __shared__ __attribute__((aligned(1024))) unsigned char lds[LDS];
+  using G = Geo<CHAIN>;
+  constexpr int HROW = G::HROW, HALO = G::HALO, MID = G::MID, PARAM = G::PARAM;
+  __shared__ __attribute__((aligned(1024))) unsigned char lds[G::LDS];
+  __shared__ int go;  // chain: 1 when every neighbour is ready
   float *par = (float *)(lds + PARAM);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int hf = wave >> 2, grp = wave & 3;  // channel half, block group
   const int tile = xcd_remap(blockIdx.x, gridDim.x);
-  const int y0 = (tile / a.tiles_x) * OTR, x0 = (tile % a.tiles_x) * OTC;
+  const int ty = tile / a.tiles_x, tx = tile % a.tiles_x;
+  const int y0 = ty * OTR, x0 = tx * OTC;
   const unsigned lds0 = lds_addr(lds);
+  const long map_bytes = (long)a.H * a.W * C * 2;
 
   // Lane l's 16 bytes of fragment (step s, channel half hf): rows 16 s +
   // 8 (l / 32) .. + 7 of output channel 32 hf + l % 32.
   half8 w[STEPS];
-  {
-    // KiB g of the halo: lane l's 16 bytes belong to halo row hy, pixel hx,
-    // chunk ch (chunk 8 and the row padding read zeros, as do offsets past
-    // the input); lanes past the halo's end load nothing.
-    const int4v xr = buffer_rsrc(a.x, (long)a.H * a.W * C * 2);
-#pragma unroll
-    for (int i = 0; i < HLOADS; i++) {
-      const int g = wave + WAVES * i, byte = g * 1024 + lane * 16;
-      const int hy = byte / HROW, within = byte - hy * HROW;
-      const int hx = within / PB, ch = (within - hx * PB) >> 4;
-      const int gy = y0 - 2 + hy, gx = x0 - 2 + hx;
-      const bool ok = hx < IC && ch < 8 && (unsigned)gy < (unsigned)a.H &&
-                      (unsigned)gx < (unsigned)a.W;
-      if (i < HLOADS - 1 || byte < HALO)  // only the last KiB runs past the halo
-        dma_lds(xr, __builtin_amdgcn_readfirstlane(lds0 + g * 1024),
-                ok ? ((gy * a.W + gx) * C + 8 * ch) * 2 : OOB);
-    }
-    // The first layer's fragments of both halves, (hf 36 + s) KiB, once per
-    // workgroup, where the first layer's results will go.
-    const int4v wr = buffer_rsrc(a.w1, WBYTES);
+  // A layer's fragments of both halves, (hf 36 + s) KiB from `at`, once per
+  // workgroup.
+  auto stage_weights = [&](const uint16_t *wp, int at) {
+    const int4v wr = buffer_rsrc(wp, WBYTES);
 #pragma unroll
     for (int i = 0; i < WLOADS; i++) {
       const int f = wave + WAVES * i;
-      dma_lds(wr, __builtin_amdgcn_readfirstlane(lds0 + MID + f * 1024), f * 1024 + lane * 16);
+      dma_lds(wr, __builtin_amdgcn_readfirstlane(lds0 + at + f * 1024), f * 1024 + lane * 16);
     }
-  }
-  if (tid < C) {
-    par[tid] = a.b1[tid];
-    par[C + tid] = a.s1[tid];
-    par[2 * C + tid] = a.b2[tid];
-    par[3 * C + tid] = a.s2[tid];
-  }
-  wait_vm<0>();
-  __syncthreads();
+  };
+  auto load_weights = [&](int at) {
 #pragma unroll
-  for (int s = 0; s < STEPS; s++) w[s] = *(const half8 *)(lds + MID + (hf * STEPS + s) * 1024 + lane * 16);
-  __syncthreads();  // every wave holds its weights: the first results may overwrite them
+    for (int s = 0; s < STEPS; s++) w[s] = *(const half8 *)(lds + at + (hf * STEPS + s) * 1024 + lane * 16);
+  };
+  auto params = [&](int k) {
+    if (tid < C) {
+      par[tid] = a.b[2 * k][tid];
+      par[C + tid] = a.s[2 * k][tid];
+      par[2 * C + tid] = a.b[2 * k + 1][tid];
+      par[3 * C + tid] = a.s[2 * k + 1][tid];
+    }
+  };
+  // Global offset of chunk ch (8 channels) of halo pixel (hy, hx), or OOB
+  // for the pad chunk and pixels outside the image.
+  auto halo_src = [&](int hy, int hx, int ch) {
+    const int gy = y0 - 2 + hy, gx = x0 - 2 + hx;
+    const bool ok = hx < IC && ch < 8 && (unsigned)gy < (unsigned)a.H && (unsigned)gx < (unsigned)a.W;
+    return ok ? ((gy * a.W + gx) * C + 8 * ch) * 2 : OOB;
+  };
 
   // The accumulators of a block, seeded with the bias: register 4 g + e is
   // channel 32 hf + 8 g + 4 (lane / 32) + e of pixel lane % 32.
@@ -183,18 +248,17 @@ __global__ __launch_bounds__(THREADS) void conv_pair(PairArgs a) {
       out[g].y &= keep;
     }
   };
-
-  // ---- phase 1: the first layer on the 18 x 26 pixels, blocks grp +
-  // 4 i (i < 4) in two passes of two; blocks past the last are computed on
-  // its final pixel and dropped ----
-#pragma unroll
-  for (int pass = 0; pass < 2; pass++) {
+  // Pass `pass` of phase 1: the first layer on blocks grp + 4 (2 pass + j),
+  // j < 2, of its pixels in first_pixel order; blocks past the last are
+  // computed on its final pixel and dropped.  Results to LDS as f16
+  // (zeros outside the image: the second layer's padding).
+  auto first_pass = [&](int pass) {
     int base[2], pix[2];
 #pragma unroll
     for (int j = 0; j < 2; j++) {
-      const int p = 32 * (grp + 4 * (2 * pass + j)) + (lane & 31);
-      pix[j] = p;
-      const int pc = p < MPIX ? p : MPIX - 1;
+      const int i = 32 * (grp + 4 * (2 * pass + j)) + (lane & 31);
+      const int pc = first_pixel<CHAIN>(i < MPIX ? i : MPIX - 1);
+      pix[j] = i < MPIX ? pc : -1;
       base[j] = (pc / MC) * HROW + (pc % MC) * PB + 16 * (lane >> 5);
     }
     floatx16 acc[2] = {seed(par), seed(par)};
@@ -205,7 +269,7 @@ __global__ __launch_bounds__(THREADS) void conv_pair(PairArgs a) {
 #pragma unroll
     for (int j = 0; j < 2; j++) {
       const int p = pix[j];
-      if (p >= MPIX) continue;
+      if (p < 0) continue;
       const int gy = y0 - 1 + p / MC, gx = x0 - 1 + p % MC;
       const bool inside = (unsigned)gy < (unsigned)a.H && (unsigned)gx < (unsigned)a.W;
       uint2 o[4];
@@ -217,112 +281,316 @@ __global__ __launch_bounds__(THREADS) void conv_pair(PairArgs a) {
       }
     }
     __builtin_amdgcn_sched_barrier(0);
-  }
-  __syncthreads();  // the first layer's results complete; the halo is free
+  };
 
-  // ---- the second layer's weights, staged where the halo was ----
-  {
-    const int4v wr = buffer_rsrc(a.w2, WBYTES);
+  int *abort_word = CHAIN ? a.flags : nullptr;
+  int *epochs = CHAIN ? a.flags + 2 : nullptr;
+  const int pairs = CHAIN ? a.pairs : 1;
+  for (int k = 0; k < pairs; k++) {
+    // ---- the first layer's weights (where its results will go) and, for
+    // a single pair or a chain's first, the whole halo from the input; a
+    // chain's later pairs find the weights staged and the halo's centre
+    // left in LDS by the pair before ----
+    if (!CHAIN || k == 0) {
+      stage_weights(a.w[2 * k], MID);
+      // KiB g of the halo: lane l's 16 bytes belong to halo row hy, pixel
+      // hx, chunk ch (chunk 8 and the row padding read zeros, as do
+      // offsets past the input); lanes past the halo's end load nothing.
+      const int4v xr = buffer_rsrc(a.x, map_bytes);
 #pragma unroll
-    for (int i = 0; i < WLOADS; i++) {
-      const int f = wave + WAVES * i;
-      dma_lds(wr, __builtin_amdgcn_readfirstlane(lds0 + f * 1024), f * 1024 + lane * 16);
+      for (int i = 0; i < G::HLOADS; i++) {
+        const int g = wave + WAVES * i, byte = g * 1024 + lane * 16;
+        const int hy = byte / HROW, within = byte - hy * HROW;
+        const int hx = within / PB, ch = (within - hx * PB) >> 4;
+        if (i < G::HLOADS - 1 || byte < HALO)  // only the last KiB runs past the halo
+          dma_lds(xr, __builtin_amdgcn_readfirstlane(lds0 + g * 1024), halo_src(hy, hx, ch));
+      }
+    }
+    params(k);
+    wait_vm<0>();  // (a chain's later pairs: also the previous border stores)
+    __syncthreads();
+    if (CHAIN && k > 0 && tid == 0)  // publish epoch k: this tile's pair k - 1 border is out
+      __hip_atomic_store(epochs + tile, k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    load_weights(MID);
+    __syncthreads();  // every wave holds its weights: the first results may overwrite them
+
+    // ---- phase 1: the first layer on the 18 x 26 pixels in two passes;
+    // a chain's first pass reads only the halo's centre, and the ring
+    // comes in between the passes ----
+    first_pass(0);
+    if (CHAIN && k > 0) {
+      // Wait for the 8 neighbours' epoch k (lanes 0..8 of wave 0, one each).
+      if (wave == 0) {
+        bool fail = false;
+        if (lane < 9 && lane != 4) {
+          const int ny = ty + lane / 3 - 1, nx = tx + lane % 3 - 1;
+          if (ny >= 0 && ny < a.tiles_y && nx >= 0 && nx < a.tiles_x) {
+            const int *f = epochs + ny * a.tiles_x + nx;
+            const unsigned long long t0 = wall_clock64();
+            while (__hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < k) {
+              if (__hip_atomic_load(abort_word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0 ||
+                  (long)(wall_clock64() - t0) > a.spin_limit) {
+                fail = true;
+                break;
+              }
+              __builtin_amdgcn_s_sleep(1);
+            }
+          }
+        }
+        const bool any = __builtin_amdgcn_ballot_w64(fail) != 0;
+        if (lane == 0) {
+          if (any) {
+            __hip_atomic_store(abort_word, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(abort_word + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          }
+          go = any ? 0 : 1;
+        }
+      }
+      __syncthreads();
+      if (go == 0) return;  // (no load of this workgroup is in flight here)
+      const int4v rr = buffer_rsrc(a.border[(k - 1) & 1], map_bytes);
+      // Staged rows 0, 1 and 18, 19: two spans of 2 rows, 1 KiB a load.
+      for (int i = wave; i < 2 * G::RSPAN; i += WAVES) {
+        const int row0 = i < G::RSPAN ? 0 : IR - 2, part = i < G::RSPAN ? i : i - G::RSPAN;
+        const int byte = part * 1024 + lane * 16;
+        const int hy = row0 + byte / HROW, within = byte % HROW;
+        const int hx = within / PB, ch = (within - hx * PB) >> 4;
+        if (byte < 2 * HROW)
+          dma_lds_device(rr, __builtin_amdgcn_readfirstlane(lds0 + row0 * HROW + part * 1024),
+                         halo_src(hy, hx, ch));
+      }
+      // Pixels 0, 1 and 26, 27 of rows 2 .. 17: 32 pieces of 2 staged
+      // pixels (18 chunks, lanes 0 .. 17).
+      for (int i = wave; i < 2 * (IR - 4); i += WAVES) {
+        const int hy = 2 + (i >> 1), hx0 = (i & 1) ? IC - 2 : 0;
+        if (lane < 18)
+          dma_lds_device(rr, __builtin_amdgcn_readfirstlane(lds0 + hy * HROW + hx0 * PB),
+                         halo_src(hy, hx0 + lane / 9, lane % 9));
+      }
+      wait_vm<0>();
+      __syncthreads();
+    }
+    first_pass(1);
+    __syncthreads();  // the first layer's results complete; the halo is free
+
+    // ---- the second layer's weights, staged where the halo was ----
+    stage_weights(a.w[2 * k + 1], 0);
+    wait_vm<0>();
+    __syncthreads();
+    load_weights(0);
+    __syncthreads();  // every wave holds its weights: the staging below may overwrite them
+
+    // ---- phase 2: the second layer on the 16 x 24 outputs, blocks grp,
+    // grp + 4, grp + 8 ----
+    int base[3];
+#pragma unroll
+    for (int j = 0; j < 3; j++) {
+      const int q = 32 * (grp + 4 * j) + (lane & 31);
+      base[j] = MID + (q / OTC) * MROW + (q % OTC) * PB + 16 * (lane >> 5);
+    }
+    floatx16 acc[3] = {seed(par + 2 * C), seed(par + 2 * C), seed(par + 2 * C)};
+    products(std::integral_constant<int, 3>{}, std::integral_constant<int, MROW>{}, base, acc);
+    float4v s4[4];
+    slopes(par + 3 * C, s4);
+
+    if constexpr (!CHAIN) {
+      // Each wave's 96 pixels of its 32 channels go out through LDS (its
+      // own 6 KiB where the halo was), so that a lane stores 16 bytes and
+      // 4 lanes a pixel's 64 contiguous bytes.  Staged pixel wp = 32 j +
+      // l % 32 holds its 4 chunks of 8 channels at chunk c ^ (wp / 4 % 4),
+      // which keeps both the writes (16 pixels, one chunk) and the reads
+      // (4 pixels, 4 chunks) free of bank conflicts.
+      unsigned char *stage = lds + wave * (OBLK / 4) * 32 * 64;
+#pragma unroll
+      for (int j = 0; j < 3; j++) {
+        uint2 o[4];
+        finish(acc[j], s4, ~0u, o);
+        const int wp = 32 * j + (lane & 31);
+#pragma unroll
+        for (int pr = 0; pr < 2; pr++) {
+          // Lanes < 32 hold channels 16 pr + 0..3 (o[2 pr]) and 16 pr +
+          // 8..11 (o[2 pr + 1]), lanes >= 32 the runs 4 above; swapping the
+          // upper half's o[2 pr] with the lower half's o[2 pr + 1] gives
+          // lane l < 32 channels 16 pr + 0..7 and lane l + 32 channels
+          // 16 pr + 8..15.
+          const auto sx = __builtin_amdgcn_permlane32_swap(o[2 * pr].x, o[2 * pr + 1].x, false, false);
+          const auto sy = __builtin_amdgcn_permlane32_swap(o[2 * pr].y, o[2 * pr + 1].y, false, false);
+          const uint4 v = {sx[0], sy[0], sx[1], sy[1]};
+          const int c = 2 * pr + (lane >> 5);
+          *(uint4 *)(stage + wp * 64 + 16 * (c ^ ((wp >> 2) & 3))) = v;
+        }
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      const __amdgpu_buffer_rsrc_t yr =
+          __builtin_amdgcn_make_buffer_rsrc(a.y, 0, (int)map_bytes, 0x00020000);
+#pragma unroll
+      for (int i = 0; i < 6; i++) {
+        const int v = lane + 64 * i, wp = v >> 2, c = v & 3;
+        const uint4 d = *(const uint4 *)(stage + wp * 64 + 16 * (c ^ ((wp >> 2) & 3)));
+        const int q = 32 * (grp + 4 * (wp >> 5)) + (wp & 31);
+        const int gy = y0 + q / OTC, gx = x0 + q % OTC;
+        typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+        const u32x4 dv = {d.x, d.y, d.z, d.w};
+        __builtin_amdgcn_raw_buffer_store_b128(
+            dv, yr, gy < a.H && gx < a.W ? (gy * a.W + gx) * C * 2 + 64 * hf + 16 * c : OOB, 0, 0);
+      }
+    } else {
+      // The results become the centre of the next pair's halo (zeros
+      // outside the image: its padding).
+#pragma unroll
+      for (int j = 0; j < 3; j++) {
+        const int q = 32 * (grp + 4 * j) + (lane & 31);
+        const bool inside = y0 + q / OTC < a.H && x0 + q % OTC < a.W;
+        uint2 o[4];
+        finish(acc[j], s4, inside ? ~0u : 0u, o);
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+          const int ch = 32 * hf + 8 * g + 4 * (lane >> 5);
+          *(uint2 *)(lds + (2 + q / OTC) * HROW + (2 + q % OTC) * PB + ch * 2) = o[g];
+        }
+      }
+      __syncthreads();  // the centre is complete; the first layer's results are read
+      // Then out, 16 bytes a lane (8 lanes a pixel): the whole tile after
+      // the last pair, else, at device scope, the pixels of the outer 2 rows
+      // (0, 1, 14, 15) and columns (0, 1, 22, 23) that the neighbours read,
+      // with the next pair's first weights staged behind them (their
+      // completion, and so the epoch, is awaited at the next pair's start).
+      const bool last = k == pairs - 1;
+      const __amdgpu_buffer_rsrc_t yr = __builtin_amdgcn_make_buffer_rsrc(
+          last ? a.y : a.border[k & 1], 0, (int)map_bytes, 0x00020000);
+      const int chunks = (last ? OPIX : BORDER) * 8;
+      for (int v = tid; v < chunks; v += THREADS) {
+        const int c = v & 7, b = v >> 3;
+        int r, col;
+        if (last) {
+          r = b / OTC;
+          col = b % OTC;
+        } else if (b < 4 * OTC) {
+          r = b / OTC;
+          r = r < 2 ? r : r + OTR - 4;
+          col = b % OTC;
+        } else {
+          r = 2 + ((b - 4 * OTC) >> 2);
+          col = (b - 4 * OTC) & 3;
+          col = col < 2 ? col : col + OTC - 4;
+        }
+        const uint4 d = *(const uint4 *)(lds + (2 + r) * HROW + (2 + col) * PB + 16 * c);
+        const int gy = y0 + r, gx = x0 + col;
+        typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+        const u32x4 dv = {d.x, d.y, d.z, d.w};
+        const int at = gy < a.H && gx < a.W ? (gy * a.W + gx) * C * 2 + 16 * c : OOB;
+        if (last)
+          __builtin_amdgcn_raw_buffer_store_b128(dv, yr, at, 0, 0);
+        else
+          __builtin_amdgcn_raw_buffer_store_b128(dv, yr, at, 0, SC1);
+      }
+      if (!last) stage_weights(a.w[2 * k + 2], MID);
     }
   }
-  wait_vm<0>();
-  __syncthreads();
-#pragma unroll
-  for (int s = 0; s < STEPS; s++) w[s] = *(const half8 *)(lds + (hf * STEPS + s) * 1024 + lane * 16);
-  __syncthreads();  // every wave holds its weights: the staging below may overwrite them
+}
 
-  // ---- phase 2: the second layer on the 16 x 24 outputs, blocks grp,
-  // grp + 4, grp + 8 ----
-  int base[3];
-#pragma unroll
-  for (int j = 0; j < 3; j++) {
-    const int q = 32 * (grp + 4 * j) + (lane & 31);
-    base[j] = MID + (q / OTC) * MROW + (q % OTC) * PB + 16 * (lane >> 5);
-  }
-  floatx16 acc[3] = {seed(par + 2 * C), seed(par + 2 * C), seed(par + 2 * C)};
-  products(std::integral_constant<int, 3>{}, std::integral_constant<int, MROW>{}, base, acc);
+// The abort word and the tile epochs of a chain (not the failure word).
+__global__ void k_clear_chain(int *flags, int tiles) {
+  for (int i = threadIdx.x; i < tiles + 2; i += blockDim.x)
+    if (i != 1) flags[i] = 0;
+}
 
-  // Each wave's 96 pixels of its 32 channels go out through LDS (its own
-  // 6 KiB where the halo was), so that a lane stores 16 bytes and 4 lanes
-  // a pixel's 64 contiguous bytes.  Staged pixel wp = 32 j + l % 32 holds
-  // its 4 chunks of 8 channels at chunk c ^ (wp / 4 % 4), which keeps both
-  // the writes (16 pixels, one chunk) and the reads (4 pixels, 4 chunks)
-  // free of bank conflicts.
-  unsigned char *stage = lds + wave * (OBLK / 4) * 32 * 64;
-  float4v s4[4];
-  slopes(par + 3 * C, s4);
-#pragma unroll
-  for (int j = 0; j < 3; j++) {
-    uint2 o[4];
-    finish(acc[j], s4, ~0u, o);
-    const int wp = 32 * j + (lane & 31);
-#pragma unroll
-    for (int pr = 0; pr < 2; pr++) {
-      // Lanes < 32 hold channels 16 pr + 0..3 (o[2 pr]) and 16 pr + 8..11
-      // (o[2 pr + 1]), lanes >= 32 the runs 4 above; swapping the upper
-      // half's o[2 pr] with the lower half's o[2 pr + 1] gives lane l < 32
-      // channels 16 pr + 0..7 and lane l + 32 channels 16 pr + 8..15.
-      const auto sx = __builtin_amdgcn_permlane32_swap(o[2 * pr].x, o[2 * pr + 1].x, false, false);
-      const auto sy = __builtin_amdgcn_permlane32_swap(o[2 * pr].y, o[2 * pr + 1].y, false, false);
-      const uint4 v = {sx[0], sy[0], sx[1], sy[1]};
-      const int c = 2 * pr + (lane >> 5);
-      *(uint4 *)(stage + wp * 64 + 16 * (c ^ ((wp >> 2) & 3))) = v;
-    }
+bool layer_ok(const ien_matrix *m, const float *slope) {
+  return m && m->k == 9 * C && m->n == C && m->kb == STEPS && m->nb >= 2 && m->d_packed &&
+         m->d_bias && slope;
+}
+
+bool maps_ok(const uint16_t *x, const uint16_t *y, int H, int W) {
+  const long bytes = (long)H * W * C * 2;
+  const uintptr_t xa = (uintptr_t)x, ya = (uintptr_t)y;
+  return H > 0 && W > 0 && bytes <= 0x7fff0000L && ((xa | ya) & 15) == 0 &&
+         (xa + bytes <= ya || ya + bytes <= xa);
+}
+
+void fill_layers(PairArgs &a, const ien_matrix *const *w, const float *const *s, int layers) {
+  for (int i = 0; i < layers; i++) {
+    a.w[i] = w[i]->d_packed;
+    a.b[i] = w[i]->d_bias;
+    a.s[i] = s[i];
   }
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  const __amdgpu_buffer_rsrc_t yr =
-      __builtin_amdgcn_make_buffer_rsrc(a.y, 0, (int)((long)a.H * a.W * C * 2), 0x00020000);
-#pragma unroll
-  for (int i = 0; i < 6; i++) {
-    const int v = lane + 64 * i, wp = v >> 2, c = v & 3;
-    const uint4 d = *(const uint4 *)(stage + wp * 64 + 16 * (c ^ ((wp >> 2) & 3)));
-    const int q = 32 * (grp + 4 * (wp >> 5)) + (wp & 31);
-    const int gy = y0 + q / OTC, gx = x0 + q % OTC;
-    typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
-    const u32x4 dv = {d.x, d.y, d.z, d.w};
-    __builtin_amdgcn_raw_buffer_store_b128(
-        dv, yr, gy < a.H && gx < a.W ? (gy * a.W + gx) * C * 2 + 64 * hf + 16 * c : OOB, 0, 0);
-  }
+  a.KB = w[0]->kb;
 }
 
 }  // namespace
 
 bool pair_supported(const PairCall &p) {
-  auto layer = [](const ien_matrix *m, const float *slope) {
-    return m && m->k == 9 * C && m->n == C && m->kb == STEPS && m->nb >= 2 && slope;
-  };
-  const long bytes = (long)p.H * p.W * C * 2;
-  const uintptr_t x = (uintptr_t)p.x, y = (uintptr_t)p.y;
-  return layer(p.w1, p.s1) && layer(p.w2, p.s2) && p.H > 0 && p.W > 0 && bytes <= 0x7fff0000L &&
-         ((x | y) & 15) == 0 && (x + bytes <= y || y + bytes <= x);
+  return layer_ok(p.w1, p.s1) && layer_ok(p.w2, p.s2) && maps_ok(p.x, p.y, p.H, p.W);
 }
 
 ien_status launch_pair(ien_ctx *ctx, const PairCall &p) {
   IEN_CHECK(pair_supported(p), IEN_ERR_INPUT, "not a pair of 3x3 64-channel PReLU layers");
-  PairArgs a;
+  PairArgs a = {};
   a.x = p.x;
   a.y = p.y;
   a.H = p.H;
   a.W = p.W;
   a.tiles_x = (p.W + OTC - 1) / OTC;
-  a.w1 = p.w1->d_packed;
-  a.w2 = p.w2->d_packed;
-  a.KB = p.w1->kb;
-  a.b1 = p.w1->d_bias;
-  a.s1 = p.s1;
-  a.b2 = p.w2->d_bias;
-  a.s2 = p.s2;
-  const long tiles = (long)a.tiles_x * ((p.H + OTR - 1) / OTR);
+  a.tiles_y = (p.H + OTR - 1) / OTR;
+  a.pairs = 1;
+  const ien_matrix *w[2] = {p.w1, p.w2};
+  const float *s[2] = {p.s1, p.s2};
+  fill_layers(a, w, s, 2);
+  const long tiles = (long)a.tiles_x * a.tiles_y;
   IEN_CHECK(tiles > 0 && tiles < (1L << 31), IEN_ERR_INPUT, "grid of %ld", tiles);
-  hipLaunchKernelGGL(conv_pair, dim3((unsigned)tiles), dim3(THREADS), 0, ctx->stream, a);
+  hipLaunchKernelGGL(conv_pair<false>, dim3((unsigned)tiles), dim3(THREADS), 0, ctx->stream, a);
   IEN_HIP(hipGetLastError());
   return IEN_OK;
+}
+
+bool chain_supported(ien_ctx *ctx, const ChainCall &c) {
+  if (!ctx->chain_flags || c.pairs < 1 || c.pairs > MAXPAIRS || !maps_ok(c.a, c.b, c.H, c.W))
+    return false;
+  for (int i = 0; i < 2 * c.pairs; i++)
+    if (!layer_ok(c.w[i], c.s[i])) return false;
+  // Every tile's workgroup resident at once: one per CU at most.
+  if (ctx->chain_per_cu < 0) {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, conv_pair<true>, THREADS, 0) != hipSuccess)
+      n = 0;
+    ctx->chain_per_cu = n;
+  }
+  const long tiles = (long)((c.W + OTC - 1) / OTC) * ((c.H + OTR - 1) / OTR);
+  return ctx->chain_per_cu >= 1 && tiles <= (long)ctx->cus && tiles <= ctx->chain_tiles;
+}
+
+ien_status launch_chain(ien_ctx *ctx, const ChainCall &c, uint16_t **out) {
+  IEN_CHECK(chain_supported(ctx, c), IEN_ERR_INPUT, "not a chain this device runs at once");
+  PairArgs a = {};
+  a.x = c.a;
+  a.border[0] = c.b;
+  a.border[1] = c.a;
+  a.y = a.border[(c.pairs - 1) & 1];
+  a.H = c.H;
+  a.W = c.W;
+  a.tiles_x = (c.W + OTC - 1) / OTC;
+  a.tiles_y = (c.H + OTR - 1) / OTR;
+  a.pairs = c.pairs;
+  fill_layers(a, c.w, c.s, 2 * c.pairs);
+  a.flags = ctx->chain_flags;
+  a.spin_limit = ctx->chain_spin;
+  const int tiles = a.tiles_x * a.tiles_y;
+  hipLaunchKernelGGL(k_clear_chain, dim3(1), dim3(256), 0, ctx->stream, a.flags, tiles);
+  hipLaunchKernelGGL(conv_pair<true>, dim3((unsigned)tiles), dim3(THREADS), 0, ctx->stream, a);
+  IEN_HIP(hipGetLastError());
+  *out = a.y;
+  return IEN_OK;
+}
+
+ien_status chain_status(ien_ctx *ctx) {
+  int word = 0;
+  IEN_HIP(hipMemcpyAsync(&word, ctx->chain_flags + 1, 4, hipMemcpyDeviceToHost, ctx->stream));
+  IEN_HIP(hipStreamSynchronize(ctx->stream));
+  if (word == 0) return IEN_OK;
+  const int zero = 0;
+  IEN_HIP(hipMemcpy(ctx->chain_flags + 1, &zero, 4, hipMemcpyHostToDevice));
+  return fail(IEN_ERR_GPU, "body chain: a tile's wait for its neighbours timed out");
 }
 
 }  // namespace ien
@@ -357,3 +625,41 @@ extern "C" ien_status ien_conv3_pair(ien_ctx *ctx, const uint16_t *d_x, uint16_t
   p.s2 = d_slope2;
   return launch_pair(ctx, p);
 }
+
+extern "C" ien_status ien_conv3_chain(ien_ctx *ctx, uint16_t *d_a, uint16_t *d_b, size_t height,
+                                      size_t width, size_t pairs, const ien_matrix *const *w,
+                                      const float *const *d_slopes, uint16_t **d_out) {
+  IEN_CHECK(ctx && d_a && d_b && w && d_slopes && d_out, IEN_ERR_INPUT, "null argument");
+  IEN_CHECK(pairs >= 1 && pairs <= MAXPAIRS, IEN_ERR_INPUT, "%zu pairs (1 to %d)", pairs, MAXPAIRS);
+  IEN_CHECK(height > 0 && width > 0 && height < (1u << 20) && width < (1u << 20), IEN_ERR_INPUT,
+            "map of %zu x %zu", height, width);
+  ChainCall c;
+  c.a = d_a;
+  c.b = d_b;
+  c.H = (int)height;
+  c.W = (int)width;
+  c.pairs = (int)pairs;
+  for (size_t i = 0; i < 2 * pairs; i++) {
+    IEN_CHECK(w[i] && d_slopes[i], IEN_ERR_INPUT, "layer %zu: null argument", i);
+    IEN_CHECK(w[i]->k == 9 * C && w[i]->n == C, IEN_ERR_INPUT,
+              "layer %zu: chain layers are 3x3 64->64 (k 576, n 64), not k %zu, n %zu", i, w[i]->k,
+              w[i]->n);
+    c.w[i] = w[i];
+    c.s[i] = d_slopes[i];
+  }
+  const size_t bytes = height * width * C * 2;
+  IEN_CHECK(bytes <= 0x7fff0000UL, IEN_ERR_INPUT, "map of %zu bytes over 2 GiB", bytes);
+  IEN_CHECK((((uintptr_t)d_a | (uintptr_t)d_b) & 15) == 0, IEN_ERR_INPUT,
+            "maps must be 16-byte aligned");
+  const uintptr_t a = (uintptr_t)d_a, b = (uintptr_t)d_b;
+  IEN_CHECK(a + bytes <= b || b + bytes <= a, IEN_ERR_INPUT, "the two maps overlap");
+  IEN_CHECK(chain_supported(ctx, c), IEN_ERR_INPUT,
+            "a %zu x %zu map has more 16 x 24 tiles than this device holds at once", height, width);
+  return launch_chain(ctx, c, d_out);
+}
+
+extern "C" ien_status ien_conv3_chain_status(ien_ctx *ctx) {
+  IEN_CHECK(ctx, IEN_ERR_INPUT, "null argument");
+  return chain_status(ctx);
+}
+

@@ -58,6 +58,14 @@ struct ien_ctx {
   // chunks): set by a driver around work that runs beside LDS-hungry
   // kernels of another branch.
   bool compact = false;
+  // Chains of body pairs (conv_pair.hip): an abort word, a failure word
+  // and chain_tiles epoch words; the workgroups of the chain kernel one CU
+  // holds (-1 until asked); the wall-clock ticks (100 MHz) a tile may wait
+  // for a neighbour.
+  int *chain_flags = nullptr;
+  int chain_tiles = 0;
+  int chain_per_cu = -1;
+  long chain_spin = 100000000;
 };
 
 // Packed weights (gemm.rs Matrix): k x n padded to whole 16 x 32 MFMA
@@ -168,6 +176,23 @@ struct PairCall {
 };
 bool pair_supported(const PairCall &p);
 ien_status launch_pair(ien_ctx *ctx, const PairCall &p);
+
+// A chain of `pairs` such pairs in one launch (layers w[0], w[1], ...,
+// slopes s[i]): the input in `a`; `b` and `a` hold the borders the tiles
+// exchange, and the output ends in the map launch_chain returns (`a` for an
+// even count).  Supported when every tile's workgroup can be resident at
+// once.  chain_status waits for the stream and reports whether every chain
+// since the last report finished (a wait for a neighbour that timed out
+// aborts its chain), clearing the report.
+struct ChainCall {
+  uint16_t *a = nullptr, *b = nullptr;
+  int H = 0, W = 0, pairs = 0;
+  const ien_matrix *w[32] = {};
+  const float *s[32] = {};
+};
+bool chain_supported(ien_ctx *ctx, const ChainCall &c);
+ien_status launch_chain(ien_ctx *ctx, const ChainCall &c, uint16_t **out);
+ien_status chain_status(ien_ctx *ctx);
 
 // io.hip: the 8-bit image passes of the models' u8 entry points, on the
 // context's stream (to_float, to_byte, LaMa's mask and compositing,

@@ -191,6 +191,8 @@ struct ien_model {
   // 8-bit images of the u8 entry point on the device (ien_model_run_u8).
   uint8_t *d_bytes = nullptr;
   size_t bytes_cap = 0;
+  // A run launched a chain of body pairs (checked when the run ends).
+  bool chained = false;
 };
 
 namespace ien {
@@ -277,7 +279,9 @@ static ien_status load_esrgan(ien_model *model, const TensorSource &take) {
 }
 
 // The launches of one run: input to f16, 34 convolutions, shuffle.  With
-// `steps`, progress is reported after each layer.
+// `steps`, progress is reported after each layer; without, the 32 body
+// layers run as one chain of pairs where the device holds every tile at
+// once.
 static ien_status enqueue_esrgan(ien_model *model, const float *d_image, size_t width,
                                  size_t height, float *d_out, Steps *steps) {
   ien_ctx *ctx = model->ctx;
@@ -290,8 +294,28 @@ static ien_status enqueue_esrgan(ien_model *model, const float *d_image, size_t 
   // body layers in one launch where the pair kernel takes them, from one
   // map to the other (so that a pair of layers 2k - 1, 2k also ends in `a`).
   uint16_t *ma = m.a, *mb = m.b;
+  ChainCall chain;
+  chain.a = m.a;
+  chain.b = m.b;
+  chain.H = (int)height;
+  chain.W = (int)width;
+  chain.pairs = (STEPS - 2) / 2;
+  for (int i = 0; i < 2 * chain.pairs; i++) {
+    chain.w[i] = model->layers[1 + i].conv;
+    chain.s[i] = model->layers[1 + i].d_slope;
+  }
+  const bool use_chain = !steps && chain_supported(ctx, chain);
   for (int i = 0; i < STEPS; i++) {
     const EsrganLayer &l = model->layers[i];
+    if (i == 1 && use_chain) {
+      // Layers 1 .. 32 from `a`, ending in `a` (an even count of pairs).
+      uint16_t *out = nullptr;
+      if ((st = launch_chain(ctx, chain, &out)) != IEN_OK) return st;
+      IEN_CHECK(out == m.a, IEN_ERR_GPU, "body chain ended outside map a");
+      model->chained = true;
+      i = STEPS - 2;
+      continue;
+    }
     const uint16_t *src = i == 0 ? m.image : (i % 2 == 1 ? ma : mb);
     uint16_t *dst = i % 2 == 0 ? ma : mb;
     if (i % 2 == 1 && i + 1 < STEPS - 1) {
@@ -504,8 +528,11 @@ static ien_status stage_bytes(ien_model *model, size_t in, size_t mask, size_t o
 static ien_status finish_run(ien_model *model, ien_status st, Steps *steps) {
   if (st == IEN_OK && steps) st = steps->drain();
   const hipError_t e = hipStreamSynchronize(model->ctx->stream);
+  const bool chained = model->chained;
+  model->chained = false;
   if (st != IEN_OK) return st;
   if (e != hipSuccess) return fail(IEN_ERR_GPU, "run: %s", hipGetErrorString(e));
+  if (chained) return chain_status(model->ctx);
   return IEN_OK;
 }
 

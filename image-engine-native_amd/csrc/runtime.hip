@@ -4,6 +4,7 @@
 // upload, ordered submissions) on HIP: one stream per context, device
 // buffers from hipMalloc, weights packed once into MFMA fragment order.
 
+#include <cstdlib>
 #include <cstring>
 #include <mutex>
 
@@ -161,6 +162,10 @@ ien_status ien_open(int device, ien_ctx **out) {
   if (e == hipSuccess) e = hipMalloc((void **)&ctx->splitk, ctx->splitk_floats * 4);
   if (e == hipSuccess) e = hipEventCreateWithFlags(&ctx->fork_ev, hipEventDisableTiming);
   if (e == hipSuccess) e = swin_static_setup(device);
+  ctx->chain_tiles = ctx->cus;
+  if (e == hipSuccess) e = hipMalloc((void **)&ctx->chain_flags, (ctx->chain_tiles + 2) * 4);
+  if (e == hipSuccess) e = hipMemset(ctx->chain_flags, 0, (ctx->chain_tiles + 2) * 4);
+  if (const char *v = std::getenv("IEN_CHAIN_SPIN_TICKS")) ctx->chain_spin = std::atol(v);
   for (int i = 0; i < ien_ctx::BRANCHES && e == hipSuccess; i++) {
     e = hipStreamCreateWithFlags(&ctx->branch[i], hipStreamNonBlocking);
     if (e == hipSuccess) e = hipEventCreateWithFlags(&ctx->join_ev[i], hipEventDisableTiming);
@@ -192,6 +197,7 @@ void ien_close(ien_ctx *ctx) {
   if (ctx->own) (void)hipStreamDestroy(ctx->own);
   (void)hipFree(ctx->zeros);
   (void)hipFree(ctx->splitk);
+  (void)hipFree(ctx->chain_flags);
   delete ctx;
 }
 

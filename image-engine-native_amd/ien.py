@@ -28,7 +28,8 @@ EXPORTS = (
     "ien_last_error", "ien_open", "ien_close", "ien_device_name", "ien_stream", "ien_set_stream",
     "ien_alloc", "ien_free", "ien_upload", "ien_download", "ien_sync",
     "ien_floats_to_halves", "ien_halves_to_floats",
-    "ien_matrix_new", "ien_matrix_free", "ien_multiply", "ien_multiply_ex", "ien_conv3", "ien_conv3_pair",
+    "ien_matrix_new", "ien_matrix_free", "ien_multiply", "ien_multiply_ex", "ien_conv3",
+    "ien_conv3_pair", "ien_conv3_chain", "ien_conv3_chain_status",
     "ien_layer_norm", "ien_gelu", "ien_sigmoid", "ien_pixel_shuffle_add", "ien_depthwise",
     "ien_model_load", "ien_model_from_tensors", "ien_model_free", "ien_model_run",
     "ien_model_run_device", "ien_model_set_graph", "ien_model_run_tiled", "ien_model_run_u8",
@@ -141,6 +142,9 @@ def load():
         L.ien_multiply_ex.argtypes = [vp, ctypes.POINTER(Input), sz, sz, vp, ctypes.POINTER(Output), i, vp, i]
         L.ien_conv3.argtypes = [vp, ctypes.POINTER(Input), vp, vp, sz, i, i, vp]
         L.ien_conv3_pair.argtypes = [vp, vp, vp, sz, sz, vp, vp, vp, vp]
+        L.ien_conv3_chain.argtypes = [vp, vp, vp, sz, sz, sz, ctypes.POINTER(vp), ctypes.POINTER(vp),
+                                      ctypes.POINTER(vp)]
+        L.ien_conv3_chain_status.argtypes = [vp]
         L.ien_layer_norm.argtypes = [vp, vp, sz, sz, sz, vp, vp]
         L.ien_gelu.argtypes = [vp, vp, sz]
         L.ien_sigmoid.argtypes = [vp, vp, sz]
@@ -318,6 +322,22 @@ def conv3_pair(ctx, x, y, height, width, m1, slope1, m2, slope2):
     """Two 3x3 64->64 PReLU layers in one launch, x -> y (H x W x 64 f16)."""
     check(load().ien_conv3_pair(ctx.h, _ptr(x), _ptr(y), height, width, m1.h, _ptr(slope1), m2.h,
                                 _ptr(slope2)))
+
+
+def conv3_chain(ctx, a, b, height, width, matrices, slopes):
+    """len(matrices) / 2 pairs of 3x3 64->64 PReLU layers in one launch; the
+    input in a, b a second map; returns the tensor (a or b) holding the
+    output."""
+    n = len(matrices)
+    w = (ctypes.c_void_p * n)(*[m.h for m in matrices])
+    s = (ctypes.c_void_p * n)(*[_ptr(x) for x in slopes])
+    out = ctypes.c_void_p()
+    check(load().ien_conv3_chain(ctx.h, _ptr(a), _ptr(b), height, width, n // 2, w, s, ctypes.byref(out)))
+    return a if out.value == a.data_ptr() else b
+
+
+def conv3_chain_status(ctx):
+    check(load().ien_conv3_chain_status(ctx.h))
 
 
 def floats_to_halves(ctx, src, dst):

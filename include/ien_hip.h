@@ -166,6 +166,22 @@ ien_status ien_conv3_pair(ien_ctx *ctx, const uint16_t *d_x, uint16_t *d_y, size
                           size_t width, const ien_matrix *w1, const float *d_slope1,
                           const ien_matrix *w2, const float *d_slope2);
 
+/* realesrgan-native network.rs:96-109, 2 pairs consecutive body steps in
+ * one launch (pairs <= 16; layer i: w[i], slopes d_slopes[i], each 3x3
+ * 64->64 with bias and PReLU), bit for bit what `pairs` ien_conv3_pair
+ * launches give.  The input is in d_a; d_b and d_a also carry the 2-pixel
+ * borders that the 16 x 24 tiles exchange, and *d_out is set to the map
+ * that holds the output (d_a for an even count).  Every tile's workgroup
+ * must be resident at once (at most one per CU: 256 tiles on MI355X);
+ * larger maps are refused.  The tiles wait for their neighbours with a
+ * bounded wait; ien_conv3_chain_status (after the stream's work) reports
+ * whether any chain since the last report gave up waiting, and clears
+ * that report. */
+ien_status ien_conv3_chain(ien_ctx *ctx, uint16_t *d_a, uint16_t *d_b, size_t height,
+                           size_t width, size_t pairs, const ien_matrix *const *w,
+                           const float *const *d_slopes, uint16_t **d_out);
+ien_status ien_conv3_chain_status(ien_ctx *ctx);
+
 /* ---- elementwise: crates/native-engine/src/math.rs --------------------- */
 /* math.rs:154-170 layer_norm over rows of c values (f16 in place, f32
  * statistics, epsilon 1e-5); gamma/beta device f32. */

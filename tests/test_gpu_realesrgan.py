@@ -131,6 +131,48 @@ def test_body_pairs_equal_single_layers(ctx, tensors, h, w):
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), float(np.abs(got - want).max())
 
 
+@pytest.mark.parametrize("h,w", [(256, 384), (50, 70), (16, 24), (37, 100), (1, 1), (300, 500)])
+def test_body_chain_equals_pairs(ctx, tensors, h, w):
+    """Without a progress callback the 32 body layers run as one chain of
+    pairs (tiles exchanging 2-pixel borders) where every tile fits on the
+    device at once (300 x 500 has more tiles than CUs and runs pair by
+    pair); with one they run a pair per launch.  Same bits either way."""
+    import ien
+
+    image = synthetic.esrgan_image(h, w, seed=h * 7 + w)
+    model = ien.Model(ctx, ien.MODEL_REALESRGAN, tensors=tensors)
+    chained = model.run(image)
+    paired = model.run(image, progress=lambda done, user: 0)
+    model.free()
+    assert np.array_equal(chained.view(np.uint32), paired.view(np.uint32)), float(np.abs(chained - paired).max())
+
+
+def test_body_chain_wait_limit(tensors, monkeypatch):
+    """A chain whose tiles may not wait at all for their neighbours (the
+    wall-clock limit forced to 0 from the host): the tiles that find a
+    neighbour behind abort, every workgroup ends, and the run reports the
+    failure; a context with the normal limit is unaffected."""
+    import ien
+
+    image = synthetic.esrgan_image(256, 384, seed=9)
+    monkeypatch.setenv("IEN_CHAIN_SPIN_TICKS", "0")
+    hurried = ien.Context(0)
+    monkeypatch.delenv("IEN_CHAIN_SPIN_TICKS")
+    model = ien.Model(hurried, ien.MODEL_REALESRGAN, tensors=tensors)
+    with pytest.raises(ien.IenError) as e:
+        model.run(image)
+    assert e.value.status == ien.ERR_GPU and "timed out" in str(e.value), str(e.value)
+    model.free()
+    hurried.close()
+    calm = ien.Context(0)
+    model = ien.Model(calm, ien.MODEL_REALESRGAN, tensors=tensors)
+    got = model.run(image)
+    want = model.run(image, progress=lambda done, user: 0)
+    model.free()
+    calm.close()
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
 def pair_inputs(ctx, tensors, h, w, seed):
     import torch
     import ien
@@ -167,6 +209,54 @@ def test_conv3_pair_op(ctx, oracle, tensors, h, w):
     assert_spread(got.astype(np.float32), want, rms_frac=2e-3, max_frac=1e-2, what=f"pair {h}x{w}")
     m1.free()
     m2.free()
+
+
+@pytest.mark.parametrize("h,w,pairs", [(256, 384, 16), (40, 100, 3), (17, 25, 1)])
+def test_conv3_chain_op(ctx, tensors, h, w, pairs):
+    """ien_conv3_chain: `pairs` pairs of body layers in one launch, bit for
+    bit the same number of ien_conv3_pair launches; the output map is the
+    first for an even count, the second for an odd one."""
+    import torch
+    import ien
+
+    layers = synthetic.esrgan_layers(tensors)[1:1 + 2 * pairs]
+    mats = [ien.Matrix(ctx, wt, b) for wt, b, _ in layers]
+    slopes = [torch.from_numpy(sl).cuda() for _, _, sl in layers]
+    x = torch.from_numpy(np.random.default_rng(h + pairs).standard_normal((h, w, 64)).astype(np.float16)).cuda()
+    a, b = x.clone(), torch.empty_like(x)
+    out = ien.conv3_chain(ctx, a, b, h, w, mats, slopes)
+    torch.cuda.synchronize()
+    ien.conv3_chain_status(ctx)
+    assert out is (a if pairs % 2 == 0 else b)
+    ref, tmp = x.clone(), torch.empty_like(x)
+    for k in range(pairs):
+        ien.conv3_pair(ctx, ref, tmp, h, w, mats[2 * k], slopes[2 * k], mats[2 * k + 1], slopes[2 * k + 1])
+        ref, tmp = tmp, ref
+    torch.cuda.synchronize()
+    assert np.array_equal(out.cpu().numpy().view(np.uint16), ref.cpu().numpy().view(np.uint16))
+    for m in mats:
+        m.free()
+
+
+def test_conv3_chain_refusals(ctx, tensors):
+    """Counts outside 1..16 and maps with more tiles than the device holds
+    at once are refused before anything is launched."""
+    import torch
+    import ien
+
+    layers = synthetic.esrgan_layers(tensors)[1:3]
+    mats = [ien.Matrix(ctx, wt, b) for wt, b, _ in layers]
+    slopes = [torch.from_numpy(sl).cuda() for _, _, sl in layers]
+    big = torch.zeros((1024, 1024, 64), dtype=torch.float16, device="cuda")
+    other = torch.zeros_like(big)
+    with pytest.raises(ien.IenError) as e:
+        ien.conv3_chain(ctx, big, other, 1024, 1024, mats, slopes)
+    assert e.value.status == ien.ERR_INPUT and "tiles" in str(e.value), str(e.value)
+    with pytest.raises(ien.IenError) as e:
+        ien.conv3_chain(ctx, big, other, 64, 64, [], [])
+    assert e.value.status == ien.ERR_INPUT and "pairs" in str(e.value), str(e.value)
+    for m in mats:
+        m.free()
 
 
 def test_conv3_pair_refusals(ctx, tensors):
