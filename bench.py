@@ -257,21 +257,25 @@ def body_chain(ctx, tensors, H, W):
 
 
 def traffic_probe(ctx, tensors, H, W):
-    """Counter-pass workload: the body pair x10, then a copy of 128 MiB
-    (a kernel of known traffic, for scaling FETCH_SIZE and WRITE_SIZE)."""
+    """Counter-pass workload: the body chain x10, then a copy of 1 GiB (a
+    kernel of known traffic, for scaling FETCH_SIZE and WRITE_SIZE) whose
+    source was written before 512 MiB of other writes, so that it is read
+    from HBM rather than from the 256 MiB memory-side cache."""
     import torch
 
     launch, free = body_chain(ctx, tensors, H, W)
     for _ in range(10):
         launch()
     torch.cuda.synchronize()
-    a = torch.empty(64 << 20, dtype=torch.float16, device="cuda").fill_(1)
+    a = torch.empty(512 << 20, dtype=torch.float16, device="cuda").fill_(1)
+    flush = torch.empty(256 << 20, dtype=torch.float16, device="cuda").fill_(2)
     c = torch.empty_like(a)
     torch.cuda.synchronize()
     c.copy_(a)
     torch.cuda.synchronize()
     free()
-    print("traffic probe: body chain x10, then a 134217728-byte copy", flush=True)
+    del flush
+    print("traffic probe: body chain x10, then a 1073741824-byte copy", flush=True)
 
 
 def host_path_ms(run, reps=3):
