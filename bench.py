@@ -29,6 +29,10 @@ other configuration carries its own cpu_baseline from the same protocol
 
 host_path_ms: ien_model_run with host buffers (upload, launches, download
 of the f32 output, synchronisation) beside the device-resident `value`.
+
+measured_peaks: this device's sustained rates beside the published peaks
+the roofline uses (2516.6 TFLOP/s f16 dense, 8 TB/s HBM): a register-only
+MFMA loop on every SIMD and a 1 GiB device copy read from HBM.
 """
 
 import argparse
@@ -278,6 +282,38 @@ def traffic_probe(ctx, tensors, H, W):
     print("traffic probe: body chain x10, then a 1073741824-byte copy", flush=True)
 
 
+def measured_peaks(ctx, stream):
+    """This device's sustained rates beside the published peaks: a
+    register-only f16 MFMA loop on every SIMD (ien_measure_mfma) and a 1 GiB
+    device-to-device copy read from HBM (its source written before 512 MiB
+    of other writes, so not served by the 256 MiB memory-side cache), timed
+    with HIP events; the copy's rate counts bytes read plus written."""
+    import torch
+
+    import ien
+
+    tf, mfma_ms = ien.measure_mfma(ctx, 100000)
+    a = torch.empty(512 << 20, dtype=torch.float16, device="cuda").fill_(1)
+    c = torch.empty_like(a)
+    rates = []
+    for _ in range(3):
+        flush = torch.empty(256 << 20, dtype=torch.float16, device="cuda").fill_(2)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        c.copy_(a)
+        e1.record()
+        e1.synchronize()
+        rates.append(2 * a.numel() * 2 / (e0.elapsed_time(e1) * 1e-3) / 1e12)
+        del flush
+    copy = sorted(rates)[1]
+    del a, c
+    return {"mfma_f16_tflops": round(tf, 1), "mfma_frac_of_published": round(tf / MFMA_F16_PEAK_TFLOPS, 3),
+            "mfma_loop_ms": round(mfma_ms, 3), "copy_tbps": round(copy, 3),
+            "copy_frac_of_published": round(copy / (HBM_PEAK_GBS / 1000), 3),
+            "copy_bytes": 2 << 30}
+
+
 def host_path_ms(run, reps=3):
     """Median milliseconds of ien_model_run (host buffers: upload, the
     launches, download and synchronisation), after a warm-up."""
@@ -479,8 +515,10 @@ def main():
     ap.add_argument("--sweep-only", action="store_true",
                     help="only the conv sweep (the workload of its kernel profile)")
     ap.add_argument("--traffic-probe", action="store_true",
-                    help="only run the dominant layer 10 times and a 128 MiB device copy "
+                    help="only run the body chain 10 times and a 1 GiB device copy "
                          "(the workload of the FETCH_SIZE / WRITE_SIZE counter passes)")
+    ap.add_argument("--peaks", action="store_true",
+                    help="only the measured peaks (MFMA loop, device copy)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py runs on one GPU only: this backend has no multi-GPU path "
@@ -500,6 +538,9 @@ def main():
     stream = ctx.stream
     H, W = 256, 384
     tensors = synthetic.esrgan_tensors()
+    if args.peaks:
+        print(json.dumps({"measured_peaks": measured_peaks(ctx, stream)}), flush=True)
+        return
     if args.traffic_probe:
         traffic_probe(ctx, tensors, H, W)
         return
@@ -560,6 +601,7 @@ def main():
             log(f"{name} timed")
     cpu = cpu_baseline(tensors, image, cpu_runs) if cpu_runs else None
     sweep_cpu = cpu_sweep(cpu_runs) if cpu_runs and not args.no_sweep else None
+    peaks = measured_peaks(ctx, stream)
 
     line = {
         "metric": METRIC,
@@ -584,6 +626,7 @@ def main():
         "gemm_sweep": gemm_sweep,
         "gemm_sweep_cpu": sweep_cpu,
         "models": models,
+        "measured_peaks": peaks,
         "device": ctx.name,
     }
     model.free()

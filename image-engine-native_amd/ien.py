@@ -29,7 +29,7 @@ EXPORTS = (
     "ien_alloc", "ien_free", "ien_upload", "ien_download", "ien_sync",
     "ien_floats_to_halves", "ien_halves_to_floats",
     "ien_matrix_new", "ien_matrix_free", "ien_multiply", "ien_multiply_ex", "ien_conv3",
-    "ien_conv3_pair", "ien_conv3_chain", "ien_conv3_chain_status",
+    "ien_conv3_pair", "ien_conv3_chain", "ien_conv3_chain_status", "ien_measure_mfma",
     "ien_layer_norm", "ien_gelu", "ien_sigmoid", "ien_pixel_shuffle_add", "ien_depthwise",
     "ien_model_load", "ien_model_from_tensors", "ien_model_free", "ien_model_run",
     "ien_model_run_device", "ien_model_set_graph", "ien_model_run_tiled", "ien_model_run_u8",
@@ -145,6 +145,7 @@ def load():
         L.ien_conv3_chain.argtypes = [vp, vp, vp, sz, sz, sz, ctypes.POINTER(vp), ctypes.POINTER(vp),
                                       ctypes.POINTER(vp)]
         L.ien_conv3_chain_status.argtypes = [vp]
+        L.ien_measure_mfma.argtypes = [vp, i, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)]
         L.ien_layer_norm.argtypes = [vp, vp, sz, sz, sz, vp, vp]
         L.ien_gelu.argtypes = [vp, vp, sz]
         L.ien_sigmoid.argtypes = [vp, vp, sz]
@@ -338,6 +339,13 @@ def conv3_chain(ctx, a, b, height, width, matrices, slopes):
 
 def conv3_chain_status(ctx):
     check(load().ien_conv3_chain_status(ctx.h))
+
+
+def measure_mfma(ctx, iters):
+    """(sustained f16 MFMA TFLOP/s, ms) of a register-only MFMA loop on every SIMD."""
+    tf, ms = ctypes.c_double(), ctypes.c_double()
+    check(load().ien_measure_mfma(ctx.h, iters, ctypes.byref(tf), ctypes.byref(ms)))
+    return tf.value, ms.value
 
 
 def floats_to_halves(ctx, src, dst):

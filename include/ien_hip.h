@@ -481,6 +481,13 @@ ien_status ien_model_run_device(ien_model *model, const float *d_image, const fl
  * graph once, then replay it (0 = eager launches). */
 ien_status ien_model_set_graph(ien_model *model, int enabled);
 
+/* No counterpart in the reference: a measurement of this device for
+ * reports.  Back-to-back v_mfma_f32_32x32x16_f16 on register operands on
+ * every SIMD (one workgroup of 8 waves per CU, 4 accumulator chains a
+ * wave, `iters` rounds), timed with HIP events on the context's stream:
+ * the sustained f16 dense rate in *tflops, the launch in *ms. */
+ien_status ien_measure_mfma(ien_ctx *ctx, int iters, double *tflops, double *ms);
+
 #ifdef __cplusplus
 }
 #endif
