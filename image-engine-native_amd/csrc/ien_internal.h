@@ -174,6 +174,21 @@ struct PairCall {
   const ien_matrix *w1 = nullptr, *w2 = nullptr;
   const float *s1 = nullptr, *s2 = nullptr;  // PReLU slopes
 };
+// rows.hip: out = x W + bias (+ old out) over `rows` rows whose first k1
+// channels come from x (rows xs halves apart) and the rest from x2, the
+// first n1 output columns going to y and the rest to y2: the two halves of
+// a map kept as separate planes.
+struct RowsPlanes {
+  const uint16_t *x = nullptr, *x2 = nullptr;
+  int xs = 0, xs2 = 0, k1 = 0;
+  long rows = 0;
+  const ien_matrix *w = nullptr;
+  uint16_t *y = nullptr, *y2 = nullptr;
+  int ys = 0, ys2 = 0, n1 = 0;
+  int accumulate = 0;
+};
+ien_status launch_rows_planes(ien_ctx *ctx, const RowsPlanes &p);
+
 bool pair_supported(const PairCall &p);
 ien_status launch_pair(ien_ctx *ctx, const PairCall &p);
 

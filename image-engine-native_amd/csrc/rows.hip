@@ -27,6 +27,9 @@
 // workgroups share a CU and hide each other's latency.
 // Tiles are dealt XCD-aware with N fastest, so a tile row's x stays in its
 // XCD's L2 for every column tile.
+// Planes: the rows may come from two maps (channels k1 .. K from x2, rows
+// xs2 apart) and go to two (columns n1 .. N to y2, rows ys2 apart), so that
+// the two halves of a map that two streams work on share no cache line.
 
 #include "conv_common.h"
 
@@ -42,6 +45,10 @@ struct RowsArgs {
   const float *bias, *slope;
   uint16_t *y;        // output row 0
   int ys;
+  const uint16_t *x2;  // channels k1 .. K (k1 = K: x only), rows xs2 apart
+  int xs2, k1;
+  uint16_t *y2;        // columns n1 .. N (n1 = N: y only), rows ys2 apart
+  int ys2, n1;
   int act, accumulate;
   int tiles_n, tiles;
   // Split-K (gridDim.y splits of kchunks chunks): raw f32 sums of split z
@@ -87,6 +94,7 @@ __global__ __launch_bounds__(256) void k_rows(RowsArgs a) {
   const int m0 = tm * R::BM;
   const unsigned l0 = lds_addr(lds);
   const int4v xr = buffer_rsrc(a.x, (long)a.M * a.xs * 2);
+  const int4v xr2 = buffer_rsrc(a.x2, (long)a.M * a.xs2 * 2);
   const int4v wr = buffer_rsrc(a.wp, (long)a.NB * a.KB * 1024);
   const int c_begin = blockIdx.y * a.kchunks;
   const int chunks = min(a.K / KC - c_begin, a.kchunks);  // this split's chunks
@@ -96,14 +104,17 @@ __global__ __launch_bounds__(256) void k_rows(RowsArgs a) {
   auto issue = [&](int lc, int s) {
     const int c = c_begin + lc;
     const unsigned base = l0 + s * R::STAGE;
+    const bool second = c * KC >= a.k1;  // (uniform: k1 is a multiple of KC)
+    const int4v sr = second ? xr2 : xr;
+    const int rs = second ? a.xs2 : a.xs, c0 = second ? c * KC - a.k1 : c * KC;
 #pragma unroll
     for (int i = 0; i < R::A_LOADS; i++) {
       const int d = wave + 4 * i;                 // KiB of the A stage
       const int row = d * (1024 / (KC * 2)) + lane / R::SLOTS;
       const int slot = lane % R::SLOTS;
       const int g = swz<R::SLOTS>(row, slot);      // the chunk this slot holds
-      dma_lds(xr, __builtin_amdgcn_readfirstlane(base + d * 1024),
-               ((m0 + row) * a.xs + c * KC + 8 * g) * 2);
+      dma_lds(sr, __builtin_amdgcn_readfirstlane(base + d * 1024),
+               ((m0 + row) * rs + c0 + 8 * g) * 2);
     }
 #pragma unroll
     for (int i = 0; i < R::B_LOADS; i++) {
@@ -187,13 +198,18 @@ __global__ __launch_bounds__(256) void k_rows(RowsArgs a) {
   // 16-byte items: row v / (BN / 8), channels 8 (v % (BN / 8)) ..., items
   // of staging pass h in rows 64 h .. 64 h + 63.  The old outputs are loaded
   // first, so their latency overlaps the staging.
+  // Output item (row, col .. col + 7) in y or, past column n1, in y2
+  // (n1 is a multiple of 8).
+  auto out_at = [&](int row, int col) {
+    return col < a.n1 ? a.y + (long)row * a.ys + col : a.y2 + (long)row * a.ys2 + (col - a.n1);
+  };
   u32x4 old[R::ITEMS];
   if (a.accumulate) {
 #pragma unroll
     for (int e = 0; e < R::ITEMS; e++) {
       const int v = tid + 256 * e, row = v / (BN / 8), col = tn * BN + 8 * (v % (BN / 8));
       const bool ok = m0 + row < a.M && col < a.N;
-      old[e] = *(const u32x4 *)(a.y + (ok ? (long)(m0 + row) * a.ys + col : 0));
+      old[e] = *(const u32x4 *)(ok ? out_at(m0 + row, col) : a.y);
     }
   }
   float *st = (float *)lds;
@@ -215,7 +231,7 @@ __global__ __launch_bounds__(256) void k_rows(RowsArgs a) {
       uint16_t o[8];
 #pragma unroll
       for (int k = 0; k < 8; k++) o[k] = f2h(actf(v8[k], col + k));
-      __builtin_memcpy(a.y + (long)(m0 + row) * a.ys + col, o, 16);
+      __builtin_memcpy(out_at(m0 + row, col), o, 16);
     }
   };
   // acc + bias as f32 rows in LDS, 64 rows at a time.
@@ -263,7 +279,8 @@ ien_status launch(ien_ctx *ctx, RowsArgs a, const ConvArgs &c) {
   const int chunks = a.K / KC;
   a.pitch = a.tiles_n * BN;
   int ksplit = 1;
-  if (chunks >= 16 && (4 * a.tiles <= ctx->cus || (a.K >= 1536 && a.tiles < ctx->cus))) {
+  const bool planes = a.k1 < a.K || a.n1 < a.N;  // (the finishing pass writes one map)
+  if (!planes && chunks >= 16 && (4 * a.tiles <= ctx->cus || (a.K >= 1536 && a.tiles < ctx->cus))) {
     ksplit = std::min(chunks / 8, (2 * ctx->cus + a.tiles - 1) / a.tiles);
     while (ksplit > 1 && (size_t)ksplit * a.M * a.pitch > ctx->splitk_floats) ksplit--;
   }
@@ -309,12 +326,57 @@ ien_status launch_rows(ien_ctx *ctx, const ConvArgs &c) {
   a.slope = c.slope;
   a.y = (uint16_t *)c.y;
   a.ys = c.ys;
+  a.x2 = a.x;
+  a.xs2 = a.xs;
+  a.k1 = a.K;
+  a.y2 = a.y;
+  a.ys2 = a.ys;
+  a.n1 = a.N;
   a.act = c.act;
   a.accumulate = c.accumulate;
   // Columns over 64: 64-row tiles (four workgroups a CU, twice the tiles of
   // 128-row ones; measured faster on every model shape); up to 64 columns:
   // 128 x 64 tiles.
   if (c.N > 64 || tiles_of(a.M, 128, a.N) < 128) return launch<64, 128, 32>(ctx, a, c);
+  return launch<128, 64, 32>(ctx, a, c);
+}
+
+ien_status launch_rows_planes(ien_ctx *ctx, const RowsPlanes &p) {
+  const ien_matrix *w = p.w;
+  IEN_CHECK(w && w->d_packed && p.rows > 0, IEN_ERR_INPUT, "rows planes: no weights or rows");
+  const int K = (int)w->k, N = (int)w->n;
+  IEN_CHECK(K % 32 == 0 && p.k1 % 32 == 0 && p.k1 > 0 && p.k1 <= K && N % 8 == 0 &&
+                p.n1 % 8 == 0 && p.n1 > 0 && p.n1 <= N,
+            IEN_ERR_INPUT, "rows planes: k %d split at %d, n %d split at %d", K, p.k1, N, p.n1);
+  const uintptr_t ptrs = (uintptr_t)p.x | (uintptr_t)p.x2 | (uintptr_t)p.y | (uintptr_t)p.y2;
+  IEN_CHECK((ptrs & 15) == 0 && p.xs % 8 == 0 && p.xs2 % 8 == 0 && p.ys % 8 == 0 &&
+                p.ys2 % 8 == 0 && p.xs >= p.k1 && p.xs2 >= K - p.k1 && p.ys >= p.n1 &&
+                p.ys2 >= N - p.n1,
+            IEN_ERR_INPUT, "rows planes: alignment or strides");
+  for (long stride : {(long)p.xs, (long)p.xs2, (long)p.ys, (long)p.ys2})
+    IEN_CHECK(stride * (p.rows + 128) * 2 <= 0x7fff0000L, IEN_ERR_INPUT, "rows planes over 2 GiB");
+  RowsArgs a{};
+  a.x = p.x;
+  a.xs = p.xs;
+  a.x2 = p.x2;
+  a.xs2 = p.xs2;
+  a.k1 = p.k1;
+  a.M = (int)p.rows;
+  a.K = K;
+  a.wp = w->d_packed;
+  a.KB = w->kb;
+  a.NB = w->nb;
+  a.N = N;
+  a.bias = w->d_bias;
+  a.y = p.y;
+  a.ys = p.ys;
+  a.y2 = p.y2;
+  a.ys2 = p.ys2;
+  a.n1 = p.n1;
+  a.act = IEN_ACT_NONE;
+  a.accumulate = p.accumulate;
+  ConvArgs c{};
+  if (N > 64 || tiles_of(a.M, 128, a.N) < 128) return launch<64, 128, 32>(ctx, a, c);
   return launch<128, 64, 32>(ctx, a, c);
 }
 

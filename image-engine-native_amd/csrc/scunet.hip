@@ -129,12 +129,44 @@ void free_maps(Scunet &s) {
 }
 
 // network.rs:158-208 run_level on the h x w map x of c channels (y, t:
-// the block's buffers).
+// the block's buffers).  The split map y (network.rs:9-13: the convolution
+// half in channels 0 .. c/2, the Swin half after it) is kept as two planes
+// of c/2 channels, y and y + pixels c/2, so that the two branches, which
+// run on two streams, write no common cache line; the split product writes
+// both planes and the join reads both, in the channel order of one map.
 ien_status run_level(Scunet &s, ScunetBlock *blocks, int h, int w, int c, Steps *steps,
                      int *step) {
   ien_ctx *ctx = s.ctx;
   const size_t pixels = (size_t)h * w, half = (size_t)c / 2;
-  ien_status st = rows_product(ctx, s.x, c, pixels, blocks[0].split, s.y, c, 0);
+  uint16_t *yc = s.y, *ysw = s.y + pixels * half;
+  auto split = [&](const ien_matrix *m) {
+    RowsPlanes p;
+    p.x = p.x2 = s.x;
+    p.xs = p.xs2 = c;
+    p.k1 = c;
+    p.rows = (long)pixels;
+    p.w = m;
+    p.y = yc;
+    p.y2 = ysw;
+    p.ys = p.ys2 = (int)half;
+    p.n1 = (int)half;
+    return launch_rows_planes(ctx, p);
+  };
+  auto join = [&](const ien_matrix *m) {
+    RowsPlanes p;
+    p.x = yc;
+    p.x2 = ysw;
+    p.xs = p.xs2 = (int)half;
+    p.k1 = (int)half;
+    p.rows = (long)pixels;
+    p.w = m;
+    p.y = p.y2 = s.x;
+    p.ys = p.ys2 = c;
+    p.n1 = c;
+    p.accumulate = 1;
+    return launch_rows_planes(ctx, p);
+  };
+  ien_status st = split(blocks[0].split);
   for (int b = 0; b < BLOCKS && st == IEN_OK; b++) {
     ScunetBlock &B = blocks[b];
     // The two halves are independent until the join: the convolution half
@@ -146,16 +178,15 @@ ien_status run_level(Scunet &s, ScunetBlock *blocks, int h, int w, int c, Steps 
       // Single-buffered: double-buffered chunks (one workgroup of 104 KiB
       // LDS a CU) crowded out the Swin half's kernels (1% slower per image).
       ctx->compact = true;
-      st = conv3(ctx, s.y, h, w, (int)half, c, B.conv1, s.t, (long)half, IEN_ACT_RELU, 0);
+      st = conv3(ctx, yc, h, w, (int)half, (long)half, B.conv1, s.t, (long)half, IEN_ACT_RELU, 0);
       if (st == IEN_OK)
-        st = conv3(ctx, s.t, h, w, (int)half, (long)half, B.conv2, s.y, c, IEN_ACT_NONE, 1);
+        st = conv3(ctx, s.t, h, w, (int)half, (long)half, B.conv2, yc, (long)half, IEN_ACT_NONE, 1);
       ctx->compact = false;
     }
-    if (st == IEN_OK) st = ien_swin_run(B.swin, s.y + half, c, h, w);
+    if (st == IEN_OK) st = ien_swin_run(B.swin, ysw, half, h, w);
     if (st == IEN_OK) st = join_branches(ctx, 1);
-    if (st == IEN_OK) st = rows_product(ctx, s.y, c, pixels, B.join, s.x, c, 1);
-    if (st == IEN_OK && b + 1 < BLOCKS)
-      st = rows_product(ctx, s.x, c, pixels, blocks[b + 1].split, s.y, c, 0);
+    if (st == IEN_OK) st = join(B.join);
+    if (st == IEN_OK && b + 1 < BLOCKS) st = split(blocks[b + 1].split);
     if (st == IEN_OK && steps) st = steps->step(ctx->stream);
     ++*step;
   }
