@@ -519,6 +519,9 @@ def main():
                          "(the workload of the FETCH_SIZE / WRITE_SIZE counter passes)")
     ap.add_argument("--peaks", action="store_true",
                     help="only the measured peaks (MFMA loop, device copy)")
+    ap.add_argument("--serial-branches", action="store_true",
+                    help="run the models' branch streams one after the other (for profiles that "
+                         "attribute time to single kernels; not for the bench line)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py runs on one GPU only: this backend has no multi-GPU path "
@@ -531,6 +534,8 @@ def main():
     import ien
     import synthetic
 
+    if args.serial_branches:
+        os.environ["IEN_SERIAL_BRANCHES"] = "1"
     if not torch.cuda.is_available():
         sys.exit("bench.py needs a GPU")
     torch.cuda.set_device(0)

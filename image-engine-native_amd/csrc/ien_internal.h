@@ -58,6 +58,10 @@ struct ien_ctx {
   // chunks): set by a driver around work that runs beside LDS-hungry
   // kernels of another branch.
   bool compact = false;
+  // Every branch's work stays on the context's stream, one kernel at a time
+  // (IEN_SERIAL_BRANCHES=1 at ien_open): for profiles that attribute time
+  // to single kernels.
+  bool serial_branches = false;
   // Chains of body pairs (conv_pair.hip): an abort word, a failure word
   // and chain_tiles epoch words; the workgroups of the chain kernel one CU
   // holds (-1 until asked); the wall-clock ticks (100 MHz) a tile may wait
@@ -95,6 +99,7 @@ struct Branch {
   hipStream_t stream;
   float *splitk;
   Branch(ien_ctx *c, int i) : ctx(c), stream(c->stream), splitk(c->splitk) {
+    if (ctx->serial_branches) return;
     ctx->stream = ctx->branch[i - 1];
     ctx->splitk = ctx->branch_splitk[i - 1];
   }
