@@ -132,6 +132,14 @@ struct PairArgs {
   uint16_t *border[2];
   int *flags;
   long spin_limit;
+  // Chain only, optional (wl null: none): a final 3x3 64 -> 48 layer
+  // (weights packed with n padded, bias; no activation) whose 48 channels
+  // are pixel-shuffled x4 and added to the f32 RGB image (H x W x 3) into
+  // out ((4 H) x (4 W) x 3 f32) instead of the last pair storing its map.
+  const uint16_t *wl;
+  const float *bl;
+  const float *image;
+  float *out;
 };
 
 constexpr int OOB = 0x7ffffff0;
@@ -150,6 +158,7 @@ __global__ __launch_bounds__(THREADS) void conv_pair(PairArgs a) {
   constexpr int HROW = G::HROW, HALO = G::HALO, MID = G::MID, PARAM = G::PARAM;
   __shared__ __attribute__((aligned(1024))) unsigned char lds[G::LDS];
   __shared__ int go;  // chain: 1 when every neighbour is ready
+  __shared__ float img[CHAIN ? OTR * OTC * 3 : 1];  // chain: the final layer's image tile
   float *par = (float *)(lds + PARAM);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -286,6 +295,61 @@ __global__ __launch_bounds__(THREADS) void conv_pair(PairArgs a) {
   int *abort_word = CHAIN ? a.flags : nullptr;
   int *epochs = CHAIN ? a.flags + 2 : nullptr;
   const int pairs = CHAIN ? a.pairs : 1;
+  // Chain: wait for the 8 neighbours' epoch k (lanes 0..8 of wave 0, one
+  // each), then load the halo's 2-pixel ring from their border map k - 1
+  // (device scope) and wait for it.  False when a wait gave up.
+  auto ring = [&](int k) {
+    if (wave == 0) {
+      bool fail = false;
+      if (lane < 9 && lane != 4) {
+        const int ny = ty + lane / 3 - 1, nx = tx + lane % 3 - 1;
+        if (ny >= 0 && ny < a.tiles_y && nx >= 0 && nx < a.tiles_x) {
+          const int *f = epochs + ny * a.tiles_x + nx;
+          const unsigned long long t0 = wall_clock64();
+          while (__hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < k) {
+            if (__hip_atomic_load(abort_word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0 ||
+                (long)(wall_clock64() - t0) > a.spin_limit) {
+              fail = true;
+              break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+          }
+        }
+      }
+      const bool any = __builtin_amdgcn_ballot_w64(fail) != 0;
+      if (lane == 0) {
+        if (any) {
+          __hip_atomic_store(abort_word, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          __hip_atomic_store(abort_word + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        go = any ? 0 : 1;
+      }
+    }
+    __syncthreads();
+    if (go == 0) return false;
+    const int4v rr = buffer_rsrc(a.border[(k - 1) & 1], map_bytes);
+    // Staged rows 0, 1 and 18, 19: two spans of 2 rows, 1 KiB a load.
+    for (int i = wave; i < 2 * G::RSPAN; i += WAVES) {
+      const int row0 = i < G::RSPAN ? 0 : IR - 2, part = i < G::RSPAN ? i : i - G::RSPAN;
+      const int byte = part * 1024 + lane * 16;
+      const int hy = row0 + byte / HROW, within = byte % HROW;
+      const int hx = within / PB, ch = (within - hx * PB) >> 4;
+      if (byte < 2 * HROW)
+        dma_lds_device(rr, __builtin_amdgcn_readfirstlane(lds0 + row0 * HROW + part * 1024),
+                       halo_src(hy, hx, ch));
+    }
+    // Pixels 0, 1 and 26, 27 of rows 2 .. 17: 32 pieces of 2 staged
+    // pixels (18 chunks, lanes 0 .. 17).
+    for (int i = wave; i < 2 * (IR - 4); i += WAVES) {
+      const int hy = 2 + (i >> 1), hx0 = (i & 1) ? IC - 2 : 0;
+      if (lane < 18)
+        dma_lds_device(rr, __builtin_amdgcn_readfirstlane(lds0 + hy * HROW + hx0 * PB),
+                       halo_src(hy, hx0 + lane / 9, lane % 9));
+    }
+    wait_vm<0>();
+    __syncthreads();
+    return true;
+  };
   for (int k = 0; k < pairs; k++) {
     // ---- the first layer's weights (where its results will go) and, for
     // a single pair or a chain's first, the whole halo from the input; a
@@ -318,58 +382,7 @@ __global__ __launch_bounds__(THREADS) void conv_pair(PairArgs a) {
     // a chain's first pass reads only the halo's centre, and the ring
     // comes in between the passes ----
     first_pass(0);
-    if (CHAIN && k > 0) {
-      // Wait for the 8 neighbours' epoch k (lanes 0..8 of wave 0, one each).
-      if (wave == 0) {
-        bool fail = false;
-        if (lane < 9 && lane != 4) {
-          const int ny = ty + lane / 3 - 1, nx = tx + lane % 3 - 1;
-          if (ny >= 0 && ny < a.tiles_y && nx >= 0 && nx < a.tiles_x) {
-            const int *f = epochs + ny * a.tiles_x + nx;
-            const unsigned long long t0 = wall_clock64();
-            while (__hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < k) {
-              if (__hip_atomic_load(abort_word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0 ||
-                  (long)(wall_clock64() - t0) > a.spin_limit) {
-                fail = true;
-                break;
-              }
-              __builtin_amdgcn_s_sleep(1);
-            }
-          }
-        }
-        const bool any = __builtin_amdgcn_ballot_w64(fail) != 0;
-        if (lane == 0) {
-          if (any) {
-            __hip_atomic_store(abort_word, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(abort_word + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          }
-          go = any ? 0 : 1;
-        }
-      }
-      __syncthreads();
-      if (go == 0) return;  // (no load of this workgroup is in flight here)
-      const int4v rr = buffer_rsrc(a.border[(k - 1) & 1], map_bytes);
-      // Staged rows 0, 1 and 18, 19: two spans of 2 rows, 1 KiB a load.
-      for (int i = wave; i < 2 * G::RSPAN; i += WAVES) {
-        const int row0 = i < G::RSPAN ? 0 : IR - 2, part = i < G::RSPAN ? i : i - G::RSPAN;
-        const int byte = part * 1024 + lane * 16;
-        const int hy = row0 + byte / HROW, within = byte % HROW;
-        const int hx = within / PB, ch = (within - hx * PB) >> 4;
-        if (byte < 2 * HROW)
-          dma_lds_device(rr, __builtin_amdgcn_readfirstlane(lds0 + row0 * HROW + part * 1024),
-                         halo_src(hy, hx, ch));
-      }
-      // Pixels 0, 1 and 26, 27 of rows 2 .. 17: 32 pieces of 2 staged
-      // pixels (18 chunks, lanes 0 .. 17).
-      for (int i = wave; i < 2 * (IR - 4); i += WAVES) {
-        const int hy = 2 + (i >> 1), hx0 = (i & 1) ? IC - 2 : 0;
-        if (lane < 18)
-          dma_lds_device(rr, __builtin_amdgcn_readfirstlane(lds0 + hy * HROW + hx0 * PB),
-                         halo_src(hy, hx0 + lane / 9, lane % 9));
-      }
-      wait_vm<0>();
-      __syncthreads();
-    }
+    if (CHAIN && k > 0 && !ring(k)) return;  // (no load of this workgroup is in flight here)
     first_pass(1);
     __syncthreads();  // the first layer's results complete; the halo is free
 
@@ -457,7 +470,7 @@ __global__ __launch_bounds__(THREADS) void conv_pair(PairArgs a) {
       // (0, 1, 14, 15) and columns (0, 1, 22, 23) that the neighbours read,
       // with the next pair's first weights staged behind them (their
       // completion, and so the epoch, is awaited at the next pair's start).
-      const bool last = k == pairs - 1;
+      const bool last = k == pairs - 1 && !a.wl;  // (a final layer follows the last pair)
       const __amdgpu_buffer_rsrc_t yr = __builtin_amdgcn_make_buffer_rsrc(
           last ? a.y : a.border[k & 1], 0, (int)map_bytes, 0x00020000);
       const int chunks = (last ? OPIX : BORDER) * 8;
@@ -486,7 +499,79 @@ __global__ __launch_bounds__(THREADS) void conv_pair(PairArgs a) {
         else
           __builtin_amdgcn_raw_buffer_store_b128(dv, yr, at, 0, SC1);
       }
-      if (!last) stage_weights(a.w[2 * k + 2], MID);
+      if (!last) stage_weights(k + 1 < pairs ? a.w[2 * k + 2] : a.wl, MID);
+    }
+  }
+
+  if constexpr (CHAIN) {
+    if (!a.wl) return;
+    // ---- the final layer on the 16 x 24 tile, read from the halo (its
+    // 1-pixel ring inside the 2-pixel one), no activation; then the pixel
+    // shuffle x4 plus the image, as f32 RGB ----
+    const int k = pairs;
+    if (tid < C) par[tid] = a.bl[tid];  // zero past channel 48
+    // The tile's image rows (24 pixels x RGB, 288 bytes each) into LDS,
+    // waited for with the ring below; rows past the image read zeros.
+    {
+      const int4v ir = buffer_rsrc(a.image, (long)a.H * a.W * 12);
+      const unsigned i0 = lds_addr(img);
+      for (int i = wave; i < 2 * OTR; i += WAVES) {
+        const int r = i >> 1, part = i & 1, e = 64 * part + lane;
+        if (e < OTC * 3)
+          dma_lds4(ir, __builtin_amdgcn_readfirstlane(i0 + (r * OTC * 3 + 64 * part) * 4),
+                   y0 + r < a.H ? (((y0 + r) * a.W + x0) * 3 + e) * 4 : OOB);
+      }
+    }
+    wait_vm<0>();
+    __syncthreads();
+    if (tid == 0) __hip_atomic_store(epochs + tile, k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    load_weights(MID);
+    __syncthreads();  // every wave holds the weights: MID may take the results
+    if (!ring(k)) return;
+    int base[3];
+#pragma unroll
+    for (int j = 0; j < 3; j++) {
+      const int q = 32 * (grp + 4 * j) + (lane & 31);
+      base[j] = (1 + q / OTC) * HROW + (1 + q % OTC) * PB + 16 * (lane >> 5);
+    }
+    floatx16 acc[3] = {seed(par), seed(par), seed(par)};
+    products(std::integral_constant<int, 3>{}, std::integral_constant<int, HROW>{}, base, acc);
+    // Results [pixel][48] in MID (73728 bytes), rounded through f16 as the
+    // last layer's map between separate launches holds them, so that the
+    // chain's output is bit for bit that of the separate launches.
+    float *res = (float *)(lds + MID);
+    auto r16 = [](float v) { return h2f(f2h(v)); };
+#pragma unroll
+    for (int j = 0; j < 3; j++) {
+      const int q = 32 * (grp + 4 * j) + (lane & 31);
+#pragma unroll
+      for (int g = 0; g < 4; g++) {
+        const int ch = 32 * hf + 8 * g + 4 * (lane >> 5);
+        if (ch < 48)
+          *(float4v *)(res + q * 48 + ch) = float4v{r16(acc[j][4 * g]), r16(acc[j][4 * g + 1]),
+                                                    r16(acc[j][4 * g + 2]), r16(acc[j][4 * g + 3])};
+      }
+    }
+    __syncthreads();
+    // Output row 4 r + i (r < 16) of the tile holds 96 pixels x RGB: 72
+    // chunks of 4 floats, three per input pixel; float f of chunk q is
+    // output pixel 4 x + j (x = f / 12, j = f / 3 % 4), colour c = f % 3:
+    // channel 16 c + 4 i + j of input pixel (r, x) plus the image's colour c.
+    const long ow = 4L * a.W;
+    for (int v = tid; v < 4 * OTR * 72; v += THREADS) {
+      const int row = v / 72, q = v - row * 72;
+      const int r = row >> 2, i = row & 3, x = q / 3;
+      const int gy = y0 + r, gx = x0 + x;
+      if (gy >= a.H || gx >= a.W) continue;
+      const float *px = res + (r * OTC + x) * 48;
+      const float *im = img + (r * OTC + x) * 3;
+      float o[4];
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const int f = 4 * q + e - 12 * x, j = f / 3, c = f - 3 * j;
+        o[e] = px[16 * c + 4 * i + j] + im[c];
+      }
+      *(float4v *)(a.out + ((4L * gy + i) * ow + 4L * x0) * 3 + 4 * q) = float4v{o[0], o[1], o[2], o[3]};
     }
   }
 }
@@ -549,6 +634,13 @@ bool chain_supported(ien_ctx *ctx, const ChainCall &c) {
     return false;
   for (int i = 0; i < 2 * c.pairs; i++)
     if (!layer_ok(c.w[i], c.s[i])) return false;
+  if (c.last) {
+    const ien_matrix *m = c.last;
+    if (m->k != 9 * C || m->n != 48 || m->kb != STEPS || m->nb < 2 || !m->d_packed || !m->d_bias ||
+        !c.image || !c.out || ((uintptr_t)c.out & 15) != 0 ||
+        (long)c.H * c.W * 48 > 0x7fff0000L)
+      return false;
+  }
   // Every tile's workgroup resident at once: one per CU at most.
   if (ctx->chain_per_cu < 0) {
     int n = 0;
@@ -575,11 +667,17 @@ ien_status launch_chain(ien_ctx *ctx, const ChainCall &c, uint16_t **out) {
   fill_layers(a, c.w, c.s, 2 * c.pairs);
   a.flags = ctx->chain_flags;
   a.spin_limit = ctx->chain_spin;
+  if (c.last) {
+    a.wl = c.last->d_packed;
+    a.bl = c.last->d_bias;
+    a.image = c.image;
+    a.out = c.out;
+  }
   const int tiles = a.tiles_x * a.tiles_y;
   hipLaunchKernelGGL(k_clear_chain, dim3(1), dim3(256), 0, ctx->stream, a.flags, tiles);
   hipLaunchKernelGGL(conv_pair<true>, dim3((unsigned)tiles), dim3(THREADS), 0, ctx->stream, a);
   IEN_HIP(hipGetLastError());
-  *out = a.y;
+  *out = c.last ? nullptr : a.y;
   return IEN_OK;
 }
 

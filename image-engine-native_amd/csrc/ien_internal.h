@@ -200,7 +200,7 @@ ien_status launch_pair(ien_ctx *ctx, const PairCall &p);
 // A chain of `pairs` such pairs in one launch (layers w[0], w[1], ...,
 // slopes s[i]): the input in `a`; `b` and `a` hold the borders the tiles
 // exchange, and the output ends in the map launch_chain returns (`a` for an
-// even count).  Supported when every tile's workgroup can be resident at
+// even count), or, with a final layer, in `out`.  Supported when every tile's workgroup can be resident at
 // once.  chain_status waits for the stream and reports whether every chain
 // since the last report finished (a wait for a neighbour that timed out
 // aborts its chain), clearing the report.
@@ -209,6 +209,12 @@ struct ChainCall {
   int H = 0, W = 0, pairs = 0;
   const ien_matrix *w[32] = {};
   const float *s[32] = {};
+  // Optional: a final 3x3 64 -> 48 layer (no activation) whose output is
+  // pixel-shuffled x4 and added to the f32 RGB image (H x W x 3) into out
+  // ((4 H) x (4 W) x 3 f32): realesrgan-native network.rs:110-141.
+  const ien_matrix *last = nullptr;
+  const float *image = nullptr;
+  float *out = nullptr;
 };
 bool chain_supported(ien_ctx *ctx, const ChainCall &c);
 ien_status launch_chain(ien_ctx *ctx, const ChainCall &c, uint16_t **out);

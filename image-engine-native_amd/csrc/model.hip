@@ -279,9 +279,9 @@ static ien_status load_esrgan(ien_model *model, const TensorSource &take) {
 }
 
 // The launches of one run: input to f16, 34 convolutions, shuffle.  With
-// `steps`, progress is reported after each layer; without, the 32 body
-// layers run as one chain of pairs where the device holds every tile at
-// once.
+// `steps`, progress is reported after each layer; without, the 33 layers
+// after the first and the shuffle run as one chain of pairs where the
+// device holds every tile at once.
 static ien_status enqueue_esrgan(ien_model *model, const float *d_image, size_t width,
                                  size_t height, float *d_out, Steps *steps) {
   ien_ctx *ctx = model->ctx;
@@ -304,17 +304,18 @@ static ien_status enqueue_esrgan(ien_model *model, const float *d_image, size_t 
     chain.w[i] = model->layers[1 + i].conv;
     chain.s[i] = model->layers[1 + i].d_slope;
   }
+  chain.last = model->layers[STEPS - 1].conv;
+  chain.image = d_image;
+  chain.out = d_out;
   const bool use_chain = !steps && chain_supported(ctx, chain);
   for (int i = 0; i < STEPS; i++) {
     const EsrganLayer &l = model->layers[i];
     if (i == 1 && use_chain) {
-      // Layers 1 .. 32 from `a`, ending in `a` (an even count of pairs).
+      // Layers 1 .. 33 and the shuffle from `a` into d_out in one launch.
       uint16_t *out = nullptr;
       if ((st = launch_chain(ctx, chain, &out)) != IEN_OK) return st;
-      IEN_CHECK(out == m.a, IEN_ERR_GPU, "body chain ended outside map a");
       model->chained = true;
-      i = STEPS - 2;
-      continue;
+      return IEN_OK;
     }
     const uint16_t *src = i == 0 ? m.image : (i % 2 == 1 ? ma : mb);
     uint16_t *dst = i % 2 == 0 ? ma : mb;
