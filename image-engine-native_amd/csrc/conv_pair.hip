@@ -140,6 +140,12 @@ struct PairArgs {
   const float *bl;
   const float *image;
   float *out;
+  // Chain only, optional (w0 null: none): the first layer, 3x3 over the
+  // image's RGB and a zero fourth channel (weights packed with k = 36 in
+  // 3 fragments, bias, PReLU slopes), computed by the first pair on its
+  // halo from the f32 image instead of reading x.
+  const uint16_t *w0;
+  const float *b0, *s0;
 };
 
 constexpr int OOB = 0x7ffffff0;
@@ -292,6 +298,100 @@ __global__ __launch_bounds__(THREADS) void conv_pair(PairArgs a) {
     __builtin_amdgcn_sched_barrier(0);
   };
 
+  // The products of the 3 output blocks of a wave (grp, grp + 4, grp + 8:
+  // 32 output pixels q each), seeded with `bias`, on a staged map whose
+  // output pixel q's tap (0, 0) is at base_of(q) (rows ROW bytes apart):
+  // two blocks, then one, each passed to emit(j, acc) as soon as its
+  // products are issued, so that no more than two blocks' accumulators and
+  // fragments are live beside the weights.
+  auto three_blocks = [&](auto row, const float *bias, auto base_of, auto emit) {
+    {
+      int base[2];
+#pragma unroll
+      for (int j = 0; j < 2; j++) base[j] = base_of(32 * (grp + 4 * j) + (lane & 31));
+      floatx16 acc[2] = {seed(bias), seed(bias)};
+      products(std::integral_constant<int, 2>{}, row, base, acc);
+      __builtin_amdgcn_sched_barrier(0);
+      emit(0, acc[0]);
+      emit(1, acc[1]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    int base[1] = {base_of(32 * (grp + 8) + (lane & 31))};
+    floatx16 acc[1] = {seed(bias)};
+    products(std::integral_constant<int, 1>{}, row, base, acc);
+    __builtin_amdgcn_sched_barrier(0);
+    emit(2, acc[0]);
+  };
+
+  // Chain, first pair with a first layer: the first layer's outputs on the
+  // whole 20 x 28 halo, from the image patch around it (22 x 30 pixels of
+  // f16 RGB and a zero fourth channel) and the layer's 6 fragments, both
+  // staged in MID; as the separate 4-channel kernel computes them (one
+  // v_mfma_f32_32x32x16_f16 step covers 4 taps of 4 channels, lane half h
+  // reading taps 4 s + 2 h and 4 s + 2 h + 1; taps 9 .. 11 read tap 0
+  // against zero weights), PReLU, zeros outside the image.
+  constexpr int PR = IR + 2, PC = IC + 2;  // the patch: 22 x 30
+  auto first_layer = [&]() {
+    for (int i = tid; i < PR * PC; i += THREADS) {
+      const int gy = y0 - 3 + i / PC, gx = x0 - 3 + i % PC;
+      uint16_t h[4] = {0, 0, 0, 0};
+      if ((unsigned)gy < (unsigned)a.H && (unsigned)gx < (unsigned)a.W) {
+        const float *im = a.image + ((long)gy * a.W + gx) * 3;
+        h[0] = f2h(im[0]);
+        h[1] = f2h(im[1]);
+        h[2] = f2h(im[2]);
+      }
+      uint2 v;
+      __builtin_memcpy(&v, h, 8);
+      *(uint2 *)(lds + MID + i * 8) = v;
+    }
+    constexpr int W0AT = MID + PR * PC * 8;  // the fragments after the patch
+    static_assert((MID + PR * PC * 8) % 16 == 0 && PR * PC * 8 + 6 * 1024 <= WBYTES, "patch");
+    if (wave < 6) {
+      const int4v w0r = buffer_rsrc(a.w0, 6 * 1024);
+      dma_lds(w0r, __builtin_amdgcn_readfirstlane(lds0 + W0AT + wave * 1024), wave * 1024 + lane * 16);
+    }
+    if (tid < C) {
+      par[tid] = a.b0[tid];
+      par[C + tid] = a.s0[tid];
+    }
+    wait_vm<0>();
+    __syncthreads();
+    half8 w0[3];
+#pragma unroll
+    for (int s = 0; s < 3; s++) w0[s] = *(const half8 *)(lds + W0AT + (hf * 3 + s) * 1024 + lane * 16);
+    float4v s4[4];
+    slopes(par + C, s4);
+    auto tap = [](int t) { return t < 9 ? ((t / 3) * PC + t % 3) * 8 : 0; };
+    for (int blk = grp; blk * 32 < IR * IC; blk += 4) {
+      const int p = 32 * blk + (lane & 31), pc = p < IR * IC ? p : IR * IC - 1;
+      const int hy = pc / IC, hx = pc % IC;
+      const unsigned char *pb = lds + MID + (hy * PC + hx) * 8;
+      floatx16 acc = seed(par);
+#pragma unroll
+      for (int s = 0; s < 3; s++) {
+        const int t0 = 4 * s + 2 * (lane >> 5);
+        typedef unsigned u32x2v __attribute__((ext_vector_type(2)));
+        const u32x2v q0 = *(const u32x2v *)(pb + tap(t0)), q1 = *(const u32x2v *)(pb + tap(t0 + 1));
+        const u32x4 raw = {q0[0], q0[1], q1[0], q1[1]};
+        half8 xb;
+        __builtin_memcpy(&xb, &raw, 16);
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(w0[s], xb, acc, 0, 0, 0);
+      }
+      if (p >= IR * IC) continue;
+      const int gy = y0 - 2 + hy, gx = x0 - 2 + hx;
+      const bool inside = (unsigned)gy < (unsigned)a.H && (unsigned)gx < (unsigned)a.W;
+      uint2 o[4];
+      finish(acc, s4, inside ? ~0u : 0u, o);
+#pragma unroll
+      for (int g = 0; g < 4; g++) {
+        const int ch = 32 * hf + 8 * g + 4 * (lane >> 5);
+        *(uint2 *)(lds + hy * HROW + hx * PB + ch * 2) = o[g];
+      }
+    }
+    __syncthreads();  // the halo is complete; MID and the parameters are free
+  };
+
   int *abort_word = CHAIN ? a.flags : nullptr;
   int *epochs = CHAIN ? a.flags + 2 : nullptr;
   const int pairs = CHAIN ? a.pairs : 1;
@@ -355,7 +455,10 @@ __global__ __launch_bounds__(THREADS) void conv_pair(PairArgs a) {
     // a single pair or a chain's first, the whole halo from the input; a
     // chain's later pairs find the weights staged and the halo's centre
     // left in LDS by the pair before ----
-    if (!CHAIN || k == 0) {
+    if (CHAIN && k == 0 && a.w0) {
+      first_layer();
+      stage_weights(a.w[0], MID);
+    } else if (!CHAIN || k == 0) {
       stage_weights(a.w[2 * k], MID);
       // KiB g of the halo: lane l's 16 bytes belong to halo row hy, pixel
       // hx, chunk ch (chunk 8 and the row padding read zeros, as do
@@ -395,14 +498,7 @@ __global__ __launch_bounds__(THREADS) void conv_pair(PairArgs a) {
 
     // ---- phase 2: the second layer on the 16 x 24 outputs, blocks grp,
     // grp + 4, grp + 8 ----
-    int base[3];
-#pragma unroll
-    for (int j = 0; j < 3; j++) {
-      const int q = 32 * (grp + 4 * j) + (lane & 31);
-      base[j] = MID + (q / OTC) * MROW + (q % OTC) * PB + 16 * (lane >> 5);
-    }
-    floatx16 acc[3] = {seed(par + 2 * C), seed(par + 2 * C), seed(par + 2 * C)};
-    products(std::integral_constant<int, 3>{}, std::integral_constant<int, MROW>{}, base, acc);
+    auto mid_base = [&](int q) { return MID + (q / OTC) * MROW + (q % OTC) * PB + 16 * (lane >> 5); };
     float4v s4[4];
     slopes(par + 3 * C, s4);
 
@@ -414,10 +510,10 @@ __global__ __launch_bounds__(THREADS) void conv_pair(PairArgs a) {
       // which keeps both the writes (16 pixels, one chunk) and the reads
       // (4 pixels, 4 chunks) free of bank conflicts.
       unsigned char *stage = lds + wave * (OBLK / 4) * 32 * 64;
-#pragma unroll
-      for (int j = 0; j < 3; j++) {
+      three_blocks(std::integral_constant<int, MROW>{}, par + 2 * C, mid_base,
+                   [&](int j, const floatx16 &acc) {
         uint2 o[4];
-        finish(acc[j], s4, ~0u, o);
+        finish(acc, s4, ~0u, o);
         const int wp = 32 * j + (lane & 31);
 #pragma unroll
         for (int pr = 0; pr < 2; pr++) {
@@ -432,7 +528,7 @@ __global__ __launch_bounds__(THREADS) void conv_pair(PairArgs a) {
           const int c = 2 * pr + (lane >> 5);
           *(uint4 *)(stage + wp * 64 + 16 * (c ^ ((wp >> 2) & 3))) = v;
         }
-      }
+      });
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -452,18 +548,18 @@ __global__ __launch_bounds__(THREADS) void conv_pair(PairArgs a) {
     } else {
       // The results become the centre of the next pair's halo (zeros
       // outside the image: its padding).
-#pragma unroll
-      for (int j = 0; j < 3; j++) {
+      three_blocks(std::integral_constant<int, MROW>{}, par + 2 * C, mid_base,
+                   [&](int j, const floatx16 &acc) {
         const int q = 32 * (grp + 4 * j) + (lane & 31);
         const bool inside = y0 + q / OTC < a.H && x0 + q % OTC < a.W;
         uint2 o[4];
-        finish(acc[j], s4, inside ? ~0u : 0u, o);
+        finish(acc, s4, inside ? ~0u : 0u, o);
 #pragma unroll
         for (int g = 0; g < 4; g++) {
           const int ch = 32 * hf + 8 * g + 4 * (lane >> 5);
           *(uint2 *)(lds + (2 + q / OTC) * HROW + (2 + q % OTC) * PB + ch * 2) = o[g];
         }
-      }
+      });
       __syncthreads();  // the centre is complete; the first layer's results are read
       // Then out, 16 bytes a lane (8 lanes a pixel): the whole tile after
       // the last pair, else, at device scope, the pixels of the outer 2 rows
@@ -528,30 +624,23 @@ __global__ __launch_bounds__(THREADS) void conv_pair(PairArgs a) {
     load_weights(MID);
     __syncthreads();  // every wave holds the weights: MID may take the results
     if (!ring(k)) return;
-    int base[3];
-#pragma unroll
-    for (int j = 0; j < 3; j++) {
-      const int q = 32 * (grp + 4 * j) + (lane & 31);
-      base[j] = (1 + q / OTC) * HROW + (1 + q % OTC) * PB + 16 * (lane >> 5);
-    }
-    floatx16 acc[3] = {seed(par), seed(par), seed(par)};
-    products(std::integral_constant<int, 3>{}, std::integral_constant<int, HROW>{}, base, acc);
     // Results [pixel][48] in MID (73728 bytes), rounded through f16 as the
     // last layer's map between separate launches holds them, so that the
     // chain's output is bit for bit that of the separate launches.
     float *res = (float *)(lds + MID);
     auto r16 = [](float v) { return h2f(f2h(v)); };
-#pragma unroll
-    for (int j = 0; j < 3; j++) {
+    three_blocks(std::integral_constant<int, HROW>{}, par,
+                 [&](int q) { return (1 + q / OTC) * HROW + (1 + q % OTC) * PB + 16 * (lane >> 5); },
+                 [&](int j, const floatx16 &acc) {
       const int q = 32 * (grp + 4 * j) + (lane & 31);
 #pragma unroll
       for (int g = 0; g < 4; g++) {
         const int ch = 32 * hf + 8 * g + 4 * (lane >> 5);
         if (ch < 48)
-          *(float4v *)(res + q * 48 + ch) = float4v{r16(acc[j][4 * g]), r16(acc[j][4 * g + 1]),
-                                                    r16(acc[j][4 * g + 2]), r16(acc[j][4 * g + 3])};
+          *(float4v *)(res + q * 48 + ch) = float4v{r16(acc[4 * g]), r16(acc[4 * g + 1]),
+                                                    r16(acc[4 * g + 2]), r16(acc[4 * g + 3])};
       }
-    }
+    });
     __syncthreads();
     // Output row 4 r + i (r < 16) of the tile holds 96 pixels x RGB: 72
     // chunks of 4 floats, three per input pixel; float f of chunk q is
@@ -634,6 +723,12 @@ bool chain_supported(ien_ctx *ctx, const ChainCall &c) {
     return false;
   for (int i = 0; i < 2 * c.pairs; i++)
     if (!layer_ok(c.w[i], c.s[i])) return false;
+  if (c.first) {
+    const ien_matrix *m = c.first;
+    if (m->k != 36 || m->n != C || m->kb != 3 || m->nb < 2 || !m->d_packed || !m->d_bias ||
+        !c.first_slope || !c.image)
+      return false;
+  }
   if (c.last) {
     const ien_matrix *m = c.last;
     if (m->k != 9 * C || m->n != 48 || m->kb != STEPS || m->nb < 2 || !m->d_packed || !m->d_bias ||
@@ -667,6 +762,12 @@ ien_status launch_chain(ien_ctx *ctx, const ChainCall &c, uint16_t **out) {
   fill_layers(a, c.w, c.s, 2 * c.pairs);
   a.flags = ctx->chain_flags;
   a.spin_limit = ctx->chain_spin;
+  if (c.first) {
+    a.w0 = c.first->d_packed;
+    a.b0 = c.first->d_bias;
+    a.s0 = c.first_slope;
+    a.image = c.image;
+  }
   if (c.last) {
     a.wl = c.last->d_packed;
     a.bl = c.last->d_bias;

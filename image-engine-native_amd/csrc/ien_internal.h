@@ -215,6 +215,11 @@ struct ChainCall {
   const ien_matrix *last = nullptr;
   const float *image = nullptr;
   float *out = nullptr;
+  // Optional: a first 3x3 layer over the image's RGB and a zero fourth
+  // channel (k = 36, 64 outputs, PReLU) that the first pair computes from
+  // `image` instead of reading `a`: network.rs:96-109 with i = 0.
+  const ien_matrix *first = nullptr;
+  const float *first_slope = nullptr;
 };
 bool chain_supported(ien_ctx *ctx, const ChainCall &c);
 ien_status launch_chain(ien_ctx *ctx, const ChainCall &c, uint16_t **out);

@@ -279,21 +279,14 @@ static ien_status load_esrgan(ien_model *model, const TensorSource &take) {
 }
 
 // The launches of one run: input to f16, 34 convolutions, shuffle.  With
-// `steps`, progress is reported after each layer; without, the 33 layers
-// after the first and the shuffle run as one chain of pairs where the
-// device holds every tile at once.
+// `steps`, progress is reported after each layer; without, the whole
+// network runs as one chain of pairs where the device holds every tile at
+// once.
 static ien_status enqueue_esrgan(ien_model *model, const float *d_image, size_t width,
                                  size_t height, float *d_out, Steps *steps) {
   ien_ctx *ctx = model->ctx;
   Maps &m = model->maps;
   const size_t pixels = width * height;
-  ien_status st = ien_pad_image(ctx, IEN_PAD_REPLICATE, d_image, nullptr, width, height, 1,
-                                m.image, 4);
-  if (st != IEN_OK) return st;
-  // Layer i writes `a` when i is even, `b` when odd (gpu.rs:163-169); two
-  // body layers in one launch where the pair kernel takes them, from one
-  // map to the other (so that a pair of layers 2k - 1, 2k also ends in `a`).
-  uint16_t *ma = m.a, *mb = m.b;
   ChainCall chain;
   chain.a = m.a;
   chain.b = m.b;
@@ -304,19 +297,27 @@ static ien_status enqueue_esrgan(ien_model *model, const float *d_image, size_t 
     chain.w[i] = model->layers[1 + i].conv;
     chain.s[i] = model->layers[1 + i].d_slope;
   }
+  chain.first = model->layers[0].conv;
+  chain.first_slope = model->layers[0].d_slope;
   chain.last = model->layers[STEPS - 1].conv;
   chain.image = d_image;
   chain.out = d_out;
-  const bool use_chain = !steps && chain_supported(ctx, chain);
+  if (!steps && chain_supported(ctx, chain)) {
+    // The whole network, image to shuffled output, in one launch.
+    uint16_t *out = nullptr;
+    ien_status st = launch_chain(ctx, chain, &out);
+    if (st == IEN_OK) model->chained = true;
+    return st;
+  }
+  ien_status st = ien_pad_image(ctx, IEN_PAD_REPLICATE, d_image, nullptr, width, height, 1,
+                                m.image, 4);
+  if (st != IEN_OK) return st;
+  // Layer i writes `a` when i is even, `b` when odd (gpu.rs:163-169); two
+  // body layers in one launch where the pair kernel takes them, from one
+  // map to the other (so that a pair of layers 2k - 1, 2k also ends in `a`).
+  uint16_t *ma = m.a, *mb = m.b;
   for (int i = 0; i < STEPS; i++) {
     const EsrganLayer &l = model->layers[i];
-    if (i == 1 && use_chain) {
-      // Layers 1 .. 33 and the shuffle from `a` into d_out in one launch.
-      uint16_t *out = nullptr;
-      if ((st = launch_chain(ctx, chain, &out)) != IEN_OK) return st;
-      model->chained = true;
-      return IEN_OK;
-    }
     const uint16_t *src = i == 0 ? m.image : (i % 2 == 1 ? ma : mb);
     uint16_t *dst = i % 2 == 0 ? ma : mb;
     if (i % 2 == 1 && i + 1 < STEPS - 1) {
