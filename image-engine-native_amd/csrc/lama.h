@@ -17,6 +17,7 @@ struct Lama {
   ien_matrix *first = nullptr, *down[3] = {}, *up[3][4] = {}, *last = nullptr;
   LamaFfc blocks[18][2];
   ien_fourier *fourier = nullptr;  // for the eighth-scale maps of the current size
+  ien_spectral *spectral_plan = nullptr;  // the fused spectral branch (sides <= 64), else null
   size_t pw = 0, ph = 0;           // padded size the maps and the plan are for
   size_t pixels = 0;               // padded pixels the maps hold
   // Full-scale 4-channel input; maps at 1, 1/2, 1/4 (reused by the ups);
@@ -38,6 +39,20 @@ void lama_padded(size_t width, size_t height, size_t *pw, size_t *ph);
 // Maps and the Fourier plan for a padded pw x ph image (outside graph
 // capture); *grew is set when buffers or the plan were replaced.
 ien_status lama_reserve(Lama *l, size_t pw, size_t ph, bool *grew);
+// spectral.hip: the spectral branch of an FFC in three launches: the front
+// two (spectral_in product and row transform; column transforms around the
+// fourier product) write the spectral map, R (h w 192 floats) and U (h half
+// 384 floats); the back one (inverse rows, residual, spectral_out product
+// accumulated with ReLU onto `out`) runs after the cross convolution.
+bool spectral_shapes(const ien_matrix *in, const ien_matrix *f, const ien_matrix *out);
+ien_status spectral_front(const ien_spectral *sp, const uint16_t *x, long xs,
+                          const ien_matrix *m_in, const ien_matrix *m_f, uint16_t *spectral,
+                          float *r, float *u);
+ien_status spectral_back(const ien_spectral *sp, const ien_matrix *m_out, const uint16_t *spectral,
+                         const float *u, uint16_t *out, long ys);
+size_t spectral_r_floats(const ien_spectral *sp);
+size_t spectral_u_floats(const ien_spectral *sp);
+
 ien_status lama_enqueue(Lama *l, const float *d_image, const float *d_mask, size_t width,
                         size_t height, float *d_out, Steps *steps);
 

@@ -95,6 +95,21 @@ ien_status ffc_run(Lama *l, const LamaFfc &f, const uint16_t *x, uint16_t *out, 
     st = conv(ctx, x, h, w, LOCAL, CHANNELS, 3, 1, f.cross, out + LOCAL, CHANNELS, IEN_ACT_NONE,
               0);
   }
+  if (st == IEN_OK && l->spectral_plan) {
+    // The spectral chain in three launches (spectral.hip): two on branch 2,
+    // the last, which accumulates onto the cross output, after the join.
+    // R in the spectrum buffer, U in the work buffer.
+    {
+      Branch b(ctx, 2);
+      st = spectral_front(l->spectral_plan, x + LOCAL, CHANNELS, f.spectral_in, f.fourier,
+                          l->spectral, (float *)l->spectrum, l->work);
+    }
+    if (st == IEN_OK) st = join_branches(ctx, 2);
+    if (st == IEN_OK)
+      st = spectral_back(l->spectral_plan, f.spectral_out, l->spectral, l->work, out + LOCAL,
+                         CHANNELS);
+    return st;
+  }
   if (st == IEN_OK) {
     Branch b(ctx, 2);
     // spectral_in: 1x1 of the global part -> 192, ReLU.
@@ -217,6 +232,8 @@ void lama_free(Lama *l) {
     }
   ien_fourier_free(l->fourier);
   l->fourier = nullptr;
+  ien_spectral_free(l->spectral_plan);
+  l->spectral_plan = nullptr;
   free_maps(*l);
   (void)hipFree(l->d_in);
   (void)hipFree(l->d_mask);
@@ -244,7 +261,13 @@ ien_status lama_reserve(Lama *l, size_t pw, size_t ph, bool *grew) {
     IEN_HIP(hipStreamSynchronize(l->ctx->stream));
     ien_fourier_free(l->fourier);
     l->fourier = nullptr;
+    ien_spectral_free(l->spectral_plan);
+    l->spectral_plan = nullptr;
     ien_status st = ien_fourier_new(l->ctx, h8, w8, &l->fourier);
+    // The fused spectral branch takes maps of sides up to 64 (images up to
+    // 512 x 512); larger ones run the unfused chain.
+    if (st == IEN_OK && h8 <= 64 && w8 <= 64)
+      st = ien_spectral_new(l->ctx, h8, w8, &l->spectral_plan);
     if (st != IEN_OK) return st;
     l->pw = pw;
     l->ph = ph;

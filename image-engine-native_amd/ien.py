@@ -40,7 +40,8 @@ EXPORTS = (
     "ien_swin_run_static",
     "ien_resize", "ien_pad_image", "ien_crop", "ien_gather_2x2", "ien_scatter_2x2", "ien_add",
     "ien_fourier_new", "ien_fourier_free", "ien_fourier_half", "ien_fourier_forward",
-    "ien_fourier_inverse",
+    "ien_fourier_inverse", "ien_spectral_new", "ien_spectral_free", "ien_spectral_work",
+    "ien_spectral_run",
 )
 
 
@@ -192,6 +193,12 @@ def load():
         L.ien_fourier_half.restype = sz
         L.ien_fourier_forward.argtypes = [vp, vp, sz, sz, vp, vp]
         L.ien_fourier_inverse.argtypes = [vp, vp, sz, vp, vp, sz]
+        L.ien_spectral_new.argtypes = [vp, sz, sz, ctypes.POINTER(vp)]
+        L.ien_spectral_free.argtypes = [vp]
+        L.ien_spectral_free.restype = None
+        L.ien_spectral_work.argtypes = [vp]
+        L.ien_spectral_work.restype = sz
+        L.ien_spectral_run.argtypes = [vp, vp, sz, vp, vp, vp, vp, vp, vp, sz]
         for name in EXPORTS:
             getattr(L, name)
         _lib = L
@@ -472,6 +479,34 @@ class Fourier:
     def free(self):
         if self.h:
             load().ien_fourier_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class Spectral:
+    """ien_spectral: LaMa's FFC spectral branch (spectral_in product, rfftn,
+    fourier product, irfftn added, spectral_out product accumulated with
+    ReLU) for height x width maps of sides up to 64."""
+
+    def __init__(self, ctx, height, width):
+        h = ctypes.c_void_p()
+        check(load().ien_spectral_new(ctx.h, height, width, ctypes.byref(h)))
+        self.h, self.height, self.width = h, height, width
+        self.work_floats = load().ien_spectral_work(h)
+
+    def run(self, x, stride, spectral_in, fourier, spectral_out, spectral, work, out, out_stride):
+        check(load().ien_spectral_run(self.h, _ptr(x), stride, spectral_in.h, fourier.h,
+                                      spectral_out.h, _ptr(spectral), _ptr(work), _ptr(out),
+                                      out_stride))
+
+    def free(self):
+        if self.h:
+            load().ien_spectral_free(self.h)
             self.h = None
 
     def __del__(self):

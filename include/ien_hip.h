@@ -399,6 +399,28 @@ ien_status ien_fourier_forward(const ien_fourier *f, const uint16_t *d_x, size_t
 ien_status ien_fourier_inverse(const ien_fourier *f, const uint16_t *d_spectrum, size_t channels,
                                float *d_work, uint16_t *d_out, size_t stride);
 
+/* crates/lama-native/src/network.rs:205-245 (Ffc::run's spectral path):
+ * spectral = ReLU(x spectral_in + b); spectrum = fourier.forward(spectral);
+ * filtered = ReLU(spectrum fourier + b) over spectrum pixels; spectral +=
+ * fourier.inverse(filtered); out = ReLU(out + spectral spectral_out), in
+ * three launches for height x width maps of sides 1 .. 64.  A plan holds the
+ * transform tables for one size. */
+typedef struct ien_spectral ien_spectral;
+ien_status ien_spectral_new(ien_ctx *ctx, size_t height, size_t width, ien_spectral **out);
+void ien_spectral_free(ien_spectral *s);
+/* Floats of d_work that ien_spectral_run needs. */
+size_t ien_spectral_work(const ien_spectral *s);
+/* d_x: the 384 global channels (f16 NHWC, pixel stride `stride`, a multiple
+ * of 8, 16-byte aligned); spectral_in 384 x 192 and fourier 384 x 384 with
+ * bias, spectral_out 192 x 384; d_spectral: height x width x 192 f16 of
+ * scratch (the spectral map); d_work: ien_spectral_work floats; d_out: the
+ * 384 global output channels (pixel stride `out_stride`, a multiple of 4),
+ * holding the cross convolution's output, which the call accumulates onto. */
+ien_status ien_spectral_run(const ien_spectral *s, const uint16_t *d_x, size_t stride,
+                            const ien_matrix *spectral_in, const ien_matrix *fourier,
+                            const ien_matrix *spectral_out, uint16_t *d_spectral, float *d_work,
+                            uint16_t *d_out, size_t out_stride);
+
 /* ---- models: crates/<model>-native/src/lib.rs Model ------------------- */
 typedef enum {
   IEN_MODEL_REALESRGAN = 0,
