@@ -412,10 +412,11 @@ void ien_spectral_free(ien_spectral *s);
 size_t ien_spectral_work(const ien_spectral *s);
 /* d_x: the 384 global channels (f16 NHWC, pixel stride `stride`, a multiple
  * of 8, 16-byte aligned); spectral_in 384 x 192 and fourier 384 x 384 with
- * bias, spectral_out 192 x 384; d_spectral: height x width x 192 f16 of
- * scratch (the spectral map); d_work: ien_spectral_work floats; d_out: the
- * 384 global output channels (pixel stride `out_stride`, a multiple of 4),
- * holding the cross convolution's output, which the call accumulates onto. */
+ * bias, spectral_out 192 x 384; d_spectral: height x 192 x width f16 of
+ * scratch (the spectral map, channel-major per row); d_work:
+ * ien_spectral_work floats; d_out: the 384 global output channels (pixel
+ * stride `out_stride`, a multiple of 8, 16-byte aligned), holding the cross
+ * convolution's output, which the call accumulates onto. */
 ien_status ien_spectral_run(const ien_spectral *s, const uint16_t *d_x, size_t stride,
                             const ien_matrix *spectral_in, const ien_matrix *fourier,
                             const ien_matrix *spectral_out, uint16_t *d_spectral, float *d_work,

@@ -86,7 +86,7 @@ def test_spectral_matches_oracle(ctx, oracle, weights, h, w):
     s_want = f16(oracle.multiply_rows(np.ascontiguousarray(x[..., LOCAL:]).reshape(h * w, GLOBAL),
                                       weights["spectral_in.weight"], weights["spectral_in.bias"],
                                       act=ACT_RELU))
-    s_got = d_spectral.float().cpu().numpy().reshape(h * w, SPECTRAL)
+    s_got = d_spectral.float().cpu().numpy().reshape(h, SPECTRAL, w).transpose(0, 2, 1).reshape(h * w, SPECTRAL)
     assert float(np.abs(s_got - s_want).max()) <= 2e-3 * float(np.abs(s_want).max()) + 1e-3
     for o in (sp, m_in, m_f, m_out):
         o.free()
