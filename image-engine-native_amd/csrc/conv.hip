@@ -1141,6 +1141,8 @@ ien_status launch_conv(ien_ctx *ctx, const ConvCall &c) {
       resident_supported(c.ks, c.stride, c.C, nchw, c.pad_reflect, c.noff, c.rows_mode,
                          (long)c.H * c.W * c.xs * 2))
     return launch_resident(ctx, a, c.ks);
+  // NCHW 1x1 products of whole planes: the register-transposing kernel.
+  if (nchw && nchw1_supported(a, c.ks, c.stride, c.rows)) return launch_nchw1(ctx, a);
   if (c.ks == 3 && c.stride == 1) {
     if (!vec) {
       if (nchw) return run_cfg<3, 1, 4, 32, 4, 2, 16, false, true>(ctx, a);

@@ -172,6 +172,18 @@ __device__ __forceinline__ void dma_lds4(int4v rsrc, unsigned wave_base, int off
                :: "s"(wave_base), "v"(off), "s"(rsrc) : "memory", "m0");
 }
 
+// This wave's LDS accesses done (lgkmcnt(0)), then the workgroup barrier,
+// without the release fence of __syncthreads, which also waits for every
+// outstanding global load (vmcnt(0)) and so for the loads a pipelined
+// kernel keeps in flight across the barrier.  Only for LDS handoffs:
+// global stores made before it are not ordered for the other waves.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xc07f);
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 // s_waitcnt vmcnt(n) alone.
 template <int N>
 __device__ __forceinline__ void wait_vm() {
@@ -232,5 +244,10 @@ bool narrow_supported(const ConvArgs &a, int ks, int stride, int nchw, int noff,
 ien_status launch_narrow(ien_ctx *ctx, ConvArgs a, int ks);
 bool few_supported(const ConvArgs &a, int ks, int stride, int nchw, int noff, int rows_mode);
 ien_status launch_few(ien_ctx *ctx, ConvArgs a, int ks);
+
+// conv_nchw.hip: 1x1 products of whole NCHW f16 planes into NCHW f16
+// planes (pixels a multiple of 8, 16-byte aligned planes), not accumulating.
+bool nchw1_supported(const ConvArgs &a, int ks, int stride, long rows);
+ien_status launch_nchw1(ien_ctx *ctx, const ConvArgs &a);
 
 }  // namespace ien

@@ -163,13 +163,53 @@ def test_nchw_in_and_out(ctx, oracle):
     close(run_gpu(ctx, x, wt, b, nchw_in=True, nchw_out=True, out_f32=True), want, f32=False)
 
 
-# NCHW 1 x 1 (the conv sweep's 256 -> 512): four 64-channel chunks over 64
-# tiles, double-buffered through registers; NCHW and NHWC outputs.
+# NCHW 1 x 1 (the conv sweep's 256 -> 512): NCHW outputs through the
+# register-transposing kernel, NHWC outputs through the general one.
 def test_nchw_1x1(ctx, oracle):
     x, wt, b = case(13, 16, 64, 256, 512, 1)
     want = want_cpu(oracle, x, wt, b, size=1)
     close(run_gpu(ctx, x, wt, b, size=1, nchw_in=True, nchw_out=True), want)
     close(run_gpu(ctx, x, wt, b, size=1, nchw_in=True), want)
+
+
+# The register-transposing NCHW 1 x 1 kernel (whole planes, NCHW f16 out,
+# not accumulating): channel counts that leave a partial 128-channel chunk
+# (48, 208), output counts that leave a partial 128-channel tile (40, 96,
+# 200), pixel counts that leave a partial 64-pixel tile (104, 24), one
+# chunk and four, every activation.
+@pytest.mark.parametrize("h,w,c,n,act", [(8, 13, 48, 40, 0), (16, 64, 208, 96, 1), (4, 6, 16, 200, 2),
+                                         (32, 32, 512, 128, 3), (64, 64, 256, 512, 4)])
+def test_nchw_1x1_planes(ctx, oracle, h, w, c, n, act):
+    x, wt, b = case(40 + c + n, h, w, c, n, 1)
+    slope = np.linspace(-0.3, 0.3, n).astype(np.float32)
+    want = want_cpu(oracle, x, wt, b, size=1, act=act, slope=slope)
+    close(run_gpu(ctx, x, wt, b, size=1, act=act, slope=slope, nchw_in=True, nchw_out=True), want)
+
+
+# NCHW 3 x 3 in and out over whole planes: odd heights, widths that leave a
+# partial 32-pixel tile, output counts that leave a partial 64-channel
+# tile, one tile and many, every activation.
+@pytest.mark.parametrize("h,w,c,n,act", [(5, 40, 64, 64, 0), (9, 24, 32, 40, 1), (16, 96, 64, 200, 2),
+                                         (64, 128, 32, 96, 3), (128, 192, 64, 64, 4), (1, 8, 64, 32, 0)])
+def test_nchw_3x3_planes(ctx, oracle, h, w, c, n, act):
+    x, wt, b = case(60 + h + c + n, h, w, c, n, 9)
+    slope = np.linspace(-0.3, 0.3, n).astype(np.float32)
+    want = want_cpu(oracle, x, wt, b, act=act, slope=slope)
+    close(run_gpu(ctx, x, wt, b, act=act, slope=slope, nchw_in=True, nchw_out=True), want)
+
+
+# Where that kernel does not apply, the general one runs: a row range, an
+# accumulating product, f32 outputs, pixel counts not a multiple of 8.
+def test_nchw_1x1_other_forms(ctx, oracle):
+    x, wt, b = case(77, 8, 16, 64, 96, 1)
+    want = want_cpu(oracle, x, wt, b, size=1)
+    close(run_gpu(ctx, x, wt, b, size=1, nchw_in=True, nchw_out=True, row0=8, rows=64), want[8:72])
+    init = np.random.default_rng(3).standard_normal((8 * 16, 96)).astype(np.float16).astype(np.float32)
+    want2 = want_cpu(oracle, x, wt, b, size=1, init=init)
+    close(run_gpu(ctx, x, wt, b, size=1, nchw_in=True, nchw_out=True, init=init), want2)
+    close(run_gpu(ctx, x, wt, b, size=1, nchw_in=True, nchw_out=True, out_f32=True), want, f32=False)
+    x3, wt3, b3 = case(78, 3, 5, 32, 64, 1)
+    close(run_gpu(ctx, x3, wt3, b3, size=1, nchw_in=True, nchw_out=True), want_cpu(oracle, x3, wt3, b3, size=1))
 
 
 def test_f32_output_and_strides(ctx, oracle):
