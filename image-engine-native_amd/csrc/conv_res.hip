@@ -75,9 +75,16 @@ struct Res8 {
   static_assert(2 * HIT < 64, "vmcnt range");
 };
 
+// ACT: the activation of a plain launch (0 .. 4), or 8 + the activation an
+// accumulating launch applies after adding the old output (its staged sums
+// are not activated).  Both compile-time: a run-time switch per element in
+// the epilogue breaks the straight-line MFMA sequence it is interleaved
+// into.
 template <int KS, int C, int ACT, bool H32 = false>
 __global__ __launch_bounds__(512) void conv_res8(ConvArgs a) {
   using R = Res8<KS, C, H32>;
+  constexpr int EACT = ACT >= 8 ? IEN_ACT_NONE : ACT;  // on the staged sums
+  constexpr int AACT = ACT >= 8 ? ACT - 8 : IEN_ACT_NONE;  // after the old output
   constexpr int IPX = R::IPX, CH = R::CH, NJ = CH / 32;
   constexpr int STEPS = R::STEPS, HC = R::HC, PB = R::PB, P = KS / 2, DEPTH = R::DEPTH;
   constexpr int HIT = R::HIT;
@@ -208,7 +215,7 @@ __global__ __launch_bounds__(512) void conv_res8(ConvArgs a) {
     __builtin_memcpy(o, &ov, 16);
 #pragma unroll
     for (int e = 0; e < 8; e++)
-      h[e] = f2h(activate(h2f(h[e]) + h2f(o[e]), a.act, slope_l[chunk * 8 + e]));
+      h[e] = f2h(act_c<AACT>(h2f(h[e]) + h2f(o[e]), slope_l[chunk * 8 + e]));
     __builtin_memcpy(&sv, h, 16);
     return sv;
   };
@@ -238,7 +245,7 @@ __global__ __launch_bounds__(512) void conv_res8(ConvArgs a) {
           __builtin_memcpy(oh, &ov, 16);
 #pragma unroll
           for (int e = 0; e < 8; e++)
-            h[e] = f2h(activate(h2f(h[e]) + h2f(oh[e]), a.act, slope_l[chunk * 8 + e]));
+            h[e] = f2h(act_c<AACT>(h2f(h[e]) + h2f(oh[e]), slope_l[chunk * 8 + e]));
           __builtin_memcpy(&hv, h, 16);
         }
         *yv = hv;
@@ -248,7 +255,7 @@ __global__ __launch_bounds__(512) void conv_res8(ConvArgs a) {
         const long at = a.out_nchw ? (long)(n0 + e) * a.ys + rel : (long)rel * a.ys + n0 + e;
         float o = h2f(h[e]);
         uint16_t *yh = (uint16_t *)a.y + at;
-        if (a.accumulate) o = activate(o + h2f(*yh), a.act, slope_l[chunk * 8 + e]);
+        if (a.accumulate) o = act_c<AACT>(o + h2f(*yh), slope_l[chunk * 8 + e]);
         *yh = f2h(o);
       }
     }
@@ -256,14 +263,14 @@ __global__ __launch_bounds__(512) void conv_res8(ConvArgs a) {
 
   // One of the 4 epilogue groups of a finished tile.  C^T fragment: the
   // lane holds pixel lane % 32 of its block; register 4 g + e is channel
-  // 32 ng + 8 g + 4 (lane / 32) + e.  (When accumulating, the dispatch
-  // picks ACT = none: the sum is staged and activated after the old output.)
+  // 32 ng + 8 g + 4 (lane / 32) + e.  (When accumulating, EACT is none: the
+  // sum is staged and activated after the old output.)
   auto epilogue = [&](const floatx16 &acc, int g, unsigned char *stage) {
     const int ch = ng * 32 + 8 * g + 4 * (lane >> 5);
     const float4v s4 = *(const float4v *)(slope_l + ch);
     uint16_t h[4];
 #pragma unroll
-    for (int e = 0; e < 4; e++) h[e] = f2h(act_c<ACT>(acc[4 * g + e], s4[e]));
+    for (int e = 0; e < 4; e++) h[e] = f2h(act_c<EACT>(acc[4 * g + e], s4[e]));
     uint2 o;
     __builtin_memcpy(&o, h, 8);
     *(uint2 *)(stage + (tpix * R::SPX + ch) * 2) = o;
@@ -423,12 +430,18 @@ template <int KS, int C, bool H32 = false>
 static ien_status run_res8(ien_ctx *ctx, ConvArgs a) {
   using R = Res8<KS, C, H32>;
   void (*kernel)(ConvArgs) = nullptr;
-  // Accumulating: the sums are staged and activated after the old output.
-  switch (a.accumulate ? IEN_ACT_NONE : a.act) {
+  // Accumulating: the sums are staged and activated after the old output
+  // (ACT 8 + the activation); the tall-tile H32 form never accumulates.
+  switch (a.act + (a.accumulate && !H32 ? 8 : 0)) {
     case IEN_ACT_RELU: kernel = conv_res8<KS, C, IEN_ACT_RELU, H32>; break;
     case IEN_ACT_PRELU: kernel = conv_res8<KS, C, IEN_ACT_PRELU, H32>; break;
     case IEN_ACT_GELU: kernel = conv_res8<KS, C, IEN_ACT_GELU, H32>; break;
     case IEN_ACT_SIGMOID: kernel = conv_res8<KS, C, IEN_ACT_SIGMOID, H32>; break;
+    case 8 + IEN_ACT_NONE: kernel = conv_res8<KS, C, 8 + IEN_ACT_NONE, H32>; break;
+    case 8 + IEN_ACT_RELU: kernel = conv_res8<KS, C, 8 + IEN_ACT_RELU, H32>; break;
+    case 8 + IEN_ACT_PRELU: kernel = conv_res8<KS, C, 8 + IEN_ACT_PRELU, H32>; break;
+    case 8 + IEN_ACT_GELU: kernel = conv_res8<KS, C, 8 + IEN_ACT_GELU, H32>; break;
+    case 8 + IEN_ACT_SIGMOID: kernel = conv_res8<KS, C, 8 + IEN_ACT_SIGMOID, H32>; break;
     default: kernel = conv_res8<KS, C, IEN_ACT_NONE, H32>; break;
   }
   const int first_row = a.p_begin / a.OW, last_row = (a.p_end - 1) / a.OW;
