@@ -83,7 +83,31 @@ ien_status ffc_run(Lama *l, const LamaFfc &f, const uint16_t *x, uint16_t *out, 
   const size_t pixels = (size_t)h * w, half = (size_t)w / 2 + 1, spix = (size_t)h * half;
   // The local convolution, the cross convolution and the spectral chain
   // are independent until the spectral output accumulates onto the cross
-  // part: local on the context's stream, cross on branch 1, the spectral
+  // part.  With the fused spectral branch (spectral.hip): its first two
+  // launches on branch 1 beside the local and cross convolutions on the
+  // context's stream (the two convolutions side by side were slower:
+  // LaMa 2.45 against 2.34 ms/image all on one stream), joined before its
+  // last launch, which accumulates onto the cross output.  R goes to the
+  // spectrum buffer, U to the work buffer.
+  if (l->spectral_plan) {
+    ien_status st = fork_branches(ctx, 1);
+    if (st == IEN_OK) {
+      Branch b(ctx, 1);
+      st = spectral_front(l->spectral_plan, x + LOCAL, CHANNELS, f.spectral_in, f.fourier,
+                          l->spectral, (float *)l->spectrum, l->work);
+    }
+    if (st == IEN_OK)
+      st = conv(ctx, x, h, w, CHANNELS, CHANNELS, 3, 1, f.local, out, CHANNELS, IEN_ACT_RELU, 0);
+    if (st == IEN_OK)
+      st = conv(ctx, x, h, w, LOCAL, CHANNELS, 3, 1, f.cross, out + LOCAL, CHANNELS, IEN_ACT_NONE,
+                0);
+    if (st == IEN_OK) st = join_branches(ctx, 1);
+    if (st == IEN_OK)
+      st = spectral_back(l->spectral_plan, f.spectral_out, l->spectral, l->work, out + LOCAL,
+                         CHANNELS);
+    return st;
+  }
+  // Unfused: local on the context's stream, cross on branch 1, the spectral
   // chain on branch 2, joined before the accumulation.
   ien_status st = fork_branches(ctx, 2);
   // local: all 512 channels -> 128, ReLU.
@@ -94,21 +118,6 @@ ien_status ffc_run(Lama *l, const LamaFfc &f, const uint16_t *x, uint16_t *out, 
     Branch b(ctx, 1);
     st = conv(ctx, x, h, w, LOCAL, CHANNELS, 3, 1, f.cross, out + LOCAL, CHANNELS, IEN_ACT_NONE,
               0);
-  }
-  if (st == IEN_OK && l->spectral_plan) {
-    // The spectral chain in three launches (spectral.hip): two on branch 2,
-    // the last, which accumulates onto the cross output, after the join.
-    // R in the spectrum buffer, U in the work buffer.
-    {
-      Branch b(ctx, 2);
-      st = spectral_front(l->spectral_plan, x + LOCAL, CHANNELS, f.spectral_in, f.fourier,
-                          l->spectral, (float *)l->spectrum, l->work);
-    }
-    if (st == IEN_OK) st = join_branches(ctx, 2);
-    if (st == IEN_OK)
-      st = spectral_back(l->spectral_plan, f.spectral_out, l->spectral, l->work, out + LOCAL,
-                         CHANNELS);
-    return st;
   }
   if (st == IEN_OK) {
     Branch b(ctx, 2);
