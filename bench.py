@@ -7,18 +7,22 @@ plus the conv sweep's MFMA utilisation and the CPU baseline.
 
 A step is one forward pass of the whole network over one synthetic image
 (seeded uniform [0, 1) input, Kaiming-normal random-init weights) with the
-input already resident in HBM: the 36 launches of a step are replayed from
-one HIP graph.  Prints one JSON line.
+input already resident in HBM: a step is one launch, the whole network as
+one chain (ien_model_run_device with graphs on: a run of one launch is
+launched directly).  Prints one JSON line.
 
-roofline: the dominant kernel is the body chain, the 32 body layers (3x3
-64->64 + PReLU each, 16 pairs) in one launch, 32 of the 34 layers of a
-step.  Its algorithmic work per launch is
-32 layers * 2 * 98304 px * 64 * 576 = 231.9 GFLOP (the halo recomputed by
-neighbouring tiles is not counted); its average duration is measured with
-HIP events on the library's stream over back-to-back launches
-(ien_conv3_chain, each after the clear of its flags, as in the model).  `traffic` (HBM bytes per launch from rocprofv3
-FETCH_SIZE / WRITE_SIZE, scaled by a copy kernel of known size) is read
-from profiles/conv_chain_256x384_hbm_traffic.txt when that summary exists.
+roofline: the dominant kernel is that launch, conv_pair<chain>: the first
+layer (3 -> 64), the 32 body layers (3x3 64->64 + PReLU each, 16 pairs)
+and the last layer (64 -> 48) plus the pixel shuffle and the image added.
+Its algorithmic work per launch is 2 * 98304 px * 576 * 64 * 32 (body)
++ 2 * 98304 * 27 * 64 (first) + 2 * 98304 * 576 * 48 (last) = 237.7 GFLOP
+(the halo recomputed by neighbouring tiles is not counted); its average
+duration is measured with HIP events on the library's stream over a graph of
+100 back-to-back runs, after 100 untimed ones (the clock settles under
+sustained load: a run's duration drifts by up to 25 % over the first tens of
+milliseconds).  `traffic` (HBM bytes per launch from rocprofv3 FETCH_SIZE /
+WRITE_SIZE, scaled by a copy kernel of known size) is read from
+profiles/realesrgan_chain_256x384_hbm_traffic.txt when that summary exists.
 
 cpu_baseline: the oracle -- the C restatement of the reference's CPU f32
 path (crates/realesrgan-native/src/network.rs over native-engine's
@@ -148,7 +152,7 @@ def sweep(ctx, stream, reps):
 
 
 def traffic_from_profiles():
-    path = ROOT / "profiles" / "conv_chain_256x384_hbm_traffic.txt"
+    path = ROOT / "profiles" / "realesrgan_chain_256x384_hbm_traffic.txt"
     if not path.exists():
         return None
     m = re.search(r"^traffic_bytes_per_launch:\s*([0-9.eE+]+)", path.read_text(), re.M)
@@ -233,43 +237,29 @@ def cpu_sweep(runs):
                       f"on {cpu_model()}; the oracle (conv3 F(4x4)/F(2x2) for 3x3, multiply for 1x1)"}
 
 
-def body_chain(ctx, tensors, H, W):
-    """The dominant launch: the 32 body layers (3x3 64->64 + PReLU each, the
-    model's body weights) at H x W on a seeded N(0, 1) f16 NHWC map, through
-    ien_conv3_chain; returns (launch, free)."""
-    import numpy as np
+def esrgan_flops(H, W):
+    """Algorithmic FLOPs of one Real-ESRGAN x4v3 run: the first layer
+    (3 -> 64), the 32 body layers (64 -> 64) and the last (64 -> 48), all 3x3."""
+    return (conv_flops(H, W, 3, 64, 3) + 32 * conv_flops(H, W, 64, 64, 3)
+            + conv_flops(H, W, 64, 48, 3))
+
+
+def traffic_probe(ctx, tensors, H, W):
+    """Counter-pass workload: the model's one launch x10 (eager, the seeded
+    image), then a copy of 1 GiB (a kernel of known traffic, for scaling
+    FETCH_SIZE and WRITE_SIZE) whose source was written before 512 MiB of
+    other writes, so that it is read from HBM rather than from the 256 MiB
+    memory-side cache."""
     import torch
 
     import ien
     import synthetic
 
-    layers = synthetic.esrgan_layers(tensors)[1:33]
-    mats = [ien.Matrix(ctx, w, b) for w, b, _ in layers]
-    slopes = [torch.from_numpy(s).cuda() for _, _, s in layers]
-    src = torch.from_numpy(np.random.default_rng(3).standard_normal((H * W, 64))).half().cuda()
-    other = torch.empty((H * W, 64), dtype=torch.float16, device="cuda")
-
-    def launch():
-        ien.conv3_chain(ctx, src, other, H, W, mats, slopes)
-
-    def free():
-        ien.conv3_chain_status(ctx)
-        for m in mats:
-            m.free()
-
-    return launch, free
-
-
-def traffic_probe(ctx, tensors, H, W):
-    """Counter-pass workload: the body chain x10, then a copy of 1 GiB (a
-    kernel of known traffic, for scaling FETCH_SIZE and WRITE_SIZE) whose
-    source was written before 512 MiB of other writes, so that it is read
-    from HBM rather than from the 256 MiB memory-side cache."""
-    import torch
-
-    launch, free = body_chain(ctx, tensors, H, W)
+    model = ien.Model(ctx, ien.MODEL_REALESRGAN, tensors=tensors)
+    d_in = torch.from_numpy(synthetic.esrgan_image(H, W)).cuda()
+    d_out = torch.empty((4 * H, 4 * W, 3), dtype=torch.float32, device="cuda")
     for _ in range(10):
-        launch()
+        model.run_device(d_in, W, H, d_out)
     torch.cuda.synchronize()
     a = torch.empty(512 << 20, dtype=torch.float16, device="cuda").fill_(1)
     flush = torch.empty(256 << 20, dtype=torch.float16, device="cuda").fill_(2)
@@ -277,9 +267,9 @@ def traffic_probe(ctx, tensors, H, W):
     torch.cuda.synchronize()
     c.copy_(a)
     torch.cuda.synchronize()
-    free()
+    model.free()
     del flush
-    print("traffic probe: body chain x10, then a 1073741824-byte copy", flush=True)
+    print("traffic probe: the Real-ESRGAN launch x10, then a 1073741824-byte copy", flush=True)
 
 
 def measured_peaks(ctx, stream):
@@ -499,7 +489,7 @@ def main():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
     ap.add_argument("--cpu-runs", type=int, default=5,
                     help="timed oracle runs per configuration (median, after one warm-up)")
@@ -550,13 +540,13 @@ def main():
         traffic_probe(ctx, tensors, H, W)
         return
     if args.scunet_only:
-        print(json.dumps(scunet_leg(ctx, max(1, args.steps // 10), 2)), flush=True)
+        print(json.dumps(scunet_leg(ctx, max(1, args.steps // 10), 10)), flush=True)
         return
     if args.lama_only:
-        print(json.dumps(lama_leg(ctx, max(1, args.steps // 10), 2)), flush=True)
+        print(json.dumps(lama_leg(ctx, max(1, args.steps // 10), 10)), flush=True)
         return
     if args.birefnet_only:
-        print(json.dumps(birefnet_leg(ctx, max(1, args.steps // 10), 2)), flush=True)
+        print(json.dumps(birefnet_leg(ctx, max(1, args.steps // 10), 10)), flush=True)
         return
     if args.sweep_only:
         print(json.dumps({"gemm_sweep": sweep(ctx, stream, args.kernel_reps)}), flush=True)
@@ -579,19 +569,22 @@ def main():
     if not bool(torch.isfinite(d_out).all()):
         sys.exit("non-finite output")
 
-    # Dominant kernel: the 32 body layers (3x3 64->64 + PReLU) in one launch at 256x384.
-    body, body_free = body_chain(ctx, tensors, H, W)
-    for _ in range(5):
-        body()
-    kms = event_time(body, max(10, args.kernel_reps // 10), stream)
-    flops = 32 * conv_flops(H, W, 64, 64, 3)
+    # Dominant kernel: the step's one launch (the whole network as one
+    # chain), 100 back-to-back runs from one graph after 100 untimed ones.
+    model.set_graph(False)
+    run = lambda: model.run_device(d_in, W, H, d_out)  # noqa: E731
+    for _ in range(100):
+        run()
+    kms = event_time(run, 100, stream)
+    model.set_graph(True)
+    flops = esrgan_flops(H, W)
     achieved = flops / (kms * 1e-3) / 1e12
     roofline = {"bound": "mfma", "achieved": round(achieved, 1), "peak": MFMA_F16_PEAK_TFLOPS,
                 "unit": "TFLOP/s", "frac": round(achieved / MFMA_F16_PEAK_TFLOPS, 4),
                 "traffic": traffic_from_profiles(),
-                "kernel": "conv_pair<chain> (the 32 3x3 64->64 + PReLU body layers in one launch, 256x384)",
+                "kernel": "conv_pair<chain> (the whole network in one launch: first layer, 32 body "
+                          "layers 3x3 64->64 + PReLU, last layer + pixel shuffle, 256x384)",
                 "kernel_us": round(kms * 1e3, 2), "flop_per_launch": flops}
-    body_free()
 
     host_ms = host_path_ms(lambda: model.run(image))
     cpu_runs = 0 if args.no_cpu else args.cpu_runs
@@ -602,7 +595,7 @@ def main():
     if not args.no_models:
         models = {}
         for name, leg in (("scunet", scunet_leg), ("lama", lama_leg), ("birefnet", birefnet_leg)):
-            models[name] = leg(ctx, max(5, args.steps // 20), 2, cpu_runs)
+            models[name] = leg(ctx, max(10, args.steps // 10), 10, cpu_runs)
             log(f"{name} timed")
     cpu = cpu_baseline(tensors, image, cpu_runs) if cpu_runs else None
     sweep_cpu = cpu_sweep(cpu_runs) if cpu_runs and not args.no_sweep else None
@@ -623,7 +616,7 @@ def main():
         "data": "synthetic (seeded uniform [0,1) image, Kaiming-normal random-init weights)",
         "config": {"workload": "Real-ESRGAN general x4v3 (SRVGGNetCompact), 1x3x256x384 -> 1x3x1024x1536",
                    "global_batch": 1, "height": H, "width": W, "layers": 34, "parallelism": "none",
-                   "execution": "one HIP graph per image"},
+                   "execution": "one launch per image (the whole network as one chain)"},
         "images_per_s": round(1e3 / ms_per_step, 1),
         "host_path_ms": host_ms,
         "roofline": roofline,

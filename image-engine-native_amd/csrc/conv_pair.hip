@@ -45,7 +45,10 @@
 // while a reader still needs it.  Every wait is bounded by a wall-clock
 // limit; a tile that runs out sets an abort word that every other waiting
 // tile sees, so all workgroups end (the run reports the failure).  The last
-// pair stores the whole tile.
+// pair stores the whole tile.  Each workgroup counts itself out as its last
+// act; the last one out returns the epochs, the abort word and the count to
+// zero, so the next chain on the stream starts from clear flags without a
+// launch of its own for them.
 
 #include "conv_common.h"
 
@@ -125,10 +128,12 @@ struct PairArgs {
   const uint16_t *w[2 * MAXPAIRS];
   const float *b[2 * MAXPAIRS], *s[2 * MAXPAIRS];
   // Chain only: the border maps (pair k stores to border[k % 2]); the
-  // flags: the abort word (zero at launch), the failure word (set with it,
-  // kept until the host reads it), then the tile epochs (tiles_x tiles_y
-  // words, zero at launch); and the wall-clock ticks (100 MHz) a wait for
-  // neighbours may take.
+  // flags: the abort word, the failure word (set with the abort word, kept
+  // until the host reads it), the count of workgroups done, then the tile
+  // epochs (tiles_x tiles_y words); all but the failure word are zero at
+  // launch and again at the end; and the wall-clock ticks (100 MHz) a wait
+  // for neighbours may take (negative: no wait succeeds, every tile with a
+  // neighbour gives up at its first wait -- the failure path on demand).
   uint16_t *border[2];
   int *flags;
   long spin_limit;
@@ -393,7 +398,26 @@ __global__ __launch_bounds__(THREADS) void conv_pair(PairArgs a) {
   };
 
   int *abort_word = CHAIN ? a.flags : nullptr;
-  int *epochs = CHAIN ? a.flags + 2 : nullptr;
+  int *epochs = CHAIN ? a.flags + 3 : nullptr;
+  // Chain: the workgroup's last act on every way out.  Only wave 0 touches
+  // the flags (the waits and the epoch stores), so it counts the workgroup
+  // out once its own flag accesses are done; the count's release orders
+  // this workgroup's epoch stores before it, and the workgroup that brings
+  // it to the grid size (every other one has left) clears the flags.
+  auto leave = [&]() {
+    if (wave != 0) return;
+    int done = 0;
+    if (lane == 0)
+      done = __hip_atomic_fetch_add(a.flags + 2, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    done = __builtin_amdgcn_readfirstlane(done);
+    if (done != (int)gridDim.x - 1) return;
+    for (int i = lane; i < (int)gridDim.x; i += 64)
+      __hip_atomic_store(epochs + i, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (lane == 0) {
+      __hip_atomic_store(abort_word, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(a.flags + 2, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  };
   const int pairs = CHAIN ? a.pairs : 1;
   // Chain: wait for the 8 neighbours' epoch k (lanes 0..8 of wave 0, one
   // each), then load the halo's 2-pixel ring from their border map k - 1
@@ -406,7 +430,8 @@ __global__ __launch_bounds__(THREADS) void conv_pair(PairArgs a) {
         if (ny >= 0 && ny < a.tiles_y && nx >= 0 && nx < a.tiles_x) {
           const int *f = epochs + ny * a.tiles_x + nx;
           const unsigned long long t0 = wall_clock64();
-          while (__hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < k) {
+          while (a.spin_limit < 0 ||
+                 __hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < k) {
             if (__hip_atomic_load(abort_word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0 ||
                 (long)(wall_clock64() - t0) > a.spin_limit) {
               fail = true;
@@ -485,7 +510,10 @@ __global__ __launch_bounds__(THREADS) void conv_pair(PairArgs a) {
     // a chain's first pass reads only the halo's centre, and the ring
     // comes in between the passes ----
     first_pass(0);
-    if (CHAIN && k > 0 && !ring(k)) return;  // (no load of this workgroup is in flight here)
+    if (CHAIN && k > 0 && !ring(k)) {  // (no load of this workgroup is in flight here)
+      leave();
+      return;
+    }
     first_pass(1);
     __syncthreads();  // the first layer's results complete; the halo is free
 
@@ -600,7 +628,10 @@ __global__ __launch_bounds__(THREADS) void conv_pair(PairArgs a) {
   }
 
   if constexpr (CHAIN) {
-    if (!a.wl) return;
+    if (!a.wl) {
+      leave();
+      return;
+    }
     // ---- the final layer on the 16 x 24 tile, read from the halo (its
     // 1-pixel ring inside the 2-pixel one), no activation; then the pixel
     // shuffle x4 plus the image, as f32 RGB ----
@@ -623,7 +654,10 @@ __global__ __launch_bounds__(THREADS) void conv_pair(PairArgs a) {
     if (tid == 0) __hip_atomic_store(epochs + tile, k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     load_weights(MID);
     __syncthreads();  // every wave holds the weights: MID may take the results
-    if (!ring(k)) return;
+    if (!ring(k)) {
+      leave();
+      return;
+    }
     // Results [pixel][48] in MID (73728 bytes), rounded through f16 as the
     // last layer's map between separate launches holds them, so that the
     // chain's output is bit for bit that of the separate launches.
@@ -662,13 +696,8 @@ __global__ __launch_bounds__(THREADS) void conv_pair(PairArgs a) {
       }
       *(float4v *)(a.out + ((4L * gy + i) * ow + 4L * x0) * 3 + 4 * q) = float4v{o[0], o[1], o[2], o[3]};
     }
+    leave();
   }
-}
-
-// The abort word and the tile epochs of a chain (not the failure word).
-__global__ void k_clear_chain(int *flags, int tiles) {
-  for (int i = threadIdx.x; i < tiles + 2; i += blockDim.x)
-    if (i != 1) flags[i] = 0;
 }
 
 bool layer_ok(const ien_matrix *m, const float *slope) {
@@ -775,7 +804,6 @@ ien_status launch_chain(ien_ctx *ctx, const ChainCall &c, uint16_t **out) {
     a.out = c.out;
   }
   const int tiles = a.tiles_x * a.tiles_y;
-  hipLaunchKernelGGL(k_clear_chain, dim3(1), dim3(256), 0, ctx->stream, a.flags, tiles);
   hipLaunchKernelGGL(conv_pair<true>, dim3((unsigned)tiles), dim3(THREADS), 0, ctx->stream, a);
   IEN_HIP(hipGetLastError());
   *out = c.last ? nullptr : a.y;

@@ -62,8 +62,8 @@ struct ien_ctx {
   // (IEN_SERIAL_BRANCHES=1 at ien_open): for profiles that attribute time
   // to single kernels.
   bool serial_branches = false;
-  // Chains of body pairs (conv_pair.hip): an abort word, a failure word
-  // and chain_tiles epoch words; the workgroups of the chain kernel one CU
+  // Chains of body pairs (conv_pair.hip): an abort word, a failure word, a
+  // count of workgroups done and chain_tiles epoch words; the workgroups of the chain kernel one CU
   // holds (-1 until asked); the wall-clock ticks (100 MHz) a tile may wait
   // for a neighbour.
   int *chain_flags = nullptr;

@@ -185,6 +185,9 @@ struct ien_model {
   ien::Maps maps;
   bool use_graph = false;
   hipGraphExec_t graph = nullptr;
+  // The capture held one launch: replaying it from a graph saves no host
+  // work and costs a few microseconds a replay, so runs launch it directly.
+  bool graph_direct = false;
   const float *graph_in = nullptr, *graph_mask = nullptr;
   float *graph_out = nullptr;
   size_t graph_w = 0, graph_h = 0;
@@ -215,6 +218,7 @@ static void free_maps(Maps &m) {
 static void drop_graph(ien_model *model) {
   if (model->graph) (void)hipGraphExecDestroy(model->graph);
   model->graph = nullptr;
+  model->graph_direct = false;
 }
 
 // gpu.rs:131-136: maps grow on demand and are never shrunk.
@@ -751,8 +755,11 @@ ien_status ien_model_run_device(ien_model *model, const float *d_image, const fl
   st = prepare(model, width, height);
   if (st != IEN_OK) return st;
   if (!model->use_graph) return enqueue(model, d_image, d_mask, width, height, d_out, nullptr);
-  if (!model->graph || model->graph_in != d_image || model->graph_mask != d_mask ||
-      model->graph_out != d_out || model->graph_w != width || model->graph_h != height) {
+  const bool same = model->graph_in == d_image && model->graph_mask == d_mask &&
+                    model->graph_out == d_out && model->graph_w == width && model->graph_h == height;
+  if (same && model->graph_direct)
+    return enqueue(model, d_image, d_mask, width, height, d_out, nullptr);
+  if (!model->graph || !same) {
     drop_graph(model);
     hipGraph_t graph = nullptr;
     IEN_HIP(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
@@ -763,17 +770,26 @@ ien_status ien_model_run_device(ien_model *model, const float *d_image, const fl
       return st;
     }
     if (e != hipSuccess) return fail(IEN_ERR_GPU, "graph capture: %s", hipGetErrorString(e));
-    e = hipGraphInstantiate(&model->graph, graph, nullptr, nullptr, 0);
-    (void)hipGraphDestroy(graph);
-    if (e != hipSuccess) {
-      model->graph = nullptr;
-      return fail(IEN_ERR_GPU, "graph instantiate: %s", hipGetErrorString(e));
+    size_t nodes = 0;
+    e = hipGraphGetNodes(graph, nullptr, &nodes);
+    if (e == hipSuccess && nodes == 1) {
+      (void)hipGraphDestroy(graph);
+      model->graph_direct = true;
+    } else {
+      if (e == hipSuccess) e = hipGraphInstantiate(&model->graph, graph, nullptr, nullptr, 0);
+      (void)hipGraphDestroy(graph);
+      if (e != hipSuccess) {
+        model->graph = nullptr;
+        return fail(IEN_ERR_GPU, "graph instantiate: %s", hipGetErrorString(e));
+      }
     }
     model->graph_in = d_image;
     model->graph_mask = d_mask;
     model->graph_out = d_out;
     model->graph_w = width;
     model->graph_h = height;
+    // (the capture ran nothing)
+    if (model->graph_direct) return enqueue(model, d_image, d_mask, width, height, d_out, nullptr);
   }
   IEN_HIP(hipGraphLaunch(model->graph, ctx->stream));
   return IEN_OK;

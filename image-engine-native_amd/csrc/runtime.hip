@@ -163,8 +163,8 @@ ien_status ien_open(int device, ien_ctx **out) {
   if (e == hipSuccess) e = hipEventCreateWithFlags(&ctx->fork_ev, hipEventDisableTiming);
   if (e == hipSuccess) e = swin_static_setup(device);
   ctx->chain_tiles = ctx->cus;
-  if (e == hipSuccess) e = hipMalloc((void **)&ctx->chain_flags, (ctx->chain_tiles + 2) * 4);
-  if (e == hipSuccess) e = hipMemset(ctx->chain_flags, 0, (ctx->chain_tiles + 2) * 4);
+  if (e == hipSuccess) e = hipMalloc((void **)&ctx->chain_flags, (ctx->chain_tiles + 3) * 4);
+  if (e == hipSuccess) e = hipMemset(ctx->chain_flags, 0, (ctx->chain_tiles + 3) * 4);
   if (const char *v = std::getenv("IEN_CHAIN_SPIN_TICKS")) ctx->chain_spin = std::atol(v);
   if (const char *v = std::getenv("IEN_SERIAL_BRANCHES")) ctx->serial_branches = std::atoi(v) != 0;
   for (int i = 0; i < ien_ctx::BRANCHES && e == hipSuccess; i++) {

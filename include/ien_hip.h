@@ -501,7 +501,10 @@ ien_status ien_model_run_device(ien_model *model, const float *d_image, const fl
                                 size_t width, size_t height, float *d_out);
 
 /* Launch-free replay: capture ien_model_run_device at this size into a HIP
- * graph once, then replay it (0 = eager launches). */
+ * graph once, then replay it (0 = eager launches).  A run that is a single
+ * launch (Real-ESRGAN with its whole network in one chain) is launched
+ * directly instead: a graph saves it no host work and adds a few
+ * microseconds a replay. */
 ien_status ien_model_set_graph(ien_model *model, int enabled);
 
 /* No counterpart in the reference: a measurement of this device for

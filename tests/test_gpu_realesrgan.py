@@ -148,20 +148,23 @@ def test_body_chain_equals_pairs(ctx, tensors, h, w):
 
 
 def test_body_chain_wait_limit(tensors, monkeypatch):
-    """A chain whose tiles may not wait at all for their neighbours (the
-    wall-clock limit forced to 0 from the host): the tiles that find a
-    neighbour behind abort, every workgroup ends, and the run reports the
-    failure; a context with the normal limit is unaffected."""
+    """A chain whose waits for neighbours never succeed (the wall-clock limit
+    set negative from the host): every tile gives up at its first wait and
+    sets the abort word, every workgroup ends, and the run reports the
+    failure; the flags are clear again for the next run, and a context with
+    the normal limit is unaffected."""
     import ien
 
     image = synthetic.esrgan_image(256, 384, seed=9)
-    monkeypatch.setenv("IEN_CHAIN_SPIN_TICKS", "0")
+    monkeypatch.setenv("IEN_CHAIN_SPIN_TICKS", "-1")
     hurried = ien.Context(0)
     monkeypatch.delenv("IEN_CHAIN_SPIN_TICKS")
     model = ien.Model(hurried, ien.MODEL_REALESRGAN, tensors=tensors)
     with pytest.raises(ien.IenError) as e:
         model.run(image)
     assert e.value.status == ien.ERR_GPU and "timed out" in str(e.value), str(e.value)
+    with pytest.raises(ien.IenError):  # again: the failure word was read, cleared and set anew
+        model.run(image)
     model.free()
     hurried.close()
     calm = ien.Context(0)
