@@ -151,6 +151,82 @@ def sweep(ctx, stream, reps):
     return results
 
 
+def elementwise(ctx, stream, reps, copy_tbps=None):
+    """The memory-bound passes at a shape a model runs them, each timed like
+    the sweep (a graph of `reps` back-to-back launches after 20 untimed):
+    algorithmic bytes (every input read once, every output written once),
+    GB/s, % of the 8 TB/s HBM peak and, when given, of the measured device
+    copy rate.  Working sets under 256 MiB may be served partly by the
+    memory-side cache."""
+    import numpy as np
+    import torch
+
+    import ien
+
+    dev, f16 = "cuda", torch.float16
+    rng = np.random.default_rng(5)
+
+    def halves(*shape):
+        return torch.from_numpy(rng.standard_normal(shape).astype(np.float16)).to(dev)
+
+    def floats(*shape):
+        return torch.from_numpy(rng.standard_normal(shape).astype(np.float32)).to(dev)
+
+    cases = []
+    # LayerNorm: BiRefNet 1024x1024, the patch embedding's norm (256x256 tokens x 96) and
+    # stage 1's merge norm (128x128 x 384), in place.
+    for rows, c in ((65536, 96), (16384, 384)):
+        x, g, b = halves(rows, c), floats(c), floats(c)
+        cases.append((f"layer_norm {rows}x{c}", 2 * rows * c * 2,
+                      lambda x=x, rows=rows, c=c, g=g, b=b: ien.layer_norm(ctx, x, rows, c, c, g, b)))
+    # Bilinear align-corners: BiRefNet's half-size stage-1 map (128x128 x 96) to 256x256,
+    # into a 192-channel map.
+    src, dst = halves(128 * 128, 96), halves(256 * 256, 192)
+    cases.append(("resize 128x128x96 -> 256x256", 2 * (128 * 128 + 256 * 256) * 96,
+                  lambda: ien.resize(ctx, src, 128, 128, 96, 96, dst, 256, 256, 192)))
+    # Window gather with the block's LayerNorm: SCUNet level 1 (512x768, 32 channels, windows
+    # of 8 shifted by 4).
+    w = ien.windows(8, 4, 512, 768)
+    wmap, wg, wb = halves(512 * 768, 32), floats(32), floats(32)
+    tokens = torch.empty((ien.window_count(w) * 64, 32), dtype=f16, device=dev)
+    cases.append(("window_gather 512x768x32 w8 s4", 2 * 2 * 512 * 768 * 32,
+                  lambda: ien.window_gather(ctx, w, wmap, 32, 32, wg, wb, tokens)))
+    # 2x2 gather and scatter: SCUNet's halving (512x768 x 64 -> 256x384 rows of 256) and doubling.
+    gmap, grows = halves(512 * 768, 64), torch.empty((256 * 384, 256), dtype=f16, device=dev)
+    cases.append(("gather_2x2 512x768x64", 2 * 2 * 512 * 768 * 64,
+                  lambda: ien.gather_2x2(ctx, gmap, 512, 768, 64, 64, ien.ORDER_ROW_MAJOR, grows)))
+    srows, smap = halves(256 * 384, 128), torch.empty((512 * 768, 32), dtype=f16, device=dev)
+    cases.append(("scatter_2x2 256x384x128 -> 512x768x32", 2 * 2 * 256 * 384 * 128,
+                  lambda: ien.scatter_2x2(ctx, srows, 128, 256, 384, 32, smap, 32)))
+    # Residual add: SCUNet level 1 (512x768 x 64).
+    ax, ay = halves(512 * 768 * 64), halves(512 * 768 * 64)
+    cases.append(("add 512x768x64", 3 * 512 * 768 * 64 * 2, lambda: ien.add(ctx, ax, ay)))
+    # Pixel shuffle x4 plus the repeated image: Real-ESRGAN at 256x384 (the path outside the chain).
+    last, img = halves(256 * 384, 48), floats(256, 384, 3)
+    sh_out = torch.empty((1024, 1536, 3), dtype=torch.float32, device=dev)
+    cases.append(("pixel_shuffle_add 256x384", 256 * 384 * (48 * 2 + 12) + 1024 * 1536 * 12,
+                  lambda: ien.pixel_shuffle_add(ctx, last, 48, img, 384, 256, sh_out)))
+    # f32 -> f16: BiRefNet's 1024x1024 RGB input; u8 -> f32: the same as bytes.
+    fimg, himg = floats(1024 * 1024 * 3), torch.empty(1024 * 1024 * 3, dtype=f16, device=dev)
+    cases.append(("floats_to_halves 1024x1024x3", 1024 * 1024 * 3 * 6,
+                  lambda: ien.floats_to_halves(ctx, fimg, himg)))
+    bimg = torch.from_numpy(rng.integers(0, 256, 1024 * 1024 * 3, dtype=np.uint8)).to(dev)
+    cases.append(("bytes_to_floats 1024x1024x3", 1024 * 1024 * 3 * 5,
+                  lambda: ien.bytes_to_floats(ctx, bimg, fimg)))
+    results = []
+    for name, nbytes, launch in cases:
+        for _ in range(20):
+            launch()
+        ms = event_time(launch, reps, stream)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        row = {"pass": name, "bytes": int(nbytes), "us": round(ms * 1e3, 2), "gbs": round(gbs, 0),
+               "hbm_pct": round(100 * gbs / HBM_PEAK_GBS, 1)}
+        if copy_tbps:
+            row["copy_pct"] = round(100 * gbs / (copy_tbps * 1000), 1)
+        results.append(row)
+    return results
+
+
 def traffic_from_profiles():
     path = ROOT / "profiles" / "realesrgan_chain_256x384_hbm_traffic.txt"
     if not path.exists():
@@ -272,17 +348,18 @@ def traffic_probe(ctx, tensors, H, W):
     print("traffic probe: the Real-ESRGAN launch x10, then a 1073741824-byte copy", flush=True)
 
 
-def measured_peaks(ctx, stream):
+def measured_peaks(ctx, stream, mfma=True):
     """This device's sustained rates beside the published peaks: a
-    register-only f16 MFMA loop on every SIMD (ien_measure_mfma) and a 1 GiB
-    device-to-device copy read from HBM (its source written before 512 MiB
-    of other writes, so not served by the 256 MiB memory-side cache), timed
-    with HIP events; the copy's rate counts bytes read plus written."""
+    register-only f16 MFMA loop on every SIMD (ien_measure_mfma; skipped
+    without `mfma`) and a 1 GiB device-to-device copy read from HBM (its
+    source written before 512 MiB of other writes, so not served by the
+    256 MiB memory-side cache), timed with HIP events; the copy's rate
+    counts bytes read plus written."""
     import torch
 
     import ien
 
-    tf, mfma_ms = ien.measure_mfma(ctx, 100000)
+    tf, mfma_ms = ien.measure_mfma(ctx, 100000) if mfma else (float("nan"), float("nan"))
     a = torch.empty(512 << 20, dtype=torch.float16, device="cuda").fill_(1)
     c = torch.empty_like(a)
     rates = []
@@ -494,6 +571,9 @@ def main():
     ap.add_argument("--cpu-runs", type=int, default=5,
                     help="timed oracle runs per configuration (median, after one warm-up)")
     ap.add_argument("--no-sweep", action="store_true", help="skip the conv sweep")
+    ap.add_argument("--no-elementwise", action="store_true", help="skip the memory-bound passes")
+    ap.add_argument("--elementwise-only", action="store_true",
+                    help="only time the memory-bound passes (and the device copy they are set beside)")
     ap.add_argument("--kernel-reps", type=int, default=100)
     ap.add_argument("--no-models", action="store_true", help="skip the other models (SCUNet, LaMa, BiRefNet)")
     ap.add_argument("--birefnet-only", action="store_true",
@@ -551,6 +631,10 @@ def main():
     if args.sweep_only:
         print(json.dumps({"gemm_sweep": sweep(ctx, stream, args.kernel_reps)}), flush=True)
         return
+    if args.elementwise_only:
+        copy = measured_peaks(ctx, stream, mfma=False)["copy_tbps"]
+        print(json.dumps({"elementwise": elementwise(ctx, stream, args.kernel_reps, copy)}), flush=True)
+        return
     image = synthetic.esrgan_image(H, W)
     model = ien.Model(ctx, ien.MODEL_REALESRGAN, tensors=tensors)
     d_in = torch.from_numpy(image).cuda()
@@ -600,6 +684,8 @@ def main():
     cpu = cpu_baseline(tensors, image, cpu_runs) if cpu_runs else None
     sweep_cpu = cpu_sweep(cpu_runs) if cpu_runs and not args.no_sweep else None
     peaks = measured_peaks(ctx, stream)
+    passes = None if args.no_elementwise else elementwise(ctx, stream, args.kernel_reps, peaks["copy_tbps"])
+    log("memory-bound passes timed")
 
     line = {
         "metric": METRIC,
@@ -623,6 +709,7 @@ def main():
         "cpu_baseline": cpu,
         "gemm_sweep": gemm_sweep,
         "gemm_sweep_cpu": sweep_cpu,
+        "elementwise": passes,
         "models": models,
         "measured_peaks": peaks,
         "device": ctx.name,

@@ -8,6 +8,7 @@
 // and grids are sized to the work, not to the CU count.
 
 #include "ien_internal.h"
+#include "lanes.h"
 
 namespace ien {
 
@@ -150,7 +151,7 @@ __global__ __launch_bounds__(256) void k_layer_norm(uint16_t *__restrict__ x, lo
     v[k] = idx < c ? h2f_e(r[idx]) : 0.0f;
     sum += v[k];
   }
-  for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
+  sum = group_sum<64>(sum);
   const float mean = sum / (float)c;
   float sq = 0.0f;
 #pragma unroll
@@ -159,7 +160,7 @@ __global__ __launch_bounds__(256) void k_layer_norm(uint16_t *__restrict__ x, lo
     float d = idx < c ? v[k] - mean : 0.0f;
     sq += d * d;
   }
-  for (int off = 32; off > 0; off >>= 1) sq += __shfl_xor(sq, off);
+  sq = group_sum<64>(sq);
   const float inv = 1.0f / sqrtf(sq / (float)c + 1e-5f);
 #pragma unroll
   for (int k = 0; k < MAXV; k++) {
@@ -168,10 +169,11 @@ __global__ __launch_bounds__(256) void k_layer_norm(uint16_t *__restrict__ x, lo
   }
 }
 
-// The same with L lanes per row (the row's 8-channel chunks rounded up to a
-// power of two, at most 64) and Q chunks per lane, 16-byte loads and
-// stores: rows of 8-aligned channels at 8-aligned strides.  The reductions
-// stay inside the row's aligned lane group.
+// The same with L lanes per row (a power of two, at most 64) and Q chunks
+// of 8 channels per lane, 16-byte loads and stores: rows of 8-aligned
+// channels at 8-aligned strides.  A lane's gamma and beta are requested
+// with its row, so their latency overlaps the row's.  The reductions stay
+// inside the row's aligned lane group.
 template <int L, int Q>
 __global__ __launch_bounds__(256) void k_layer_norm_vec(uint16_t *__restrict__ x, long rows, int c,
                                                         long stride,
@@ -183,14 +185,24 @@ __global__ __launch_bounds__(256) void k_layer_norm_vec(uint16_t *__restrict__ x
   uint16_t *r = x + row * stride;
   const int chunks = c >> 3;
   float v[8 * Q];
+  float4 g[2 * Q], b[2 * Q];
+  u32x4 raw[Q];
+#pragma unroll
+  for (int q = 0; q < Q; q++) {
+    const int k = min(sub + L * q, chunks - 1);  // (lanes past the row repeat its last chunk)
+    raw[q] = *(const u32x4 *)(r + 8 * k);
+    g[2 * q] = *(const float4 *)(gamma + 8 * k);
+    g[2 * q + 1] = *(const float4 *)(gamma + 8 * k + 4);
+    b[2 * q] = *(const float4 *)(beta + 8 * k);
+    b[2 * q + 1] = *(const float4 *)(beta + 8 * k + 4);
+  }
   float sum = 0.0f;
 #pragma unroll
   for (int q = 0; q < Q; q++) {
     const int k = sub + L * q;
     if (k < chunks) {
-      const u32x4 raw = *(const u32x4 *)(r + 8 * k);
       uint16_t h[8];
-      __builtin_memcpy(h, &raw, 16);
+      __builtin_memcpy(h, &raw[q], 16);
 #pragma unroll
       for (int e = 0; e < 8; e++) v[8 * q + e] = h2f_e(h[e]);
     } else {
@@ -200,8 +212,7 @@ __global__ __launch_bounds__(256) void k_layer_norm_vec(uint16_t *__restrict__ x
 #pragma unroll
     for (int e = 0; e < 8; e++) sum += v[8 * q + e];
   }
-#pragma unroll
-  for (int off = L / 2; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
+  sum = group_sum<L>(sum);
   const float mean = sum / (float)c;
   float sq = 0.0f;
 #pragma unroll
@@ -213,15 +224,13 @@ __global__ __launch_bounds__(256) void k_layer_norm_vec(uint16_t *__restrict__ x
         sq += d * d;
       }
     }
-#pragma unroll
-  for (int off = L / 2; off > 0; off >>= 1) sq += __shfl_xor(sq, off);
+  sq = group_sum<L>(sq);
   const float inv = 1.0f / sqrtf(sq / (float)c + 1e-5f);
 #pragma unroll
   for (int q = 0; q < Q; q++) {
     const int k = sub + L * q;
     if (k < chunks) {
-      const float4 g0 = *(const float4 *)(gamma + 8 * k), g1 = *(const float4 *)(gamma + 8 * k + 4);
-      const float4 b0 = *(const float4 *)(beta + 8 * k), b1 = *(const float4 *)(beta + 8 * k + 4);
+      const float4 g0 = g[2 * q], g1 = g[2 * q + 1], b0 = b[2 * q], b1 = b[2 * q + 1];
       const float gg[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
       const float bb[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
       uint16_t h[8];
@@ -584,25 +593,30 @@ ien_status ien_layer_norm(ien_ctx *ctx, uint16_t *d_x, size_t rows, size_t c, si
   const bool vec = c % 8 == 0 && stride % 8 == 0 && ((uintptr_t)d_x & 15) == 0 &&
                    ((uintptr_t)d_gamma & 15) == 0 && ((uintptr_t)d_beta & 15) == 0;
   if (vec) {
+    // Lanes: the largest power of two dividing the chunks (no idle lanes)
+    // when that leaves at most 3 chunks a lane, else the chunks rounded up
+    // to a power of two (at most 64 lanes, up to 6 chunks each).
     const int chunks = (int)(c / 8);
-    int lanes = 1;
-    while (lanes < chunks && lanes < 64) lanes *= 2;
-    const int q = (chunks + lanes - 1) / lanes;  // at most 6 (c <= 3072)
+    int lanes = std::min(chunks & -chunks, 64), q = (chunks + lanes - 1) / lanes;
+    if (q > 3) {
+      lanes = 1;
+      while (lanes < chunks && lanes < 64) lanes *= 2;
+      q = (chunks + lanes - 1) / lanes;  // at most 6 (c <= 3072)
+    }
     const size_t threads = rows * (size_t)lanes;
     const dim3 grid((unsigned)((threads + 255) / 256));
-    void (*k)(uint16_t *, long, int, long, const float *, const float *) = nullptr;
-    switch (lanes) {
-      case 1: k = k_layer_norm_vec<1, 1>; break;
-      case 2: k = k_layer_norm_vec<2, 1>; break;
-      case 4: k = k_layer_norm_vec<4, 1>; break;
-      case 8: k = k_layer_norm_vec<8, 1>; break;
-      case 16: k = k_layer_norm_vec<16, 1>; break;
-      case 32: k = k_layer_norm_vec<32, 1>; break;
-      default:
-        k = q == 1 ? k_layer_norm_vec<64, 1> : q == 2 ? k_layer_norm_vec<64, 2>
-            : q <= 3 ? k_layer_norm_vec<64, 3> : k_layer_norm_vec<64, 6>;
-        break;
-    }
+    using K = void (*)(uint16_t *, long, int, long, const float *, const float *);
+    static const K table[7][3] = {
+        {k_layer_norm_vec<1, 1>, k_layer_norm_vec<1, 2>, k_layer_norm_vec<1, 3>},
+        {k_layer_norm_vec<2, 1>, k_layer_norm_vec<2, 2>, k_layer_norm_vec<2, 3>},
+        {k_layer_norm_vec<4, 1>, k_layer_norm_vec<4, 2>, k_layer_norm_vec<4, 3>},
+        {k_layer_norm_vec<8, 1>, k_layer_norm_vec<8, 2>, k_layer_norm_vec<8, 3>},
+        {k_layer_norm_vec<16, 1>, k_layer_norm_vec<16, 2>, k_layer_norm_vec<16, 3>},
+        {k_layer_norm_vec<32, 1>, k_layer_norm_vec<32, 2>, k_layer_norm_vec<32, 3>},
+        {k_layer_norm_vec<64, 1>, k_layer_norm_vec<64, 2>, k_layer_norm_vec<64, 3>}};
+    int level = 0;
+    while ((1 << level) < lanes) level++;
+    const K k = q <= 3 ? table[level][q - 1] : k_layer_norm_vec<64, 6>;
     hipLaunchKernelGGL(k, grid, dim3(256), 0, ctx->stream, d_x, (long)rows, (int)c, (long)stride,
                        d_gamma, d_beta);
     IEN_HIP(hipGetLastError());

@@ -4,10 +4,11 @@
 // keeps the known pixels (lama-native lib.rs:138-155), and BiRefNet's
 // ImageNet normalisation (birefnet-native lib.rs:111-116).
 //
-// Every pass is HBM-bound and trivially parallel: a thread owns 16
-// consecutive bytes (one 16-byte load or store) and the floats they map to
-// (four 16-byte accesses), with a scalar path for a ragged end or
-// unaligned pointers.
+// Every pass is HBM-bound and trivially parallel: a thread takes quads of 4
+// consecutive values (4 bytes, one 16-byte float access), 4 quads a step,
+// 256 quads apart, so that each wave instruction reads or writes one
+// contiguous run and each thread has 4 loads in flight; a scalar path
+// covers the ragged end and unaligned pointers.
 
 #include <cmath>
 
@@ -17,7 +18,6 @@ namespace ien {
 namespace {
 
 typedef float float4v __attribute__((ext_vector_type(4)));
-typedef uint8_t byte16 __attribute__((ext_vector_type(16)));
 
 unsigned grid_for16(size_t n) {
   size_t g = (n + 16 * 256 - 1) / (16 * 256);
@@ -41,61 +41,72 @@ __device__ __forceinline__ uint8_t to_byte(float v) {
   return (uint8_t)roundf(c * 255.0f);
 }
 
-__global__ void k_bytes_to_floats(const uint8_t *__restrict__ src, float *__restrict__ dst,
-                                  size_t n, int vec) {
-  for (size_t i = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) * 16; i < n;
-       i += (size_t)gridDim.x * blockDim.x * 16) {
-    if (vec && i + 16 <= n) {
-      const byte16 b = *(const byte16 *)(src + i);
+typedef uint8_t byte4 __attribute__((ext_vector_type(4)));
+
+// The quads of n values: load(q) for the 4 quads of a step first, then
+// put(q, loaded) (q < n / 4); then the last n % 4 values one by one
+// (tail(j), block 0).
+template <typename V, typename Load, typename Put, typename Tail>
+__device__ __forceinline__ void quads(size_t n, Load load, Put put, Tail tail) {
+  const size_t nq = n / 4;
+  for (size_t b = (size_t)blockIdx.x * 1024; b < nq; b += (size_t)gridDim.x * 1024) {
+    V v[4];
 #pragma unroll
-      for (int q = 0; q < 4; q++) {
-        float4v f = {to_float(b[4 * q]), to_float(b[4 * q + 1]), to_float(b[4 * q + 2]),
-                     to_float(b[4 * q + 3])};
-        *(float4v *)(dst + i + 4 * q) = f;
-      }
-    } else {
-      for (size_t j = i; j < n && j < i + 16; j++) dst[j] = to_float(src[j]);
+    for (int k = 0; k < 4; k++) {
+      const size_t q = b + threadIdx.x + 256 * k;
+      if (q < nq) v[k] = load(q);
+    }
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const size_t q = b + threadIdx.x + 256 * k;
+      if (q < nq) put(q, v[k]);
     }
   }
+  if (blockIdx.x == 0 && threadIdx.x < n % 4) tail(4 * nq + threadIdx.x);
+}
+
+// Every value one by one (pointers not aligned for the quads).
+template <typename F>
+__device__ __forceinline__ void singles(size_t n, F f) {
+  for (size_t j = (size_t)blockIdx.x * blockDim.x + threadIdx.x; j < n;
+       j += (size_t)gridDim.x * blockDim.x)
+    f(j);
+}
+
+__global__ void k_bytes_to_floats(const uint8_t *__restrict__ src, float *__restrict__ dst,
+                                  size_t n, int vec) {
+  auto one = [&](size_t j) { dst[j] = to_float(src[j]); };
+  if (!vec) return singles(n, one);
+  quads<byte4>(
+      n, [&](size_t q) { return *(const byte4 *)(src + 4 * q); },
+      [&](size_t q, byte4 b) {
+        *(float4v *)(dst + 4 * q) = float4v{to_float(b[0]), to_float(b[1]), to_float(b[2]), to_float(b[3])};
+      },
+      one);
 }
 
 __global__ void k_floats_to_bytes(const float *__restrict__ src, uint8_t *__restrict__ dst,
                                   size_t n, int vec) {
-  for (size_t i = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) * 16; i < n;
-       i += (size_t)gridDim.x * blockDim.x * 16) {
-    if (vec && i + 16 <= n) {
-      float4v f[4];
-#pragma unroll
-      for (int q = 0; q < 4; q++) f[q] = *(const float4v *)(src + i + 4 * q);
-      byte16 b;
-#pragma unroll
-      for (int q = 0; q < 4; q++)
-#pragma unroll
-        for (int e = 0; e < 4; e++) b[4 * q + e] = to_byte(f[q][e]);
-      *(byte16 *)(dst + i) = b;
-    } else {
-      for (size_t j = i; j < n && j < i + 16; j++) dst[j] = to_byte(src[j]);
-    }
-  }
+  auto one = [&](size_t j) { dst[j] = to_byte(src[j]); };
+  if (!vec) return singles(n, one);
+  quads<float4v>(
+      n, [&](size_t q) { return *(const float4v *)(src + 4 * q); },
+      [&](size_t q, float4v f) {
+        *(byte4 *)(dst + 4 * q) = byte4{to_byte(f[0]), to_byte(f[1]), to_byte(f[2]), to_byte(f[3])};
+      },
+      one);
 }
 
 // lama-native lib.rs:142: f32::from(u8::from(m != 0)).
 __global__ void k_mask_bytes(const uint8_t *__restrict__ src, float *__restrict__ dst, size_t n,
                              int vec) {
-  for (size_t i = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) * 16; i < n;
-       i += (size_t)gridDim.x * blockDim.x * 16) {
-    if (vec && i + 16 <= n) {
-      const byte16 b = *(const byte16 *)(src + i);
-#pragma unroll
-      for (int q = 0; q < 4; q++) {
-        float4v f = {b[4 * q] ? 1.0f : 0.0f, b[4 * q + 1] ? 1.0f : 0.0f,
-                     b[4 * q + 2] ? 1.0f : 0.0f, b[4 * q + 3] ? 1.0f : 0.0f};
-        *(float4v *)(dst + i + 4 * q) = f;
-      }
-    } else {
-      for (size_t j = i; j < n && j < i + 16; j++) dst[j] = src[j] ? 1.0f : 0.0f;
-    }
-  }
+  auto bit = [](uint8_t m) { return m ? 1.0f : 0.0f; };
+  auto one = [&](size_t j) { dst[j] = bit(src[j]); };
+  if (!vec) return singles(n, one);
+  quads<byte4>(
+      n, [&](size_t q) { return *(const byte4 *)(src + 4 * q); },
+      [&](size_t q, byte4 b) { *(float4v *)(dst + 4 * q) = float4v{bit(b[0]), bit(b[1]), bit(b[2]), bit(b[3])}; },
+      one);
 }
 
 // birefnet-native lib.rs:113-116: (f32::from(v) / 255.0 - MEAN[c]) / STD[c]
@@ -110,48 +121,46 @@ __device__ __forceinline__ float normalized(uint8_t v, int c, const Stats &s) {
 
 __global__ void k_normalize_bytes(const uint8_t *__restrict__ src, float *__restrict__ dst,
                                   size_t n, Stats s, int vec) {
-  for (size_t i = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) * 16; i < n;
-       i += (size_t)gridDim.x * blockDim.x * 16) {
-    if (vec && i + 16 <= n) {
-      const byte16 b = *(const byte16 *)(src + i);
-      int c = (int)(i % 3);
-      float v[16];
+  auto one = [&](size_t j) { dst[j] = normalized(src[j], (int)(j % 3), s); };
+  if (!vec) return singles(n, one);
+  quads<byte4>(
+      n, [&](size_t q) { return *(const byte4 *)(src + 4 * q); },
+      [&](size_t q, byte4 b) {
+        int c = (int)((4 * q) % 3);
+        float v[4];
 #pragma unroll
-      for (int e = 0; e < 16; e++) {
-        v[e] = normalized(b[e], c, s);
-        c = c == 2 ? 0 : c + 1;
-      }
-#pragma unroll
-      for (int q = 0; q < 4; q++)
-        *(float4v *)(dst + i + 4 * q) = float4v{v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
-    } else {
-      for (size_t j = i; j < n && j < i + 16; j++) dst[j] = normalized(src[j], (int)(j % 3), s);
-    }
-  }
+        for (int e = 0; e < 4; e++) {
+          v[e] = normalized(b[e], c, s);
+          c = c == 2 ? 0 : c + 1;
+        }
+        *(float4v *)(dst + 4 * q) = float4v{v[0], v[1], v[2], v[3]};
+      },
+      one);
 }
 
 // lama-native lib.rs:147-155: the known pixels keep their bytes, the holes
 // (mask byte not 0) take the prediction as bytes.  Values of interleaved
 // RGB: value i belongs to pixel i / 3.
+struct Composite {
+  byte4 rgb;
+  float4v pred;
+};
+
 __global__ void k_composite_bytes(const uint8_t *__restrict__ rgb, const uint8_t *__restrict__ mask,
                                   const float *__restrict__ pred, uint8_t *__restrict__ out,
                                   size_t n, int vec) {
-  for (size_t i = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) * 16; i < n;
-       i += (size_t)gridDim.x * blockDim.x * 16) {
-    if (vec && i + 16 <= n) {
-      const byte16 b = *(const byte16 *)(rgb + i);
-      float4v f[4];
+  auto one = [&](size_t j) { out[j] = mask[j / 3] ? to_byte(pred[j]) : rgb[j]; };
+  if (!vec) return singles(n, one);
+  quads<Composite>(
+      n,
+      [&](size_t q) { return Composite{*(const byte4 *)(rgb + 4 * q), *(const float4v *)(pred + 4 * q)}; },
+      [&](size_t q, Composite c) {
+        byte4 o;
 #pragma unroll
-      for (int q = 0; q < 4; q++) f[q] = *(const float4v *)(pred + i + 4 * q);
-      byte16 o;
-#pragma unroll
-      for (int e = 0; e < 16; e++)
-        o[e] = mask[(i + e) / 3] ? to_byte(f[e / 4][e % 4]) : b[e];
-      *(byte16 *)(out + i) = o;
-    } else {
-      for (size_t j = i; j < n && j < i + 16; j++) out[j] = mask[j / 3] ? to_byte(pred[j]) : rgb[j];
-    }
-  }
+        for (int e = 0; e < 4; e++) o[e] = mask[(4 * q + e) / 3] ? to_byte(c.pred[e]) : c.rgb[e];
+        *(byte4 *)(out + 4 * q) = o;
+      },
+      one);
 }
 
 }  // namespace

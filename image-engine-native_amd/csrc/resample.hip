@@ -51,6 +51,65 @@ __device__ __forceinline__ void put(const ResizeArgs &a, long at, float v) {
   }
 }
 
+// One thread per output pixel and 8-channel chunk: four 16-byte loads, the
+// blend in f32, one 16-byte store of halves or two of floats (with the old
+// values loaded the same way when adding).  32-bit indexing (the host
+// checks the item count), the output type and the add fixed per instance.
+template <bool F32, bool ADD>
+__global__ __launch_bounds__(256) void k_resize8(ResizeArgs a, int per, int items) {
+  const int item = blockIdx.x * 256 + threadIdx.x;
+  if (item >= items) return;
+  const int pix = item / per, k = item - pix * per;
+  const int y = pix / a.dw, x = pix - y * a.dw;
+  const Tap ty = axis_tap(y, a.sh, a.dh), tx = axis_tap(x, a.sw, a.dw);
+  const float w11 = tx.d2 * ty.d2, w21 = tx.d1 * ty.d2, w12 = tx.d2 * ty.d1, w22 = tx.d1 * ty.d1;
+  const int ss = (int)a.sstride;
+  const uint16_t *s0 = a.src + (ty.i0 * a.sw) * ss + 8 * k, *s1 = a.src + (ty.i1 * a.sw) * ss + 8 * k;
+  const u32x4 r11 = *(const u32x4 *)(s0 + tx.i0 * ss), r21 = *(const u32x4 *)(s0 + tx.i1 * ss);
+  const u32x4 r12 = *(const u32x4 *)(s1 + tx.i0 * ss), r22 = *(const u32x4 *)(s1 + tx.i1 * ss);
+  const long out = (long)pix * a.dstride + 8 * k;
+  float old[8] = {};
+  if constexpr (ADD) {
+    if constexpr (F32) {
+      const float4v o0 = *(const float4v *)((const float *)a.dst + out);
+      const float4v o1 = *(const float4v *)((const float *)a.dst + out + 4);
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        old[e] = o0[e];
+        old[4 + e] = o1[e];
+      }
+    } else {
+      const u32x4 o = *(const u32x4 *)((const uint16_t *)a.dst + out);
+      uint16_t h[8];
+      __builtin_memcpy(h, &o, 16);
+#pragma unroll
+      for (int e = 0; e < 8; e++) old[e] = h2f(h[e]);
+    }
+  }
+  uint16_t h11[8], h21[8], h12[8], h22[8];
+  __builtin_memcpy(h11, &r11, 16);
+  __builtin_memcpy(h21, &r21, 16);
+  __builtin_memcpy(h12, &r12, 16);
+  __builtin_memcpy(h22, &r22, 16);
+  float v[8];
+#pragma unroll
+  for (int e = 0; e < 8; e++) {
+    const float b = w11 * h2f(h11[e]) + w21 * h2f(h21[e]) + w12 * h2f(h12[e]) + w22 * h2f(h22[e]);
+    v[e] = ADD ? old[e] + b : b;
+  }
+  if constexpr (F32) {
+    *(float4v *)((float *)a.dst + out) = float4v{v[0], v[1], v[2], v[3]};
+    *(float4v *)((float *)a.dst + out + 4) = float4v{v[4], v[5], v[6], v[7]};
+  } else {
+    uint16_t o[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) o[e] = f2h(v[e]);
+    u32x4 w;
+    __builtin_memcpy(&w, o, 16);
+    *(u32x4 *)((uint16_t *)a.dst + out) = w;
+  }
+}
+
 // One thread per output pixel and 8-channel chunk (VEC) or channel.
 template <bool VEC>
 __global__ __launch_bounds__(256) void k_resize(ResizeArgs a) {
@@ -197,7 +256,18 @@ ien_status ien_resize(ien_ctx *ctx, const uint16_t *d_src, size_t sh, size_t sw,
   const bool vec = c % 8 == 0 && src_stride % 8 == 0 && ((uintptr_t)d_src & 15) == 0;
   const long items = (long)dh * dw * (vec ? c / 8 : c);
   if (items == 0) return IEN_OK;
-  if (vec)
+  // Whole 16-byte stores: the output aligned and its pixels whole chunks
+  // apart; every index in 32 bits.
+  const size_t osize = out_type == IEN_OUT_F32 ? 4 : 2;
+  const bool store16 = vec && ((uintptr_t)d_dst & 15) == 0 && (dst_stride * osize) % 16 == 0 &&
+                       sh * sw * src_stride < (1u << 31) && items < (1L << 31);
+  if (store16) {
+    const int per = (int)(c / 8), n = (int)items;
+    const dim3 grid(grid256(items)), block(256);
+    auto kernel = out_type == IEN_OUT_F32 ? (add ? k_resize8<true, true> : k_resize8<true, false>)
+                                          : (add ? k_resize8<false, true> : k_resize8<false, false>);
+    hipLaunchKernelGGL(kernel, grid, block, 0, ctx->stream, a, per, n);
+  } else if (vec)
     hipLaunchKernelGGL(k_resize<true>, dim3(grid256(items)), dim3(256), 0, ctx->stream, a);
   else
     hipLaunchKernelGGL(k_resize<false>, dim3(grid256(items)), dim3(256), 0, ctx->stream, a);

@@ -5,6 +5,7 @@
 // crates/native-engine/src/attention.rs).
 
 #include "conv_common.h"
+#include "lanes.h"
 #include "window_geo.h"
 
 namespace ien {
@@ -27,72 +28,97 @@ __device__ __forceinline__ u32x4 pack8(const float *v) {
 }
 
 // L lanes per window row (the row's 8-channel chunks rounded up to a power
-// of two, at most 64), 64 / L rows per wave: gather, LayerNorm (mean, then
-// the mean square deviation, eps 1e-5: math.rs:95-116), or a zero row past
-// the edge.  A lane holds one 8-channel chunk, two when L = 64 and c > 512
-// (c <= 1024).  The reductions stay inside the row's aligned lane group.
-template <int L>
+// of two, at most 64), 64 / L rows per wave instruction, R such rows per
+// lane group: gather, LayerNorm (mean, then the mean square deviation, eps
+// 1e-5: math.rs:95-116), or a zero row past the edge.  A lane holds one
+// 8-channel chunk, two when L = 64 and c > 512 (c <= 1024).  The R rows'
+// loads and the lane's gamma and beta are all requested first; wave v's
+// instruction j covers rows (R v + j) 64 / L .. + 64 / L - 1, whole runs of
+// consecutive rows.  The reductions stay inside the row's aligned lane
+// group (DPP moves up to 16 lanes); row and window arithmetic in 32 bits
+// (the host checks the thread count).
+template <int L, int R>
 __global__ __launch_bounds__(256) void k_window_gather(WinGeo g, const uint16_t *__restrict__ map,
                                                        long stride, int c,
                                                        const float *__restrict__ gamma,
                                                        const float *__restrict__ beta,
                                                        uint16_t *__restrict__ tokens) {
-  constexpr int Q = L == 64 ? 2 : 1;
+  constexpr int Q = L == 64 ? 2 : 1, RPW = 64 / L;
   const int sub = threadIdx.x & (L - 1);
-  const long row = ((long)blockIdx.x * 256 + threadIdx.x) / L;
-  if (row >= g.windows * g.n) return;  // whole lane groups leave together
-  const long src = win_source(g, row / g.n, (int)(row % g.n));
-  uint16_t *dst = tokens + row * c;
-  const int chunks = c >> 3;
-  if (src < 0) {
-    const u32x4 zero = {0u, 0u, 0u, 0u};
-    for (int k = sub; k < chunks; k += L) *(u32x4 *)(dst + 8 * k) = zero;
-    return;
+  const int wave = (int)((blockIdx.x * 256 + threadIdx.x) >> 6);
+  const int row0 = wave * R * RPW + (int)((threadIdx.x & 63) / L);
+  const int rows = (int)g.windows * g.n, chunks = c >> 3;
+  int src[R];
+#pragma unroll
+  for (int j = 0; j < R; j++) {
+    const int row = row0 + j * RPW;
+    const int w = row / g.n;
+    src[j] = row < rows ? win_source(g, w, row - w * g.n) : -1;
   }
-  const uint16_t *s = map + src * stride;
-  float v[8 * Q];
-  float sum = 0.0f;
+  u32x4 raw[R][Q];
+  float4 gb[4 * Q];
 #pragma unroll
   for (int q = 0; q < Q; q++) {
-    const int k = sub + L * q;
-    if (k < chunks) {
-      unpack8(*(const u32x4 *)(s + 8 * k), v + 8 * q);
-    } else {
+    const int k = min(sub + L * q, chunks - 1);  // (lanes past the row repeat its last chunk)
 #pragma unroll
-      for (int e = 0; e < 8; e++) v[8 * q + e] = 0.0f;
+    for (int j = 0; j < R; j++)
+      if (src[j] >= 0) raw[j][q] = *(const u32x4 *)(map + (long)src[j] * stride + 8 * k);
+    gb[4 * q] = *(const float4 *)(gamma + 8 * k);
+    gb[4 * q + 1] = *(const float4 *)(gamma + 8 * k + 4);
+    gb[4 * q + 2] = *(const float4 *)(beta + 8 * k);
+    gb[4 * q + 3] = *(const float4 *)(beta + 8 * k + 4);
+  }
+#pragma unroll
+  for (int j = 0; j < R; j++) {
+    const int row = row0 + j * RPW;
+    if (row >= rows) continue;  // (whole lane groups)
+    uint16_t *dst = tokens + (long)row * c;
+    if (src[j] < 0) {
+      const u32x4 zero = {0u, 0u, 0u, 0u};
+      for (int k = sub; k < chunks; k += L) *(u32x4 *)(dst + 8 * k) = zero;
+      continue;
     }
+    float v[8 * Q];
+    float sum = 0.0f;
 #pragma unroll
-    for (int e = 0; e < 8; e++) sum += v[8 * q + e];
-  }
+    for (int q = 0; q < Q; q++) {
+      const int k = sub + L * q;
+      if (k < chunks) {
+        unpack8(raw[j][q], v + 8 * q);
+      } else {
 #pragma unroll
-  for (int off = L / 2; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
-  const float mean = sum / (float)c;
-  float sq = 0.0f;
+        for (int e = 0; e < 8; e++) v[8 * q + e] = 0.0f;
+      }
 #pragma unroll
-  for (int q = 0; q < Q; q++) {
-    if (sub + L * q < chunks) {
+      for (int e = 0; e < 8; e++) sum += v[8 * q + e];
+    }
+    sum = group_sum<L>(sum);
+    const float mean = sum / (float)c;
+    float sq = 0.0f;
 #pragma unroll
-      for (int e = 0; e < 8; e++) {
-        const float d = v[8 * q + e] - mean;
-        sq += d * d;
+    for (int q = 0; q < Q; q++) {
+      if (sub + L * q < chunks) {
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+          const float d = v[8 * q + e] - mean;
+          sq += d * d;
+        }
       }
     }
-  }
+    sq = group_sum<L>(sq);
+    const float inv = 1.0f / sqrtf(sq / (float)c + 1e-5f);
 #pragma unroll
-  for (int off = L / 2; off > 0; off >>= 1) sq += __shfl_xor(sq, off);
-  const float inv = 1.0f / sqrtf(sq / (float)c + 1e-5f);
+    for (int q = 0; q < Q; q++) {
+      const int k = sub + L * q;
+      if (k < chunks) {
+        const float4 g0 = gb[4 * q], g1 = gb[4 * q + 1], b0 = gb[4 * q + 2], b1 = gb[4 * q + 3];
+        const float gg[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+        const float bb[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+        float o[8];
 #pragma unroll
-  for (int q = 0; q < Q; q++) {
-    const int k = sub + L * q;
-    if (k < chunks) {
-      const float4 g0 = *(const float4 *)(gamma + 8 * k), g1 = *(const float4 *)(gamma + 8 * k + 4);
-      const float4 b0 = *(const float4 *)(beta + 8 * k), b1 = *(const float4 *)(beta + 8 * k + 4);
-      const float gg[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
-      const float bb[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
-      float o[8];
-#pragma unroll
-      for (int e = 0; e < 8; e++) o[e] = (v[8 * q + e] - mean) * inv * gg[e] + bb[e];
-      *(u32x4 *)(dst + 8 * k) = pack8(o);
+        for (int e = 0; e < 8; e++) o[e] = (v[8 * q + e] - mean) * inv * gg[e] + bb[e];
+        *(u32x4 *)(dst + 8 * k) = pack8(o);
+      }
     }
   }
 }
@@ -397,21 +423,26 @@ ien_status ien_window_gather(ien_ctx *ctx, const ien_windows *w, const uint16_t 
   const int chunks = c / 8;
   int lanes = 1;
   while (lanes < chunks && lanes < 64) lanes *= 2;
-  const long threads = rows * lanes;
-  IEN_CHECK((threads + 255) / 256 < (1L << 31), IEN_ERR_INPUT, "%ld rows", rows);
+  // One row a lane group (2 and 4 measured no faster at SCUNet's level 1):
+  // waves of 64 / lanes rows, whole workgroups.
+  constexpr int R = 1;
+  const long per_block = 4L * R * (64 / lanes);
+  const long blocks = (rows + per_block - 1) / per_block;
+  IEN_CHECK(blocks * per_block < (1L << 31) && blocks * 256 < (1L << 31), IEN_ERR_INPUT, "%ld rows",
+            rows);
   void (*k)(WinGeo, const uint16_t *, long, int, const float *, const float *, uint16_t *) =
       nullptr;
   switch (lanes) {
-    case 1: k = k_window_gather<1>; break;
-    case 2: k = k_window_gather<2>; break;
-    case 4: k = k_window_gather<4>; break;
-    case 8: k = k_window_gather<8>; break;
-    case 16: k = k_window_gather<16>; break;
-    case 32: k = k_window_gather<32>; break;
-    default: k = k_window_gather<64>; break;
+    case 1: k = k_window_gather<1, R>; break;
+    case 2: k = k_window_gather<2, R>; break;
+    case 4: k = k_window_gather<4, R>; break;
+    case 8: k = k_window_gather<8, R>; break;
+    case 16: k = k_window_gather<16, R>; break;
+    case 32: k = k_window_gather<32, R>; break;
+    default: k = k_window_gather<64, R>; break;
   }
-  hipLaunchKernelGGL(k, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, ctx->stream, g,
-                     d_map, (long)stride, c, d_gamma, d_beta, d_tokens);
+  hipLaunchKernelGGL(k, dim3((unsigned)blocks), dim3(256), 0, ctx->stream, g, d_map, (long)stride, c,
+                     d_gamma, d_beta, d_tokens);
   IEN_HIP(hipGetLastError());
   return IEN_OK;
 }

@@ -30,6 +30,17 @@ __device__ __forceinline__ long win_source(const WinGeo &g, long w, int i) {
   return (long)y * g.width + x;
 }
 
+// The same in 32-bit arithmetic (window counts and maps under 2^31).
+__device__ __forceinline__ int win_source(const WinGeo &g, int w, int i) {
+  const int wy = w / g.wx, wxi = w - wy * g.wx;
+  int y = wy * g.window + i / g.window + g.shift;
+  int x = wxi * g.window + i % g.window + g.shift;
+  if (y >= g.ph) y -= g.ph;
+  if (x >= g.pw) x -= g.pw;
+  if (y >= g.height || x >= g.width) return -1;
+  return y * g.width + x;
+}
+
 // swin.rs:171-176: 1 for a window last in its row, 2 last in its column.
 __device__ __forceinline__ int win_class(const WinGeo &g, long w) {
   if (g.shift == 0) return 0;

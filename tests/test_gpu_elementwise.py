@@ -50,7 +50,8 @@ def test_pixel_shuffle_add_bit_exact(ctx, oracle, h, w, stride):
 
 
 @pytest.mark.parametrize("rows,c", [(1, 32), (77, 96), (300, 768), (5, 3072), (9, 37), (40, 8),
-                                    (33, 1536), (7, 2048), (130, 2304)])
+                                    (33, 1536), (7, 2048), (130, 2304), (1000, 96), (64, 384),
+                                    (11, 24), (13, 48), (17, 56), (21, 192), (19, 160)])
 def test_layer_norm(ctx, oracle, rows, c):
     import torch
     import ien

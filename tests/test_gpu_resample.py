@@ -12,7 +12,7 @@ pytestmark = pytest.mark.gpu
 
 @pytest.mark.parametrize("sh,sw,dh,dw,c", [(5, 7, 9, 13, 8), (32, 32, 64, 64, 64), (64, 64, 32, 32, 16),
                                            (256, 256, 1024, 1024, 1), (1, 5, 3, 9, 3), (17, 23, 17, 23, 24)])
-@pytest.mark.parametrize("out_f32,add", [(False, False), (True, False), (True, True)])
+@pytest.mark.parametrize("out_f32,add", [(False, False), (False, True), (True, False), (True, True)])
 def test_resize(ctx, oracle, sh, sw, dh, dw, c, out_f32, add):
     import torch
     import ien
