@@ -136,6 +136,7 @@ def sweep(ctx, stream, reps):
     import synthetic
 
     results = []
+    counters = sweep_counters_from_profiles()
     for entry in synthetic.SWEEP:
         case = SweepCase(ctx, entry[0])
         for _ in range(5):
@@ -146,6 +147,8 @@ def sweep(ctx, stream, reps):
         row = {"shape": case.name, "us": round(ms * 1e3, 2), "tflops": round(tflops, 1),
                "mfma_util_pct": round(100 * tflops / MFMA_F16_PEAK_TFLOPS, 1),
                "hbm_gbs": round(gbs, 0), "hbm_pct": round(100 * gbs / HBM_PEAK_GBS, 1)}
+        if case.name in counters:
+            row["rocprof"] = counters[case.name]
         results.append(row)
         case.free()
     return results
@@ -225,6 +228,37 @@ def elementwise(ctx, stream, reps, copy_tbps=None):
             row["copy_pct"] = round(100 * gbs / (copy_tbps * 1000), 1)
         results.append(row)
     return results
+
+
+def counters_from_profiles(cfg):
+    """The counter-derived figures of one configuration from its committed
+    summary (profiles/<cfg>_counters.md, made from `--counter-probe` runs
+    under rocprofv3 --pmc): rocprof_frac (algorithmic GFLOP over the
+    serialized kernel time, of the f16 peak), mfma_busy_pct, traffic bytes
+    per image and their ratio to the compulsory bytes; None without it."""
+    path = ROOT / "profiles" / f"{cfg}_counters.md"
+    if not path.exists():
+        return None
+    out = {}
+    for key in ("rocprof_frac", "mfma_busy_pct", "traffic_bytes_per_image", "traffic_ratio", "serial_kernel_us"):
+        m = re.search(rf"^{key}:\s*([0-9.eE+-]+)", path.read_text(), re.M)
+        if m:
+            out[key] = float(m.group(1))
+    out["source"] = f"profiles/{cfg}_counters.md"
+    return out
+
+
+def sweep_counters_from_profiles():
+    """Per sweep shape: traffic bytes per launch, its ratio to the
+    algorithmic bytes, MFMA busy % and rocprof_frac (profiles/sweep_counters.md)."""
+    path = ROOT / "profiles" / "sweep_counters.md"
+    if not path.exists():
+        return {}
+    out = {}
+    for m in re.finditer(r"^shape (\S+): (.*)$", path.read_text(), re.M):
+        f = m.group(2).split()
+        out[m.group(1)] = {f[i]: float(f[i + 1]) for i in range(0, len(f) - 1, 2)}
+    return out
 
 
 def traffic_from_profiles():
@@ -320,9 +354,11 @@ def esrgan_flops(H, W):
             + conv_flops(H, W, 64, 48, 3))
 
 
-def traffic_probe(ctx, tensors, H, W):
-    """Counter-pass workload: the model's one launch x10 (eager, the seeded
-    image), then a copy of 1 GiB (a kernel of known traffic, for scaling
+def counter_probe(ctx, name, runs):
+    """Counter-pass workload of one configuration (for rocprofv3 --pmc):
+    `runs` eager runs of its model on its synthetic input (one dispatch a
+    kernel; the branches on their streams), or every sweep shape `runs`
+    times; then a copy of 1 GiB (a kernel of known traffic, for scaling
     FETCH_SIZE and WRITE_SIZE) whose source was written before 512 MiB of
     other writes, so that it is read from HBM rather than from the 256 MiB
     memory-side cache."""
@@ -331,21 +367,54 @@ def traffic_probe(ctx, tensors, H, W):
     import ien
     import synthetic
 
-    model = ien.Model(ctx, ien.MODEL_REALESRGAN, tensors=tensors)
-    d_in = torch.from_numpy(synthetic.esrgan_image(H, W)).cuda()
-    d_out = torch.empty((4 * H, 4 * W, 3), dtype=torch.float32, device="cuda")
-    for _ in range(10):
-        model.run_device(d_in, W, H, d_out)
-    torch.cuda.synchronize()
-    a = torch.empty(512 << 20, dtype=torch.float16, device="cuda").fill_(1)
-    flush = torch.empty(256 << 20, dtype=torch.float16, device="cuda").fill_(2)
+    dev = "cuda"
+    if name == "sweep":
+        for entry in synthetic.SWEEP:
+            case = SweepCase(ctx, entry[0])
+            for _ in range(runs):
+                case.launch()
+            torch.cuda.synchronize()
+            case.free()
+        what = f"each conv-sweep shape x{runs}"
+    else:
+        if name == "esrgan":
+            h, w, kind, tensors = 256, 384, ien.MODEL_REALESRGAN, synthetic.esrgan_tensors()
+            image, mask, out = synthetic.esrgan_image(h, w), None, (4 * h, 4 * w, 3)
+        elif name == "scunet":
+            h, w, kind, tensors = 512, 768, ien.MODEL_SCUNET, synthetic.scunet_tensors()
+            image, mask, out = synthetic.scunet_image(h, w), None, (h, w, 3)
+        elif name == "lama":
+            h, w, kind, tensors = 512, 512, ien.MODEL_LAMA, synthetic.lama_tensors()
+            image, mask, out = synthetic.lama_image(h, w), synthetic.lama_mask(h, w), (h, w, 3)
+        elif name == "birefnet":
+            h = w = 1024
+            kind, tensors = ien.MODEL_BIREFNET, synthetic.birefnet_tensors()
+            image, mask, out = synthetic.birefnet_image(h), None, (h, w)
+        else:
+            sys.exit(f"unknown counter probe {name!r}")
+        model = ien.Model(ctx, kind, tensors=tensors)
+        d_in = torch.from_numpy(image).to(dev)
+        d_mask = None if mask is None else torch.from_numpy(mask).to(dev)
+        d_out = torch.empty(out, dtype=torch.float32, device=dev)
+        for _ in range(runs):
+            model.run_device(d_in, w, h, d_out, d_mask=d_mask)
+        torch.cuda.synchronize()
+        model.free()
+        what = f"the {name} model x{runs} (eager)"
+    a = torch.empty(512 << 20, dtype=torch.float16, device=dev).fill_(1)
+    flush = torch.empty(256 << 20, dtype=torch.float16, device=dev).fill_(2)
     c = torch.empty_like(a)
     torch.cuda.synchronize()
     c.copy_(a)
     torch.cuda.synchronize()
-    model.free()
     del flush
-    print("traffic probe: the Real-ESRGAN launch x10, then a 1073741824-byte copy", flush=True)
+    print(f"counter probe: {what}, then a 1073741824-byte copy", flush=True)
+
+
+def traffic_probe(ctx):
+    """The dominant kernel's counter-pass workload: the Real-ESRGAN model's
+    one launch x10 (eager, the seeded image), then the 1 GiB copy."""
+    counter_probe(ctx, "esrgan", 10)
 
 
 def measured_peaks(ctx, stream, mfma=True):
@@ -572,6 +641,9 @@ def main():
                     help="timed oracle runs per configuration (median, after one warm-up)")
     ap.add_argument("--no-sweep", action="store_true", help="skip the conv sweep")
     ap.add_argument("--no-elementwise", action="store_true", help="skip the memory-bound passes")
+    ap.add_argument("--counter-probe", choices=["esrgan", "scunet", "lama", "birefnet", "sweep"],
+                    help="only run one configuration eagerly, then a 1 GiB copy (for rocprofv3 --pmc passes)")
+    ap.add_argument("--probe-runs", type=int, default=3, help="runs of the counter probe's workload")
     ap.add_argument("--elementwise-only", action="store_true",
                     help="only time the memory-bound passes (and the device copy they are set beside)")
     ap.add_argument("--kernel-reps", type=int, default=100)
@@ -617,7 +689,10 @@ def main():
         print(json.dumps({"measured_peaks": measured_peaks(ctx, stream)}), flush=True)
         return
     if args.traffic_probe:
-        traffic_probe(ctx, tensors, H, W)
+        traffic_probe(ctx)
+        return
+    if args.counter_probe:
+        counter_probe(ctx, args.counter_probe, args.probe_runs)
         return
     if args.scunet_only:
         print(json.dumps(scunet_leg(ctx, max(1, args.steps // 10), 10)), flush=True)
@@ -668,7 +743,8 @@ def main():
                 "traffic": traffic_from_profiles(),
                 "kernel": "conv_pair<chain> (the whole network in one launch: first layer, 32 body "
                           "layers 3x3 64->64 + PReLU, last layer + pixel shuffle, 256x384)",
-                "kernel_us": round(kms * 1e3, 2), "flop_per_launch": flops}
+                "kernel_us": round(kms * 1e3, 2), "flop_per_launch": flops,
+                "rocprof": counters_from_profiles("esrgan")}
 
     host_ms = host_path_ms(lambda: model.run(image))
     cpu_runs = 0 if args.no_cpu else args.cpu_runs
@@ -680,6 +756,7 @@ def main():
         models = {}
         for name, leg in (("scunet", scunet_leg), ("lama", lama_leg), ("birefnet", birefnet_leg)):
             models[name] = leg(ctx, max(10, args.steps // 10), 10, cpu_runs)
+            models[name]["rocprof"] = counters_from_profiles(name)
             log(f"{name} timed")
     cpu = cpu_baseline(tensors, image, cpu_runs) if cpu_runs else None
     sweep_cpu = cpu_sweep(cpu_runs) if cpu_runs and not args.no_sweep else None
