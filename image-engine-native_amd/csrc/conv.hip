@@ -144,11 +144,12 @@ __global__ __launch_bounds__(256) void conv_mfma(ConvArgs a) {
   // Bias and PReLU slope of this lane's accumulator column, per N-block:
   // loaded now, used after the products.
   float bias_r[NBW], slope_r[NBW];
-  if (a.ksplit > 1) a.y = (float *)a.y + (long)blockIdx.y * (a.p_end - a.p_begin) * a.ys;
+  const bool raw_split = a.ksplit > 1 && !a.part;  // raw sums for a finishing pass
+  if (raw_split) a.y = (float *)a.y + (long)blockIdx.y * (a.p_end - a.p_begin) * a.ys;
 #pragma unroll
   for (int j = 0; j < NBW; j++) {
     const int n = (nblk0 + j) * 32 + (lane & 31);  // < NB * 32: the bias is padded
-    bias_r[j] = a.ksplit > 1 ? 0.0f : a.bias[n];
+    bias_r[j] = raw_split ? 0.0f : a.bias[n];
     slope_r[j] = a.act == IEN_ACT_PRELU ? a.slope[min(n, a.N - 1)] : 0.0f;
   }
 
@@ -546,6 +547,65 @@ __global__ __launch_bounds__(256) void conv_mfma(ConvArgs a) {
       __syncthreads();
 
       compute(lds_raw, cc);
+    }
+  }
+
+  // ---- split-K counted in per tile: this split's sums go out (16 bytes a
+  // lane per accumulator quarter, in register order, at device scope so
+  // that a split on another XCD reads them from memory), then the tile's
+  // counter; the split that brings it to ksplit returns it to zero, adds
+  // the tile's sums in split order and carries on with the epilogue ----
+  if (a.ksplit > 1 && a.part) {
+    int *last = (int *)lds_raw;  // (written after the barrier below: every wave is past its products)
+    constexpr int G = MBW * NBW * 4;  // 16-byte groups a thread
+    constexpr int SC1 = 16;           // cache policy bits of a device-scope access
+    const int z = blockIdx.y;
+    const long first = (long)blockIdx.x * a.ksplit;  // the tile's first split block
+    const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(
+        a.part, (short)0, (int)((long)gridDim.x * a.ksplit * G * 4096), 0x00020000);
+    auto at = [&](int s, int g) { return (int)((((first + s) * G + g) * 256 + tid) * 16); };
+#pragma unroll
+    for (int i = 0; i < MBW; i++)
+#pragma unroll
+      for (int j = 0; j < NBW; j++)
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          const float4v v = {acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
+                             acc[i][j][4 * q + 3]};
+          __builtin_amdgcn_raw_buffer_store_b128(*(const u32x4 *)&v, pr, at(z, (i * NBW + j) * 4 + q),
+                                                 0, SC1);
+        }
+    wait_vm<0>();  // this thread's sums are out
+    __syncthreads();
+    if (tid == 0) {
+      const int done =
+          __hip_atomic_fetch_add(a.tile_count + blockIdx.x, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      *last = done == a.ksplit - 1;
+      if (*last) __hip_atomic_store(a.tile_count + blockIdx.x, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (!*last) return;
+    // The sums in split order, this split's own read back too (the order,
+    // and so the result, must not depend on which split came last).
+#pragma unroll
+    for (int i = 0; i < MBW; i++)
+#pragma unroll
+      for (int j = 0; j < NBW; j++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
+    for (int s = 0; s < a.ksplit; s++) {
+#pragma unroll
+      for (int i = 0; i < MBW; i++)
+#pragma unroll
+        for (int j = 0; j < NBW; j++)
+#pragma unroll
+          for (int q = 0; q < 4; q++) {
+            const u32x4 raw =
+                __builtin_amdgcn_raw_buffer_load_b128(pr, at(s, (i * NBW + j) * 4 + q), 0, SC1);
+            const float4v v = *(const float4v *)&raw;
+#pragma unroll
+            for (int e = 0; e < 4; e++) acc[i][j][4 * q + e] += v[e];
+          }
     }
   }
 
@@ -1038,7 +1098,23 @@ static ien_status run_cfg(ien_ctx *ctx, ConvArgs a) {
     a.kchunks = chunks;
     return launch(a, dim3((unsigned)blocks));
   }
+  // Double-buffered launches of up to 4 splits, each tile's splits counted
+  // in: its last split adds them and finishes the tile (the sums of a split
+  // block: 256 threads x MBW NBW accumulators).  Deeper splits keep the
+  // finishing pass, which spreads the additions over every CU rather than
+  // one split a tile (BiRefNet's 8-tile, 32-split decoder products: 3.11
+  // -> 3.18 ms an image counted in), and so do the single-buffered launches
+  // (BiRefNet's 7 x 7 products in 4 splits: 3.16 -> 3.19 ms).
+  const long split_floats = 256L * Cfg::MBW * NBW * 16;
+  if (db && a.ksplit <= 4 && blocks <= ien_ctx::SPLITK_TILES &&
+      blocks * a.ksplit * split_floats <= (long)ctx->splitk_floats) {
+    a.part = ctx->splitk;
+    a.tile_count = (int *)(ctx->splitk + ctx->splitk_floats);
+    return launch(a, dim3((unsigned)blocks, (unsigned)a.ksplit));
+  }
   ConvArgs pa = a;
+  pa.part = nullptr;
+  pa.tile_count = nullptr;
   pa.y = ctx->splitk;
   pa.ys = pitch;
   pa.out_f32 = 1;
@@ -1070,7 +1146,7 @@ ien_status launch_conv(ien_ctx *ctx, const ConvCall &c) {
   const long out_extent = c.out_nchw ? (long)w->n * c.ys : c.rows * c.ys;
   IEN_CHECK(in_extent < (1L << 31) && out_extent < (1L << 31) && c.row0 + c.rows < (1L << 31),
             IEN_ERR_INPUT, "tensors over 2^31 elements");
-  ConvArgs a;
+  ConvArgs a{};
   std::memset(&a, 0, sizeof a);
   a.x = c.x;
   a.H = c.H;

@@ -41,7 +41,12 @@ struct ConvArgs {
   // Split-K: blockIdx.y takes channel chunks [kchunks y, kchunks (y + 1)),
   // and with ksplit > 1 the launch writes raw f32 sums (no bias) to
   // y + y_index * (p_end - p_begin) * ys, NHWC; a finishing pass adds them.
+  // With `part` set instead, each split writes its sums to part and counts
+  // itself in on tile_count[blockIdx.x]; the tile's last split adds them
+  // in split order and runs the epilogue itself (no finishing pass).
   int ksplit, kchunks;
+  float *part;
+  int *tile_count;
 };
 
 __device__ __forceinline__ int reflect_idx(int i, int n) {

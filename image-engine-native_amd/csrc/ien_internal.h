@@ -44,9 +44,12 @@ struct ien_ctx {
   // loads that write LDS directly (they cannot write a constant).
   uint16_t *zeros = nullptr;
   // Split-K partial sums of the convolution kernels (f32), allocated once
-  // with the context so that no launch allocates (graph capture).
+  // with the context so that no launch allocates (graph capture):
+  // splitk_floats of them, then SPLITK_TILES int tile counters (zero at
+  // open; a launch that counts its splits in returns each to zero).
   float *splitk = nullptr;
   size_t splitk_floats = 0;
+  static constexpr int SPLITK_TILES = 65536;
   // Branch streams (default priority, non-blocking) with their own split-K
   // workspaces: independent parts of a network run on them between fork()
   // and join(), so that they overlap on the GPU (and in a captured graph).

@@ -128,6 +128,11 @@ __global__ __launch_bounds__(256) void k_rows(RowsArgs a) {
 
   const int wm = BN == 128 ? (wave & 1) : wave;   // block of WM 32-row blocks
   const int wn = BN == 128 ? (wave >> 1) : 0;     // 64-column block
+  // The epilogue's bias for this lane's two columns, requested now so that
+  // its latency hides behind the products (padded to whole 32-column blocks).
+  float bias_r[2];
+#pragma unroll
+  for (int j = 0; j < 2; j++) bias_r[j] = a.bias[tn * BN + (wn * 2 + j) * 32 + l32];
   floatx16 acc[R::WM][2];
 #pragma unroll
   for (int i = 0; i < R::WM; i++)
@@ -243,7 +248,7 @@ __global__ __launch_bounds__(256) void k_rows(RowsArgs a) {
 #pragma unroll
       for (int j = 0; j < 2; j++) {
         const int col = (wn * 2 + j) * 32 + l32;
-        const float b = a.bias[tn * BN + col];  // padded to whole 32-column blocks
+        const float b = bias_r[j];
 #pragma unroll
         for (int i = 0; i < R::WM; i++)
 #pragma unroll

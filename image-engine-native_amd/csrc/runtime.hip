@@ -157,9 +157,14 @@ ien_status ien_open(int device, ien_ctx **out) {
   ctx->stream = ctx->own;
   e = hipMalloc(&ctx->zeros, 4096);
   if (e == hipSuccess) e = hipMemset(ctx->zeros, 0, 4096);
-  // 32 MiB of split-K partial sums.
+  // 32 MiB of split-K partial sums, then 256 KiB of tile counters.
   ctx->splitk_floats = (size_t)8 << 20;
-  if (e == hipSuccess) e = hipMalloc((void **)&ctx->splitk, ctx->splitk_floats * 4);
+  auto workspace = [&](float **p) {
+    hipError_t r = hipMalloc((void **)p, (ctx->splitk_floats + ien_ctx::SPLITK_TILES) * 4);
+    if (r == hipSuccess) r = hipMemset(*p + ctx->splitk_floats, 0, ien_ctx::SPLITK_TILES * 4);
+    return r;
+  };
+  if (e == hipSuccess) e = workspace(&ctx->splitk);
   if (e == hipSuccess) e = hipEventCreateWithFlags(&ctx->fork_ev, hipEventDisableTiming);
   if (e == hipSuccess) e = swin_static_setup(device);
   ctx->chain_tiles = ctx->cus;
@@ -170,8 +175,7 @@ ien_status ien_open(int device, ien_ctx **out) {
   for (int i = 0; i < ien_ctx::BRANCHES && e == hipSuccess; i++) {
     e = hipStreamCreateWithFlags(&ctx->branch[i], hipStreamNonBlocking);
     if (e == hipSuccess) e = hipEventCreateWithFlags(&ctx->join_ev[i], hipEventDisableTiming);
-    if (e == hipSuccess)
-      e = hipMalloc((void **)&ctx->branch_splitk[i], ctx->splitk_floats * 4);
+    if (e == hipSuccess) e = workspace(&ctx->branch_splitk[i]);
   }
   if (e != hipSuccess) {
     const std::string why = hipGetErrorString(e);

@@ -107,6 +107,22 @@ def test_conv3x3_large_grid(ctx, oracle):
     close(run_gpu(ctx, x, wt, b, pad=1), want_cpu(oracle, x, wt, b, pad=1))
 
 
+# A small map with a deep reduction (LaMa's FFC local convolution: 64 x 64,
+# 512 -> 128, reflect padding) runs in 4 splits of the channels whose
+# partial sums each tile's last split adds (no finishing pass): against the
+# oracle, plain and with ReLU onto an accumulated output, and bit for bit
+# the same over repeated launches (the sums are added in split order,
+# whichever split comes last).
+@pytest.mark.parametrize("act,acc", [(0, False), (1, True)])
+def test_split_k_counted_in(ctx, oracle, act, acc):
+    x, wt, b = case(21, 64, 64, 512, 128, 9)
+    init = (np.random.default_rng(22).standard_normal((64 * 64, 128)) * 0.5).astype(np.float16).astype(
+        np.float32) if acc else None
+    runs = [run_gpu(ctx, x, wt, b, pad=1, act=act, init=init) for _ in range(3)]
+    close(runs[0], want_cpu(oracle, x, wt, b, pad=1, act=act, init=None if init is None else init.copy()))
+    assert all(np.array_equal(r.view(np.uint32), runs[0].view(np.uint32)) for r in runs[1:])
+
+
 @pytest.mark.parametrize("c", [3, 4, 8, 16])
 def test_conv3x3_few_channels(ctx, oracle, c):
     x, wt, b = case(2, 11, 37, c, 64, 9)
