@@ -42,6 +42,7 @@
 // rows, which then stay in that XCD's L2.
 
 #include "conv_common.h"
+#include "lanes.h"
 
 namespace ien {
 
@@ -998,10 +999,77 @@ __global__ __launch_bounds__(256) void k_splitk_finish8(const float *__restrict_
   *(u32x4 *)yo = *(const u32x4 *)o;
 }
 
+// The same for outputs too few to fill the CUs (deep splits of small
+// maps): T lanes an 8-channel item, lane t adding splits t, t + T, ... in
+// order, then the group's sum (a fixed order, so repeated launches agree);
+// the group's first lane finishes the item.
+template <int T>
+__global__ __launch_bounds__(256) void k_splitk_finish8_lanes(const float *__restrict__ part,
+                                                              int ksplit, long rows, int pitch, int N,
+                                                              const float *__restrict__ bias,
+                                                              const float *__restrict__ slope, int act,
+                                                              int accumulate, uint16_t *y, long ys) {
+  const long i = ((long)blockIdx.x * 256 + threadIdx.x) / T;
+  const int t = threadIdx.x & (T - 1);
+  const int groups = N >> 3;
+  if (i >= rows * groups) return;  // (whole lane groups)
+  const long p = i / groups;
+  const int n = (int)(i - p * groups) * 8;
+  float4v s0 = {0.0f, 0.0f, 0.0f, 0.0f}, s1 = s0;
+  for (int z = t; z < ksplit; z += T) {
+    const float *q = part + ((long)z * rows + p) * pitch + n;
+    s0 += *(const float4v *)q;
+    s1 += *(const float4v *)(q + 4);
+  }
+  float v[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
+#pragma unroll
+  for (int e = 0; e < 8; e++) v[e] = group_sum<T>(v[e]);
+  if (t != 0) return;
+  const float4v b0 = *(const float4v *)(bias + n), b1 = *(const float4v *)(bias + n + 4);
+#pragma unroll
+  for (int e = 0; e < 4; e++) {
+    v[e] += b0[e];
+    v[4 + e] += b1[e];
+  }
+  uint16_t *yo = y + p * ys + n;
+  if (accumulate) {
+    uint16_t h[8];
+    *(u32x4 *)h = *(const u32x4 *)yo;
+#pragma unroll
+    for (int e = 0; e < 8; e++) v[e] += h2f(h[e]);
+  }
+  uint16_t o[8];
+  auto out = [&](auto actf) {
+#pragma unroll
+    for (int e = 0; e < 8; e++) o[e] = f2h(actf(v[e], e));
+  };
+  switch (act) {
+    case IEN_ACT_RELU: out([&](float x, int) { return act_c<IEN_ACT_RELU>(x, 0.0f); }); break;
+    case IEN_ACT_GELU: out([&](float x, int) { return act_c<IEN_ACT_GELU>(x, 0.0f); }); break;
+    case IEN_ACT_SIGMOID: out([&](float x, int) { return act_c<IEN_ACT_SIGMOID>(x, 0.0f); }); break;
+    case IEN_ACT_PRELU: out([&](float x, int e) { return act_c<IEN_ACT_PRELU>(x, slope[n + e]); }); break;
+    default: out([&](float x, int) { return x; }); break;
+  }
+  *(u32x4 *)yo = *(const u32x4 *)o;
+}
+
 ien_status splitk_finish(ien_ctx *ctx, int ksplit, long rows, int pitch, const ConvArgs &a) {
   if (!a.out_f32 && !a.out_nchw && a.N % 8 == 0 && pitch % 8 == 0 && a.ys % 8 == 0 &&
       (((uintptr_t)a.y) & 15) == 0) {
     const long items = rows * (a.N / 8);
+    // Fewer items than 64 Ki threads: up to 8 lanes an item (no more than
+    // the splits).
+    int lanes = 1;
+    while (lanes < 8 && 2 * lanes <= ksplit && items * lanes < 65536) lanes *= 2;
+    if (lanes > 1) {
+      auto k = lanes == 2 ? k_splitk_finish8_lanes<2> : lanes == 4 ? k_splitk_finish8_lanes<4>
+                                                                    : k_splitk_finish8_lanes<8>;
+      hipLaunchKernelGGL(k, dim3((unsigned)((items * lanes + 255) / 256)), dim3(256), 0, ctx->stream,
+                         (const float *)ctx->splitk, ksplit, rows, pitch, a.N, a.bias, a.slope, a.act,
+                         a.accumulate, (uint16_t *)a.y, (long)a.ys);
+      IEN_HIP(hipGetLastError());
+      return IEN_OK;
+    }
     hipLaunchKernelGGL(k_splitk_finish8, dim3((unsigned)((items + 255) / 256)), dim3(256), 0,
                        ctx->stream, (const float *)ctx->splitk, ksplit, rows, pitch, a.N, a.bias,
                        a.slope, a.act, a.accumulate, (uint16_t *)a.y, (long)a.ys);
