@@ -121,6 +121,19 @@ def scunet_names():
     return out
 
 
+def gathered_position_bias(rel, window, swin_layout):
+    """[heads][N][N] position bias gathered from a relative-position table,
+    the way both models' attention builds it: `rel` is [(2W - 1)^2][heads]
+    (Swin: birefnet-native swin.rs) or [heads][2W - 1][2W - 1] (scunet-native
+    swin.rs); entry (i, j) takes cell (yi - yj + W - 1, xi - xj + W - 1)."""
+    side, n = 2 * window - 1, window * window
+    i = np.arange(n)
+    y, x = i // window, i % window
+    cell = (y[:, None] - y[None, :] + window - 1) * side + (x[:, None] - x[None, :] + window - 1)
+    table = rel.T if swin_layout else rel.reshape(rel.shape[0], side * side)
+    return np.stack([table[h][cell] for h in range(table.shape[0])])
+
+
 def scunet_tensors(seed=WEIGHT_SEED, init="trunc_normal"):
     """name -> array for every SCUNet tensor.  init: "trunc_normal" (the
     configuration's std 0.02) or "fan" (N(0, 1/fan_in) weights, for parity
@@ -130,7 +143,12 @@ def scunet_tensors(seed=WEIGHT_SEED, init="trunc_normal"):
     for name, shape in scunet_names():
         last = name.rsplit(".", 1)[-1]
         is_norm = ".ln1." in name or ".ln2." in name
-        if init == "trunc_normal":
+        if last == "position_bias":
+            # A relative-position table [heads][15][15], gathered per window.
+            side = 2 * SCUNET_WINDOW - 1
+            rel = rng.standard_normal((shape[0], side, side)) * (0.02 if init == "trunc_normal" else 1.0)
+            v = gathered_position_bias(rel, SCUNET_WINDOW, swin_layout=False)
+        elif init == "trunc_normal":
             if is_norm:
                 v = np.ones(shape) if last == "weight" else np.zeros(shape)
             elif last == "bias":
@@ -317,8 +335,11 @@ def birefnet_tensors(seed=WEIGHT_SEED, window=BIREFNET_WINDOW, init="trunc_norma
                 else:
                     v = (1 + 0.1 * rng.standard_normal(shape)) if last == "weight" else 0.1 * rng.standard_normal(shape)
             elif name.endswith("position_bias"):
-                v = (np.clip(rng.standard_normal(shape), -2, 2) * 0.02 if init == "trunc_normal"
-                     else rng.standard_normal(shape))
+                # A relative-position table [(2W - 1)^2][heads], gathered per window.
+                rel_shape = ((2 * window - 1) ** 2, shape[0])
+                rel = (np.clip(rng.standard_normal(rel_shape), -2, 2) * 0.02 if init == "trunc_normal"
+                       else rng.standard_normal(rel_shape))
+                v = gathered_position_bias(rel, window, swin_layout=True)
             elif last == "bias":
                 v = np.zeros(shape) if init == "trunc_normal" else 0.05 * rng.standard_normal(shape)
             elif init == "trunc_normal" and not name.startswith("patch_embed"):

@@ -64,3 +64,34 @@ def test_swin_block(ctx, oracle, c, window, shift, masked, sizes):
         assert err.max() < 5e-2, (h, w, err.max())
         assert np.sqrt(np.mean(err ** 2)) < 6e-3, (h, w)
     blk.free()
+
+
+# Position biases gathered from a relative-position table, as both models'
+# weights hold them (every entry of a cell's offset the same value), at
+# windows 12, 7 and 8, shifted windows' region masks included.
+@pytest.mark.parametrize("c,window,shift,masked,size", [
+    (96, 12, 6, -100.0, (24, 30)),   # Swin-T stage 1 at window 12, shifted; windows past the edge
+    (32, 12, 0, -100.0, (24, 24)),
+    (96, 7, 3, -100.0, (14, 21)),
+    (256, 8, 4, -np.inf, (16, 24)),  # SCUNet body, shifted
+])
+def test_swin_block_relative_bias(ctx, oracle, c, window, shift, masked, size):
+    import torch
+    import ien
+
+    rng = np.random.default_rng(7 * c + window + shift)
+    wt = block_weights(rng, c, window)
+    heads, side = c // 32, 2 * window - 1
+    rel = (0.5 * rng.standard_normal((side * side, heads))).astype(np.float32)
+    wt["position"] = ien.position_bias(rel, heads, window, ien.POS_SWIN)
+    blk = ien.Swin(ctx, c, window, shift, masked, wt)
+    h, w = size
+    x = rng.standard_normal((h, w, c)).astype(np.float16)
+    md = torch.from_numpy(x.reshape(h * w, c)).cuda()
+    blk.run(md, c, h, w)
+    torch.cuda.synchronize()
+    got = md.float().cpu().numpy().reshape(h, w, c)
+    want = oracle_block(oracle, x.astype(np.float32), window, shift, masked, wt)
+    err = np.abs(got - want)
+    assert err.max() < 5e-2 and np.sqrt(np.mean(err ** 2)) < 6e-3, (err.max(), np.sqrt(np.mean(err ** 2)))
+    blk.free()
