@@ -341,6 +341,34 @@ def test_rows(ctx, oracle, m, k, n):
     close(out.float().cpu().numpy(), want)
 
 
+# A deep product with a small output (64 rows, 4096 deep, 64 wide): one tile
+# in 8 splits of the reduction, whose finishing pass takes 8 lanes an item
+# (strided splits, then a fixed group sum): against the oracle with ReLU
+# onto an accumulated output, and bit for bit the same over repeats.
+def test_deep_split_small_output(ctx, oracle):
+    import torch
+    import ien
+
+    rng = np.random.default_rng(31)
+    m, k, n = 64, 4096, 64
+    a = f16(rng.standard_normal((m, k)))
+    wt = f16(rng.standard_normal((k, n)) / np.sqrt(k))
+    b = rng.standard_normal(n).astype(np.float32)
+    init = f16(rng.standard_normal((m, n)))
+    want = oracle.multiply_rows(a, wt, b, act=oracle.ACT_RELU, out=init.copy(), accumulate=True)
+    at = torch.from_numpy(a).half().cuda()
+    mat = ien.Matrix(ctx, wt, b)
+    runs = []
+    for _ in range(3):
+        out = torch.from_numpy(init).half().cuda()
+        ien.multiply(ctx, ien.rows_input(at, k), 0, m, mat, out, n, act=ien.ACT_RELU, accumulate=True)
+        torch.cuda.synchronize()
+        runs.append(out.float().cpu().numpy())
+    mat.free()
+    close(runs[0], want)
+    assert all(np.array_equal(r, runs[0]) for r in runs[1:])
+
+
 # Row products with enough tiles for the pipelined row kernel: 128 x 64
 # tiles (N <= 64), 64 x 128 tiles (wider N) and, with K at least 512 deep
 # and few tiles, split-K into the finishing pass (the last three), K a
