@@ -194,6 +194,14 @@ struct RowsPlanes {
   uint16_t *y = nullptr, *y2 = nullptr;
   int ys = 0, ys2 = 0, n1 = 0;
   int accumulate = 0;
+  // 2 x 2 regroupings, one plane each way (0: none).  gather_w2: row r is
+  // the 2 x 2 pixel group (2 (r / gather_w2) + dy, 2 (r % gather_w2) + dx)
+  // of x, a map 2 gather_w2 wide with pixels xs apart, channels in blocks
+  // of k / 4 by 2 dy + dx (ien_gather_2x2's row-major order).  scatter_w:
+  // rows are the pixels of a map scatter_w wide, and column block q of n / 4
+  // goes to pixel (2 (r / scatter_w) + q / 2, 2 (r % scatter_w) + q % 2) of
+  // y, a map 2 scatter_w wide with pixels ys apart (ien_scatter_2x2).
+  int gather_w2 = 0, scatter_w = 0;
 };
 ien_status launch_rows_planes(ien_ctx *ctx, const RowsPlanes &p);
 

@@ -49,6 +49,13 @@ struct RowsArgs {
   int xs2, k1;
   uint16_t *y2;        // columns n1 .. N (n1 = N: y only), rows ys2 apart
   int ys2, n1;
+  // 2 x 2 regroupings (0: none).  g2w: row r is the 2 x 2 group of pixels
+  // (2 (r / g2w) + dy, 2 (r % g2w) + dx) of a map 2 g2w wide (pixels xs
+  // apart), channel block q = 2 dy + dx of K / 4 channels each.  s2w: the
+  // rows are the pixels of a map s2w wide; column block q of N / 4 goes to
+  // pixel (2 (r / s2w) + q / 2, 2 (r % s2w) + q % 2) of a map 2 s2w wide
+  // (pixels ys apart).
+  int g2w, s2w;
   int act, accumulate;
   int tiles_n, tiles;
   // Split-K (gridDim.y splits of kchunks chunks): raw f32 sums of split z
@@ -82,7 +89,9 @@ __device__ __forceinline__ int swz(int r, int g) {
   return g ^ ((SLOTS == 8 ? r : r >> 1) & (SLOTS - 1));
 }
 
-template <int BM, int BN, int KC>
+// MODE 0: plain rows; 1: 2 x 2 gathered rows (g2w); 2: rows scattered over
+// 2 x 2 output pixels (s2w).
+template <int BM, int BN, int KC, int MODE>
 __global__ __launch_bounds__(256) void k_rows(RowsArgs a) {
   using R = RowsCfg<BM, BN, KC>;
   static_assert(BM == 128 || BN == 128, "64-row tiles are 128 columns wide");
@@ -93,11 +102,21 @@ __global__ __launch_bounds__(256) void k_rows(RowsArgs a) {
   const int tm = t / a.tiles_n, tn = t - tm * a.tiles_n;
   const int m0 = tm * R::BM;
   const unsigned l0 = lds_addr(lds);
-  const int4v xr = buffer_rsrc(a.x, (long)a.M * a.xs * 2);
+  const int4v xr = buffer_rsrc(a.x, (long)a.M * (MODE == 1 ? 4 : 1) * a.xs * 2);
   const int4v xr2 = buffer_rsrc(a.x2, (long)a.M * a.xs2 * 2);
   const int4v wr = buffer_rsrc(a.wp, (long)a.NB * a.KB * 1024);
   const int c_begin = blockIdx.y * a.kchunks;
   const int chunks = min(a.K / KC - c_begin, a.kchunks);  // this split's chunks
+  // Gathered rows: the pixel of each A load's row at channel block 0.
+  int gpix[R::A_LOADS];
+  if constexpr (MODE == 1) {
+#pragma unroll
+    for (int i = 0; i < R::A_LOADS; i++) {
+      const int m = m0 + (wave + 4 * i) * (1024 / (KC * 2)) + lane / R::SLOTS;
+      const int yy = m / a.g2w;
+      gpix[i] = 4 * yy * a.g2w + 2 * (m - yy * a.g2w);
+    }
+  }
 
   // Chunk c into stage s: A rows m0 .. m0 + BM - 1, channels c KC .. + KC - 1;
   // B fragments of column blocks tn BN / 32 .. and k blocks c KC / 16 ...
@@ -113,8 +132,12 @@ __global__ __launch_bounds__(256) void k_rows(RowsArgs a) {
       const int row = d * (1024 / (KC * 2)) + lane / R::SLOTS;
       const int slot = lane % R::SLOTS;
       const int g = swz<R::SLOTS>(row, slot);      // the chunk this slot holds
-      dma_lds(sr, __builtin_amdgcn_readfirstlane(base + d * 1024),
-               ((m0 + row) * rs + c0 + 8 * g) * 2);
+      int off = ((m0 + row) * rs + c0 + 8 * g) * 2;
+      if constexpr (MODE == 1) {
+        const int cin = a.K >> 2, q = c0 / cin;
+        off = ((gpix[i] + (q >> 1) * 2 * a.g2w + (q & 1)) * rs + c0 - q * cin + 8 * g) * 2;
+      }
+      dma_lds(sr, __builtin_amdgcn_readfirstlane(base + d * 1024), off);
     }
 #pragma unroll
     for (int i = 0; i < R::B_LOADS; i++) {
@@ -206,6 +229,11 @@ __global__ __launch_bounds__(256) void k_rows(RowsArgs a) {
   // Output item (row, col .. col + 7) in y or, past column n1, in y2
   // (n1 is a multiple of 8).
   auto out_at = [&](int row, int col) {
+    if constexpr (MODE == 2) {
+      const int cout = a.N >> 2, q = col / cout, y = row / a.s2w;
+      const long pixel = (long)(2 * y + (q >> 1)) * (2 * a.s2w) + 2 * (row - y * a.s2w) + (q & 1);
+      return a.y + pixel * a.ys + (col - q * cout);
+    }
     return col < a.n1 ? a.y + (long)row * a.ys + col : a.y2 + (long)row * a.ys2 + (col - a.n1);
   };
   u32x4 old[R::ITEMS];
@@ -277,14 +305,16 @@ __global__ __launch_bounds__(256) void k_rows(RowsArgs a) {
 // least 256 deep.  (Splitting products that already fill most CUs, such as
 // SCUNet's 1024-deep fc2 over 192 tiles, cost more in partial sums and the
 // finishing pass than it gained.)
-template <int BM, int BN, int KC>
+template <int BM, int BN, int KC, int MODE = 0>
 ien_status launch(ien_ctx *ctx, RowsArgs a, const ConvArgs &c) {
   a.tiles_n = (a.N + BN - 1) / BN;
   a.tiles = (a.M + BM - 1) / BM * a.tiles_n;
   const int chunks = a.K / KC;
   a.pitch = a.tiles_n * BN;
   int ksplit = 1;
-  const bool planes = a.k1 < a.K || a.n1 < a.N;  // (the finishing pass writes one map)
+  // (The finishing pass writes one map, row by row; gathered rows are
+  // split like any others.)
+  const bool planes = a.k1 < a.K || a.n1 < a.N || MODE == 2;
   if (!planes && chunks >= 16 && (4 * a.tiles <= ctx->cus || (a.K >= 1536 && a.tiles < ctx->cus))) {
     ksplit = std::min(chunks / 8, (2 * ctx->cus + a.tiles - 1) / a.tiles);
     while (ksplit > 1 && (size_t)ksplit * a.M * a.pitch > ctx->splitk_floats) ksplit--;
@@ -292,7 +322,7 @@ ien_status launch(ien_ctx *ctx, RowsArgs a, const ConvArgs &c) {
   a.kchunks = (chunks + ksplit - 1) / ksplit;
   ksplit = (chunks + a.kchunks - 1) / a.kchunks;
   a.part = ksplit > 1 ? ctx->splitk : nullptr;
-  hipLaunchKernelGGL((k_rows<BM, BN, KC>), dim3((unsigned)a.tiles, (unsigned)ksplit), dim3(256), 0,
+  hipLaunchKernelGGL((k_rows<BM, BN, KC, MODE>), dim3((unsigned)a.tiles, (unsigned)ksplit), dim3(256), 0,
                      ctx->stream, a);
   IEN_HIP(hipGetLastError());
   if (ksplit == 1) return IEN_OK;
@@ -353,13 +383,25 @@ ien_status launch_rows_planes(ien_ctx *ctx, const RowsPlanes &p) {
   IEN_CHECK(K % 32 == 0 && p.k1 % 32 == 0 && p.k1 > 0 && p.k1 <= K && N % 8 == 0 &&
                 p.n1 % 8 == 0 && p.n1 > 0 && p.n1 <= N,
             IEN_ERR_INPUT, "rows planes: k %d split at %d, n %d split at %d", K, p.k1, N, p.n1);
+  const bool gather = p.gather_w2 > 0, scatter = p.scatter_w > 0;
+  IEN_CHECK(p.gather_w2 >= 0 && p.scatter_w >= 0 &&
+                (!gather || (p.k1 == K && K % 128 == 0 && p.rows % p.gather_w2 == 0)) &&
+                (!scatter || (p.n1 == N && N % 32 == 0 && p.rows % p.scatter_w == 0 && !p.accumulate)),
+            IEN_ERR_INPUT, "rows planes: 2 x 2 regrouping of k %d / n %d over %ld rows", K, N, p.rows);
+  // A gathered row reads K / 4 channels of each pixel; a scattered one
+  // writes N / 4.
+  const int kx = gather ? K / 4 : p.k1, ny = scatter ? N / 4 : p.n1;
+  const long xrows = gather ? 4 * p.rows : p.rows, yrows = scatter ? 4 * p.rows : p.rows;
   const uintptr_t ptrs = (uintptr_t)p.x | (uintptr_t)p.x2 | (uintptr_t)p.y | (uintptr_t)p.y2;
   IEN_CHECK((ptrs & 15) == 0 && p.xs % 8 == 0 && p.xs2 % 8 == 0 && p.ys % 8 == 0 &&
-                p.ys2 % 8 == 0 && p.xs >= p.k1 && p.xs2 >= K - p.k1 && p.ys >= p.n1 &&
+                p.ys2 % 8 == 0 && p.xs >= kx && p.xs2 >= K - p.k1 && p.ys >= ny &&
                 p.ys2 >= N - p.n1,
             IEN_ERR_INPUT, "rows planes: alignment or strides");
-  for (long stride : {(long)p.xs, (long)p.xs2, (long)p.ys, (long)p.ys2})
-    IEN_CHECK(stride * (p.rows + 128) * 2 <= 0x7fff0000L, IEN_ERR_INPUT, "rows planes over 2 GiB");
+  IEN_CHECK((long)p.xs * (xrows + 512) * 2 <= 0x7fff0000L &&
+                (long)p.xs2 * (p.rows + 128) * 2 <= 0x7fff0000L &&
+                (long)p.ys * (yrows + 512) * 2 <= 0x7fff0000L &&
+                (long)p.ys2 * (p.rows + 128) * 2 <= 0x7fff0000L,
+            IEN_ERR_INPUT, "rows planes over 2 GiB");
   RowsArgs a{};
   a.x = p.x;
   a.xs = p.xs;
@@ -378,9 +420,21 @@ ien_status launch_rows_planes(ien_ctx *ctx, const RowsPlanes &p) {
   a.y2 = p.y2;
   a.ys2 = p.ys2;
   a.n1 = p.n1;
+  a.g2w = p.gather_w2;
+  a.s2w = p.scatter_w;
   a.act = IEN_ACT_NONE;
   a.accumulate = p.accumulate;
+  // The output as the split-K finishing pass reads it (one map: no planes
+  // split-K).
   ConvArgs c{};
+  c.N = N;
+  c.bias = w->d_bias;
+  c.y = p.y;
+  c.ys = p.ys;
+  c.act = IEN_ACT_NONE;
+  c.accumulate = p.accumulate;
+  if (gather) return launch<64, 128, 32, 1>(ctx, a, c);
+  if (scatter) return launch<64, 128, 32, 2>(ctx, a, c);
   if (N > 64 || tiles_of(a.M, 128, a.N) < 128) return launch<64, 128, 32>(ctx, a, c);
   return launch<128, 64, 32>(ctx, a, c);
 }

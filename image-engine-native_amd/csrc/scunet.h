@@ -24,7 +24,7 @@ struct Scunet {
   ien_matrix *head = nullptr, *tail = nullptr, *halve[3] = {}, *dbl[3] = {};
   ScunetBlock down[3][4], body[4], up[3][4];
   size_t pixels = 0;  // padded pixels the maps hold
-  uint16_t *img = nullptr, *x = nullptr, *y = nullptr, *t = nullptr, *rows = nullptr,
+  uint16_t *img = nullptr, *x = nullptr, *y = nullptr, *t = nullptr,
            *skip[3] = {}, *out16 = nullptr;
   float *d_in = nullptr, *d_out = nullptr;  // host-API staging
   size_t staged = 0;                        // pixels of the staging buffers

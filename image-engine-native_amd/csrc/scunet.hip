@@ -2,7 +2,8 @@
 // network.rs:113-354): f16 NHWC maps, the block's 3x3 convolutions and the
 // head and tail through the implicit-GEMM kernels, 1x1 products over pixel
 // rows, the Swin half through ien_swin, the 2x2 halving and doubling
-// convolutions as gathers / scatters around row products.  One event is
+// convolutions as row products that gather / scatter 2 x 2 pixel groups
+// themselves.  One event is
 // recorded after each of the 28 blocks for progress reports.
 
 #include <algorithm>
@@ -16,20 +17,6 @@ namespace ien {
 namespace {
 
 constexpr int DIM = 64, BLOCKS = 4, WINDOW = 8, MULTIPLE = 64;
-
-ien_status rows_product(ien_ctx *ctx, const uint16_t *in, size_t k, size_t rows,
-                        const ien_matrix *m, uint16_t *out, size_t stride, int accumulate) {
-  ien_input x{};
-  x.kind = IEN_INPUT_ROWS;
-  x.data = in;
-  x.stride = k;
-  ien_output o{};
-  o.data = out;
-  o.stride = stride;
-  o.layout = IEN_LAYOUT_NHWC;
-  o.type = IEN_OUT_F16;
-  return ien_multiply_ex(ctx, &x, 0, rows, m, &o, IEN_ACT_NONE, nullptr, accumulate);
-}
 
 // A 3x3 zero-padded convolution of an h x w f16 NHWC map.
 ien_status conv3(ien_ctx *ctx, const uint16_t *x, int h, int w, int c, long xs,
@@ -120,7 +107,7 @@ void free_block(ScunetBlock &b) {
 }
 
 void free_maps(Scunet &s) {
-  for (uint16_t **p : {&s.img, &s.x, &s.y, &s.t, &s.rows, &s.skip[0], &s.skip[1], &s.skip[2],
+  for (uint16_t **p : {&s.img, &s.x, &s.y, &s.t, &s.skip[0], &s.skip[1], &s.skip[2],
                        &s.out16}) {
     (void)hipFree(*p);
     *p = nullptr;
@@ -254,8 +241,7 @@ void scunet_padded(size_t width, size_t height, size_t *pw, size_t *ph) {
 
 // The maps grow on demand (never shrink): at the padded size P pixels, x and
 // y hold P x 64 halves (every level's c-channel map has at most that), t
-// P x 32, rows P x 64 (a level's 2 x 2 gather, or the doubling product), the
-// skips P/4 x 128, P/16 x 256, P/64 x 512.
+// P x 32, the skips P/4 x 128, P/16 x 256, P/64 x 512.
 ien_status scunet_reserve(Scunet *s, size_t pw, size_t ph) {
   // Each level's blocks: down l at 1 / 2^l, the body at 1 / 8, up l at
   // 1 / 2^(2 - l).
@@ -282,7 +268,6 @@ ien_status scunet_reserve(Scunet *s, size_t pw, size_t ph) {
   if (e == hipSuccess) e = alloc(&s->x, P * DIM);
   if (e == hipSuccess) e = alloc(&s->y, P * DIM);
   if (e == hipSuccess) e = alloc(&s->t, P * DIM / 2);
-  if (e == hipSuccess) e = alloc(&s->rows, P * DIM);
   for (int l = 0; l < 3 && e == hipSuccess; l++) e = alloc(&s->skip[l], (P >> (2 * l + 2)) * (128 << l));
   if (e == hipSuccess) e = alloc(&s->out16, P * 4);
   if (e != hipSuccess) {
@@ -308,32 +293,65 @@ ien_status scunet_enqueue(Scunet *s, const float *d_image, size_t width, size_t 
   if ((st = conv3(ctx, s->img, h, w, 4, 8, s->head, s->x, DIM, IEN_ACT_NONE, 0)) != IEN_OK) return st;
   for (int l = 0; l < 3; l++) {
     if ((st = run_level(*s, s->down[l], h, w, c, steps, &step)) != IEN_OK) return st;
-    // network.rs:403-437 halved, kept as the skip of the level up.
-    if ((st = ien_gather_2x2(ctx, s->x, h, w, c, c, IEN_ORDER_ROW_MAJOR, s->rows)) != IEN_OK)
-      return st;
+    // network.rs:403-437 halved, kept as the skip of the level up: a
+    // product over the map's 2 x 2 pixel groups.
     const size_t q = (size_t)(h / 2) * (w / 2);
-    if ((st = rows_product(ctx, s->rows, 4 * c, q, s->halve[l], s->skip[l], 2 * c, 0)) != IEN_OK)
-      return st;
+    {
+      RowsPlanes p;
+      p.x = p.x2 = s->x;
+      p.xs = p.xs2 = c;
+      p.k1 = 4 * c;
+      p.rows = (long)q;
+      p.w = s->halve[l];
+      p.y = p.y2 = s->skip[l];
+      p.ys = p.ys2 = 2 * c;
+      p.n1 = 2 * c;
+      p.gather_w2 = w / 2;
+      if ((st = launch_rows_planes(ctx, p)) != IEN_OK) return st;
+    }
     h /= 2;
     w /= 2;
     c *= 2;
     IEN_HIP(hipMemcpyAsync(s->x, s->skip[l], q * c * 2, hipMemcpyDeviceToDevice, ctx->stream));
   }
   if ((st = run_level(*s, s->body, h, w, c, steps, &step)) != IEN_OK) return st;
+  // The doubling writes its scattered output into y, which then takes the
+  // part of x (y is free between levels); swapped back after the enqueue.
+  bool swapped = false;
+  auto unswap = [&]() {
+    if (swapped) std::swap(s->x, s->y);
+    swapped = false;
+  };
   for (int l = 0; l < 3; l++) {
     const size_t pixels = (size_t)h * w;
-    if ((st = ien_add(ctx, s->x, s->skip[2 - l], pixels * c)) != IEN_OK) return st;
-    // network.rs:439-478 doubled.
-    if ((st = rows_product(ctx, s->x, c, pixels, s->dbl[l], s->rows, 2 * c, 0)) != IEN_OK) return st;
-    if ((st = ien_scatter_2x2(ctx, s->rows, 2 * c, h, w, c / 2, s->x, c / 2)) != IEN_OK) return st;
+    if ((st = ien_add(ctx, s->x, s->skip[2 - l], pixels * c)) != IEN_OK) return unswap(), st;
+    // network.rs:439-478 doubled: each pixel's product scattered over its 2
+    // x 2 output pixels.
+    {
+      RowsPlanes p;
+      p.x = p.x2 = s->x;
+      p.xs = p.xs2 = c;
+      p.k1 = c;
+      p.rows = (long)pixels;
+      p.w = s->dbl[l];
+      p.y = p.y2 = s->y;
+      p.ys = p.ys2 = c / 2;
+      p.n1 = 2 * c;
+      p.scatter_w = w;
+      if ((st = launch_rows_planes(ctx, p)) != IEN_OK) return unswap(), st;
+    }
+    std::swap(s->x, s->y);
+    swapped = !swapped;
     h *= 2;
     w *= 2;
     c /= 2;
-    if ((st = run_level(*s, s->up[l], h, w, c, steps, &step)) != IEN_OK) return st;
+    if ((st = run_level(*s, s->up[l], h, w, c, steps, &step)) != IEN_OK) return unswap(), st;
   }
-  if ((st = conv3(ctx, s->img, h, w, 4, 8, s->head, s->x, DIM, IEN_ACT_NONE, 1)) != IEN_OK) return st;
-  if ((st = conv3(ctx, s->x, h, w, DIM, DIM, s->tail, s->out16, 4, IEN_ACT_NONE, 0)) != IEN_OK)
-    return st;
+  if ((st = conv3(ctx, s->img, h, w, 4, 8, s->head, s->x, DIM, IEN_ACT_NONE, 1)) != IEN_OK)
+    return unswap(), st;
+  st = conv3(ctx, s->x, h, w, DIM, DIM, s->tail, s->out16, 4, IEN_ACT_NONE, 0);
+  unswap();
+  if (st != IEN_OK) return st;
   return ien_crop(ctx, s->out16, pw, 4, width, height, 3, d_out);
 }
 
