@@ -202,6 +202,8 @@ struct RowsPlanes {
   // goes to pixel (2 (r / scatter_w) + q / 2, 2 (r % scatter_w) + q % 2) of
   // y, a map 2 scatter_w wide with pixels ys apart (ien_scatter_2x2).
   int gather_w2 = 0, scatter_w = 0;
+  // With gather_w2: a second copy of the output rows (ys apart), or null.
+  uint16_t *ydup = nullptr;
 };
 ien_status launch_rows_planes(ien_ctx *ctx, const RowsPlanes &p);
 

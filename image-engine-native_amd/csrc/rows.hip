@@ -56,6 +56,7 @@ struct RowsArgs {
   // pixel (2 (r / s2w) + q / 2, 2 (r % s2w) + q % 2) of a map 2 s2w wide
   // (pixels ys apart).
   int g2w, s2w;
+  uint16_t *ydup;  // gathered rows: a second copy of the output (rows ys apart), or null
   int act, accumulate;
   int tiles_n, tiles;
   // Split-K (gridDim.y splits of kchunks chunks): raw f32 sums of split z
@@ -265,6 +266,8 @@ __global__ __launch_bounds__(256) void k_rows(RowsArgs a) {
 #pragma unroll
       for (int k = 0; k < 8; k++) o[k] = f2h(actf(v8[k], col + k));
       __builtin_memcpy(out_at(m0 + row, col), o, 16);
+      if constexpr (MODE == 1)
+        if (a.ydup) __builtin_memcpy(a.ydup + (long)(m0 + row) * a.ys + col, o, 16);
     }
   };
   // acc + bias as f32 rows in LDS, 64 rows at a time.
@@ -326,7 +329,12 @@ ien_status launch(ien_ctx *ctx, RowsArgs a, const ConvArgs &c) {
                      ctx->stream, a);
   IEN_HIP(hipGetLastError());
   if (ksplit == 1) return IEN_OK;
-  return splitk_finish(ctx, ksplit, a.M, a.pitch, c);
+  const ien_status st = splitk_finish(ctx, ksplit, a.M, a.pitch, c);
+  if (st != IEN_OK || !a.ydup) return st;
+  // The finishing pass writes one map: the second copy follows it.
+  IEN_HIP(hipMemcpy2DAsync(a.ydup, (size_t)a.ys * 2, a.y, (size_t)a.ys * 2, (size_t)a.N * 2,
+                           (size_t)a.M, hipMemcpyDeviceToDevice, ctx->stream));
+  return IEN_OK;
 }
 
 }  // namespace
@@ -386,7 +394,8 @@ ien_status launch_rows_planes(ien_ctx *ctx, const RowsPlanes &p) {
   const bool gather = p.gather_w2 > 0, scatter = p.scatter_w > 0;
   IEN_CHECK(p.gather_w2 >= 0 && p.scatter_w >= 0 &&
                 (!gather || (p.k1 == K && K % 128 == 0 && p.rows % p.gather_w2 == 0)) &&
-                (!scatter || (p.n1 == N && N % 32 == 0 && p.rows % p.scatter_w == 0 && !p.accumulate)),
+                (!scatter || (p.n1 == N && N % 32 == 0 && p.rows % p.scatter_w == 0 && !p.accumulate)) &&
+                (!p.ydup || (gather && p.n1 == N && ((uintptr_t)p.ydup & 15) == 0 && !p.accumulate)),
             IEN_ERR_INPUT, "rows planes: 2 x 2 regrouping of k %d / n %d over %ld rows", K, N, p.rows);
   // A gathered row reads K / 4 channels of each pixel; a scattered one
   // writes N / 4.
@@ -422,6 +431,7 @@ ien_status launch_rows_planes(ien_ctx *ctx, const RowsPlanes &p) {
   a.n1 = p.n1;
   a.g2w = p.gather_w2;
   a.s2w = p.scatter_w;
+  a.ydup = p.ydup;
   a.act = IEN_ACT_NONE;
   a.accumulate = p.accumulate;
   // The output as the split-K finishing pass reads it (one map: no planes

@@ -291,8 +291,16 @@ ien_status scunet_enqueue(Scunet *s, const float *d_image, size_t width, size_t 
   int h = (int)ph, w = (int)pw, c = DIM, step = 0;
   // The head (no bias); computed again at the end as the skip into the tail.
   if ((st = conv3(ctx, s->img, h, w, 4, 8, s->head, s->x, DIM, IEN_ACT_NONE, 0)) != IEN_OK) return st;
+  // The halving writes the skip and a working copy in y, which then takes
+  // the part of x (y is free between levels); the doubling writes its
+  // scattered output into y likewise.  Swapped back after the enqueue.
+  bool swapped = false;
+  auto unswap = [&]() {
+    if (swapped) std::swap(s->x, s->y);
+    swapped = false;
+  };
   for (int l = 0; l < 3; l++) {
-    if ((st = run_level(*s, s->down[l], h, w, c, steps, &step)) != IEN_OK) return st;
+    if ((st = run_level(*s, s->down[l], h, w, c, steps, &step)) != IEN_OK) return unswap(), st;
     // network.rs:403-437 halved, kept as the skip of the level up: a
     // product over the map's 2 x 2 pixel groups.
     const size_t q = (size_t)(h / 2) * (w / 2);
@@ -307,21 +315,16 @@ ien_status scunet_enqueue(Scunet *s, const float *d_image, size_t width, size_t 
       p.ys = p.ys2 = 2 * c;
       p.n1 = 2 * c;
       p.gather_w2 = w / 2;
-      if ((st = launch_rows_planes(ctx, p)) != IEN_OK) return st;
+      p.ydup = s->y;
+      if ((st = launch_rows_planes(ctx, p)) != IEN_OK) return unswap(), st;
     }
+    std::swap(s->x, s->y);
+    swapped = !swapped;
     h /= 2;
     w /= 2;
     c *= 2;
-    IEN_HIP(hipMemcpyAsync(s->x, s->skip[l], q * c * 2, hipMemcpyDeviceToDevice, ctx->stream));
   }
-  if ((st = run_level(*s, s->body, h, w, c, steps, &step)) != IEN_OK) return st;
-  // The doubling writes its scattered output into y, which then takes the
-  // part of x (y is free between levels); swapped back after the enqueue.
-  bool swapped = false;
-  auto unswap = [&]() {
-    if (swapped) std::swap(s->x, s->y);
-    swapped = false;
-  };
+  if ((st = run_level(*s, s->body, h, w, c, steps, &step)) != IEN_OK) return unswap(), st;
   for (int l = 0; l < 3; l++) {
     const size_t pixels = (size_t)h * w;
     if ((st = ien_add(ctx, s->x, s->skip[2 - l], pixels * c)) != IEN_OK) return unswap(), st;
