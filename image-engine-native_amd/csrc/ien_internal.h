@@ -204,6 +204,9 @@ struct RowsPlanes {
   int gather_w2 = 0, scatter_w = 0;
   // With gather_w2: a second copy of the output rows (ys apart), or null.
   uint16_t *ydup = nullptr;
+  // A map (rows ys apart) added to the f16 result, rounded again: the
+  // product followed by ien_add in one pass; or null.
+  const uint16_t *add = nullptr;
 };
 ien_status launch_rows_planes(ien_ctx *ctx, const RowsPlanes &p);
 

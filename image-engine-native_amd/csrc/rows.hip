@@ -57,6 +57,7 @@ struct RowsArgs {
   // (pixels ys apart).
   int g2w, s2w;
   uint16_t *ydup;  // gathered rows: a second copy of the output (rows ys apart), or null
+  const uint16_t *add2;  // MODE 3: a map added to the rounded result (rows ys apart)
   int act, accumulate;
   int tiles_n, tiles;
   // Split-K (gridDim.y splits of kchunks chunks): raw f32 sums of split z
@@ -91,7 +92,8 @@ __device__ __forceinline__ int swz(int r, int g) {
 }
 
 // MODE 0: plain rows; 1: 2 x 2 gathered rows (g2w); 2: rows scattered over
-// 2 x 2 output pixels (s2w).
+// 2 x 2 output pixels (s2w); 3: plain rows whose f16 result gets add2 added
+// and is rounded again (a separate map addition after the product).
 template <int BM, int BN, int KC, int MODE>
 __global__ __launch_bounds__(256) void k_rows(RowsArgs a) {
   using R = RowsCfg<BM, BN, KC>;
@@ -237,7 +239,15 @@ __global__ __launch_bounds__(256) void k_rows(RowsArgs a) {
     }
     return col < a.n1 ? a.y + (long)row * a.ys + col : a.y2 + (long)row * a.ys2 + (col - a.n1);
   };
-  u32x4 old[R::ITEMS];
+  u32x4 old[R::ITEMS], old2[MODE == 3 ? R::ITEMS : 1];
+  if constexpr (MODE == 3) {
+#pragma unroll
+    for (int e = 0; e < R::ITEMS; e++) {
+      const int v = tid + 256 * e, row = v / (BN / 8), col = tn * BN + 8 * (v % (BN / 8));
+      const bool ok = m0 + row < a.M && col < a.N;
+      old2[e] = *(const u32x4 *)(a.add2 + (ok ? (long)(m0 + row) * a.ys + col : 0));
+    }
+  }
   if (a.accumulate) {
 #pragma unroll
     for (int e = 0; e < R::ITEMS; e++) {
@@ -265,6 +275,12 @@ __global__ __launch_bounds__(256) void k_rows(RowsArgs a) {
       uint16_t o[8];
 #pragma unroll
       for (int k = 0; k < 8; k++) o[k] = f2h(actf(v8[k], col + k));
+      if constexpr (MODE == 3) {
+        uint16_t h2[8];
+        __builtin_memcpy(h2, &old2[e], 16);
+#pragma unroll
+        for (int k = 0; k < 8; k++) o[k] = f2h(h2f(o[k]) + h2f(h2[k]));
+      }
       __builtin_memcpy(out_at(m0 + row, col), o, 16);
       if constexpr (MODE == 1)
         if (a.ydup) __builtin_memcpy(a.ydup + (long)(m0 + row) * a.ys + col, o, 16);
@@ -317,7 +333,7 @@ ien_status launch(ien_ctx *ctx, RowsArgs a, const ConvArgs &c) {
   int ksplit = 1;
   // (The finishing pass writes one map, row by row; gathered rows are
   // split like any others.)
-  const bool planes = a.k1 < a.K || a.n1 < a.N || MODE == 2;
+  const bool planes = a.k1 < a.K || a.n1 < a.N || MODE == 2 || MODE == 3;
   if (!planes && chunks >= 16 && (4 * a.tiles <= ctx->cus || (a.K >= 1536 && a.tiles < ctx->cus))) {
     ksplit = std::min(chunks / 8, (2 * ctx->cus + a.tiles - 1) / a.tiles);
     while (ksplit > 1 && (size_t)ksplit * a.M * a.pitch > ctx->splitk_floats) ksplit--;
@@ -395,7 +411,8 @@ ien_status launch_rows_planes(ien_ctx *ctx, const RowsPlanes &p) {
   IEN_CHECK(p.gather_w2 >= 0 && p.scatter_w >= 0 &&
                 (!gather || (p.k1 == K && K % 128 == 0 && p.rows % p.gather_w2 == 0)) &&
                 (!scatter || (p.n1 == N && N % 32 == 0 && p.rows % p.scatter_w == 0 && !p.accumulate)) &&
-                (!p.ydup || (gather && p.n1 == N && ((uintptr_t)p.ydup & 15) == 0 && !p.accumulate)),
+                (!p.ydup || (gather && p.n1 == N && ((uintptr_t)p.ydup & 15) == 0 && !p.accumulate)) &&
+                (!p.add || (!gather && !scatter && p.n1 == N && ((uintptr_t)p.add & 15) == 0)),
             IEN_ERR_INPUT, "rows planes: 2 x 2 regrouping of k %d / n %d over %ld rows", K, N, p.rows);
   // A gathered row reads K / 4 channels of each pixel; a scattered one
   // writes N / 4.
@@ -432,6 +449,7 @@ ien_status launch_rows_planes(ien_ctx *ctx, const RowsPlanes &p) {
   a.g2w = p.gather_w2;
   a.s2w = p.scatter_w;
   a.ydup = p.ydup;
+  a.add2 = p.add;
   a.act = IEN_ACT_NONE;
   a.accumulate = p.accumulate;
   // The output as the split-K finishing pass reads it (one map: no planes
@@ -444,6 +462,7 @@ ien_status launch_rows_planes(ien_ctx *ctx, const RowsPlanes &p) {
   c.act = IEN_ACT_NONE;
   c.accumulate = p.accumulate;
   if (gather) return launch<64, 128, 32, 1>(ctx, a, c);
+  if (p.add) return launch<64, 128, 32, 3>(ctx, a, c);
   if (scatter) return launch<64, 128, 32, 2>(ctx, a, c);
   if (N > 64 || tiles_of(a.M, 128, a.N) < 128) return launch<64, 128, 32>(ctx, a, c);
   return launch<128, 64, 32>(ctx, a, c);

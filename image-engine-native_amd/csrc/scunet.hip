@@ -121,8 +121,10 @@ void free_maps(Scunet &s) {
 // of c/2 channels, y and y + pixels c/2, so that the two branches, which
 // run on two streams, write no common cache line; the split product writes
 // both planes and the join reads both, in the channel order of one map.
+// `add_after`, when not null, is added onto x after the last block (the
+// skip of the level below), in the last join's pass.
 ien_status run_level(Scunet &s, ScunetBlock *blocks, int h, int w, int c, Steps *steps,
-                     int *step) {
+                     int *step, const uint16_t *add_after = nullptr) {
   ien_ctx *ctx = s.ctx;
   const size_t pixels = (size_t)h * w, half = (size_t)c / 2;
   uint16_t *yc = s.y, *ysw = s.y + pixels * half;
@@ -139,7 +141,7 @@ ien_status run_level(Scunet &s, ScunetBlock *blocks, int h, int w, int c, Steps 
     p.n1 = (int)half;
     return launch_rows_planes(ctx, p);
   };
-  auto join = [&](const ien_matrix *m) {
+  auto join = [&](const ien_matrix *m, const uint16_t *add) {
     RowsPlanes p;
     p.x = yc;
     p.x2 = ysw;
@@ -151,6 +153,7 @@ ien_status run_level(Scunet &s, ScunetBlock *blocks, int h, int w, int c, Steps 
     p.ys = p.ys2 = c;
     p.n1 = c;
     p.accumulate = 1;
+    p.add = add;
     return launch_rows_planes(ctx, p);
   };
   ien_status st = split(blocks[0].split);
@@ -172,7 +175,7 @@ ien_status run_level(Scunet &s, ScunetBlock *blocks, int h, int w, int c, Steps 
     }
     if (st == IEN_OK) st = ien_swin_run(B.swin, ysw, half, h, w);
     if (st == IEN_OK) st = join_branches(ctx, 1);
-    if (st == IEN_OK) st = join(B.join);
+    if (st == IEN_OK) st = join(B.join, b + 1 < BLOCKS ? nullptr : add_after);
     if (st == IEN_OK && b + 1 < BLOCKS) st = split(blocks[b + 1].split);
     if (st == IEN_OK && steps) st = steps->step(ctx->stream);
     ++*step;
@@ -324,10 +327,12 @@ ien_status scunet_enqueue(Scunet *s, const float *d_image, size_t width, size_t 
     w /= 2;
     c *= 2;
   }
-  if ((st = run_level(*s, s->body, h, w, c, steps, &step)) != IEN_OK) return unswap(), st;
+  // Each level up starts from the map plus the skip of its size, added in
+  // the last join of the level below it.
+  if ((st = run_level(*s, s->body, h, w, c, steps, &step, s->skip[2])) != IEN_OK)
+    return unswap(), st;
   for (int l = 0; l < 3; l++) {
     const size_t pixels = (size_t)h * w;
-    if ((st = ien_add(ctx, s->x, s->skip[2 - l], pixels * c)) != IEN_OK) return unswap(), st;
     // network.rs:439-478 doubled: each pixel's product scattered over its 2
     // x 2 output pixels.
     {
@@ -348,7 +353,9 @@ ien_status scunet_enqueue(Scunet *s, const float *d_image, size_t width, size_t 
     h *= 2;
     w *= 2;
     c /= 2;
-    if ((st = run_level(*s, s->up[l], h, w, c, steps, &step)) != IEN_OK) return unswap(), st;
+    if ((st = run_level(*s, s->up[l], h, w, c, steps, &step, l < 2 ? s->skip[1 - l] : nullptr)) !=
+        IEN_OK)
+      return unswap(), st;
   }
   if ((st = conv3(ctx, s->img, h, w, 4, 8, s->head, s->x, DIM, IEN_ACT_NONE, 1)) != IEN_OK)
     return unswap(), st;
