@@ -186,6 +186,7 @@ struct PairCall {
 // channels come from x (rows xs halves apart) and the rest from x2, the
 // first n1 output columns going to y and the rest to y2: the two halves of
 // a map kept as separate planes.
+struct WinGeo;
 struct RowsPlanes {
   const uint16_t *x = nullptr, *x2 = nullptr;
   int xs = 0, xs2 = 0, k1 = 0;
@@ -207,6 +208,11 @@ struct RowsPlanes {
   // A map (rows ys apart) added to the f16 result, rounded again: the
   // product followed by ien_add in one pass; or null.
   const uint16_t *add = nullptr;
+  // Rows are the tokens of these windows over y's map (rows ys apart): each
+  // row's f16 result is added onto its map pixel and rounded again, tokens
+  // past the edge dropped (the product followed by ien_window_scatter_add);
+  // or null.
+  const WinGeo *windows = nullptr;
 };
 ien_status launch_rows_planes(ien_ctx *ctx, const RowsPlanes &p);
 

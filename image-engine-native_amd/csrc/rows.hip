@@ -32,6 +32,7 @@
 // the two halves of a map that two streams work on share no cache line.
 
 #include "conv_common.h"
+#include "window_geo.h"
 
 namespace ien {
 namespace {
@@ -58,6 +59,7 @@ struct RowsArgs {
   int g2w, s2w;
   uint16_t *ydup;  // gathered rows: a second copy of the output (rows ys apart), or null
   const uint16_t *add2;  // MODE 3: a map added to the rounded result (rows ys apart)
+  WinGeo wg;             // MODE 4: row r is token r % n of window r / n of y's map
   int act, accumulate;
   int tiles_n, tiles;
   // Split-K (gridDim.y splits of kchunks chunks): raw f32 sums of split z
@@ -93,7 +95,9 @@ __device__ __forceinline__ int swz(int r, int g) {
 
 // MODE 0: plain rows; 1: 2 x 2 gathered rows (g2w); 2: rows scattered over
 // 2 x 2 output pixels (s2w); 3: plain rows whose f16 result gets add2 added
-// and is rounded again (a separate map addition after the product).
+// and is rounded again (a separate map addition after the product); 4: rows
+// are window tokens whose rounded result is added onto their map pixel
+// (ien_window_scatter_add after the product), tokens past the edge dropped.
 template <int BM, int BN, int KC, int MODE>
 __global__ __launch_bounds__(256) void k_rows(RowsArgs a) {
   using R = RowsCfg<BM, BN, KC>;
@@ -239,7 +243,20 @@ __global__ __launch_bounds__(256) void k_rows(RowsArgs a) {
     }
     return col < a.n1 ? a.y + (long)row * a.ys + col : a.y2 + (long)row * a.ys2 + (col - a.n1);
   };
-  u32x4 old[R::ITEMS], old2[MODE == 3 ? R::ITEMS : 1];
+  // MODE 4: the map pixel of an output row, or null past the map's edge.
+  auto win_dst = [&](int row, int col) -> uint16_t * {
+    const int w = row / a.wg.n, src = win_source(a.wg, w, row - w * a.wg.n);
+    return src < 0 ? nullptr : a.y + (long)src * a.ys + col;
+  };
+  u32x4 old[R::ITEMS], old2[MODE >= 3 ? R::ITEMS : 1];
+  if constexpr (MODE == 4) {
+#pragma unroll
+    for (int e = 0; e < R::ITEMS; e++) {
+      const int v = tid + 256 * e, row = v / (BN / 8), col = tn * BN + 8 * (v % (BN / 8));
+      const uint16_t *q = m0 + row < a.M && col < a.N ? win_dst(m0 + row, col) : nullptr;
+      old2[e] = *(const u32x4 *)(q ? q : a.y);
+    }
+  }
   if constexpr (MODE == 3) {
 #pragma unroll
     for (int e = 0; e < R::ITEMS; e++) {
@@ -263,6 +280,13 @@ __global__ __launch_bounds__(256) void k_rows(RowsArgs a) {
       const int v = tid + 256 * e, row = v / (BN / 8), c8 = 8 * (v % (BN / 8));
       const int col = tn * BN + c8;
       if (m0 + row >= a.M || col >= a.N) continue;
+      uint16_t *dst = nullptr;
+      if constexpr (MODE == 4) {
+        dst = win_dst(m0 + row, col);
+        if (!dst) continue;
+      } else {
+        dst = out_at(m0 + row, col);
+      }
       const float *sr = st + (row - 64 * half) * R::SP + c8;
       const float4v s0 = *(const float4v *)sr, s1 = *(const float4v *)(sr + 4);
       float v8[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
@@ -275,13 +299,13 @@ __global__ __launch_bounds__(256) void k_rows(RowsArgs a) {
       uint16_t o[8];
 #pragma unroll
       for (int k = 0; k < 8; k++) o[k] = f2h(actf(v8[k], col + k));
-      if constexpr (MODE == 3) {
+      if constexpr (MODE >= 3) {
         uint16_t h2[8];
         __builtin_memcpy(h2, &old2[e], 16);
 #pragma unroll
         for (int k = 0; k < 8; k++) o[k] = f2h(h2f(o[k]) + h2f(h2[k]));
       }
-      __builtin_memcpy(out_at(m0 + row, col), o, 16);
+      __builtin_memcpy(dst, o, 16);
       if constexpr (MODE == 1)
         if (a.ydup) __builtin_memcpy(a.ydup + (long)(m0 + row) * a.ys + col, o, 16);
     }
@@ -333,7 +357,7 @@ ien_status launch(ien_ctx *ctx, RowsArgs a, const ConvArgs &c) {
   int ksplit = 1;
   // (The finishing pass writes one map, row by row; gathered rows are
   // split like any others.)
-  const bool planes = a.k1 < a.K || a.n1 < a.N || MODE == 2 || MODE == 3;
+  const bool planes = a.k1 < a.K || a.n1 < a.N || MODE >= 2;
   if (!planes && chunks >= 16 && (4 * a.tiles <= ctx->cus || (a.K >= 1536 && a.tiles < ctx->cus))) {
     ksplit = std::min(chunks / 8, (2 * ctx->cus + a.tiles - 1) / a.tiles);
     while (ksplit > 1 && (size_t)ksplit * a.M * a.pitch > ctx->splitk_floats) ksplit--;
@@ -412,7 +436,11 @@ ien_status launch_rows_planes(ien_ctx *ctx, const RowsPlanes &p) {
                 (!gather || (p.k1 == K && K % 128 == 0 && p.rows % p.gather_w2 == 0)) &&
                 (!scatter || (p.n1 == N && N % 32 == 0 && p.rows % p.scatter_w == 0 && !p.accumulate)) &&
                 (!p.ydup || (gather && p.n1 == N && ((uintptr_t)p.ydup & 15) == 0 && !p.accumulate)) &&
-                (!p.add || (!gather && !scatter && p.n1 == N && ((uintptr_t)p.add & 15) == 0)),
+                (!p.add || (!gather && !scatter && p.n1 == N && ((uintptr_t)p.add & 15) == 0)) &&
+                (!p.windows ||
+                 (!gather && !scatter && !p.add && !p.accumulate && p.n1 == N &&
+                  p.rows == p.windows->windows * p.windows->n && p.windows->windows < (1L << 31) &&
+                  (long)p.windows->height * p.windows->width * p.ys * 2 <= 0x7fff0000L)),
             IEN_ERR_INPUT, "rows planes: 2 x 2 regrouping of k %d / n %d over %ld rows", K, N, p.rows);
   // A gathered row reads K / 4 channels of each pixel; a scattered one
   // writes N / 4.
@@ -463,6 +491,10 @@ ien_status launch_rows_planes(ien_ctx *ctx, const RowsPlanes &p) {
   c.accumulate = p.accumulate;
   if (gather) return launch<64, 128, 32, 1>(ctx, a, c);
   if (p.add) return launch<64, 128, 32, 3>(ctx, a, c);
+  if (p.windows) {
+    a.wg = *p.windows;
+    return launch<64, 128, 32, 4>(ctx, a, c);
+  }
   if (scatter) return launch<64, 128, 32, 2>(ctx, a, c);
   if (N > 64 || tiles_of(a.M, 128, a.N) < 128) return launch<64, 128, 32>(ctx, a, c);
   return launch<128, 64, 32>(ctx, a, c);

@@ -9,6 +9,7 @@
 #include <vector>
 
 #include "ien_internal.h"
+#include "window_geo.h"
 
 using namespace ien;
 
@@ -156,9 +157,22 @@ ien_status run_block(ien_swin *b, uint16_t *d_map, size_t stride, int height, in
       st = rows_product(ctx, tok, c, rows, b->qkv, wide, 3 * c, IEN_ACT_NONE, 0);
     if (st == IEN_OK)
       st = window_attention(ctx, &w, wide, b->c, b->d_packed, true, att);
-    if (st == IEN_OK)
-      st = rows_product(ctx, att, c, rows, b->proj, tok, c, IEN_ACT_NONE, 0);
-    if (st == IEN_OK) st = ien_window_scatter_add(ctx, &w, tok, b->c, d_map, stride);
+    // The projection added straight back onto the map's pixels.
+    WinGeo g;
+    if (st == IEN_OK) st = geometry(&w, &g);
+    if (st == IEN_OK) {
+      RowsPlanes p;
+      p.x = p.x2 = att;
+      p.xs = p.xs2 = (int)c;
+      p.k1 = (int)c;
+      p.rows = (long)rows;
+      p.w = b->proj;
+      p.y = p.y2 = d_map;
+      p.ys = p.ys2 = (int)stride;
+      p.n1 = (int)c;
+      p.windows = &g;
+      st = launch_rows_planes(ctx, p);
+    }
   }
   if (st != IEN_OK) return st;
   // mlp (scunet swin.rs:236-275): every token normalised, fc1 + GELU, fc2
