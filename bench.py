@@ -60,6 +60,41 @@ def log(msg):
     print(f"bench: {msg}", file=sys.stderr, flush=True)
 
 
+# Device bytes in use (hipMemGetInfo) before the library's context opened:
+# each configuration reports what it holds above that.
+_DEVICE_BASE = 0
+
+
+def device_in_use():
+    import torch
+
+    free, total = torch.cuda.mem_get_info()
+    return total - free
+
+
+def device_mib(extra_note=None):
+    """Device memory the run holds: the context (its split-K workspace and
+    chain flags), the model (weights, maps grown to this size, Swin scratch,
+    plans) and the run's input and output tensors, in MiB above what was in
+    use before the context opened. The library never shrinks its maps, so
+    this is the configuration's peak; read before the model is freed."""
+    import torch
+
+    torch.cuda.synchronize()
+    return round((device_in_use() - _DEVICE_BASE) / 2**20, 1)
+
+
+def host_peak_mib():
+    """VmHWM of this process (realesrgan-bench.rs:82-87 prints the same)."""
+    try:
+        for line in open("/proc/self/status"):
+            if line.startswith("VmHWM"):
+                return round(int(line.split()[1]) / 1024, 1)
+    except OSError:
+        pass
+    return None
+
+
 def conv_flops(h, w, cin, cout, size):
     return 2.0 * h * w * cout * cin * size * size
 
@@ -159,8 +194,11 @@ def elementwise(ctx, stream, reps, copy_tbps=None):
     the sweep (a graph of `reps` back-to-back launches after 20 untimed):
     algorithmic bytes (every input read once, every output written once),
     GB/s, % of the 8 TB/s HBM peak and, when given, of the measured device
-    copy rate.  Working sets under 256 MiB may be served partly by the
-    memory-side cache."""
+    copy rate.  Each pass cycles over enough copies of its buffers that the
+    launches between two uses of one copy touch more than 512 MiB: twice the
+    256 MiB memory-side cache, so every launch reads and writes HBM."""
+    import itertools
+
     import numpy as np
     import torch
 
@@ -175,58 +213,97 @@ def elementwise(ctx, stream, reps, copy_tbps=None):
     def floats(*shape):
         return torch.from_numpy(rng.standard_normal(shape).astype(np.float32)).to(dev)
 
+    # (name, algorithmic bytes, make): make() allocates one copy of the
+    # pass's buffers and returns its launch.
     cases = []
+
     # LayerNorm: BiRefNet 1024x1024, the patch embedding's norm (256x256 tokens x 96) and
     # stage 1's merge norm (128x128 x 384), in place.
-    for rows, c in ((65536, 96), (16384, 384)):
+    def layer_norm(rows, c):
         x, g, b = halves(rows, c), floats(c), floats(c)
-        cases.append((f"layer_norm {rows}x{c}", 2 * rows * c * 2,
-                      lambda x=x, rows=rows, c=c, g=g, b=b: ien.layer_norm(ctx, x, rows, c, c, g, b)))
+        return lambda: ien.layer_norm(ctx, x, rows, c, c, g, b)
+
+    for rows, c in ((65536, 96), (16384, 384)):
+        cases.append((f"layer_norm {rows}x{c}", 2 * rows * c * 2, lambda rows=rows, c=c: layer_norm(rows, c)))
+
     # Bilinear align-corners: BiRefNet's half-size stage-1 map (128x128 x 96) to 256x256,
     # into a 192-channel map.
-    src, dst = halves(128 * 128, 96), halves(256 * 256, 192)
-    cases.append(("resize 128x128x96 -> 256x256", 2 * (128 * 128 + 256 * 256) * 96,
-                  lambda: ien.resize(ctx, src, 128, 128, 96, 96, dst, 256, 256, 192)))
+    def resize():
+        src, dst = halves(128 * 128, 96), halves(256 * 256, 192)
+        return lambda: ien.resize(ctx, src, 128, 128, 96, 96, dst, 256, 256, 192)
+
+    cases.append(("resize 128x128x96 -> 256x256", 2 * (128 * 128 + 256 * 256) * 96, resize))
+
     # Window gather with the block's LayerNorm: SCUNet level 1 (512x768, 32 channels, windows
     # of 8 shifted by 4).
     w = ien.windows(8, 4, 512, 768)
-    wmap, wg, wb = halves(512 * 768, 32), floats(32), floats(32)
-    tokens = torch.empty((ien.window_count(w) * 64, 32), dtype=f16, device=dev)
-    cases.append(("window_gather 512x768x32 w8 s4", 2 * 2 * 512 * 768 * 32,
-                  lambda: ien.window_gather(ctx, w, wmap, 32, 32, wg, wb, tokens)))
+
+    def window_gather():
+        wmap, wg, wb = halves(512 * 768, 32), floats(32), floats(32)
+        tokens = torch.empty((ien.window_count(w) * 64, 32), dtype=f16, device=dev)
+        return lambda: ien.window_gather(ctx, w, wmap, 32, 32, wg, wb, tokens)
+
+    cases.append(("window_gather 512x768x32 w8 s4", 2 * 2 * 512 * 768 * 32, window_gather))
+
     # 2x2 gather and scatter: SCUNet's halving (512x768 x 64 -> 256x384 rows of 256) and doubling.
-    gmap, grows = halves(512 * 768, 64), torch.empty((256 * 384, 256), dtype=f16, device=dev)
-    cases.append(("gather_2x2 512x768x64", 2 * 2 * 512 * 768 * 64,
-                  lambda: ien.gather_2x2(ctx, gmap, 512, 768, 64, 64, ien.ORDER_ROW_MAJOR, grows)))
-    srows, smap = halves(256 * 384, 128), torch.empty((512 * 768, 32), dtype=f16, device=dev)
-    cases.append(("scatter_2x2 256x384x128 -> 512x768x32", 2 * 2 * 256 * 384 * 128,
-                  lambda: ien.scatter_2x2(ctx, srows, 128, 256, 384, 32, smap, 32)))
+    def gather_2x2():
+        gmap, grows = halves(512 * 768, 64), torch.empty((256 * 384, 256), dtype=f16, device=dev)
+        return lambda: ien.gather_2x2(ctx, gmap, 512, 768, 64, 64, ien.ORDER_ROW_MAJOR, grows)
+
+    cases.append(("gather_2x2 512x768x64", 2 * 2 * 512 * 768 * 64, gather_2x2))
+
+    def scatter_2x2():
+        srows, smap = halves(256 * 384, 128), torch.empty((512 * 768, 32), dtype=f16, device=dev)
+        return lambda: ien.scatter_2x2(ctx, srows, 128, 256, 384, 32, smap, 32)
+
+    cases.append(("scatter_2x2 256x384x128 -> 512x768x32", 2 * 2 * 256 * 384 * 128, scatter_2x2))
+
     # Residual add: SCUNet level 1 (512x768 x 64).
-    ax, ay = halves(512 * 768 * 64), halves(512 * 768 * 64)
-    cases.append(("add 512x768x64", 3 * 512 * 768 * 64 * 2, lambda: ien.add(ctx, ax, ay)))
+    def add():
+        ax, ay = halves(512 * 768 * 64), halves(512 * 768 * 64)
+        return lambda: ien.add(ctx, ax, ay)
+
+    cases.append(("add 512x768x64", 3 * 512 * 768 * 64 * 2, add))
+
     # Pixel shuffle x4 plus the repeated image: Real-ESRGAN at 256x384 (the path outside the chain).
-    last, img = halves(256 * 384, 48), floats(256, 384, 3)
-    sh_out = torch.empty((1024, 1536, 3), dtype=torch.float32, device=dev)
-    cases.append(("pixel_shuffle_add 256x384", 256 * 384 * (48 * 2 + 12) + 1024 * 1536 * 12,
-                  lambda: ien.pixel_shuffle_add(ctx, last, 48, img, 384, 256, sh_out)))
+    def shuffle():
+        last, img = halves(256 * 384, 48), floats(256, 384, 3)
+        sh_out = torch.empty((1024, 1536, 3), dtype=torch.float32, device=dev)
+        return lambda: ien.pixel_shuffle_add(ctx, last, 48, img, 384, 256, sh_out)
+
+    cases.append(("pixel_shuffle_add 256x384", 256 * 384 * (48 * 2 + 12) + 1024 * 1536 * 12, shuffle))
+
     # f32 -> f16: BiRefNet's 1024x1024 RGB input; u8 -> f32: the same as bytes.
-    fimg, himg = floats(1024 * 1024 * 3), torch.empty(1024 * 1024 * 3, dtype=f16, device=dev)
-    cases.append(("floats_to_halves 1024x1024x3", 1024 * 1024 * 3 * 6,
-                  lambda: ien.floats_to_halves(ctx, fimg, himg)))
-    bimg = torch.from_numpy(rng.integers(0, 256, 1024 * 1024 * 3, dtype=np.uint8)).to(dev)
-    cases.append(("bytes_to_floats 1024x1024x3", 1024 * 1024 * 3 * 5,
-                  lambda: ien.bytes_to_floats(ctx, bimg, fimg)))
+    def to_halves():
+        fimg, himg = floats(1024 * 1024 * 3), torch.empty(1024 * 1024 * 3, dtype=f16, device=dev)
+        return lambda: ien.floats_to_halves(ctx, fimg, himg)
+
+    cases.append(("floats_to_halves 1024x1024x3", 1024 * 1024 * 3 * 6, to_halves))
+
+    def to_floats():
+        bimg = torch.from_numpy(rng.integers(0, 256, 1024 * 1024 * 3, dtype=np.uint8)).to(dev)
+        fimg = torch.empty(1024 * 1024 * 3, dtype=torch.float32, device=dev)
+        return lambda: ien.bytes_to_floats(ctx, bimg, fimg)
+
+    cases.append(("bytes_to_floats 1024x1024x3", 1024 * 1024 * 3 * 5, to_floats))
+
     results = []
-    for name, nbytes, launch in cases:
+    for name, nbytes, make in cases:
+        copies = max(2, -(-(512 << 20) // int(nbytes)) + 1)
+        launches = [make() for _ in range(copies)]
+        turn = itertools.cycle(launches)
+        launch = lambda: next(turn)()  # noqa: E731
         for _ in range(20):
             launch()
         ms = event_time(launch, reps, stream)
         gbs = nbytes / (ms * 1e-3) / 1e9
         row = {"pass": name, "bytes": int(nbytes), "us": round(ms * 1e3, 2), "gbs": round(gbs, 0),
-               "hbm_pct": round(100 * gbs / HBM_PEAK_GBS, 1)}
+               "hbm_pct": round(100 * gbs / HBM_PEAK_GBS, 1), "copies": copies}
         if copy_tbps:
             row["copy_pct"] = round(100 * gbs / (copy_tbps * 1000), 1)
         results.append(row)
+        del launches, launch, turn
+        torch.cuda.empty_cache()
     return results
 
 
@@ -481,13 +558,16 @@ def scunet_leg(ctx, steps, warmup, cpu_runs=0):
     torch.cuda.synchronize()
     ms = (time.perf_counter() - t0) * 1e3 / steps
     ok = bool(torch.isfinite(d_out).all())
+    dev_mib = device_mib()
     model.free()
+    del d_in, d_out
+    torch.cuda.empty_cache()
     if not ok:
         sys.exit("SCUNet: non-finite output")
     leg = {"workload": "SCUNet 1x3x512x768 (28 Swin-Conv blocks, 64/128/256/512)", "ms_per_image": round(ms, 3),
            "images_per_s": round(1e3 / ms, 2), "gflop_per_image": SCUNET_GFLOP,
            "tflops": round(SCUNET_GFLOP / ms, 1), "mfma_frac": round(SCUNET_GFLOP / ms / MFMA_F16_PEAK_TFLOPS, 4),
-           "host_path_ms": host_ms}
+           "host_path_ms": host_ms, "device_peak_mib": dev_mib}
     if cpu_runs:
         O = oracle_module()
         names = synthetic.scunet_names()
@@ -536,13 +616,17 @@ def lama_leg(ctx, steps, warmup, cpu_runs=0):
     torch.cuda.synchronize()
     ms = (time.perf_counter() - t0) * 1e3 / steps
     ok = bool(torch.isfinite(d_out).all())
+    dev_mib = device_mib()
     model.free()
+    del d_in, d_out
+    torch.cuda.empty_cache()
     if not ok:
         sys.exit("LaMa: non-finite output")
     gflop = round(lama_gflop(h, w), 1)
     leg = {"workload": "Big LaMa 1x4x512x512 (18 FFC blocks at 64x64x512)", "ms_per_image": round(ms, 3),
            "images_per_s": round(1e3 / ms, 2), "gflop_per_image": gflop, "tflops": round(gflop / ms, 1),
-           "mfma_frac": round(gflop / ms / MFMA_F16_PEAK_TFLOPS, 4), "host_path_ms": host_ms}
+           "mfma_frac": round(gflop / ms / MFMA_F16_PEAK_TFLOPS, 4), "host_path_ms": host_ms,
+           "device_peak_mib": dev_mib}
     if cpu_runs:
         O = oracle_module()
         names = synthetic.lama_names()
@@ -614,7 +698,10 @@ def birefnet_leg(ctx, steps, warmup, cpu_runs=0):
     torch.cuda.synchronize()
     ms = (time.perf_counter() - t0) * 1e3 / steps
     ok = bool(torch.isfinite(d_out).all())
+    dev_mib = device_mib()
     model.free()
+    del d_in, d_out
+    torch.cuda.empty_cache()
     if not ok:
         sys.exit("BiRefNet: non-finite output")
     gflop = round(birefnet_gflop(side, 12), 1)
@@ -622,7 +709,7 @@ def birefnet_leg(ctx, steps, warmup, cpu_runs=0):
            "ms_per_image": round(ms, 3), "images_per_s": round(1e3 / ms, 2), "gflop_per_image": gflop,
            "gflop_unpadded_windows": round(birefnet_gflop(side, 12, padded=False), 1),
            "tflops": round(gflop / ms, 1), "mfma_frac": round(gflop / ms / MFMA_F16_PEAK_TFLOPS, 4),
-           "host_path_ms": host_ms}
+           "host_path_ms": host_ms, "device_peak_mib": dev_mib}
     if cpu_runs:
         O = oracle_module()
         names = synthetic.birefnet_names(12)
@@ -681,6 +768,9 @@ def main():
     if not torch.cuda.is_available():
         sys.exit("bench.py needs a GPU")
     torch.cuda.set_device(0)
+    global _DEVICE_BASE
+    torch.zeros(1, device="cuda")
+    _DEVICE_BASE = device_in_use()
     ctx = ien.Context(0)
     stream = ctx.stream
     H, W = 256, 384
@@ -747,6 +837,10 @@ def main():
                 "rocprof": counters_from_profiles("esrgan")}
 
     host_ms = host_path_ms(lambda: model.run(image))
+    memory = {"device_peak_mib": device_mib(), "host_peak_mib": host_peak_mib(),
+              "what": "device: the context, the model and the run's input and output, above what was in "
+                      "use before the context opened (hipMemGetInfo); host: VmHWM after the Real-ESRGAN "
+                      "runs, before any CPU baseline"}
     cpu_runs = 0 if args.no_cpu else args.cpu_runs
     log("Real-ESRGAN timed")
     gemm_sweep = None if args.no_sweep else sweep(ctx, stream, args.kernel_reps)
@@ -782,6 +876,7 @@ def main():
                    "execution": "one launch per image (the whole network as one chain)"},
         "images_per_s": round(1e3 / ms_per_step, 1),
         "host_path_ms": host_ms,
+        "memory": memory,
         "roofline": roofline,
         "cpu_baseline": cpu,
         "gemm_sweep": gemm_sweep,

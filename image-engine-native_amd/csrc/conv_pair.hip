@@ -128,14 +128,17 @@ struct PairArgs {
   const uint16_t *w[2 * MAXPAIRS];
   const float *b[2 * MAXPAIRS], *s[2 * MAXPAIRS];
   // Chain only: the border maps (pair k stores to border[k % 2]); the
-  // flags: the abort word, the failure word (set with the abort word, kept
-  // until the host reads it), the count of workgroups done, then the tile
-  // epochs (tiles_x tiles_y words); all but the failure word are zero at
-  // launch and again at the end; and the wall-clock ticks (100 MHz) a wait
-  // for neighbours may take (negative: no wait succeeds, every tile with a
-  // neighbour gives up at its first wait -- the failure path on demand).
+  // flags: the abort word, the failure word (raised to this launch's
+  // sequence number `seq` when a wait gives up, never lowered, so the host
+  // tells which launches failed without clearing it), the count of
+  // workgroups done, then the tile epochs (tiles_x tiles_y words); all but
+  // the failure word are zero at launch and again at the end; and the
+  // wall-clock ticks (100 MHz) a wait for neighbours may take (negative: no
+  // wait succeeds, every tile with a neighbour gives up at its first wait --
+  // the failure path on demand).
   uint16_t *border[2];
   int *flags;
+  int seq;
   long spin_limit;
   // Chain only, optional (wl null: none): a final 3x3 64 -> 48 layer
   // (weights packed with n padded, bias; no activation) whose 48 channels
@@ -445,7 +448,8 @@ __global__ __launch_bounds__(THREADS) void conv_pair(PairArgs a) {
       if (lane == 0) {
         if (any) {
           __hip_atomic_store(abort_word, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          __hip_atomic_store(abort_word + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          __hip_atomic_fetch_max(abort_word + 1, a.seq, __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT);
         }
         go = any ? 0 : 1;
       }
@@ -790,6 +794,7 @@ ien_status launch_chain(ien_ctx *ctx, const ChainCall &c, uint16_t **out) {
   a.pairs = c.pairs;
   fill_layers(a, c.w, c.s, 2 * c.pairs);
   a.flags = ctx->chain_flags;
+  a.seq = ++ctx->chain_seq;
   a.spin_limit = ctx->chain_spin;
   if (c.first) {
     a.w0 = c.first->d_packed;
@@ -810,13 +815,12 @@ ien_status launch_chain(ien_ctx *ctx, const ChainCall &c, uint16_t **out) {
   return IEN_OK;
 }
 
-ien_status chain_status(ien_ctx *ctx) {
+ien_status chain_status(ien_ctx *ctx, int first) {
   int word = 0;
   IEN_HIP(hipMemcpyAsync(&word, ctx->chain_flags + 1, 4, hipMemcpyDeviceToHost, ctx->stream));
   IEN_HIP(hipStreamSynchronize(ctx->stream));
-  if (word == 0) return IEN_OK;
-  const int zero = 0;
-  IEN_HIP(hipMemcpy(ctx->chain_flags + 1, &zero, 4, hipMemcpyHostToDevice));
+  if (word < first || word <= ctx->chain_reported) return IEN_OK;
+  ctx->chain_reported = word;
   return fail(IEN_ERR_GPU, "body chain: a tile's wait for its neighbours timed out");
 }
 
@@ -887,6 +891,7 @@ extern "C" ien_status ien_conv3_chain(ien_ctx *ctx, uint16_t *d_a, uint16_t *d_b
 
 extern "C" ien_status ien_conv3_chain_status(ien_ctx *ctx) {
   IEN_CHECK(ctx, IEN_ERR_INPUT, "null argument");
-  return chain_status(ctx);
+  IEN_HIP(hipSetDevice(ctx->device));
+  return chain_status(ctx, 1);
 }
 

@@ -70,6 +70,9 @@ struct ien_ctx {
   // holds (-1 until asked); the wall-clock ticks (100 MHz) a tile may wait
   // for a neighbour.
   int *chain_flags = nullptr;
+  // Sequence number of the last chain launched on this context, and the
+  // highest failed one already reported (chain_status).
+  int chain_seq = 0, chain_reported = 0;
   int chain_tiles = 0;
   int chain_per_cu = -1;
   long chain_spin = 100000000;
@@ -223,9 +226,11 @@ ien_status launch_pair(ien_ctx *ctx, const PairCall &p);
 // slopes s[i]): the input in `a`; `b` and `a` hold the borders the tiles
 // exchange, and the output ends in the map launch_chain returns (`a` for an
 // even count), or, with a final layer, in `out`.  Supported when every tile's workgroup can be resident at
-// once.  chain_status waits for the stream and reports whether every chain
-// since the last report finished (a wait for a neighbour that timed out
-// aborts its chain), clearing the report.
+// once.  Each launch takes the context's next sequence number;
+// chain_status(ctx, first) waits for the stream and reports IEN_ERR_GPU
+// when a chain numbered `first` or later gave up (a wait for a neighbour
+// that timed out aborts its chain) and that failure was not reported
+// before.
 struct ChainCall {
   uint16_t *a = nullptr, *b = nullptr;
   int H = 0, W = 0, pairs = 0;
@@ -245,7 +250,7 @@ struct ChainCall {
 };
 bool chain_supported(ien_ctx *ctx, const ChainCall &c);
 ien_status launch_chain(ien_ctx *ctx, const ChainCall &c, uint16_t **out);
-ien_status chain_status(ien_ctx *ctx);
+ien_status chain_status(ien_ctx *ctx, int first);
 
 // io.hip: the 8-bit image passes of the models' u8 entry points, on the
 // context's stream (to_float, to_byte, LaMa's mask and compositing,

@@ -194,8 +194,11 @@ struct ien_model {
   // 8-bit images of the u8 entry point on the device (ien_model_run_u8).
   uint8_t *d_bytes = nullptr;
   size_t bytes_cap = 0;
-  // A run launched a chain of body pairs (checked when the run ends).
-  bool chained = false;
+  // A run launched a chain of body pairs (checked when the run ends), the
+  // sequence number of its first chain, and whether one of them gave up; a
+  // run repeated after such a failure takes the pair path (no_chain).
+  bool chained = false, chain_fell = false, no_chain = false;
+  int chain_first = 0;
 };
 
 namespace ien {
@@ -306,9 +309,10 @@ static ien_status enqueue_esrgan(ien_model *model, const float *d_image, size_t 
   chain.last = model->layers[STEPS - 1].conv;
   chain.image = d_image;
   chain.out = d_out;
-  if (!steps && chain_supported(ctx, chain)) {
+  if (!steps && !model->no_chain && chain_supported(ctx, chain)) {
     // The whole network, image to shuffled output, in one launch.
     uint16_t *out = nullptr;
+    if (!model->chained) model->chain_first = ctx->chain_seq + 1;
     ien_status st = launch_chain(ctx, chain, &out);
     if (st == IEN_OK) model->chained = true;
     return st;
@@ -538,8 +542,27 @@ static ien_status finish_run(ien_model *model, ien_status st, Steps *steps) {
   model->chained = false;
   if (st != IEN_OK) return st;
   if (e != hipSuccess) return fail(IEN_ERR_GPU, "run: %s", hipGetErrorString(e));
-  if (chained) return chain_status(model->ctx);
+  if (chained && (st = chain_status(model->ctx, model->chain_first)) != IEN_OK) {
+    model->chain_fell = true;
+    return st;
+  }
   return IEN_OK;
+}
+
+// A host-buffer run whose chain gave up (a neighbour's workgroup was not
+// resident in time: another stream or process holding CUs) is issued once
+// more through the pair path, which gives the same bits and needs no
+// workgroups resident together.
+template <class Run>
+static ien_status with_pair_fallback(ien_model *model, Run run) {
+  model->chain_fell = false;
+  ien_status st = run();
+  if (st != IEN_ERR_GPU || !model->chain_fell) return st;
+  model->chain_fell = false;
+  model->no_chain = true;
+  st = run();
+  model->no_chain = false;
+  return st;
 }
 
 // realesrgan-native lib.rs:230-289 / scunet-native lib.rs:192-247 tiled:
@@ -548,8 +571,9 @@ static ien_status finish_run(ien_model *model, ien_status st, Steps *steps) {
 // T is float (run_float_tiled) or uint8_t (Model::run: to_float on the way
 // in, to_byte on the way out, both on the device).
 template <typename T>
-static ien_status run_tiled(ien_model *model, const T *image, size_t width, size_t height,
-                            size_t tile, size_t margin, T *out, ien_progress progress, void *user) {
+static ien_status run_tiled_once(ien_model *model, const T *image, size_t width, size_t height,
+                                 size_t tile, size_t margin, T *out, ien_progress progress,
+                                 void *user) {
   IEN_CHECK(model->kind == IEN_MODEL_REALESRGAN || model->kind == IEN_MODEL_SCUNET,
             IEN_ERR_INPUT, "only Real-ESRGAN and SCUNet run in tiles");
   ien_status st = check_size(model, width, height);
@@ -617,6 +641,14 @@ static ien_status run_tiled(ien_model *model, const T *image, size_t width, size
     }
   }
   return finish_run(model, st, sp);
+}
+
+template <typename T>
+static ien_status run_tiled(ien_model *model, const T *image, size_t width, size_t height,
+                            size_t tile, size_t margin, T *out, ien_progress progress, void *user) {
+  return with_pair_fallback(model, [&]() {
+    return run_tiled_once(model, image, width, height, tile, margin, out, progress, user);
+  });
 }
 
 }  // namespace ien
@@ -741,9 +773,8 @@ ien_status ien_model_set_graph(ien_model *model, int enabled) {
   return IEN_OK;
 }
 
-ien_status ien_model_run_device(ien_model *model, const float *d_image, const float *d_mask,
-                                size_t width, size_t height, float *d_out) {
-  IEN_CHECK(model && d_image && d_out, IEN_ERR_INPUT, "null argument");
+static ien_status run_device(ien_model *model, const float *d_image, const float *d_mask,
+                             size_t width, size_t height, float *d_out) {
   if (model->kind == IEN_MODEL_LAMA)
     IEN_CHECK(d_mask != nullptr, IEN_ERR_INPUT, "LaMa needs a mask");
   else
@@ -795,9 +826,27 @@ ien_status ien_model_run_device(ien_model *model, const float *d_image, const fl
   return IEN_OK;
 }
 
-ien_status ien_model_run(ien_model *model, const float *image, const float *mask, size_t width,
-                         size_t height, float *out, ien_progress progress, void *user) {
-  IEN_CHECK(model && image && out, IEN_ERR_INPUT, "null argument");
+ien_status ien_model_run_device(ien_model *model, const float *d_image, const float *d_mask,
+                                size_t width, size_t height, float *d_out) {
+  IEN_CHECK(model && d_image && d_out, IEN_ERR_INPUT, "null argument");
+  const ien_status st = run_device(model, d_image, d_mask, width, height, d_out);
+  // The device path does not wait for its chains: ien_model_status reports
+  // them.
+  model->chained = false;
+  return st;
+}
+
+ien_status ien_model_status(ien_model *model) {
+  IEN_CHECK(model, IEN_ERR_INPUT, "no model");
+  ien_ctx *ctx = model->ctx;
+  IEN_HIP(hipSetDevice(ctx->device));
+  const hipError_t e = hipStreamSynchronize(ctx->stream);
+  if (e != hipSuccess) return fail(IEN_ERR_GPU, "run: %s", hipGetErrorString(e));
+  return chain_status(ctx, 1);
+}
+
+static ien_status run_host(ien_model *model, const float *image, const float *mask, size_t width,
+                           size_t height, float *out, ien_progress progress, void *user) {
   ien_status st = check_mask(model, mask != nullptr);
   if (st == IEN_OK) st = check_size(model, width, height);
   if (st != IEN_OK) return st;
@@ -814,6 +863,14 @@ ien_status ien_model_run(ien_model *model, const float *image, const float *mask
   if ((st = finish_run(model, st, sp)) != IEN_OK) return st;
   IEN_HIP(hipMemcpy(out, io.out, pixels * out_per_pixel(model) * 4, hipMemcpyDeviceToHost));
   return IEN_OK;
+}
+
+ien_status ien_model_run(ien_model *model, const float *image, const float *mask, size_t width,
+                         size_t height, float *out, ien_progress progress, void *user) {
+  IEN_CHECK(model && image && out, IEN_ERR_INPUT, "null argument");
+  return with_pair_fallback(model, [&]() {
+    return run_host(model, image, mask, width, height, out, progress, user);
+  });
 }
 
 ien_status ien_model_run_tiled(ien_model *model, const float *image, size_t width,

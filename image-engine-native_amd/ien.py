@@ -32,7 +32,7 @@ EXPORTS = (
     "ien_conv3_pair", "ien_conv3_chain", "ien_conv3_chain_status", "ien_measure_mfma",
     "ien_layer_norm", "ien_gelu", "ien_sigmoid", "ien_pixel_shuffle_add", "ien_depthwise",
     "ien_model_load", "ien_model_from_tensors", "ien_model_free", "ien_model_run",
-    "ien_model_run_device", "ien_model_set_graph", "ien_model_run_tiled", "ien_model_run_u8",
+    "ien_model_run_device", "ien_model_status", "ien_model_set_graph", "ien_model_run_tiled", "ien_model_run_u8",
     "ien_bytes_to_floats", "ien_floats_to_bytes", "ien_mask_bytes", "ien_normalize_bytes",
     "ien_composite_bytes",
     "ien_window_count", "ien_position_bias", "ien_bias_tables", "ien_window_gather",
@@ -165,6 +165,7 @@ def load():
         L.ien_normalize_bytes.argtypes = [vp, vp, sz, vp, vp, vp]
         L.ien_composite_bytes.argtypes = [vp, vp, vp, vp, sz, vp]
         L.ien_model_run_device.argtypes = [vp, vp, vp, sz, sz, vp]
+        L.ien_model_status.argtypes = [vp]
         L.ien_model_set_graph.argtypes = [vp, i]
         wp = ctypes.POINTER(Windows)
         L.ien_window_count.argtypes = [wp]
@@ -676,3 +677,8 @@ class Model:
     def run_device(self, d_image, width, height, d_out, d_mask=None):
         check(load().ien_model_run_device(self.h, _ptr(d_image), None if d_mask is None else _ptr(d_mask),
                                           width, height, _ptr(d_out)))
+
+    def status(self):
+        """Waits for the model's stream; raises IenError (ERR_GPU) when a chain
+        launched by run_device since the last report gave up."""
+        check(load().ien_model_status(self.h))

@@ -496,9 +496,24 @@ ien_status ien_model_run_u8(ien_model *model, const uint8_t *rgb, const uint8_t 
                             void *user);
 
 /* The same on device buffers (f32 NHWC in and out), no host copies and no
- * synchronisation: the hot path a serving loop or a benchmark times. */
+ * synchronisation: the hot path a serving loop or a benchmark times.
+ * Real-ESRGAN runs as one chain launch whose tiles wait for their
+ * neighbours; that needs every tile's workgroup resident at once (one per
+ * CU), so another stream or process holding CUs for longer than the wait's
+ * limit (1 s) makes the chain give up and leave its output incomplete.  The
+ * call cannot see that when it returns: ien_model_status does. */
 ien_status ien_model_run_device(ien_model *model, const float *d_image, const float *d_mask,
                                 size_t width, size_t height, float *d_out);
+
+/* No counterpart in the reference (its runs are synchronous): waits for the
+ * model's stream and returns IEN_ERR_GPU ("body chain: ...", the reference's
+ * Error::Gpu, lib.rs:130-136: fall back) when a chain launched by
+ * ien_model_run_device since the last report gave up, or when the stream
+ * failed; each failure is reported once.  The host-buffer runs
+ * (ien_model_run, _tiled, _u8) check their own chains and repeat a run
+ * whose chain gave up through two-layer launches (the same bits), so they
+ * never need this call. */
+ien_status ien_model_status(ien_model *model);
 
 /* Launch-free replay: capture ien_model_run_device at this size into a HIP
  * graph once, then replay it (0 = eager launches).  A run that is a single

@@ -150,30 +150,59 @@ def test_body_chain_equals_pairs(ctx, tensors, h, w):
 def test_body_chain_wait_limit(tensors, monkeypatch):
     """A chain whose waits for neighbours never succeed (the wall-clock limit
     set negative from the host): every tile gives up at its first wait and
-    sets the abort word, every workgroup ends, and the run reports the
-    failure; the flags are clear again for the next run, and a context with
-    the normal limit is unaffected."""
+    sets the abort word, and every workgroup ends.
+    - The host-buffer run sees the failure and repeats the run through the
+      pair launches: the same bits as a run with the normal limit.
+    - The device path returns at once; ien_model_status then reports the
+      failure (IEN_ERR_GPU) once, and a second status call is clean.
+    - A context with the normal limit is unaffected, on both paths."""
+    import torch
     import ien
 
     image = synthetic.esrgan_image(256, 384, seed=9)
+    calm = ien.Context(0)
+    model = ien.Model(calm, ien.MODEL_REALESRGAN, tensors=tensors)
+    want = model.run(image, progress=lambda done, user: 0)  # the pair path
+    model.free()
+    calm.close()
+
     monkeypatch.setenv("IEN_CHAIN_SPIN_TICKS", "-1")
     hurried = ien.Context(0)
     monkeypatch.delenv("IEN_CHAIN_SPIN_TICKS")
     model = ien.Model(hurried, ien.MODEL_REALESRGAN, tensors=tensors)
+    got = model.run(image)  # chain gives up, repeated through pairs
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    model.status()  # the host run's failure was handled and is not reported again
+    d_in = torch.from_numpy(image).cuda()
+    d_out = torch.zeros((1024, 1536, 3), dtype=torch.float32, device="cuda")
+    model.set_graph(False)
+    model.run_device(d_in, 384, 256, d_out)
     with pytest.raises(ien.IenError) as e:
-        model.run(image)
+        model.status()
     assert e.value.status == ien.ERR_GPU and "timed out" in str(e.value), str(e.value)
-    with pytest.raises(ien.IenError):  # again: the failure word was read, cleared and set anew
-        model.run(image)
+    model.status()  # reported once
+    model.set_graph(True)
+    model.run_device(d_in, 384, 256, d_out)
+    model.run_device(d_in, 384, 256, d_out)
+    with pytest.raises(ien.IenError):
+        model.status()
+    again = model.run(image)  # a host run after unreported device failures: still the right bits
+    assert np.array_equal(again.view(np.uint32), want.view(np.uint32))
     model.free()
     hurried.close()
+
     calm = ien.Context(0)
     model = ien.Model(calm, ien.MODEL_REALESRGAN, tensors=tensors)
     got = model.run(image)
-    want = model.run(image, progress=lambda done, user: 0)
+    d_out.zero_()
+    model.set_graph(True)
+    model.run_device(d_in, 384, 256, d_out)
+    model.status()
+    dev = d_out.cpu().numpy()
     model.free()
     calm.close()
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    assert np.array_equal(dev.view(np.uint32), want.view(np.uint32))
 
 
 def pair_inputs(ctx, tensors, h, w, seed):
