@@ -276,6 +276,15 @@ std::vector<float> pack_bias_tables(const float *tables, int classes, int heads,
 ien_status window_attention(ien_ctx *ctx, const ien_windows *w, const uint16_t *d_qkv, int c,
                             const float *d_tables, bool packed, uint16_t *d_out);
 
+// window_attend.hip: gather, LayerNorm 1, the head's q, k, v and the
+// attention in one pass per window and head, into the windows' rows of c
+// (what the unfused gather, qkv product and attention give); widths by 32,
+// windows of up to 64 or 129 .. 160 tokens, tables packed.
+bool window_qkv_attention_supported(int c, int window);
+ien_status window_qkv_attention(ien_ctx *ctx, const ien_windows *win, const uint16_t *d_map,
+                                size_t stride, int c, const float *gamma, const float *beta,
+                                const ien_matrix *qkv, const float *d_tables, uint16_t *d_out);
+
 bool swin_mlp_supported(int c);
 // The device address of ien_swin_run_static's static scratch on `device`
 // (current), looked up once per device.

@@ -152,11 +152,16 @@ ien_status run_block(ien_swin *b, uint16_t *d_map, size_t stride, int height, in
     st = swin_attend(ctx, &w, d_map, stride, b->c, g1, b1, b->qkv, b->d_attn_proj,
                      b->proj->d_bias, b->d_packed);
   } else {
-    st = ien_window_gather(ctx, &w, d_map, stride, b->c, g1, b1, tok);
-    if (st == IEN_OK)
-      st = rows_product(ctx, tok, c, rows, b->qkv, wide, 3 * c, IEN_ACT_NONE, 0);
-    if (st == IEN_OK)
-      st = window_attention(ctx, &w, wide, b->c, b->d_packed, true, att);
+    if (rows16 && window_qkv_attention_supported(b->c, b->window)) {
+      // Gather, LayerNorm, q k v and attention in one pass per window and head.
+      st = window_qkv_attention(ctx, &w, d_map, stride, b->c, g1, b1, b->qkv, b->d_packed, att);
+    } else {
+      st = ien_window_gather(ctx, &w, d_map, stride, b->c, g1, b1, tok);
+      if (st == IEN_OK)
+        st = rows_product(ctx, tok, c, rows, b->qkv, wide, 3 * c, IEN_ACT_NONE, 0);
+      if (st == IEN_OK)
+        st = window_attention(ctx, &w, wide, b->c, b->d_packed, true, att);
+    }
     // The projection added straight back onto the map's pixels.
     WinGeo g;
     if (st == IEN_OK) st = geometry(&w, &g);

@@ -4,7 +4,8 @@ or_swin_attend followed by or_swin_mlp, on f16-rounded maps; a second run
 on a larger map reuses the block (scratch grown on demand).  Window 8 with
 32, 64 or 128 channels runs the fused per-window attention (at 32 with the
 MLP in the same pass); 32, 64 and 96 channels otherwise the fused MLP pass;
-the other widths and windows the unfused path."""
+the other widths and windows run the gather, q k v and attention of a
+window and head in one pass (window_attend.hip), then the projection."""
 
 import numpy as np
 import pytest
@@ -41,6 +42,8 @@ def oracle_block(oracle, x, window, shift, masked, wt):
     (256, 8, 0, -np.inf, [(8, 16), (9, 13)]),     # SCUNet body; a ragged last row block
     (192, 12, 6, -100.0, [(12, 24)]),             # Swin-T stage 2
     (384, 12, 0, -100.0, [(12, 12)]),             # Swin-T stage 3 (MLP through the row products)
+    (768, 12, 6, -100.0, [(16, 16)]),             # Swin-T stage 4 of a 512 image: rows read three times
+    (384, 7, 3, -100.0, [(10, 9)]),               # the reference's stage 3 window, rows read three times
 ])
 def test_swin_block(ctx, oracle, c, window, shift, masked, sizes):
     import torch
