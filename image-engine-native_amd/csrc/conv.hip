@@ -47,7 +47,7 @@
 namespace ien {
 
 template <int KS, int S, int TR, int TC, int MSPLIT, int NBW, int CK, bool VEC, bool IN_NCHW,
-          bool DB = false>
+          bool DB = false, int NBUF = 2>
 struct ConvCfg {
   static constexpr int NSPLIT = 4 / MSPLIT;
   static constexpr int BN = 32 * NBW * NSPLIT;
@@ -82,7 +82,7 @@ struct ConvCfg {
   static constexpr int STAGE_NCHW = NBW * 32 * (MBW * 32 + 4);
   static constexpr int STAGE = STAGE_NHWC > STAGE_NCHW ? STAGE_NHWC : STAGE_NCHW;
   static constexpr int MAIN_BYTES = HALO_BYTES + B_BYTES;
-  static constexpr int BUFS = DB ? 2 : 1;
+  static constexpr int BUFS = DB ? NBUF : 1;
   static constexpr int LDS_BYTES =
       BUFS * MAIN_BYTES > 4 * STAGE * 4 ? BUFS * MAIN_BYTES : 4 * STAGE * 4;
   // Direct-to-LDS loads per wave and chunk (DB): the halo's KiBs (NHWC)
@@ -94,7 +94,8 @@ struct ConvCfg {
   static constexpr int NITEMS = (NGROUPS + 255) / 256;
   // (Double buffering takes 16-channel steps: NHWC through direct-to-LDS
   // loads, NCHW through registers.)
-  static constexpr bool FITS = (!DB || VEC) && LDS_BYTES <= 160 * 1024 && DW < 64;
+  static constexpr bool FITS = (!DB || VEC) && (NBUF == 2 || DMA) && LDS_BYTES <= 160 * 1024 &&
+                               (NBUF - 1) * DW < 64;
   static_assert(MB % MSPLIT == 0, "M-blocks must split evenly over waves");
   static_assert(TC % 32 == 0, "tile columns are whole M-blocks");
   static_assert(!VEC || CK % 16 == 0, "16-channel steps");
@@ -120,9 +121,9 @@ __device__ __forceinline__ int swz_slot(int p, int c) {
 }
 
 template <int KS, int S, int TR, int TC, int MSPLIT, int NBW, int CK, bool VEC, bool IN_NCHW,
-          bool DB = false>
+          bool DB = false, int NBUF = 2>
 __global__ __launch_bounds__(256) void conv_mfma(ConvArgs a) {
-  using Cfg = ConvCfg<KS, S, TR, TC, MSPLIT, NBW, CK, VEC, IN_NCHW, DB>;
+  using Cfg = ConvCfg<KS, S, TR, TC, MSPLIT, NBW, CK, VEC, IN_NCHW, DB, NBUF>;
   constexpr int HR = Cfg::HR, HC = Cfg::HC, CKP = Cfg::CKP, MBW = Cfg::MBW, NBT = Cfg::NBT;
   constexpr int KSTEPS = Cfg::KSTEPS;
   constexpr int P = KS == 0 ? 0 : KS / 2;
@@ -416,18 +417,25 @@ __global__ __launch_bounds__(256) void conv_mfma(ConvArgs a) {
         dma_lds(wrs, __builtin_amdgcn_readfirstlane(bb + Cfg::HALO_BYTES + f * 1024), off);
       }
     };
-    if (c_begin < c_end) issue(c_begin, 0);
-    int i = 0;
-    for (int c0 = c_begin; c0 < c_end; c0 += CK, i++) {
-      const bool next = c0 + CK < c_end;  // uniform
-      if (next) issue(c0 + CK, (i + 1) & 1);
-      if (next)
+    // NBUF buffers: NBUF - 1 chunks in flight while one is multiplied.
+    const int nchunks = (c_end - c_begin + CK - 1) / CK;
+#pragma unroll
+    for (int q = 0; q < NBUF - 1; q++)
+      if (q < nchunks) issue(c_begin + q * CK, q);
+    for (int i = 0; i < nchunks; i++) {
+      if (i + NBUF - 1 < nchunks) issue(c_begin + (i + NBUF - 1) * CK, (i + NBUF - 1) % NBUF);
+      // Loads complete in order: chunk i is in once at most the later
+      // chunks' loads are outstanding.
+      const int ahead = min(NBUF - 1, nchunks - 1 - i);  // uniform
+      if (NBUF > 2 && ahead >= 2)
+        wait_vm<(NBUF > 2 ? 2 * Cfg::DW : 0)>();
+      else if (ahead == 1)
         wait_vm<Cfg::DW>();
       else
         wait_vm<0>();
       __syncthreads();  // chunk i is in every wave's view
-      compute(lds_raw + (i & 1) * Cfg::MAIN_BYTES, CK);
-      __syncthreads();  // every wave is done with buffer i % 2 before chunk i + 2 fills it
+      compute(lds_raw + (i % NBUF) * Cfg::MAIN_BYTES, CK);
+      __syncthreads();  // every wave is done with buffer i % NBUF before chunk i + NBUF fills it
     }
   } else {
     for (int c0 = c_begin; c0 < c_end; c0 += CK) {
@@ -1146,7 +1154,24 @@ static ien_status run_cfg(ien_ctx *ctx, ConvArgs a) {
   }
   a.kchunks = (chunks + ksplit - 1) / ksplit;
   a.ksplit = (chunks + a.kchunks - 1) / a.kchunks;
+  // Three chunk buffers (two chunks in flight) where a workgroup runs at
+  // least three chunks and as many workgroups still fit a CU.
+  bool db3 = false;
+  if constexpr (VEC && KS > 0 && ConvCfg<KS, S, TR, TC, MSPLIT, NBW, CK, VEC, IN_NCHW, true, 3>::FITS) {
+    constexpr int FIT3 =
+        160 * 1024 / ConvCfg<KS, S, TR, TC, MSPLIT, NBW, CK, VEC, IN_NCHW, true, 3>::LDS_BYTES;
+    db3 = db && a.kchunks >= 3 && blocks * a.ksplit <= (long)ctx->cus * FIT3;
+  }
   auto launch = [&](const ConvArgs &la, dim3 grid) -> ien_status {
+    if constexpr (VEC && KS > 0 &&
+                  ConvCfg<KS, S, TR, TC, MSPLIT, NBW, CK, VEC, IN_NCHW, true, 3>::FITS) {
+      if (db3) {
+        hipLaunchKernelGGL((conv_mfma<KS, S, TR, TC, MSPLIT, NBW, CK, VEC, IN_NCHW, true, 3>), grid,
+                           dim3(256), 0, ctx->stream, la);
+        IEN_HIP(hipGetLastError());
+        return IEN_OK;
+      }
+    }
     if constexpr (VEC && KS > 0 &&
                   ConvCfg<KS, S, TR, TC, MSPLIT, NBW, CK, VEC, IN_NCHW, true>::FITS) {
       if (db) {
