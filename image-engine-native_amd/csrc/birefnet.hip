@@ -231,25 +231,47 @@ struct FullParams {
   float bias_out, head_bias;
 };
 
-// decoder.rs:637-757 FullResolution::add with the head bias: 16 x 16 pixel
-// tiles, one thread a pixel, the tile's image patch with two pixels around
-// it (zeros outside the image) staged in LDS as three planes.
+// decoder.rs:637-757 FullResolution::add with the head bias.  One
+// workgroup per 32 x 32 pixel tile; the tile's image patch with two pixels
+// around it (zeros outside the image) staged in LDS as three planes.
 //  - Pixels off the image's edge ring: the composed 5x5 convolution
-//    (composed_row: the bias, then each tap's three products in order).
-//  - Tiles on the image's border then compute their ring pixels exactly
-//    (decoder.rs:700-734 exact: conv1 + bias1 at each in-image neighbour,
-//    the intermediate map's zero padding reached, then conv_out): the ring
-//    pixels are numbered within the tile, and 16 threads take one, each
-//    holding 4 of the 64 intermediate channels over the neighbours; a
-//    16-lane sum adds them.
-constexpr int FT = 16, FP = FT + 4;
+//    (composed_row: the bias, then each tap's three products in order),
+//    four neighbouring pixels a thread, which share each tap row's reads.
+//  - The edge ring's pixels are computed exactly (decoder.rs:700-734: conv1
+//    + bias1 at each in-image neighbour, the intermediate map's zero
+//    padding reached, then conv_out), dealt over all workgroups, four at a
+//    time (one a wave): lane k takes intermediate channel k over the
+//    neighbours, and a 64-lane sum adds the channels.  (The ring left to
+//    the border tiles alone had made them take 80 us against a few for
+//    the others.)
+constexpr int FT = 32, FP = FT + 4;
 __global__ __launch_bounds__(256) void k_full_res(const float *__restrict__ image, int side,
                                                   FullParams f, float *__restrict__ out) {
-  __shared__ float patch[3][FP][FP];
-  __shared__ int ring_count[4];
-  __shared__ short ring_pixel[2 * FT];
-  const int t = threadIdx.x, ly = t / FT, lx = t % FT;
-  const int y0 = blockIdx.y * FT, x0 = blockIdx.x * FT;
+  __shared__ __attribute__((aligned(16))) float patch[3][FP][FP];
+  __shared__ float rpatch[4][3][5][5];  // each wave's ring pixel's 5 x 5 window
+  const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
+  const int tiles = side / FT;
+  const int y0 = (int)(blockIdx.x / tiles) * FT, x0 = (int)(blockIdx.x % tiles) * FT;
+  // Ring pixels r of this workgroup: per = ceil(ring / workgroups), taken
+  // four at a time; ring order: the top row left to right, the right
+  // column down, the bottom row right to left, the left column up.
+  const int ring = 4 * (side - 1), per = (ring + (int)gridDim.x - 1) / (int)gridDim.x;
+  auto ring_pos = [&](int r, int &ry, int &rx) {
+    const int e = side - 1;
+    if (r < e) {
+      ry = 0;
+      rx = r;
+    } else if (r < 2 * e) {
+      ry = r - e;
+      rx = e;
+    } else if (r < 3 * e) {
+      ry = e;
+      rx = e - (r - 2 * e);
+    } else {
+      ry = e - (r - 3 * e);
+      rx = 0;
+    }
+  };
   for (int i = t; i < FP * FP; i += 256) {
     const int py = y0 - 2 + i / FP, px = x0 - 2 + i % FP;
     const bool in = py >= 0 && px >= 0 && py < side && px < side;
@@ -258,60 +280,75 @@ __global__ __launch_bounds__(256) void k_full_res(const float *__restrict__ imag
     for (int c = 0; c < 3; c++) patch[c][i / FP][i % FP] = in ? p[c] : 0.0f;
   }
   __syncthreads();
-  const int y = y0 + ly, x = x0 + lx;
-  const bool ring = y == 0 || x == 0 || y == side - 1 || x == side - 1;
-  if (!ring) {
-    float s = f.composed[75];
-    for (int e = 0; e < 25; e++) {
-      const int py = ly + e / 5, px = lx + e % 5;
-      s += f.composed[3 * e] * patch[0][py][px] + f.composed[3 * e + 1] * patch[1][py][px] +
-           f.composed[3 * e + 2] * patch[2][py][px];
-    }
-    out[(long)y * side + x] = f.head_bias + s;
-  }
-  if (blockIdx.x != 0 && blockIdx.y != 0 && blockIdx.x + 1 != gridDim.x && blockIdx.y + 1 != gridDim.y)
-    return;  // the whole tile is off the ring
-  const int wave = t / 64, lane = t % 64;
-  const unsigned long long mask = __ballot(ring);
-  if (lane == 0) ring_count[wave] = __popcll(mask);
-  __syncthreads();
-  int before = 0, rings = 0;
-  for (int w = 0; w < 4; w++) {
-    before += w < wave ? ring_count[w] : 0;
-    rings += ring_count[w];
-  }
-  if (ring) ring_pixel[before + __popcll(mask & ((1ull << lane) - 1))] = (short)t;
-  __syncthreads();
-  const int g = t % 16;
-  for (int r0 = 0; r0 < rings; r0 += 16) {
-    const int r = r0 + t / 16;
-    float v = 0.0f;
-    int ry = 0, rx = 0;
-    if (r < rings) {
-      const int pt = ring_pixel[r], py = pt / FT, px = pt % FT;
-      ry = y0 + py;
-      rx = x0 + px;
-      for (int d = 0; d < 9; d++) {
-        const int qy = ry + d / 3 - 1, qx = rx + d % 3 - 1;
-        if (qy < 0 || qx < 0 || qy >= side || qx >= side) continue;
+
+  // ---- off the ring: thread t, row t / 8, pixels 4 (t % 8) .. + 3 ----
+  {
+    const int ly = t >> 3, lx = (t & 7) * 4;
+    const int y = y0 + ly;
+    float s[4];
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-          const int k = g + 16 * j;
-          float m = f.bias1[k];
-          for (int e = 0; e < 9; e++) {
-            const int sy = py + d / 3 + e / 3, sx = px + d % 3 + e % 3;
+    for (int q = 0; q < 4; q++) s[q] = f.composed[75];
 #pragma unroll
-            for (int c = 0; c < 3; c++) m += patch[c][sy][sx] * f.conv1[(e * 3 + c) * INTER + k];
-          }
-          v += m * f.conv_out[d * INTER + k];
-        }
+    for (int dy = 0; dy < 5; dy++) {
+      float row[3][8];
+#pragma unroll
+      for (int c = 0; c < 3; c++) {
+        const float4 a = *(const float4 *)&patch[c][ly + dy][lx];
+        const float4 b = *(const float4 *)&patch[c][ly + dy][lx + 4];
+        row[c][0] = a.x; row[c][1] = a.y; row[c][2] = a.z; row[c][3] = a.w;
+        row[c][4] = b.x; row[c][5] = b.y; row[c][6] = b.z; row[c][7] = b.w;
+      }
+#pragma unroll
+      for (int dx = 0; dx < 5; dx++) {
+        const int e = dy * 5 + dx;
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+          s[q] += f.composed[3 * e] * row[0][q + dx] + f.composed[3 * e + 1] * row[1][q + dx] +
+                  f.composed[3 * e + 2] * row[2][q + dx];
       }
     }
-    v += __shfl_xor(v, 8);
-    v += __shfl_xor(v, 4);
-    v += __shfl_xor(v, 2);
-    v += __shfl_xor(v, 1);
-    if (r < rings && g == 0) out[(long)ry * side + rx] = f.head_bias + (f.bias_out + v);
+    float *o = out + (long)y * side + x0 + lx;
+    const bool edge_row = y == 0 || y == side - 1;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      const int x = x0 + lx + q;
+      if (!edge_row && x != 0 && x != side - 1) o[q] = f.head_bias + s[q];
+    }
+  }
+
+  // ---- the ring: wave w takes pixel r = blockIdx.x per + 4 i + w ----
+  for (int i = 0; i < per; i += 4) {
+    const int r = (int)blockIdx.x * per + i + wave;
+    const bool live = i + wave < per && r < ring;  // uniform per wave
+    int ry = 0, rx = 0;
+    if (live) ring_pos(r, ry, rx);
+    __syncthreads();  // (the previous round's windows are read)
+    if (live)
+      for (int j = lane; j < 75; j += 64) {  // 3 x 25 values over the wave's 64 lanes
+        const int c = j / 25, e = j % 25;
+        const int py = ry - 2 + e / 5, px = rx - 2 + e % 5;
+        const bool in = py >= 0 && px >= 0 && py < side && px < side;
+        rpatch[wave][c][e / 5][e % 5] = in ? image[((long)py * side + px) * 3 + c] : 0.0f;
+      }
+    __syncthreads();
+    if (!live) continue;
+    const int k = lane;
+    float v = 0.0f;
+    for (int d = 0; d < 9; d++) {
+      const int qy = ry + d / 3 - 1, qx = rx + d % 3 - 1;
+      if (qy < 0 || qx < 0 || qy >= side || qx >= side) continue;
+      float m = f.bias1[k];
+#pragma unroll
+      for (int e = 0; e < 9; e++) {
+        const int sy = d / 3 + e / 3, sx = d % 3 + e % 3;
+#pragma unroll
+        for (int c = 0; c < 3; c++) m += rpatch[wave][c][sy][sx] * f.conv1[(e * 3 + c) * INTER + k];
+      }
+      v += m * f.conv_out[d * INTER + k];
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+    if (lane == 0) out[(long)ry * side + rx] = f.head_bias + (f.bias_out + v);
   }
 }
 
@@ -926,7 +963,7 @@ ien_status birefnet_enqueue(Birefnet *b, const float *d_image, size_t side_, flo
   if (st != IEN_OK) return st;
   const FullParams fp{b->d_full, b->d_full + 76, b->d_full + 76 + 27 * INTER,
                       b->d_full + 76 + 28 * INTER, b->bias_out, b->head_bias};
-  hipLaunchKernelGGL(k_full_res, dim3((unsigned)(side / FT), (unsigned)(side / FT)), dim3(256), 0,
+  hipLaunchKernelGGL(k_full_res, dim3((unsigned)((side / FT) * (side / FT))), dim3(256), 0,
                      ctx->stream, d_image, side, fp, d_logits);
   IEN_HIP(hipGetLastError());
   st = ien_resize(ctx, b->low, prev_grid, prev_grid, 1, 1, d_logits, side, side, 1, IEN_OUT_F32, 1);
