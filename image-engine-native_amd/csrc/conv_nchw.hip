@@ -1,6 +1,7 @@
-// conv_nchw.hip -- 1x1 products of NCHW f16 maps into NCHW f16 maps on
-// gfx950 (gemm.rs:514-667 multiply on an Image input of one tap, channel
-// planes in and out): Y[n][p] = act(sum_c W[c][n] X[c][p] + b[n]).
+// conv_nchw.hip -- 1x1 products and 3x3 64 -> 64 convolutions of NCHW f16
+// maps into NCHW f16 maps on gfx950 (gemm.rs:514-667 multiply on an Image
+// input, channel planes in and out): Y[n][p] = act(sum_c W[c][n] X[c][p] +
+// b[n]) for one tap; the 3x3 kernel is further down.
 //
 // NCHW puts the pixels of one channel next to each other, while an MFMA
 // operand needs eight consecutive reduction (channel) values in a lane.  The
@@ -148,6 +149,202 @@ __global__ __launch_bounds__(256) void k_nchw1(NchwArgs a) {
   }
 }
 
+
+// ---- 3x3 convolutions of 64 channels into 64 (NCHW in and out) ----
+//
+// One workgroup of 4 waves per tile of 4 output rows x 96 pixels, the
+// layer's whole K: its 72 KiB of weight fragments (both 32-channel output
+// blocks, 36 k steps each) land straight in LDS, and the tile's 6 x 98
+// pixel halo is transposed in registers (4 channels x 8 pixels -> 8 pixels
+// x 4 channels, as k_nchw1 does) into a pixel-major LDS tile of 144-byte
+// pixels, whose 32 consecutive pixels are an A fragment read without bank
+// conflicts.  Wave w computes tile row w: 3 pixel blocks x 2 channel
+// blocks, so each k step reads 5 fragments for 6 MFMAs.
+//
+// K runs in two channel halves (taps, then 16-channel steps within each,
+// the general kernel's order for 32-channel chunks): both halves' loads
+// are issued at once, and the second half's pixels are transposed after
+// the first half's products, which hide its loads.  Results are staged in
+// LDS (where the halo was) and leave as 16-byte stores along pixel rows.
+constexpr int N3_TR = 4, N3_TC = 96, N3_HR = 6, N3_HC = 98, N3_GROUPS = 14;
+constexpr int N3_PX = 72;  // halves per halo pixel: 64 channels + 8 of padding
+// Halves per halo row: 16 past the pixels, so that rows 2 k and 2 k + 1
+// sit 16 banks apart (their halves of one transpose write share a cycle).
+constexpr int N3_RP = N3_HC * N3_PX + 16;
+constexpr int N3_HALO = N3_HR * N3_RP * 2;             // 84864
+constexpr int N3_WFRAGS = 2 * 36;                      // 2 channel blocks x 36 k steps
+constexpr int N3_LDS = N3_HALO + N3_WFRAGS * 1024;     // 158592
+constexpr int N3_UNITS = N3_HR * N3_GROUPS * 8;        // per half: (row, 8-pixel group, channel quad)
+constexpr int N3_ITEMS = (N3_UNITS + 255) / 256;
+constexpr int N3_YP = N3_TC + 8;                       // halves per staged output row
+static_assert(N3_HALO % 1024 == 0 || N3_HALO % 16 == 0, "fragments 16-byte aligned");
+static_assert(N3_LDS <= 160 * 1024, "LDS budget");
+static_assert(N3_GROUPS * 8 >= N3_HC + 7, "groups cover the halo columns");
+static_assert(N3_TR * 64 * N3_YP * 2 <= N3_HALO, "output staging within the halo");
+static_assert(N3_HR % 2 == 0, "row pairs");
+
+struct Nchw3Args {
+  const uint16_t *x;
+  int xs, H, W;  // plane stride (halves), map size (W a multiple of 8)
+  const uint16_t *wp;
+  int KB;
+  const uint16_t *zeros;
+  const float *bias, *slope;
+  uint16_t *y;
+  int ys;
+  int tiles_x, tiles;
+};
+
+template <int ACT>
+__global__ __launch_bounds__(256) void k_nchw3(Nchw3Args a) {
+  __shared__ __attribute__((aligned(1024))) unsigned char lds[N3_LDS];
+  uint16_t *halo = (uint16_t *)lds;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, col = lane & 31, hi = lane >> 5;
+  const int t = xcd_remap(blockIdx.x, a.tiles);
+  const int y0 = (t / a.tiles_x) * N3_TR, x0 = (t % a.tiles_x) * N3_TC;
+
+  float bias[2], slope[2];
+#pragma unroll
+  for (int nb = 0; nb < 2; nb++) {
+    bias[nb] = a.bias[32 * nb + col];
+    slope[nb] = ACT == IEN_ACT_PRELU ? a.slope[32 * nb + col] : 0.0f;
+  }
+
+  // Half h's weight fragments: blocks nb, taps, its two 16-channel steps
+  // (fragment nb KB + 4 tap + 2 h + g of the packed matrix), 9 a wave,
+  // straight into LDS at the same fragment index.
+  const int4v wrs = uniform_rsrc(a.wp, 72L * 1024);
+  const unsigned wlds = lds_addr(lds + N3_HALO);
+  const int wv = __builtin_amdgcn_readfirstlane(wave);  // in SGPRs: the LDS base is one
+  auto dma_w = [&](int h) {
+#pragma unroll
+    for (int i = 0; i < 9; i++) {
+      const int e = 4 * i + wv, nb = e / 18, tg = e % 18;
+      const int f = nb * 36 + (tg >> 1) * 4 + 2 * h + (tg & 1);
+      dma_lds(wrs, wlds + f * 1024, f * 1024 + lane * 16);
+    }
+  };
+  // Half h's halo units: rows 2 p + rr (input row y0 - 1 + that), group g
+  // (input pixels x0 - 8 + 8 g ..+ 7), channels 32 h + 4 q ..+ 3.  Lanes
+  // 0-7 of each 16 take the quads of one row, 8-15 the next row's, so a
+  // transpose write of 16 lanes fills 32 distinct banks.  Groups outside
+  // the map read the zero page.
+  u32x4 v[2][N3_ITEMS][4];
+  auto unit = [&](int u, int &r, int &g, int &q) {
+    q = u & 7;
+    const int rr = (u >> 3) & 1, gp = u >> 4, p = gp / N3_GROUPS;
+    g = gp - p * N3_GROUPS;
+    r = 2 * p + rr;
+  };
+  auto load_x = [&](int h) {
+#pragma unroll
+    for (int j = 0; j < N3_ITEMS; j++) {
+      int r, g, q;
+      const int u = tid + 256 * j;
+      unit(u, r, g, q);
+      const int iy = y0 - 1 + r, gx = x0 - 8 + 8 * g;
+      const bool ok = u < N3_UNITS && iy >= 0 && iy < a.H && gx >= 0 && gx < a.W;
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+        v[h][j][i] = *(const u32x4 *)(ok ? a.x + (long)(32 * h + 4 * q + i) * a.xs +
+                                               (long)iy * a.W + gx
+                                         : a.zeros);
+    }
+  };
+  auto store_x = [&](int h) {
+#pragma unroll
+    for (int j = 0; j < N3_ITEMS; j++) {
+      int r, g, q;
+      const int u = tid + 256 * j;
+      unit(u, r, g, q);
+      // Pixel e of the group is halo column 8 g + e - 7.
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        const int hc = 8 * g + e - 7;
+        const unsigned sel = (e & 1) ? 0x07060302u : 0x05040100u;
+        uint2 o;
+        o.x = __builtin_amdgcn_perm(v[h][j][1][e >> 1], v[h][j][0][e >> 1], sel);
+        o.y = __builtin_amdgcn_perm(v[h][j][3][e >> 1], v[h][j][2][e >> 1], sel);
+        if (u < N3_UNITS && hc >= 0 && hc < N3_HC)
+          *(uint2 *)(halo + r * N3_RP + hc * N3_PX + 32 * h + 4 * q) = o;
+      }
+    }
+  };
+
+  // Row `wave` of the tile: pixel blocks b (32 b ..+ 31), channel blocks nb.
+  floatx16 acc[3][2] = {};
+  const uint16_t *ab = halo + wave * N3_RP + col * N3_PX + 8 * hi;
+  const uint16_t *wb = (const uint16_t *)(lds + N3_HALO) + lane * 8;
+  auto products = [&](int h) {
+    // Step s: tap s / 2, channels 32 h + 16 (s % 2) ..+ 15.
+    auto frag = [&](int s, half8 *av, half8 *bv) {
+      const int tap = s >> 1, g = 2 * h + (s & 1), dy = tap / 3, dx = tap % 3;
+#pragma unroll
+      for (int b = 0; b < 3; b++)
+        av[b] = *(const half8 *)(ab + dy * N3_RP + (32 * b + dx) * N3_PX + 16 * g);
+#pragma unroll
+      for (int nb = 0; nb < 2; nb++) bv[nb] = *(const half8 *)(wb + (nb * 36 + tap * 4 + g) * 512);
+    };
+    half8 av[2][3], bv[2][2];
+    frag(0, av[0], bv[0]);
+#pragma unroll
+    for (int s = 0; s < 18; s++) {
+      if (s + 1 < 18) frag(s + 1, av[(s + 1) & 1], bv[(s + 1) & 1]);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int b = 0; b < 3; b++)
+#pragma unroll
+        for (int nb = 0; nb < 2; nb++)
+          acc[b][nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[s & 1][b], bv[s & 1][nb],
+                                                              acc[b][nb], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  dma_w(0);
+  load_x(0);
+  dma_w(1);
+  load_x(1);
+  wait_vm<9 + 4 * N3_ITEMS>();  // half 0's fragments and pixels have landed
+  store_x(0);
+  lds_barrier();
+  products(0);
+  wait_vm<0>();
+  store_x(1);
+  lds_barrier();
+  products(1);
+  lds_barrier();  // every wave is done with the halo: it becomes the output staging
+
+  // D[pixel][channel]: accumulator r holds pixel 8 (r / 4) + 4 hi + r % 4
+  // of the block, channel col; staged [row][channel][pixel].
+  uint16_t *ys = halo + wave * 64 * N3_YP;
+#pragma unroll
+  for (int b = 0; b < 3; b++)
+#pragma unroll
+    for (int nb = 0; nb < 2; nb++)
+#pragma unroll
+      for (int r4 = 0; r4 < 4; r4++) {
+        uint2 o;
+        const float v0 = act_c<ACT>(acc[b][nb][4 * r4 + 0] + bias[nb], slope[nb]);
+        const float v1 = act_c<ACT>(acc[b][nb][4 * r4 + 1] + bias[nb], slope[nb]);
+        const float v2 = act_c<ACT>(acc[b][nb][4 * r4 + 2] + bias[nb], slope[nb]);
+        const float v3 = act_c<ACT>(acc[b][nb][4 * r4 + 3] + bias[nb], slope[nb]);
+        o.x = (uint32_t)f2h(v0) | ((uint32_t)f2h(v1) << 16);
+        o.y = (uint32_t)f2h(v2) | ((uint32_t)f2h(v3) << 16);
+        *(uint2 *)(ys + (32 * nb + col) * N3_YP + 32 * b + 8 * r4 + 4 * hi) = o;
+      }
+  lds_barrier();
+  // 12 16-byte pieces per (row, channel): 3072 a tile, 12 a thread.
+#pragma unroll
+  for (int i = 0; i < N3_TR * 64 * 12 / 256; i++) {
+    const int e = tid + 256 * i, k = e % 12, rn = e / 12, row = rn >> 6, n = rn & 63;
+    const int oy = y0 + row, ox = x0 + 8 * k;
+    if (oy < a.H && ox < a.W)
+      *(u32x4 *)(a.y + (long)n * a.ys + (long)oy * a.W + ox) =
+          *(const u32x4 *)(halo + rn * N3_YP + 8 * k);
+  }
+}
+
 }  // namespace
 
 bool nchw1_supported(const ConvArgs &a, int ks, int stride, long rows) {
@@ -170,6 +367,33 @@ ien_status launch_nchw1(ien_ctx *ctx, const ConvArgs &a) {
       hipLaunchKernelGGL(k_nchw1<IEN_ACT_SIGMOID>, grid, dim3(256), 0, ctx->stream, n);
       break;
     default: hipLaunchKernelGGL(k_nchw1<IEN_ACT_NONE>, grid, dim3(256), 0, ctx->stream, n); break;
+  }
+  IEN_HIP(hipGetLastError());
+  return IEN_OK;
+}
+
+bool nchw3_supported(const ConvArgs &a, int ks, int stride, long rows) {
+  const long P = (long)a.H * a.W;
+  return ks == 3 && stride == 1 && a.C == 64 && a.N == 64 && a.KB == 36 && !a.rows_mode &&
+         !a.pad_reflect && a.noff == 0 && a.out_nchw && !a.out_f32 && !a.accumulate &&
+         a.p_begin == 0 && rows == P && a.OH == a.H && a.OW == a.W && a.W % 8 == 0 &&
+         a.xs % 8 == 0 && a.ys % 8 == 0 && (((uintptr_t)a.x | (uintptr_t)a.y) & 15) == 0 &&
+         a.xs >= P && a.ys >= P && 64L * a.xs < (1L << 31) && 64L * a.ys < (1L << 31);
+}
+
+ien_status launch_nchw3(ien_ctx *ctx, const ConvArgs &a) {
+  Nchw3Args n{a.x, a.xs, a.H, a.W, a.wp, a.KB, a.zeros, a.bias, a.slope, (uint16_t *)a.y, a.ys,
+              (a.W + N3_TC - 1) / N3_TC, 0};
+  n.tiles = n.tiles_x * ((a.H + N3_TR - 1) / N3_TR);
+  const dim3 grid((unsigned)n.tiles);
+  switch (a.act) {
+    case IEN_ACT_RELU: hipLaunchKernelGGL(k_nchw3<IEN_ACT_RELU>, grid, dim3(256), 0, ctx->stream, n); break;
+    case IEN_ACT_GELU: hipLaunchKernelGGL(k_nchw3<IEN_ACT_GELU>, grid, dim3(256), 0, ctx->stream, n); break;
+    case IEN_ACT_PRELU: hipLaunchKernelGGL(k_nchw3<IEN_ACT_PRELU>, grid, dim3(256), 0, ctx->stream, n); break;
+    case IEN_ACT_SIGMOID:
+      hipLaunchKernelGGL(k_nchw3<IEN_ACT_SIGMOID>, grid, dim3(256), 0, ctx->stream, n);
+      break;
+    default: hipLaunchKernelGGL(k_nchw3<IEN_ACT_NONE>, grid, dim3(256), 0, ctx->stream, n); break;
   }
   IEN_HIP(hipGetLastError());
   return IEN_OK;

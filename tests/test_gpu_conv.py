@@ -214,6 +214,19 @@ def test_nchw_3x3_planes(ctx, oracle, h, w, c, n, act):
     close(run_gpu(ctx, x, wt, b, act=act, slope=slope, nchw_in=True, nchw_out=True), want)
 
 
+# The NCHW 3 x 3 64 -> 64 kernel (4 x 96 tiles, the layer's weights in
+# LDS): heights that leave a partial 4-row tile, widths (multiples of 8)
+# that leave a partial 96-pixel tile or fall short of one, every
+# activation.
+@pytest.mark.parametrize("h,w,act", [(4, 96, 0), (7, 200, 1), (13, 104, 3), (3, 8, 2), (10, 392, 4),
+                                     (33, 16, 3)])
+def test_nchw_3x3_64(ctx, oracle, h, w, act):
+    x, wt, b = case(90 + h + w, h, w, 64, 64, 9)
+    slope = np.linspace(-0.3, 0.3, 64).astype(np.float32)
+    want = want_cpu(oracle, x, wt, b, act=act, slope=slope)
+    close(run_gpu(ctx, x, wt, b, act=act, slope=slope, nchw_in=True, nchw_out=True), want)
+
+
 # Where that kernel does not apply, the general one runs: a row range, an
 # accumulating product, f32 outputs, pixel counts not a multiple of 8.
 def test_nchw_1x1_other_forms(ctx, oracle):
