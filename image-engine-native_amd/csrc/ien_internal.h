@@ -219,6 +219,20 @@ struct RowsPlanes {
 };
 ien_status launch_rows_planes(ien_ctx *ctx, const RowsPlanes &p);
 
+// join_split.hip: a SCUNet block boundary over `rows` pixels of a c-channel
+// map x (rows c apart), c = 64 or 128: x += join([yc | ysw]) + join bias,
+// rounded to f16, then [yc | ysw] = split(x) + split bias, the split map as
+// two planes of c / 2 channels (rows c / 2 apart), both updated in place.
+// The same bits as the two row products (the join accumulating onto x).
+struct JoinSplit {
+  uint16_t *yc = nullptr, *ysw = nullptr, *x = nullptr;
+  long rows = 0;
+  int c = 0;
+  const ien_matrix *join = nullptr, *split = nullptr;
+};
+bool join_split_supported(const JoinSplit &p);
+ien_status launch_join_split(ien_ctx *ctx, const JoinSplit &p);
+
 bool pair_supported(const PairCall &p);
 ien_status launch_pair(ien_ctx *ctx, const PairCall &p);
 

@@ -1,7 +1,8 @@
 // scunet.hip -- the SCUNet U-Net on the GPU (crates/scunet-native/src/
 // network.rs:113-354): f16 NHWC maps, the block's 3x3 convolutions and the
 // head and tail through the implicit-GEMM kernels, 1x1 products over pixel
-// rows, the Swin half through ien_swin, the 2x2 halving and doubling
+// rows (a block's join and the next block's split in one pass at 64 and
+// 128 channels), the Swin half through ien_swin, the 2x2 halving and doubling
 // convolutions as row products that gather / scatter 2 x 2 pixel groups
 // themselves.  One event is
 // recorded after each of the 28 blocks for progress reports.
@@ -175,8 +176,22 @@ ien_status run_level(Scunet &s, ScunetBlock *blocks, int h, int w, int c, Steps 
     }
     if (st == IEN_OK) st = ien_swin_run(B.swin, ysw, half, h, w);
     if (st == IEN_OK) st = join_branches(ctx, 1);
-    if (st == IEN_OK) st = join(B.join, b + 1 < BLOCKS ? nullptr : add_after);
-    if (st == IEN_OK && b + 1 < BLOCKS) st = split(blocks[b + 1].split);
+    // The join and the next block's split in one pass where it applies
+    // (64 and 128 channels), else as two row products.
+    JoinSplit js;
+    js.yc = yc;
+    js.ysw = ysw;
+    js.x = s.x;
+    js.rows = (long)pixels;
+    js.c = c;
+    js.join = B.join;
+    js.split = b + 1 < BLOCKS ? blocks[b + 1].split : nullptr;
+    if (st == IEN_OK && b + 1 < BLOCKS && join_split_supported(js)) {
+      st = launch_join_split(ctx, js);
+    } else {
+      if (st == IEN_OK) st = join(B.join, b + 1 < BLOCKS ? nullptr : add_after);
+      if (st == IEN_OK && b + 1 < BLOCKS) st = split(blocks[b + 1].split);
+    }
     if (st == IEN_OK && steps) st = steps->step(ctx->stream);
     ++*step;
   }
