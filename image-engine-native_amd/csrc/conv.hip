@@ -680,13 +680,21 @@ __global__ __launch_bounds__(256) void conv_mfma(ConvArgs a) {
                           (((uintptr_t)a.y) & 15) == 0;
     if (groups16) {
       uint16_t *yh = (uint16_t *)a.y;
-      u32x4 old[ITEMS];
+      u32x4 old[ITEMS], add[ITEMS];
       if (a.accumulate) {
 #pragma unroll
         for (int t = 0; t < ITEMS; t++) {
           int g;
           const long at = item_at(t, g);
           old[t] = *(const u32x4 *)(yh + (at >= 0 ? at : 0));
+        }
+      }
+      if (a.add2) {
+#pragma unroll
+        for (int t = 0; t < ITEMS; t++) {
+          int g;
+          const long at = item_at(t, g);
+          add[t] = *(const u32x4 *)(a.add2 + (at >= 0 ? at : 0));
         }
       }
       auto store = [&](auto actf) {
@@ -709,6 +717,12 @@ __global__ __launch_bounds__(256) void conv_mfma(ConvArgs a) {
           } else {
 #pragma unroll
             for (int e = 0; e < 8; e++) o[e] = f2h(v[e]);  // activated in the accumulators
+          }
+          if (a.add2) {
+            uint16_t ah[8];
+            __builtin_memcpy(ah, &add[t], 16);
+#pragma unroll
+            for (int e = 0; e < 8; e++) o[e] = f2h(h2f(o[e]) + h2f(ah[e]));
           }
           u32x4 ov;
           __builtin_memcpy(&ov, o, 16);
@@ -966,13 +980,23 @@ __global__ __launch_bounds__(256) void k_splitk_finish_nchw(const float *__restr
   }
 }
 
+// o[e] = f16(o[e] + add[e]) for 8 halves: the map added after the
+// activation and rounding, as ien_add adds it.
+__device__ __forceinline__ void add_after(uint16_t *o, const uint16_t *add) {
+  uint16_t h[8];
+  *(u32x4 *)h = *(const u32x4 *)add;
+#pragma unroll
+  for (int e = 0; e < 8; e++) o[e] = f2h(h2f(o[e]) + h2f(h[e]));
+}
+
 // The same for f16 NHWC outputs with 8-aligned widths and strides: 8
 // channels per thread, 16-byte loads and stores, one loop per activation.
 __global__ __launch_bounds__(256) void k_splitk_finish8(const float *__restrict__ part, int ksplit,
                                                         long rows, int pitch, int N,
                                                         const float *__restrict__ bias,
                                                         const float *__restrict__ slope, int act,
-                                                        int accumulate, uint16_t *y, long ys) {
+                                                        int accumulate, uint16_t *y, long ys,
+                                                        const uint16_t *add2) {
   const long i = (long)blockIdx.x * 256 + threadIdx.x;
   const int groups = N >> 3;
   if (i >= rows * groups) return;
@@ -1004,6 +1028,7 @@ __global__ __launch_bounds__(256) void k_splitk_finish8(const float *__restrict_
     case IEN_ACT_PRELU: out([&](float x, int e) { return act_c<IEN_ACT_PRELU>(x, slope[n + e]); }); break;
     default: out([&](float x, int) { return x; }); break;
   }
+  if (add2) add_after(o, add2 + p * ys + n);
   *(u32x4 *)yo = *(const u32x4 *)o;
 }
 
@@ -1016,7 +1041,8 @@ __global__ __launch_bounds__(256) void k_splitk_finish8_lanes(const float *__res
                                                               int ksplit, long rows, int pitch, int N,
                                                               const float *__restrict__ bias,
                                                               const float *__restrict__ slope, int act,
-                                                              int accumulate, uint16_t *y, long ys) {
+                                                              int accumulate, uint16_t *y, long ys,
+                                                              const uint16_t *add2) {
   const long i = ((long)blockIdx.x * 256 + threadIdx.x) / T;
   const int t = threadIdx.x & (T - 1);
   const int groups = N >> 3;
@@ -1058,10 +1084,14 @@ __global__ __launch_bounds__(256) void k_splitk_finish8_lanes(const float *__res
     case IEN_ACT_PRELU: out([&](float x, int e) { return act_c<IEN_ACT_PRELU>(x, slope[n + e]); }); break;
     default: out([&](float x, int) { return x; }); break;
   }
+  if (add2) add_after(o, add2 + p * ys + n);
   *(u32x4 *)yo = *(const u32x4 *)o;
 }
 
 ien_status splitk_finish(ien_ctx *ctx, int ksplit, long rows, int pitch, const ConvArgs &a) {
+  IEN_CHECK(!a.add2 || (!a.out_f32 && !a.out_nchw && a.N % 8 == 0 && pitch % 8 == 0 &&
+                        a.ys % 8 == 0 && (((uintptr_t)a.y | (uintptr_t)a.add2) & 15) == 0),
+            IEN_ERR_INPUT, "an added map needs whole 16-byte f16 groups");
   if (!a.out_f32 && !a.out_nchw && a.N % 8 == 0 && pitch % 8 == 0 && a.ys % 8 == 0 &&
       (((uintptr_t)a.y) & 15) == 0) {
     const long items = rows * (a.N / 8);
@@ -1074,13 +1104,13 @@ ien_status splitk_finish(ien_ctx *ctx, int ksplit, long rows, int pitch, const C
                                                                     : k_splitk_finish8_lanes<8>;
       hipLaunchKernelGGL(k, dim3((unsigned)((items * lanes + 255) / 256)), dim3(256), 0, ctx->stream,
                          (const float *)ctx->splitk, ksplit, rows, pitch, a.N, a.bias, a.slope, a.act,
-                         a.accumulate, (uint16_t *)a.y, (long)a.ys);
+                         a.accumulate, (uint16_t *)a.y, (long)a.ys, a.add2);
       IEN_HIP(hipGetLastError());
       return IEN_OK;
     }
     hipLaunchKernelGGL(k_splitk_finish8, dim3((unsigned)((items + 255) / 256)), dim3(256), 0,
                        ctx->stream, (const float *)ctx->splitk, ksplit, rows, pitch, a.N, a.bias,
-                       a.slope, a.act, a.accumulate, (uint16_t *)a.y, (long)a.ys);
+                       a.slope, a.act, a.accumulate, (uint16_t *)a.y, (long)a.ys, a.add2);
   } else if (a.out_nchw) {
     const dim3 grid((unsigned)((rows + 31) / 32), (unsigned)((a.N + 31) / 32));
     hipLaunchKernelGGL(k_splitk_finish_nchw, grid, dim3(256), 0, ctx->stream,
@@ -1214,6 +1244,7 @@ static ien_status run_cfg(ien_ctx *ctx, ConvArgs a) {
   pa.out_nchw = 0;
   pa.act = IEN_ACT_NONE;
   pa.accumulate = 0;
+  pa.add2 = nullptr;
   const ien_status st = launch(pa, dim3((unsigned)blocks, (unsigned)a.ksplit));
   if (st != IEN_OK) return st;
   return splitk_finish(ctx, a.ksplit, rows, pitch, a);
@@ -1270,6 +1301,7 @@ ien_status launch_conv(ien_ctx *ctx, const ConvCall &c) {
   a.out_f32 = c.out_f32;
   a.act = c.act;
   a.accumulate = c.accumulate;
+  a.add2 = c.add2;
 
   // 16-channel MFMA steps; NHWC halo loads of 16 bytes need aligned pixels.
   const bool vec = c.C % 16 == 0 && (nchw || (c.xs % 8 == 0 && ((uintptr_t)c.x & 15) == 0));
@@ -1278,6 +1310,13 @@ ien_status launch_conv(ien_ctx *ctx, const ConvCall &c) {
   return ck == 64 ? run_cfg<KS, S, TR, TC, 4, 2, 64, true, L>(ctx, a)              \
          : ck == 32 ? run_cfg<KS, S, TR, TC, 4, 2, 32, true, L>(ctx, a)            \
                     : run_cfg<KS, S, TR, TC, 4, 2, 16, true, L>(ctx, a)
+  // An added map: the general kernel's 16-byte f16 group epilogue (and its
+  // split-K finishing passes) only; the special kernels below are skipped.
+  IEN_CHECK(!c.add2 || (!nchw && !c.rows_mode && c.noff == 0 && c.ks == 3 && c.stride == 1 &&
+                        vec && !c.out_nchw && !c.out_f32 && c.ys % 8 == 0 && w->n % 8 == 0 &&
+                        (((uintptr_t)c.y | (uintptr_t)c.add2) & 15) == 0),
+            IEN_ERR_INPUT, "an added map needs an NHWC 3x3 product with whole 16-byte f16 groups");
+  const bool special = !c.add2;
   if (c.rows_mode) {
     // Input::Rows: a virtual image 32 pixels wide, rows in order.
     IEN_CHECK(!nchw && c.ks == 1 && c.noff == 0, IEN_ERR_INPUT, "rows are NHWC, one tap");
@@ -1301,12 +1340,13 @@ ien_status launch_conv(ien_ctx *ctx, const ConvCall &c) {
   // Four input channels (the models' image inputs) and few outputs (their
   // last convolutions): the general kernel would pad these to 16-channel
   // steps and 64-channel tiles.
-  if (narrow_supported(a, c.ks, c.stride, nchw, c.noff, c.rows_mode))
+  if (special && narrow_supported(a, c.ks, c.stride, nchw, c.noff, c.rows_mode))
     return launch_narrow(ctx, a, c.ks);
-  if (few_supported(a, c.ks, c.stride, nchw, c.noff, c.rows_mode)) return launch_few(ctx, a, c.ks);
+  if (special && few_supported(a, c.ks, c.stride, nchw, c.noff, c.rows_mode))
+    return launch_few(ctx, a, c.ks);
   // Resident weights: NHWC, zero padding, 16, 32 or 64 channels, K <= 640.
   // Its results are staged as f16: f32 outputs take the general kernel.
-  if (vec && !c.out_f32 &&
+  if (special && vec && !c.out_f32 &&
       resident_supported(c.ks, c.stride, c.C, nchw, c.pad_reflect, c.noff, c.rows_mode,
                          (long)c.H * c.W * c.xs * 2))
     return launch_resident(ctx, a, c.ks);

@@ -47,6 +47,9 @@ struct ConvArgs {
   int ksplit, kchunks;
   float *part;
   int *tile_count;
+  // NHWC f16 outputs in 16-byte groups: a map (rows ys apart) added to the
+  // rounded result and rounded again, or null.
+  const uint16_t *add2;
 };
 
 __device__ __forceinline__ int reflect_idx(int i, int n) {

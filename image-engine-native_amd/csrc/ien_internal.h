@@ -171,6 +171,10 @@ struct ConvCall {
   int act = IEN_ACT_NONE;
   const float *slope = nullptr;
   int accumulate = 0;
+  // Optional, NHWC f16 outputs of 3x3 stride-1 products only: a map (rows
+  // ys apart, 16-byte aligned) added to each f16 result after the
+  // activation, rounded again (the product followed by ien_add; it may be y).
+  const uint16_t *add2 = nullptr;
 };
 
 ien_status launch_conv(ien_ctx *ctx, const ConvCall &c);

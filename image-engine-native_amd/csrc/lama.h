@@ -48,8 +48,12 @@ bool spectral_shapes(const ien_matrix *in, const ien_matrix *f, const ien_matrix
 ien_status spectral_front(const ien_spectral *sp, const uint16_t *x, long xs,
                           const ien_matrix *m_in, const ien_matrix *m_f, uint16_t *spectral,
                           float *r, float *u);
+// The result (ReLU(out + spectral_out(spectral + irfft(u)))) goes to dst
+// (out when null), with `add` (rows ys apart, or null) added after the
+// rounding and rounded again.
 ien_status spectral_back(const ien_spectral *sp, const ien_matrix *m_out, const uint16_t *spectral,
-                         const float *u, uint16_t *out, long ys);
+                         const float *u, uint16_t *out, long ys, uint16_t *dst = nullptr,
+                         const uint16_t *add = nullptr);
 size_t spectral_r_floats(const ien_spectral *sp);
 size_t spectral_u_floats(const ien_spectral *sp);
 

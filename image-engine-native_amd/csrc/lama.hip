@@ -34,8 +34,9 @@ ien_status matrix(ien_ctx *ctx, const TensorSource &take, const std::string &nam
 // A size x size convolution (reflect padding) of an h x w f16 NHWC map.
 ien_status conv(ien_ctx *ctx, const uint16_t *x, int h, int w, int c, long xs, int size,
                 int step, const ien_matrix *m, uint16_t *y, long ys, ien_act act,
-                int accumulate) {
+                int accumulate, const uint16_t *add2 = nullptr) {
   ConvCall cc;
+  cc.add2 = add2;
   cc.x = x;
   cc.H = h;
   cc.W = w;
@@ -77,8 +78,14 @@ ien_status rows_product(ien_ctx *ctx, const uint16_t *in, size_t k, size_t rows,
   return launch_conv(ctx, cc);
 }
 
-// network.rs:174-249 Ffc::run: out = ffc(x), both h x w maps of 512.
-ien_status ffc_run(Lama *l, const LamaFfc &f, const uint16_t *x, uint16_t *out, int h, int w) {
+// network.rs:174-249 Ffc::run: out = ffc(x), both h x w maps of 512.  With
+// `residual` (the fused spectral branch only), the block's residual add
+// (network.rs:257-262, x += ffc1(ffc0(x))) runs in the last launches'
+// epilogues: the local part and the spectral back kernel add their rounded
+// results onto `residual` in place (the sums ien_add would make), and
+// `out` holds only the cross output the back kernel reads.
+ien_status ffc_run(Lama *l, const LamaFfc &f, const uint16_t *x, uint16_t *out, int h, int w,
+                   uint16_t *residual = nullptr) {
   ien_ctx *ctx = l->ctx;
   const size_t pixels = (size_t)h * w, half = (size_t)w / 2 + 1, spix = (size_t)h * half;
   // The local convolution, the cross convolution and the spectral chain
@@ -97,14 +104,16 @@ ien_status ffc_run(Lama *l, const LamaFfc &f, const uint16_t *x, uint16_t *out, 
                           l->spectral, (float *)l->spectrum, l->work);
     }
     if (st == IEN_OK)
-      st = conv(ctx, x, h, w, CHANNELS, CHANNELS, 3, 1, f.local, out, CHANNELS, IEN_ACT_RELU, 0);
+      st = conv(ctx, x, h, w, CHANNELS, CHANNELS, 3, 1, f.local, residual ? residual : out,
+                CHANNELS, IEN_ACT_RELU, 0, residual);
     if (st == IEN_OK)
       st = conv(ctx, x, h, w, LOCAL, CHANNELS, 3, 1, f.cross, out + LOCAL, CHANNELS, IEN_ACT_NONE,
                 0);
     if (st == IEN_OK) st = join_branches(ctx, 1);
     if (st == IEN_OK)
       st = spectral_back(l->spectral_plan, f.spectral_out, l->spectral, l->work, out + LOCAL,
-                         CHANNELS);
+                         CHANNELS, residual ? residual + LOCAL : nullptr,
+                         residual ? residual + LOCAL : nullptr);
     return st;
   }
   // Unfused: local on the context's stream, cross on branch 1, the spectral
@@ -343,8 +352,13 @@ ien_status lama_enqueue(Lama *l, const float *d_image, const float *d_mask, size
   const size_t eighth = (size_t)h * w;
   for (int b = 0; b < BLOCKS && st == IEN_OK; b++) {
     st = ffc_run(l, l->blocks[b][0], l->a, l->mid, h, w);
-    if (st == IEN_OK) st = ffc_run(l, l->blocks[b][1], l->mid, l->out, h, w);
-    if (st == IEN_OK) st = ien_add(ctx, l->a, l->out, eighth * CHANNELS);
+    if (l->spectral_plan) {
+      // The residual add in the second FFC's epilogues.
+      if (st == IEN_OK) st = ffc_run(l, l->blocks[b][1], l->mid, l->out, h, w, l->a);
+    } else {
+      if (st == IEN_OK) st = ffc_run(l, l->blocks[b][1], l->mid, l->out, h, w);
+      if (st == IEN_OK) st = ien_add(ctx, l->a, l->out, eighth * CHANNELS);
+    }
     if (st == IEN_OK) st = done();
   }
   // The ups write the quarter, half and full-scale maps again.

@@ -410,6 +410,10 @@ struct BackArgs {
   int kb_o;
   uint16_t *out;
   int ys;
+  // Where the result goes (rows ys apart, out's layout) and a map added to
+  // it after the ReLU and rounding, rounded again (or null).
+  uint16_t *dst;
+  const uint16_t *add;
 };
 
 constexpr int UP = MAX_SIDE + 8;
@@ -576,10 +580,24 @@ __global__ __launch_bounds__(256) void k_spectral_back(BackArgs p) {
   __syncthreads();
   // 16 lanes write one pixel's 256 bytes.
   {
-    uint16_t *og = p.out + (long)y * w * p.ys + NG * g;
-    for (int q = tid; q < 16 * w; q += 256) {
-      const int x = q >> 4, c = q & 15;
-      *(u32x4 *)(og + (long)x * p.ys + 8 * c) = *(const u32x4 *)(ob + x * OBP + 8 * c);
+    const long row = (long)y * w * p.ys + NG * g;
+    uint16_t *og = p.dst + row;
+    if (p.add) {
+      const uint16_t *ag = p.add + row;
+      for (int q = tid; q < 16 * w; q += 256) {
+        const int x = q >> 4, c = q & 15;
+        uint16_t o[8], h[8];
+        *(u32x4 *)o = *(const u32x4 *)(ob + x * OBP + 8 * c);
+        *(u32x4 *)h = *(const u32x4 *)(ag + (long)x * p.ys + 8 * c);
+#pragma unroll
+        for (int e = 0; e < 8; e++) o[e] = f2h(h2f(o[e]) + h2f(h[e]));
+        *(u32x4 *)(og + (long)x * p.ys + 8 * c) = *(const u32x4 *)o;
+      }
+    } else {
+      for (int q = tid; q < 16 * w; q += 256) {
+        const int x = q >> 4, c = q & 15;
+        *(u32x4 *)(og + (long)x * p.ys + 8 * c) = *(const u32x4 *)(ob + x * OBP + 8 * c);
+      }
     }
   }
 }
@@ -661,10 +679,13 @@ ien_status spectral_front(const ien_spectral *sp, const uint16_t *x, long xs,
 }
 
 ien_status spectral_back(const ien_spectral *sp, const ien_matrix *m_out, const uint16_t *spectral,
-                         const float *u, uint16_t *out, long ys) {
+                         const float *u, uint16_t *out, long ys, uint16_t *dst,
+                         const uint16_t *add) {
   ien_ctx *ctx = sp->ctx;
+  IEN_CHECK((((uintptr_t)dst | (uintptr_t)add) & 15) == 0, IEN_ERR_INPUT,
+            "spectral output and added map 16-byte aligned");
   BackArgs b{u, sp->h, sp->w, sp->half, sp->xp, sp->nbx, sp->d_tr, spectral, m_out->d_packed,
-             m_out->kb, out, (int)ys};
+             m_out->kb, out, (int)ys, dst ? dst : out, add};
   hipLaunchKernelGGL(k_spectral_back, dim3((unsigned)sp->h, BACK_GROUPS), dim3(256), 0,
                      ctx->stream, b);
   IEN_HIP(hipGetLastError());
@@ -784,7 +805,8 @@ ien_status ien_spectral_run(const ien_spectral *sp, const uint16_t *d_x, size_t 
             SPEC2);
   float *r = d_work, *u = d_work + spectral_r_floats(sp);
   ien_status st = spectral_front(sp, d_x, (long)stride, spectral_in, fourier, d_spectral, r, u);
-  if (st == IEN_OK) st = spectral_back(sp, spectral_out, d_spectral, u, d_out, (long)out_stride);
+  if (st == IEN_OK)
+    st = spectral_back(sp, spectral_out, d_spectral, u, d_out, (long)out_stride, nullptr, nullptr);
   return st;
 }
 
