@@ -13,9 +13,9 @@
 //    integer taps with modulator 2 sigmoid(0) = 1, decoder.rs:254-313) or,
 //    where a branch's offsets are not zero, its offset convolution, the
 //    bilinear samples and their product in chunks of rows; and
-//    conv1 accumulated onto that bias; the gate as a 3x3 convolution to 16
+//    conv1 with that bias; the gate as a 3x3 convolution to 16
 //    channels and a per-pixel sigmoid scale; the image-to-patches stacks;
-//    the head before the final resize; the full-resolution branch in 16 x 16
+//    the head before the final resize; the full-resolution branch in 32 x 32
 //    tiles, its composed 5x5 convolution off the edge ring and, in the
 //    border tiles, both convolutions on the ring (decoder.rs:594-757).
 // One event is recorded after each of 14 steps (the 2 x 4 backbone stages,
@@ -135,14 +135,6 @@ __global__ __launch_bounds__(256) void k_pool_finish(const float *__restrict__ p
   }
   __syncthreads();
   if (tid < INTER) bias[tid] = cb[tid] + (((bsum[0][tid] + bsum[1][tid]) + bsum[2][tid]) + bsum[3][tid]);
-}
-
-// Every row of a rows x 64 map set to the (f16-rounded) bias.
-__global__ __launch_bounds__(256) void k_fill_rows(uint16_t *__restrict__ x, long rows,
-                                                   const float *__restrict__ bias) {
-  const long i = (long)blockIdx.x * 256 + threadIdx.x;
-  if (i >= rows * INTER) return;
-  x[i] = f2h(bias[i % INTER]);
 }
 
 // decoder.rs:378-401 the gate: out[p] *= sigmoid(b + sum_k g[p][k] w[k]),
@@ -479,8 +471,10 @@ ien_status conv(ien_ctx *ctx, const uint16_t *x, int h, int w, int c, long xs, i
 }
 
 ien_status rows_product(ien_ctx *ctx, const uint16_t *in, size_t k, long xs, size_t rows,
-                        const ien_matrix *m, uint16_t *out, long ys, ien_act act, int accumulate) {
+                        const ien_matrix *m, uint16_t *out, long ys, ien_act act, int accumulate,
+                        const float *bias = nullptr) {
   ConvCall cc;
+  cc.bias = bias;
   cc.x = in;
   cc.rows_mode = 1;
   cc.C = (int)k;
@@ -611,11 +605,10 @@ ien_status block_run(Birefnet *b, const BirefnetBlock &B, const uint16_t *in, in
                      : conv(ctx, b->t, h, w, INTER, INTER, ASPP_SIZES[i], B.branch[i],
                             b->cat + i * BRANCH, 4 * BRANCH, IEN_ACT_RELU, 0);
   if (st != IEN_OK) return st;
-  hipLaunchKernelGGL(k_fill_rows, dim3(blocks_for(pixels * INTER, 256)), dim3(256), 0, ctx->stream,
-                     b->a, pixels, b->d_bias);
-  IEN_HIP(hipGetLastError());
+  // conv1 over the four branches with the pooling's part (constant over the
+  // pixels) and conv1's bias as its bias.
   st = rows_product(ctx, b->cat, 4 * BRANCH, 4 * BRANCH, pixels, B.conv1, b->a, INTER,
-                    IEN_ACT_RELU, 1);
+                    IEN_ACT_RELU, 0, b->d_bias);
   if (st == IEN_OK)
     st = conv(ctx, b->a, h, w, INTER, INTER, 3, B.conv_out, out, B.cout, IEN_ACT_NONE, 0);
   if (st == IEN_OK && B.gate) {
@@ -653,13 +646,10 @@ ien_status backbone_run(Birefnet *b, const uint16_t *img, int side, bool half,
     }
     const long n = (long)grid * grid;
     if (!half) {
-      st = copy_cols(ctx, b->x, n, c, c, b->level[s], 2L * c);
-      if (st == IEN_OK)
-        st = ien_layer_norm(ctx, b->level[s], n, c, 2 * c, b->d_norm[s], b->d_norm[s] + c);
+      st = layer_norm_to(ctx, b->x, c, b->level[s], 2L * c, n, c, b->d_norm[s], b->d_norm[s] + c);
     } else {
       // The half-size map, normalised, then resized to the full grid.
-      st = copy_cols(ctx, b->x, n, c, c, b->tmp, c);
-      if (st == IEN_OK) st = ien_layer_norm(ctx, b->tmp, n, c, c, b->d_norm[s], b->d_norm[s] + c);
+      st = layer_norm_to(ctx, b->x, c, b->tmp, c, n, c, b->d_norm[s], b->d_norm[s] + c);
       if (st == IEN_OK)
         st = ien_resize(ctx, b->tmp, grid, grid, c, c, b->level[s] + c, 2 * grid, 2 * grid, 2 * c,
                         IEN_OUT_F16, 0);
@@ -865,7 +855,10 @@ ien_status birefnet_reserve(Birefnet *b, size_t side, bool *grew) {
   if (e == hipSuccess) e = alloc(&b->mid, Q * INTER);
   if (e == hipSuccess) e = alloc(&b->low, Q);
   if (e == hipSuccess) e = hipMalloc((void **)&b->partial, POOL_PARTS * INTER * 4);
-  if (e == hipSuccess) e = hipMalloc((void **)&b->d_bias, INTER * 4);
+  // conv1's biases: 64 written per run, padded with zeros to the product's
+  // 128-column tiles.
+  if (e == hipSuccess) e = hipMalloc((void **)&b->d_bias, 2 * INTER * 4);
+  if (e == hipSuccess) e = hipMemset(b->d_bias, 0, 2 * INTER * 4);
   if (e == hipSuccess && b->deformable) {
     e = hipMalloc((void **)&b->offs, Q * 3 * 49 * 4);
     if (e == hipSuccess) e = hipMalloc((void **)&b->samples, SAMPLE_BYTES);

@@ -1293,7 +1293,7 @@ ien_status launch_conv(ien_ctx *ctx, const ConvCall &c) {
   a.KB = w->kb;
   a.NB = w->nb;
   a.N = (int)w->n;
-  a.bias = w->d_bias;
+  a.bias = c.bias ? c.bias : w->d_bias;
   a.slope = c.slope;
   a.y = c.y;
   a.ys = (int)c.ys;

@@ -171,6 +171,9 @@ struct ConvCall {
   int act = IEN_ACT_NONE;
   const float *slope = nullptr;
   int accumulate = 0;
+  // Optional: device biases in place of the matrix's (as many as its padded
+  // columns, whole 32-column blocks).
+  const float *bias = nullptr;
   // Optional, NHWC f16 outputs of 3x3 stride-1 products only: a map (rows
   // ys apart, 16-byte aligned) added to each f16 result after the
   // activation, rounded again (the product followed by ien_add; it may be y).
@@ -222,6 +225,14 @@ struct RowsPlanes {
   const WinGeo *windows = nullptr;
 };
 ien_status launch_rows_planes(ien_ctx *ctx, const RowsPlanes &p);
+
+// elementwise.hip: LayerNorm (math.rs:95-116, eps 1e-5) of `rows` rows of c
+// values read from src (sstride apart) into dst (stride apart), in place
+// when they are the same rows (ien_layer_norm); other rows need 8-aligned
+// channels and strides and 16-byte aligned maps.
+ien_status layer_norm_to(ien_ctx *ctx, const uint16_t *src, size_t sstride, uint16_t *dst,
+                         size_t stride, size_t rows, size_t c, const float *gamma,
+                         const float *beta);
 
 // join_split.hip: a SCUNet block boundary over `rows` pixels of a c-channel
 // map x (rows c apart), c = 64 or 128: x += join([yc | ysw]) + join bias,
