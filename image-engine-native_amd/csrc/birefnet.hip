@@ -656,11 +656,10 @@ ien_status backbone_run(Birefnet *b, const uint16_t *img, int side, bool half,
     }
     if (st == IEN_OK && s < 3) {
       // swin.rs:377-405 merge: (0,0), (1,0), (0,1), (1,1) by (row, column).
-      st = ien_gather_2x2(ctx, b->x, grid, grid, c, c, IEN_ORDER_COLUMN_MAJOR, b->mrows);
+      // The 2 x 2 groups gathered as the LayerNorm over 4c reads them.
       const long half_tokens = n / 4;
-      if (st == IEN_OK)
-        st = ien_layer_norm(ctx, b->mrows, half_tokens, 4 * c, 4 * c, b->d_merge_ln[s],
-                            b->d_merge_ln[s] + 4 * c);
+      st = layer_norm_to(ctx, b->x, c, b->mrows, 4 * c, half_tokens, 4 * c, b->d_merge_ln[s],
+                         b->d_merge_ln[s] + 4 * c, grid / 2);
       if (st == IEN_OK)
         st = rows_product(ctx, b->mrows, 4 * c, 4 * c, half_tokens, b->merge[s], b->x, 2 * c,
                           IEN_ACT_NONE, 0);

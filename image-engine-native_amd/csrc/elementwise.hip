@@ -175,17 +175,29 @@ __global__ __launch_bounds__(256) void k_layer_norm(uint16_t *__restrict__ x, lo
 // with its row, so their latency overlaps the row's.  The reductions stay
 // inside the row's aligned lane group.
 // Rows are read from `src` (sstride apart) and written to x (stride
-// apart); the two may be the same rows (in place).
+// apart); the two may be the same rows (in place).  With g2w > 0 row r is
+// instead the 2 x 2 pixel group (2 (r / g2w) + dy, 2 (r % g2w) + dx) of a
+// map 2 g2w wide (pixels sstride apart, c / 4 channels each), in
+// column-major order: channel block q = dy + 2 dx (ien_gather_2x2's
+// column-major rows, gathered as they are read).
 template <int L, int Q>
 __global__ __launch_bounds__(256) void k_layer_norm_vec(const uint16_t *src, long sstride,
                                                         uint16_t *x, long rows, int c, long stride,
                                                         const float *__restrict__ gamma,
-                                                        const float *__restrict__ beta) {
+                                                        const float *__restrict__ beta, int g2w) {
   const int sub = threadIdx.x & (L - 1);
   const long row = ((long)blockIdx.x * 256 + threadIdx.x) / L;
   if (row >= rows) return;  // whole lane groups leave together
   const uint16_t *rs = src + row * sstride;
   uint16_t *r = x + row * stride;
+  // Chunk k of the row (8 channels).
+  auto chunk_at = [&](int k) -> const uint16_t * {
+    if (g2w == 0) return rs + 8 * k;
+    const int qc = (c >> 5), q = k / qc, kk = k - q * qc;  // c / 4 channels a block
+    const long ry = row / g2w, rx = row - ry * g2w;
+    const long pixel = (2 * ry + (q & 1)) * (2L * g2w) + 2 * rx + (q >> 1);
+    return src + pixel * sstride + 8 * kk;
+  };
   const int chunks = c >> 3;
   float v[8 * Q];
   float4 g[2 * Q], b[2 * Q];
@@ -193,7 +205,7 @@ __global__ __launch_bounds__(256) void k_layer_norm_vec(const uint16_t *src, lon
 #pragma unroll
   for (int q = 0; q < Q; q++) {
     const int k = min(sub + L * q, chunks - 1);  // (lanes past the row repeat its last chunk)
-    raw[q] = *(const u32x4 *)(rs + 8 * k);
+    raw[q] = *(const u32x4 *)chunk_at(k);
     g[2 * q] = *(const float4 *)(gamma + 8 * k);
     g[2 * q + 1] = *(const float4 *)(gamma + 8 * k + 4);
     b[2 * q] = *(const float4 *)(beta + 8 * k);
@@ -591,7 +603,7 @@ ien_status ien_pixel_shuffle_add(ien_ctx *ctx, const uint16_t *d_last, size_t la
 ien_status ien_layer_norm(ien_ctx *ctx, uint16_t *d_x, size_t rows, size_t c, size_t stride,
                           const float *d_gamma, const float *d_beta) {
   IEN_CHECK(ctx && d_x && d_gamma && d_beta, IEN_ERR_INPUT, "null argument");
-  return layer_norm_to(ctx, d_x, stride, d_x, stride, rows, c, d_gamma, d_beta);
+  return layer_norm_to(ctx, d_x, stride, d_x, stride, rows, c, d_gamma, d_beta, 0);
 }
 
 }  // extern "C"
@@ -600,14 +612,17 @@ namespace ien {
 
 ien_status layer_norm_to(ien_ctx *ctx, const uint16_t *d_src, size_t sstride, uint16_t *d_x,
                          size_t stride, size_t rows, size_t c, const float *d_gamma,
-                         const float *d_beta) {
-  IEN_CHECK(c > 0 && c <= 3072 && stride >= c && sstride >= c, IEN_ERR_INPUT, "rows of %zu values", c);
+                         const float *d_beta, int gather_w2) {
+  IEN_CHECK(c > 0 && c <= 3072 && stride >= c && sstride >= (gather_w2 ? c / 4 : c),
+            IEN_ERR_INPUT, "rows of %zu values", c);
   if (rows == 0) return IEN_OK;
   const bool vec = c % 8 == 0 && stride % 8 == 0 && sstride % 8 == 0 &&
                    (((uintptr_t)d_x | (uintptr_t)d_src) & 15) == 0 &&
                    ((uintptr_t)d_gamma & 15) == 0 && ((uintptr_t)d_beta & 15) == 0;
-  IEN_CHECK(vec || d_src == d_x, IEN_ERR_INPUT,
+  IEN_CHECK(vec || (d_src == d_x && gather_w2 == 0), IEN_ERR_INPUT,
             "LayerNorm into other rows: 8-aligned channels and strides, 16-byte aligned rows");
+  IEN_CHECK(gather_w2 >= 0 && (gather_w2 == 0 || (c % 32 == 0 && rows % gather_w2 == 0)),
+            IEN_ERR_INPUT, "2 x 2 groups of %zu channels over %zu rows", c, rows);
   if (vec) {
     // Lanes: the largest power of two dividing the chunks (no idle lanes)
     // when that leaves at most 3 chunks a lane, else the chunks rounded up
@@ -622,7 +637,7 @@ ien_status layer_norm_to(ien_ctx *ctx, const uint16_t *d_src, size_t sstride, ui
     const size_t threads = rows * (size_t)lanes;
     const dim3 grid((unsigned)((threads + 255) / 256));
     using K = void (*)(const uint16_t *, long, uint16_t *, long, int, long, const float *,
-                       const float *);
+                       const float *, int);
     static const K table[7][3] = {
         {k_layer_norm_vec<1, 1>, k_layer_norm_vec<1, 2>, k_layer_norm_vec<1, 3>},
         {k_layer_norm_vec<2, 1>, k_layer_norm_vec<2, 2>, k_layer_norm_vec<2, 3>},
@@ -635,7 +650,7 @@ ien_status layer_norm_to(ien_ctx *ctx, const uint16_t *d_src, size_t sstride, ui
     while ((1 << level) < lanes) level++;
     const K k = q <= 3 ? table[level][q - 1] : k_layer_norm_vec<64, 6>;
     hipLaunchKernelGGL(k, grid, dim3(256), 0, ctx->stream, d_src, (long)sstride, d_x, (long)rows,
-                       (int)c, (long)stride, d_gamma, d_beta);
+                       (int)c, (long)stride, d_gamma, d_beta, gather_w2);
     IEN_HIP(hipGetLastError());
     return IEN_OK;
   }

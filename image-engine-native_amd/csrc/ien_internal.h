@@ -229,10 +229,13 @@ ien_status launch_rows_planes(ien_ctx *ctx, const RowsPlanes &p);
 // elementwise.hip: LayerNorm (math.rs:95-116, eps 1e-5) of `rows` rows of c
 // values read from src (sstride apart) into dst (stride apart), in place
 // when they are the same rows (ien_layer_norm); other rows need 8-aligned
-// channels and strides and 16-byte aligned maps.
+// channels and strides and 16-byte aligned maps.  With gather_w2 > 0 the
+// rows are read as ien_gather_2x2's column-major 2 x 2 groups of src, a map
+// 2 gather_w2 wide of c / 4 channels (pixels sstride apart; c a multiple
+// of 32).
 ien_status layer_norm_to(ien_ctx *ctx, const uint16_t *src, size_t sstride, uint16_t *dst,
                          size_t stride, size_t rows, size_t c, const float *gamma,
-                         const float *beta);
+                         const float *beta, int gather_w2 = 0);
 
 // join_split.hip: a SCUNet block boundary over `rows` pixels of a c-channel
 // map x (rows c apart), c = 64 or 128: x += join([yc | ysw]) + join bias,
