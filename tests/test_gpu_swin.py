@@ -64,8 +64,13 @@ def test_swin_block(ctx, oracle, c, window, shift, masked, sizes):
         assert np.all(got[:, c:] == 3.0)  # channels past c untouched
         want = oracle_block(oracle, x.astype(np.float32), window, shift, masked, wt)
         err = np.abs(got[:, :c].reshape(h, w, c) - want)
-        assert err.max() < 5e-2, (h, w, err.max())
-        assert np.sqrt(np.mean(err ** 2)) < 6e-3, (h, w)
+        # The block's outputs reach 4-6 (unit-variance inputs plus the two
+        # residual branches), where one f16 ulp is 2^-8 to 2^-7: the bound
+        # is 2e-3 of the peak, about two ulps there (measured up to 3.5e-3
+        # at peaks of 4-5.6, RMS under 5e-4).
+        peak = max(1.0, float(np.abs(want).max()))
+        assert err.max() < 2e-3 * peak, (h, w, err.max(), peak)
+        assert np.sqrt(np.mean(err ** 2)) < 1e-3, (h, w)
     blk.free()
 
 
