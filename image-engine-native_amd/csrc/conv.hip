@@ -671,6 +671,10 @@ __global__ __launch_bounds__(256) void conv_mfma(ConvArgs a) {
       const int p = oy * a.OW + ox;
       const int n = nblk0 * 32 + 8 * g;
       if (oy >= a.OH || ox >= a.OW || p < a.p_begin || p >= a.p_end || n >= a.N) return -1;
+      if (a.phase) {
+        const int q = a.phase - 1;
+        return ((long)(2 * oy + (q >> 1)) * (2 * a.OW) + 2 * ox + (q & 1)) * a.ys + n;
+      }
       return (long)(p - a.p_begin) * a.ys + n;
     };
     // f16 outputs in whole 16-byte groups: the old values (when
@@ -1176,7 +1180,7 @@ static ien_status run_cfg(ien_ctx *ctx, ConvArgs a) {
   }
   int ksplit = 1;
   const bool idle = 4 * blocks <= ctx->cus || (KS == 1 && T * a.C >= 1536 && blocks < ctx->cus);
-  if (VEC && chunks >= 2 * min_chunks && idle) {
+  if (VEC && chunks >= 2 * min_chunks && idle && !a.phase) {
     ksplit = (int)std::min<long>(chunks / min_chunks, (2L * ctx->cus + blocks - 1) / blocks);
     if (db) ksplit = (int)std::min<long>({(long)ksplit, ctx->cus / blocks, chunks / 2L});
     ksplit = std::max(ksplit, 1);
@@ -1302,6 +1306,7 @@ ien_status launch_conv(ien_ctx *ctx, const ConvCall &c) {
   a.act = c.act;
   a.accumulate = c.accumulate;
   a.add2 = c.add2;
+  a.phase = c.phase;
 
   // 16-channel MFMA steps; NHWC halo loads of 16 bytes need aligned pixels.
   const bool vec = c.C % 16 == 0 && (nchw || (c.xs % 8 == 0 && ((uintptr_t)c.x & 15) == 0));
@@ -1316,7 +1321,13 @@ ien_status launch_conv(ien_ctx *ctx, const ConvCall &c) {
                         vec && !c.out_nchw && !c.out_f32 && c.ys % 8 == 0 && w->n % 8 == 0 &&
                         (((uintptr_t)c.y | (uintptr_t)c.add2) & 15) == 0),
             IEN_ERR_INPUT, "an added map needs an NHWC 3x3 product with whole 16-byte f16 groups");
-  const bool special = !c.add2;
+  IEN_CHECK(c.phase == 0 ||
+                (c.phase >= 1 && c.phase <= 4 && !nchw && !c.rows_mode && vec && c.stride == 1 &&
+                 !c.out_nchw && !c.out_f32 && c.row0 == 0 && c.rows == (long)c.OH * c.OW &&
+                 c.ys % 8 == 0 && w->n % 8 == 0 && ((uintptr_t)c.y & 15) == 0 &&
+                 (c.ks == 3 || c.noff > 0)),
+            IEN_ERR_INPUT, "a phase-scattered output needs a whole NHWC product in 16-byte f16 groups");
+  const bool special = !c.add2 && !c.phase;
   if (c.rows_mode) {
     // Input::Rows: a virtual image 32 pixels wide, rows in order.
     IEN_CHECK(!nchw && c.ks == 1 && c.noff == 0, IEN_ERR_INPUT, "rows are NHWC, one tap");

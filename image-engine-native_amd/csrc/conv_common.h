@@ -50,6 +50,10 @@ struct ConvArgs {
   // NHWC f16 outputs in 16-byte groups: a map (rows ys apart) added to the
   // rounded result and rounded again, or null.
   const uint16_t *add2;
+  // The same outputs, whole maps, not split over K: 0, or 1 + 2 py + px to
+  // write output pixel (y, x) to pixel (2 y + py, 2 x + px) of a map
+  // 2 OH x 2 OW (pixels ys apart), one phase of a transposed convolution.
+  int phase;
 };
 
 __device__ __forceinline__ int reflect_idx(int i, int n) {

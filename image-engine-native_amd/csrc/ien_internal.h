@@ -178,6 +178,11 @@ struct ConvCall {
   // ys apart, 16-byte aligned) added to each f16 result after the
   // activation, rounded again (the product followed by ien_add; it may be y).
   const uint16_t *add2 = nullptr;
+  // Optional, the same outputs and 3x3 or offset-tap products over whole
+  // maps: 1 + 2 py + px writes output pixel (y, x) to pixel (2 y + py,
+  // 2 x + px) of y, a map 2 OH x 2 OW with pixels ys apart (a transposed
+  // convolution's phase scattered as it is stored); 0 for none.
+  int phase = 0;
 };
 
 ien_status launch_conv(ien_ctx *ctx, const ConvCall &c);

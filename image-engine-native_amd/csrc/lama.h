@@ -21,10 +21,10 @@ struct Lama {
   size_t pw = 0, ph = 0;           // padded size the maps and the plan are for
   size_t pixels = 0;               // padded pixels the maps hold
   // Full-scale 4-channel input; maps at 1, 1/2, 1/4 (reused by the ups);
-  // eighth-scale a, mid, out, spectral; spectra; phase products; RGB.
+  // eighth-scale a, mid, out, spectral; spectra; RGB.
   uint16_t *in4 = nullptr, *m0 = nullptr, *m1 = nullptr, *m2 = nullptr, *a = nullptr,
            *mid = nullptr, *out = nullptr, *spectral = nullptr, *spectrum = nullptr,
-           *filtered = nullptr, *rows = nullptr, *rgb = nullptr;
+           *filtered = nullptr, *rgb = nullptr;
   float *work = nullptr;
   float *d_in = nullptr, *d_mask = nullptr, *d_out = nullptr;  // host-API staging
   size_t staged = 0;

@@ -151,9 +151,9 @@ ien_status ffc_run(Lama *l, const LamaFfc &f, const uint16_t *x, uint16_t *out, 
   return st;
 }
 
-// network.rs:279-335 Up::run: the four phase products into rows of 4 cout
-// values (phase p at columns p cout), then the 2 x 2 scatter into the
-// doubled map.
+// network.rs:279-335 Up::run: the four phase products, each storing its
+// outputs straight to their pixels of the doubled map (phase p = 2 py + px
+// to pixel (2 y + py, 2 x + px)).
 ien_status up_run(Lama *l, ien_matrix *const *phases, const uint16_t *x, int h, int w, int cin,
                   int cout, uint16_t *y) {
   for (int p = 0; p < 4; p++) {
@@ -178,18 +178,19 @@ ien_status up_run(Lama *l, ien_matrix *const *phases, const uint16_t *x, int h, 
     cc.row0 = 0;
     cc.rows = (long)h * w;
     cc.w = phases[p];
-    cc.y = l->rows + (size_t)p * cout;
-    cc.ys = 4L * cout;
+    cc.y = y;
+    cc.ys = cout;
+    cc.phase = 1 + p;
     cc.act = IEN_ACT_RELU;
     ien_status st = launch_conv(l->ctx, cc);
     if (st != IEN_OK) return st;
   }
-  return ien_scatter_2x2(l->ctx, l->rows, 4 * (size_t)cout, h, w, cout, y, cout);
+  return IEN_OK;
 }
 
 void free_maps(Lama &l) {
   for (uint16_t **p : {&l.in4, &l.m0, &l.m1, &l.m2, &l.a, &l.mid, &l.out, &l.spectral,
-                       &l.spectrum, &l.filtered, &l.rows, &l.rgb}) {
+                       &l.spectrum, &l.filtered, &l.rgb}) {
     (void)hipFree(*p);
     *p = nullptr;
   }
@@ -309,7 +310,6 @@ ien_status lama_reserve(Lama *l, size_t pw, size_t ph, bool *grew) {
   if (e == hipSuccess) e = alloc(&l->spectral, P / 64 * SPECTRAL);
   if (e == hipSuccess) e = alloc(&l->spectrum, S * 2 * SPECTRAL);
   if (e == hipSuccess) e = alloc(&l->filtered, S * 2 * SPECTRAL);
-  if (e == hipSuccess) e = alloc(&l->rows, P * 64);
   if (e == hipSuccess) e = alloc(&l->rgb, P * 3);
   if (e == hipSuccess) e = hipMalloc((void **)&l->work, S * 2 * SPECTRAL * 4);
   if (e != hipSuccess) {
