@@ -74,9 +74,12 @@ constexpr int STEPS = 9 * C / 16;
 constexpr int MBLK = (MPIX + 31) / 32, OBLK = OPIX / 32;
 constexpr int WAVES = 8, THREADS = 64 * WAVES;
 constexpr int WLOADS = WBYTES / (1024 * WAVES);  // 1 KiB weight loads per wave
-constexpr int BORDER = 4 * OTC + 4 * (OTR - 4);  // output pixels in the outer 2 rows / columns
 constexpr int INNER = (MR - 4) * (MC - 4);       // first-layer pixels that read no halo ring
 constexpr int MAXPAIRS = 16;
+#ifndef IEN_PAIR_PREFETCH
+#define IEN_PAIR_PREFETCH 1
+#endif
+constexpr int PREFETCH = IEN_PAIR_PREFETCH;  // steps a B fragment is loaded ahead of its products
 static_assert((MROW - 23 * PB) % 256 == PB, "first layer's rows");
 static_assert(MBLK <= 16 && OBLK == 12 && INNER >= 8 * 32, "block split over the waves");
 static_assert(WLOADS * 1024 * WAVES == WBYTES, "weight loads");
@@ -196,10 +199,6 @@ __global__ __launch_bounds__(THREADS) void conv_pair(PairArgs a) {
       dma_lds(wr, __builtin_amdgcn_readfirstlane(lds0 + at + f * 1024), f * 1024 + lane * 16);
     }
   };
-  auto load_weights = [&](int at) {
-#pragma unroll
-    for (int s = 0; s < STEPS; s++) w[s] = *(const half8 *)(lds + at + (hf * STEPS + s) * 1024 + lane * 16);
-  };
   auto params = [&](int k) {
     if (tid < C) {
       par[tid] = a.b[2 * k][tid];
@@ -229,29 +228,45 @@ __global__ __launch_bounds__(THREADS) void conv_pair(PairArgs a) {
     return acc;
   };
   // acc[j] += W^T X^T over the 36 steps for NB blocks whose lane bases are
-  // base[j] in a staged map of rows ROW bytes apart.
-  auto products = [&](auto nblocks, auto row, const int *base, floatx16 *acc) {
+  // base[j] in a staged map of rows ROW bytes apart.  With STREAM the
+  // weights come into w from their staging at `wat` in step with the B
+  // fragments (the first products after a layer's weights are staged), so
+  // that their loads overlap the products instead of preceding them.
+  auto products = [&](auto nblocks, auto row, const int *base, floatx16 *acc, auto stream,
+                      int wat) {
     constexpr int NB = decltype(nblocks)::value, ROW = decltype(row)::value;
-    constexpr int DEPTH = NB > 2 ? 2 : 3;  // B fragment prefetch
+    constexpr bool STREAM = decltype(stream)::value;
+    constexpr int DEPTH = PREFETCH;  // steps the B fragments are loaded ahead
     auto frag = [&](int j, int s) {
       const int tap = s / 4, kc = s % 4;
       return *(const half8 *)(lds + base[j] + (tap / 3) * ROW + (tap % 3) * PB + 32 * kc);
     };
     half8 xv[NB][DEPTH + 1];
 #pragma unroll
-    for (int s = 0; s < DEPTH; s++)
+    for (int s = 0; s < DEPTH; s++) {
+      if (STREAM) w[s] = *(const half8 *)(lds + wat + (hf * STEPS + s) * 1024 + lane * 16);
 #pragma unroll
       for (int j = 0; j < NB; j++) xv[j][s] = frag(j, s);
+    }
 #pragma unroll
     for (int s = 0; s < STEPS; s++) {
-      if (s + DEPTH < STEPS)
+      if (s + DEPTH < STEPS) {
+        if (STREAM)
+          w[s + DEPTH] = *(const half8 *)(lds + wat + (hf * STEPS + s + DEPTH) * 1024 + lane * 16);
 #pragma unroll
         for (int j = 0; j < NB; j++) xv[j][(s + DEPTH) % (DEPTH + 1)] = frag(j, s + DEPTH);
+      }
 #pragma unroll
       for (int j = 0; j < NB; j++)
         acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(w[s], xv[j][s % (DEPTH + 1)], acc[j], 0, 0, 0);
+      // Keeps each step's loads ahead of the products they feed: left to
+      // itself the scheduler sinks them to just before their use, and every
+      // product then waits out an LDS round trip.
+      __builtin_amdgcn_sched_barrier(0);
     }
   };
+  using streamed = std::true_type;
+  using held = std::false_type;
   // The PReLU slopes of the lane's 16 channels, the same for every block.
   auto slopes = [&](const float *slope, float4v *s4) {
 #pragma unroll
@@ -274,8 +289,14 @@ __global__ __launch_bounds__(THREADS) void conv_pair(PairArgs a) {
   // Pass `pass` of phase 1: the first layer on blocks grp + 4 (2 pass + j),
   // j < 2, of its pixels in first_pixel order; blocks past the last are
   // computed on its final pixel and dropped.  Results to LDS as f16
-  // (zeros outside the image: the second layer's padding).
-  auto first_pass = [&](int pass) {
+  // (zeros outside the image: the second layer's padding).  Pass 0 streams
+  // the layer's weights from their staging in MID.  after() runs once the
+  // products are issued, before the results are stored: pass 0's waits for
+  // every wave to hold its weights (MID then takes the results), pass 1's
+  // for every wave to be done with the halo and stages the next weights
+  // there, behind this pass's epilogue.
+  auto first_pass = [&](auto pass_c, auto after) {
+    constexpr int pass = decltype(pass_c)::value;
     int base[2], pix[2];
 #pragma unroll
     for (int j = 0; j < 2; j++) {
@@ -285,8 +306,10 @@ __global__ __launch_bounds__(THREADS) void conv_pair(PairArgs a) {
       base[j] = (pc / MC) * HROW + (pc % MC) * PB + 16 * (lane >> 5);
     }
     floatx16 acc[2] = {seed(par), seed(par)};
-    products(std::integral_constant<int, 2>{}, std::integral_constant<int, HROW>{}, base, acc);
+    products(std::integral_constant<int, 2>{}, std::integral_constant<int, HROW>{}, base, acc,
+             std::integral_constant<bool, pass == 0>{}, MID);
     __builtin_amdgcn_sched_barrier(0);
+    after();
     float4v s4[4];
     slopes(par + C, s4);
 #pragma unroll
@@ -311,22 +334,25 @@ __global__ __launch_bounds__(THREADS) void conv_pair(PairArgs a) {
   // output pixel q's tap (0, 0) is at base_of(q) (rows ROW bytes apart):
   // two blocks, then one, each passed to emit(j, acc) as soon as its
   // products are issued, so that no more than two blocks' accumulators and
-  // fragments are live beside the weights.
-  auto three_blocks = [&](auto row, const float *bias, auto base_of, auto emit) {
+  // fragments are live beside the weights.  The first two stream the
+  // layer's weights from their staging at `wat`, which emit may overwrite
+  // once every wave has them (the barrier after those products).
+  auto three_blocks = [&](auto row, const float *bias, int wat, auto base_of, auto emit) {
     {
       int base[2];
 #pragma unroll
       for (int j = 0; j < 2; j++) base[j] = base_of(32 * (grp + 4 * j) + (lane & 31));
       floatx16 acc[2] = {seed(bias), seed(bias)};
-      products(std::integral_constant<int, 2>{}, row, base, acc);
+      products(std::integral_constant<int, 2>{}, row, base, acc, streamed{}, wat);
       __builtin_amdgcn_sched_barrier(0);
+      __syncthreads();  // every wave holds its weights: emit may overwrite their staging
       emit(0, acc[0]);
       emit(1, acc[1]);
       __builtin_amdgcn_sched_barrier(0);
     }
     int base[1] = {base_of(32 * (grp + 8) + (lane & 31))};
     floatx16 acc[1] = {seed(bias)};
-    products(std::integral_constant<int, 1>{}, row, base, acc);
+    products(std::integral_constant<int, 1>{}, row, base, acc, held{}, 0);
     __builtin_amdgcn_sched_barrier(0);
     emit(2, acc[0]);
   };
@@ -402,11 +428,13 @@ __global__ __launch_bounds__(THREADS) void conv_pair(PairArgs a) {
 
   int *abort_word = CHAIN ? a.flags : nullptr;
   int *epochs = CHAIN ? a.flags + 3 : nullptr;
-  // Chain: the workgroup's last act on every way out.  Only wave 0 touches
-  // the flags (the waits and the epoch stores), so it counts the workgroup
-  // out once its own flag accesses are done; the count's release orders
-  // this workgroup's epoch stores before it, and the workgroup that brings
-  // it to the grid size (every other one has left) clears the flags.
+  // Chain: the workgroup's last act on every way out.  Only wave 0 writes
+  // the flags (the epoch stores, the abort and failure words); every wave
+  // reads the epochs and the abort word, always before the barrier that
+  // ends a ring wait, so once wave 0 counts the workgroup out no access of
+  // it to the flags remains.  The count's release orders wave 0's flag
+  // stores before it, and the workgroup that brings it to the grid size
+  // (every other one has left) clears the flags.
   auto leave = [&]() {
     if (wave != 0) return;
     int done = 0;
@@ -422,63 +450,83 @@ __global__ __launch_bounds__(THREADS) void conv_pair(PairArgs a) {
     }
   };
   const int pairs = CHAIN ? a.pairs : 1;
-  // Chain: wait for the 8 neighbours' epoch k (lanes 0..8 of wave 0, one
-  // each), then load the halo's 2-pixel ring from their border map k - 1
-  // (device scope) and wait for it.  False when a wait gave up.
-  auto ring = [&](int k) {
-    if (wave == 0) {
-      bool fail = false;
-      if (lane < 9 && lane != 4) {
-        const int ny = ty + lane / 3 - 1, nx = tx + lane % 3 - 1;
-        if (ny >= 0 && ny < a.tiles_y && nx >= 0 && nx < a.tiles_x) {
-          const int *f = epochs + ny * a.tiles_x + nx;
-          const unsigned long long t0 = wall_clock64();
-          while (a.spin_limit < 0 ||
-                 __hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < k) {
-            if (__hip_atomic_load(abort_word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0 ||
-                (long)(wall_clock64() - t0) > a.spin_limit) {
-              fail = true;
-              break;
-            }
-            __builtin_amdgcn_s_sleep(1);
-          }
-        }
-      }
-      const bool any = __builtin_amdgcn_ballot_w64(fail) != 0;
-      if (lane == 0) {
-        if (any) {
-          __hip_atomic_store(abort_word, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          __hip_atomic_fetch_max(abort_word + 1, a.seq, __ATOMIC_RELAXED,
-                                 __HIP_MEMORY_SCOPE_AGENT);
-        }
-        go = any ? 0 : 1;
-      }
+  // Chain: lane n < 9 (n != 4) of a wave watches neighbour (ty + n / 3 - 1,
+  // tx + n % 3 - 1): its epoch word, or null where there is none.
+  auto neighbour = [&]() -> const int * {
+    if (lane < 9 && lane != 4) {
+      const int ny = ty + lane / 3 - 1, nx = tx + lane % 3 - 1;
+      if (ny >= 0 && ny < a.tiles_y && nx >= 0 && nx < a.tiles_x) return epochs + ny * a.tiles_x + nx;
     }
-    __syncthreads();
-    if (go == 0) return false;
+    return nullptr;
+  };
+  // Chain: this wave's share of the loads of the halo's 2-pixel ring from
+  // the neighbours' border map (k - 1) % 2, at device scope.  A load fills
+  // one contiguous KiB of LDS, 16 bytes a lane: staged chunk q of a run of
+  // pixels is chunk q % 9 of pixel q / 9 (chunk 8, the pad, and pixels
+  // outside the image read zeros).
+  auto ring_loads = [&](int k) {
+    // The lane index through an opaque move: the offsets below are then
+    // computed where they are used rather than kept live (or spilled) from
+    // the kernel's start, so that no spill reload, whose wait would also
+    // wait for every load in flight, lands between these loads.
+    int lane;
+    asm volatile("v_mov_b32 %0, %1" : "=v"(lane) : "v"(tid & 63));
     const int4v rr = buffer_rsrc(a.border[(k - 1) & 1], map_bytes);
-    // Staged rows 0, 1 and 18, 19: two spans of 2 rows, 1 KiB a load.
-    for (int i = wave; i < 2 * G::RSPAN; i += WAVES) {
-      const int row0 = i < G::RSPAN ? 0 : IR - 2, part = i < G::RSPAN ? i : i - G::RSPAN;
-      const int byte = part * 1024 + lane * 16;
-      const int hy = row0 + byte / HROW, within = byte % HROW;
-      const int hx = within / PB, ch = (within - hx * PB) >> 4;
-      if (byte < 2 * HROW)
-        dma_lds_device(rr, __builtin_amdgcn_readfirstlane(lds0 + row0 * HROW + part * 1024),
-                       halo_src(hy, hx, ch));
+    auto src = [&](int gy, int gx, int c) {
+      const bool ok = c < 8 && (unsigned)gx < (unsigned)a.W && (unsigned)gy < (unsigned)a.H;
+      return ok ? ((gy * a.W + gx) * C + 8 * c) * 2 : OOB;
+    };
+    // Halo rows 0, 1, 18, 19 whole: 28 pixels, 252 chunks, 4 loads a row
+    // (the last 4 lanes of the fourth write zeros into the row's padding).
+    for (int i = wave; i < 16; i += WAVES) {
+      const int r = i >> 2, part = i & 3, hy = r < 2 ? r : r + IR - 4;
+      const int q = 64 * part + lane, p = (int)((unsigned)q / 9u);
+      dma_lds_device(rr, __builtin_amdgcn_readfirstlane(lds0 + hy * HROW + part * 1024),
+                     q < 9 * IC ? src(y0 - 2 + hy, x0 - 2 + p, q - 9 * p) : OOB);
     }
-    // Pixels 0, 1 and 26, 27 of rows 2 .. 17: 32 pieces of 2 staged
-    // pixels (18 chunks, lanes 0 .. 17).
+    // Pixels 0, 1 and 26, 27 of rows 2 .. 17: 18 chunks (lanes 0 .. 17) a load.
     for (int i = wave; i < 2 * (IR - 4); i += WAVES) {
       const int hy = 2 + (i >> 1), hx0 = (i & 1) ? IC - 2 : 0;
+      const int p = lane >= 9 ? 1 : 0;
       if (lane < 18)
         dma_lds_device(rr, __builtin_amdgcn_readfirstlane(lds0 + hy * HROW + hx0 * PB),
-                       halo_src(hy, hx0 + lane / 9, lane % 9));
+                       src(y0 - 2 + hy, x0 - 2 + hx0 + p, lane - 9 * p));
+    }
+  };
+  // Chain: the ring of pair k.  Each wave waits for its neighbours' epoch k
+  // (lane n for neighbour n) and issues its share of the loads, then waits
+  // for them; the barrier follows.  False when a wait gave up: wave 0 then
+  // raises the abort word (which every waiting tile watches) and the
+  // failure word.
+  auto ring = [&](int k) {
+    bool fail = false;
+    if (const int *f = neighbour()) {
+      const unsigned long long t0 = wall_clock64();
+      while (a.spin_limit < 0 ||
+             __hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < k) {
+        if (__hip_atomic_load(abort_word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0 ||
+            (long)(wall_clock64() - t0) > a.spin_limit) {
+          fail = true;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+      }
+    }
+    if (__builtin_amdgcn_ballot_w64(fail) != 0) {
+      if (lane == 0) go = 0;
+    } else {
+      ring_loads(k);
     }
     wait_vm<0>();
     __syncthreads();
-    return true;
+    if (go != 0) return true;
+    if (tid == 0) {
+      __hip_atomic_store(abort_word, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_fetch_max(abort_word + 1, a.seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    return false;
   };
+  if (CHAIN && tid == 0) go = 1;  // (seen after the first pair's opening barrier)
   for (int k = 0; k < pairs; k++) {
     // ---- the first layer's weights (where its results will go) and, for
     // a single pair or a chain's first, the whole halo from the input; a
@@ -507,26 +555,24 @@ __global__ __launch_bounds__(THREADS) void conv_pair(PairArgs a) {
     __syncthreads();
     if (CHAIN && k > 0 && tid == 0)  // publish epoch k: this tile's pair k - 1 border is out
       __hip_atomic_store(epochs + tile, k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    load_weights(MID);
-    __syncthreads();  // every wave holds its weights: the first results may overwrite them
 
     // ---- phase 1: the first layer on the 18 x 26 pixels in two passes;
     // a chain's first pass reads only the halo's centre, and the ring
     // comes in between the passes ----
-    first_pass(0);
+    first_pass(std::integral_constant<int, 0>{}, [] {
+      __syncthreads();  // every wave holds its weights: MID may take the results
+    });
     if (CHAIN && k > 0 && !ring(k)) {  // (no load of this workgroup is in flight here)
       leave();
       return;
     }
-    first_pass(1);
-    __syncthreads();  // the first layer's results complete; the halo is free
-
-    // ---- the second layer's weights, staged where the halo was ----
-    stage_weights(a.w[2 * k + 1], 0);
+    // ---- and the second layer's weights, staged where the halo was ----
+    first_pass(std::integral_constant<int, 1>{}, [&] {
+      __syncthreads();  // every wave is done with the halo
+      stage_weights(a.w[2 * k + 1], 0);
+    });
     wait_vm<0>();
-    __syncthreads();
-    load_weights(0);
-    __syncthreads();  // every wave holds its weights: the staging below may overwrite them
+    __syncthreads();  // the first layer's results complete, the weights staged
 
     // ---- phase 2: the second layer on the 16 x 24 outputs, blocks grp,
     // grp + 4, grp + 8 ----
@@ -542,7 +588,7 @@ __global__ __launch_bounds__(THREADS) void conv_pair(PairArgs a) {
       // which keeps both the writes (16 pixels, one chunk) and the reads
       // (4 pixels, 4 chunks) free of bank conflicts.
       unsigned char *stage = lds + wave * (OBLK / 4) * 32 * 64;
-      three_blocks(std::integral_constant<int, MROW>{}, par + 2 * C, mid_base,
+      three_blocks(std::integral_constant<int, MROW>{}, par + 2 * C, 0, mid_base,
                    [&](int j, const floatx16 &acc) {
         uint2 o[4];
         finish(acc, s4, ~0u, o);
@@ -580,54 +626,63 @@ __global__ __launch_bounds__(THREADS) void conv_pair(PairArgs a) {
     } else {
       // The results become the centre of the next pair's halo (zeros
       // outside the image: its padding).
-      three_blocks(std::integral_constant<int, MROW>{}, par + 2 * C, mid_base,
+      const bool last = k == pairs - 1 && !a.wl;  // (a final layer follows the last pair)
+      const __amdgpu_buffer_rsrc_t br =
+          __builtin_amdgcn_make_buffer_rsrc(a.border[k & 1], 0, (int)map_bytes, 0x00020000);
+      three_blocks(std::integral_constant<int, MROW>{}, par + 2 * C, 0, mid_base,
                    [&](int j, const floatx16 &acc) {
-        const int q = 32 * (grp + 4 * j) + (lane & 31);
-        const bool inside = y0 + q / OTC < a.H && x0 + q % OTC < a.W;
+        const int q = 32 * (grp + 4 * j) + (lane & 31), r = q / OTC, col = q % OTC;
+        const bool inside = y0 + r < a.H && x0 + col < a.W;
         uint2 o[4];
         finish(acc, s4, inside ? ~0u : 0u, o);
 #pragma unroll
         for (int g = 0; g < 4; g++) {
           const int ch = 32 * hf + 8 * g + 4 * (lane >> 5);
-          *(uint2 *)(lds + (2 + q / OTC) * HROW + (2 + q % OTC) * PB + ch * 2) = o[g];
+          *(uint2 *)(lds + (2 + r) * HROW + (2 + col) * PB + ch * 2) = o[g];
         }
       });
       __syncthreads();  // the centre is complete; the first layer's results are read
-      // Then out, 16 bytes a lane (8 lanes a pixel): the whole tile after
-      // the last pair, else, at device scope, the pixels of the outer 2 rows
-      // (0, 1, 14, 15) and columns (0, 1, 22, 23) that the neighbours read,
-      // with the next pair's first weights staged behind them (their
-      // completion, and so the epoch, is awaited at the next pair's start).
-      const bool last = k == pairs - 1 && !a.wl;  // (a final layer follows the last pair)
-      const __amdgpu_buffer_rsrc_t yr = __builtin_amdgcn_make_buffer_rsrc(
-          last ? a.y : a.border[k & 1], 0, (int)map_bytes, 0x00020000);
-      const int chunks = (last ? OPIX : BORDER) * 8;
-      for (int v = tid; v < chunks; v += THREADS) {
-        const int c = v & 7, b = v >> 3;
-        int r, col;
-        if (last) {
-          r = b / OTC;
-          col = b % OTC;
-        } else if (b < 4 * OTC) {
-          r = b / OTC;
-          r = r < 2 ? r : r + OTR - 4;
-          col = b % OTC;
-        } else {
-          r = 2 + ((b - 4 * OTC) >> 2);
-          col = (b - 4 * OTC) & 3;
-          col = col < 2 ? col : col + OTC - 4;
+      if (last) {
+        // The whole tile out, 16 bytes a lane (8 lanes a pixel).
+        const __amdgpu_buffer_rsrc_t yr =
+            __builtin_amdgcn_make_buffer_rsrc(a.y, 0, (int)map_bytes, 0x00020000);
+        for (int v = tid; v < OPIX * 8; v += THREADS) {
+          const int c = v & 7, b = v >> 3, r = b / OTC, col = b % OTC;
+          const uint4 d = *(const uint4 *)(lds + (2 + r) * HROW + (2 + col) * PB + 16 * c);
+          const int gy = y0 + r, gx = x0 + col;
+          typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+          const u32x4 dv = {d.x, d.y, d.z, d.w};
+          __builtin_amdgcn_raw_buffer_store_b128(
+              dv, yr, gy < a.H && gx < a.W ? (gy * a.W + gx) * C * 2 + 16 * c : OOB, 0, 0);
         }
-        const uint4 d = *(const uint4 *)(lds + (2 + r) * HROW + (2 + col) * PB + 16 * c);
-        const int gy = y0 + r, gx = x0 + col;
-        typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
-        const u32x4 dv = {d.x, d.y, d.z, d.w};
-        const int at = gy < a.H && gx < a.W ? (gy * a.W + gx) * C * 2 + 16 * c : OOB;
-        if (last)
-          __builtin_amdgcn_raw_buffer_store_b128(dv, yr, at, 0, 0);
-        else
-          __builtin_amdgcn_raw_buffer_store_b128(dv, yr, at, 0, SC1);
+      } else {
+        // The pixels of the outer 2 rows (0, 1, 14, 15) and columns (0, 1,
+        // 22, 23), which the neighbours read, to border map k % 2 at device
+        // scope, with the next pair's first weights staged behind them
+        // (their completion, and so the epoch, is awaited at the next
+        // pair's start).  (Stored straight from the registers during phase
+        // 2 instead, they cost more than this pass.)
+        for (int v = tid; v < (4 * OTC + 4 * (OTR - 4)) * 8; v += THREADS) {
+          const int c = v & 7, b = v >> 3;
+          int r, col;
+          if (b < 4 * OTC) {
+            r = b / OTC;
+            r = r < 2 ? r : r + OTR - 4;
+            col = b % OTC;
+          } else {
+            r = 2 + ((b - 4 * OTC) >> 2);
+            col = (b - 4 * OTC) & 3;
+            col = col < 2 ? col : col + OTC - 4;
+          }
+          const uint4 d = *(const uint4 *)(lds + (2 + r) * HROW + (2 + col) * PB + 16 * c);
+          const int gy = y0 + r, gx = x0 + col;
+          typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+          const u32x4 dv = {d.x, d.y, d.z, d.w};
+          const int at = gy < a.H && gx < a.W ? (gy * a.W + gx) * C * 2 + 16 * c : OOB;
+          __builtin_amdgcn_raw_buffer_store_b128(dv, br, at, 0, SC1);
+        }
+        stage_weights(k + 1 < pairs ? a.w[2 * k + 2] : a.wl, MID);
       }
-      if (!last) stage_weights(k + 1 < pairs ? a.w[2 * k + 2] : a.wl, MID);
     }
   }
 
@@ -656,8 +711,6 @@ __global__ __launch_bounds__(THREADS) void conv_pair(PairArgs a) {
     wait_vm<0>();
     __syncthreads();
     if (tid == 0) __hip_atomic_store(epochs + tile, k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    load_weights(MID);
-    __syncthreads();  // every wave holds the weights: MID may take the results
     if (!ring(k)) {
       leave();
       return;
@@ -667,7 +720,7 @@ __global__ __launch_bounds__(THREADS) void conv_pair(PairArgs a) {
     // chain's output is bit for bit that of the separate launches.
     float *res = (float *)(lds + MID);
     auto r16 = [](float v) { return h2f(f2h(v)); };
-    three_blocks(std::integral_constant<int, HROW>{}, par,
+    three_blocks(std::integral_constant<int, HROW>{}, par, MID,
                  [&](int q) { return (1 + q / OTC) * HROW + (1 + q % OTC) * PB + 16 * (lane >> 5); },
                  [&](int j, const floatx16 &acc) {
       const int q = 32 * (grp + 4 * j) + (lane & 31);
