@@ -112,9 +112,14 @@ __device__ __forceinline__ float act_c(float v, float slope) {
   else if constexpr (ACT == IEN_ACT_PRELU) {
     // v < 0 ? v slope : v as a bit select on v's sign (no compare, so no
     // mask register per value); only -0 with a negative slope differs (+0).
+    // One v_bfi_b32 does the select ((m & a) | (~m & b)), which the
+    // compiler otherwise spells as three instructions.
     const int m = __builtin_bit_cast(int, v) >> 31;
-    return __builtin_bit_cast(float, (__builtin_bit_cast(int, v * slope) & m) |
-                                         (__builtin_bit_cast(int, v) & ~m));
+    int r;
+    asm("v_bfi_b32 %0, %1, %2, %3"
+        : "=v"(r)
+        : "v"(m), "v"(__builtin_bit_cast(int, v * slope)), "v"(__builtin_bit_cast(int, v)));
+    return __builtin_bit_cast(float, r);
   }
   else if constexpr (ACT == IEN_ACT_GELU) return gelu_f(v);
   else if constexpr (ACT == IEN_ACT_SIGMOID) return sigmoid_f(v);
