@@ -662,8 +662,16 @@ __global__ __launch_bounds__(THREADS) void conv_pair(PairArgs a) {
         // (their completion, and so the epoch, is awaited at the next
         // pair's start).  (Stored straight from the registers during phase
         // 2 instead, they cost more than this pass.)
-        for (int v = tid; v < (4 * OTC + 4 * (OTR - 4)) * 8; v += THREADS) {
-          const int c = v & 7, b = v >> 3;
+        // All of a thread's chunks are read from LDS before any is stored.
+        constexpr int CHUNKS = (4 * OTC + 4 * (OTR - 4)) * 8;
+        constexpr int PER = (CHUNKS + THREADS - 1) / THREADS;
+        typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+        u32x4 dv[PER];
+        int at[PER];
+#pragma unroll
+        for (int i = 0; i < PER; i++) {
+          const int v = tid + THREADS * i, vc = v < CHUNKS ? v : CHUNKS - 1;
+          const int c = vc & 7, b = vc >> 3;
           int r, col;
           if (b < 4 * OTC) {
             r = b / OTC;
@@ -675,12 +683,12 @@ __global__ __launch_bounds__(THREADS) void conv_pair(PairArgs a) {
             col = col < 2 ? col : col + OTC - 4;
           }
           const uint4 d = *(const uint4 *)(lds + (2 + r) * HROW + (2 + col) * PB + 16 * c);
+          dv[i] = u32x4{d.x, d.y, d.z, d.w};
           const int gy = y0 + r, gx = x0 + col;
-          typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
-          const u32x4 dv = {d.x, d.y, d.z, d.w};
-          const int at = gy < a.H && gx < a.W ? (gy * a.W + gx) * C * 2 + 16 * c : OOB;
-          __builtin_amdgcn_raw_buffer_store_b128(dv, br, at, 0, SC1);
+          at[i] = v < CHUNKS && gy < a.H && gx < a.W ? (gy * a.W + gx) * C * 2 + 16 * c : OOB;
         }
+#pragma unroll
+        for (int i = 0; i < PER; i++) __builtin_amdgcn_raw_buffer_store_b128(dv[i], br, at[i], 0, SC1);
         stage_weights(k + 1 < pairs ? a.w[2 * k + 2] : a.wl, MID);
       }
     }
