@@ -543,6 +543,19 @@ __global__ __launch_bounds__(256) void k_spectral_back(BackArgs p) {
       dma16(og + (long)x * p.ys + 8 * (c & 15), lds + f * 1024);
     }
   }
+  // The residual this row's results are added to (when there is one): at
+  // most 4 of its 16-byte items a thread (16 w items, w <= 64), requested
+  // now so that their latency passes behind the product below.
+  constexpr int AITEMS = 16 * MAX_SIDE / 256;
+  const long orow = (long)y * w * p.ys + NG * g;
+  u32x4 addv[AITEMS];
+  if (p.add) {
+#pragma unroll
+    for (int i = 0; i < AITEMS; i++) {
+      const int q = tid + 256 * i, x = min(q >> 4, w - 1), c = q & 15;
+      addv[i] = *(const u32x4 *)(p.add + orow + (long)x * p.ys + 8 * c);
+    }
+  }
   // spectral_out: D[n][x] = sum_c W[c][n] S2[x][c], the weights as the A
   // operand; out = ReLU(out + D), staged in LDS.
   floatx16 dacc[2];
@@ -580,18 +593,19 @@ __global__ __launch_bounds__(256) void k_spectral_back(BackArgs p) {
   __syncthreads();
   // 16 lanes write one pixel's 256 bytes.
   {
-    const long row = (long)y * w * p.ys + NG * g;
-    uint16_t *og = p.dst + row;
+    uint16_t *og = p.dst + orow;
     if (p.add) {
-      const uint16_t *ag = p.add + row;
-      for (int q = tid; q < 16 * w; q += 256) {
-        const int x = q >> 4, c = q & 15;
-        uint16_t o[8], h[8];
-        *(u32x4 *)o = *(const u32x4 *)(ob + x * OBP + 8 * c);
-        *(u32x4 *)h = *(const u32x4 *)(ag + (long)x * p.ys + 8 * c);
 #pragma unroll
-        for (int e = 0; e < 8; e++) o[e] = f2h(h2f(o[e]) + h2f(h[e]));
-        *(u32x4 *)(og + (long)x * p.ys + 8 * c) = *(const u32x4 *)o;
+      for (int i = 0; i < AITEMS; i++) {
+        const int q = tid + 256 * i, x = q >> 4, c = q & 15;
+        if (q < 16 * w) {
+          uint16_t o[8], h[8];
+          *(u32x4 *)o = *(const u32x4 *)(ob + x * OBP + 8 * c);
+          *(u32x4 *)h = addv[i];
+#pragma unroll
+          for (int e = 0; e < 8; e++) o[e] = f2h(h2f(o[e]) + h2f(h[e]));
+          *(u32x4 *)(og + (long)x * p.ys + 8 * c) = *(const u32x4 *)o;
+        }
       }
     } else {
       for (int q = tid; q < 16 * w; q += 256) {
