@@ -194,7 +194,10 @@ def elementwise(ctx, stream, reps, copy_tbps=None):
     the sweep (a graph of `reps` back-to-back launches after 20 untimed):
     algorithmic bytes (every input read once, every output written once),
     GB/s, % of the 8 TB/s HBM peak and, when given, of the measured device
-    copy rate.  Each pass cycles over enough copies of its buffers that the
+    copy rate, and the time a device copy of the same bytes takes timed the
+    same way (`of_same_size_copy_pct`: that time over the pass's, 100 when
+    the pass moves its bytes as fast as a copy of that size).  Each pass
+    cycles over enough copies of its buffers that the
     launches between two uses of one copy touch more than 512 MiB: twice the
     256 MiB memory-side cache, so every launch reads and writes HBM."""
     import itertools
@@ -287,8 +290,16 @@ def elementwise(ctx, stream, reps, copy_tbps=None):
 
     cases.append(("bytes_to_floats 1024x1024x3", 1024 * 1024 * 3 * 5, to_floats))
 
-    results = []
-    for name, nbytes, make in cases:
+    # The same bytes moved by a plain device copy (half of them read, half
+    # written), timed the same way: what a pass of that size can reach when
+    # its fixed costs (the launch, the first loads' latency, the tail) weigh
+    # as much as its traffic.
+    def same_size_copy(nbytes):
+        n = max(8, int(nbytes) // 4)  # halves: 2n bytes read + 2n written
+        src, dst = halves(n), torch.empty(n, dtype=f16, device=dev)
+        return lambda: dst.copy_(src)
+
+    def timed(nbytes, make):
         copies = max(2, -(-(512 << 20) // int(nbytes)) + 1)
         launches = [make() for _ in range(copies)]
         turn = itertools.cycle(launches)
@@ -296,14 +307,22 @@ def elementwise(ctx, stream, reps, copy_tbps=None):
         for _ in range(20):
             launch()
         ms = event_time(launch, reps, stream)
+        del launches, launch, turn
+        torch.cuda.empty_cache()
+        return ms, copies
+
+    results = []
+    for name, nbytes, make in cases:
+        ms, copies = timed(nbytes, make)
+        copy_ms, _ = timed(nbytes, lambda nbytes=nbytes: same_size_copy(nbytes))
         gbs = nbytes / (ms * 1e-3) / 1e9
         row = {"pass": name, "bytes": int(nbytes), "us": round(ms * 1e3, 2), "gbs": round(gbs, 0),
-               "hbm_pct": round(100 * gbs / HBM_PEAK_GBS, 1), "copies": copies}
+               "hbm_pct": round(100 * gbs / HBM_PEAK_GBS, 1), "copies": copies,
+               "same_size_copy_us": round(copy_ms * 1e3, 2),
+               "of_same_size_copy_pct": round(100 * copy_ms / ms, 1)}
         if copy_tbps:
             row["copy_pct"] = round(100 * gbs / (copy_tbps * 1000), 1)
         results.append(row)
-        del launches, launch, turn
-        torch.cuda.empty_cache()
     return results
 
 
