@@ -1365,6 +1365,8 @@ ien_status launch_conv(ien_ctx *ctx, const ConvCall &c) {
   if (nchw && nchw1_supported(a, c.ks, c.stride, c.rows)) return launch_nchw1(ctx, a);
   // NCHW 3x3 64 -> 64: the whole layer's weights and a 4 x 96 tile a CU.
   if (nchw && nchw3_supported(a, c.ks, c.stride, c.rows)) return launch_nchw3(ctx, a);
+  // NCHW 3x3 128 -> 128: 2 x 96 tiles a channel half, K in double-buffered quarters.
+  if (nchw && nchw3q_supported(a, c.ks, c.stride, c.rows)) return launch_nchw3q(ctx, a);
   if (c.ks == 3 && c.stride == 1) {
     if (!vec) {
       if (nchw) return run_cfg<3, 1, 4, 32, 4, 2, 16, false, true>(ctx, a);

@@ -267,8 +267,11 @@ ien_status launch_few(ien_ctx *ctx, ConvArgs a, int ks);
 bool nchw1_supported(const ConvArgs &a, int ks, int stride, long rows);
 ien_status launch_nchw1(ien_ctx *ctx, const ConvArgs &a);
 // The same file: zero-padded 3x3 convolutions of 64 NCHW f16 channels into
-// 64 (whole maps, widths a multiple of 8), not accumulating.
+// 64, and of 128 into 128 (whole maps, widths a multiple of 8), not
+// accumulating.
 bool nchw3_supported(const ConvArgs &a, int ks, int stride, long rows);
 ien_status launch_nchw3(ien_ctx *ctx, const ConvArgs &a);
+bool nchw3q_supported(const ConvArgs &a, int ks, int stride, long rows);
+ien_status launch_nchw3q(ien_ctx *ctx, const ConvArgs &a);
 
 }  // namespace ien

@@ -345,6 +345,197 @@ __global__ __launch_bounds__(256) void k_nchw3(Nchw3Args a) {
   }
 }
 
+// ---- 3x3 convolutions of 128 channels into 128 (NCHW in and out) ----
+//
+// One workgroup of 4 waves per tile of 2 output rows x 96 pixels and one
+// half (64) of the output channels; the two halves of a pixel tile are
+// neighbours in the XCD-aware order, so the second finds the halo in the
+// first's L2.  K runs in four 32-channel quarters (taps, then 16-channel
+// steps within each: the general kernel's order at 32-channel chunks)
+// through two LDS buffers: a quarter's 36 KiB of weight fragments land by
+// buffer loads straight into LDS, and its 4 x 98 pixel halo is loaded into
+// registers and transposed (4 channels x 8 pixels -> 8 pixels x 4
+// channels, as k_nchw1 does) into a pixel-major tile of 80-byte pixels.
+// While quarter i is multiplied, quarter i + 1 sits in the other buffer
+// and quarter i + 2's halo is in flight in registers.  Wave w computes
+// row w / 2 of the tile against channel block w % 2 of the half: 3 pixel
+// blocks, 4 fragments read for 3 MFMAs a k step.
+constexpr int Q_TR = 2, Q_TC = 96, Q_HR = 4, Q_HC = 98, Q_GROUPS = 14;
+constexpr int Q_PX = 40;           // halves per halo pixel: 32 channels + 8
+constexpr int Q_RP = Q_HC * Q_PX;  // halves per halo row: rows 40 banks apart
+constexpr int Q_HALO = (Q_HR * Q_RP * 2 + 1023) / 1024 * 1024;  // 31744
+constexpr int Q_WFRAGS = 2 * 18;                                // 2 channel blocks x 9 taps x 2 steps
+constexpr int Q_BUF = Q_HALO + Q_WFRAGS * 1024;                 // 68608
+constexpr int Q_LDS = 2 * Q_BUF;                                // 137216
+constexpr int Q_UNITS = Q_HR * Q_GROUPS * 8;  // per quarter: (row, 8-pixel group, channel quad)
+constexpr int Q_ITEMS = (Q_UNITS + 255) / 256;
+constexpr int Q_YP = Q_TC + 8;  // halves per staged output row
+static_assert(Q_LDS <= 160 * 1024, "LDS budget");
+static_assert(Q_GROUPS * 8 >= Q_HC + 7, "groups cover the halo columns");
+static_assert(Q_TR * 64 * Q_YP * 2 <= Q_HALO, "output staging within a halo buffer");
+static_assert(Q_HR % 2 == 0, "row pairs");
+
+struct Nchw3qArgs {
+  const uint16_t *x;
+  int xs, H, W;          // plane stride (halves), map size (W a multiple of 8)
+  const uint16_t *wp;    // packed 1152 x 128 fragments, 72 k steps a channel block
+  const uint16_t *zeros;
+  const float *bias, *slope;
+  uint16_t *y;
+  int ys;
+  int tiles_x, tiles;    // pixel tiles across; tiles = 2 x pixel tiles
+};
+
+template <int ACT>
+__global__ __launch_bounds__(256) void k_nchw3q(Nchw3qArgs a) {
+  __shared__ __attribute__((aligned(1024))) unsigned char lds[Q_LDS];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, col = lane & 31, hi = lane >> 5;
+  const int t = xcd_remap(blockIdx.x, a.tiles), nh = t & 1, pt = t >> 1;
+  const int y0 = (pt / a.tiles_x) * Q_TR, x0 = (pt % a.tiles_x) * Q_TC;
+  const int row = wave >> 1, nb = wave & 1;
+  const int och = 64 * nh + 32 * nb + col;
+  const float bias = a.bias[och];
+  const float slope = ACT == IEN_ACT_PRELU ? a.slope[och] : 0.0f;
+
+  // Quarter q's weight fragments of this half: LDS slot e = b 18 + 2 tap + g
+  // holds packed fragment (2 nh + b) 72 + 8 tap + 2 q + g; 9 a wave.
+  const int4v wrs = uniform_rsrc(a.wp + (size_t)nh * 2 * 72 * 512, 2L * 72 * 1024);
+  const int wv = __builtin_amdgcn_readfirstlane(wave);  // in SGPRs: the LDS base is one
+  auto dma_w = [&](int q, int buf) {
+    const unsigned base = lds_addr(lds + buf * Q_BUF + Q_HALO);
+#pragma unroll
+    for (int i = 0; i < 9; i++) {
+      const int e = 4 * i + wv, b = e / 18, tg = e % 18;
+      const int f = b * 72 + (tg >> 1) * 8 + 2 * q + (tg & 1);
+      dma_lds(wrs, base + e * 1024, f * 1024 + lane * 16);
+    }
+  };
+  // Halo units of a quarter: rows 2 p + rr (input row y0 - 1 + that), group
+  // g (input pixels x0 - 8 + 8 g ..+ 7), channels 32 q + 4 c4 ..+ 3.  Lanes
+  // 0-7 of each 16 take the quads of one row, 8-15 the next row's.  Groups
+  // outside the map read the zero page.
+  auto unit = [&](int u, int &r, int &g, int &c4) {
+    c4 = u & 7;
+    const int rr = (u >> 3) & 1, gp = u >> 4, p = gp / Q_GROUPS;
+    g = gp - p * Q_GROUPS;
+    r = 2 * p + rr;
+  };
+  auto load_x = [&](int q, u32x4 (&v)[Q_ITEMS][4]) {
+#pragma unroll
+    for (int j = 0; j < Q_ITEMS; j++) {
+      int r, g, c4;
+      const int u = tid + 256 * j;
+      unit(u, r, g, c4);
+      const int iy = y0 - 1 + r, gx = x0 - 8 + 8 * g;
+      const bool ok = u < Q_UNITS && iy >= 0 && iy < a.H && gx >= 0 && gx < a.W;
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+        v[j][i] = *(const u32x4 *)(ok ? a.x + (long)(32 * q + 4 * c4 + i) * a.xs +
+                                            (long)iy * a.W + gx
+                                      : a.zeros);
+    }
+  };
+  auto store_x = [&](const u32x4 (&v)[Q_ITEMS][4], int buf) {
+    uint16_t *halo = (uint16_t *)(lds + buf * Q_BUF);
+#pragma unroll
+    for (int j = 0; j < Q_ITEMS; j++) {
+      int r, g, c4;
+      const int u = tid + 256 * j;
+      unit(u, r, g, c4);
+      // Pixel e of the group is halo column 8 g + e - 7.
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        const int hc = 8 * g + e - 7;
+        const unsigned sel = (e & 1) ? 0x07060302u : 0x05040100u;
+        uint2 o;
+        o.x = __builtin_amdgcn_perm(v[j][1][e >> 1], v[j][0][e >> 1], sel);
+        o.y = __builtin_amdgcn_perm(v[j][3][e >> 1], v[j][2][e >> 1], sel);
+        if (u < Q_UNITS && hc >= 0 && hc < Q_HC)
+          *(uint2 *)(halo + r * Q_RP + hc * Q_PX + 4 * c4) = o;
+      }
+    }
+  };
+
+  // Pixel blocks b (32 b ..+ 31) of tile row `row`, channel block nb.
+  floatx16 acc[3] = {};
+  auto products = [&](int buf) {
+    const uint16_t *ab = (const uint16_t *)(lds + buf * Q_BUF) + row * Q_RP + col * Q_PX + 8 * hi;
+    const uint16_t *wb = (const uint16_t *)(lds + buf * Q_BUF + Q_HALO) + nb * 18 * 512 + lane * 8;
+    // Step s: tap s / 2, channels 16 (s % 2) ..+ 15 of the quarter.
+    auto frag = [&](int s, half8 *av, half8 &bv) {
+      const int tap = s >> 1, g = s & 1, dy = tap / 3, dx = tap % 3;
+#pragma unroll
+      for (int b = 0; b < 3; b++)
+        av[b] = *(const half8 *)(ab + dy * Q_RP + (32 * b + dx) * Q_PX + 16 * g);
+      bv = *(const half8 *)(wb + (2 * tap + g) * 512);
+    };
+    half8 av[2][3], bv[2];
+    frag(0, av[0], bv[0]);
+#pragma unroll
+    for (int s = 0; s < 18; s++) {
+      if (s + 1 < 18) frag(s + 1, av[(s + 1) & 1], bv[(s + 1) & 1]);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int b = 0; b < 3; b++)
+        acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[s & 1][b], bv[s & 1], acc[b], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  u32x4 va[Q_ITEMS][4], vb[Q_ITEMS][4];
+  dma_w(0, 0);
+  load_x(0, va);
+  dma_w(1, 1);
+  load_x(1, vb);
+  wait_vm<9 + 4 * Q_ITEMS>();  // quarter 0's fragments and pixels have landed
+  store_x(va, 0);
+  lds_barrier();
+  load_x(2, va);
+  products(0);
+  wait_vm<4 * Q_ITEMS>();  // quarter 1's (quarter 2's pixels still in flight)
+  store_x(vb, 1);
+  lds_barrier();  // every wave is done with buffer 0
+  dma_w(2, 0);
+  load_x(3, vb);
+  products(1);
+  wait_vm<4 * Q_ITEMS>();  // quarter 2's (quarter 3's pixels still in flight)
+  store_x(va, 0);
+  lds_barrier();  // every wave is done with buffer 1
+  dma_w(3, 1);
+  products(0);
+  wait_vm<0>();
+  store_x(vb, 1);
+  lds_barrier();  // every wave is done with buffer 0: its halo becomes the output staging
+  products(1);
+
+  // D[pixel][channel]: accumulator r holds pixel 8 (r / 4) + 4 hi + r % 4
+  // of the block, channel col; staged [row][channel of the half][pixel].
+  uint16_t *ys = (uint16_t *)lds + (row * 64 + 32 * nb + col) * Q_YP;
+#pragma unroll
+  for (int b = 0; b < 3; b++)
+#pragma unroll
+    for (int r4 = 0; r4 < 4; r4++) {
+      uint2 o;
+      const float v0 = act_c<ACT>(acc[b][4 * r4 + 0] + bias, slope);
+      const float v1 = act_c<ACT>(acc[b][4 * r4 + 1] + bias, slope);
+      const float v2 = act_c<ACT>(acc[b][4 * r4 + 2] + bias, slope);
+      const float v3 = act_c<ACT>(acc[b][4 * r4 + 3] + bias, slope);
+      o.x = (uint32_t)f2h(v0) | ((uint32_t)f2h(v1) << 16);
+      o.y = (uint32_t)f2h(v2) | ((uint32_t)f2h(v3) << 16);
+      *(uint2 *)(ys + 32 * b + 8 * r4 + 4 * hi) = o;
+    }
+  lds_barrier();
+  // 12 16-byte pieces per (row, channel): 1536 a tile, 6 a thread.
+#pragma unroll
+  for (int i = 0; i < Q_TR * 64 * 12 / 256; i++) {
+    const int e = tid + 256 * i, k = e % 12, rn = e / 12, rr = rn >> 6, n = rn & 63;
+    const int oy = y0 + rr, ox = x0 + 8 * k;
+    if (oy < a.H && ox < a.W)
+      *(u32x4 *)(a.y + (long)(64 * nh + n) * a.ys + (long)oy * a.W + ox) =
+          *(const u32x4 *)((const uint16_t *)lds + rn * Q_YP + 8 * k);
+  }
+}
+
 }  // namespace
 
 bool nchw1_supported(const ConvArgs &a, int ks, int stride, long rows) {
@@ -394,6 +585,35 @@ ien_status launch_nchw3(ien_ctx *ctx, const ConvArgs &a) {
       hipLaunchKernelGGL(k_nchw3<IEN_ACT_SIGMOID>, grid, dim3(256), 0, ctx->stream, n);
       break;
     default: hipLaunchKernelGGL(k_nchw3<IEN_ACT_NONE>, grid, dim3(256), 0, ctx->stream, n); break;
+  }
+  IEN_HIP(hipGetLastError());
+  return IEN_OK;
+}
+
+bool nchw3q_supported(const ConvArgs &a, int ks, int stride, long rows) {
+  const long P = (long)a.H * a.W;
+  return ks == 3 && stride == 1 && a.C == 128 && a.N == 128 && a.KB == 72 && !a.rows_mode &&
+         !a.pad_reflect && a.noff == 0 && a.out_nchw && !a.out_f32 && !a.accumulate &&
+         a.p_begin == 0 && rows == P && a.OH == a.H && a.OW == a.W && a.W % 8 == 0 &&
+         a.xs % 8 == 0 && a.ys % 8 == 0 && (((uintptr_t)a.x | (uintptr_t)a.y) & 15) == 0 &&
+         a.xs >= P && a.ys >= P && 128L * a.xs < (1L << 31) && 128L * a.ys < (1L << 31);
+}
+
+ien_status launch_nchw3q(ien_ctx *ctx, const ConvArgs &a) {
+  Nchw3qArgs n{a.x, a.xs, a.H, a.W, a.wp, a.zeros, a.bias, a.slope, (uint16_t *)a.y, a.ys,
+               (a.W + Q_TC - 1) / Q_TC, 0};
+  n.tiles = 2 * n.tiles_x * ((a.H + Q_TR - 1) / Q_TR);
+  const dim3 grid((unsigned)n.tiles);
+  switch (a.act) {
+    case IEN_ACT_RELU: hipLaunchKernelGGL(k_nchw3q<IEN_ACT_RELU>, grid, dim3(256), 0, ctx->stream, n); break;
+    case IEN_ACT_GELU: hipLaunchKernelGGL(k_nchw3q<IEN_ACT_GELU>, grid, dim3(256), 0, ctx->stream, n); break;
+    case IEN_ACT_PRELU:
+      hipLaunchKernelGGL(k_nchw3q<IEN_ACT_PRELU>, grid, dim3(256), 0, ctx->stream, n);
+      break;
+    case IEN_ACT_SIGMOID:
+      hipLaunchKernelGGL(k_nchw3q<IEN_ACT_SIGMOID>, grid, dim3(256), 0, ctx->stream, n);
+      break;
+    default: hipLaunchKernelGGL(k_nchw3q<IEN_ACT_NONE>, grid, dim3(256), 0, ctx->stream, n); break;
   }
   IEN_HIP(hipGetLastError());
   return IEN_OK;

@@ -227,6 +227,19 @@ def test_nchw_3x3_64(ctx, oracle, h, w, act):
     close(run_gpu(ctx, x, wt, b, act=act, slope=slope, nchw_in=True, nchw_out=True), want)
 
 
+# The NCHW 3 x 3 128 -> 128 kernel (2 x 96 tiles a channel half, K in four
+# double-buffered quarters): heights that leave a partial 2-row tile, widths
+# (multiples of 8) that leave a partial 96-pixel tile or fall short of one,
+# every activation.
+@pytest.mark.parametrize("h,w,act", [(2, 96, 0), (5, 200, 1), (9, 104, 3), (3, 8, 2), (6, 392, 4),
+                                     (1, 16, 3)])
+def test_nchw_3x3_128(ctx, oracle, h, w, act):
+    x, wt, b = case(190 + h + w, h, w, 128, 128, 9)
+    slope = np.linspace(-0.3, 0.3, 128).astype(np.float32)
+    want = want_cpu(oracle, x, wt, b, act=act, slope=slope)
+    close(run_gpu(ctx, x, wt, b, act=act, slope=slope, nchw_in=True, nchw_out=True), want)
+
+
 # Where that kernel does not apply, the general one runs: a row range, an
 # accumulating product, f32 outputs, pixel counts not a multiple of 8.
 def test_nchw_1x1_other_forms(ctx, oracle):
