@@ -56,6 +56,10 @@ struct Birefnet {
            *a = nullptr, *cat = nullptr, *g = nullptr, *prev = nullptr, *stacked = nullptr,
            *mid = nullptr, *low = nullptr;
   float *partial = nullptr, *d_bias = nullptr;
+  // The half-size backbone's own patch rows, token map, merge rows and Swin
+  // scratch: it runs on a branch stream beside the full-size one.
+  uint16_t *hprow = nullptr, *hx = nullptr, *hmrows = nullptr, *hscratch = nullptr;
+  size_t hscratch_halves = 0;
   float *d_in = nullptr, *d_out = nullptr;  // host-API staging
   size_t staged = 0;
 };

@@ -434,7 +434,8 @@ void free_block(BirefnetBlock &B) {
 void free_maps(Birefnet &b) {
   for (uint16_t **p : {&b.img16, &b.half16, &b.prow, &b.x, &b.mrows, &b.level[0], &b.level[1],
                        &b.level[2], &b.level[3], &b.tmp, &b.x4, &b.in, &b.t, &b.a, &b.cat, &b.g,
-                       &b.prev, &b.stacked, &b.mid, &b.low}) {
+                       &b.prev, &b.stacked, &b.mid, &b.low, &b.hprow, &b.hx, &b.hmrows,
+                       &b.hscratch}) {
     (void)hipFree(*p);
     *p = nullptr;
   }
@@ -444,6 +445,7 @@ void free_maps(Birefnet &b) {
   (void)hipFree(b.samples);
   b.partial = b.d_bias = b.offs = nullptr;
   b.samples = nullptr;
+  b.hscratch_halves = 0;
   b.side = 0;
 }
 
@@ -628,47 +630,92 @@ ien_status block_run(Birefnet *b, const BirefnetBlock &B, const uint16_t *in, in
 // each stage's normalised output into level buffer s (columns `col` of
 // rows 2 c wide) directly for the full size, through `tmp` and a resize for
 // the half size.
-ien_status backbone_run(Birefnet *b, const uint16_t *img, int side, bool half,
-                        Steps *steps, int *step) {
+// The buffers one backbone run works in: the full-size run uses the
+// model's, the half-size run (on a branch stream) its own.
+struct BackboneBufs {
+  uint16_t *prow, *x, *mrows, *scratch;
+  size_t scratch_halves;  // 0: each block's own scratch
+};
+
+// swin.rs:171-215 Backbone::run on the f16 image `img` (side x side x 3):
+// the patch embedding, then stage by stage (backbone_stage).
+ien_status backbone_embed(Birefnet *b, const BackboneBufs &k, const uint16_t *img, int side) {
   ien_ctx *ctx = b->ctx;
-  int grid = side / 4;
+  const int grid = side / 4;
   const long tokens = (long)grid * grid;
   hipLaunchKernelGGL(k_patch_rows, dim3(blocks_for(tokens * 4, 256)), dim3(256), 0, ctx->stream,
-                     img, side, b->prow);
+                     img, side, k.prow);
   IEN_HIP(hipGetLastError());
-  ien_status st = rows_product(ctx, b->prow, 48, 48, tokens, b->embed, b->x, 96, IEN_ACT_NONE, 0);
-  if (st == IEN_OK) st = ien_layer_norm(ctx, b->x, tokens, 96, 96, b->d_embed_ln, b->d_embed_ln + 96);
-  for (int s = 0; s < 4 && st == IEN_OK; s++) {
-    const int c = STAGE_C[s];
-    for (ien_swin *blk : b->blocks[s]) {
-      st = ien_swin_run(blk, b->x, c, grid, grid);
-      if (st != IEN_OK) return st;
-    }
-    const long n = (long)grid * grid;
-    if (!half) {
-      st = layer_norm_to(ctx, b->x, c, b->level[s], 2L * c, n, c, b->d_norm[s], b->d_norm[s] + c);
-    } else {
-      // The half-size map, normalised, then resized to the full grid.
-      st = layer_norm_to(ctx, b->x, c, b->tmp, c, n, c, b->d_norm[s], b->d_norm[s] + c);
-      if (st == IEN_OK)
-        st = ien_resize(ctx, b->tmp, grid, grid, c, c, b->level[s] + c, 2 * grid, 2 * grid, 2 * c,
-                        IEN_OUT_F16, 0);
-    }
-    if (st == IEN_OK && s < 3) {
-      // swin.rs:377-405 merge: (0,0), (1,0), (0,1), (1,1) by (row, column).
-      // The 2 x 2 groups gathered as the LayerNorm over 4c reads them.
-      const long half_tokens = n / 4;
-      st = layer_norm_to(ctx, b->x, c, b->mrows, 4 * c, half_tokens, 4 * c, b->d_merge_ln[s],
-                         b->d_merge_ln[s] + 4 * c, grid / 2);
-      if (st == IEN_OK)
-        st = rows_product(ctx, b->mrows, 4 * c, 4 * c, half_tokens, b->merge[s], b->x, 2 * c,
-                          IEN_ACT_NONE, 0);
-      grid /= 2;
-    }
-    if (st == IEN_OK && steps) st = steps->step(ctx->stream);
-    ++*step;
+  ien_status st = rows_product(ctx, k.prow, 48, 48, tokens, b->embed, k.x, 96, IEN_ACT_NONE, 0);
+  if (st == IEN_OK) st = ien_layer_norm(ctx, k.x, tokens, 96, 96, b->d_embed_ln, b->d_embed_ln + 96);
+  return st;
+}
+
+// Stage s on a grid x grid token map: its blocks, the stage output
+// normalised into level buffer s (columns 0 .. c of rows 2 c wide)
+// directly for the full size, through `tmp` and a resize into columns
+// c .. 2 c for the half size; then the merge (s < 3).
+ien_status backbone_stage(Birefnet *b, const BackboneBufs &k, int s, int grid, bool half) {
+  ien_ctx *ctx = b->ctx;
+  const int c = STAGE_C[s];
+  ien_status st = IEN_OK;
+  for (ien_swin *blk : b->blocks[s]) {
+    st = k.scratch_halves ? swin_run_with(blk, k.x, c, grid, grid, k.scratch, k.scratch_halves)
+                          : ien_swin_run(blk, k.x, c, grid, grid);
+    if (st != IEN_OK) return st;
+  }
+  const long n = (long)grid * grid;
+  if (!half) {
+    st = layer_norm_to(ctx, k.x, c, b->level[s], 2L * c, n, c, b->d_norm[s], b->d_norm[s] + c);
+  } else {
+    st = layer_norm_to(ctx, k.x, c, b->tmp, c, n, c, b->d_norm[s], b->d_norm[s] + c);
+    if (st == IEN_OK)
+      st = ien_resize(ctx, b->tmp, grid, grid, c, c, b->level[s] + c, 2 * grid, 2 * grid, 2 * c,
+                      IEN_OUT_F16, 0);
+  }
+  if (st == IEN_OK && s < 3) {
+    // swin.rs:377-405 merge: (0,0), (1,0), (0,1), (1,1) by (row, column).
+    // The 2 x 2 groups gathered as the LayerNorm over 4c reads them.
+    const long half_tokens = n / 4;
+    st = layer_norm_to(ctx, k.x, c, k.mrows, 4 * c, half_tokens, 4 * c, b->d_merge_ln[s],
+                       b->d_merge_ln[s] + 4 * c, grid / 2);
+    if (st == IEN_OK)
+      st = rows_product(ctx, k.mrows, 4 * c, 4 * c, half_tokens, b->merge[s], k.x, 2 * c,
+                        IEN_ACT_NONE, 0);
   }
   return st;
+}
+
+// Both backbones (lib.rs:144-171: the image and its half-size resize), the
+// half-size one on branch stream 1, stage by stage beside the full-size
+// one: its launches are small and leave most CUs to the other.  The two
+// write disjoint columns of the level buffers.
+ien_status backbones_run(Birefnet *b, int side, Steps *steps, int *step) {
+  ien_ctx *ctx = b->ctx;
+  const BackboneBufs full{b->prow, b->x, b->mrows, nullptr, 0};
+  const BackboneBufs half{b->hprow, b->hx, b->hmrows, b->hscratch, b->hscratch_halves};
+  ien_status st = fork_branches(ctx, 1);
+  if (st == IEN_OK) st = backbone_embed(b, full, b->img16, side);
+  if (st == IEN_OK) {
+    Branch br(ctx, 1);
+    st = backbone_embed(b, half, b->half16, side / 2);
+  }
+  for (int s = 0; s < 4 && st == IEN_OK; s++) {
+    st = backbone_stage(b, full, s, side >> (s + 2), false);
+    if (st == IEN_OK && steps) st = steps->step(ctx->stream);
+    ++*step;
+    if (st != IEN_OK) break;
+    {
+      Branch br(ctx, 1);
+      st = backbone_stage(b, half, s, side >> (s + 3), true);
+      if (st == IEN_OK && steps) st = steps->step(ctx->stream);
+    }
+    ++*step;
+  }
+  // (After a failure or a cancel the branch is joined all the same, so
+  // that nothing on it outlives the run.)
+  const ien_status js = join_branches(ctx, 1);
+  return st != IEN_OK ? st : js;
 }
 
 }  // namespace
@@ -853,6 +900,19 @@ ien_status birefnet_reserve(Birefnet *b, size_t side, bool *grew) {
   if (e == hipSuccess) e = alloc(&b->stacked, 3 * P);
   if (e == hipSuccess) e = alloc(&b->mid, Q * INTER);
   if (e == hipSuccess) e = alloc(&b->low, Q);
+  // The half-size backbone: a quarter of the full one's rows, and the
+  // largest Swin scratch its blocks take.
+  if (e == hipSuccess) e = alloc(&b->hprow, Q / 4 * 48);
+  if (e == hipSuccess) e = alloc(&b->hx, Q / 4 * 96);
+  if (e == hipSuccess) e = alloc(&b->hmrows, Q / 4 * 96);
+  size_t hs = 0;
+  for (int s = 0; s < 4; s++)
+    for (ien_swin *blk : b->blocks[s]) {
+      const int g = (int)(side >> (s + 3));
+      hs = std::max(hs, swin_scratch_halves(blk, g, g));
+    }
+  if (e == hipSuccess) e = alloc(&b->hscratch, std::max<size_t>(hs, 8));
+  if (e == hipSuccess) b->hscratch_halves = std::max<size_t>(hs, 8);
   if (e == hipSuccess) e = hipMalloc((void **)&b->partial, POOL_PARTS * INTER * 4);
   // conv1's biases: 64 written per run, padded with zeros to the product's
   // 128-column tiles.
@@ -882,8 +942,7 @@ ien_status birefnet_enqueue(Birefnet *b, const float *d_image, size_t side_, flo
   if (st == IEN_OK)
     st = ien_resize(ctx, b->img16, side, side, 3, 3, b->half16, side / 2, side / 2, 3, IEN_OUT_F16,
                     0);
-  if (st == IEN_OK) st = backbone_run(b, b->img16, side, false, steps, &step);
-  if (st == IEN_OK) st = backbone_run(b, b->half16, side / 2, true, steps, &step);
+  if (st == IEN_OK) st = backbones_run(b, side, steps, &step);
   if (st != IEN_OK) return st;
   // The squeeze block's input: levels 1..3 resized to level 4's grid, then
   // level 4 (decoder.rs:840-859).

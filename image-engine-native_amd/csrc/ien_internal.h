@@ -302,6 +302,11 @@ ien_status composite_bytes(ien_ctx *ctx, const uint8_t *rgb, const uint8_t *mask
 
 // swin.hip: a block's scratch grown for a height x width map in advance.
 ien_status swin_reserve(ien_swin *b, int height, int width);
+// Scratch halves of a block's run on a height x width map, and a run with
+// the caller's scratch of that size (runs of one block on two streams).
+size_t swin_scratch_halves(const ien_swin *b, int height, int width);
+ien_status swin_run_with(ien_swin *b, uint16_t *d_map, size_t stride, int height, int width,
+                         uint16_t *scratch, size_t halves);
 
 // swin_mlp.hip: map rows += fc2(GELU(fc1(LayerNorm(rows)))) in one pass,
 // for c = 32, 64 and 96 (16-byte aligned rows).

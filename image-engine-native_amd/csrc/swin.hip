@@ -209,6 +209,27 @@ ien_status swin_reserve(ien_swin *b, int height, int width) {
   return reserve(b, rows > tokens ? rows : tokens);
 }
 
+// Halves of scratch a block's run on a height x width map may use (the
+// unfused path's window rows at 6c halves each), or 0 for an invalid map.
+size_t swin_scratch_halves(const ien_swin *b, int height, int width) {
+  return block_rows(b, height, width) * 6 * (size_t)b->c;
+}
+
+// A block's run with the caller's scratch (at least swin_scratch_halves),
+// so that runs of one block on different streams do not share the block's
+// own scratch.
+ien_status swin_run_with(ien_swin *b, uint16_t *d_map, size_t stride, int height, int width,
+                         uint16_t *scratch, size_t halves) {
+  IEN_CHECK(b && d_map && scratch, IEN_ERR_INPUT, "null argument");
+  const size_t rows = block_rows(b, height, width);
+  IEN_CHECK(rows > 0, IEN_ERR_INPUT, "map %d x %d", height, width);
+  const size_t c = (size_t)b->c;
+  IEN_CHECK(rows * 6 * c <= halves, IEN_ERR_INPUT, "scratch of %zu halves for %zu", halves,
+            rows * 6 * c);
+  uint16_t *wide = scratch, *tok = wide + rows * 4 * c, *att = tok + rows * c;
+  return run_block(b, d_map, stride, height, width, wide, tok, att);
+}
+
 // Once per device, with that device current (ien_open): the device
 // address of `scratch` for ien_swin_run_static.
 hipError_t swin_static_setup(int device) {
