@@ -99,6 +99,36 @@ def test_birefnet_graph_and_progress(ctx):
     model.free()
 
 
+# The half-size backbone runs on a branch stream beside the full-size one;
+# with every branch on the context's stream (IEN_SERIAL_BRANCHES, read when
+# a context opens) the launches are the same, so the logits are the same
+# bits, eager and replayed.
+def test_birefnet_branches_match_serial(monkeypatch):
+    import torch
+    import ien
+
+    side = 256
+    t = synthetic.birefnet_tensors(init="fan")
+    img = synthetic.birefnet_image(side, seed=21)
+    got = {}
+    for serial in ("0", "1"):
+        monkeypatch.setenv("IEN_SERIAL_BRANCHES", serial)
+        c = ien.Context(0)
+        model = ien.Model(c, ien.MODEL_BIREFNET, tensors=t)
+        got[serial, "eager"] = model.run(img)
+        d_in = torch.from_numpy(img).cuda()
+        d_out = torch.empty((side, side), dtype=torch.float32, device="cuda")
+        model.set_graph(True)
+        model.run_device(d_in, side, side, d_out)
+        torch.cuda.synchronize()
+        got[serial, "graph"] = d_out.cpu().numpy()
+        model.free()
+        c.close()
+    ref = got["1", "eager"].view(np.uint32)
+    for key, out in got.items():
+        assert np.array_equal(out.view(np.uint32), ref), key
+
+
 @pytest.mark.parametrize("init", ["trunc_normal", "fan"])
 def test_birefnet_config_size_matches_oracle(ctx, oracle, init):
     """1 x 3 x 1024 x 1024 N(0, 1), window 12, the configuration's size,
