@@ -597,15 +597,27 @@ ien_status block_run(Birefnet *b, const BirefnetBlock &B, const uint16_t *in, in
   const long pixels = (long)h * w;
   ien_status st = conv(ctx, in, h, w, B.cin, B.cin, 3, B.conv_in, b->t, INTER, IEN_ACT_RELU, 0);
   if (st != IEN_OK) return st;
-  hipLaunchKernelGGL(k_pool_partial, dim3(POOL_PARTS), dim3(256), 0, ctx->stream, b->t, pixels,
-                     b->partial);
-  hipLaunchKernelGGL(k_pool_finish, dim3(1), dim3(256), 0, ctx->stream, b->partial, pixels,
-                     B.d_pool, b->d_bias);
-  IEN_HIP(hipGetLastError());
+  // The pooling branch only feeds conv1's bias: it runs on branch stream 1
+  // beside the four branch convolutions (one workgroup of its two passes
+  // would otherwise hold up the CUs between them).
+  st = fork_branches(ctx, 1);
+  if (st != IEN_OK) return st;
+  {
+    Branch br(ctx, 1);
+    hipLaunchKernelGGL(k_pool_partial, dim3(POOL_PARTS), dim3(256), 0, ctx->stream, b->t, pixels,
+                       b->partial);
+    hipLaunchKernelGGL(k_pool_finish, dim3(1), dim3(256), 0, ctx->stream, b->partial, pixels,
+                       B.d_pool, b->d_bias);
+  }
+  if (const hipError_t le = hipGetLastError(); le != hipSuccess)
+    st = fail(IEN_ERR_GPU, "pooling launch: %s", hipGetErrorString(le));
   for (int i = 0; i < 4 && st == IEN_OK; i++)
     st = B.offset[i] ? deformable_branch(b, B, i, h, w)
                      : conv(ctx, b->t, h, w, INTER, INTER, ASPP_SIZES[i], B.branch[i],
                             b->cat + i * BRANCH, 4 * BRANCH, IEN_ACT_RELU, 0);
+  // (Joined after a failure too, so that nothing on the branch outlives the run.)
+  const ien_status js = join_branches(ctx, 1);
+  if (st == IEN_OK) st = js;
   if (st != IEN_OK) return st;
   // conv1 over the four branches with the pooling's part (constant over the
   // pixels) and conv1's bias as its bias.
