@@ -94,18 +94,20 @@ ien_status ffc_run(Lama *l, const LamaFfc &f, const uint16_t *x, uint16_t *out, 
   // launches on branch 1 beside the local and cross convolutions on the
   // context's stream (the two convolutions side by side were slower:
   // LaMa 2.45 against 2.34 ms/image all on one stream), joined before its
-  // last launch, which accumulates onto the cross output.  R goes to the
+  // last launch, which accumulates onto the cross output.  The local
+  // convolution is enqueued before the branch's launches, so that its
+  // workgroups (one a CU) are not held back behind theirs.  R goes to the
   // spectrum buffer, U to the work buffer.
   if (l->spectral_plan) {
     ien_status st = fork_branches(ctx, 1);
+    if (st == IEN_OK)
+      st = conv(ctx, x, h, w, CHANNELS, CHANNELS, 3, 1, f.local, residual ? residual : out,
+                CHANNELS, IEN_ACT_RELU, 0, residual);
     if (st == IEN_OK) {
       Branch b(ctx, 1);
       st = spectral_front(l->spectral_plan, x + LOCAL, CHANNELS, f.spectral_in, f.fourier,
                           l->spectral, (float *)l->spectrum, l->work);
     }
-    if (st == IEN_OK)
-      st = conv(ctx, x, h, w, CHANNELS, CHANNELS, 3, 1, f.local, residual ? residual : out,
-                CHANNELS, IEN_ACT_RELU, 0, residual);
     if (st == IEN_OK)
       st = conv(ctx, x, h, w, LOCAL, CHANNELS, 3, 1, f.cross, out + LOCAL, CHANNELS, IEN_ACT_NONE,
                 0);
