@@ -48,6 +48,12 @@ bool spectral_shapes(const ien_matrix *in, const ien_matrix *f, const ien_matrix
 ien_status spectral_front(const ien_spectral *sp, const uint16_t *x, long xs,
                           const ien_matrix *m_in, const ien_matrix *m_f, uint16_t *spectral,
                           float *r, float *u);
+// The front's two launches one at a time: the rows (spectral map and R),
+// then the columns (U).
+ien_status spectral_rows(const ien_spectral *sp, const uint16_t *x, long xs,
+                         const ien_matrix *m_in, uint16_t *spectral, float *r);
+ien_status spectral_columns(const ien_spectral *sp, const ien_matrix *m_f, const float *r,
+                            float *u);
 // The result (ReLU(out + spectral_out(spectral + irfft(u)))) goes to dst
 // (out when null), with `add` (rows ys apart, or null) added after the
 // rounding and rounded again.

@@ -90,23 +90,25 @@ ien_status ffc_run(Lama *l, const LamaFfc &f, const uint16_t *x, uint16_t *out, 
   const size_t pixels = (size_t)h * w, half = (size_t)w / 2 + 1, spix = (size_t)h * half;
   // The local convolution, the cross convolution and the spectral chain
   // are independent until the spectral output accumulates onto the cross
-  // part.  With the fused spectral branch (spectral.hip): its first two
-  // launches on branch 1 beside the local and cross convolutions on the
-  // context's stream (the two convolutions side by side were slower:
-  // LaMa 2.45 against 2.34 ms/image all on one stream), joined before its
-  // last launch, which accumulates onto the cross output.  The local
-  // convolution is enqueued before the branch's launches, so that its
-  // workgroups (one a CU) are not held back behind theirs.  R goes to the
-  // spectrum buffer, U to the work buffer.
+  // part.  With the fused spectral branch (spectral.hip): its row launch
+  // first (192 short workgroups), then its column launch on branch 1 beside
+  // the local and cross convolutions on the context's stream (the two
+  // convolutions side by side were slower: LaMa 2.45 against 2.34 ms/image
+  // all on one stream), joined before its last launch, which accumulates
+  // onto the cross output.  The local convolution is enqueued before the
+  // branch's launch, so that its workgroups (one a CU) are not held back
+  // behind the columns'.  R goes to the spectrum buffer, U to the work
+  // buffer.
   if (l->spectral_plan) {
-    ien_status st = fork_branches(ctx, 1);
+    ien_status st = spectral_rows(l->spectral_plan, x + LOCAL, CHANNELS, f.spectral_in,
+                                  l->spectral, (float *)l->spectrum);
+    if (st == IEN_OK) st = fork_branches(ctx, 1);
     if (st == IEN_OK)
       st = conv(ctx, x, h, w, CHANNELS, CHANNELS, 3, 1, f.local, residual ? residual : out,
                 CHANNELS, IEN_ACT_RELU, 0, residual);
     if (st == IEN_OK) {
       Branch b(ctx, 1);
-      st = spectral_front(l->spectral_plan, x + LOCAL, CHANNELS, f.spectral_in, f.fourier,
-                          l->spectral, (float *)l->spectrum, l->work);
+      st = spectral_columns(l->spectral_plan, f.fourier, (const float *)l->spectrum, l->work);
     }
     if (st == IEN_OK)
       st = conv(ctx, x, h, w, LOCAL, CHANNELS, 3, 1, f.cross, out + LOCAL, CHANNELS, IEN_ACT_NONE,

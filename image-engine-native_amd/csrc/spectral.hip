@@ -675,21 +675,33 @@ bool spectral_shapes(const ien_matrix *in, const ien_matrix *f, const ien_matrix
          f->n == SPEC2 && f->d_bias && out->k == SPEC && out->n == SPEC2;
 }
 
-ien_status spectral_front(const ien_spectral *sp, const uint16_t *x, long xs,
-                          const ien_matrix *m_in, const ien_matrix *m_f, uint16_t *spectral,
-                          float *r, float *u) {
+ien_status spectral_rows(const ien_spectral *sp, const uint16_t *x, long xs,
+                         const ien_matrix *m_in, uint16_t *spectral, float *r) {
   ien_ctx *ctx = sp->ctx;
   FrontArgs a{x, (int)xs, sp->h, sp->w, sp->xp, sp->mb, m_in->d_packed, m_in->kb, m_in->d_bias,
               sp->d_tf, spectral, r};
   hipLaunchKernelGGL(k_spectral_front, dim3((unsigned)sp->h, SPEC / 64), dim3(256), 0, ctx->stream,
                      a);
   IEN_HIP(hipGetLastError());
+  return IEN_OK;
+}
+
+ien_status spectral_columns(const ien_spectral *sp, const ien_matrix *m_f, const float *r,
+                            float *u) {
+  ien_ctx *ctx = sp->ctx;
   ColumnArgs c{r, sp->h, sp->w, sp->half, sp->yp, sp->nba, sp->d_ta, sp->d_tc, m_f->d_packed,
                m_f->kb, m_f->d_bias, u};
   const unsigned column_blocks = 8u * COLUMN_GROUPS * (unsigned)((sp->half + 7) / 8);
   hipLaunchKernelGGL(k_spectral_columns, dim3(column_blocks), dim3(512), 0, ctx->stream, c);
   IEN_HIP(hipGetLastError());
   return IEN_OK;
+}
+
+ien_status spectral_front(const ien_spectral *sp, const uint16_t *x, long xs,
+                          const ien_matrix *m_in, const ien_matrix *m_f, uint16_t *spectral,
+                          float *r, float *u) {
+  const ien_status st = spectral_rows(sp, x, xs, m_in, spectral, r);
+  return st == IEN_OK ? spectral_columns(sp, m_f, r, u) : st;
 }
 
 ien_status spectral_back(const ien_spectral *sp, const ien_matrix *m_out, const uint16_t *spectral,
