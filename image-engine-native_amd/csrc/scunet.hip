@@ -161,8 +161,10 @@ ien_status run_level(Scunet &s, ScunetBlock *blocks, int h, int w, int c, Steps 
   for (int b = 0; b < BLOCKS && st == IEN_OK; b++) {
     ScunetBlock &B = blocks[b];
     // The two halves are independent until the join: the convolution half
-    // on branch 1, the Swin half on the context's stream.
+    // on branch 1, the Swin half (the longer) on the context's stream,
+    // enqueued first.
     st = fork_branches(ctx, 1);
+    if (st == IEN_OK) st = ien_swin_run(B.swin, ysw, half, h, w);
     if (st == IEN_OK) {
       Branch br(ctx, 1);
       // network.rs:135-153 convolve: conv3 + ReLU into t, conv3 added back.
@@ -174,7 +176,6 @@ ien_status run_level(Scunet &s, ScunetBlock *blocks, int h, int w, int c, Steps 
         st = conv3(ctx, s.t, h, w, (int)half, (long)half, B.conv2, yc, (long)half, IEN_ACT_NONE, 1);
       ctx->compact = false;
     }
-    if (st == IEN_OK) st = ien_swin_run(B.swin, ysw, half, h, w);
     if (st == IEN_OK) st = join_branches(ctx, 1);
     // The join and the next block's split in one pass where it applies
     // (64 and 128 channels), else as two row products.
