@@ -1356,8 +1356,10 @@ ien_status launch_conv(ien_ctx *ctx, const ConvCall &c) {
   if (special && few_supported(a, c.ks, c.stride, nchw, c.noff, c.rows_mode))
     return launch_few(ctx, a, c.ks);
   // Resident weights: NHWC, zero padding, 16, 32 or 64 channels, K <= 640.
-  // Its results are staged as f16: f32 outputs take the general kernel.
-  if (special && vec && !c.out_f32 &&
+  // Its results are staged as f16: f32 outputs take the general kernel, and
+  // so do compact launches of 64 channels (beside another branch's kernels,
+  // whose workgroups the resident one's 158 KiB of LDS would shut out).
+  if (special && vec && !c.out_f32 && !(ctx->compact && c.C == 64) &&
       resident_supported(c.ks, c.stride, c.C, nchw, c.pad_reflect, c.noff, c.rows_mode,
                          (long)c.H * c.W * c.xs * 2))
     return launch_resident(ctx, a, c.ks);
