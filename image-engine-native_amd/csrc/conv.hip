@@ -1410,7 +1410,10 @@ ien_status launch_conv(ien_ctx *ctx, const ConvCall &c) {
     IEN_CHECK(!nchw, IEN_ERR_INPUT, "7x7 convolutions read NHWC");
     if (!vec) return run_cfg<7, 1, 4, 32, 4, 2, 16, false, false>(ctx, a);
     // 8 x 32 tiles (two M-blocks a wave): each chunk's 49-tap fragments
-    // (98 KiB at 64 output channels) are staged for twice the pixels.
+    // (98 KiB at 64 output channels) are staged for twice the pixels; 16 x 32
+    // tiles (four a wave) where those still make two rounds of the CUs.
+    const long tall = (long)((c.OH + 15) / 16) * ((c.OW + 31) / 32) * ((a.N + 63) / 64);
+    if (tall >= 2L * ctx->cus) return run_cfg<7, 1, 16, 32, 4, 2, 16, true, false>(ctx, a);
     return run_cfg<7, 1, 8, 32, 4, 2, 16, true, false>(ctx, a);
   }
 #undef IEN_CK
