@@ -527,6 +527,22 @@ __global__ __launch_bounds__(THREADS) void conv_pair(PairArgs a) {
     return false;
   };
   if (CHAIN && tid == 0) go = 1;  // (seen after the first pair's opening barrier)
+  // A chain's final layer adds the tile's image rows (24 pixels x RGB,
+  // 288 bytes each): into their own LDS array now, so that the loads are
+  // long done when the tail needs them (the first pair's waits cover them);
+  // rows past the image read zeros.
+  if constexpr (CHAIN) {
+    if (a.wl) {
+      const int4v ir = buffer_rsrc(a.image, (long)a.H * a.W * 12);
+      const unsigned i0 = lds_addr(img);
+      for (int i = wave; i < 2 * OTR; i += WAVES) {
+        const int r = i >> 1, part = i & 1, e = 64 * part + lane;
+        if (e < OTC * 3)
+          dma_lds4(ir, __builtin_amdgcn_readfirstlane(i0 + (r * OTC * 3 + 64 * part) * 4),
+                   y0 + r < a.H ? (((y0 + r) * a.W + x0) * 3 + e) * 4 : OOB);
+      }
+    }
+  }
   for (int k = 0; k < pairs; k++) {
     // ---- the first layer's weights (where its results will go) and, for
     // a single pair or a chain's first, the whole halo from the input; a
@@ -704,19 +720,7 @@ __global__ __launch_bounds__(THREADS) void conv_pair(PairArgs a) {
     // shuffle x4 plus the image, as f32 RGB ----
     const int k = pairs;
     if (tid < C) par[tid] = a.bl[tid];  // zero past channel 48
-    // The tile's image rows (24 pixels x RGB, 288 bytes each) into LDS,
-    // waited for with the ring below; rows past the image read zeros.
-    {
-      const int4v ir = buffer_rsrc(a.image, (long)a.H * a.W * 12);
-      const unsigned i0 = lds_addr(img);
-      for (int i = wave; i < 2 * OTR; i += WAVES) {
-        const int r = i >> 1, part = i & 1, e = 64 * part + lane;
-        if (e < OTC * 3)
-          dma_lds4(ir, __builtin_amdgcn_readfirstlane(i0 + (r * OTC * 3 + 64 * part) * 4),
-                   y0 + r < a.H ? (((y0 + r) * a.W + x0) * 3 + e) * 4 : OOB);
-      }
-    }
-    wait_vm<0>();
+    wait_vm<0>();  // the last border stores (the image rows landed long ago)
     __syncthreads();
     if (tid == 0) __hip_atomic_store(epochs + tile, k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (!ring(k)) {
