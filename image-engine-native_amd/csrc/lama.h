@@ -26,6 +26,9 @@ struct Lama {
            *mid = nullptr, *out = nullptr, *spectral = nullptr, *spectrum = nullptr,
            *filtered = nullptr, *rgb = nullptr;
   float *work = nullptr;
+  // The FFC pipeline's cross-stream points: the context's stream after a
+  // local convolution, branch 2 after a cross convolution.
+  hipEvent_t ev_local = nullptr, ev_cross = nullptr;
   float *d_in = nullptr, *d_mask = nullptr, *d_out = nullptr;  // host-API staging
   size_t staged = 0;
 };

@@ -78,48 +78,12 @@ ien_status rows_product(ien_ctx *ctx, const uint16_t *in, size_t k, size_t rows,
   return launch_conv(ctx, cc);
 }
 
-// network.rs:174-249 Ffc::run: out = ffc(x), both h x w maps of 512.  With
-// `residual` (the fused spectral branch only), the block's residual add
-// (network.rs:257-262, x += ffc1(ffc0(x))) runs in the last launches'
-// epilogues: the local part and the spectral back kernel add their rounded
-// results onto `residual` in place (the sums ien_add would make), and
-// `out` holds only the cross output the back kernel reads.
-ien_status ffc_run(Lama *l, const LamaFfc &f, const uint16_t *x, uint16_t *out, int h, int w,
-                   uint16_t *residual = nullptr) {
+// network.rs:174-249 Ffc::run: out = ffc(x), both h x w maps of 512, with
+// the unfused spectral chain (maps of sides over 64; the fused branch runs
+// in ffc_pipeline).
+ien_status ffc_run(Lama *l, const LamaFfc &f, const uint16_t *x, uint16_t *out, int h, int w) {
   ien_ctx *ctx = l->ctx;
   const size_t pixels = (size_t)h * w, half = (size_t)w / 2 + 1, spix = (size_t)h * half;
-  // The local convolution, the cross convolution and the spectral chain
-  // are independent until the spectral output accumulates onto the cross
-  // part.  With the fused spectral branch (spectral.hip): its row launch
-  // first (192 short workgroups), then its column launch on branch 1 beside
-  // the local and cross convolutions on the context's stream (the two
-  // convolutions side by side were slower: LaMa 2.45 against 2.34 ms/image
-  // all on one stream), joined before its last launch, which accumulates
-  // onto the cross output.  The local convolution is enqueued before the
-  // branch's launch, so that its workgroups (one a CU) are not held back
-  // behind the columns'.  R goes to the spectrum buffer, U to the work
-  // buffer.
-  if (l->spectral_plan) {
-    ien_status st = spectral_rows(l->spectral_plan, x + LOCAL, CHANNELS, f.spectral_in,
-                                  l->spectral, (float *)l->spectrum);
-    if (st == IEN_OK) st = fork_branches(ctx, 1);
-    if (st == IEN_OK)
-      st = conv(ctx, x, h, w, CHANNELS, CHANNELS, 3, 1, f.local, residual ? residual : out,
-                CHANNELS, IEN_ACT_RELU, 0, residual);
-    if (st == IEN_OK) {
-      Branch b(ctx, 1);
-      st = spectral_columns(l->spectral_plan, f.fourier, (const float *)l->spectrum, l->work);
-    }
-    if (st == IEN_OK)
-      st = conv(ctx, x, h, w, LOCAL, CHANNELS, 3, 1, f.cross, out + LOCAL, CHANNELS, IEN_ACT_NONE,
-                0);
-    if (st == IEN_OK) st = join_branches(ctx, 1);
-    if (st == IEN_OK)
-      st = spectral_back(l->spectral_plan, f.spectral_out, l->spectral, l->work, out + LOCAL,
-                         CHANNELS, residual ? residual + LOCAL : nullptr,
-                         residual ? residual + LOCAL : nullptr);
-    return st;
-  }
   // Unfused: local on the context's stream, cross on branch 1, the spectral
   // chain on branch 2, joined before the accumulation.
   ien_status st = fork_branches(ctx, 2);
@@ -209,6 +173,8 @@ void free_maps(Lama &l) {
 // writes them).
 ien_status lama_load(ien_ctx *ctx, const TensorSource &take, Lama *l) {
   l->ctx = ctx;
+  IEN_HIP(hipEventCreateWithFlags(&l->ev_local, hipEventDisableTiming));
+  IEN_HIP(hipEventCreateWithFlags(&l->ev_cross, hipEventDisableTiming));
   ien_status st = matrix(ctx, take, "first", 49 * 4, 64, true, &l->first);
   const int dins[3] = {64, 128, 256}, douts[3] = {128, 256, CHANNELS};
   for (int i = 0; i < 3 && st == IEN_OK; i++)
@@ -261,6 +227,9 @@ void lama_free(Lama *l) {
   (void)hipFree(l->d_in);
   (void)hipFree(l->d_mask);
   (void)hipFree(l->d_out);
+  if (l->ev_local) (void)hipEventDestroy(l->ev_local);
+  if (l->ev_cross) (void)hipEventDestroy(l->ev_cross);
+  l->ev_local = l->ev_cross = nullptr;
 }
 
 // network.rs:337-344 padded: sides to multiples of 8.
@@ -325,6 +294,95 @@ ien_status lama_reserve(Lama *l, size_t pw, size_t ph, bool *grew) {
 }
 
 // network.rs:415-489 Network::run.
+// The 18 blocks' FFCs with the fused spectral branch (network.rs:249-262,
+// x += ffc1(ffc0(x)): the second FFC's local convolution and back launch
+// add their rounded results onto x in place, the sums ien_add would make),
+// as a pipeline over three streams.  FFC k: its spectral rows (192 short
+// workgroups) and then its local convolution on the context's stream (the
+// local convolution enqueued before the branches' launches, so that its
+// workgroups, one a CU, are not held back behind theirs), its spectral
+// columns on branch 1, its back launch on the context's stream after both
+// (R in the spectrum buffer, U in the work buffer).  Its cross
+// convolution reads only the local part of its input, which the previous
+// FFC's local convolution has written: it runs on branch 2 from there on,
+// beside that FFC's columns and back launch (which leave CUs idle: 192
+// workgroups of one a CU each).  What the early cross convolution writes
+// (the global part of FFC k's output map) no launch before FFC k's back
+// reads: FFC k - 1 reads the other map (or, for the second FFC of a
+// block, x, whose global part it only reads in its rows and local launches,
+// both before the wait).
+template <class Done>
+ien_status ffc_pipeline(Lama *l, int h, int w, Done &done) {
+  ien_ctx *ctx = l->ctx;
+  struct Ffc {
+    const LamaFfc *f;
+    const uint16_t *x;
+    uint16_t *out, *residual;
+  };
+  Ffc ffcs[2 * BLOCKS];
+  for (int b = 0; b < BLOCKS; b++) {
+    ffcs[2 * b] = {&l->blocks[b][0], l->a, l->mid, nullptr};
+    ffcs[2 * b + 1] = {&l->blocks[b][1], l->mid, l->out, l->a};
+  }
+  constexpr int N = 2 * BLOCKS;
+  auto cross = [&](const Ffc &c) {
+    return conv(ctx, c.x, h, w, LOCAL, CHANNELS, 3, 1, c.f->cross, c.out + LOCAL, CHANNELS,
+                IEN_ACT_NONE, 0);
+  };
+  const bool split = !ctx->serial_branches;
+  hipStream_t branch2 = ctx->branch[1];
+  // The first cross convolution: x's local part is final now.
+  ien_status st = IEN_OK;
+  if (split) {
+    IEN_HIP(hipEventRecord(l->ev_local, ctx->stream));
+    IEN_HIP(hipStreamWaitEvent(branch2, l->ev_local, 0));
+  }
+  {
+    Branch br(ctx, 2);
+    st = cross(ffcs[0]);
+  }
+  for (int k = 0; k < N && st == IEN_OK; k++) {
+    const Ffc &c = ffcs[k];
+    st = spectral_rows(l->spectral_plan, c.x + LOCAL, CHANNELS, c.f->spectral_in, l->spectral,
+                       (float *)l->spectrum);
+    if (st == IEN_OK) st = fork_branches(ctx, 1);
+    if (st == IEN_OK)
+      st = conv(ctx, c.x, h, w, CHANNELS, CHANNELS, 3, 1, c.f->local,
+                c.residual ? c.residual : c.out, CHANNELS, IEN_ACT_RELU, 0, c.residual);
+    if (st != IEN_OK) break;
+    if (split) {
+      // Branch 2 holds this FFC's cross convolution: mark it, then queue the
+      // next FFC's after this local convolution.
+      IEN_HIP(hipEventRecord(l->ev_cross, branch2));
+      if (k + 1 < N) {
+        IEN_HIP(hipEventRecord(l->ev_local, ctx->stream));
+        IEN_HIP(hipStreamWaitEvent(branch2, l->ev_local, 0));
+      }
+    }
+    if (k + 1 < N) {
+      Branch br(ctx, 2);
+      st = cross(ffcs[k + 1]);
+    }
+    if (st == IEN_OK) {
+      Branch br(ctx, 1);
+      st = spectral_columns(l->spectral_plan, c.f->fourier, (const float *)l->spectrum, l->work);
+    }
+    if (st == IEN_OK) st = join_branches(ctx, 1);
+    if (st == IEN_OK && split) IEN_HIP(hipStreamWaitEvent(ctx->stream, l->ev_cross, 0));
+    if (st == IEN_OK)
+      st = spectral_back(l->spectral_plan, c.f->spectral_out, l->spectral, l->work, c.out + LOCAL,
+                         CHANNELS, c.residual ? c.residual + LOCAL : nullptr,
+                         c.residual ? c.residual + LOCAL : nullptr);
+    if (st == IEN_OK && k % 2 == 1) st = done();
+  }
+  // (After a failure or a cancel: nothing on branch 2 outlives the run.)
+  if (split) {
+    IEN_HIP(hipEventRecord(l->ev_cross, branch2));
+    IEN_HIP(hipStreamWaitEvent(ctx->stream, l->ev_cross, 0));
+  }
+  return st;
+}
+
 ien_status lama_enqueue(Lama *l, const float *d_image, const float *d_mask, size_t width,
                         size_t height, float *d_out, Steps *steps) {
   ien_ctx *ctx = l->ctx;
@@ -354,16 +412,15 @@ ien_status lama_enqueue(Lama *l, const float *d_image, const float *d_mask, size
     if (st == IEN_OK) st = done();
   }
   const size_t eighth = (size_t)h * w;
-  for (int b = 0; b < BLOCKS && st == IEN_OK; b++) {
-    st = ffc_run(l, l->blocks[b][0], l->a, l->mid, h, w);
-    if (l->spectral_plan) {
-      // The residual add in the second FFC's epilogues.
-      if (st == IEN_OK) st = ffc_run(l, l->blocks[b][1], l->mid, l->out, h, w, l->a);
-    } else {
+  if (l->spectral_plan && st == IEN_OK) {
+    st = ffc_pipeline(l, h, w, done);
+  } else {
+    for (int b = 0; b < BLOCKS && st == IEN_OK; b++) {
+      st = ffc_run(l, l->blocks[b][0], l->a, l->mid, h, w);
       if (st == IEN_OK) st = ffc_run(l, l->blocks[b][1], l->mid, l->out, h, w);
       if (st == IEN_OK) st = ien_add(ctx, l->a, l->out, eighth * CHANNELS);
+      if (st == IEN_OK) st = done();
     }
-    if (st == IEN_OK) st = done();
   }
   // The ups write the quarter, half and full-scale maps again.
   for (int i = 0; i < 3 && st == IEN_OK; i++) {
