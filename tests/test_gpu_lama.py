@@ -105,3 +105,34 @@ def test_lama_checks_size_and_mask(ctx, tensors):
         model.run(synthetic.lama_image(16, 16))
     assert e.value.status == ien.ERR_INPUT
     model.free()
+
+
+# The FFCs run as a pipeline over three streams (each cross convolution
+# beside the previous FFC's columns and back launch); with every branch on
+# the context's stream (IEN_SERIAL_BRANCHES, read when a context opens) the
+# launches are the same, so the output is the same bits, eager and replayed:
+# a race between the streams would show as a difference.
+def test_lama_branches_match_serial(monkeypatch, tensors):
+    import torch
+    import ien
+
+    h = w = 256
+    img, mask = synthetic.lama_image(h, w, seed=31), synthetic.lama_mask(h, w, seed=32)
+    got = {}
+    for serial in ("0", "1"):
+        monkeypatch.setenv("IEN_SERIAL_BRANCHES", serial)
+        c = ien.Context(0)
+        model = ien.Model(c, ien.MODEL_LAMA, tensors=tensors)
+        got[serial, "eager"] = model.run(img, mask=mask)
+        d_img, d_mask = torch.from_numpy(img).cuda(), torch.from_numpy(mask).cuda()
+        d_out = torch.empty_like(d_img)
+        model.set_graph(True)
+        for r in range(2):
+            model.run_device(d_img, w, h, d_out, d_mask)
+            torch.cuda.synchronize()
+            got[serial, "graph", r] = d_out.cpu().numpy()
+        model.free()
+        c.close()
+    ref = got["1", "eager"].view(np.uint32)
+    for key, out in got.items():
+        assert np.array_equal(out.view(np.uint32), ref), key
