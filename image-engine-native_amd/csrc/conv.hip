@@ -132,8 +132,9 @@ __global__ __launch_bounds__(256) void conv_mfma(ConvArgs a) {
   uint16_t *bl = (uint16_t *)(lds_raw + Cfg::HALO_BYTES);
 
   const int bid = xcd_remap(blockIdx.x, gridDim.x);
-  const int tn = bid % a.tiles_n;
-  const int t = bid / a.tiles_n;
+  const int tpix = a.tiles_x * a.tiles_y;
+  const int tn = a.n_major ? bid / tpix : bid % a.tiles_n;
+  const int t = a.n_major ? bid % tpix : bid / a.tiles_n;
   const int tx = t % a.tiles_x;
   const int ty = t / a.tiles_x + a.ty_begin;
   const int oy0 = ty * TR, ox0 = tx * TC;
@@ -1177,6 +1178,17 @@ static ien_status run_cfg(ien_ctx *ctx, ConvArgs a) {
       db = layout_ok && !ctx->compact && blocks <= (long)ctx->cus * FIT && chunks >= 2 &&
            (IN_NCHW || in_bytes <= 0x7fff0000L) && (long)a.NB * a.KB * 1024 <= 0x7fff0000L;
     }
+  }
+  // Each XCD takes a contiguous band of blocks.  Channels fastest, every
+  // band reads all the weights and its share of the input halos; pixels
+  // fastest, the reverse.  Take the order that fetches fewer bytes.
+  {
+    const long tpix = (long)a.tiles_y * a.tiles_x;
+    const double wb = (double)a.tiles_n * Cfg::NBT * a.KB * 1024.0;
+    const double xb = (double)tpix * Cfg::HR * Cfg::HC * a.C * 2.0;
+    const double by_n = xb * std::max(1.0, 8.0 / tpix) + wb * std::min(8L, tpix);
+    const double by_pix = wb * std::max(1.0, 8.0 / a.tiles_n) + xb * std::min(8, a.tiles_n);
+    a.n_major = a.tiles_n > 1 && (blocks & 7) == 0 && by_pix < by_n;
   }
   int ksplit = 1;
   const bool idle = 4 * blocks <= ctx->cus || (KS == 1 && T * a.C >= 1536 && blocks < ctx->cus);

@@ -54,6 +54,11 @@ struct ConvArgs {
   // write output pixel (y, x) to pixel (2 y + py, 2 x + px) of a map
   // 2 OH x 2 OW (pixels ys apart), one phase of a transposed convolution.
   int phase;
+  // Tile order: 0 = output channels fastest (each XCD's band of blocks
+  // covers a few pixel tiles at every channel tile), 1 = pixels fastest
+  // (a band covers few channel tiles at every pixel tile: for weights
+  // larger than the inputs, so each XCD's L2 fetches its share of them once).
+  int n_major;
 };
 
 __device__ __forceinline__ int reflect_idx(int i, int n) {
